@@ -1,0 +1,215 @@
+/*
+ * mugen_attn.h -- C ABI of the MI355X (gfx950) attention library for Mugen.
+ *
+ * Drop-in boundary for Mugen's attention operators.  In the reference the
+ * operators are private members of TransformerModel::Impl, reached through
+ * two seams that this ABI replaces:
+ *
+ *   CPU:  void cpu_attention(const f16* q, uint32_t layer, uint32_t seq_len,
+ *                            f16* out)           src/core/model/transformer.cpp:2441
+ *         void cpu_mla_attention(const f16* q, const LayerWeights&,
+ *                                uint32_t layer, uint32_t seq_len, f16* out)
+ *                                                 src/core/model/transformer.cpp:2539
+ *   GPU:  MetalCompute::DispatchParams built by
+ *         make_flash_attention_decode_dp           src/core/model/transformer.cpp:852-870
+ *         make_prefill_attention_dp                src/core/model/transformer.cpp:828-850
+ *         make_scatter_kv_dp                       src/core/model/transformer.cpp:872-886
+ *         and run by dispatch_sync / dispatch_chain_sync
+ *                                                  src/core/compute/metal_compute.h:84-89
+ *
+ * Conventions (all entry points):
+ *   - plain C: pointers, sizes, enums; no C++ or framework types cross it;
+ *   - every pointer to tensor data is a DEVICE pointer owned by the caller;
+ *     the library never allocates device memory inside a compute call;
+ *     scratch ("workspace") is caller-provided, sized by *_workspace_size;
+ *   - `stream` is a hipStream_t passed as void* (NULL = default stream);
+ *     calls are stream-ordered and never synchronise the host;
+ *   - return 0 on success, a negative MUGEN_ATTN_E_* code otherwise;
+ *     mugen_attn_last_error() gives a message (thread-local).  The
+ *     reference's convention is std::expected<..., std::string>
+ *     (metal_compute.h:84-89); the C++ adapter mugen_attn.hpp maps codes +
+ *     message back to that shape;
+ *   - calls on distinct streams with distinct workspaces are thread-safe.
+ */
+#ifndef MUGEN_ATTN_H
+#define MUGEN_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MUGEN_ATTN_ABI_VERSION 1
+
+/* status codes */
+#define MUGEN_ATTN_OK 0
+#define MUGEN_ATTN_E_INVALID (-1)     /* null pointer, bad shape or stride      */
+#define MUGEN_ATTN_E_UNSUPPORTED (-2) /* shape/dtype combination not compiled   */
+#define MUGEN_ATTN_E_WORKSPACE (-3)   /* workspace missing or too small         */
+#define MUGEN_ATTN_E_HIP (-4)         /* HIP runtime error (launch / device)    */
+
+/* element types (storage); arithmetic is always fp32-accumulate */
+typedef enum {
+    MUGEN_ATTN_F32 = 0,
+    MUGEN_ATTN_F16 = 1, /* IEEE binary16, the reference's f16 (_Float16) */
+    MUGEN_ATTN_BF16 = 2
+} mugen_attn_dtype;
+
+/*
+ * GQA decode: one new query token per sequence against its K/V cache.
+ * Replaces cpu_attention (transformer.cpp:2441-2485) and the
+ * flash_attention_decode dispatch (kernel_sources.h:2900-2999,
+ * transformer.cpp:852-870).
+ *
+ *   q        [batch][n_heads][head_dim]                       (kv_dtype)
+ *   k_cache  sequence b starts at k_cache + b*seq_stride elements; token t of
+ *   v_cache  kv head j sits at + t*n_kv_heads*head_dim + j*head_dim, i.e. the
+ *            reference's per-layer token-major [max_seq][Hk*d] buffer
+ *            (buf_kv_gpu_k/v, transformer.cpp:3382-3394)
+ *   seq_lens device int32 [batch]: tokens 0..seq_lens[b]-1 are attended
+ *            (the reference's seq_len argument); 0 gives a zero output row
+ *   out      [batch][n_heads][head_dim]                       (out_dtype)
+ *
+ *   kv head of query head h = h / (n_heads / n_kv_heads)   (transformer.cpp:2452)
+ *   scale <= 0 selects 1/sqrt(head_dim)                     (transformer.cpp:2444)
+ *   max_seq_len: host-side upper bound of seq_lens (sizes the split-K grid)
+ *   num_splits: 0 = automatic; otherwise the context-split count (>= 1)
+ *
+ * Supported: head_dim in {64, 128}; n_heads / n_kv_heads in [1, 16];
+ * kv_dtype in {F16, BF16} (q has the same dtype); out_dtype F16/BF16/F32.
+ */
+typedef struct mugen_attn_gqa_decode_args {
+    const void* q;
+    const void* k_cache;
+    const void* v_cache;
+    const int32_t* seq_lens;
+    void* out;
+    int32_t batch;
+    int32_t n_heads;
+    int32_t n_kv_heads;
+    int32_t head_dim;
+    int32_t max_seq_len;
+    int32_t num_splits;
+    int64_t seq_stride; /* elements between consecutive sequences' caches */
+    float scale;
+    int32_t kv_dtype;   /* mugen_attn_dtype */
+    int32_t out_dtype;  /* mugen_attn_dtype */
+} mugen_attn_gqa_decode_args;
+
+size_t mugen_attn_gqa_decode_workspace_size(const mugen_attn_gqa_decode_args* args);
+int mugen_attn_gqa_decode(const mugen_attn_gqa_decode_args* args, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/*
+ * GQA causal prefill (flash attention) over one sequence.
+ * Replaces flash_prefill_attention (kernel_sources.h:2769-2896) and
+ * make_prefill_attention_dp (transformer.cpp:828-850); same buffers and
+ * constants: Q_batch, K_cache, V_cache, O_batch, n_heads, n_kv_heads,
+ * head_dim, kv_len, start_position, N.
+ *
+ *   q      [n_tokens][n_heads][head_dim]
+ *   k, v   [kv_len][n_kv_heads*head_dim]  (the cache, new tokens included)
+ *   out    [n_tokens][n_heads][head_dim]
+ *   token i attends to keys [0, start_pos + i]   (kernel_sources.h:2796)
+ *   causal = 0 lets every token see all kv_len keys.
+ *
+ * Supported: head_dim in {64, 128}; n_heads / n_kv_heads in [1, 8];
+ * dtype F16 or BF16 for q/k/v; out_dtype F16/BF16/F32.  No workspace.
+ */
+typedef struct mugen_attn_gqa_prefill_args {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* out;
+    int32_t n_tokens;
+    int32_t n_heads;
+    int32_t n_kv_heads;
+    int32_t head_dim;
+    int32_t kv_len;
+    int32_t start_pos;
+    int32_t causal;
+    float scale;
+    int32_t dtype;
+    int32_t out_dtype;
+} mugen_attn_gqa_prefill_args;
+
+int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* args, void* stream);
+
+/*
+ * MLA absorbed attention over the compressed latent cache: decode (q_len 1)
+ * and speculative verify (q_len > 1, causal among the new tokens).
+ * Replaces the latent core of cpu_mla_attention (transformer.cpp:2576-2608),
+ * batched over sequences and over the verify tokens that the reference
+ * processes one call at a time (transformer.cpp:1325-1337).
+ *
+ *   q       [batch][q_len][n_heads][kv_rank + rope_dim]: absorbed query,
+ *           q_nope.W_UK (kv_rank) followed by q_rope (rope_dim)
+ *   latent  sequence b at latent + b*seq_stride elements; token rows of
+ *           kv_rank + rope_dim (c_kv then k_rope), the reference's
+ *           buf_kv_compressed layout (transformer.cpp:3397-3407)
+ *   seq_lens device int32 [batch]: cache length INCLUDING the q_len new
+ *           tokens; query i sees seq_len - q_len + i + 1 tokens
+ *   out     [batch][q_len][n_heads][kv_rank]  o = sum_t p_t c_t[0:kv_rank]
+ *   scale   must be > 0 (the reference uses 1/sqrt(qk_nope + qk_rope),
+ *           transformer.cpp:2550; 1/sqrt(192) for DeepSeek V2/V3)
+ *
+ * Supported: kv_rank 512, rope_dim 64; latent dtype F16 or BF16; q dtype
+ * F32 (split into two 16-bit halves, fp32-accurate) or equal to the latent
+ * dtype; out_dtype F32, F16 or BF16.
+ */
+typedef struct mugen_attn_mla_decode_args {
+    const void* q;
+    const void* latent;
+    const int32_t* seq_lens;
+    void* out;
+    int32_t batch;
+    int32_t q_len;
+    int32_t n_heads;
+    int32_t kv_rank;
+    int32_t rope_dim;
+    int32_t max_seq_len;
+    int32_t num_splits;
+    int64_t seq_stride;
+    float scale;
+    int32_t q_dtype;
+    int32_t latent_dtype;
+    int32_t out_dtype;
+} mugen_attn_mla_decode_args;
+
+size_t mugen_attn_mla_decode_workspace_size(const mugen_attn_mla_decode_args* args);
+int mugen_attn_mla_decode(const mugen_attn_mla_decode_args* args, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/*
+ * scatter_kv: dst[offset + i] = src[i], i < count, 16-bit elements.
+ * Replaces scatter_kv (kernel_sources.h:3018-3028) / make_scatter_kv_dp
+ * (transformer.cpp:872-886): the per-token append of K/V rows or latent
+ * rows into the per-layer cache.
+ */
+int mugen_attn_scatter_kv(const void* src, void* dst, uint64_t offset, uint64_t count,
+                          void* stream);
+
+/* last error message of the calling thread ("" if none) */
+const char* mugen_attn_last_error(void);
+/* library version string */
+const char* mugen_attn_version(void);
+
+/*
+ * Optional kernel timing (for benchmarks): when enabled, every compute call
+ * brackets each kernel it launches with HIP events on the call's stream.
+ * mugen_attn_timing_read synchronises on the recorded events and returns
+ * the summed milliseconds and launch count of the kernel named `kernel`
+ * ("gqa_decode", "gqa_decode_combine", "gqa_prefill", "mla_decode",
+ * "mla_decode_combine", "scatter_kv").
+ */
+int mugen_attn_timing_enable(int enable);
+int mugen_attn_timing_read(const char* kernel, double* total_ms, int64_t* launches);
+void mugen_attn_timing_reset(void);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* MUGEN_ATTN_H */

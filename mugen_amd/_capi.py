@@ -1,0 +1,131 @@
+"""ctypes binding of libmugen_attn.so (the C ABI in include/mugen_attn.h).
+
+The library is loaded from this package directory only; a missing library
+raises immediately -- there is no fallback implementation.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmugen_attn.so")
+
+OK = 0
+E_INVALID = -1
+E_UNSUPPORTED = -2
+E_WORKSPACE = -3
+E_HIP = -4
+
+F32, F16, BF16 = 0, 1, 2
+
+# every symbol include/mugen_attn.h declares
+EXPORTS = (
+    "mugen_attn_gqa_decode_workspace_size",
+    "mugen_attn_gqa_decode",
+    "mugen_attn_gqa_prefill",
+    "mugen_attn_mla_decode_workspace_size",
+    "mugen_attn_mla_decode",
+    "mugen_attn_scatter_kv",
+    "mugen_attn_last_error",
+    "mugen_attn_version",
+    "mugen_attn_timing_enable",
+    "mugen_attn_timing_read",
+    "mugen_attn_timing_reset",
+)
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+
+
+class GqaDecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", _vp), ("k_cache", _vp), ("v_cache", _vp), ("seq_lens", _vp), ("out", _vp),
+        ("batch", _i32), ("n_heads", _i32), ("n_kv_heads", _i32), ("head_dim", _i32),
+        ("max_seq_len", _i32), ("num_splits", _i32), ("seq_stride", _i64), ("scale", _f32),
+        ("kv_dtype", _i32), ("out_dtype", _i32),
+    ]
+
+
+class GqaPrefillArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", _vp), ("k", _vp), ("v", _vp), ("out", _vp),
+        ("n_tokens", _i32), ("n_heads", _i32), ("n_kv_heads", _i32), ("head_dim", _i32),
+        ("kv_len", _i32), ("start_pos", _i32), ("causal", _i32), ("scale", _f32),
+        ("dtype", _i32), ("out_dtype", _i32),
+    ]
+
+
+class MlaDecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", _vp), ("latent", _vp), ("seq_lens", _vp), ("out", _vp),
+        ("batch", _i32), ("q_len", _i32), ("n_heads", _i32), ("kv_rank", _i32), ("rope_dim", _i32),
+        ("max_seq_len", _i32), ("num_splits", _i32), ("seq_stride", _i64), ("scale", _f32),
+        ("q_dtype", _i32), ("latent_dtype", _i32), ("out_dtype", _i32),
+    ]
+
+
+class MugenAttnError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libmugen_attn.so; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} not found: build it with `python -m mugen_amd.build` "
+                "(or __graft_entry__.build()); mugen_amd has no CPU fallback")
+        L = ctypes.CDLL(LIB_PATH)
+        L.mugen_attn_gqa_decode_workspace_size.argtypes = [ctypes.POINTER(GqaDecodeArgs)]
+        L.mugen_attn_gqa_decode_workspace_size.restype = ctypes.c_size_t
+        L.mugen_attn_gqa_decode.argtypes = [ctypes.POINTER(GqaDecodeArgs), _vp, ctypes.c_size_t, _vp]
+        L.mugen_attn_gqa_decode.restype = ctypes.c_int
+        L.mugen_attn_gqa_prefill.argtypes = [ctypes.POINTER(GqaPrefillArgs), _vp]
+        L.mugen_attn_gqa_prefill.restype = ctypes.c_int
+        L.mugen_attn_mla_decode_workspace_size.argtypes = [ctypes.POINTER(MlaDecodeArgs)]
+        L.mugen_attn_mla_decode_workspace_size.restype = ctypes.c_size_t
+        L.mugen_attn_mla_decode.argtypes = [ctypes.POINTER(MlaDecodeArgs), _vp, ctypes.c_size_t, _vp]
+        L.mugen_attn_mla_decode.restype = ctypes.c_int
+        L.mugen_attn_scatter_kv.argtypes = [_vp, _vp, ctypes.c_uint64, ctypes.c_uint64, _vp]
+        L.mugen_attn_scatter_kv.restype = ctypes.c_int
+        L.mugen_attn_last_error.restype = ctypes.c_char_p
+        L.mugen_attn_version.restype = ctypes.c_char_p
+        L.mugen_attn_timing_enable.argtypes = [ctypes.c_int]
+        L.mugen_attn_timing_read.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
+                                             ctypes.POINTER(_i64)]
+        L.mugen_attn_timing_reset.restype = None
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != OK:
+        raise MugenAttnError(rc, lib().mugen_attn_last_error().decode())
+
+
+def version() -> str:
+    return lib().mugen_attn_version().decode()
+
+
+def timing_enable(on: bool) -> None:
+    check(lib().mugen_attn_timing_enable(1 if on else 0))
+
+
+def timing_read(kernel: str) -> tuple[float, int]:
+    ms = ctypes.c_double(0.0)
+    n = _i64(0)
+    check(lib().mugen_attn_timing_read(kernel.encode(), ctypes.byref(ms), ctypes.byref(n)))
+    return ms.value, n.value
+
+
+def timing_reset() -> None:
+    lib().mugen_attn_timing_reset()

@@ -1,0 +1,167 @@
+"""Torch-tensor front end of the gfx950 attention operators.
+
+Thin wrappers that pass device pointers of torch tensors, plus torch's
+current HIP stream, through the C ABI (include/mugen_attn.h).  Torch is
+used only for device memory and streams; all compute is in
+libmugen_attn.so.  Operator names follow the reference's seams:
+
+  attention_decode         <- cpu_attention / flash_attention_decode
+                              (transformer.cpp:2441-2485, kernel_sources.h:2900-2999)
+  flash_prefill_attention  <- flash_prefill_attention (kernel_sources.h:2769-2896)
+  mla_attention            <- cpu_mla_attention latent core (transformer.cpp:2576-2608)
+  scatter_kv               <- scatter_kv (kernel_sources.h:3018-3028)
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _capi
+
+_DT = {torch.float32: _capi.F32, torch.float16: _capi.F16, torch.bfloat16: _capi.BF16}
+
+
+def _dt(t: torch.dtype) -> int:
+    try:
+        return _DT[t]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t}") from None
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _need_cuda(*ts: torch.Tensor):
+    for t in ts:
+        if not t.is_cuda:
+            raise ValueError("mugen_amd operators take device tensors (no CPU path)")
+        if not t.is_contiguous():
+            raise ValueError("mugen_amd operators take contiguous tensors")
+
+
+# ------------------------------------------------------------------ GQA decode
+
+def gqa_decode_args(q, k_cache, v_cache, seq_lens, out, max_seq_len, scale=0.0, num_splits=0):
+    B, H, D = q.shape
+    Hk = k_cache.shape[-2]
+    seq_stride = k_cache[0].numel() if k_cache.dim() == 4 else 0
+    a = _capi.GqaDecodeArgs()
+    a.q, a.k_cache, a.v_cache = q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr()
+    a.seq_lens, a.out = seq_lens.data_ptr(), out.data_ptr()
+    a.batch, a.n_heads, a.n_kv_heads, a.head_dim = B, H, Hk, D
+    a.max_seq_len, a.num_splits, a.seq_stride, a.scale = int(max_seq_len), int(num_splits), seq_stride, float(scale)
+    a.kv_dtype, a.out_dtype = _dt(k_cache.dtype), _dt(out.dtype)
+    return a
+
+
+def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                     seq_lens: torch.Tensor, max_seq_len: int | None = None, *,
+                     out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+                     scale: float = 0.0, num_splits: int = 0,
+                     workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """GQA decode.  q [B,H,D]; k/v cache [B,max_T,Hk,D] (token-major per
+    sequence); seq_lens int32 [B] on device.  Returns out [B,H,D]."""
+    _need_cuda(q, k_cache, v_cache, seq_lens)
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache/v_cache must be [B, max_T, Hk, D] and equal shapes")
+    if seq_lens.dtype != torch.int32:
+        raise TypeError("seq_lens must be int32")
+    if max_seq_len is None:
+        max_seq_len = k_cache.shape[1]
+    if out is None:
+        out = torch.empty(q.shape, dtype=out_dtype or q.dtype, device=q.device)
+    a = gqa_decode_args(q, k_cache, v_cache, seq_lens, out, max_seq_len, scale, num_splits)
+    L = _capi.lib()
+    need = L.mugen_attn_gqa_decode_workspace_size(ctypes.byref(a))
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _capi.check(L.mugen_attn_gqa_decode(ctypes.byref(a), _ptr(workspace), ws_bytes, _stream(q.device)))
+    return out
+
+
+# ------------------------------------------------------------------ GQA prefill
+
+def flash_prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, start_pos: int = 0, *,
+                            causal: bool = True, out: torch.Tensor | None = None,
+                            out_dtype: torch.dtype | None = None, scale: float = 0.0) -> torch.Tensor:
+    """Causal GQA prefill.  q [N,H,D]; k/v [kv_len,Hk,D] (cache incl. the new
+    tokens); token i sees keys [0, start_pos+i].  Returns out [N,H,D]."""
+    _need_cuda(q, k, v)
+    N, H, D = q.shape
+    kv_len, Hk, Dk = k.shape
+    if Dk != D or v.shape != k.shape:
+        raise ValueError("k/v must be [kv_len, Hk, D] matching q's head_dim")
+    if out is None:
+        out = torch.empty(q.shape, dtype=out_dtype or q.dtype, device=q.device)
+    a = _capi.GqaPrefillArgs()
+    a.q, a.k, a.v, a.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
+    a.n_tokens, a.n_heads, a.n_kv_heads, a.head_dim = N, H, Hk, D
+    a.kv_len, a.start_pos, a.causal, a.scale = kv_len, int(start_pos), 1 if causal else 0, float(scale)
+    a.dtype, a.out_dtype = _dt(q.dtype), _dt(out.dtype)
+    _capi.check(_capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), _stream(q.device)))
+    return out
+
+
+# ------------------------------------------------------------------ MLA
+
+def mla_args(q, latent, seq_lens, out, max_seq_len, scale, num_splits=0):
+    B, q_len, H, C = q.shape
+    a = _capi.MlaDecodeArgs()
+    a.q, a.latent, a.seq_lens, a.out = q.data_ptr(), latent.data_ptr(), seq_lens.data_ptr(), out.data_ptr()
+    a.batch, a.q_len, a.n_heads, a.kv_rank, a.rope_dim = B, q_len, H, 512, C - 512
+    a.max_seq_len, a.num_splits = int(max_seq_len), int(num_splits)
+    a.seq_stride = latent[0].numel()
+    a.scale = float(scale)
+    a.q_dtype, a.latent_dtype, a.out_dtype = _dt(q.dtype), _dt(latent.dtype), _dt(out.dtype)
+    return a
+
+
+def mla_attention(q: torch.Tensor, latent: torch.Tensor, seq_lens: torch.Tensor,
+                  max_seq_len: int | None = None, *, scale: float = 1.0 / math.sqrt(192.0),
+                  out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32,
+                  num_splits: int = 0, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """MLA absorbed attention (decode: q_len 1; verify: q_len > 1, causal).
+
+    q [B,q_len,H,576] (q_nope.W_UK ++ q_rope); latent [B,max_T,576];
+    seq_lens int32 [B] = cache length incl. the q_len new tokens.
+    Returns out [B,q_len,H,512]."""
+    _need_cuda(q, latent, seq_lens)
+    if q.dim() != 4 or latent.dim() != 3 or latent.shape[-1] != q.shape[-1]:
+        raise ValueError("q must be [B,q_len,H,576] and latent [B,max_T,576]")
+    if seq_lens.dtype != torch.int32:
+        raise TypeError("seq_lens must be int32")
+    if max_seq_len is None:
+        max_seq_len = latent.shape[1]
+    B, q_len, H, _ = q.shape
+    if out is None:
+        out = torch.empty((B, q_len, H, 512), dtype=out_dtype, device=q.device)
+    a = mla_args(q, latent, seq_lens, out, max_seq_len, scale, num_splits)
+    L = _capi.lib()
+    need = L.mugen_attn_mla_decode_workspace_size(ctypes.byref(a))
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _capi.check(L.mugen_attn_mla_decode(ctypes.byref(a), _ptr(workspace), ws_bytes, _stream(q.device)))
+    return out
+
+
+# ------------------------------------------------------------------ scatter_kv
+
+def scatter_kv(src: torch.Tensor, dst: torch.Tensor, offset: int) -> torch.Tensor:
+    """dst.view(-1)[offset : offset+src.numel()] = src (16-bit elements)."""
+    _need_cuda(src, dst)
+    if src.element_size() != 2 or dst.element_size() != 2:
+        raise TypeError("scatter_kv copies 16-bit elements")
+    if offset < 0 or offset + src.numel() > dst.numel():
+        raise ValueError("scatter_kv: destination range out of bounds")
+    _capi.check(_capi.lib().mugen_attn_scatter_kv(_ptr(src), _ptr(dst), int(offset), src.numel(),
+                                                  _stream(src.device)))
+    return dst

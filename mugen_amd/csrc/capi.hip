@@ -1,0 +1,398 @@
+// capi.hip -- extern "C" entry points of libmugen_attn (see include/mugen_attn.h).
+//
+// Validation, split-K planning, workspace carving and optional event timing
+// live here; the kernels are in gqa_decode.hip, gqa_prefill.hip and
+// mla_decode.hip.  Nothing here allocates device memory or synchronises
+// the host (except mugen_attn_timing_read, which waits on its own events).
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace mugen_attn {
+
+// ------------------------------------------------------------------ errors
+
+static thread_local std::string g_last_error;
+
+static int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+static int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return MUGEN_ATTN_OK;
+    return fail(MUGEN_ATTN_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// ------------------------------------------------------------------ timing
+
+struct KernelTimer {
+    std::mutex mu;
+    bool enabled = false;
+    struct Pending { std::string name; hipEvent_t a, b; };
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> pool;
+    std::unordered_map<std::string, std::pair<double, int64_t>> totals;
+    hipEvent_t open_a = nullptr;
+
+    hipEvent_t get() {
+        if (!pool.empty()) { hipEvent_t e = pool.back(); pool.pop_back(); return e; }
+        hipEvent_t e = nullptr;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        return e;
+    }
+    void drain() {  // caller holds mu
+        for (auto& p : pending) {
+            float ms = 0.f;
+            if (hipEventSynchronize(p.b) == hipSuccess && hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+                auto& t = totals[p.name];
+                t.first += ms;
+                t.second += 1;
+            }
+            pool.push_back(p.a);
+            pool.push_back(p.b);
+        }
+        pending.clear();
+    }
+};
+
+static KernelTimer g_timer;
+
+KernelTimer* active_timer() { return g_timer.enabled ? &g_timer : nullptr; }
+
+void timer_begin(KernelTimer* t, const char*, hipStream_t st) {
+    if (!t) return;
+    std::lock_guard<std::mutex> lk(t->mu);
+    t->open_a = t->get();
+    if (t->open_a) (void)hipEventRecord(t->open_a, st);
+}
+
+void timer_end(KernelTimer* t, const char* name, hipStream_t st) {
+    if (!t) return;
+    std::lock_guard<std::mutex> lk(t->mu);
+    if (!t->open_a) return;
+    hipEvent_t b = t->get();
+    if (!b) return;
+    (void)hipEventRecord(b, st);
+    t->pending.push_back({name, t->open_a, b});
+    t->open_a = nullptr;
+    if (t->pending.size() > 4096) t->drain();
+}
+
+// ------------------------------------------------------------------ scatter_kv
+
+__global__ void scatter_kv_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                  uint64_t offset, uint64_t count) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) dst[offset + i] = src[i];
+}
+
+// 16-byte vector copy when both ends are 16-byte aligned
+__global__ void scatter_kv16_kernel(const u32x4_t* __restrict__ src, u32x4_t* __restrict__ dst,
+                                    uint64_t n16) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n16) dst[i] = src[i];
+}
+
+hipError_t launch_scatter_kv(const uint16_t* src, uint16_t* dst, uint64_t offset, uint64_t count,
+                             hipStream_t st, KernelTimer* t) {
+    if (count == 0) return hipSuccess;
+    timer_begin(t, "scatter_kv", st);
+    uint16_t* d = dst + offset;
+    if ((((uintptr_t)src | (uintptr_t)d) & 15) == 0 && (count & 7) == 0) {
+        const uint64_t n16 = count / 8;
+        hipLaunchKernelGGL(scatter_kv16_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, st,
+                           reinterpret_cast<const u32x4_t*>(src), reinterpret_cast<u32x4_t*>(d), n16);
+    } else {
+        hipLaunchKernelGGL(scatter_kv_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, st, src,
+                           dst, offset, count);
+    }
+    timer_end(t, "scatter_kv", st);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ planning
+
+static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+static bool is16(int dt) { return dt == DT_F16 || dt == DT_BF16; }
+static bool is_out(int dt) { return dt == DT_F32 || dt == DT_F16 || dt == DT_BF16; }
+
+// GQA decode: tokens per split (multiple of 64 = one 16-token block per wave)
+static int gqa_chunk(const mugen_attn_gqa_decode_args* a) {
+    const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
+    if (a->num_splits > 0) {
+        const int c = ceil_div(maxT, a->num_splits);
+        return ceil_div(c, 64) * 64;
+    }
+    // aim for ~512 workgroups (2 per CU) over the whole batch
+    const int64_t items = (int64_t)a->batch * a->n_kv_heads;
+    int64_t c = ((int64_t)maxT * items + 511) / 512;
+    c = ((c + 63) / 64) * 64;
+    if (c < 64) c = 64;
+    if (c > 4096) c = 4096;
+    return (int)c;
+}
+
+static int gqa_validate(const mugen_attn_gqa_decode_args* a) {
+    if (!a) return fail(MUGEN_ATTN_E_INVALID, "gqa_decode: null args");
+    if (!a->q || !a->k_cache || !a->v_cache || !a->seq_lens || !a->out)
+        return fail(MUGEN_ATTN_E_INVALID, "gqa_decode: null tensor pointer");
+    if (a->batch <= 0 || a->n_heads <= 0 || a->n_kv_heads <= 0 || a->max_seq_len < 0 || a->num_splits < 0)
+        return fail(MUGEN_ATTN_E_INVALID, "gqa_decode: batch/heads must be > 0, max_seq_len/num_splits >= 0");
+    if (a->n_heads % a->n_kv_heads)
+        return fail(MUGEN_ATTN_E_INVALID, "gqa_decode: n_heads %d not a multiple of n_kv_heads %d", a->n_heads,
+                    a->n_kv_heads);
+    if (a->n_heads / a->n_kv_heads > 16)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode: n_heads/n_kv_heads = %d > 16",
+                    a->n_heads / a->n_kv_heads);
+    if (a->head_dim != 64 && a->head_dim != 128)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode: head_dim %d (supported: 64, 128)", a->head_dim);
+    if (!is16(a->kv_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode: kv_dtype must be F16 or BF16");
+    if (!is_out(a->out_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode: bad out_dtype");
+    if (a->batch > 1 && a->seq_stride < (int64_t)a->max_seq_len * a->n_kv_heads * a->head_dim)
+        return fail(MUGEN_ATTN_E_INVALID, "gqa_decode: seq_stride %lld smaller than max_seq_len*Hk*D",
+                    (long long)a->seq_stride);
+    if (((uintptr_t)a->q | (uintptr_t)a->k_cache | (uintptr_t)a->v_cache) & 15)
+        return fail(MUGEN_ATTN_E_INVALID, "gqa_decode: q/k/v must be 16-byte aligned");
+    if (a->batch > 1 && (a->seq_stride % 8))
+        return fail(MUGEN_ATTN_E_INVALID, "gqa_decode: seq_stride must be a multiple of 8 elements");
+    return MUGEN_ATTN_OK;
+}
+
+static size_t gqa_ws(const mugen_attn_gqa_decode_args* a, int chunk, int* splits_out) {
+    const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
+    const int splits = ceil_div(maxT, chunk);
+    if (splits_out) *splits_out = splits;
+    if (splits <= 1) return 0;
+    const size_t slots = (size_t)a->batch * a->n_heads * splits;
+    return slots * (size_t)a->head_dim * 4 + slots * 2 * 4 + 256;
+}
+
+// MLA: rows per workgroup and tokens per split
+static int mla_variant(const mugen_attn_mla_decode_args*) { return 1; }
+
+static int mla_chunk(const mugen_attn_mla_decode_args* a, int variant) {
+    const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
+    if (a->num_splits > 0) {
+        const int c = ceil_div(maxT, a->num_splits);
+        return ceil_div(c, 32) * 32;
+    }
+    const int R = a->q_len * a->n_heads;
+    const int64_t nrb = ceil_div(R, mla_rows_per_block(variant));
+    // ~one workgroup per CU (256 CUs): the kernel runs 1 wave per SIMD
+    int64_t c = ((int64_t)maxT * a->batch * nrb + 255) / 256;
+    c = ((c + 31) / 32) * 32;
+    if (c < 64) c = 64;
+    return (int)c;
+}
+
+static int mla_validate(const mugen_attn_mla_decode_args* a) {
+    if (!a) return fail(MUGEN_ATTN_E_INVALID, "mla_decode: null args");
+    if (!a->q || !a->latent || !a->seq_lens || !a->out)
+        return fail(MUGEN_ATTN_E_INVALID, "mla_decode: null tensor pointer");
+    if (a->batch <= 0 || a->q_len <= 0 || a->n_heads <= 0 || a->max_seq_len < 0 || a->num_splits < 0)
+        return fail(MUGEN_ATTN_E_INVALID, "mla_decode: batch/q_len/n_heads must be > 0");
+    if (a->kv_rank != 512 || a->rope_dim != 64)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_decode: kv_rank %d / rope_dim %d (supported: 512 / 64)",
+                    a->kv_rank, a->rope_dim);
+    if (!(a->scale > 0.f) || !isfinite(a->scale))
+        return fail(MUGEN_ATTN_E_INVALID, "mla_decode: scale must be finite and > 0");
+    if (!is16(a->latent_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_decode: latent dtype must be F16/BF16");
+    if (a->q_dtype != DT_F32 && a->q_dtype != a->latent_dtype)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_decode: q dtype must be F32 or the latent dtype");
+    if (!is_out(a->out_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_decode: bad out_dtype");
+    if (a->batch > 1 && a->seq_stride < (int64_t)a->max_seq_len * 576)
+        return fail(MUGEN_ATTN_E_INVALID, "mla_decode: seq_stride smaller than max_seq_len*576");
+    if (((uintptr_t)a->q | (uintptr_t)a->latent) & 15)
+        return fail(MUGEN_ATTN_E_INVALID, "mla_decode: q/latent must be 16-byte aligned");
+    if (a->batch > 1 && (a->seq_stride % 8))
+        return fail(MUGEN_ATTN_E_INVALID, "mla_decode: seq_stride must be a multiple of 8 elements");
+    if ((int64_t)a->q_len * a->n_heads > (1 << 20))
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_decode: q_len*n_heads too large");
+    return MUGEN_ATTN_OK;
+}
+
+static size_t mla_ws(const mugen_attn_mla_decode_args* a, int chunk, int* splits_out) {
+    const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
+    const int splits = ceil_div(maxT, chunk);
+    if (splits_out) *splits_out = splits;
+    if (splits <= 1) return 0;
+    const size_t slots = (size_t)a->batch * splits * a->q_len * a->n_heads;
+    return slots * 512 * 4 + slots * 2 * 4 + 256;
+}
+
+static float* align256(void* p) {
+    return reinterpret_cast<float*>((reinterpret_cast<uintptr_t>(p) + 255) & ~uintptr_t(255));
+}
+
+}  // namespace mugen_attn
+
+using namespace mugen_attn;
+
+extern "C" {
+
+const char* mugen_attn_last_error(void) { return g_last_error.c_str(); }
+
+const char* mugen_attn_version(void) { return "mugen_attn 0.1.0 (gfx950, abi 1)"; }
+
+size_t mugen_attn_gqa_decode_workspace_size(const mugen_attn_gqa_decode_args* a) {
+    if (gqa_validate(a) != MUGEN_ATTN_OK) return 0;
+    return gqa_ws(a, gqa_chunk(a), nullptr);
+}
+
+int mugen_attn_gqa_decode(const mugen_attn_gqa_decode_args* a, void* ws, size_t ws_bytes, void* stream) {
+    int rc = gqa_validate(a);
+    if (rc) return rc;
+    const int chunk = gqa_chunk(a);
+    int splits = 1;
+    const size_t need = gqa_ws(a, chunk, &splits);
+    if (need > 0 && (!ws || ws_bytes < need))
+        return fail(MUGEN_ATTN_E_WORKSPACE, "gqa_decode: workspace of %zu bytes required, %zu given", need,
+                    ws_bytes);
+    GqaDecodeParams p{};
+    p.q = static_cast<const uint16_t*>(a->q);
+    p.k = static_cast<const uint16_t*>(a->k_cache);
+    p.v = static_cast<const uint16_t*>(a->v_cache);
+    p.seq_lens = a->seq_lens;
+    p.out = a->out;
+    p.H = a->n_heads;
+    p.G = a->n_heads / a->n_kv_heads;
+    p.row_stride = a->n_kv_heads * a->head_dim;
+    p.chunk = chunk;
+    p.num_splits = splits;
+    p.seq_stride = a->seq_stride;
+    const float scale = a->scale > 0.f ? a->scale : 1.f / sqrtf((float)a->head_dim);
+    p.scale_log2 = scale * kLog2e;
+    if (splits > 1) {
+        float* base = align256(ws);
+        const size_t slots = (size_t)a->batch * a->n_heads * splits;
+        p.ws_o = base;
+        p.ws_ml = base + slots * a->head_dim;
+    }
+    hipError_t e = launch_gqa_decode(p, a->batch, a->n_kv_heads, a->head_dim, a->kv_dtype, a->out_dtype,
+                                     static_cast<hipStream_t>(stream), active_timer());
+    return hip_status(e, "gqa_decode launch");
+}
+
+int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
+    if (!a) return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: null args");
+    if (!a->q || !a->k || !a->v || !a->out) return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: null tensor pointer");
+    if (a->n_tokens < 0 || a->n_heads <= 0 || a->n_kv_heads <= 0 || a->kv_len < 0 || a->start_pos < 0)
+        return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: negative size");
+    if (a->n_heads % a->n_kv_heads) return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: n_heads % n_kv_heads != 0");
+    if (a->n_heads / a->n_kv_heads > 8)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: n_heads/n_kv_heads > 8");
+    if (a->head_dim != 64 && a->head_dim != 128)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: head_dim %d (supported: 64, 128)", a->head_dim);
+    if (!is16(a->dtype) || !is_out(a->out_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: dtype");
+    if (((uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->v) & 15)
+        return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: q/k/v must be 16-byte aligned");
+    if (a->n_tokens == 0) return MUGEN_ATTN_OK;
+    if (a->kv_len == 0) return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: kv_len == 0 with n_tokens > 0");
+    if (a->causal && a->start_pos + a->n_tokens > a->kv_len)
+        return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: start_pos + n_tokens (%d) > kv_len (%d)",
+                    a->start_pos + a->n_tokens, a->kv_len);
+    GqaPrefillParams p{};
+    p.q = static_cast<const uint16_t*>(a->q);
+    p.k = static_cast<const uint16_t*>(a->k);
+    p.v = static_cast<const uint16_t*>(a->v);
+    p.out = a->out;
+    p.N = a->n_tokens;
+    p.H = a->n_heads;
+    p.G = a->n_heads / a->n_kv_heads;
+    p.row_stride = a->n_kv_heads * a->head_dim;
+    p.kv_len = a->kv_len;
+    p.start_pos = a->start_pos;
+    p.causal = a->causal ? 1 : 0;
+    const float scale = a->scale > 0.f ? a->scale : 1.f / sqrtf((float)a->head_dim);
+    p.scale_log2 = scale * kLog2e;
+    hipError_t e = launch_gqa_prefill(p, a->n_kv_heads, a->head_dim, a->dtype, a->out_dtype,
+                                      static_cast<hipStream_t>(stream), active_timer());
+    return hip_status(e, "gqa_prefill launch");
+}
+
+size_t mugen_attn_mla_decode_workspace_size(const mugen_attn_mla_decode_args* a) {
+    if (mla_validate(a) != MUGEN_ATTN_OK) return 0;
+    const int v = mla_variant(a);
+    return mla_ws(a, mla_chunk(a, v), nullptr);
+}
+
+int mugen_attn_mla_decode(const mugen_attn_mla_decode_args* a, void* ws, size_t ws_bytes, void* stream) {
+    int rc = mla_validate(a);
+    if (rc) return rc;
+    const int variant = mla_variant(a);
+    const int chunk = mla_chunk(a, variant);
+    int splits = 1;
+    const size_t need = mla_ws(a, chunk, &splits);
+    if (need > 0 && (!ws || ws_bytes < need))
+        return fail(MUGEN_ATTN_E_WORKSPACE, "mla_decode: workspace of %zu bytes required, %zu given", need,
+                    ws_bytes);
+    MlaParams p{};
+    p.q = a->q;
+    p.lat = static_cast<const uint16_t*>(a->latent);
+    p.seq_lens = a->seq_lens;
+    p.out = a->out;
+    p.q_len = a->q_len;
+    p.H = a->n_heads;
+    p.R = a->q_len * a->n_heads;
+    p.chunk = chunk;
+    p.num_splits = splits;
+    p.seq_stride = a->seq_stride;
+    p.scale_log2 = a->scale * kLog2e;
+    if (splits > 1) {
+        float* base = align256(ws);
+        const size_t slots = (size_t)a->batch * splits * p.R;
+        p.ws_o = base;
+        p.ws_ml = base + slots * 512;
+    }
+    hipError_t e = launch_mla_decode(p, a->batch, variant, a->q_dtype, a->latent_dtype, a->out_dtype,
+                                     static_cast<hipStream_t>(stream), active_timer());
+    return hip_status(e, "mla_decode launch");
+}
+
+int mugen_attn_scatter_kv(const void* src, void* dst, uint64_t offset, uint64_t count, void* stream) {
+    if (count == 0) return MUGEN_ATTN_OK;
+    if (!src || !dst) return fail(MUGEN_ATTN_E_INVALID, "scatter_kv: null pointer");
+    hipError_t e = launch_scatter_kv(static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), offset, count,
+                                     static_cast<hipStream_t>(stream), active_timer());
+    return hip_status(e, "scatter_kv launch");
+}
+
+int mugen_attn_timing_enable(int enable) {
+    std::lock_guard<std::mutex> lk(g_timer.mu);
+    g_timer.enabled = enable != 0;
+    return MUGEN_ATTN_OK;
+}
+
+int mugen_attn_timing_read(const char* kernel, double* total_ms, int64_t* launches) {
+    if (!kernel) return fail(MUGEN_ATTN_E_INVALID, "timing_read: null kernel name");
+    std::lock_guard<std::mutex> lk(g_timer.mu);
+    g_timer.drain();
+    auto it = g_timer.totals.find(kernel);
+    if (total_ms) *total_ms = it == g_timer.totals.end() ? 0.0 : it->second.first;
+    if (launches) *launches = it == g_timer.totals.end() ? 0 : it->second.second;
+    return MUGEN_ATTN_OK;
+}
+
+void mugen_attn_timing_reset(void) {
+    std::lock_guard<std::mutex> lk(g_timer.mu);
+    g_timer.drain();
+    g_timer.totals.clear();
+}
+
+}  // extern "C"

@@ -1,0 +1,75 @@
+// kernels.h -- internal kernel parameter blocks and launchers (not ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mugen_attn {
+
+struct KernelTimer;  // defined in capi.hip
+void timer_begin(KernelTimer* t, const char* name, hipStream_t st);
+void timer_end(KernelTimer* t, const char* name, hipStream_t st);
+
+struct GqaDecodeParams {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const int32_t* seq_lens;
+    void* out;
+    float* ws_o;   // [B][H][splits][D]   unnormalised partial outputs
+    float* ws_ml;  // [B][H][splits][2]   (max in log2 units, sum)
+    int H;
+    int G;           // query heads per kv head
+    int row_stride;  // elements between consecutive tokens (Hk * D)
+    int chunk;       // tokens per split
+    int num_splits;
+    int64_t seq_stride;
+    float scale_log2;  // softmax scale * log2(e)
+};
+
+hipError_t launch_gqa_decode(const GqaDecodeParams& p, int B, int Hk, int D, int kv_dt, int out_dt,
+                             hipStream_t st, KernelTimer* t);
+
+struct GqaPrefillParams {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    void* out;
+    int N;
+    int H;
+    int G;
+    int row_stride;  // Hk * D
+    int kv_len;
+    int start_pos;
+    int causal;
+    float scale_log2;
+};
+
+hipError_t launch_gqa_prefill(const GqaPrefillParams& p, int Hk, int D, int dt, int out_dt,
+                              hipStream_t st, KernelTimer* t);
+
+struct MlaParams {
+    const void* q;         // [B][q_len*H][576], f32 or the latent dtype
+    const uint16_t* lat;   // latent cache
+    const int32_t* seq_lens;
+    void* out;             // [B][q_len*H][512]
+    float* ws_o;           // [B][splits][R][512]
+    float* ws_ml;          // [B][splits][R][2]
+    int q_len;
+    int H;
+    int R;                 // q_len * H rows per sequence
+    int chunk;
+    int num_splits;
+    int64_t seq_stride;
+    float scale_log2;
+};
+
+// rows of queries handled by one MLA workgroup for a given variant
+int mla_rows_per_block(int variant);
+hipError_t launch_mla_decode(const MlaParams& p, int B, int variant, int q_dt, int lat_dt,
+                             int out_dt, hipStream_t st, KernelTimer* t);
+
+hipError_t launch_scatter_kv(const uint16_t* src, uint16_t* dst, uint64_t offset, uint64_t count,
+                             hipStream_t st, KernelTimer* t);
+
+}  // namespace mugen_attn

@@ -1,0 +1,383 @@
+/*
+ * attn_oracle.c -- CPU restatement of Mugen's attention paths.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker the parity tests,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg compare the HIP
+ * kernels against.  Nothing in the product library (mugen_amd/) links,
+ * loads or calls it.
+ *
+ * Restated from (reference paths relative to the Mugen source tree):
+ *   oracle_gqa_attention  <- TransformerModel::Impl::cpu_attention,
+ *                            src/core/model/transformer.cpp:2441-2485
+ *                            (GQA map kv_h = h / (H/Hk) :2452, scale
+ *                            1/sqrt(head_dim) :2444, fp32 dot :2458-2465,
+ *                            max-subtract softmax with std::exp :2467-2473,
+ *                            p-weighted V sum d-outer/s-inner :2476-2483)
+ *   oracle_gqa_prefill    <- flash_prefill_attention semantics,
+ *                            src/metal/kernel_sources.h:2769-2896, causal rule
+ *                            causal_len = start + token + 1 (:2796), and the
+ *                            per-token CPU rule transformer.cpp:1334-1335
+ *   oracle_mla_attention  <- latent core of cpu_mla_attention,
+ *                            src/core/model/transformer.cpp:2576-2608 (score
+ *                            = q_abs . c[0:512] + q_rope . c[512:576] summed
+ *                            into one fp32 accumulator, times scale :2550;
+ *                            softmax :2591-2598; o = sum_t p_t c_t[0:512]
+ *                            accumulated s-outer/d-inner :2602-2608);
+ *                            multi-query (verify) rows follow the per-token
+ *                            call seq_len = start_position + t + 1
+ *                            (transformer.cpp:1325-1337).
+ *   oracle_scatter_kv     <- scatter_kv, src/metal/kernel_sources.h:3018-3028
+ *
+ * The summation orders above are kept (sequential fp32 sums, expf, divide
+ * by the sum) so that the float variant reproduces the reference's rounding
+ * behaviour; the double variants are the same algorithm in fp64 and serve
+ * as the tolerance anchor.  Inputs arrive as float arrays that already hold
+ * the storage-dtype values (fp16/bf16 rounded); the reference widens each
+ * f16 element with static_cast<float>, which is exact, so this is the same
+ * arithmetic.
+ *
+ * Departure (documented): seq_len == 0 is undefined in the reference
+ * (max_element of an empty range); here the output row is all zeros, which
+ * is what the reference's Metal flash kernels produce (inv_sum = 0 when
+ * running_sum == 0, kernel_sources.h:2982).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------ */
+/* dtype rounding helpers (IEEE binary16 and bfloat16, round-to-even)  */
+/* ------------------------------------------------------------------ */
+
+static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+uint16_t oracle_f32_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40); /* NaN */
+    uint32_t lsb = (u >> 16) & 1u;
+    u += 0x7fffu + lsb;
+    return (uint16_t)(u >> 16);
+}
+
+float oracle_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+float oracle_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu;
+    uint32_t man = h & 0x3ffu;
+    if (exp == 0) {
+        if (man == 0) return u2f(sign);
+        /* subnormal: value = man * 2^-24 */
+        float v = (float)man * 5.9604644775390625e-08f;
+        return sign ? -v : v;
+    }
+    if (exp == 31) return u2f(sign | 0x7f800000u | (man << 13));
+    return u2f(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+uint16_t oracle_f32_to_f16(float f) {
+    uint32_t u = f2u(f);
+    uint32_t sign = (u >> 16) & 0x8000u;
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);          /* NaN */
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);         /* overflow -> inf */
+    if (a < 0x38800000u) {                                            /* subnormal / zero */
+        /* value in units of 2^-24, round to nearest even */
+        float v = u2f(a) * 16777216.0f;
+        float r = rintf(v); /* default rounding mode: nearest-even */
+        return (uint16_t)(sign | (uint32_t)r);
+    }
+    uint32_t exp = (a >> 23) - 112u;
+    uint32_t man = a & 0x7fffffu;
+    uint32_t half = (exp << 10) | (man >> 13);
+    uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (half & 1u))) half += 1u;
+    return (uint16_t)(sign | half);
+}
+
+/* Round a float array in place to the values representable in `dtype`
+ * (0 = f32: no-op, 1 = f16, 2 = bf16) and optionally emit the raw bits. */
+void oracle_round_to_dtype(float* x, uint16_t* bits_out, int64_t n, int dtype) {
+    for (int64_t i = 0; i < n; i++) {
+        uint16_t b;
+        if (dtype == 1) { b = oracle_f32_to_f16(x[i]); x[i] = oracle_f16_to_f32(b); }
+        else if (dtype == 2) { b = oracle_f32_to_bf16(x[i]); x[i] = oracle_bf16_to_f32(b); }
+        else continue;
+        if (bits_out) bits_out[i] = b;
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* seeded normal generator: mt19937_64 + Box-Muller                    */
+/* ------------------------------------------------------------------ */
+
+typedef struct { uint64_t mt[312]; int idx; } mt64_t;
+
+static void mt64_seed(mt64_t* s, uint64_t seed) {
+    s->mt[0] = seed;
+    for (int i = 1; i < 312; i++)
+        s->mt[i] = 6364136223846793005ULL * (s->mt[i - 1] ^ (s->mt[i - 1] >> 62)) + (uint64_t)i;
+    s->idx = 312;
+}
+
+static uint64_t mt64_next(mt64_t* s) {
+    static const uint64_t UM = 0xFFFFFFFF80000000ULL, LM = 0x7FFFFFFFULL;
+    if (s->idx >= 312) {
+        for (int i = 0; i < 312; i++) {
+            uint64_t x = (s->mt[i] & UM) | (s->mt[(i + 1) % 312] & LM);
+            uint64_t xa = x >> 1;
+            if (x & 1ULL) xa ^= 0xB5026F5AA96619E9ULL;
+            s->mt[i] = s->mt[(i + 156) % 312] ^ xa;
+        }
+        s->idx = 0;
+    }
+    uint64_t x = s->mt[s->idx++];
+    x ^= (x >> 29) & 0x5555555555555555ULL;
+    x ^= (x << 17) & 0x71D67FFFEDA60000ULL;
+    x ^= (x << 37) & 0xFFF7EEE000000000ULL;
+    x ^= x >> 43;
+    return x;
+}
+
+/* First output of mt19937_64 seeded with 5489 must be 14514284786278117030
+ * (the C++ standard's required value); exposed for the self-test. */
+uint64_t oracle_mt64_first(uint64_t seed, int64_t skip) {
+    mt64_t s; mt64_seed(&s, seed);
+    for (int64_t i = 0; i < skip; i++) mt64_next(&s);
+    return mt64_next(&s);
+}
+
+/* n normal draws N(mean, std^2); pairs from Box-Muller, u in (0, 1]. */
+void oracle_randn(uint64_t seed, int64_t n, float mean, float stdv, float* out) {
+    mt64_t s; mt64_seed(&s, seed);
+    const double two_pi = 6.283185307179586476925286766559;
+    for (int64_t i = 0; i < n; i += 2) {
+        double u1 = ((double)(mt64_next(&s) >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+        double u2 = (double)(mt64_next(&s) >> 11) * (1.0 / 9007199254740992.0);
+        double r = sqrt(-2.0 * log(u1));
+        out[i] = (float)(mean + stdv * r * cos(two_pi * u2));
+        if (i + 1 < n) out[i + 1] = (float)(mean + stdv * r * sin(two_pi * u2));
+    }
+}
+
+/* n integers uniform in [lo, hi] (inclusive), for ragged context lengths. */
+void oracle_randint(uint64_t seed, int64_t n, int32_t lo, int32_t hi, int32_t* out) {
+    mt64_t s; mt64_seed(&s, seed);
+    uint64_t span = (uint64_t)((int64_t)hi - lo + 1);
+    for (int64_t i = 0; i < n; i++) out[i] = lo + (int32_t)(mt64_next(&s) % span);
+}
+
+/* ------------------------------------------------------------------ */
+/* GQA decode: one query token per sequence (cpu_attention)            */
+/* ------------------------------------------------------------------ */
+/*
+ * q        [B][H][D]
+ * k, v     sequence b starts at b*seq_stride; token t, kv head j at
+ *          t*(Hk*D) + j*D  (the reference's token-major [T][Hk*D] layout,
+ *          kv_stride = Hk*D, transformer.cpp:2446)
+ * out      [B][H][D]
+ * scale    <= 0 selects 1/sqrt(D)
+ */
+#define GQA_PRE(REAL)                                                                \
+    int G = H / Hk;                                                                        \
+    int64_t kv_stride = (int64_t)Hk * D;                                                   \
+    /* the reference computes the scale in float (transformer.cpp:2444) */ \
+    REAL sc = (REAL)(scale > 0 ? scale : 1.0f / sqrtf((float)D));
+#define GQA_BODY(REAL, EXP)                                                                \
+    for (int64_t bh = 0; bh < (int64_t)B * H; bh++) {                                      \
+        int b = (int)(bh / H), h = (int)(bh % H);                                          \
+        int T = seq_lens[b];                                                               \
+        const float* qh = q + ((int64_t)b * H + h) * D;                                    \
+        const float* kb = k + b * seq_stride + (int64_t)(h / G) * D;                       \
+        const float* vb = v + b * seq_stride + (int64_t)(h / G) * D;                       \
+        OUT_T* oh = out + ((int64_t)b * H + h) * D;                                        \
+        if (T <= 0) { for (int d = 0; d < D; d++) oh[d] = 0; continue; }                   \
+        REAL* s = (REAL*)malloc(sizeof(REAL) * (size_t)T);                                 \
+        for (int t = 0; t < T; t++) {                                                      \
+            REAL dot = 0;                                                                  \
+            for (int d = 0; d < D; d++) dot += (REAL)qh[d] * (REAL)kb[t * kv_stride + d]; \
+            s[t] = dot * sc;                                                               \
+        }                                                                                  \
+        REAL mx = s[0];                                                                    \
+        for (int t = 1; t < T; t++) if (s[t] > mx) mx = s[t];                              \
+        REAL sum = 0;                                                                      \
+        for (int t = 0; t < T; t++) { s[t] = EXP(s[t] - mx); sum += s[t]; }                \
+        for (int t = 0; t < T; t++) s[t] /= sum;                                           \
+        for (int d = 0; d < D; d++) {                                                      \
+            REAL val = 0;                                                                  \
+            for (int t = 0; t < T; t++) val += s[t] * (REAL)vb[t * kv_stride + d];         \
+            oh[d] = (OUT_T)val;                                                            \
+        }                                                                                  \
+        free(s);                                                                           \
+    }
+
+#define OUT_T float
+void oracle_gqa_attention_f32(const float* q, const float* k, const float* v,
+                              const int32_t* seq_lens, float* out, int B, int H, int Hk,
+                              int D, int64_t seq_stride, float scale, int nthreads) {
+    GQA_PRE(float)
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(dynamic, 1) if (nthreads != 1)
+#endif
+    GQA_BODY(float, expf)
+}
+#undef OUT_T
+#define OUT_T double
+void oracle_gqa_attention_f64(const float* q, const float* k, const float* v,
+                              const int32_t* seq_lens, double* out, int B, int H, int Hk,
+                              int D, int64_t seq_stride, float scale) {
+    GQA_PRE(double)
+    GQA_BODY(double, exp)
+}
+#undef OUT_T
+
+/* ------------------------------------------------------------------ */
+/* GQA causal prefill (flash_prefill_attention semantics)              */
+/* ------------------------------------------------------------------ */
+/*
+ * q     [N][H][D]  (token-major Q_batch)
+ * k, v  [kv_len][Hk*D]
+ * out   [N][H][D]
+ * token i attends to keys [0, start + i]  (causal_len = start + i + 1,
+ * clipped to kv_len)
+ */
+#define PREFILL_PRE(REAL)                                                            \
+    int G = H / Hk;                                                                        \
+    int64_t kv_stride = (int64_t)Hk * D;                                                   \
+    /* the reference computes the scale in float (transformer.cpp:2444) */ \
+    REAL sc = (REAL)(scale > 0 ? scale : 1.0f / sqrtf((float)D));
+#define PREFILL_BODY(REAL, EXP)                                                            \
+    for (int64_t ih = 0; ih < (int64_t)N * H; ih++) {                                      \
+        int i = (int)(ih / H), h = (int)(ih % H);                                          \
+        int T = start + i + 1;                                                             \
+        if (T > kv_len) T = kv_len;                                                        \
+        const float* qh = q + ((int64_t)i * H + h) * D;                                    \
+        const float* kb = k + (int64_t)(h / G) * D;                                        \
+        const float* vb = v + (int64_t)(h / G) * D;                                        \
+        OUT_T* oh = out + ((int64_t)i * H + h) * D;                                        \
+        if (T <= 0) { for (int d = 0; d < D; d++) oh[d] = 0; continue; }                   \
+        REAL* s = (REAL*)malloc(sizeof(REAL) * (size_t)T);                                 \
+        for (int t = 0; t < T; t++) {                                                      \
+            REAL dot = 0;                                                                  \
+            for (int d = 0; d < D; d++) dot += (REAL)qh[d] * (REAL)kb[t * kv_stride + d]; \
+            s[t] = dot * sc;                                                               \
+        }                                                                                  \
+        REAL mx = s[0];                                                                    \
+        for (int t = 1; t < T; t++) if (s[t] > mx) mx = s[t];                              \
+        REAL sum = 0;                                                                      \
+        for (int t = 0; t < T; t++) { s[t] = EXP(s[t] - mx); sum += s[t]; }                \
+        for (int t = 0; t < T; t++) s[t] /= sum;                                           \
+        for (int d = 0; d < D; d++) {                                                      \
+            REAL val = 0;                                                                  \
+            for (int t = 0; t < T; t++) val += s[t] * (REAL)vb[t * kv_stride + d];         \
+            oh[d] = (OUT_T)val;                                                            \
+        }                                                                                  \
+        free(s);                                                                           \
+    }
+
+#define OUT_T float
+void oracle_gqa_prefill_f32(const float* q, const float* k, const float* v, float* out,
+                            int N, int H, int Hk, int D, int kv_len, int start, float scale,
+                            int nthreads) {
+    PREFILL_PRE(float)
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(dynamic, 1) if (nthreads != 1)
+#endif
+    PREFILL_BODY(float, expf)
+}
+#undef OUT_T
+#define OUT_T double
+void oracle_gqa_prefill_f64(const float* q, const float* k, const float* v, double* out,
+                            int N, int H, int Hk, int D, int kv_len, int start, float scale) {
+    PREFILL_PRE(double)
+    PREFILL_BODY(double, exp)
+}
+#undef OUT_T
+
+/* ------------------------------------------------------------------ */
+/* MLA absorbed attention over the latent cache (cpu_mla_attention)    */
+/* ------------------------------------------------------------------ */
+/*
+ * q       [B][q_len][H][kv_rank + rope]   absorbed query (q_nope.W_UK ++ q_rope)
+ * latent  sequence b at b*seq_stride; token t at t*(kv_rank + rope)
+ * out     [B][q_len][H][kv_rank]          o = sum_t p_t * c_t[0:kv_rank]
+ * query i of q_len sees T_i = seq_len[b] - q_len + i + 1 tokens
+ */
+#define MLA_PRE(REAL)                                                                      \
+    int C = kv_rank + rope;                                                                \
+    REAL sc = (REAL)scale;
+#define MLA_BODY(REAL, EXP)                                                                \
+    for (int64_t bqh = 0; bqh < (int64_t)B * q_len * H; bqh++) {                           \
+        int b = (int)(bqh / ((int64_t)q_len * H));                                         \
+        int qi = (int)((bqh / H) % q_len);                                                 \
+        int T = seq_lens[b] - q_len + qi + 1;                                              \
+        const float* qa = q + bqh * C;                                                     \
+        const float* cb = latent + b * seq_stride;                                         \
+        OUT_T* oh = out + bqh * kv_rank;                                                   \
+        if (T <= 0) { for (int d = 0; d < kv_rank; d++) oh[d] = 0; continue; }             \
+        REAL* s = (REAL*)malloc(sizeof(REAL) * (size_t)T);                                 \
+        for (int t = 0; t < T; t++) {                                                      \
+            const float* cs = cb + (int64_t)t * C;                                         \
+            REAL acc = 0;                                                                  \
+            for (int d = 0; d < kv_rank; d++) acc += (REAL)qa[d] * (REAL)cs[d];            \
+            for (int d = 0; d < rope; d++) acc += (REAL)qa[kv_rank + d] * (REAL)cs[kv_rank + d]; \
+            s[t] = acc * sc;                                                               \
+        }                                                                                  \
+        REAL mx = s[0];                                                                    \
+        for (int t = 1; t < T; t++) if (s[t] > mx) mx = s[t];                              \
+        REAL sum = 0;                                                                      \
+        for (int t = 0; t < T; t++) { s[t] = EXP(s[t] - mx); sum += s[t]; }                \
+        for (int t = 0; t < T; t++) s[t] /= sum;                                           \
+        REAL* o = (REAL*)calloc((size_t)kv_rank, sizeof(REAL));                            \
+        for (int t = 0; t < T; t++) {                                                      \
+            const float* cs = cb + (int64_t)t * C;                                         \
+            REAL w = s[t];                                                                 \
+            for (int d = 0; d < kv_rank; d++) o[d] += w * (REAL)cs[d];                     \
+        }                                                                                  \
+        for (int d = 0; d < kv_rank; d++) oh[d] = (OUT_T)o[d];                             \
+        free(o);                                                                           \
+        free(s);                                                                           \
+    }
+
+#define OUT_T float
+void oracle_mla_attention_f32(const float* q, const float* latent, const int32_t* seq_lens,
+                              float* out, int B, int q_len, int H, int kv_rank, int rope,
+                              int64_t seq_stride, float scale, int nthreads) {
+    MLA_PRE(float)
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(dynamic, 1) if (nthreads != 1)
+#endif
+    MLA_BODY(float, expf)
+}
+#undef OUT_T
+#define OUT_T double
+void oracle_mla_attention_f64(const float* q, const float* latent, const int32_t* seq_lens,
+                              double* out, int B, int q_len, int H, int kv_rank, int rope,
+                              int64_t seq_stride, float scale) {
+    MLA_PRE(double)
+    MLA_BODY(double, exp)
+}
+#undef OUT_T
+
+/* ------------------------------------------------------------------ */
+/* scatter_kv: dst[offset + i] = src[i] for i < count (16-bit elements) */
+/* ------------------------------------------------------------------ */
+void oracle_scatter_kv(const uint16_t* src, uint16_t* dst, int64_t offset, int64_t count) {
+    for (int64_t i = 0; i < count; i++) dst[offset + i] = src[i];
+}
+
+int oracle_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

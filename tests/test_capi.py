@@ -1,0 +1,123 @@
+"""C-ABI library checks that need no GPU: it loads, exports every function
+include/mugen_attn.h declares, and rejects bad arguments before touching
+the device (validation runs on the host)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from mugen_amd import _capi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    src = open(os.path.join(ROOT, "include", "mugen_attn.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(mugen_attn_\w+)\s*\(", src)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    L = _capi.lib()
+    declared = header_functions()
+    assert len(declared) >= 11
+    for name in declared:
+        assert hasattr(L, name), f"{name} declared in mugen_attn.h but not exported"
+    assert sorted(declared) == sorted(_capi.EXPORTS)
+    assert "gfx950" in _capi.version()
+
+
+def _gqa_args(**kw):
+    a = _capi.GqaDecodeArgs()
+    a.q = a.k_cache = a.v_cache = a.seq_lens = a.out = 0x1000
+    a.batch, a.n_heads, a.n_kv_heads, a.head_dim, a.max_seq_len = 1, 28, 4, 128, 4096
+    a.seq_stride, a.kv_dtype, a.out_dtype = 0, _capi.F16, _capi.F16
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def _call_gqa(a, ws=None, nbytes=0):
+    return _capi.lib().mugen_attn_gqa_decode(ctypes.byref(a), ws, nbytes, None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(q=0), _capi.E_INVALID),
+    (dict(n_heads=30), _capi.E_INVALID),          # not a multiple of n_kv_heads
+    (dict(head_dim=96), _capi.E_UNSUPPORTED),
+    (dict(n_heads=68, n_kv_heads=4), _capi.E_UNSUPPORTED),  # G = 17 > 16
+    (dict(kv_dtype=_capi.F32), _capi.E_UNSUPPORTED),
+    (dict(batch=2, seq_stride=10), _capi.E_INVALID),
+    (dict(q=0x1002), _capi.E_INVALID),            # misaligned
+])
+def test_gqa_decode_rejects_bad_args(kw, code):
+    assert _call_gqa(_gqa_args(**kw)) == code
+    assert _capi.lib().mugen_attn_last_error().decode()
+
+
+def test_gqa_workspace_size_and_missing_workspace():
+    a = _gqa_args()
+    need = _capi.lib().mugen_attn_gqa_decode_workspace_size(ctypes.byref(a))
+    assert need > 0
+    assert _call_gqa(a) == _capi.E_WORKSPACE
+    assert "workspace" in _capi.lib().mugen_attn_last_error().decode()
+    a1 = _gqa_args(num_splits=1)
+    assert _capi.lib().mugen_attn_gqa_decode_workspace_size(ctypes.byref(a1)) == 0
+
+
+def _mla_args(**kw):
+    a = _capi.MlaDecodeArgs()
+    a.q = a.latent = a.seq_lens = a.out = 0x1000
+    a.batch, a.q_len, a.n_heads, a.kv_rank, a.rope_dim = 8, 1, 128, 512, 64
+    a.max_seq_len, a.seq_stride, a.scale = 8192, 8192 * 576, 0.0721
+    a.q_dtype = a.latent_dtype = _capi.BF16
+    a.out_dtype = _capi.F32
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(latent=0), _capi.E_INVALID),
+    (dict(kv_rank=256), _capi.E_UNSUPPORTED),
+    (dict(scale=0.0), _capi.E_INVALID),
+    (dict(q_dtype=_capi.F16), _capi.E_UNSUPPORTED),  # neither f32 nor the latent dtype
+    (dict(seq_stride=100), _capi.E_INVALID),
+])
+def test_mla_rejects_bad_args(kw, code):
+    a = _mla_args(**kw)
+    assert _capi.lib().mugen_attn_mla_decode(ctypes.byref(a), None, 0, None) == code
+
+
+def test_mla_workspace():
+    a = _mla_args()
+    need = _capi.lib().mugen_attn_mla_decode_workspace_size(ctypes.byref(a))
+    assert need >= 8 * 128 * 512 * 4
+    assert _capi.lib().mugen_attn_mla_decode(ctypes.byref(a), None, 0, None) == _capi.E_WORKSPACE
+
+
+def test_prefill_rejects_bad_args():
+    a = _capi.GqaPrefillArgs()
+    a.q = a.k = a.v = a.out = 0x1000
+    a.n_tokens, a.n_heads, a.n_kv_heads, a.head_dim, a.kv_len, a.start_pos, a.causal = 512, 32, 8, 64, 100, 0, 1
+    a.dtype = a.out_dtype = _capi.BF16
+    assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.E_INVALID  # kv_len < N
+    a.kv_len, a.head_dim = 512, 80
+    assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.E_UNSUPPORTED
+    a.head_dim, a.n_tokens = 64, 0
+    assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.OK  # nothing to do
+
+
+def test_scatter_kv_validation():
+    assert _capi.lib().mugen_attn_scatter_kv(None, None, 0, 0, None) == _capi.OK
+    assert _capi.lib().mugen_attn_scatter_kv(None, None, 0, 5, None) == _capi.E_INVALID
+
+
+def test_python_front_end_refuses_cpu_tensors():
+    import torch
+    import mugen_amd
+    q = torch.zeros(1, 4, 64, dtype=torch.float16)
+    k = torch.zeros(1, 8, 1, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="device tensors"):
+        mugen_amd.attention_decode(q, k, k, torch.ones(1, dtype=torch.int32))

@@ -1,0 +1,92 @@
+"""MLA absorbed decode / verify on the GPU vs the CPU oracle
+(latent core of cpu_mla_attention)."""
+import numpy as np
+import pytest
+import torch
+
+import mugen_amd
+from oracle import oracle as O
+from tests import cases as C
+
+pytestmark = pytest.mark.gpu
+
+
+def run_gpu(c, device, out_dtype=C.F32, num_splits=0, seq_lens=None, q=None):
+    sl_np = c["seq_lens"] if seq_lens is None else np.asarray(seq_lens, np.int32)
+    C.say(f"mla B={c['B']} q_len={c['q_len']} H={c['H']} maxT={c['max_T']} q={c['q_dtype']} "
+          f"lat={c['lat_dtype']} out={out_dtype} splits={num_splits} lens={list(sl_np)[:8]}")
+    if q is None:
+        q = C.to_dev(c["q"] if c["q_dtype"] == C.F32 else c["qb"], c["q_dtype"], device)
+    lat = C.to_dev(c["latb"], c["lat_dtype"], device)
+    sl = torch.from_numpy(sl_np).to(device)
+    out = mugen_amd.mla_attention(q, lat, sl, c["max_T"], scale=C.MLA_SCALE,
+                                  out_dtype=C.torch_dtype(out_dtype), num_splits=num_splits)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def test_v2lite_decode_config(device):
+    # B=1, H=16, q f32 ~N(0,1), latent fp16 [1024x576] ~N(0,0.5)
+    c = C.mla_case(42, 1, 1, 16, [1024], q_dtype=C.F32, lat_dtype=C.F16)
+    ref = C.mla_ref(c)
+    for splits in (0, 1):
+        C.assert_close(run_gpu(c, device, C.F32, splits), ref, f"v2-lite splits={splits}")
+
+
+def test_v3_decode_config(device):
+    # B=8, H=128, bf16, T ~ U[1024, 8192]
+    lens = O.randint(45, 8, 1024, 8192)
+    c = C.mla_case(45, 8, 1, 128, lens, max_T=8192, q_dtype=C.BF16, lat_dtype=C.BF16)
+    ref = C.mla_ref(c, nthreads=8)
+    C.assert_close(run_gpu(c, device), ref, "v3 decode")
+
+
+def test_v3_verify_config_sampled_heads_and_causal_consistency(device):
+    # B=4, q_len=5, H=128, T=32768; the oracle checks a head sample,
+    # and every verify row must equal a decode call at seq_len T-5+i+1
+    T = 32768
+    c = C.mla_case(46, 4, 5, 128, [T] * 4, q_dtype=C.BF16, lat_dtype=C.BF16)
+    got = run_gpu(c, device)
+    heads = [0, 1, 63, 64, 127]
+    ref = C.mla_ref(c, nthreads=8, heads=heads)
+    C.assert_close(got[:, :, heads, :], ref, "v3 verify (sampled heads)")
+    qdev = C.to_dev(c["qb"], C.BF16, device)
+    for i in range(5):
+        qi = qdev[:, i:i + 1].contiguous()
+        dec = run_gpu(dict(c, q_len=1), device, seq_lens=[T - 5 + i + 1] * 4, q=qi)
+        np.testing.assert_allclose(got[:, i:i + 1], dec, atol=5e-5, rtol=1e-4)
+
+
+@pytest.mark.parametrize("B,q_len,H,lens,qdt,ldt", [
+    (3, 1, 16, [1, 31, 33], C.F32, C.F16),
+    (2, 1, 20, [64, 0], C.BF16, C.BF16),
+    (2, 3, 7, [3, 100], C.F32, C.BF16),
+    (1, 5, 128, [4], C.BF16, C.BF16),      # q_len > visible tokens for the first rows
+    (2, 2, 64, [700, 129], C.F16, C.F16),
+])
+def test_edges(device, B, q_len, H, lens, qdt, ldt):
+    c = C.mla_case(47 + H, B, q_len, H, lens, q_dtype=qdt, lat_dtype=ldt)
+    ref = C.mla_ref(c)
+    for splits in (0, 1, 4):
+        C.assert_close(run_gpu(c, device, C.F32, splits), ref, f"mla edge splits={splits}")
+
+
+@pytest.mark.parametrize("od", [C.F16, C.BF16])
+def test_16bit_outputs(device, od):
+    c = C.mla_case(48, 2, 1, 32, [500, 900], q_dtype=C.BF16, lat_dtype=C.BF16)
+    C.assert_close(run_gpu(c, device, od), C.mla_ref(c), f"out dtype {od}")
+
+
+def test_split_count_invariance(device):
+    c = C.mla_case(49, 2, 1, 128, [5000, 2100], q_dtype=C.BF16, lat_dtype=C.BF16)
+    outs = [run_gpu(c, device, C.F32, s) for s in (1, 0, 9, 100)]
+    for o in outs[1:]:
+        np.testing.assert_allclose(o, outs[0], atol=2e-5, rtol=1e-4)
+
+
+def test_golden_fixture(device):
+    fx = np.load(C.golden_path("mla_verify_small.npz"))
+    c = dict(B=int(fx["B"]), q_len=int(fx["q_len"]), H=int(fx["H"]), max_T=int(fx["max_T"]),
+             q_dtype=int(fx["q_dtype"]), lat_dtype=int(fx["lat_dtype"]), q=fx["q"], qb=fx["qb"],
+             latb=fx["latb"], seq_lens=fx["seq_lens"])
+    C.assert_close(run_gpu(c, device), fx["out_f64"], "golden mla_verify_small")

@@ -1,0 +1,234 @@
+"""Pins of the CPU oracle (CPU only).
+
+The reference ships no golden vectors or attention tests for this path, so
+each oracle function is pinned by checks chosen so that a plausible
+mistake (dropped term, wrong head map, wrong causal bound, transposed
+operand, missing normalisation) fails at least one of them:
+  * known answers: the C++ standard's mt19937_64 outputs; IEEE rounding
+    against numpy/torch conversions;
+  * an independent fp64 numpy formulation (vectorised, masked softmax);
+  * closed forms: T=1 -> V_0; q=0 or identical keys -> mean(V); a dominant
+    score -> V of the argmax; T=0 -> 0;
+  * invariants: KV permutation, GQA head map, prefill row == decode at
+    seq_len start+t+1, MLA verify row == decode at seq_len T-q_len+i+1,
+    MLA == MQA with one 576-dim kv head and V = latent[:, :512].
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests import cases as C
+
+
+# ------------------------------------------------------------ generator / dtypes
+
+def test_mt19937_64_known_answers():
+    # std::mt19937_64 default seed 5489: first output and the 10000th
+    # ([rand.predef] requires 9981545732273789042 for the latter)
+    assert O.lib().oracle_mt64_first(5489, 0) == 14514284786278117030
+    assert O.lib().oracle_mt64_first(5489, 9999) == 9981545732273789042
+
+
+def test_randn_moments_and_determinism():
+    x = O.randn(42, (200_000,))
+    assert abs(float(x.mean())) < 0.01 and abs(float(x.std()) - 1.0) < 0.01
+    np.testing.assert_array_equal(x, O.randn(42, (200_000,)))
+    y = O.randn(7, (1001,), 3.0, 0.5)
+    assert abs(float(y.mean()) - 3.0) < 0.1
+
+
+def test_randint_range():
+    r = O.randint(43, 10000, 256, 4096)
+    assert r.min() >= 256 and r.max() <= 4096 and len(np.unique(r)) > 3000
+
+
+def test_f16_rounding_matches_numpy():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(20000).astype(np.float32) * s for s in (1e-6, 1e-3, 1, 100, 3e4)])
+    x = np.concatenate([x, np.array([0.0, -0.0, 65504, 65520, 1e9, 5.96e-8, 2.98e-8, 6.1e-5], np.float32)])
+    v, bits = O.round_to(x, O.F16)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16)
+    np.testing.assert_array_equal(bits, ref.view(np.uint16))
+    np.testing.assert_array_equal(v, ref.astype(np.float32))
+
+
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.standard_normal(50000).astype(np.float32) * s for s in (1e-30, 1, 1e30)])
+    v, bits = O.round_to(x, O.BF16)
+    ref = torch.from_numpy(x).to(torch.bfloat16)
+    np.testing.assert_array_equal(bits, ref.view(torch.int16).numpy().view(np.uint16))
+    np.testing.assert_array_equal(v, ref.float().numpy())
+
+
+# ------------------------------------------------------------ GQA decode
+
+@pytest.mark.parametrize("B,H,Hk,D,lens", [
+    (1, 4, 4, 64, [37]),
+    (3, 28, 4, 128, [1, 130, 77]),
+    (2, 8, 1, 64, [200, 5]),
+    (2, 16, 2, 128, [0, 33]),
+])
+def test_gqa_oracle_vs_fp64_bruteforce(B, H, Hk, D, lens):
+    c = C.gqa_decode_case(11, B, H, Hk, D, lens)
+    ref = O.gqa_attention_np64(c["q"], c["k"], c["v"], c["seq_lens"], H, Hk, D, c["seq_stride"])
+    got32 = C.gqa_decode_ref(c)
+    got64 = C.gqa_decode_ref(c, f64=True)
+    np.testing.assert_allclose(got64, ref, atol=1e-12, rtol=1e-10)
+    np.testing.assert_allclose(got32, ref, atol=2e-6, rtol=1e-4)
+
+
+def test_gqa_closed_forms():
+    H, Hk, D, T = 8, 2, 64, 50
+    c = C.gqa_decode_case(3, 1, H, Hk, D, [T])
+    G = H // Hk
+    # T = 1 -> out = V_0 of the head's kv group (exact in fp32)
+    out1 = O.gqa_attention(c["q"], c["k"], c["v"], [1], H, Hk, D, c["seq_stride"])
+    for h in range(H):
+        np.testing.assert_array_equal(out1[0, h], c["v"][0, 0, h // G])
+    # q = 0 -> uniform weights -> mean of V rows
+    out0 = O.gqa_attention(np.zeros_like(c["q"]), c["k"], c["v"], [T], H, Hk, D, c["seq_stride"], f64=True)
+    for h in range(H):
+        np.testing.assert_allclose(out0[0, h], c["v"][0, :T, h // G].astype(np.float64).mean(0), atol=1e-12)
+    # identical keys -> mean of V rows
+    k_same = np.repeat(c["k"][:, :1], c["max_T"], axis=1).copy()
+    outk = O.gqa_attention(c["q"], k_same, c["v"], [T], H, Hk, D, c["seq_stride"], f64=True)
+    np.testing.assert_allclose(outk[0], out0[0], atol=1e-12)
+    # one dominant score -> that row's V
+    k_dom = c["k"].copy()
+    k_dom[0, 17] = 0.0
+    q_dom = np.zeros_like(c["q"])
+    q_dom[0, :, 0] = 1.0
+    k_dom[0, :, :, 0] = 0.0
+    k_dom[0, 17, :, 0] = 1000.0
+    outd = O.gqa_attention(q_dom, k_dom, c["v"], [T], H, Hk, D, c["seq_stride"], f64=True)
+    for h in range(H):
+        np.testing.assert_allclose(outd[0, h], c["v"][0, 17, h // G], atol=1e-12)
+    # T = 0 -> zeros (documented departure: reference is undefined)
+    assert np.all(O.gqa_attention(c["q"], c["k"], c["v"], [0], H, Hk, D, c["seq_stride"]) == 0)
+
+
+def test_gqa_permutation_and_head_map():
+    H, Hk, D, T = 12, 3, 64, 40
+    c = C.gqa_decode_case(5, 1, H, Hk, D, [T])
+    perm = np.random.default_rng(0).permutation(T)
+    kp = c["k"].copy()
+    vp = c["v"].copy()
+    kp[0, :T] = c["k"][0, perm]
+    vp[0, :T] = c["v"][0, perm]
+    a = O.gqa_attention(c["q"], c["k"], c["v"], [T], H, Hk, D, c["seq_stride"], f64=True)
+    b = O.gqa_attention(c["q"], kp, vp, [T], H, Hk, D, c["seq_stride"], f64=True)
+    np.testing.assert_allclose(a, b, atol=1e-12)
+    # head h reads kv head h // (H/Hk): moving one kv head changes exactly its G query heads
+    k2 = c["k"].copy()
+    k2[0, :, 1] += np.random.default_rng(1).standard_normal(k2[0, :, 1].shape).astype(np.float32)
+    b2 = O.gqa_attention(c["q"], k2, c["v"], [T], H, Hk, D, c["seq_stride"], f64=True)
+    changed = np.abs(b2 - a).max(axis=-1)[0] > 1e-9
+    assert list(np.nonzero(changed)[0]) == [4, 5, 6, 7]
+
+
+# ------------------------------------------------------------ prefill
+
+@pytest.mark.parametrize("N,H,Hk,D,start", [(9, 4, 2, 64, 0), (20, 8, 8, 128, 13), (33, 6, 2, 64, 3)])
+def test_prefill_oracle_vs_fp64_bruteforce(N, H, Hk, D, start):
+    c = C.prefill_case(21, N, H, Hk, D, start)
+    ref = O.gqa_prefill_np64(c["q"], c["k"], c["v"], N, H, Hk, D, c["kv_len"], start)
+    np.testing.assert_allclose(C.prefill_ref(c, f64=True), ref, atol=1e-12, rtol=1e-10)
+    np.testing.assert_allclose(C.prefill_ref(c), ref, atol=2e-6, rtol=1e-4)
+
+
+def test_prefill_row_equals_decode_at_causal_len():
+    N, H, Hk, D, start = 12, 8, 2, 64, 5
+    c = C.prefill_case(22, N, H, Hk, D, start)
+    pre = C.prefill_ref(c, f64=True)
+    kv = c["kv_len"]
+    for t in range(N):
+        dec = O.gqa_attention(c["q"][t][None], c["k"].reshape(1, kv, Hk, D), c["v"].reshape(1, kv, Hk, D),
+                              [start + t + 1], H, Hk, D, kv * Hk * D, f64=True)
+        np.testing.assert_array_equal(pre[t], dec[0])
+
+
+# ------------------------------------------------------------ MLA
+
+@pytest.mark.parametrize("B,q_len,H,lens", [(1, 1, 4, [70]), (2, 3, 5, [40, 3]), (2, 1, 2, [0, 9])])
+def test_mla_oracle_vs_fp64_bruteforce(B, q_len, H, lens):
+    c = C.mla_case(31, B, q_len, H, lens, q_dtype=O.F32, lat_dtype=O.F16)
+    ref = O.mla_attention_np64(c["q"], c["lat"], c["seq_lens"], q_len, H, C.MLA_SCALE)
+    np.testing.assert_allclose(C.mla_ref(c, f64=True), ref, atol=1e-12, rtol=1e-10)
+    np.testing.assert_allclose(C.mla_ref(c), ref, atol=2e-6, rtol=1e-4)
+
+
+def test_mla_equals_mqa_with_one_576_dim_head():
+    # MLA latent core == MQA with Hk=1, d_qk=576 and V = latent[:, :512]
+    T, H = 60, 6
+    c = C.mla_case(32, 1, 1, H, [T], q_dtype=O.F32, lat_dtype=O.BF16)
+    mla = C.mla_ref(c, f64=True)[0, 0]
+    k = c["lat"].reshape(1, T, 1, 576)
+    v = k.copy()
+    v[..., 512:] = 0.0
+    mqa = O.gqa_attention(c["q"].reshape(1, H, 576), k, v, [T], H, 1, 576, T * 576, C.MLA_SCALE, f64=True)[0]
+    np.testing.assert_array_equal(mla, mqa[:, :512])
+    np.testing.assert_array_equal(mqa[:, 512:], 0.0)
+
+
+def test_mla_closed_forms():
+    H = 3
+    c = C.mla_case(33, 1, 1, H, [1], max_T=8, q_dtype=O.F32, lat_dtype=O.F16)
+    out = C.mla_ref(c)
+    for h in range(H):  # T = 1 -> c_0[0:512]
+        np.testing.assert_array_equal(out[0, 0, h], c["lat"][0, 0, :512])
+    q0 = dict(c, q=np.zeros_like(c["q"]), seq_lens=np.array([8], np.int32))
+    out0 = C.mla_ref(q0, f64=True)
+    np.testing.assert_allclose(out0[0, 0, 0], c["lat"][0, :8, :512].astype(np.float64).mean(0), atol=1e-12)
+    # the rope part of the score matters: q_rope . k_rope alone selects a token
+    qr = np.zeros_like(c["q"])
+    lat = c["lat"].copy()
+    lat[0, :, 512:] = 0.0
+    lat[0, 5, 512] = 1.0
+    qr[0, 0, :, 512] = 4000.0
+    outr = O.mla_attention(qr, lat, [8], 1, H, C.MLA_SCALE, seq_stride=8 * 576, f64=True)
+    np.testing.assert_allclose(outr[0, 0, 1], lat[0, 5, :512], atol=1e-12)
+
+
+def test_mla_verify_row_equals_decode_at_causal_len():
+    B, q_len, H, T = 2, 5, 4, 50
+    c = C.mla_case(34, B, q_len, H, [T, 7], max_T=T, q_dtype=O.F32, lat_dtype=O.BF16)
+    ver = C.mla_ref(c, f64=True)
+    for b in range(B):
+        for i in range(q_len):
+            Ti = int(c["seq_lens"][b]) - q_len + i + 1
+            dec = O.mla_attention(c["q"][b:b + 1, i:i + 1].copy(), c["lat"][b:b + 1].copy(), [Ti], 1, H,
+                                  C.MLA_SCALE, seq_stride=T * 576, f64=True)
+            np.testing.assert_array_equal(ver[b, i], dec[0, 0])
+
+
+# ------------------------------------------------------------ scatter_kv
+
+def test_scatter_kv_oracle():
+    src = np.arange(100, dtype=np.uint16)
+    dst = np.full(1000, 7, np.uint16)
+    out = O.scatter_kv(src, dst, 321, 100)
+    np.testing.assert_array_equal(out[321:421], src)
+    assert np.all(out[:321] == 7) and np.all(out[421:] == 7)
+
+
+# ------------------------------------------------------------ committed fixtures
+
+def test_golden_fixtures_reproduce():
+    fx = np.load(C.golden_path("gqa_decode_small.npz"))
+    q, k, v = (O.bits_to_f32(fx[n], int(fx["dtype"])) for n in ("qb", "kb", "vb"))
+    out = O.gqa_attention(q, k, v, fx["seq_lens"], int(fx["H"]), int(fx["Hk"]), int(fx["D"]),
+                          int(fx["max_T"]) * int(fx["Hk"]) * int(fx["D"]))
+    np.testing.assert_array_equal(out, fx["out_f32"])
+    fx = np.load(C.golden_path("prefill_small.npz"))
+    q, k, v = (O.bits_to_f32(fx[n], int(fx["dtype"])) for n in ("qb", "kb", "vb"))
+    N, kv = int(fx["N"]), int(fx["N"]) + int(fx["start"])
+    out = O.gqa_prefill(q, k, v, N, int(fx["H"]), int(fx["Hk"]), int(fx["D"]), kv, int(fx["start"]))
+    np.testing.assert_array_equal(out, fx["out_f32"])
+    fx = np.load(C.golden_path("mla_verify_small.npz"))
+    lat = O.bits_to_f32(fx["latb"], int(fx["lat_dtype"]))
+    out = O.mla_attention(fx["q"], lat, fx["seq_lens"], int(fx["q_len"]), int(fx["H"]), C.MLA_SCALE,
+                          seq_stride=int(fx["max_T"]) * 576)
+    np.testing.assert_array_equal(out, fx["out_f32"])

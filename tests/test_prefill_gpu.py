@@ -1,0 +1,57 @@
+"""GQA causal prefill on the GPU vs the CPU oracle (flash_prefill_attention
+semantics)."""
+import numpy as np
+import pytest
+import torch
+
+import mugen_amd
+from tests import cases as C
+
+pytestmark = pytest.mark.gpu
+
+
+def run_gpu(c, device, out_dtype=None, causal=True):
+    out_dtype = c["dtype"] if out_dtype is None else out_dtype
+    C.say(f"prefill N={c['N']} H={c['H']} Hk={c['Hk']} D={c['D']} start={c['start']} dtype={c['dtype']} "
+          f"out={out_dtype} causal={causal}")
+    q = C.to_dev(c["qb"], c["dtype"], device)
+    k = C.to_dev(c["kb"], c["dtype"], device)
+    v = C.to_dev(c["vb"], c["dtype"], device)
+    out = mugen_amd.flash_prefill_attention(q, k, v, c["start"], causal=causal,
+                                            out_dtype=C.torch_dtype(out_dtype))
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def test_llama1b_config(device):
+    # N=512, H=32, Hk=8, D=64, bf16, causal
+    c = C.prefill_case(44, 512, 32, 8, 64, 0, C.BF16)
+    ref = C.prefill_ref(c, nthreads=8)
+    C.assert_close(run_gpu(c, device), ref, "llama-1b prefill bf16 out")
+    C.assert_close(run_gpu(c, device, C.F32), ref, "llama-1b prefill f32 out")
+
+
+@pytest.mark.parametrize("N,H,Hk,D,start,dtype", [
+    (1, 8, 2, 64, 0, C.F16), (17, 4, 4, 128, 0, C.BF16), (40, 28, 4, 128, 100, C.F16),
+    (100, 16, 2, 64, 7, C.BF16), (65, 12, 3, 64, 0, C.F16), (200, 8, 1, 128, 300, C.BF16),
+])
+def test_shapes_and_offsets(device, N, H, Hk, D, start, dtype):
+    c = C.prefill_case(50 + N, N, H, Hk, D, start, dtype)
+    C.assert_close(run_gpu(c, device, C.F32), C.prefill_ref(c), f"prefill N={N} start={start}")
+
+
+def test_non_causal(device):
+    c = C.prefill_case(51, 33, 8, 2, 64, 0, C.F16)
+    from oracle import oracle as O
+    # non-causal == every row sees all kv_len keys == decode over the whole cache
+    ref = O.gqa_attention(c["q"], c["k"].reshape(1, c["kv_len"], 2, 64).repeat(33, 0),
+                          c["v"].reshape(1, c["kv_len"], 2, 64).repeat(33, 0), [c["kv_len"]] * 33, 8, 2, 64,
+                          c["kv_len"] * 2 * 64)
+    C.assert_close(run_gpu(c, device, C.F32, causal=False), ref, "non-causal")
+
+
+def test_golden_fixture(device):
+    fx = np.load(C.golden_path("prefill_small.npz"))
+    c = dict(N=int(fx["N"]), H=int(fx["H"]), Hk=int(fx["Hk"]), D=int(fx["D"]), start=int(fx["start"]),
+             dtype=int(fx["dtype"]), qb=fx["qb"], kb=fx["kb"], vb=fx["vb"])
+    C.assert_close(run_gpu(c, device, C.F32), fx["out_f64"], "golden prefill_small")
