@@ -1,0 +1,265 @@
+"""Benchmark of the MI355X attention subsystem (one GPU).
+
+Headline workload (the metric's north-star case): MLA absorbed decode at
+DeepSeek-V3 shape -- batch 8, 128 heads, q_len 1, bf16 absorbed queries
+~N(0,1), bf16 latent cache of 576 dims per token ~N(0,0.5), context
+lengths uniform in [1024, 8192], scale 1/sqrt(192), split-K with fp32
+log-sum-exp combine, fp32 output.  One step = one layer's attention call
+(main kernel + combine) with all inputs resident in HBM.
+
+value = algorithmic HBM bytes of the step / step time (GB/s):
+  sum_b T_b*576*2 (latent) + B*H*576*2 (q) + B*H*512*4 (out).
+The other BASELINE configs are measured the same way and reported under
+"configs" (us per layer-step plus GB/s or TFLOP/s).
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only NAME]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import mugen_amd  # noqa: E402
+from mugen_amd import _capi  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0     # MI355X HBM3E
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+METRIC = json.load(open(os.path.join(ROOT, "BASELINE.json")))["metric"]
+MLA_SCALE = 1.0 / math.sqrt(192.0)
+
+
+def seeded_lens(seed, n, lo, hi):
+    g = np.random.default_rng(seed)
+    return g.integers(lo, hi + 1, n).astype(np.int32)
+
+
+def randn(shape, std, dtype, gen, dev):
+    return (torch.randn(shape, generator=gen, device=dev, dtype=torch.float32) * std).to(dtype)
+
+
+class Case:
+    name = ""
+    kernel = ""          # dominant kernel's timing name
+    bound = "hbm"
+    unit = "GB/s"
+
+    def step(self):
+        raise NotImplementedError
+
+
+class MlaDecode(Case):
+    bound = "hbm"
+    kernel = "mla_decode"
+
+    def __init__(self, dev, B, H, q_len, lens, max_T, q_dtype, lat_dtype, seed, name):
+        self.name = name
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.B, self.H, self.q_len = B, H, q_len
+        self.lens = np.asarray(lens, np.int32)
+        self.q = randn((B, q_len, H, 576), 1.0, q_dtype, g, dev)
+        self.lat = randn((B, max_T, 576), 0.5, lat_dtype, g, dev)
+        self.sl = torch.from_numpy(self.lens).to(dev)
+        self.max_T = max_T
+        self.out = torch.empty((B, q_len, H, 512), dtype=torch.float32, device=dev)
+        self.ws = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
+        esz_q = self.q.element_size()
+        self.bytes = float(self.lens.sum()) * 576 * self.lat.element_size() + B * q_len * H * (576 * esz_q + 512 * 4)
+        vis = sum(int(T) - q_len + i + 1 for T in self.lens for i in range(q_len))
+        self.flops = 2.0 * H * (576 + 512) * vis
+        if q_len > 1:
+            self.bound, self.unit = "mfma", "TFLOP/s"
+
+    def step(self):
+        mugen_amd.mla_attention(self.q, self.lat, self.sl, self.max_T, scale=MLA_SCALE, out=self.out,
+                                workspace=self.ws)
+
+    def cpu_sample(self, seconds_target=10.0):
+        """Time the oracle (single-thread C port of cpu_mla_attention's core)
+        on whole sequences of this workload until ~seconds_target of work;
+        returns (bytes_per_s_equivalent, description)."""
+        from oracle import oracle as O
+        done_rows_tok = 0.0
+        elapsed = 0.0
+        nseq = 0
+        for b in range(self.B):
+            q = self.q[b:b + 1].float().cpu().numpy()
+            T = int(self.lens[b])
+            lat = self.lat[b:b + 1, :T].float().cpu().numpy()
+            t0 = time.perf_counter()
+            O.mla_attention(q, lat, [T], self.q_len, self.H, MLA_SCALE, seq_stride=T * 576, nthreads=1)
+            elapsed += time.perf_counter() - t0
+            done_rows_tok += self.H * sum(T - self.q_len + i + 1 for i in range(self.q_len))
+            nseq += 1
+            if elapsed > seconds_target:
+                break
+        total_rows_tok = self.H * sum(int(T) - self.q_len + i + 1 for T in self.lens for i in range(self.q_len))
+        full_s = elapsed * total_rows_tok / done_rows_tok
+        return full_s, f"{nseq} of {self.B} sequences (all {self.H} heads), scaled by row-tokens"
+
+
+class GqaDecode(Case):
+    bound = "hbm"
+    kernel = "gqa_decode"
+
+    def __init__(self, dev, B, H, Hk, D, lens, max_T, seed, name):
+        self.name = name
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.lens = np.asarray(lens, np.int32)
+        self.q = randn((B, H, D), 1.0, torch.float16, g, dev)
+        self.k = randn((B, max_T, Hk, D), 1.0, torch.float16, g, dev)
+        self.v = randn((B, max_T, Hk, D), 1.0, torch.float16, g, dev)
+        self.sl = torch.from_numpy(self.lens).to(dev)
+        self.max_T = max_T
+        self.out = torch.empty((B, H, D), dtype=torch.float16, device=dev)
+        self.ws = torch.empty(1 << 26, dtype=torch.uint8, device=dev)
+        self.bytes = float(self.lens.sum()) * Hk * D * 2 * 2 + B * H * D * 2 * 2
+        self.flops = 4.0 * H * D * float(self.lens.sum())
+
+    def step(self):
+        mugen_amd.attention_decode(self.q, self.k, self.v, self.sl, self.max_T, out=self.out, workspace=self.ws)
+
+
+class Prefill(Case):
+    bound = "mfma"
+    unit = "TFLOP/s"
+    kernel = "gqa_prefill"
+
+    def __init__(self, dev, N, H, Hk, D, seed, name):
+        self.name = name
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.q = randn((N, H, D), 1.0, torch.bfloat16, g, dev)
+        self.k = randn((N, Hk, D), 1.0, torch.bfloat16, g, dev)
+        self.v = randn((N, Hk, D), 1.0, torch.bfloat16, g, dev)
+        self.out = torch.empty((N, H, D), dtype=torch.bfloat16, device=dev)
+        self.flops = 4.0 * H * D * N * (N + 1) / 2
+        self.bytes = (N * H * D * 2) * 2 + N * Hk * D * 2 * 2
+
+    def step(self):
+        mugen_amd.flash_prefill_attention(self.q, self.k, self.v, 0, out=self.out)
+
+
+def time_case(case, steps, warmup, dev):
+    for _ in range(warmup):
+        case.step()
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        case.step()
+    e1.record()
+    torch.cuda.synchronize(dev)
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ms = e0.elapsed_time(e1) / steps
+    # per-kernel durations (HIP events around each launch, on the launch stream)
+    _capi.timing_reset()
+    _capi.timing_enable(True)
+    for _ in range(steps):
+        case.step()
+    torch.cuda.synchronize(dev)
+    _capi.timing_enable(False)
+    k_ms, k_n = _capi.timing_read(case.kernel)
+    c_ms, c_n = _capi.timing_read(case.kernel + "_combine")
+    return dict(ms_per_step=ms, wall_ms=wall_ms, kernel_ms=k_ms / max(k_n, 1),
+                combine_ms=(c_ms / c_n) if c_n else 0.0)
+
+
+def rate(case, ms):
+    if case.unit == "TFLOP/s":
+        return case.flops / (ms * 1e-3) / 1e12
+    return case.bytes / (ms * 1e-3) / 1e9
+
+
+def load_traffic(kernel, workload):
+    path = os.path.join(ROOT, "profiles", f"{kernel}__{workload}.traffic.json")
+    if os.path.exists(path):
+        try:
+            return json.load(open(path)).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default=None, help="run only the named workload")
+    ap.add_argument("--headline-only", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of it "
+                          "(see DESIGN.md for how the path would shard)", "n_gpus": args.gpus}))
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    head = MlaDecode(dev, 8, 128, 1, seeded_lens(45, 8, 1024, 8192), 8192, torch.bfloat16, torch.bfloat16, 45,
+                     "mla_decode_v3")
+    cases = [head]
+    if not args.headline_only:
+        cases += [
+            MlaDecode(dev, 1, 16, 1, [1024], 1024, torch.float32, torch.float16, 42, "mla_decode_v2lite"),
+            GqaDecode(dev, 1, 28, 4, 128, [4096], 4096, 43, "gqa_decode_qwen7b_b1"),
+            GqaDecode(dev, 16, 28, 4, 128, seeded_lens(44, 16, 256, 4096), 4096, 44, "gqa_decode_qwen7b_b16"),
+            Prefill(dev, 512, 32, 8, 64, 46, "gqa_prefill_llama1b"),
+            MlaDecode(dev, 4, 128, 5, [32768] * 4, 32768, torch.bfloat16, torch.bfloat16, 47, "mla_verify_v3"),
+        ]
+    if args.only:
+        cases = [c for c in cases if c.name == args.only]
+    results = {}
+    for c in cases:
+        print(f"# timing {c.name}", file=sys.stderr, flush=True)
+        t = time_case(c, args.steps, args.warmup, dev)
+        results[c.name] = dict(
+            us_per_step=round(t["ms_per_step"] * 1e3, 3),
+            kernel_us=round(t["kernel_ms"] * 1e3, 3),
+            combine_us=round(t["combine_ms"] * 1e3, 3),
+            rate=round(rate(c, t["ms_per_step"]), 2), unit=c.unit,
+            kernel_rate=round(rate(c, t["kernel_ms"]), 2),
+            frac_of_peak=round(rate(c, t["ms_per_step"]) / (PEAK_HBM_GBS if c.unit == "GB/s" else PEAK_BF16_TFLOPS), 4),
+            algorithmic_bytes=c.bytes, algorithmic_flops=c.flops)
+
+    h = results.get(head.name) if head in cases else None
+    line = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded torch.randn: q ~N(0,1), latent ~N(0,0.5); ctx lens seeded U[1024,8192])",
+            "config": {"workload": "mla_absorbed_decode_deepseek_v3", "batch": 8, "n_heads": 128, "q_len": 1,
+                       "latent_dim": 576, "kv_rank": 512, "ctx_lens": [int(x) for x in head.lens],
+                       "max_ctx": 8192, "split_k": "auto", "out_dtype": "f32"}}
+    if h:
+        line["value"] = h["rate"]
+        line["ms_per_step"] = round(h["us_per_step"] / 1e3, 6)
+        line["us_per_layer_step"] = h["us_per_step"]
+        kb = head.bytes
+        ach = kb / (h["kernel_us"] * 1e-6) / 1e9
+        line["roofline"] = {"bound": "hbm", "kernel": "mla_decode", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS,
+                            "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4),
+                            "traffic": load_traffic("mla_decode", "v3_b8_h128"),
+                            "kernel_us": h["kernel_us"], "combine_us": h["combine_us"]}
+        if not args.no_cpu:
+            full_s, sample = head.cpu_sample()
+            line["cpu_baseline"] = {"value": round(head.bytes / full_s / 1e9, 4), "unit": "GB/s", "cores": 1,
+                                    "kind": "port", "us_per_layer_step": round(full_s * 1e6, 1),
+                                    "sample": sample, "host_cores_available": os.cpu_count()}
+    line["configs"] = results
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

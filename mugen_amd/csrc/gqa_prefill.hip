@@ -15,7 +15,10 @@
 //    permutation that leaves each lane 8 consecutive keys of its query row,
 //    online softmax in registers, then O += P . V with P taken straight from
 //    registers as the A operand and V gathered from LDS as the B operand;
-//  * tiles entirely above the causal diagonal are never visited.
+//  * tiles entirely above the causal diagonal are never visited;
+//  * with bf16 inputs P is split into hi + lo bf16 terms (two MFMAs on the
+//    same V operand): a single bf16 P carries 2^-9 relative error per
+//    weight, which short causal rows do not average away.
 #include "common.h"
 #include "kernels.h"
 
@@ -29,6 +32,7 @@ __global__ __launch_bounds__(256) void gqa_prefill_kernel(GqaPrefillParams p) {
     constexpr int LROW = D + 8;    // padded LDS row (halves)
     constexpr int CPR = D / 8;     // 16-byte chunks per row
     constexpr int CPT = KT * CPR / 256;  // chunks per thread per matrix
+    constexpr int NP = p_terms<DT>();    // 16-bit terms P is split into
     __shared__ __attribute__((aligned(16))) uint16_t ks[KT * LROW];
     __shared__ __attribute__((aligned(16))) uint16_t vs[KT * LROW];
 
@@ -130,7 +134,7 @@ __global__ __launch_bounds__(256) void gqa_prefill_kernel(GqaPrefillParams p) {
             const float m_use = (m_new == kNegInf) ? 0.f : m_new;
             const float alpha = fast_exp2(m_run[mb] - m_use);
             float ps = 0.f;
-            u32x4_t pfr[2];
+            u32x4_t pfr[2][NP];
 #pragma unroll
             for (int grp = 0; grp < 2; grp++) {
 #pragma unroll
@@ -138,8 +142,7 @@ __global__ __launch_bounds__(256) void gqa_prefill_kernel(GqaPrefillParams p) {
                     x[grp][j] = fast_exp2(x[grp][j] - m_use);
                     ps += x[grp][j];
                 }
-                pfr[grp] = u32x4_t{pack2<DT>(x[grp][0], x[grp][1]), pack2<DT>(x[grp][2], x[grp][3]),
-                                   pack2<DT>(x[grp][4], x[grp][5]), pack2<DT>(x[grp][6], x[grp][7])};
+                split_p<DT, NP>(x[grp], pfr[grp]);
             }
             l_part[mb] = l_part[mb] * alpha + ps;
             m_run[mb] = m_new;
@@ -164,7 +167,9 @@ __global__ __launch_bounds__(256) void gqa_prefill_kernel(GqaPrefillParams p) {
                         const uint32_t e1 = bcol[(2 * j + 1) * LROW + 16 * d];
                         bw[j] = e0 | (e1 << 16);
                     }
-                    o[mb][d] = mfma16x16x32<DT>(pfr[grp], u32x4_t{bw[0], bw[1], bw[2], bw[3]}, o[mb][d]);
+                    const u32x4_t bf = u32x4_t{bw[0], bw[1], bw[2], bw[3]};
+#pragma unroll
+                    for (int pp = 0; pp < NP; pp++) o[mb][d] = mfma16x16x32<DT>(pfr[grp][pp], bf, o[mb][d]);
                 }
             }
         }

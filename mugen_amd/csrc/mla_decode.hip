@@ -24,7 +24,9 @@
 //  * online softmax in the exp2 domain; the split-K partials (m, l, o) are
 //    merged by mla_decode_combine with fp32 log-sum-exp.
 //  * q in fp32 is split into hi + lo 16-bit halves (two MFMAs), which keeps
-//    the scores fp32-accurate like the reference's float q_absorbed.
+//    the scores fp32-accurate like the reference's float q_absorbed;
+//  * with a bf16 cache P is split the same way (hi + lo bf16, two MFMAs on
+//    one latent B operand), keeping the weights at ~2^-17 relative error.
 #include "common.h"
 #include "kernels.h"
 
@@ -42,6 +44,7 @@ template <int MB, int QDT, int DT, int OUT_DT>
 __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     constexpr int KS = kCD / 32;  // 18 k-steps over the 576 dims
     constexpr int NQ = (QDT == DT_F32) ? 2 : 1;
+    constexpr int NP = p_terms<DT>();
     __shared__ __attribute__((aligned(16))) uint16_t lds[kTT * kLROW];
 
     const int rb = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
@@ -143,7 +146,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
         }
 
         // ---- online softmax; lane holds tokens tt + 8g + (4nb + i) of row n
-        u32x4_t pfrag[MB];
+        u32x4_t pfrag[MB][NP];
         float alpha_row[MB][4];
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) {
@@ -172,8 +175,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
             }
             l_part[mb] = l_part[mb] * alpha + ps;
             m_run[mb] = m_new;
-            pfrag[mb] = u32x4_t{pack2<DT>(x[0], x[1]), pack2<DT>(x[2], x[3]),
-                                pack2<DT>(x[4], x[5]), pack2<DT>(x[6], x[7])};
+            split_p<DT, NP>(x, pfrag[mb]);
             // O rows are 4g+i: fetch their alpha from lane (4g+i)
 #pragma unroll
             for (int i = 0; i < 4; i++) alpha_row[mb][i] = __shfl(alpha, 4 * g + i, 64);
@@ -200,7 +202,10 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
             }
             const u32x4_t bf = u32x4_t{bw[0], bw[1], bw[2], bw[3]};
 #pragma unroll
-            for (int mb = 0; mb < MB; mb++) o[mb][d] = mfma16x16x32<DT>(pfrag[mb], bf, o[mb][d]);
+            for (int mb = 0; mb < MB; mb++) {
+#pragma unroll
+                for (int pp = 0; pp < NP; pp++) o[mb][d] = mfma16x16x32<DT>(pfrag[mb][pp], bf, o[mb][d]);
+            }
         }
     }
 

@@ -29,6 +29,7 @@ def within_tol(got, ref, atol=ATOL, rtol=RTOL):
 
 def assert_close(got, ref, what="", atol=ATOL, rtol=RTOL):
     ok, mx = within_tol(got, ref, atol, rtol)
+    print(f"  {what}: max-abs err {mx:.3e}", flush=True)
     assert ok, f"{what}: max-abs err {mx:.3e} exceeds atol {atol} + rtol {rtol}*|ref|"
     return mx
 
