@@ -81,7 +81,7 @@ class MlaDecode(Case):
 
     def step(self):
         mugen_amd.mla_attention(self.q, self.lat, self.sl, self.max_T, scale=MLA_SCALE, out=self.out,
-                                workspace=self.ws)
+                                workspace=self.ws, seq_lens_host=self.lens)
 
     def cpu_sample(self, seconds_target=10.0):
         """Time the oracle (single-thread C port of cpu_mla_attention's core)
@@ -126,7 +126,8 @@ class GqaDecode(Case):
         self.flops = 4.0 * H * D * float(self.lens.sum())
 
     def step(self):
-        mugen_amd.attention_decode(self.q, self.k, self.v, self.sl, self.max_T, out=self.out, workspace=self.ws)
+        mugen_amd.attention_decode(self.q, self.k, self.v, self.sl, self.max_T, out=self.out, workspace=self.ws,
+                                   seq_lens_host=self.lens)
 
 
 class Prefill(Case):

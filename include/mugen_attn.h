@@ -96,6 +96,9 @@ typedef struct mugen_attn_gqa_decode_args {
     float scale;
     int32_t kv_dtype;   /* mugen_attn_dtype */
     int32_t out_dtype;  /* mugen_attn_dtype */
+    /* optional HOST copy of seq_lens (NULL allowed): lets the planner size
+     * the context splits for ragged batches; results do not depend on it */
+    const int32_t* seq_lens_host;
 } mugen_attn_gqa_decode_args;
 
 size_t mugen_attn_gqa_decode_workspace_size(const mugen_attn_gqa_decode_args* args);
@@ -176,6 +179,8 @@ typedef struct mugen_attn_mla_decode_args {
     int32_t q_dtype;
     int32_t latent_dtype;
     int32_t out_dtype;
+    /* optional HOST copy of seq_lens (NULL allowed), planning hint only */
+    const int32_t* seq_lens_host;
 } mugen_attn_mla_decode_args;
 
 size_t mugen_attn_mla_decode_workspace_size(const mugen_attn_mla_decode_args* args);

@@ -45,7 +45,7 @@ class GqaDecodeArgs(ctypes.Structure):
         ("q", _vp), ("k_cache", _vp), ("v_cache", _vp), ("seq_lens", _vp), ("out", _vp),
         ("batch", _i32), ("n_heads", _i32), ("n_kv_heads", _i32), ("head_dim", _i32),
         ("max_seq_len", _i32), ("num_splits", _i32), ("seq_stride", _i64), ("scale", _f32),
-        ("kv_dtype", _i32), ("out_dtype", _i32),
+        ("kv_dtype", _i32), ("out_dtype", _i32), ("seq_lens_host", _vp),
     ]
 
 
@@ -63,7 +63,7 @@ class MlaDecodeArgs(ctypes.Structure):
         ("q", _vp), ("latent", _vp), ("seq_lens", _vp), ("out", _vp),
         ("batch", _i32), ("q_len", _i32), ("n_heads", _i32), ("kv_rank", _i32), ("rope_dim", _i32),
         ("max_seq_len", _i32), ("num_splits", _i32), ("seq_stride", _i64), ("scale", _f32),
-        ("q_dtype", _i32), ("latent_dtype", _i32), ("out_dtype", _i32),
+        ("q_dtype", _i32), ("latent_dtype", _i32), ("out_dtype", _i32), ("seq_lens_host", _vp),
     ]
 
 

@@ -38,6 +38,14 @@ def _stream(device: torch.device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+def _host_lens(seq_lens_host):
+    """int32 host array for the planner hint (or None)."""
+    if seq_lens_host is None:
+        return None
+    import numpy as np
+    return np.ascontiguousarray(seq_lens_host, dtype=np.int32)
+
+
 def _need_cuda(*ts: torch.Tensor):
     for t in ts:
         if not t.is_cuda:
@@ -65,9 +73,10 @@ def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
                      seq_lens: torch.Tensor, max_seq_len: int | None = None, *,
                      out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
                      scale: float = 0.0, num_splits: int = 0,
-                     workspace: torch.Tensor | None = None) -> torch.Tensor:
+                     workspace: torch.Tensor | None = None, seq_lens_host=None) -> torch.Tensor:
     """GQA decode.  q [B,H,D]; k/v cache [B,max_T,Hk,D] (token-major per
-    sequence); seq_lens int32 [B] on device.  Returns out [B,H,D]."""
+    sequence); seq_lens int32 [B] on device; seq_lens_host: optional host
+    copy used only to balance the context splits.  Returns out [B,H,D]."""
     _need_cuda(q, k_cache, v_cache, seq_lens)
     if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
         raise ValueError("k_cache/v_cache must be [B, max_T, Hk, D] and equal shapes")
@@ -78,6 +87,9 @@ def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     if out is None:
         out = torch.empty(q.shape, dtype=out_dtype or q.dtype, device=q.device)
     a = gqa_decode_args(q, k_cache, v_cache, seq_lens, out, max_seq_len, scale, num_splits)
+    hl = _host_lens(seq_lens_host)
+    if hl is not None:
+        a.seq_lens_host = hl.ctypes.data
     L = _capi.lib()
     need = L.mugen_attn_gqa_decode_workspace_size(ctypes.byref(a))
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
@@ -127,7 +139,8 @@ def mla_args(q, latent, seq_lens, out, max_seq_len, scale, num_splits=0):
 def mla_attention(q: torch.Tensor, latent: torch.Tensor, seq_lens: torch.Tensor,
                   max_seq_len: int | None = None, *, scale: float = 1.0 / math.sqrt(192.0),
                   out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32,
-                  num_splits: int = 0, workspace: torch.Tensor | None = None) -> torch.Tensor:
+                  num_splits: int = 0, workspace: torch.Tensor | None = None,
+                  seq_lens_host=None) -> torch.Tensor:
     """MLA absorbed attention (decode: q_len 1; verify: q_len > 1, causal).
 
     q [B,q_len,H,576] (q_nope.W_UK ++ q_rope); latent [B,max_T,576];
@@ -144,6 +157,9 @@ def mla_attention(q: torch.Tensor, latent: torch.Tensor, seq_lens: torch.Tensor,
     if out is None:
         out = torch.empty((B, q_len, H, 512), dtype=out_dtype, device=q.device)
     a = mla_args(q, latent, seq_lens, out, max_seq_len, scale, num_splits)
+    hl = _host_lens(seq_lens_host)
+    if hl is not None:
+        a.seq_lens_host = hl.ctypes.data
     L = _capi.lib()
     need = L.mugen_attn_mla_decode_workspace_size(ctypes.byref(a))
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):

@@ -132,20 +132,41 @@ static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b)
 static bool is16(int dt) { return dt == DT_F16 || dt == DT_BF16; }
 static bool is_out(int dt) { return dt == DT_F32 || dt == DT_F16 || dt == DT_BF16; }
 
-// GQA decode: tokens per split (multiple of 64 = one 16-token block per wave)
-static int gqa_chunk(const mugen_attn_gqa_decode_args* a) {
-    const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
-    if (a->num_splits > 0) {
-        const int c = ceil_div(maxT, a->num_splits);
-        return ceil_div(c, 64) * 64;
-    }
-    // aim for ~512 workgroups (2 per CU) over the whole batch
-    const int64_t items = (int64_t)a->batch * a->n_kv_heads;
-    int64_t c = ((int64_t)maxT * items + 511) / 512;
-    c = ((c + 63) / 64) * 64;
-    if (c < 64) c = 64;
-    if (c > 4096) c = 4096;
+// Token count the planner balances: the sum of the host hint when given,
+// else batch * max_seq_len.
+static int64_t planned_tokens(const int32_t* host_lens, int batch, int max_seq_len) {
+    if (!host_lens) return (int64_t)batch * (max_seq_len > 0 ? max_seq_len : 1);
+    int64_t t = 0;
+    for (int b = 0; b < batch; b++) t += host_lens[b] > 0 ? host_lens[b] : 0;
+    return t > 0 ? t : 1;
+}
+
+// Tokens per split for a workgroup count target; rounded to `quantum`, and
+// large enough that no more than kMaxSplits splits cover max_seq_len.
+static int plan_chunk(int64_t tokens_x_groups, int target_wgs, int quantum, int max_seq_len) {
+    int64_t c = (tokens_x_groups + target_wgs - 1) / target_wgs;
+    c = ((c + quantum - 1) / quantum) * quantum;
+    if (c < quantum) c = quantum;
+    const int64_t min_c = ((int64_t)(max_seq_len > 0 ? max_seq_len : 1) + kMaxSplits - 1) / kMaxSplits;
+    if (c < min_c) c = ((min_c + quantum - 1) / quantum) * quantum;
     return (int)c;
+}
+
+static int explicit_chunk(int max_seq_len, int num_splits, int quantum) {
+    const int maxT = max_seq_len > 0 ? max_seq_len : 1;
+    int64_t c = ((int64_t)maxT + num_splits - 1) / num_splits;
+    c = ((c + quantum - 1) / quantum) * quantum;
+    const int64_t min_c = ((int64_t)maxT + kMaxSplits - 1) / kMaxSplits;
+    if (c < min_c) c = ((min_c + quantum - 1) / quantum) * quantum;
+    return (int)c;
+}
+
+// GQA decode: tokens per split (multiple of 64 = one 16-token block per wave);
+// ~2 resident 256-thread workgroups per CU over 256 CUs
+static int gqa_chunk(const mugen_attn_gqa_decode_args* a) {
+    if (a->num_splits > 0) return explicit_chunk(a->max_seq_len, a->num_splits, 64);
+    const int64_t work = planned_tokens(a->seq_lens_host, a->batch, a->max_seq_len) * a->n_kv_heads;
+    return plan_chunk(work, 512, 64, a->max_seq_len);
 }
 
 static int gqa_validate(const mugen_attn_gqa_decode_args* a) {
@@ -183,22 +204,20 @@ static size_t gqa_ws(const mugen_attn_gqa_decode_args* a, int chunk, int* splits
     return slots * (size_t)a->head_dim * 4 + slots * 2 * 4 + 256;
 }
 
-// MLA: rows per workgroup and tokens per split
-static int mla_variant(const mugen_attn_mla_decode_args*) { return 1; }
+// MLA: 128-row workgroups (32 rows per wave) when there are enough rows and
+// q is 16-bit, else 64-row workgroups
+static int mla_variant(const mugen_attn_mla_decode_args* a) {
+    const int R = a->q_len * a->n_heads;
+    return (R > 64 && a->q_dtype != DT_F32) ? 2 : 1;
+}
 
+// one 256-thread workgroup per CU (the kernel holds ~460 registers per lane)
 static int mla_chunk(const mugen_attn_mla_decode_args* a, int variant) {
-    const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
-    if (a->num_splits > 0) {
-        const int c = ceil_div(maxT, a->num_splits);
-        return ceil_div(c, 32) * 32;
-    }
+    if (a->num_splits > 0) return explicit_chunk(a->max_seq_len, a->num_splits, 32);
     const int R = a->q_len * a->n_heads;
     const int64_t nrb = ceil_div(R, mla_rows_per_block(variant));
-    // ~one workgroup per CU (256 CUs): the kernel runs 1 wave per SIMD
-    int64_t c = ((int64_t)maxT * a->batch * nrb + 255) / 256;
-    c = ((c + 31) / 32) * 32;
-    if (c < 64) c = 64;
-    return (int)c;
+    const int64_t work = planned_tokens(a->seq_lens_host, a->batch, a->max_seq_len) * nrb;
+    return plan_chunk(work, 256, 32, a->max_seq_len);
 }
 
 static int mla_validate(const mugen_attn_mla_decode_args* a) {
@@ -231,7 +250,7 @@ static size_t mla_ws(const mugen_attn_mla_decode_args* a, int chunk, int* splits
     const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
     const int splits = ceil_div(maxT, chunk);
     if (splits_out) *splits_out = splits;
-    if (splits <= 1) return 0;
+    // every split (a single one included) writes an fp32 (m, l, o) partial
     const size_t slots = (size_t)a->batch * splits * a->q_len * a->n_heads;
     return slots * 512 * 4 + slots * 2 * 4 + 256;
 }
@@ -339,7 +358,7 @@ int mugen_attn_mla_decode(const mugen_attn_mla_decode_args* a, void* ws, size_t 
     const int chunk = mla_chunk(a, variant);
     int splits = 1;
     const size_t need = mla_ws(a, chunk, &splits);
-    if (need > 0 && (!ws || ws_bytes < need))
+    if (!ws || ws_bytes < need)
         return fail(MUGEN_ATTN_E_WORKSPACE, "mla_decode: workspace of %zu bytes required, %zu given", need,
                     ws_bytes);
     MlaParams p{};
@@ -349,18 +368,20 @@ int mugen_attn_mla_decode(const mugen_attn_mla_decode_args* a, void* ws, size_t 
     p.out = a->out;
     p.q_len = a->q_len;
     p.H = a->n_heads;
+    p.B = a->batch;
     p.R = a->q_len * a->n_heads;
+    p.nrb = ceil_div(p.R, mla_rows_per_block(variant));
     p.chunk = chunk;
     p.num_splits = splits;
     p.seq_stride = a->seq_stride;
     p.scale_log2 = a->scale * kLog2e;
-    if (splits > 1) {
+    {
         float* base = align256(ws);
         const size_t slots = (size_t)a->batch * splits * p.R;
         p.ws_o = base;
         p.ws_ml = base + slots * 512;
     }
-    hipError_t e = launch_mla_decode(p, a->batch, variant, a->q_dtype, a->latent_dtype, a->out_dtype,
+    hipError_t e = launch_mla_decode(p, variant, a->q_dtype, a->latent_dtype, a->out_dtype,
                                      static_cast<hipStream_t>(stream), active_timer());
     return hip_status(e, "mla_decode launch");
 }

@@ -119,6 +119,97 @@ __device__ __forceinline__ float wave_xor(float v, int mask) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// LDS transpose read (gfx950 ds_read_b64_tr_b16).  Within each 16-lane
+// group, lane i receives element (i % 4) of the 8-byte chunks addressed by
+// lanes 4r + i/4, r = 0..3: with lane (4r + c) pointing at row r, columns
+// [4c, 4c+4) of a row-major 16-bit tile, lane i gets column i of rows 0..3.
+__device__ __forceinline__ u32x2_t lds_read_tr16(const uint16_t* p) {
+    typedef short s16x4_t __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4_t* lds_s16x4_ptr;
+    const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(const_cast<uint16_t*>(p)));
+    return __builtin_bit_cast(u32x2_t, v);
+}
+
+// block-wide (wave64 x nwaves) max / sum through a small LDS scratch
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+// Split-K log-sum-exp weights for one output row: given the (m, l) pairs of
+// nact splits (m in log2 units, stride 2 floats apart by `ml_stride`),
+// writes f_s = 2^(m_s - M) to LDS and returns 1 / sum_s f_s l_s (0 when
+// no split saw a token).  All threads of the block must call it.
+constexpr int kMaxSplits = 4096;
+__device__ __forceinline__ float lse_weights(const float* ml, int64_t ml_stride, int nact, float* f_lds,
+                                             float* red_lds) {
+    const int tid = threadIdx.x, nw = blockDim.x >> 6, w = tid >> 6;
+    float mloc = kNegInf;
+    for (int s = tid; s < nact; s += blockDim.x) mloc = fmaxf(mloc, ml[s * ml_stride]);
+    mloc = wave_max(mloc);
+    if ((tid & 63) == 0) red_lds[w] = mloc;
+    __syncthreads();
+    float M = red_lds[0];
+    for (int i = 1; i < nw; i++) M = fmaxf(M, red_lds[i]);
+    __syncthreads();
+    float lloc = 0.f;
+    for (int s = tid; s < nact; s += blockDim.x) {
+        const float m = ml[s * ml_stride];
+        const float f = (m == kNegInf) ? 0.f : fast_exp2(m - M);
+        f_lds[s] = f;
+        lloc += f * ml[s * ml_stride + 1];
+    }
+    lloc = wave_sum(lloc);
+    if ((tid & 63) == 0) red_lds[w] = lloc;
+    __syncthreads();
+    float L = 0.f;
+    for (int i = 0; i < nw; i++) L += red_lds[i];
+    return L > 0.f ? 1.f / L : 0.f;
+}
+
+// ---------------------------------------------------------------- LDS DMA
+//
+// gfx950 global_load_lds_dwordx4: each lane's 16 bytes at `src` land in LDS
+// at M0 + 16*lane (one contiguous KiB per wave instruction).  Issued from
+// inline asm so the compiler's wait-count pass, which cannot tell an
+// in-flight DMA from the LDS reads of another buffer, does not serialise
+// the ring buffer with vmcnt(0); callers order it with vm_wait<N>() and
+// lds_barrier().  `lds_byte_addr` must be wave-uniform.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// `sbase` (wave-uniform, SGPR pair) + per-lane 32-bit byte offset `voff`
+__device__ __forceinline__ void dma16s(uint32_t lds_byte_addr, const void* sbase, uint32_t voff) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_byte_addr);
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2"
+        :
+        : "s"(m0), "v"(voff), "s"(sbase)
+        : "memory", "m0");
+}
+
+// wait until at most N vector-memory operations of this wave are in flight
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// workgroup barrier that also orders the compiler's memory accesses,
+// without the full fence (and its vmcnt(0)) of __syncthreads()
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
+}
+
 __device__ __forceinline__ u32x4_t load16(const void* p) {
     return *reinterpret_cast<const u32x4_t*>(p);
 }

@@ -202,25 +202,29 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(GqaDecodeParams p) {
     }
 }
 
-// Log-sum-exp merge of the split partials of one (sequence, head).
+// Log-sum-exp merge of the split partials of one (sequence, head): the
+// split weights are computed in parallel, then each thread sums its dim
+// over the splits with independent (unrolled) loads.
 template <int D, int OUT_DT>
 __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p) {
+    __shared__ float f_lds[kMaxSplits];
+    __shared__ float red_lds[4];
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     const int T = p.seq_lens[b];
     const int nact = min(p.num_splits, (T + p.chunk - 1) / p.chunk);
     const int64_t bh = (int64_t)b * p.H + h;
-    const float* ml = p.ws_ml + bh * p.num_splits * 2;
-    const float* os = p.ws_o + bh * p.num_splits * D;
-    float M = kNegInf;
-    for (int s = 0; s < nact; s++) M = fmaxf(M, ml[2 * s]);
-    float L = 0.f, O = 0.f;
-    for (int s = 0; s < nact; s++) {
-        const float m = ml[2 * s];
-        const float f = (m == kNegInf) ? 0.f : fast_exp2(m - M);
-        L += f * ml[2 * s + 1];
-        O += f * os[(int64_t)s * D + d];
+    const float inv = lse_weights(p.ws_ml + bh * p.num_splits * 2, 2, nact, f_lds, red_lds);
+    const float* os = p.ws_o + bh * p.num_splits * D + d;
+    float O0 = 0.f, O1 = 0.f, O2 = 0.f, O3 = 0.f;
+    int s = 0;
+    for (; s + 4 <= nact; s += 4) {
+        O0 += f_lds[s] * os[(int64_t)s * D];
+        O1 += f_lds[s + 1] * os[(int64_t)(s + 1) * D];
+        O2 += f_lds[s + 2] * os[(int64_t)(s + 2) * D];
+        O3 += f_lds[s + 3] * os[(int64_t)(s + 3) * D];
     }
-    store_out<OUT_DT>(p.out, bh * D + d, L > 0.f ? O / L : 0.f);
+    for (; s < nact; s++) O0 += f_lds[s] * os[(int64_t)s * D];
+    store_out<OUT_DT>(p.out, bh * D + d, ((O0 + O1) + (O2 + O3)) * inv);
 }
 
 // ------------------------------------------------------------------ launch

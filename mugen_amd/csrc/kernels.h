@@ -55,19 +55,21 @@ struct MlaParams {
     void* out;             // [B][q_len*H][512]
     float* ws_o;           // [B][splits][R][512]
     float* ws_ml;          // [B][splits][R][2]
+    int B;
     int q_len;
     int H;
     int R;                 // q_len * H rows per sequence
+    int nrb;               // row blocks per sequence (ceil(R / rows per block))
     int chunk;
     int num_splits;
     int64_t seq_stride;
     float scale_log2;
 };
 
-// rows of queries handled by one MLA workgroup for a given variant
+// rows of queries handled by one MLA workgroup for a given variant (1 or 2)
 int mla_rows_per_block(int variant);
-hipError_t launch_mla_decode(const MlaParams& p, int B, int variant, int q_dt, int lat_dt,
-                             int out_dt, hipStream_t st, KernelTimer* t);
+hipError_t launch_mla_decode(const MlaParams& p, int variant, int q_dt, int lat_dt, int out_dt,
+                             hipStream_t st, KernelTimer* t);
 
 hipError_t launch_scatter_kv(const uint16_t* src, uint16_t* dst, uint64_t offset, uint64_t count,
                              hipStream_t st, KernelTimer* t);

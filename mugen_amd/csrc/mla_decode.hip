@@ -10,51 +10,97 @@
 // Design: all heads share one latent row, so attention is a pair of dense
 // contractions, S = Q[rows x 576] . L^T and O = P . L[:, 0:512], run on
 // MFMA 16x16x32 (bf16 or fp16 in, fp32 accumulate):
-//  * workgroup = (block of 64*MB query rows, context split, sequence);
-//    4 waves, each owning 16*MB rows; Q of those rows stays in registers as
-//    the B operand of S^T = L . Q^T; O[rows x 512] is accumulated in
-//    registers (MB x 32 MFMA tiles per wave);
-//  * latent tiles of 32 tokens are staged into LDS (padded rows, 16-byte
-//    reads conflict-free), the next tile is prefetched into registers while
-//    the current one is consumed;
+//  * workgroup = (block of 64*MB query rows, context split, sequence); 4
+//    waves, each owning 16*MB rows.  MB = 2 (32 rows per wave) halves the
+//    LDS bytes per MFMA flop versus 16 rows: every latent fragment read from
+//    LDS feeds two MFMAs.  Q of the wave's rows stays in VGPRs (B operand of
+//    S^T = L . Q^T); O[rows x 512] is accumulated in AGPRs;
+//  * the S MFMAs are issued from inline asm with VGPR accumulators so that
+//    the 256-register O accumulator alone owns the AGPR file (the compiler
+//    would otherwise put both in AGPRs and spill);
+//  * latent tiles of 32 tokens stream into a 3-deep LDS ring by direct
+//    global->LDS DMA (global_load_lds_dwordx4), two tiles in flight, padded
+//    rows (74 x 16 B) so the MFMA operand reads spread over the banks; the
+//    tile loop is unrolled by the ring depth so buffer bases are constants;
 //  * S^T uses a token permutation (A-row m of token block nb is token
-//    8*(m/4) + 4*nb + m%4) so that each lane ends up holding 8 CONSECUTIVE
-//    tokens of its query row: exactly the k-slots of its P operand for the
-//    P.L product, so P never leaves registers;
-//  * online softmax in the exp2 domain; the split-K partials (m, l, o) are
-//    merged by mla_decode_combine with fp32 log-sum-exp.
-//  * q in fp32 is split into hi + lo 16-bit halves (two MFMAs), which keeps
-//    the scores fp32-accurate like the reference's float q_absorbed;
-//  * with a bf16 cache P is split the same way (hi + lo bf16, two MFMAs on
-//    one latent B operand), keeping the weights at ~2^-17 relative error.
+//    8*(m/4) + 4*nb + m%4) so each lane ends up holding 8 CONSECUTIVE tokens
+//    of its query row: exactly its k-slots as the A operand of P.L, so P
+//    never leaves registers;
+//  * the P.L B operand (8 tokens of one latent dim per lane) comes from the
+//    row-major tile through two ds_read_b64_tr_b16 transpose reads;
+//  * softmax in the exp2 domain against a reference max fixed at each row's
+//    first visible tile: later weights may exceed 1 (bf16 P keeps fp32's
+//    exponent range), so O is never rescaled.  A row whose score overshoots
+//    the reference by the dtype's headroom is flagged (NaN max) and the
+//    combine kernel recomputes that (row, split) exactly in fp32;
+//  * every workgroup writes an fp32 (m, l, o) partial; mla_decode_combine
+//    merges the splits of a row with fp32 log-sum-exp;
+//  * q in fp32 is split into hi + lo 16-bit halves (two MFMAs), keeping the
+//    scores fp32-accurate like the reference's float q_absorbed.
 #include "common.h"
 #include "kernels.h"
 
 namespace mugen_attn {
 
-constexpr int kKR = 512;               // kv_lora_rank
-constexpr int kRD = 64;                // rope dims
-constexpr int kCD = kKR + kRD;         // 576 latent dims per token
-constexpr int kTT = 32;                // tokens per LDS tile
-constexpr int kLROW = kCD + 8;         // LDS row stride (halves): 1168 B
-constexpr int kChunks = kTT * kCD / 8; // 16-byte chunks per tile (2304)
-constexpr int kCPT = kChunks / 256;    // chunks per thread (9)
+constexpr int kKR = 512;                // kv_lora_rank
+constexpr int kRD = 64;                 // rope dims
+constexpr int kCD = kKR + kRD;          // 576 latent dims per token
+constexpr int kTT = 32;                 // tokens per LDS tile
+constexpr int kLROW = kCD + 16;         // LDS row stride (halves): 1184 B = 74 x 16 B
+constexpr int kSlotsRow = kLROW / 8;    // 16-byte slots per LDS row (72 data + 2 pad)
+constexpr int kDmaPerWave = 10;         // DMA instructions per wave per tile (40 x 1 KiB)
+constexpr int kBufBytes = 4 * kDmaPerWave * 1024;  // 40 KiB per ring buffer (37 KiB used)
+constexpr int kNBuf = 3;                // ring depth: two tiles in flight
 
-template <int MB, int QDT, int DT, int OUT_DT>
+// Reference-max headroom (log2 units): with the max fixed at the first
+// visible tile, later weights may reach 2^TH.  bf16 P keeps fp32's exponent
+// range (O stays far from fp32 overflow); fp16 P tops out at 65504.
+template <int DT>
+__device__ constexpr float headroom_log2() { return DT == DT_BF16 ? 64.f : 15.f; }
+
+// S-chain MFMA with a VGPR accumulator (FIRST: C = 0)
+template <int DT, bool FIRST>
+__device__ __forceinline__ void mfma_s(f32x4_t& acc, const u32x4_t& a, const u32x4_t& b) {
+    if constexpr (FIRST) {
+        if constexpr (DT == DT_BF16)
+            asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b));
+        else
+            asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b));
+    } else {
+        if constexpr (DT == DT_BF16)
+            asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+        else
+            asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+    }
+}
+
+template <int MB, int QDT, int DT>
 __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     constexpr int KS = kCD / 32;  // 18 k-steps over the 576 dims
     constexpr int NQ = (QDT == DT_F32) ? 2 : 1;
-    constexpr int NP = p_terms<DT>();
-    __shared__ __attribute__((aligned(16))) uint16_t lds[kTT * kLROW];
+    constexpr float TH = headroom_log2<DT>();
+    __shared__ __attribute__((aligned(1024))) uint16_t ring[kNBuf][kBufBytes / 2];
 
-    const int rb = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
+    // XCD-aware work mapping: consecutive work items (the row blocks of one
+    // (sequence, split), then the splits of a sequence) land on one XCD,
+    // whose L2 then serves the latent tile to every row block
+    const int nxcd = 8;
+    const int per_xcd = gridDim.x / nxcd;
+    const int wi = (blockIdx.x % nxcd) * per_xcd + blockIdx.x / nxcd;
+    const int nrb = p.nrb;
+    const int rb = wi % nrb;
+    const int s = (wi / nrb) % p.num_splits;
+    const int b = wi / (nrb * p.num_splits);
+    if (b >= p.B) return;
+
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int T = p.seq_lens[b];
     const int t_begin = s * p.chunk;
     const int t_end = min(t_begin + p.chunk, T);
-    if (p.num_splits > 1 && t_begin >= T) return;
+    if (t_begin >= T) return;  // empty split: the combine skips it
+    const int ntiles = (t_end - t_begin + kTT - 1) / kTT;
 
     const int row0 = rb * (64 * MB) + w * (16 * MB);
     const uint16_t* lat = p.lat + (int64_t)b * p.seq_stride;
@@ -91,63 +137,76 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
         }
     }
 
+    // ---- tile staging by LDS DMA: wave w fills ring slots [64K, 64K+64) for
+    // K = w + 4k; slot -> (token slot/74, 16-byte chunk slot%74).  Offsets
+    // are clamped to the split's last valid byte, so pad chunks, slots past
+    // the tile and tokens past t_end all read valid cache rows (masked later)
+    const uint32_t ring_base = lds_addr(&ring[0][0]);
+    auto issue = [&](int tt, int buf) {
+        const uint16_t* tbase = lat + (int64_t)tt * kCD;               // wave-uniform
+        const uint32_t lim = (uint32_t)(t_end - tt) * (kCD * 2) - 16;  // last valid chunk
+#pragma unroll
+        for (int k = 0; k < kDmaPerWave; k++) {
+            const int K = w + 4 * k;
+            const int slot = 64 * K + lane;
+            const int tok = slot / kSlotsRow, ch = slot - tok * kSlotsRow;
+            const uint32_t off = (uint32_t)(tok * (kCD * 2) + (ch < kCD / 8 ? ch : 0) * 16);
+            dma16s(ring_base + buf * kBufBytes + K * 1024, tbase, min(off, lim));
+        }
+    };
+
+    // A-operand row of token block nb for this lane: token 8*(n/4) + 4*nb + n%4
+    const int aoff = (8 * (n >> 2) + (n & 3)) * kLROW + 8 * g;
+    // transpose-read offset: lane (i, g) of read h points at token 8g + 4h + i/4,
+    // latent dims 4*(i%4) .. +4 of the 16-dim block
+    const int troff = (8 * g + (n >> 2)) * kLROW + 4 * (n & 3);
+
     f32x4_t o[MB][32];
-    float m_run[MB], l_part[MB];
+    float m_ref[MB], l_part[MB];  // reference max (log2 units) and partial sum
+    bool ovf_row[MB];             // this lane's S-row overshot the headroom
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
-        m_run[mb] = kNegInf;
+        m_ref[mb] = kNegInf;
         l_part[mb] = 0.f;
+        ovf_row[mb] = false;
 #pragma unroll
         for (int d = 0; d < 32; d++) o[mb][d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
 
-    // ---- tile staging: chunk c = tid + 256*i -> token c/72, dims (c%72)*8
-    u32x4_t pf[kCPT];
-    auto fetch = [&](int tt) {
-#pragma unroll
-        for (int i = 0; i < kCPT; i++) {
-            const int c = tid + 256 * i;
-            const int tok = min(tt + c / 72, t_end - 1);
-            pf[i] = load16(lat + (int64_t)tok * kCD + (c % 72) * 8);
-        }
-    };
-    if (t_begin < t_end) fetch(t_begin);
+    auto step = [&](int it, auto buf_tag) {
+        constexpr int BUF = decltype(buf_tag)::value;
+        if (it + 1 < ntiles) vm_wait<kDmaPerWave>();
+        else vm_wait<0>();
+        lds_barrier();  // tile `it` landed for every wave; buffer (it+2)%3 is free
+        if (it + 2 < ntiles) issue(t_begin + kTT * (it + 2), (BUF + 2) % kNBuf);
+        const uint16_t* tile = &ring[BUF][0];
+        const int tt = t_begin + kTT * it;
 
-    // A-operand row of token block nb for this lane: token 8*(n/4) + 4*nb + n%4
-    const int arow0 = 8 * (n >> 2) + (n & 3);
-
-    for (int tt = t_begin; tt < t_end; tt += kTT) {
-        __syncthreads();  // previous tile fully consumed
-#pragma unroll
-        for (int i = 0; i < kCPT; i++) {
-            const int c = tid + 256 * i;
-            *reinterpret_cast<u32x4_t*>(&lds[(c / 72) * kLROW + (c % 72) * 8]) = pf[i];
-        }
-        __syncthreads();
-        if (tt + kTT < t_end) fetch(tt + kTT);
-
-        // ---- S^T = L . Q^T  (two 16-token blocks)
+        // ---- S^T = L . Q^T  (two 16-token blocks), VGPR accumulators
         f32x4_t sacc[MB][2];
-#pragma unroll
-        for (int mb = 0; mb < MB; mb++) sacc[mb][0] = sacc[mb][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
 #pragma unroll
             for (int nb = 0; nb < 2; nb++) {
-                const u32x4_t a = *reinterpret_cast<const u32x4_t*>(
-                    &lds[(arow0 + 4 * nb) * kLROW + 32 * ks + 8 * g]);
+                const u32x4_t a = *reinterpret_cast<const u32x4_t*>(tile + aoff + 4 * nb * kLROW + 32 * ks);
 #pragma unroll
                 for (int mb = 0; mb < MB; mb++) {
 #pragma unroll
-                    for (int qq = 0; qq < NQ; qq++)
-                        sacc[mb][nb] = mfma16x16x32<DT>(a, qf[mb][qq][ks], sacc[mb][nb]);
+                    for (int qq = 0; qq < NQ; qq++) {
+                        if (ks == 0 && qq == 0) mfma_s<DT, true>(sacc[mb][nb], a, qf[mb][qq][ks]);
+                        else mfma_s<DT, false>(sacc[mb][nb], a, qf[mb][qq][ks]);
+                    }
                 }
             }
         }
+        // the asm MFMAs are hidden from the hazard recognizer: wait out their
+        // pipeline before the VALU reads the results
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+            asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(sacc[mb][0]), "+v"(sacc[mb][1]));
 
-        // ---- online softmax; lane holds tokens tt + 8g + (4nb + i) of row n
-        u32x4_t pfrag[MB][NP];
-        float alpha_row[MB][4];
+        // ---- softmax weights; lane holds tokens tt + 8g + (4nb + i) of row n
+        u32x4_t pfrag[MB];
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) {
             float x[8];
@@ -164,118 +223,169 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
             }
             mt = fmaxf(mt, wave_xor(mt, 16));
             mt = fmaxf(mt, wave_xor(mt, 32));
-            const float m_new = fmaxf(m_run[mb], mt);
-            const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-            const float alpha = fast_exp2(m_run[mb] - m_use);
+            if (m_ref[mb] == kNegInf) m_ref[mb] = mt;  // first visible tile: O is still 0
+            ovf_row[mb] |= mt > m_ref[mb] + TH;
+            const float m_use = (m_ref[mb] == kNegInf) ? 0.f : m_ref[mb];
             float ps = 0.f;
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 x[j] = fast_exp2(x[j] - m_use);
                 ps += x[j];
             }
-            l_part[mb] = l_part[mb] * alpha + ps;
-            m_run[mb] = m_new;
-            split_p<DT, NP>(x, pfrag[mb]);
-            // O rows are 4g+i: fetch their alpha from lane (4g+i)
-#pragma unroll
-            for (int i = 0; i < 4; i++) alpha_row[mb][i] = __shfl(alpha, 4 * g + i, 64);
-        }
-#pragma unroll
-        for (int mb = 0; mb < MB; mb++) {
-#pragma unroll
-            for (int d = 0; d < 32; d++) {
-#pragma unroll
-                for (int i = 0; i < 4; i++) o[mb][d][i] *= alpha_row[mb][i];
-            }
+            l_part[mb] += ps;
+            pfrag[mb] = u32x4_t{pack2<DT>(x[0], x[1]), pack2<DT>(x[2], x[3]),
+                                pack2<DT>(x[4], x[5]), pack2<DT>(x[6], x[7])};
         }
 
-        // ---- O += P . L[:, 0:512]; B operand: L[tt + 8g + j][16d + n], j < 8
-        const uint16_t* bcol = &lds[(8 * g) * kLROW + n];
+        // ---- O += P . L[:, 0:512]; B operand L[tt + 8g + j][16d + n], j < 8
 #pragma unroll
         for (int d = 0; d < 32; d++) {
-            uint32_t bw[4];
+            const u32x2_t lo = lds_read_tr16(tile + troff + 16 * d);
+            const u32x2_t hi = lds_read_tr16(tile + troff + 4 * kLROW + 16 * d);
+            const u32x4_t bf = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t e0 = bcol[(2 * j) * kLROW + 16 * d];
-                const uint32_t e1 = bcol[(2 * j + 1) * kLROW + 16 * d];
-                bw[j] = e0 | (e1 << 16);
-            }
-            const u32x4_t bf = u32x4_t{bw[0], bw[1], bw[2], bw[3]};
-#pragma unroll
-            for (int mb = 0; mb < MB; mb++) {
-#pragma unroll
-                for (int pp = 0; pp < NP; pp++) o[mb][d] = mfma16x16x32<DT>(pfrag[mb][pp], bf, o[mb][d]);
-            }
+            for (int mb = 0; mb < MB; mb++) o[mb][d] = mfma16x16x32<DT>(pfrag[mb], bf, o[mb][d]);
         }
+    };
+
+    issue(t_begin, 0);
+    if (ntiles > 1) issue(t_begin + kTT, 1);
+    for (int it = 0; it < ntiles; it += kNBuf) {
+        step(it, std::integral_constant<int, 0>{});
+        if (it + 1 < ntiles) step(it + 1, std::integral_constant<int, 1>{});
+        if (it + 2 < ntiles) step(it + 2, std::integral_constant<int, 2>{});
     }
 
-    // ---- epilogue
+    // ---- epilogue: unnormalised (m, l, o) partial of this split
+    const int64_t sbase = ((int64_t)b * p.num_splits + s) * p.R;
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
         float l = l_part[mb];
         l += wave_xor(l, 16);
         l += wave_xor(l, 32);
-        const int srow = row0 + 16 * mb + n;  // S-layout row of this lane
-        float l_row[4], inv_row[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            l_row[i] = __shfl(l, 4 * g + i, 64);
-            inv_row[i] = l_row[i] > 0.f ? 1.f / l_row[i] : 0.f;
+            const int row = row0 + 16 * mb + 4 * g + i;
+            if (row < p.R) {
+                float* dst = p.ws_o + (sbase + row) * kKR + n;
+#pragma unroll
+                for (int d = 0; d < 32; d++) dst[16 * d] = o[mb][d][i];
+            }
         }
-        if (p.num_splits == 1) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int row = row0 + 16 * mb + 4 * g + i;
-                if (row < p.R) {
-                    const int64_t base = ((int64_t)b * p.R + row) * kKR + n;
-#pragma unroll
-                    for (int d = 0; d < 32; d++)
-                        store_out<OUT_DT>(p.out, base + 16 * d, o[mb][d][i] * inv_row[i]);
-                }
-            }
-        } else {
-            const int64_t sbase = ((int64_t)b * p.num_splits + s) * p.R;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int row = row0 + 16 * mb + 4 * g + i;
-                if (row < p.R) {
-                    float* dst = p.ws_o + (sbase + row) * kKR + n;
-#pragma unroll
-                    for (int d = 0; d < 32; d++) dst[16 * d] = o[mb][d][i];
-                }
-            }
-            if (g == 0 && srow < p.R) {
-                p.ws_ml[(sbase + srow) * 2 + 0] = m_run[mb];
-                p.ws_ml[(sbase + srow) * 2 + 1] = l;
-            }
+        const int srow = row0 + 16 * mb + n;  // S-layout row of this lane
+        if (g == 0 && srow < p.R) {
+            p.ws_ml[(sbase + srow) * 2 + 0] = ovf_row[mb] ? __builtin_nanf("") : m_ref[mb];
+            p.ws_ml[(sbase + srow) * 2 + 1] = l;
         }
     }
 }
 
+// Exact fp32 recompute of one (row, split) partial, for rows the main kernel
+// flagged: pass 1 finds the row max, pass 2 accumulates l and o, both over
+// batches of 128 tokens (one token's 576-dim score per thread).
+template <int QDT, int DT>
+__device__ void mla_recompute_split(const MlaParams& p, int b, int row, int s, float* x_lds, float* red_lds,
+                                    float* ml_out, float* o_out) {
+    const int tid = threadIdx.x, d0 = tid * 4;
+    const int T = p.seq_lens[b];
+    const int teff = T - p.q_len + row / p.H + 1;
+    const int t_begin = s * p.chunk;
+    const int t_end = min(min(t_begin + p.chunk, T), teff);
+    const uint16_t* lat = p.lat + (int64_t)b * p.seq_stride;
+    auto qval = [&](int d) -> float {
+        const int64_t i = ((int64_t)b * p.R + row) * kCD + d;
+        if constexpr (QDT == DT_F32) return static_cast<const float*>(p.q)[i];
+        else return to_f32<DT>(static_cast<const uint16_t*>(p.q)[i]);
+    };
+    auto score = [&](int t) -> float {
+        const uint16_t* c = lat + (int64_t)t * kCD;
+        float acc = 0.f;
+        for (int d = 0; d < kCD; d++) acc += qval(d) * to_f32<DT>(c[d]);
+        return acc * p.scale_log2;
+    };
+    float M = kNegInf;
+    for (int t0 = t_begin; t0 < t_end; t0 += 128) {
+        const int t = t0 + tid;
+        float v = t < t_end ? score(t) : kNegInf;
+        v = wave_max(v);
+        if ((tid & 63) == 0) red_lds[tid >> 6] = v;
+        __syncthreads();
+        M = fmaxf(M, fmaxf(red_lds[0], red_lds[1]));
+        __syncthreads();
+    }
+    float L = 0.f;
+    f32x4_t O = {0.f, 0.f, 0.f, 0.f};
+    for (int t0 = t_begin; t0 < t_end; t0 += 128) {
+        const int t = t0 + tid;
+        x_lds[tid] = t < t_end ? fast_exp2(score(t) - M) : 0.f;
+        __syncthreads();
+        const int nt = min(128, t_end - t0);
+        for (int j = 0; j < nt; j++) {
+            const float pw = x_lds[j];
+            L += pw;
+            const uint16_t* c = lat + (int64_t)(t0 + j) * kCD + d0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) O[k] += pw * to_f32<DT>(c[k]);
+        }
+        __syncthreads();
+    }
+    *reinterpret_cast<f32x4_t*>(o_out + d0) = O;
+    if (tid == 0) {
+        ml_out[0] = M;
+        ml_out[1] = L;
+    }
+}
+
 // Log-sum-exp merge of split partials: one workgroup per (row, sequence),
-// 128 threads x 4 dims.
-template <int OUT_DT>
+// 128 threads x 4 dims; flagged splits are recomputed first, then the split
+// weights are formed in parallel and each thread sums its 4 dims over the
+// splits with independent 16-byte loads.
+template <int QDT, int DT, int OUT_DT>
 __global__ __launch_bounds__(128) void mla_decode_combine_kernel(MlaParams p) {
+    __shared__ float f_lds[kMaxSplits];
+    __shared__ float red_lds[2];
+    __shared__ int nflag;
     const int row = blockIdx.x, b = blockIdx.y, d = threadIdx.x * 4;
     const int T = p.seq_lens[b];
     const int nact = min(p.num_splits, (T + p.chunk - 1) / p.chunk);
-    float M = kNegInf;
-    for (int s = 0; s < nact; s++)
-        M = fmaxf(M, p.ws_ml[(((int64_t)b * p.num_splits + s) * p.R + row) * 2]);
-    float L = 0.f;
-    f32x4_t O = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < nact; s++) {
-        const int64_t slot = ((int64_t)b * p.num_splits + s) * p.R + row;
-        const float m = p.ws_ml[slot * 2];
-        const float f = (m == kNegInf) ? 0.f : fast_exp2(m - M);
-        L += f * p.ws_ml[slot * 2 + 1];
-        const f32x4_t v = *reinterpret_cast<const f32x4_t*>(p.ws_o + slot * kKR + d);
-        O += f * v;
+    const int64_t slot0 = (int64_t)b * p.num_splits * p.R + row;  // split s at slot0 + s*R
+    const int64_t st = (int64_t)p.R;
+
+    // rare path: recompute partials whose max is flagged as NaN
+    if (threadIdx.x == 0) nflag = 0;
+    __syncthreads();
+    for (int s = threadIdx.x; s < nact; s += blockDim.x)
+        if (__builtin_isnan(p.ws_ml[(slot0 + s * st) * 2])) nflag = 1;
+    __syncthreads();
+    if (nflag) {
+        for (int s = 0; s < nact; s++) {
+            const int64_t slot = slot0 + s * st;
+            const bool flagged = __builtin_isnan(p.ws_ml[slot * 2]);
+            __syncthreads();
+            if (flagged)
+                mla_recompute_split<QDT, DT>(p, b, row, s, f_lds, red_lds, p.ws_ml + slot * 2,
+                                             p.ws_o + slot * kKR);
+            __threadfence_block();
+            __syncthreads();
+        }
     }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
+
+    const float inv = lse_weights(p.ws_ml + slot0 * 2, st * 2, nact, f_lds, red_lds);
+    const float* os = p.ws_o + slot0 * kKR + d;
+    const int64_t ost = st * kKR;
+    f32x4_t O0 = {0.f, 0.f, 0.f, 0.f}, O1 = O0, O2 = O0, O3 = O0;
+    int s = 0;
+    for (; s + 4 <= nact; s += 4) {
+        O0 += f_lds[s] * *reinterpret_cast<const f32x4_t*>(os + s * ost);
+        O1 += f_lds[s + 1] * *reinterpret_cast<const f32x4_t*>(os + (s + 1) * ost);
+        O2 += f_lds[s + 2] * *reinterpret_cast<const f32x4_t*>(os + (s + 2) * ost);
+        O3 += f_lds[s + 3] * *reinterpret_cast<const f32x4_t*>(os + (s + 3) * ost);
+    }
+    for (; s < nact; s++) O0 += f_lds[s] * *reinterpret_cast<const f32x4_t*>(os + s * ost);
+    const f32x4_t O = ((O0 + O1) + (O2 + O3)) * inv;
     const int64_t base = ((int64_t)b * p.R + row) * kKR + d;
 #pragma unroll
-    for (int c = 0; c < 4; c++) store_out<OUT_DT>(p.out, base + c, O[c] * inv);
+    for (int c = 0; c < 4; c++) store_out<OUT_DT>(p.out, base + c, O[c]);
 }
 
 // ------------------------------------------------------------------ launch
@@ -283,42 +393,38 @@ __global__ __launch_bounds__(128) void mla_decode_combine_kernel(MlaParams p) {
 int mla_rows_per_block(int variant) { return 64 * variant; }
 
 template <int MB, int QDT, int DT, int OUT_DT>
-static hipError_t launch_mla_t(const MlaParams& p, int B, hipStream_t st, KernelTimer* t) {
-    const int nrb = (p.R + 64 * MB - 1) / (64 * MB);
+static hipError_t launch_mla_t(const MlaParams& p, hipStream_t st, KernelTimer* t) {
+    const int items = p.B * p.nrb * p.num_splits;
+    const int grid = (items + 7) / 8 * 8;  // multiple of the XCD count
     timer_begin(t, "mla_decode", st);
-    hipLaunchKernelGGL((mla_decode_kernel<MB, QDT, DT, OUT_DT>), dim3(nrb, p.num_splits, B),
-                       dim3(256), 0, st, p);
+    hipLaunchKernelGGL((mla_decode_kernel<MB, QDT, DT>), dim3(grid), dim3(256), 0, st, p);
     timer_end(t, "mla_decode", st);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || p.num_splits == 1) return e;
+    if (e != hipSuccess) return e;
     timer_begin(t, "mla_decode_combine", st);
-    hipLaunchKernelGGL((mla_decode_combine_kernel<OUT_DT>), dim3(p.R, B), dim3(128), 0, st, p);
+    hipLaunchKernelGGL((mla_decode_combine_kernel<QDT, DT, OUT_DT>), dim3(p.R, p.B), dim3(128), 0, st, p);
     timer_end(t, "mla_decode_combine", st);
     return hipGetLastError();
 }
 
 template <int MB, int QDT, int DT>
-static hipError_t launch_mla_o(const MlaParams& p, int B, int out_dt, hipStream_t st, KernelTimer* t) {
-    if (out_dt == DT_F32) return launch_mla_t<MB, QDT, DT, DT_F32>(p, B, st, t);
-    if (out_dt == DT_F16) return launch_mla_t<MB, QDT, DT, DT_F16>(p, B, st, t);
-    return launch_mla_t<MB, QDT, DT, DT_BF16>(p, B, st, t);
+static hipError_t launch_mla_o(const MlaParams& p, int out_dt, hipStream_t st, KernelTimer* t) {
+    if (out_dt == DT_F32) return launch_mla_t<MB, QDT, DT, DT_F32>(p, st, t);
+    if (out_dt == DT_F16) return launch_mla_t<MB, QDT, DT, DT_F16>(p, st, t);
+    return launch_mla_t<MB, QDT, DT, DT_BF16>(p, st, t);
 }
 
-template <int MB>
-static hipError_t launch_mla_mb(const MlaParams& p, int B, int q_dt, int lat_dt, int out_dt,
-                                hipStream_t st, KernelTimer* t) {
-    if (lat_dt == DT_F16) {
-        if (q_dt == DT_F32) return launch_mla_o<MB, DT_F32, DT_F16>(p, B, out_dt, st, t);
-        return launch_mla_o<MB, DT_F16, DT_F16>(p, B, out_dt, st, t);
-    }
-    if (q_dt == DT_F32) return launch_mla_o<MB, DT_F32, DT_BF16>(p, B, out_dt, st, t);
-    return launch_mla_o<MB, DT_BF16, DT_BF16>(p, B, out_dt, st, t);
-}
-
-hipError_t launch_mla_decode(const MlaParams& p, int B, int variant, int q_dt, int lat_dt, int out_dt,
+hipError_t launch_mla_decode(const MlaParams& p, int variant, int q_dt, int lat_dt, int out_dt,
                              hipStream_t st, KernelTimer* t) {
-    (void)variant;
-    return launch_mla_mb<1>(p, B, q_dt, lat_dt, out_dt, st, t);
+    // variant 2 (128 rows per workgroup) needs 16-bit q (register budget)
+    if (lat_dt == DT_F16) {
+        if (q_dt == DT_F32) return launch_mla_o<1, DT_F32, DT_F16>(p, out_dt, st, t);
+        if (variant == 2) return launch_mla_o<2, DT_F16, DT_F16>(p, out_dt, st, t);
+        return launch_mla_o<1, DT_F16, DT_F16>(p, out_dt, st, t);
+    }
+    if (q_dt == DT_F32) return launch_mla_o<1, DT_F32, DT_BF16>(p, out_dt, st, t);
+    if (variant == 2) return launch_mla_o<2, DT_BF16, DT_BF16>(p, out_dt, st, t);
+    return launch_mla_o<1, DT_BF16, DT_BF16>(p, out_dt, st, t);
 }
 
 }  // namespace mugen_attn

@@ -54,7 +54,7 @@ def test_v3_verify_config_sampled_heads_and_causal_consistency(device):
     for i in range(5):
         qi = qdev[:, i:i + 1].contiguous()
         dec = run_gpu(dict(c, q_len=1), device, seq_lens=[T - 5 + i + 1] * 4, q=qi)
-        np.testing.assert_allclose(got[:, i:i + 1], dec, atol=5e-5, rtol=1e-4)
+        np.testing.assert_allclose(got[:, i:i + 1], dec, atol=5e-4, rtol=1e-3)
 
 
 @pytest.mark.parametrize("B,q_len,H,lens,qdt,ldt", [
@@ -80,8 +80,9 @@ def test_16bit_outputs(device, od):
 def test_split_count_invariance(device):
     c = C.mla_case(49, 2, 1, 128, [5000, 2100], q_dtype=C.BF16, lat_dtype=C.BF16)
     outs = [run_gpu(c, device, C.F32, s) for s in (1, 0, 9, 100)]
+    # bf16 softmax weights: each split rounds its own P (relative 2^-9)
     for o in outs[1:]:
-        np.testing.assert_allclose(o, outs[0], atol=2e-5, rtol=1e-4)
+        np.testing.assert_allclose(o, outs[0], atol=5e-4, rtol=1e-3)
 
 
 def test_golden_fixture(device):
@@ -90,3 +91,22 @@ def test_golden_fixture(device):
              q_dtype=int(fx["q_dtype"]), lat_dtype=int(fx["lat_dtype"]), q=fx["q"], qb=fx["qb"],
              latb=fx["latb"], seq_lens=fx["seq_lens"])
     C.assert_close(run_gpu(c, device), fx["out_f64"], "golden mla_verify_small")
+
+
+@pytest.mark.parametrize("ldt,big", [(C.F16, 300.0), (C.BF16, 1000.0)])
+@pytest.mark.parametrize("splits", [0, 1])
+def test_late_score_overshoot_uses_exact_fallback(device, ldt, big, splits):
+    # a token far into the context scores far above every token of the first
+    # tile (beyond the weights' headroom): the flagged rows are recomputed
+    c = C.mla_case(60, 2, 2, 16, [900, 300], q_dtype=ldt, lat_dtype=ldt)
+    lat = c["lat"].copy()
+    lat[0, 700, :] = 0.0
+    lat[0, 700, 0] = big
+    lat[1, 250, 3] = -big
+    lat, latb = O.round_to(lat, ldt)
+    q = c["q"].copy()
+    q[:, :, :, 0] = np.abs(q[:, :, :, 0]) + 1.0
+    q[:, :, :, 3] = -np.abs(q[:, :, :, 3]) - 1.0
+    q, qb = O.round_to(q, ldt)
+    c2 = dict(c, lat=lat, latb=latb, q=q, qb=qb)
+    C.assert_close(run_gpu(c2, device, C.F32, splits), C.mla_ref(c2), f"overshoot fallback splits={splits}")
