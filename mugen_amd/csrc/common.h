@@ -67,9 +67,18 @@ __device__ __forceinline__ uint16_t from_f32(float f) {
     else return __builtin_bit_cast(uint16_t, _Float16(f));
 }
 
+// two fp32 -> packed 16-bit pair (RNE); gfx950 converts bf16 in hardware
+// (v_cvt_pk_bf16_f32) and fp16 with v_cvt_pk_f16_f32
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-    return uint32_t(from_f32<DT>(a)) | (uint32_t(from_f32<DT>(b)) << 16);
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    if constexpr (DT == DT_BF16) {
+        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+    } else {
+        typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
+    }
 }
 
 // store one fp32 value as OUT_DT

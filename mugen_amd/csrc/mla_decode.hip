@@ -19,9 +19,9 @@
 //    the 256-register O accumulator alone owns the AGPR file (the compiler
 //    would otherwise put both in AGPRs and spill);
 //  * latent tiles of 32 tokens stream into a 3-deep LDS ring by direct
-//    global->LDS DMA (global_load_lds_dwordx4), two tiles in flight, padded
-//    rows (74 x 16 B) so the MFMA operand reads spread over the banks; the
-//    tile loop is unrolled by the ring depth so buffer bases are constants;
+//    global->LDS DMA (global_load_lds_dwordx4), two tiles in flight; rows
+//    are XOR-swizzled in 16-byte chunks so both MFMA operand reads are
+//    bank-conflict free;
 //  * S^T uses a token permutation (A-row m of token block nb is token
 //    8*(m/4) + 4*nb + m%4) so each lane ends up holding 8 CONSECUTIVE tokens
 //    of its query row: exactly its k-slots as the A operand of P.L, so P
@@ -46,11 +46,23 @@ constexpr int kKR = 512;                // kv_lora_rank
 constexpr int kRD = 64;                 // rope dims
 constexpr int kCD = kKR + kRD;          // 576 latent dims per token
 constexpr int kTT = 32;                 // tokens per LDS tile
-constexpr int kLROW = kCD + 16;         // LDS row stride (halves): 1184 B = 74 x 16 B
-constexpr int kSlotsRow = kLROW / 8;    // 16-byte slots per LDS row (72 data + 2 pad)
-constexpr int kDmaPerWave = 10;         // DMA instructions per wave per tile (40 x 1 KiB)
-constexpr int kBufBytes = 4 * kDmaPerWave * 1024;  // 40 KiB per ring buffer (37 KiB used)
+constexpr int kRowBytes = kCD * 2;      // 1152 B per latent row (72 x 16-byte chunks)
+constexpr int kTileBytes = kTT * kRowBytes;       // 36 KiB
+constexpr int kDmaPerWave = kTileBytes / 1024 / 4;  // 9 one-KiB DMA instructions per wave
 constexpr int kNBuf = 3;                // ring depth: two tiles in flight
+
+// LDS swizzle: 16-byte chunk c of tile row r is stored at chunk c ^ swz(r).
+// gfx950 LDS serves 64 banks x 4 B per clock: 16 lanes of a b128 read or
+// 32 lanes of a b64 (transpose) read per cycle.  1152-byte rows put every
+// even row on bank 0 and every odd row on bank 32, so unswizzled the S
+// operand reads (rows 8*(n/4) + n%4 + 4nb) cost 8x and the transpose reads
+// (rows 8g + n/4 + 4hh) 4x their minimum.  This XOR of row bits 1, 3, 4
+// (found by exhaustive search over XOR swizzles against that bank model,
+// which reproduces measured conflict counts) makes both conflict-free; it
+// ignores row bit 2, so the nb / hh row offsets keep the same swizzle.
+__host__ __device__ constexpr int swz(int r) {
+    return (((r >> 1) & 1) * 2) ^ (((r >> 3) & 1) * 4) ^ ((r >> 4) & 1);
+}
 
 // Reference-max headroom (log2 units): with the max fixed at the first
 // visible tile, later weights may reach 2^TH.  bf16 P keeps fp32's exponent
@@ -79,18 +91,20 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     constexpr int KS = kCD / 32;  // 18 k-steps over the 576 dims
     constexpr int NQ = (QDT == DT_F32) ? 2 : 1;
     constexpr float TH = headroom_log2<DT>();
-    __shared__ __attribute__((aligned(1024))) uint16_t ring[kNBuf][kBufBytes / 2];
+    __shared__ __attribute__((aligned(1024))) uint16_t ring[kNBuf][kTileBytes / 2];
 
-    // XCD-aware work mapping: consecutive work items (the row blocks of one
-    // (sequence, split), then the splits of a sequence) land on one XCD,
-    // whose L2 then serves the latent tile to every row block
+    // XCD-aware work mapping.  Workgroups are dealt to the 8 XCDs round-robin
+    // by blockIdx.  A group = the nrb row blocks of one (sequence, split);
+    // they read the same latent tiles, so all of a group's row blocks go to
+    // one XCD (its L2 serves the tile to each), while consecutive groups go
+    // to different XCDs so every XCD gets an even share of the splits.
     const int nxcd = 8;
-    const int per_xcd = gridDim.x / nxcd;
-    const int wi = (blockIdx.x % nxcd) * per_xcd + blockIdx.x / nxcd;
+    const int xcd = blockIdx.x % nxcd, slot = blockIdx.x / nxcd;
     const int nrb = p.nrb;
-    const int rb = wi % nrb;
-    const int s = (wi / nrb) % p.num_splits;
-    const int b = wi / (nrb * p.num_splits);
+    const int rb = slot % nrb;
+    const int grp = (slot / nrb) * nxcd + xcd;  // (sequence, split) group
+    const int s = grp % p.num_splits;
+    const int b = grp / p.num_splits;
     if (b >= p.B) return;
 
     const int tid = threadIdx.x;
@@ -112,7 +126,9 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     for (int mb = 0; mb < MB; mb++) {
         const int row = row0 + 16 * mb + n;
         const bool ok = row < p.R;
-        teff[mb] = ok ? (T - p.q_len + row / p.H + 1) : 0;
+        // rows past R (padding of the last row block) have q = 0 and are
+        // treated as visible everywhere; their output is never stored
+        teff[mb] = ok ? (T - p.q_len + row / p.H + 1) : T;
         const int64_t qoff = ((int64_t)b * p.R + (ok ? row : 0)) * kCD + 8 * g;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
@@ -137,58 +153,101 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
         }
     }
 
-    // ---- tile staging by LDS DMA: wave w fills ring slots [64K, 64K+64) for
-    // K = w + 4k; slot -> (token slot/74, 16-byte chunk slot%74).  Offsets
-    // are clamped to the split's last valid byte, so pad chunks, slots past
-    // the tile and tokens past t_end all read valid cache rows (masked later)
-    const uint32_t ring_base = lds_addr(&ring[0][0]);
-    auto issue = [&](int tt, int buf) {
-        const uint16_t* tbase = lat + (int64_t)tt * kCD;               // wave-uniform
-        const uint32_t lim = (uint32_t)(t_end - tt) * (kCD * 2) - 16;  // last valid chunk
+    // smallest visible length over the wave's rows: tiles below it need no mask
+    int teff_min = teff[0];
 #pragma unroll
-        for (int k = 0; k < kDmaPerWave; k++) {
-            const int K = w + 4 * k;
-            const int slot = 64 * K + lane;
-            const int tok = slot / kSlotsRow, ch = slot - tok * kSlotsRow;
-            const uint32_t off = (uint32_t)(tok * (kCD * 2) + (ch < kCD / 8 ? ch : 0) * 16);
-            dma16s(ring_base + buf * kBufBytes + K * 1024, tbase, min(off, lim));
+    for (int mb = 1; mb < MB; mb++) teff_min = min(teff_min, teff[mb]);
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) teff_min = min(teff_min, __shfl_xor(teff_min, m, 64));
+
+    // Q loads complete here, through a wait the compiler's wait-count pass
+    // understands: it then inserts no vmcnt(0) inside the tile loop (where
+    // it would also drain the ring's in-flight DMA it cannot see)
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+
+    // ---- tile staging by LDS DMA: wave w fills LDS chunks [64K, 64K+64) of
+    // the tile for K = w + 4k; LDS chunk (r, pc) holds source chunk
+    // (r, pc ^ swz(r)).  Offsets are clamped to the split's last valid byte,
+    // so tokens past t_end read valid cache rows (masked later)
+    const uint32_t ring_base = lds_addr(&ring[0][0]);
+    uint32_t dma_off[kDmaPerWave];
+#pragma unroll
+    for (int k = 0; k < kDmaPerWave; k++) {
+        const int slot = 64 * (w + 4 * k) + lane;
+        const int r = slot / (kRowBytes / 16), pc = slot - r * (kRowBytes / 16);
+        dma_off[k] = (uint32_t)(r * kRowBytes + ((pc ^ swz(r)) * 16));
+    }
+    auto issue = [&](int tt, int buf) {
+        const uint16_t* tbase = lat + (int64_t)tt * kCD;  // wave-uniform
+        const uint32_t lds0 = ring_base + buf * kTileBytes + w * 1024;
+        if (tt + kTT <= t_end) {  // whole tile valid: precomputed offsets
+#pragma unroll
+            for (int k = 0; k < kDmaPerWave; k++) dma16s(lds0 + k * 4096, tbase, dma_off[k]);
+        } else {  // last tile of the split: clamp to its last valid chunk
+            const uint32_t lim = (uint32_t)(t_end - tt) * kRowBytes - 16;
+#pragma unroll
+            for (int k = 0; k < kDmaPerWave; k++) dma16s(lds0 + k * 4096, tbase, min(dma_off[k], lim));
         }
     };
 
-    // A-operand row of token block nb for this lane: token 8*(n/4) + 4*nb + n%4
-    const int aoff = (8 * (n >> 2) + (n & 3)) * kLROW + 8 * g;
-    // transpose-read offset: lane (i, g) of read h points at token 8g + 4h + i/4,
-    // latent dims 4*(i%4) .. +4 of the 16-dim block
-    const int troff = (8 * g + (n >> 2)) * kLROW + 4 * (n & 3);
+    // S operand (A): row ar = 8*(n/4) + n%4 (+4nb), logical chunk 4ks + g.
+    // swz(ar) does not depend on nb; (4ks + g) ^ h = 8*(ks/2) + ((4*(ks%2) + g) ^ h)
+    const int ar0 = 8 * (n >> 2) + (n & 3);
+    const int hA = swz(ar0);
+    const uint32_t a_off0 = ar0 * kRowBytes + ((g ^ hA) * 16);
+    const uint32_t a_off1 = ar0 * kRowBytes + (((4 + g) ^ hA) * 16);
+    // P.L operand (transpose reads): lane (i, g) of read hh reads row
+    // 8g + 4hh + i/4, logical bytes 32d + 8*(i%4) = chunk 2d + (i%4)/2
+    const int tr0 = 8 * g + (n >> 2);
+    const int hT = swz(tr0);  // independent of hh
+    uint32_t t_off[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        t_off[j] = tr0 * kRowBytes + (((2 * j + ((n & 3) >> 1)) ^ hT) * 16) + 8 * (n & 1);
 
     f32x4_t o[MB][32];
     float m_ref[MB], l_part[MB];  // reference max (log2 units) and partial sum
-    bool ovf_row[MB];             // this lane's S-row overshot the headroom
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
         m_ref[mb] = kNegInf;
         l_part[mb] = 0.f;
-        ovf_row[mb] = false;
 #pragma unroll
         for (int d = 0; d < 32; d++) o[mb][d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
 
-    auto step = [&](int it, auto buf_tag) {
-        constexpr int BUF = decltype(buf_tag)::value;
+    const char* ring_bytes = reinterpret_cast<const char*>(&ring[0][0]);
+    issue(t_begin, 0);
+    if (ntiles > 1) issue(t_begin + kTT, 1);
+    int buf = 0;
+    for (int it = 0; it < ntiles; it++) {
         if (it + 1 < ntiles) vm_wait<kDmaPerWave>();
         else vm_wait<0>();
-        lds_barrier();  // tile `it` landed for every wave; buffer (it+2)%3 is free
-        if (it + 2 < ntiles) issue(t_begin + kTT * (it + 2), (BUF + 2) % kNBuf);
-        const uint16_t* tile = &ring[BUF][0];
+        lds_barrier();  // tile `it` landed for every wave; the buffer of tile it-1 is free
+        if (it + 2 < ntiles) issue(t_begin + kTT * (it + 2), buf == 0 ? 2 : buf - 1);
+        const char* tile = ring_bytes + buf * kTileBytes;
+        buf = buf == kNBuf - 1 ? 0 : buf + 1;
         const int tt = t_begin + kTT * it;
 
-        // ---- S^T = L . Q^T  (two 16-token blocks), VGPR accumulators
+        // ---- S^T = L . Q^T  (two 16-token blocks), VGPR accumulators.
+        // Software-pipelined: operands of k-step ks+SPD are requested while
+        // step ks runs, so each LDS read has ~2 steps of MFMA work to land.
+        constexpr int SPD = 3;
+        auto a_ptr = [&](int ks, int nb) {
+            return reinterpret_cast<const u32x4_t*>(tile + ((ks & 1) ? a_off1 : a_off0) + 128 * (ks >> 1) +
+                                                    4 * kRowBytes * nb);
+        };
+        u32x4_t abuf[SPD][2];
+#pragma unroll
+        for (int j = 0; j < SPD; j++) {
+            abuf[j][0] = *a_ptr(j, 0);
+            abuf[j][1] = *a_ptr(j, 1);
+        }
         f32x4_t sacc[MB][2];
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
 #pragma unroll
             for (int nb = 0; nb < 2; nb++) {
-                const u32x4_t a = *reinterpret_cast<const u32x4_t*>(tile + aoff + 4 * nb * kLROW + 32 * ks);
+                const u32x4_t a = abuf[ks % SPD][nb];
 #pragma unroll
                 for (int mb = 0; mb < MB; mb++) {
 #pragma unroll
@@ -198,62 +257,95 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
                     }
                 }
             }
+            if (ks + SPD < KS) {
+                abuf[ks % SPD][0] = *a_ptr(ks + SPD, 0);
+                abuf[ks % SPD][1] = *a_ptr(ks + SPD, 1);
+            }
         }
+        // first P.L operands requested now, to land during the softmax
+        constexpr int VPD = 6;
+        auto tr_load = [&](int d) {
+            const char* tp = tile + t_off[d & 3] + 128 * (d >> 2);
+            const u32x2_t lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(tp));
+            const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(tp + 4 * kRowBytes));
+            return u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+        };
+        u32x4_t bbuf[VPD];
+#pragma unroll
+        for (int j = 0; j < VPD; j++) bbuf[j] = tr_load(j);
         // the asm MFMAs are hidden from the hazard recognizer: wait out their
         // pipeline before the VALU reads the results
 #pragma unroll
         for (int mb = 0; mb < MB; mb++)
             asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(sacc[mb][0]), "+v"(sacc[mb][1]));
 
-        // ---- softmax weights; lane holds tokens tt + 8g + (4nb + i) of row n
-        u32x4_t pfrag[MB];
+        // ---- softmax weights; lane holds tokens tt + 8g + (4nb + i) of row n.
+        // A row's reference max is the max of its first visible tile (a
+        // cross-lane reduction, taken only while some row of the wave has
+        // none yet); afterwards each weight is exp2(s*scale*log2e - m_ref),
+        // one fma + one exp2, and only edge tiles (split end, causal rows)
+        // pay for masking.
+        bool fresh = false;
 #pragma unroll
-        for (int mb = 0; mb < MB; mb++) {
-            float x[8];
-            float mt = kNegInf;
+        for (int mb = 0; mb < MB; mb++) fresh |= (m_ref[mb] == kNegInf);
+        if (__any(fresh)) {
 #pragma unroll
-            for (int nb = 0; nb < 2; nb++) {
+            for (int mb = 0; mb < MB; mb++) {
+                float mt = kNegInf;
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int tok = tt + 8 * g + 4 * nb + i;
-                    const bool vis = tok < t_end && tok < teff[mb];
-                    x[4 * nb + i] = vis ? sacc[mb][nb][i] * p.scale_log2 : kNegInf;
-                    mt = fmaxf(mt, x[4 * nb + i]);
+                for (int nb = 0; nb < 2; nb++) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int tok = tt + 8 * g + 4 * nb + i;
+                        const bool vis = tok < t_end && tok < teff[mb];
+                        mt = fmaxf(mt, vis ? sacc[mb][nb][i] * p.scale_log2 : kNegInf);
+                    }
                 }
+                mt = fmaxf(mt, wave_xor(mt, 16));
+                mt = fmaxf(mt, wave_xor(mt, 32));
+                if (m_ref[mb] == kNegInf) m_ref[mb] = mt;  // O of this row is still 0
             }
-            mt = fmaxf(mt, wave_xor(mt, 16));
-            mt = fmaxf(mt, wave_xor(mt, 32));
-            if (m_ref[mb] == kNegInf) m_ref[mb] = mt;  // first visible tile: O is still 0
-            ovf_row[mb] |= mt > m_ref[mb] + TH;
-            const float m_use = (m_ref[mb] == kNegInf) ? 0.f : m_ref[mb];
-            float ps = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                x[j] = fast_exp2(x[j] - m_use);
-                ps += x[j];
-            }
-            l_part[mb] += ps;
-            pfrag[mb] = u32x4_t{pack2<DT>(x[0], x[1]), pack2<DT>(x[2], x[3]),
-                                pack2<DT>(x[4], x[5]), pack2<DT>(x[6], x[7])};
         }
+        u32x4_t pfrag[MB];
+        auto weights = [&](auto masked_tag) {
+            constexpr bool MASKED = decltype(masked_tag)::value;
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++) {
+                const float mneg = (m_ref[mb] == kNegInf) ? 0.f : -m_ref[mb];
+                float x[8];
+#pragma unroll
+                for (int nb = 0; nb < 2; nb++) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        float v = fmaf(sacc[mb][nb][i], p.scale_log2, mneg);
+                        if constexpr (MASKED) {
+                            const int tok = tt + 8 * g + 4 * nb + i;
+                            v = (tok < t_end && tok < teff[mb]) ? v : kNegInf;
+                        }
+                        x[4 * nb + i] = fast_exp2(v);
+                    }
+                }
+                l_part[mb] += ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
+                pfrag[mb] = u32x4_t{pack2<DT>(x[0], x[1]), pack2<DT>(x[2], x[3]),
+                                    pack2<DT>(x[4], x[5]), pack2<DT>(x[6], x[7])};
+            }
+        };
+        // wave-uniform: interior tiles (the common case) carry no mask
+        if (tt + kTT <= t_end && tt + kTT <= teff_min) weights(std::false_type{});
+        else weights(std::true_type{});
 
-        // ---- O += P . L[:, 0:512]; B operand L[tt + 8g + j][16d + n], j < 8
+        // ---- O += P . L[:, 0:512]; B operand L[tt + 8g + j][16d + n], j < 8.
+        // The schedule is pinned to [MFMA x MB][2 transpose reads of d+VPD]
+        // so VPD steps of reads stay in flight behind the MFMAs.
 #pragma unroll
         for (int d = 0; d < 32; d++) {
-            const u32x2_t lo = lds_read_tr16(tile + troff + 16 * d);
-            const u32x2_t hi = lds_read_tr16(tile + troff + 4 * kLROW + 16 * d);
-            const u32x4_t bf = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+            const u32x4_t bf = bbuf[d % VPD];
+            if (d + VPD < 32) bbuf[d % VPD] = tr_load(d + VPD);
 #pragma unroll
             for (int mb = 0; mb < MB; mb++) o[mb][d] = mfma16x16x32<DT>(pfrag[mb], bf, o[mb][d]);
+            __builtin_amdgcn_sched_group_barrier(0x008, MB, 0);
+            if (d + VPD < 32) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
-    };
-
-    issue(t_begin, 0);
-    if (ntiles > 1) issue(t_begin + kTT, 1);
-    for (int it = 0; it < ntiles; it += kNBuf) {
-        step(it, std::integral_constant<int, 0>{});
-        if (it + 1 < ntiles) step(it + 1, std::integral_constant<int, 1>{});
-        if (it + 2 < ntiles) step(it + 2, std::integral_constant<int, 2>{});
     }
 
     // ---- epilogue: unnormalised (m, l, o) partial of this split
@@ -274,7 +366,10 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
         }
         const int srow = row0 + 16 * mb + n;  // S-layout row of this lane
         if (g == 0 && srow < p.R) {
-            p.ws_ml[(sbase + srow) * 2 + 0] = ovf_row[mb] ? __builtin_nanf("") : m_ref[mb];
+            // every weight is <= l: a sum past the headroom means some weight
+            // may have overflowed its 16-bit P; flag the row for the exact path
+            const bool ovf = !(l <= exp2f(TH));
+            p.ws_ml[(sbase + srow) * 2 + 0] = ovf ? __builtin_nanf("") : m_ref[mb];
             p.ws_ml[(sbase + srow) * 2 + 1] = l;
         }
     }
@@ -394,8 +489,8 @@ int mla_rows_per_block(int variant) { return 64 * variant; }
 
 template <int MB, int QDT, int DT, int OUT_DT>
 static hipError_t launch_mla_t(const MlaParams& p, hipStream_t st, KernelTimer* t) {
-    const int items = p.B * p.nrb * p.num_splits;
-    const int grid = (items + 7) / 8 * 8;  // multiple of the XCD count
+    const int groups = p.B * p.num_splits;         // (sequence, split) pairs
+    const int grid = 8 * p.nrb * ((groups + 7) / 8);  // see the XCD mapping in the kernel
     timer_begin(t, "mla_decode", st);
     hipLaunchKernelGGL((mla_decode_kernel<MB, QDT, DT>), dim3(grid), dim3(256), 0, st, p);
     timer_end(t, "mla_decode", st);
