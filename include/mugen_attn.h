@@ -179,7 +179,10 @@ typedef struct mugen_attn_mla_decode_args {
     int32_t q_dtype;
     int32_t latent_dtype;
     int32_t out_dtype;
-    /* optional HOST copy of seq_lens (NULL allowed), planning hint only */
+    /* optional HOST copy of seq_lens (NULL allowed).  When given it sizes the
+     * grid to exactly the active context splits, so every entry must be >=
+     * the device value (normally equal; a larger value only costs idle
+     * workgroups).  NULL sizes the grid for batch * max_seq_len. */
     const int32_t* seq_lens_host;
 } mugen_attn_mla_decode_args;
 

@@ -143,20 +143,21 @@ static int64_t planned_tokens(const int32_t* host_lens, int batch, int max_seq_l
 
 // Tokens per split for a workgroup count target; rounded to `quantum`, and
 // large enough that no more than kMaxSplits splits cover max_seq_len.
-static int plan_chunk(int64_t tokens_x_groups, int target_wgs, int quantum, int max_seq_len) {
+static int plan_chunk(int64_t tokens_x_groups, int target_wgs, int quantum, int max_seq_len,
+                      int max_splits = kMaxSplits) {
     int64_t c = (tokens_x_groups + target_wgs - 1) / target_wgs;
     c = ((c + quantum - 1) / quantum) * quantum;
     if (c < quantum) c = quantum;
-    const int64_t min_c = ((int64_t)(max_seq_len > 0 ? max_seq_len : 1) + kMaxSplits - 1) / kMaxSplits;
+    const int64_t min_c = ((int64_t)(max_seq_len > 0 ? max_seq_len : 1) + max_splits - 1) / max_splits;
     if (c < min_c) c = ((min_c + quantum - 1) / quantum) * quantum;
     return (int)c;
 }
 
-static int explicit_chunk(int max_seq_len, int num_splits, int quantum) {
+static int explicit_chunk(int max_seq_len, int num_splits, int quantum, int max_splits = kMaxSplits) {
     const int maxT = max_seq_len > 0 ? max_seq_len : 1;
     int64_t c = ((int64_t)maxT + num_splits - 1) / num_splits;
     c = ((c + quantum - 1) / quantum) * quantum;
-    const int64_t min_c = ((int64_t)maxT + kMaxSplits - 1) / kMaxSplits;
+    const int64_t min_c = ((int64_t)maxT + max_splits - 1) / max_splits;
     if (c < min_c) c = ((min_c + quantum - 1) / quantum) * quantum;
     return (int)c;
 }
@@ -211,13 +212,38 @@ static int mla_variant(const mugen_attn_mla_decode_args* a) {
     return (R > 64 && a->q_dtype != DT_F32) ? 2 : 1;
 }
 
-// one 256-thread workgroup per CU (the kernel holds ~460 registers per lane)
+// Active (sequence, split) groups for a chunk: exact from the host length
+// hint, else the batch * max_seq_len upper bound.
+static int64_t mla_groups(const mugen_attn_mla_decode_args* a, int chunk) {
+    if (!a->seq_lens_host) return (int64_t)a->batch * ceil_div(a->max_seq_len > 0 ? a->max_seq_len : 1, chunk);
+    int64_t g = 0;
+    for (int b = 0; b < a->batch; b++) g += a->seq_lens_host[b] > 0 ? ceil_div(a->seq_lens_host[b], chunk) : 0;
+    return g;
+}
+
+// The MLA kernel runs one 256-thread workgroup per CU (~480 registers per
+// lane, 108 KiB LDS), and each workgroup pays a fixed cost (Q fragments,
+// ring fill, partial store) on top of ~1.8 us per 32-token tile.  The plan:
+// the smallest chunk (multiple of 32) whose nrb * active groups fit ONE
+// dispatch round of 256 CUs -- maximum parallelism, no second round.
 static int mla_chunk(const mugen_attn_mla_decode_args* a, int variant) {
-    if (a->num_splits > 0) return explicit_chunk(a->max_seq_len, a->num_splits, 32);
+    if (a->num_splits > 0) return explicit_chunk(a->max_seq_len, a->num_splits, 32, kMaxMlaSplits);
     const int R = a->q_len * a->n_heads;
     const int64_t nrb = ceil_div(R, mla_rows_per_block(variant));
-    const int64_t work = planned_tokens(a->seq_lens_host, a->batch, a->max_seq_len) * nrb;
-    return plan_chunk(work, 256, 32, a->max_seq_len);
+    const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
+    const int cmax = ceil_div(maxT, 32) * 32;
+    const int cmin = ceil_div(ceil_div(maxT, kMaxMlaSplits), 32) * 32;
+    const int64_t wg_budget = 256;
+    if (nrb * mla_groups(a, cmax) > wg_budget) return cmax;  // one split per sequence already fills a round
+    int lo = cmin < 32 ? 32 : cmin, hi = cmax;               // groups(c) is non-increasing in c
+    while (lo < hi) {
+        const int mid = ((lo + hi) / 2) / 32 * 32;
+        if (mid <= lo) break;
+        if (nrb * mla_groups(a, mid) <= wg_budget) hi = mid;
+        else lo = mid + 32;
+    }
+    if (nrb * mla_groups(a, lo) > wg_budget) lo = hi;
+    return lo;
 }
 
 static int mla_validate(const mugen_attn_mla_decode_args* a) {
@@ -251,8 +277,10 @@ static size_t mla_ws(const mugen_attn_mla_decode_args* a, int chunk, int* splits
     const int splits = ceil_div(maxT, chunk);
     if (splits_out) *splits_out = splits;
     // every split (a single one included) writes an fp32 (m, l, o) partial
-    const size_t slots = (size_t)a->batch * splits * a->q_len * a->n_heads;
-    return slots * 512 * 4 + slots * 2 * 4 + 256;
+    const size_t R = (size_t)a->q_len * a->n_heads;
+    const size_t rows16 = (R + 15) / 16 * 16;  // O partials are stored per 16-row block
+    const size_t sb = (size_t)a->batch * splits;
+    return sb * rows16 * 512 * 2 + sb * R * 2 * 4 + 256;
 }
 
 static float* align256(void* p) {
@@ -371,15 +399,17 @@ int mugen_attn_mla_decode(const mugen_attn_mla_decode_args* a, void* ws, size_t 
     p.B = a->batch;
     p.R = a->q_len * a->n_heads;
     p.nrb = ceil_div(p.R, mla_rows_per_block(variant));
+    p.nq = ceil_div(p.R, 16);
+    p.groups = (int)mla_groups(a, chunk);
     p.chunk = chunk;
     p.num_splits = splits;
     p.seq_stride = a->seq_stride;
     p.scale_log2 = a->scale * kLog2e;
     {
         float* base = align256(ws);
-        const size_t slots = (size_t)a->batch * splits * p.R;
+        const size_t sb = (size_t)a->batch * splits;
         p.ws_o = base;
-        p.ws_ml = base + slots * 512;
+        p.ws_ml = base + sb * (size_t)p.nq * 16 * 512 / 2;  // after the fp16 O blob
     }
     hipError_t e = launch_mla_decode(p, variant, a->q_dtype, a->latent_dtype, a->out_dtype,
                                      static_cast<hipStream_t>(stream), active_timer());

@@ -156,6 +156,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 // writes f_s = 2^(m_s - M) to LDS and returns 1 / sum_s f_s l_s (0 when
 // no split saw a token).  All threads of the block must call it.
 constexpr int kMaxSplits = 4096;
+constexpr int kMaxMlaSplits = 512;  // MLA combine keeps per-row split weights in LDS
 __device__ __forceinline__ float lse_weights(const float* ml, int64_t ml_stride, int nact, float* f_lds,
                                              float* red_lds) {
     const int tid = threadIdx.x, nw = blockDim.x >> 6, w = tid >> 6;

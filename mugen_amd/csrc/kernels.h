@@ -53,13 +53,15 @@ struct MlaParams {
     const uint16_t* lat;   // latent cache
     const int32_t* seq_lens;
     void* out;             // [B][q_len*H][512]
-    float* ws_o;           // [B][splits][R][512]
+    float* ws_o;           // [B][splits][nq][32][64] fp16x4 fragments of o/l (see blob_frag)
     float* ws_ml;          // [B][splits][R][2]
     int B;
     int q_len;
     int H;
     int R;                 // q_len * H rows per sequence
     int nrb;               // row blocks per sequence (ceil(R / rows per block))
+    int nq;                // 16-row blocks per sequence (ceil(R / 16))
+    int groups;            // active (sequence, split) groups the grid covers (upper bound)
     int chunk;
     int num_splits;
     int64_t seq_stride;

@@ -33,8 +33,10 @@
 //    exponent range), so O is never rescaled.  A row whose score overshoots
 //    the reference by the dtype's headroom is flagged (NaN max) and the
 //    combine kernel recomputes that (row, split) exactly in fp32;
-//  * every workgroup writes an fp32 (m, l, o) partial; mla_decode_combine
-//    merges the splits of a row with fp32 log-sum-exp;
+//  * every workgroup writes its split's (m, l) in fp32 and the normalised
+//    o/l (a convex combination of latent rows) in fp16, in accumulator-
+//    fragment order; mla_decode_combine merges the splits of a row with
+//    fp32 log-sum-exp weights and fp32 accumulation;
 //  * q in fp32 is split into hi + lo 16-bit halves (two MFMAs), keeping the
 //    scores fp32-accurate like the reference's float q_absorbed.
 #include "common.h"
@@ -70,6 +72,14 @@ __host__ __device__ constexpr int swz(int r) {
 template <int DT>
 __device__ constexpr float headroom_log2() { return DT == DT_BF16 ? 64.f : 15.f; }
 
+// O partial blob (normalised o/l, fp16), in MFMA accumulator-fragment
+// order: for sequence b, split s and 16-row block q, the 4-element fragment
+//   (((b*S + s)*nq + q)*32 + d)*64 + lane
+// holds rows 16q + 4*(lane/16) + i (i = 0..3) at column 16d + lane%16.
+__device__ __forceinline__ int64_t blob_frag(const MlaParams& p, int b, int s, int q, int d, int lane) {
+    return ((((int64_t)b * p.num_splits + s) * p.nq + q) * 32 + d) * 64 + lane;
+}
+
 // S-chain MFMA with a VGPR accumulator (FIRST: C = 0)
 template <int DT, bool FIRST>
 __device__ __forceinline__ void mfma_s(f32x4_t& acc, const u32x4_t& a, const u32x4_t& b) {
@@ -98,14 +108,26 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     // they read the same latent tiles, so all of a group's row blocks go to
     // one XCD (its L2 serves the tile to each), while consecutive groups go
     // to different XCDs so every XCD gets an even share of the splits.
+    // Groups are numbered compactly over the ACTIVE splits only (sequence j
+    // contributes ceil(seq_lens[j] / chunk) of them), so a grid sized from
+    // the host's length hint has no idle workgroups and every XCD gets an
+    // even share in a single dispatch round.
     const int nxcd = 8;
     const int xcd = blockIdx.x % nxcd, slot = blockIdx.x / nxcd;
     const int nrb = p.nrb;
     const int rb = slot % nrb;
-    const int grp = (slot / nrb) * nxcd + xcd;  // (sequence, split) group
-    const int s = grp % p.num_splits;
-    const int b = grp / p.num_splits;
-    if (b >= p.B) return;
+    const int grp = (slot / nrb) * nxcd + xcd;  // active (sequence, split) group
+    int b = -1, s = 0;
+    for (int j = 0, acc = 0; j < p.B; j++) {  // uniform scalar loop over the batch
+        const int nsj = (p.seq_lens[j] + p.chunk - 1) / p.chunk;
+        if (grp < acc + nsj) {
+            b = j;
+            s = grp - acc;
+            break;
+        }
+        acc += nsj;
+    }
+    if (b < 0) return;  // grid padding past the last active split
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
@@ -113,7 +135,6 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     const int T = p.seq_lens[b];
     const int t_begin = s * p.chunk;
     const int t_end = min(t_begin + p.chunk, T);
-    if (t_begin >= T) return;  // empty split: the combine skips it
     const int ntiles = (t_end - t_begin + kTT - 1) / kTT;
 
     const int row0 = rb * (64 * MB) + w * (16 * MB);
@@ -348,40 +369,58 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
         }
     }
 
-    // ---- epilogue: unnormalised (m, l, o) partial of this split
-    const int64_t sbase = ((int64_t)b * p.num_splits + s) * p.R;
+    // ---- epilogue: (m, l, o/l) partial of this split.  The normalised O is
+    // a convex combination of latent rows and goes out as fp16 in
+    // accumulator-fragment order (4 rows x 1 column per lane, 512 B
+    // contiguous per store instruction); m and l stay fp32.  A row whose
+    // weights or normalised values left the 16-bit ranges is flagged (NaN m)
+    // for the exact fp32 recompute in the combine kernel.
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
         float l = l_part[mb];
         l += wave_xor(l, 16);
         l += wave_xor(l, 32);
+        float inv[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int row = row0 + 16 * mb + 4 * g + i;
-            if (row < p.R) {
-                float* dst = p.ws_o + (sbase + row) * kKR + n;
+            const float lr = __shfl(l, 4 * g + i, 64);
+            inv[i] = lr > 0.f ? 1.f / lr : 0.f;
+        }
+        const int rblk = row0 + 16 * mb;  // first row of this 16-row block
+        bool big = false;
+        if (rblk < p.R) {
+            u32x2_t* dst = reinterpret_cast<u32x2_t*>(p.ws_o) + blob_frag(p, b, s, rblk >> 4, 0, lane);
 #pragma unroll
-                for (int d = 0; d < 32; d++) dst[16 * d] = o[mb][d][i];
+            for (int d = 0; d < 32; d++) {
+                const f32x4_t v = o[mb][d] * f32x4_t{inv[0], inv[1], inv[2], inv[3]};
+                big |= fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))) > 65000.f;
+                dst[d * 64] = u32x2_t{pack2<DT_F16>(v[0], v[1]), pack2<DT_F16>(v[2], v[3])};
             }
         }
-        const int srow = row0 + 16 * mb + n;  // S-layout row of this lane
+        // rows 4g+i of this lane overflowed -> tell their S-layout lanes (row n)
+        const uint64_t big_mask = __ballot(big);
+        const bool row_big = (big_mask >> (n >> 2) * 16) & 0xffffull;  // any lane of quad n/4
+        const int srow = rblk + n;  // S-layout row of this lane
         if (g == 0 && srow < p.R) {
             // every weight is <= l: a sum past the headroom means some weight
-            // may have overflowed its 16-bit P; flag the row for the exact path
-            const bool ovf = !(l <= exp2f(TH));
-            p.ws_ml[(sbase + srow) * 2 + 0] = ovf ? __builtin_nanf("") : m_ref[mb];
-            p.ws_ml[(sbase + srow) * 2 + 1] = l;
+            // may have overflowed its 16-bit P
+            const bool ovf = !(l <= exp2f(TH)) || row_big;
+            const int64_t slot = ((int64_t)b * p.num_splits + s) * p.R + srow;
+            p.ws_ml[slot * 2 + 0] = ovf ? __builtin_nanf("") : m_ref[mb];
+            p.ws_ml[slot * 2 + 1] = l;
         }
     }
 }
 
 // Exact fp32 recompute of one (row, split) partial, for rows the main kernel
 // flagged: pass 1 finds the row max, pass 2 accumulates l and o, both over
-// batches of 128 tokens (one token's 576-dim score per thread).
+// batches of blockDim tokens (one token's 576-dim score per thread); each
+// thread then owns 512/blockDim output columns.
 template <int QDT, int DT>
-__device__ void mla_recompute_split(const MlaParams& p, int b, int row, int s, float* x_lds, float* red_lds,
-                                    float* ml_out, float* o_out) {
-    const int tid = threadIdx.x, d0 = tid * 4;
+__device__ void mla_recompute_split(const MlaParams& p, int b, int row, int s, float* x_lds, float* red_lds) {
+    const int tid = threadIdx.x, nt = blockDim.x, nw = nt >> 6;
+    constexpr int kMaxCols = 8;  // 512 / 64: at least one wave per workgroup
+    const int ncols = kKR / nt;
     const int T = p.seq_lens[b];
     const int teff = T - p.q_len + row / p.H + 1;
     const int t_begin = s * p.chunk;
@@ -399,88 +438,149 @@ __device__ void mla_recompute_split(const MlaParams& p, int b, int row, int s, f
         return acc * p.scale_log2;
     };
     float M = kNegInf;
-    for (int t0 = t_begin; t0 < t_end; t0 += 128) {
+    for (int t0 = t_begin; t0 < t_end; t0 += nt) {
         const int t = t0 + tid;
-        float v = t < t_end ? score(t) : kNegInf;
-        v = wave_max(v);
+        float v = wave_max(t < t_end ? score(t) : kNegInf);
         if ((tid & 63) == 0) red_lds[tid >> 6] = v;
         __syncthreads();
-        M = fmaxf(M, fmaxf(red_lds[0], red_lds[1]));
+        for (int w = 0; w < nw; w++) M = fmaxf(M, red_lds[w]);
         __syncthreads();
     }
     float L = 0.f;
-    f32x4_t O = {0.f, 0.f, 0.f, 0.f};
-    for (int t0 = t_begin; t0 < t_end; t0 += 128) {
+    float O[kMaxCols] = {};
+    for (int t0 = t_begin; t0 < t_end; t0 += nt) {
         const int t = t0 + tid;
         x_lds[tid] = t < t_end ? fast_exp2(score(t) - M) : 0.f;
         __syncthreads();
-        const int nt = min(128, t_end - t0);
-        for (int j = 0; j < nt; j++) {
+        const int cnt = min(nt, t_end - t0);
+        for (int j = 0; j < cnt; j++) {
             const float pw = x_lds[j];
             L += pw;
-            const uint16_t* c = lat + (int64_t)(t0 + j) * kCD + d0;
-#pragma unroll
-            for (int k = 0; k < 4; k++) O[k] += pw * to_f32<DT>(c[k]);
+            const uint16_t* c = lat + (int64_t)(t0 + j) * kCD;
+            for (int k = 0; k < ncols; k++) O[k] += pw * to_f32<DT>(c[tid + k * nt]);
         }
         __syncthreads();
     }
-    *reinterpret_cast<f32x4_t*>(o_out + d0) = O;
+    // normalised, fp16, fragment order; fp32 values beyond fp16 cannot come
+    // from a convex combination of finite 16-bit latent rows
+    uint16_t* blob = reinterpret_cast<uint16_t*>(p.ws_o);
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    for (int k = 0; k < ncols; k++) {
+        const int col = tid + k * nt;
+        const int lane = 16 * ((row & 15) >> 2) + (col & 15);
+        blob[blob_frag(p, b, s, row >> 4, col >> 4, lane) * 4 + (row & 3)] = from_f32<DT_F16>(O[k] * inv);
+    }
     if (tid == 0) {
-        ml_out[0] = M;
-        ml_out[1] = L;
+        const int64_t slot = ((int64_t)b * p.num_splits + s) * p.R + row;
+        p.ws_ml[slot * 2 + 0] = M;
+        p.ws_ml[slot * 2 + 1] = L;
     }
 }
 
-// Log-sum-exp merge of split partials: one workgroup per (row, sequence),
-// 128 threads x 4 dims; flagged splits are recomputed first, then the split
-// weights are formed in parallel and each thread sums its 4 dims over the
-// splits with independent 16-byte loads.
+// Log-sum-exp merge of the split partials.  Workgroup = (16-row block,
+// group of 8 column blocks, sequence).  The per-row split weights
+// w_s = 2^(m_s - M) l_s are formed once in LDS (16 splits x 16 rows in
+// parallel); then lane l of wave w reads, per split, the fp16 fragments
+// (4 rows x 1 column) of column blocks 2w, 2w+1 -- the order the main
+// kernel wrote, 512 B contiguous per wave -- and accumulates in fp32.
+// Rows the main kernel flagged are recomputed first.
 template <int QDT, int DT, int OUT_DT>
-__global__ __launch_bounds__(128) void mla_decode_combine_kernel(MlaParams p) {
-    __shared__ float f_lds[kMaxSplits];
-    __shared__ float red_lds[2];
+__global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
+    __shared__ __attribute__((aligned(16))) float wts[kMaxMlaSplits][16];
+    __shared__ float red[16][16];
+    __shared__ float linv[16];
+    __shared__ float x_lds[256];
     __shared__ int nflag;
-    const int row = blockIdx.x, b = blockIdx.y, d = threadIdx.x * 4;
+    const int qb = blockIdx.x, dg = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, dsub = tid >> 6;
+    const int g = lane >> 4, n = lane & 15;
     const int T = p.seq_lens[b];
     const int nact = min(p.num_splits, (T + p.chunk - 1) / p.chunk);
-    const int64_t slot0 = (int64_t)b * p.num_splits * p.R + row;  // split s at slot0 + s*R
-    const int64_t st = (int64_t)p.R;
+    const int64_t ml_st = (int64_t)p.R * 2;  // floats between splits of one row
+    const float* ml0 = p.ws_ml + (int64_t)b * p.num_splits * p.R * 2;
 
-    // rare path: recompute partials whose max is flagged as NaN
-    if (threadIdx.x == 0) nflag = 0;
+    // rare path: recompute (row, split) partials flagged with a NaN max
+    if (tid == 0) nflag = 0;
     __syncthreads();
-    for (int s = threadIdx.x; s < nact; s += blockDim.x)
-        if (__builtin_isnan(p.ws_ml[(slot0 + s * st) * 2])) nflag = 1;
+    for (int k = tid; k < 16 * nact; k += 256) {
+        const int row = qb * 16 + (k & 15), s = k >> 4;
+        if (row < p.R && __builtin_isnan(ml0[s * ml_st + row * 2])) nflag = 1;
+    }
     __syncthreads();
     if (nflag) {
-        for (int s = 0; s < nact; s++) {
-            const int64_t slot = slot0 + s * st;
-            const bool flagged = __builtin_isnan(p.ws_ml[slot * 2]);
+        for (int k = 0; k < 16 * nact; k++) {
+            const int row = qb * 16 + (k & 15), s = k >> 4;
+            const bool flagged = row < p.R && __builtin_isnan(ml0[s * ml_st + row * 2]);
             __syncthreads();
-            if (flagged)
-                mla_recompute_split<QDT, DT>(p, b, row, s, f_lds, red_lds, p.ws_ml + slot * 2,
-                                             p.ws_o + slot * kKR);
+            if (flagged) mla_recompute_split<QDT, DT>(p, b, row, s, x_lds, &red[0][0]);
             __threadfence_block();
             __syncthreads();
         }
     }
 
-    const float inv = lse_weights(p.ws_ml + slot0 * 2, st * 2, nact, f_lds, red_lds);
-    const float* os = p.ws_o + slot0 * kKR + d;
-    const int64_t ost = st * kKR;
-    f32x4_t O0 = {0.f, 0.f, 0.f, 0.f}, O1 = O0, O2 = O0, O3 = O0;
-    int s = 0;
-    for (; s + 4 <= nact; s += 4) {
-        O0 += f_lds[s] * *reinterpret_cast<const f32x4_t*>(os + s * ost);
-        O1 += f_lds[s + 1] * *reinterpret_cast<const f32x4_t*>(os + (s + 1) * ost);
-        O2 += f_lds[s + 2] * *reinterpret_cast<const f32x4_t*>(os + (s + 2) * ost);
-        O3 += f_lds[s + 3] * *reinterpret_cast<const f32x4_t*>(os + (s + 3) * ost);
-    }
-    for (; s < nact; s++) O0 += f_lds[s] * *reinterpret_cast<const f32x4_t*>(os + s * ost);
-    const f32x4_t O = ((O0 + O1) + (O2 + O3)) * inv;
-    const int64_t base = ((int64_t)b * p.R + row) * kKR + d;
+    // split weights: thread (row r = tid%16, split phase sl = tid/16)
+    {
+        const int r = tid & 15, sl = tid >> 4, row = qb * 16 + r;
+        const bool ok = row < p.R;
+        float mx = kNegInf;
+        for (int s = sl; s < nact; s += 16) mx = fmaxf(mx, ok ? ml0[s * ml_st + row * 2] : kNegInf);
+        red[sl][r] = mx;
+        __syncthreads();
+        float M = kNegInf;
 #pragma unroll
-    for (int c = 0; c < 4; c++) store_out<OUT_DT>(p.out, base + c, O[c]);
+        for (int j = 0; j < 16; j++) M = fmaxf(M, red[j][r]);
+        __syncthreads();
+        float sum = 0.f;
+        for (int s = sl; s < nact; s += 16) {
+            const float m = ok ? ml0[s * ml_st + row * 2] : kNegInf;
+            const float w = (m == kNegInf) ? 0.f : fast_exp2(m - M) * ml0[s * ml_st + row * 2 + 1];
+            wts[s][r] = w;
+            sum += w;
+        }
+        red[sl][r] = sum;
+        __syncthreads();
+        if (tid < 16) {
+            float L = 0.f;
+#pragma unroll
+            for (int j = 0; j < 16; j++) L += red[j][tid];
+            linv[tid] = L > 0.f ? 1.f / L : 0.f;
+        }
+        __syncthreads();
+    }
+
+    const int d0 = dg * 8 + dsub * 2;
+    const u32x2_t* src = reinterpret_cast<const u32x2_t*>(p.ws_o) + blob_frag(p, b, 0, qb, d0, lane);
+    const int64_t frag_st = (int64_t)p.nq * 32 * 64;  // fragments between splits
+    auto h4 = [](u32x2_t v) {
+        return f32x4_t{lo_f32<DT_F16>(v[0]), hi_f32<DT_F16>(v[0]), lo_f32<DT_F16>(v[1]), hi_f32<DT_F16>(v[1])};
+    };
+    f32x4_t A0 = {0.f, 0.f, 0.f, 0.f}, A1 = A0, B0 = A0, B1 = A0;
+    int s = 0;
+    for (; s + 2 <= nact; s += 2) {
+        const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(&wts[s][4 * g]);
+        const f32x4_t w1 = *reinterpret_cast<const f32x4_t*>(&wts[s + 1][4 * g]);
+        A0 += w0 * h4(src[s * frag_st]);
+        A1 += w0 * h4(src[s * frag_st + 64]);
+        B0 += w1 * h4(src[(s + 1) * frag_st]);
+        B1 += w1 * h4(src[(s + 1) * frag_st + 64]);
+    }
+    if (s < nact) {
+        const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(&wts[s][4 * g]);
+        A0 += w0 * h4(src[s * frag_st]);
+        A1 += w0 * h4(src[s * frag_st + 64]);
+    }
+    A0 += B0;
+    A1 += B1;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = qb * 16 + 4 * g + i;
+        if (row < p.R) {
+            const float inv = linv[4 * g + i];
+            const int64_t base = ((int64_t)b * p.R + row) * kKR + 16 * d0 + n;
+            store_out<OUT_DT>(p.out, base, A0[i] * inv);
+            store_out<OUT_DT>(p.out, base + 16, A1[i] * inv);
+        }
+    }
 }
 
 // ------------------------------------------------------------------ launch
@@ -489,15 +589,14 @@ int mla_rows_per_block(int variant) { return 64 * variant; }
 
 template <int MB, int QDT, int DT, int OUT_DT>
 static hipError_t launch_mla_t(const MlaParams& p, hipStream_t st, KernelTimer* t) {
-    const int groups = p.B * p.num_splits;         // (sequence, split) pairs
-    const int grid = 8 * p.nrb * ((groups + 7) / 8);  // see the XCD mapping in the kernel
+    const int grid = 8 * p.nrb * ((p.groups + 7) / 8);  // see the XCD mapping in the kernel
     timer_begin(t, "mla_decode", st);
     hipLaunchKernelGGL((mla_decode_kernel<MB, QDT, DT>), dim3(grid), dim3(256), 0, st, p);
     timer_end(t, "mla_decode", st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     timer_begin(t, "mla_decode_combine", st);
-    hipLaunchKernelGGL((mla_decode_combine_kernel<QDT, DT, OUT_DT>), dim3(p.R, p.B), dim3(128), 0, st, p);
+    hipLaunchKernelGGL((mla_decode_combine_kernel<QDT, DT, OUT_DT>), dim3(p.nq, 4, p.B), dim3(256), 0, st, p);
     timer_end(t, "mla_decode_combine", st);
     return hipGetLastError();
 }

@@ -110,3 +110,18 @@ def test_late_score_overshoot_uses_exact_fallback(device, ldt, big, splits):
     q, qb = O.round_to(q, ldt)
     c2 = dict(c, lat=lat, latb=latb, q=q, qb=qb)
     C.assert_close(run_gpu(c2, device, C.F32, splits), C.mla_ref(c2), f"overshoot fallback splits={splits}")
+
+
+def test_host_length_hint_matches_no_hint(device):
+    # the hint only plans the grid: equal results with and without it
+    lens = O.randint(70, 5, 100, 3000)
+    c = C.mla_case(70, 5, 1, 128, lens, max_T=3000, q_dtype=C.BF16, lat_dtype=C.BF16)
+    q = C.to_dev(c["qb"], C.BF16, device)
+    lat = C.to_dev(c["latb"], C.BF16, device)
+    sl = torch.from_numpy(c["seq_lens"]).to(device)
+    C.say("mla hint vs no hint")
+    a = mugen_amd.mla_attention(q, lat, sl, 3000, scale=C.MLA_SCALE).cpu().numpy()
+    bb = mugen_amd.mla_attention(q, lat, sl, 3000, scale=C.MLA_SCALE, seq_lens_host=c["seq_lens"]).cpu().numpy()
+    torch.cuda.synchronize()
+    C.assert_close(a, C.mla_ref(c, nthreads=8), "no hint")
+    C.assert_close(bb, C.mla_ref(c, nthreads=8), "hint")
