@@ -199,6 +199,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None, help="run only the named workload")
     ap.add_argument("--headline-only", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="first run 5 plain device copies of MIB MiB (reference kernel for HBM counter scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of it "
@@ -209,6 +211,15 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+
+    if args.calibrate_copy > 0:
+        n = args.calibrate_copy << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        del src, dst
 
     head = MlaDecode(dev, 8, 128, 1, seeded_lens(45, 8, 1024, 8192), 8192, torch.bfloat16, torch.bfloat16, 45,
                      "mla_decode_v3")
