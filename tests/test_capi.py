@@ -121,3 +121,39 @@ def test_python_front_end_refuses_cpu_tensors():
     k = torch.zeros(1, 8, 1, 64, dtype=torch.float16)
     with pytest.raises(ValueError, match="device tensors"):
         mugen_amd.attention_decode(q, k, k, torch.ones(1, dtype=torch.int32))
+
+
+ADAPTER_PROGRAM = r"""
+#include "mugen_attn.hpp"
+#include <cstdio>
+int main() {
+    mugen_attn_gqa_decode_args a{};                // null pointers: rejected on the host
+    auto r = mugen_attn::gqa_decode(a, nullptr, 0, nullptr);
+    if (r || r.has_value() || r.error().empty()) return 1;
+    auto ok = mugen_attn::check(MUGEN_ATTN_OK);
+    if (!ok) return 2;
+    std::printf("%s\n", r.error().c_str());
+    return 0;
+}
+"""
+
+
+def test_cpp_adapter_maps_status_to_expected(tmp_path):
+    """include/mugen_attn.hpp compiles as C++20 and C++23 and turns a
+    rejected call into a failed Status carrying the library's message."""
+    import shutil
+    import subprocess
+    cxx = shutil.which("g++")
+    if cxx is None:
+        pytest.skip("no host C++ compiler")
+    src = tmp_path / "adapter.cpp"
+    src.write_text(ADAPTER_PROGRAM)
+    libdir = os.path.join(ROOT, "mugen_amd")
+    for std in ("c++20", "c++23"):
+        exe = tmp_path / f"adapter_{std}"
+        subprocess.run([cxx, f"-std={std}", "-Wall", "-Werror", str(src), "-I", os.path.join(ROOT, "include"),
+                        "-L", libdir, "-lmugen_attn", f"-Wl,-rpath,{libdir}", "-Wl,-rpath,/opt/rocm/lib",
+                        "-o", str(exe)], check=True)
+        out = subprocess.run([str(exe)], capture_output=True, text=True)
+        assert out.returncode == 0, out
+        assert out.stdout.strip()
