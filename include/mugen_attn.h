@@ -19,7 +19,8 @@
  *
  * Conventions (all entry points):
  *   - plain C: pointers, sizes, enums; no C++ or framework types cross it;
- *   - every pointer to tensor data is a DEVICE pointer owned by the caller;
+ *   - every pointer to tensor data is a DEVICE pointer owned by the caller,
+ *     16-byte aligned (q, caches and outputs);
  *     the library never allocates device memory inside a compute call;
  *     scratch ("workspace") is caller-provided, sized by *_workspace_size;
  *   - `stream` is a hipStream_t passed as void* (NULL = default stream);

@@ -347,13 +347,15 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     if (a->head_dim != 64 && a->head_dim != 128)
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: head_dim %d (supported: 64, 128)", a->head_dim);
     if (!is16(a->dtype) || !is_out(a->out_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: dtype");
-    if (((uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->v) & 15)
-        return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: q/k/v must be 16-byte aligned");
+    if (((uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->v | (uintptr_t)a->out) & 15)
+        return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: q/k/v/out must be 16-byte aligned");
     if (a->n_tokens == 0) return MUGEN_ATTN_OK;
     if (a->kv_len == 0) return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: kv_len == 0 with n_tokens > 0");
     if (a->causal && a->start_pos + a->n_tokens > a->kv_len)
         return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: start_pos + n_tokens (%d) > kv_len (%d)",
                     a->start_pos + a->n_tokens, a->kv_len);
+    if ((int64_t)a->kv_len * a->n_kv_heads * a->head_dim * 2 > INT32_MAX)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: K/V cache larger than 2 GiB per tensor");
     GqaPrefillParams p{};
     p.q = static_cast<const uint16_t*>(a->q);
     p.k = static_cast<const uint16_t*>(a->k);

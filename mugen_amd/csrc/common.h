@@ -94,15 +94,16 @@ __device__ __forceinline__ void store_out(void* base, int64_t idx, float v) {
 template <int DT>
 __host__ __device__ constexpr int p_terms() { return DT == DT_BF16 ? 2 : 1; }
 
-// Pack 8 fp32 weights into NP A-operand fragments (hi, then lo residual).
+// Pack 8 fp32 weights into NP A/B-operand fragments (hi, then the lo
+// residual), both rounded to nearest even by the hardware pack.
 template <int DT, int NP>
 __device__ __forceinline__ void split_p(const float* x, u32x4_t* frag) {
     uint32_t hi[4], lo[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const uint16_t h0 = from_f32<DT>(x[2 * j]), h1 = from_f32<DT>(x[2 * j + 1]);
-        hi[j] = uint32_t(h0) | (uint32_t(h1) << 16);
-        if constexpr (NP > 1) lo[j] = pack2<DT>(x[2 * j] - to_f32<DT>(h0), x[2 * j + 1] - to_f32<DT>(h1));
+        hi[j] = pack2<DT>(x[2 * j], x[2 * j + 1]);
+        if constexpr (NP > 1)
+            lo[j] = pack2<DT>(x[2 * j] - lo_f32<DT>(hi[j]), x[2 * j + 1] - hi_f32<DT>(hi[j]));
     }
     frag[0] = u32x4_t{hi[0], hi[1], hi[2], hi[3]};
     if constexpr (NP > 1) frag[1] = u32x4_t{lo[0], lo[1], lo[2], lo[3]};

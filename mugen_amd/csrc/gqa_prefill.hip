@@ -5,17 +5,23 @@
 // attends to keys [0, start_position + i] (kernel_sources.h:2796), kv head
 // = h / (H/Hk), scale 1/sqrt(D), fp32 softmax accumulation.
 //
-// Design (MFMA-bound):
-//  * workgroup = (16-token query block, kv head); its 4 waves take the G
-//    query heads of that kv head (wave w: heads w, w+4, ...), so every K/V
-//    tile staged in LDS feeds all G heads of the group (GQA reuse);
-//  * query blocks are launched longest-first (causal rows near the end see
-//    the most keys) to shorten the tail;
-//  * per 64-key tile: S^T = K . Q^T on MFMA 16x16x32 with the token
-//    permutation that leaves each lane 8 consecutive keys of its query row,
-//    online softmax in registers, then O += P . V with P taken straight from
-//    registers as the A operand and V gathered from LDS as the B operand;
-//  * tiles entirely above the causal diagonal are never visited;
+// Design.  At prefill sizes of a small model (N = 512, 32 heads) the whole
+// problem is ~1 GFLOP: the kernel is bound by the length of each
+// workgroup's serial tile chain, not by MFMA throughput, so the layout aims
+// at a short chain with every load in flight early:
+//  * workgroup = (16-token query block, kv head), 8 waves: wave w takes
+//    query heads w%4 (+4) of the group and key half w/4 of every 64-key
+//    tile, so a tile costs each wave half the MFMA work and the two halves'
+//    (max, sum, O) are merged through LDS at the end;
+//  * K/V tiles reach LDS by global_load_lds DMA into a 4-deep ring, three
+//    tiles ahead of the compute; rows are XOR-swizzled in 16-byte chunks so
+//    the K operand reads (ds_read_b128) and the V operand transpose reads
+//    (ds_read_b64_tr_b16) are both free of bank conflicts;
+//  * S^T = K . Q^T with the token permutation that leaves each lane 8
+//    consecutive keys of its query row, so P feeds O += P . V as the A
+//    operand straight from registers;
+//  * query blocks are launched longest-first; tiles above the causal
+//    diagonal are never loaded;
 //  * with bf16 inputs P is split into hi + lo bf16 terms (two MFMAs on the
 //    same V operand): a single bf16 P carries 2^-9 relative error per
 //    weight, which short causal rows do not average away.
@@ -24,46 +30,117 @@
 
 namespace mugen_attn {
 
+namespace {
+
+constexpr int kKT = 64;    // keys per tile
+constexpr int kNBuf = 4;   // ring depth: three tiles in flight
+constexpr int kWaves = 8;
+
+// 16-byte chunk c of tile row r is stored at chunk c ^ pf_swz<D>(r).  LDS
+// serves 64 banks x 4 B per clock (16 lanes of ds_read_b128, 32 lanes of a
+// transpose read).  The K reads of a 16-lane group touch rows
+// 8a + b (+4), a, b in 0..3, at one logical chunk; the transpose reads of
+// lane groups g, g+1 touch rows 8g + r and 8g + 8 + r, r in 0..3, at chunks
+// 2d, 2d + 1.  D = 64 rows are 128 B (two rows per bank cycle), D = 128
+// rows 256 B.  Both swizzles make every such set hit distinct banks and
+// ignore row bits 2 and 5 (the +4 and key-half row offsets).
+template <int D>
+__host__ __device__ constexpr int pf_swz(int r) {
+    if constexpr (D == 64)
+        return (((r >> 1) & 1) * 2) ^ (((r >> 3) & 1) * 4) ^ ((r >> 4) & 1);
+    else
+        return ((r & 1) * 2) ^ (((r >> 1) & 1) * 4) ^ (((r >> 3) & 1) * 8) ^ ((r >> 4) & 1);
+}
+
+}  // namespace
+
 template <int D, int MB, int DT, int OUT_DT>
-__global__ __launch_bounds__(256) void gqa_prefill_kernel(GqaPrefillParams p) {
-    constexpr int KK = D / 32;     // k-steps of S over head_dim
-    constexpr int DB = D / 16;     // 16-wide output column blocks
-    constexpr int KT = 64;         // keys per tile
-    constexpr int LROW = D + 8;    // padded LDS row (halves)
-    constexpr int CPR = D / 8;     // 16-byte chunks per row
-    constexpr int CPT = KT * CPR / 256;  // chunks per thread per matrix
-    constexpr int NP = p_terms<DT>();    // 16-bit terms P is split into
-    __shared__ __attribute__((aligned(16))) uint16_t ks[KT * LROW];
-    __shared__ __attribute__((aligned(16))) uint16_t vs[KT * LROW];
+__global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
+    constexpr int KK = D / 32;                 // k-steps of S over head_dim
+    constexpr int DB = D / 16;                 // 16-wide output column blocks
+    constexpr int RB = D * 2;                  // bytes per tile row
+    constexpr int CR = D / 8;                  // 16-byte chunks per row
+    constexpr int MAT = kKT * RB;              // bytes of one K or V tile
+    constexpr int DPW = 2 * MAT / 1024 / kWaves;  // 1-KiB DMA ops per wave per tile (K and V)
+    constexpr int NP = p_terms<DT>();
+    static_assert(DPW >= 2 && DPW % 2 == 0, "tile split");
+    __shared__ __attribute__((aligned(16))) char ring[kNBuf][2 * MAT];
 
     const int qb = gridDim.x - 1 - blockIdx.x;  // longest rows first
     const int kvh = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int hs = w & 3, kh = w >> 2;
     const int n = lane & 15, g = lane >> 4;
     const int t0 = qb * 16;
     const int G = p.G;
+
+    // keys visible to the last token of the block; this lane's row limit
+    int kend = p.kv_len;
+    if (p.causal) kend = min(kend, p.start_pos + min(t0 + 16, p.N));
+    const int ntiles = (kend + kKT - 1) / kKT;
+    const int row_lim = p.causal ? min(p.start_pos + t0 + n + 1, p.kv_len) : p.kv_len;
+    // the first row's limit: tiles wholly below it need no mask
+    const int mask_from = p.causal ? min(p.start_pos + t0 + 1, p.kv_len) : p.kv_len;
+
+    // ---- DMA of tile rows: wave w moves K chunks [64(w + 8k), +64) and the
+    // same V chunks; slot s = row s / CR, physical chunk s % CR, whose data
+    // is logical chunk (s % CR) ^ pf_swz(row)
+    const uint32_t ring_base = lds_addr(&ring[0][0]);
+    const int rs_bytes = p.row_stride * 2;
+    int dma_row[DPW / 2];
+    uint32_t dma_col[DPW / 2];
+#pragma unroll
+    for (int k = 0; k < DPW / 2; k++) {
+        const int slot = 64 * (w + kWaves * k) + lane;
+        const int r = slot / CR, pc = slot % CR;
+        dma_row[k] = r;
+        dma_col[k] = (uint32_t)((pc ^ pf_swz<D>(r)) * 16);
+    }
+    const uint16_t* kb = p.k + (int64_t)kvh * D;
+    const uint16_t* vb = p.v + (int64_t)kvh * D;
+    auto issue = [&](int it) {
+        const int kt = it * kKT;
+        const uint32_t lds0 = ring_base + (it % kNBuf) * (2 * MAT) + w * 1024;
+#pragma unroll
+        for (int k = 0; k < DPW / 2; k++) {
+            const uint32_t off = (uint32_t)min(kt + dma_row[k], kend - 1) * rs_bytes + dma_col[k];
+            dma16s(lds0 + k * kWaves * 1024, kb, off);
+            dma16s(lds0 + MAT + k * kWaves * 1024, vb, off);
+        }
+    };
+    for (int it = 0; it < min(ntiles, kNBuf - 1); it++) issue(it);
 
     // Q^T fragments: lane holds q[token t0+n][head][32kk + 8g .. +8]
     u32x4_t qf[MB][KK];
     bool head_ok[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
-        const int hg = w + 4 * mb;
+        const int hg = hs + 4 * mb;
         head_ok[mb] = hg < G;
         const int tok = min(t0 + n, p.N - 1);
         const uint16_t* qp = p.q + ((int64_t)tok * p.H + kvh * G + (head_ok[mb] ? hg : 0)) * D + 8 * g;
 #pragma unroll
         for (int kk = 0; kk < KK; kk++) qf[mb][kk] = load16(qp + 32 * kk);
     }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no compiler waits inside the loop
 
-    // keys visible to the last token of the block
-    int kend = p.kv_len;
-    if (p.causal) kend = min(kend, p.start_pos + min(t0 + 16, p.N));
-    // this lane's S-row (token t0 + n) limit
-    const int row_lim = p.causal ? min(p.start_pos + t0 + n + 1, p.kv_len) : p.kv_len;
+    // K operand (A): row 32kh + 8(n/4) + n%4 (+4nb), logical chunk g + 4kk
+    const int ar = 32 * kh + 8 * (n >> 2) + (n & 3);
+    uint32_t a_off[KK];
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++) a_off[kk] = ar * RB + (((g + 4 * kk) ^ pf_swz<D>(ar)) * 16);
+    // V operand (B, transpose reads): row 32kh + 8g + n/4 (+4), logical
+    // bytes 32d + 8(n%4) = chunk 2d + (n%4)/2, half (n%2)
+    const int tr = 32 * kh + 8 * g + (n >> 2);
+    uint32_t t_off[DB];
+#pragma unroll
+    for (int d = 0; d < DB; d++) t_off[d] = MAT + tr * RB + (((2 * d + ((n & 3) >> 1)) ^ pf_swz<D>(tr)) * 16) + 8 * (n & 1);
 
+    // O^T accumulators: o[mb][d] lane (g, n) holds O[query t0+n][16d + 4g + i]
+    // (O^T = V^T . P^T, so each lane owns one query row and the softmax's
+    // per-row factors need no cross-lane moves)
     f32x4_t o[MB][DB];
-    float m_run[MB], l_part[MB];
+    float m_run[MB], l_part[MB];  // running max (log2 units) of row t0+n, partial sum
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
         m_run[mb] = kNegInf;
@@ -71,127 +148,148 @@ __global__ __launch_bounds__(256) void gqa_prefill_kernel(GqaPrefillParams p) {
 #pragma unroll
         for (int d = 0; d < DB; d++) o[mb][d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
+    // lazy max: weights may grow to 2^kHeadroom before the row is re-based
+    constexpr float kHeadroom = 8.f;
 
-    const uint16_t* kbase = p.k + (int64_t)kvh * D;
-    const uint16_t* vbase = p.v + (int64_t)kvh * D;
-    const int arow0 = 8 * (n >> 2) + (n & 3);
+    for (int it = 0; it < ntiles; it++) {
+        // tiles issued after `it`: min(ntiles - 1, it + kNBuf - 2) - it
+        const int after = min(ntiles - 1, it + kNBuf - 2) - it;
+        if (after >= 2) vm_wait<2 * DPW>();
+        else if (after == 1) vm_wait<DPW>();
+        else vm_wait<0>();
+        lds_barrier();  // tile `it` landed for all waves; tile it-1's buffer is free
+        if (it + kNBuf - 1 < ntiles) issue(it + kNBuf - 1);
+        const char* tile = &ring[it % kNBuf][0];
+        const int kt = it * kKT;
+        const bool need_mask = kt + kKT > mask_from;
 
-    for (int kt = 0; kt < kend; kt += KT) {
-        u32x4_t kr[CPT], vr[CPT];
+        // K operand fragments, shared by the MB heads
+        u32x4_t af[2][KK];
 #pragma unroll
-        for (int i = 0; i < CPT; i++) {
-            const int c = tid + 256 * i;
-            const int key = min(kt + c / CPR, kend - 1);
-            kr[i] = load16(kbase + (int64_t)key * p.row_stride + (c % CPR) * 8);
-            vr[i] = load16(vbase + (int64_t)key * p.row_stride + (c % CPR) * 8);
-        }
-        __syncthreads();  // previous tile consumed
+        for (int nb = 0; nb < 2; nb++)
 #pragma unroll
-        for (int i = 0; i < CPT; i++) {
-            const int c = tid + 256 * i;
-            *reinterpret_cast<u32x4_t*>(&ks[(c / CPR) * LROW + (c % CPR) * 8]) = kr[i];
-            *reinterpret_cast<u32x4_t*>(&vs[(c / CPR) * LROW + (c % CPR) * 8]) = vr[i];
+            for (int kk = 0; kk < KK; kk++)
+                af[nb][kk] = *reinterpret_cast<const u32x4_t*>(tile + a_off[kk] + nb * 4 * RB);
+        u32x4_t vf[DB];
+#pragma unroll
+        for (int d = 0; d < DB; d++) {
+            const u32x2_t lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(tile + t_off[d]));
+            const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(tile + t_off[d] + 4 * RB));
+            vf[d] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
         }
-        __syncthreads();
 
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) {
             if (!head_ok[mb]) continue;
-            // S^T for 2 groups of 32 keys, each 2 permuted 16-key blocks
-            f32x4_t sacc[2][2];
+            f32x4_t sacc[2];
 #pragma unroll
-            for (int grp = 0; grp < 2; grp++) {
+            for (int nb = 0; nb < 2; nb++) {
+                f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int nb = 0; nb < 2; nb++) {
-                    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-                    const uint16_t* arow = &ks[(32 * grp + arow0 + 4 * nb) * LROW + 8 * g];
+                for (int kk = 0; kk < KK; kk++) acc = mfma16x16x32<DT>(af[nb][kk], qf[mb][kk], acc);
+                sacc[nb] = acc;
+            }
+            // lane: query row t0+n, keys kt + 32kh + 8g + 4nb + i (raw scores)
+            float s[8];
 #pragma unroll
-                    for (int kk = 0; kk < KK; kk++)
-                        acc = mfma16x16x32<DT>(*reinterpret_cast<const u32x4_t*>(arow + 32 * kk),
-                                               qf[mb][kk], acc);
-                    sacc[grp][nb] = acc;
+            for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) s[4 * nb + i] = sacc[nb][i];
+            if (need_mask) {
+                const int key0 = kt + 32 * kh + 8 * g;
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    if (key0 + j >= row_lim) s[j] = kNegInf;
+            }
+            float smax = s[0];
+#pragma unroll
+            for (int j = 1; j < 8; j++) smax = fmaxf(smax, s[j]);
+            // re-base the row only when a weight would exceed 2^kHeadroom
+            if (__any(smax * p.scale_log2 > m_run[mb] + kHeadroom)) {
+                float mt = smax * p.scale_log2;
+                mt = fmaxf(mt, wave_xor(mt, 16));
+                mt = fmaxf(mt, wave_xor(mt, 32));
+                const float m_new = fmaxf(m_run[mb], mt);
+                if (m_new > m_run[mb]) {
+                    const float alpha = fast_exp2(m_run[mb] - m_new);  // 0 when m_run = -inf
+                    l_part[mb] *= alpha;
+#pragma unroll
+                    for (int d = 0; d < DB; d++) o[mb][d] *= alpha;
+                    m_run[mb] = m_new;
                 }
             }
-            // lane: row t0+n, keys kt + 32grp + 8g + 4nb + i
-            float x[2][8];
-            float mt = kNegInf;
-#pragma unroll
-            for (int grp = 0; grp < 2; grp++) {
-#pragma unroll
-                for (int nb = 0; nb < 2; nb++) {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int key = kt + 32 * grp + 8 * g + 4 * nb + i;
-                        const float v = key < row_lim ? sacc[grp][nb][i] * p.scale_log2 : kNegInf;
-                        x[grp][4 * nb + i] = v;
-                        mt = fmaxf(mt, v);
-                    }
-                }
-            }
-            mt = fmaxf(mt, wave_xor(mt, 16));
-            mt = fmaxf(mt, wave_xor(mt, 32));
-            const float m_new = fmaxf(m_run[mb], mt);
-            const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-            const float alpha = fast_exp2(m_run[mb] - m_use);
+            // every row with a visible key has a finite m_run here
+            const float nm = m_run[mb] == kNegInf ? 0.f : -m_run[mb];
+            float x[8];
             float ps = 0.f;
-            u32x4_t pfr[2][NP];
 #pragma unroll
-            for (int grp = 0; grp < 2; grp++) {
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    x[grp][j] = fast_exp2(x[grp][j] - m_use);
-                    ps += x[grp][j];
-                }
-                split_p<DT, NP>(x[grp], pfr[grp]);
+            for (int j = 0; j < 8; j++) {
+                x[j] = fast_exp2(fmaf(s[j], p.scale_log2, nm));
+                ps += x[j];
             }
-            l_part[mb] = l_part[mb] * alpha + ps;
-            m_run[mb] = m_new;
-            float arow_[4];
+            l_part[mb] += ps;
+            u32x4_t pfr[NP];
+            split_p<DT, NP>(x, pfr);
 #pragma unroll
-            for (int i = 0; i < 4; i++) arow_[i] = __shfl(alpha, 4 * g + i, 64);
+            for (int d = 0; d < DB; d++)
 #pragma unroll
-            for (int d = 0; d < DB; d++) {
-#pragma unroll
-                for (int i = 0; i < 4; i++) o[mb][d][i] *= arow_[i];
-            }
-            // O += P . V ; B operand V[kt + 32grp + 8g + j][16d + n]
-#pragma unroll
-            for (int grp = 0; grp < 2; grp++) {
-                const uint16_t* bcol = &vs[(32 * grp + 8 * g) * LROW + n];
-#pragma unroll
-                for (int d = 0; d < DB; d++) {
-                    uint32_t bw[4];
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const uint32_t e0 = bcol[(2 * j) * LROW + 16 * d];
-                        const uint32_t e1 = bcol[(2 * j + 1) * LROW + 16 * d];
-                        bw[j] = e0 | (e1 << 16);
-                    }
-                    const u32x4_t bf = u32x4_t{bw[0], bw[1], bw[2], bw[3]};
-#pragma unroll
-                    for (int pp = 0; pp < NP; pp++) o[mb][d] = mfma16x16x32<DT>(pfr[grp][pp], bf, o[mb][d]);
-                }
-            }
+                for (int pp = 0; pp < NP; pp++) o[mb][d] = mfma16x16x32<DT>(vf[d], pfr[pp], o[mb][d]);
         }
     }
 
-    // epilogue: normalise and store rows t0 + 4g + i
+    // ---- merge the two key halves: waves 4..7 hand (m, l, O) to waves 0..3
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
-        if (!head_ok[mb]) continue;
         float l = l_part[mb];
         l += wave_xor(l, 16);
         l += wave_xor(l, 32);
-        const int h = kvh * G + w + 4 * mb;
+        l_part[mb] = l;
+    }
+    __syncthreads();  // every wave is done with the ring
+    float* xf = reinterpret_cast<float*>(&ring[0][0]);
+    // per (head slot, mb): DB*64 f32x4 of O^T, then 16 m and 16 l
+    constexpr int XS = DB * 64 * 4 + 32;
+    if (kh == 1) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float lr = __shfl(l, 4 * g + i, 64);
-            const float inv = lr > 0.f ? 1.f / lr : 0.f;
-            const int tok = t0 + 4 * g + i;
-            if (tok < p.N) {
-                const int64_t base = ((int64_t)tok * p.H + h) * D + n;
+        for (int mb = 0; mb < MB; mb++) {
+            if (!head_ok[mb]) continue;
+            float* xb = xf + (hs * MB + mb) * XS;
 #pragma unroll
-                for (int d = 0; d < DB; d++) store_out<OUT_DT>(p.out, base + 16 * d, o[mb][d][i] * inv);
+            for (int d = 0; d < DB; d++) reinterpret_cast<f32x4_t*>(xb)[d * 64 + lane] = o[mb][d];
+            if (g == 0) {
+                xb[DB * 256 + n] = m_run[mb];
+                xb[DB * 256 + 16 + n] = l_part[mb];
+            }
+        }
+    }
+    __syncthreads();
+    if (kh == 1) return;
+    const int tok = t0 + n;
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+        if (!head_ok[mb]) continue;
+        const float* xb = xf + (hs * MB + mb) * XS;
+        const float m0 = m_run[mb], l0 = l_part[mb];
+        const float m1 = xb[DB * 256 + n], l1 = xb[DB * 256 + 16 + n];
+        const float M = fmaxf(m0, m1);
+        const float a0 = m0 == kNegInf ? 0.f : fast_exp2(m0 - M);
+        const float a1 = m1 == kNegInf ? 0.f : fast_exp2(m1 - M);
+        const float lt = a0 * l0 + a1 * l1;
+        const float inv = lt > 0.f ? 1.f / lt : 0.f;
+        const float c0 = a0 * inv, c1 = a1 * inv;
+        if (tok < p.N) {
+            const int h = kvh * G + hs + 4 * mb;
+            const int64_t base = ((int64_t)tok * p.H + h) * D + 4 * g;
+#pragma unroll
+            for (int d = 0; d < DB; d++) {
+                const f32x4_t o1 = reinterpret_cast<const f32x4_t*>(xb)[d * 64 + lane];
+                const f32x4_t r = o[mb][d] * c0 + o1 * c1;
+                if constexpr (OUT_DT == DT_F32) {
+                    *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.out) + base + 16 * d) = r;
+                } else {
+                    *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.out) + base + 16 * d) =
+                        u32x2_t{pack2<OUT_DT>(r[0], r[1]), pack2<OUT_DT>(r[2], r[3])};
+                }
             }
         }
     }
@@ -203,7 +301,7 @@ template <int D, int MB, int DT, int OUT_DT>
 static hipError_t launch_pf_t(const GqaPrefillParams& p, int Hk, hipStream_t st, KernelTimer* t) {
     dim3 grid((p.N + 15) / 16, Hk);
     timer_begin(t, "gqa_prefill", st);
-    hipLaunchKernelGGL((gqa_prefill_kernel<D, MB, DT, OUT_DT>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gqa_prefill_kernel<D, MB, DT, OUT_DT>), grid, dim3(64 * kWaves), 0, st, p);
     timer_end(t, "gqa_prefill", st);
     return hipGetLastError();
 }
