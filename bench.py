@@ -204,7 +204,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of it "
-                          "(see DESIGN.md for how the path would shard)", "n_gpus": args.gpus}))
+                          "(sharding the path over GPUs is a design note, not a measured mode)", "n_gpus": args.gpus}))
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)

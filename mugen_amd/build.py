@@ -33,7 +33,8 @@ def common_flags() -> list[str]:
     return [
         f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
         "-I", INCLUDE, "-I", CSRC,
-        # packed fp32 VALU ops off for all device code
+        # no packed fp32 VALU ops (v_pk_*_f32) in device code: some of their
+        # forms have produced silently wrong results on this hardware
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wno-unused-command-line-argument",
     ]
