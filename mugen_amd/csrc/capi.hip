@@ -209,7 +209,8 @@ static size_t gqa_ws(const mugen_attn_gqa_decode_args* a, int chunk, int* splits
 // q is 16-bit, else 64-row workgroups
 static int mla_variant(const mugen_attn_mla_decode_args* a) {
     const int R = a->q_len * a->n_heads;
-    return (R > 64 && a->q_dtype != DT_F32) ? 2 : 1;
+    if (R <= 64 || a->q_dtype == DT_F32) return 1;
+    return 3;
 }
 
 // Active (sequence, split) groups for a chunk: exact from the host length
@@ -227,20 +228,21 @@ static int64_t mla_groups(const mugen_attn_mla_decode_args* a, int chunk) {
 // the smallest chunk (multiple of 32) whose nrb * active groups fit ONE
 // dispatch round of 256 CUs -- maximum parallelism, no second round.
 static int mla_chunk(const mugen_attn_mla_decode_args* a, int variant) {
-    if (a->num_splits > 0) return explicit_chunk(a->max_seq_len, a->num_splits, 32, kMaxMlaSplits);
+    const int q = mla_tile_tokens(variant);  // chunks are whole tiles
+    if (a->num_splits > 0) return explicit_chunk(a->max_seq_len, a->num_splits, q, kMaxMlaSplits);
     const int R = a->q_len * a->n_heads;
     const int64_t nrb = ceil_div(R, mla_rows_per_block(variant));
     const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
-    const int cmax = ceil_div(maxT, 32) * 32;
-    const int cmin = ceil_div(ceil_div(maxT, kMaxMlaSplits), 32) * 32;
+    const int cmax = ceil_div(maxT, q) * q;
+    const int cmin = ceil_div(ceil_div(maxT, kMaxMlaSplits), q) * q;
     const int64_t wg_budget = 256;
     if (nrb * mla_groups(a, cmax) > wg_budget) return cmax;  // one split per sequence already fills a round
-    int lo = cmin < 32 ? 32 : cmin, hi = cmax;               // groups(c) is non-increasing in c
+    int lo = cmin < q ? q : cmin, hi = cmax;                 // groups(c) is non-increasing in c
     while (lo < hi) {
-        const int mid = ((lo + hi) / 2) / 32 * 32;
+        const int mid = ((lo + hi) / 2) / q * q;
         if (mid <= lo) break;
         if (nrb * mla_groups(a, mid) <= wg_budget) hi = mid;
-        else lo = mid + 32;
+        else lo = mid + q;
     }
     if (nrb * mla_groups(a, lo) > wg_budget) lo = hi;
     return lo;

@@ -68,8 +68,9 @@ struct MlaParams {
     float scale_log2;
 };
 
-// rows of queries handled by one MLA workgroup for a given variant (1 or 2)
+// query rows of one MLA workgroup, and tokens per LDS tile, of a variant (1..3)
 int mla_rows_per_block(int variant);
+int mla_tile_tokens(int variant);
 hipError_t launch_mla_decode(const MlaParams& p, int variant, int q_dt, int lat_dt, int out_dt,
                              hipStream_t st, KernelTimer* t);
 

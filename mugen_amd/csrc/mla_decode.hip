@@ -96,12 +96,22 @@ __device__ __forceinline__ void mfma_s(f32x4_t& acc, const u32x4_t& a, const u32
     }
 }
 
-template <int MB, int QDT, int DT>
+template <int MB, int TS, int QDT, int DT>
 __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     constexpr int KS = kCD / 32;  // 18 k-steps over the 576 dims
     constexpr int NQ = (QDT == DT_F32) ? 2 : 1;
     constexpr float TH = headroom_log2<DT>();
-    __shared__ __attribute__((aligned(1024))) uint16_t ring[kNBuf][kTileBytes / 2];
+    // TS = 1: the 4 waves split the rows of a 32-token tile (3-deep ring).
+    // TS = 2: 64-token tiles (2-deep ring); wave w takes rows of group w%2
+    // and the 32-token half w/2 of every tile, and the two halves of a row
+    // group are merged at the end -- half the rows per workgroup for the
+    // same MFMA work, so half the split partials and query loads.
+    constexpr int TILE_T = kTT * TS;                 // tokens per tile
+    constexpr int TILE_B = TILE_T * kRowBytes;       // bytes per tile
+    constexpr int NBUF = TS == 1 ? kNBuf : 2;        // ring depth
+    constexpr int DPW = kDmaPerWave * TS;            // 1-KiB DMA ops per wave per tile
+    constexpr int RG = 4 / TS;                       // row groups (waves per token slice)
+    __shared__ __attribute__((aligned(1024))) char ring[NBUF * TILE_B];
 
     // XCD-aware work mapping.  Workgroups are dealt to the 8 XCDs round-robin
     // by blockIdx.  A group = the nrb row blocks of one (sequence, split);
@@ -135,14 +145,66 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     const int T = p.seq_lens[b];
     const int t_begin = s * p.chunk;
     const int t_end = min(t_begin + p.chunk, T);
-    const int ntiles = (t_end - t_begin + kTT - 1) / kTT;
+    const int ntiles = (t_end - t_begin + TILE_T - 1) / TILE_T;
 
-    const int row0 = rb * (64 * MB) + w * (16 * MB);
+    const int rg = w % RG, th = w / RG;  // row group, token slice of each tile
+    const int row0 = rb * (RG * 16 * MB) + rg * (16 * MB);
     const uint16_t* lat = p.lat + (int64_t)b * p.seq_stride;
+
+    // ---- tile staging by LDS DMA: wave w fills LDS chunks [64K, 64K+64) of
+    // the tile for K = w + 4k; LDS chunk (r, pc) holds source chunk
+    // (r, pc ^ swz(r)).  Offsets are clamped to the split's last valid byte,
+    // so tokens past t_end read valid cache rows (masked later)
+    const uint32_t ring_base = lds_addr(&ring[0]);
+    uint32_t dma_off[DPW];
+#pragma unroll
+    for (int k = 0; k < DPW; k++) {
+        const int slot = 64 * (w + 4 * k) + lane;
+        const int r = slot / (kRowBytes / 16), pc = slot - r * (kRowBytes / 16);
+        dma_off[k] = (uint32_t)(r * kRowBytes + ((pc ^ swz(r)) * 16));
+    }
+    auto issue = [&](int tt, int buf) {
+        const uint16_t* tbase = lat + (int64_t)tt * kCD;  // wave-uniform
+        const uint32_t lds0 = ring_base + buf * TILE_B + w * 1024;
+        if (tt + TILE_T <= t_end) {  // whole tile valid: precomputed offsets
+#pragma unroll
+            for (int k = 0; k < DPW; k++) dma16s(lds0 + k * 4096, tbase, dma_off[k]);
+        } else {  // last tile of the split: clamp to its last valid chunk
+            const uint32_t lim = (uint32_t)(t_end - tt) * kRowBytes - 16;
+#pragma unroll
+            for (int k = 0; k < DPW; k++) dma16s(lds0 + k * 4096, tbase, min(dma_off[k], lim));
+        }
+    };
 
     // ---- Q^T fragments (B operand): lane holds Q[row0+16mb+n][32ks+8g .. +8]
     u32x4_t qf[MB][NQ][KS];
     int teff[MB];  // visible tokens of this lane's S-row
+    if constexpr (TS == 2) {
+        // the workgroup's 64 query rows (contiguous in q) arrive by LDS DMA
+        // in ring buffer 1, laid out and swizzled like latent rows, ahead of
+        // tile 0; both token slices of a row group then read them from LDS
+        static_assert(TS == 1 || QDT != DT_F32, "token-sliced variant takes 16-bit q");
+        const uint16_t* qrows = static_cast<const uint16_t*>(p.q) + ((int64_t)b * p.R + rb * 64) * kCD;
+        const uint32_t qlim = (uint32_t)min(64, p.R - rb * 64) * kRowBytes - 16;
+        const uint32_t q_lds = ring_base + TILE_B + w * 1024;
+#pragma unroll
+        for (int k = 0; k < DPW; k++) dma16s(q_lds + k * 4096, qrows, min(dma_off[k], qlim));
+        issue(t_begin, 0);
+        vm_wait<DPW>();  // the query rows landed (tile 0 may still fly)
+        lds_barrier();
+        const char* qt = &ring[TILE_B];
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) {
+            const int r = rg * 32 + 16 * mb + n, row = rb * 64 + r;
+            const bool ok = row < p.R;
+            teff[mb] = ok ? (T - p.q_len + row / p.H + 1) : T;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                const u32x4_t v = *reinterpret_cast<const u32x4_t*>(qt + r * kRowBytes + (((4 * ks + g) ^ swz(r)) * 16));
+                qf[mb][0][ks] = ok ? v : u32x4_t{0, 0, 0, 0};
+            }
+        }
+    } else {
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
         const int row = row0 + 16 * mb + n;
@@ -173,6 +235,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
             }
         }
     }
+    }
 
     // smallest visible length over the wave's rows: tiles below it need no mask
     int teff_min = teff[0];
@@ -185,31 +248,6 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     // understands: it then inserts no vmcnt(0) inside the tile loop (where
     // it would also drain the ring's in-flight DMA it cannot see)
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-
-    // ---- tile staging by LDS DMA: wave w fills LDS chunks [64K, 64K+64) of
-    // the tile for K = w + 4k; LDS chunk (r, pc) holds source chunk
-    // (r, pc ^ swz(r)).  Offsets are clamped to the split's last valid byte,
-    // so tokens past t_end read valid cache rows (masked later)
-    const uint32_t ring_base = lds_addr(&ring[0][0]);
-    uint32_t dma_off[kDmaPerWave];
-#pragma unroll
-    for (int k = 0; k < kDmaPerWave; k++) {
-        const int slot = 64 * (w + 4 * k) + lane;
-        const int r = slot / (kRowBytes / 16), pc = slot - r * (kRowBytes / 16);
-        dma_off[k] = (uint32_t)(r * kRowBytes + ((pc ^ swz(r)) * 16));
-    }
-    auto issue = [&](int tt, int buf) {
-        const uint16_t* tbase = lat + (int64_t)tt * kCD;  // wave-uniform
-        const uint32_t lds0 = ring_base + buf * kTileBytes + w * 1024;
-        if (tt + kTT <= t_end) {  // whole tile valid: precomputed offsets
-#pragma unroll
-            for (int k = 0; k < kDmaPerWave; k++) dma16s(lds0 + k * 4096, tbase, dma_off[k]);
-        } else {  // last tile of the split: clamp to its last valid chunk
-            const uint32_t lim = (uint32_t)(t_end - tt) * kRowBytes - 16;
-#pragma unroll
-            for (int k = 0; k < kDmaPerWave; k++) dma16s(lds0 + k * 4096, tbase, min(dma_off[k], lim));
-        }
-    };
 
     // S operand (A): row ar = 8*(n/4) + n%4 (+4nb), logical chunk 4ks + g.
     // swz(ar) does not depend on nb; (4ks + g) ^ h = 8*(ks/2) + ((4*(ks%2) + g) ^ h)
@@ -236,18 +274,22 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
         for (int d = 0; d < 32; d++) o[mb][d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
 
-    const char* ring_bytes = reinterpret_cast<const char*>(&ring[0][0]);
-    issue(t_begin, 0);
-    if (ntiles > 1) issue(t_begin + kTT, 1);
+    const char* ring_bytes = &ring[0];
+    if constexpr (TS == 1) {  // (TS = 2 issued tile 0 with the query rows)
+        issue(t_begin, 0);
+        if (ntiles > 1) issue(t_begin + TILE_T, 1);
+    }
     int buf = 0;
     for (int it = 0; it < ntiles; it++) {
-        if (it + 1 < ntiles) vm_wait<kDmaPerWave>();
+        if (NBUF > 2 && it + 1 < ntiles) vm_wait<DPW>();
         else vm_wait<0>();
         lds_barrier();  // tile `it` landed for every wave; the buffer of tile it-1 is free
-        if (it + 2 < ntiles) issue(t_begin + kTT * (it + 2), buf == 0 ? 2 : buf - 1);
-        const char* tile = ring_bytes + buf * kTileBytes;
-        buf = buf == kNBuf - 1 ? 0 : buf + 1;
-        const int tt = t_begin + kTT * it;
+        if (it + NBUF - 1 < ntiles)
+            issue(t_begin + TILE_T * (it + NBUF - 1), buf == 0 ? NBUF - 1 : buf - 1);
+        // this wave's 32-token slice of the tile (same swizzle: it ignores row bit 5)
+        const char* tile = ring_bytes + buf * TILE_B + th * kTT * kRowBytes;
+        buf = buf == NBUF - 1 ? 0 : buf + 1;
+        const int tt = t_begin + TILE_T * it + th * kTT;
 
         // ---- S^T = L . Q^T  (two 16-token blocks), VGPR accumulators.
         // Software-pipelined: operands of k-step ks+SPD are requested while
@@ -375,39 +417,124 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     // contiguous per store instruction); m and l stay fp32.  A row whose
     // weights or normalised values left the 16-bit ranges is flagged (NaN m)
     // for the exact fp32 recompute in the combine kernel.
+    float lrow[MB];  // S-layout row n: full sum of this wave's token slice
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
         float l = l_part[mb];
         l += wave_xor(l, 16);
         l += wave_xor(l, 32);
-        float inv[4];
+        lrow[mb] = l;
+    }
+    // Per S-layout row n: weight c0 of this wave's O and c1 of the other
+    // token slice's O in the normalised merge, the merged (max, sum), and
+    // the headroom flag (every weight of a slice is <= its l).
+    float c0[MB], c1[MB], mrow[MB], Lrow[MB];
+    bool ovf[MB];
+    constexpr int DH = 32 / TS;  // 16-column blocks this wave stores (from th * DH)
+    const f32x4_t* ox = nullptr;     // TS = 2: the partner's O for this wave's columns, in LDS
+    uint64_t* big_x = nullptr;        // TS = 2: the partner's overflow ballots
+    if constexpr (TS == 1) {
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) {
+            c0[mb] = lrow[mb] > 0.f ? 1.f / lrow[mb] : 0.f;
+            c1[mb] = 0.f;
+            mrow[mb] = m_ref[mb];
+            Lrow[mb] = lrow[mb];
+            ovf[mb] = !(lrow[mb] <= exp2f(TH));
+        }
+    } else {
+        // the two token slices of a row group swap the O columns the other
+        // one stores (16 blocks each), plus (m, l), through LDS
+        __syncthreads();  // every wave is done with the ring (its DMA has landed)
+        constexpr int XB = MB * 16 * 64;  // f32x4 per (row group, slice) area
+        f32x4_t* xo = reinterpret_cast<f32x4_t*>(&ring[0]);
+        float2* xml = reinterpret_cast<float2*>(&ring[0] + RG * 2 * XB * 16);
+        big_x = reinterpret_cast<uint64_t*>(&ring[0] + RG * 2 * XB * 16 + RG * 2 * MB * 16 * 8);
+        f32x4_t* mine = xo + (rg * 2 + th) * XB;
+        // O columns are picked with compile-time indices (a runtime index
+        // would move the accumulator array out of registers)
+        auto give = [&](auto half) {
+            constexpr int D0 = decltype(half)::value * DH;
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+                for (int d = 0; d < DH; d++) mine[(mb * DH + d) * 64 + lane] = o[mb][D0 + d];
+        };
+        if (th == 0) give(std::integral_constant<int, 1>{});
+        else give(std::integral_constant<int, 0>{});
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+            if (g == 0) xml[((rg * 2 + th) * MB + mb) * 16 + n] = make_float2(m_ref[mb], lrow[mb]);
+        __syncthreads();
+        ox = xo + (rg * 2 + 1 - th) * XB;
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) {
+            const float2 v1 = xml[((rg * 2 + 1 - th) * MB + mb) * 16 + n];
+            const float m0 = m_ref[mb], l0 = lrow[mb], m1 = v1.x, l1 = v1.y;
+            const float M = fmaxf(m0, m1);
+            const float a0 = m0 == kNegInf ? 0.f : fast_exp2(m0 - M);
+            const float a1 = m1 == kNegInf ? 0.f : fast_exp2(m1 - M);
+            const float L = a0 * l0 + a1 * l1;
+            const float inv = L > 0.f ? 1.f / L : 0.f;
+            c0[mb] = a0 * inv;
+            c1[mb] = a1 * inv;
+            mrow[mb] = M;
+            Lrow[mb] = L;
+            ovf[mb] = !(l0 <= exp2f(TH)) || !(l1 <= exp2f(TH));
+        }
+    }
+    uint64_t big_mask[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+        float k0[4], k1[4];  // the factors of O rows 4g+i
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float lr = __shfl(l, 4 * g + i, 64);
-            inv[i] = lr > 0.f ? 1.f / lr : 0.f;
+            k0[i] = __shfl(c0[mb], 4 * g + i, 64);
+            if constexpr (TS == 2) k1[i] = __shfl(c1[mb], 4 * g + i, 64);
         }
         const int rblk = row0 + 16 * mb;  // first row of this 16-row block
-        bool big = false;
-        if (rblk < p.R) {
-            u32x2_t* dst = reinterpret_cast<u32x2_t*>(p.ws_o) + blob_frag(p, b, s, rblk >> 4, 0, lane);
+        float vmax = 0.f;                 // largest |o/l| this lane stores
+        auto put = [&](auto half) {
+            constexpr int D0 = decltype(half)::value * DH;
+            u32x2_t* dst = reinterpret_cast<u32x2_t*>(p.ws_o) + blob_frag(p, b, s, rblk >> 4, D0, lane);
 #pragma unroll
-            for (int d = 0; d < 32; d++) {
-                const f32x4_t v = o[mb][d] * f32x4_t{inv[0], inv[1], inv[2], inv[3]};
-                big |= fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))) > 65000.f;
+            for (int d = 0; d < DH; d++) {
+                f32x4_t v = o[mb][D0 + d] * f32x4_t{k0[0], k0[1], k0[2], k0[3]};
+                if constexpr (TS == 2) v += ox[(mb * DH + d) * 64 + lane] * f32x4_t{k1[0], k1[1], k1[2], k1[3]};
+                vmax = fmaxf(vmax, fmaxf(fabsf(v[0]), fabsf(v[1])));
+                vmax = fmaxf(vmax, fmaxf(fabsf(v[2]), fabsf(v[3])));
                 dst[d * 64] = u32x2_t{pack2<DT_F16>(v[0], v[1]), pack2<DT_F16>(v[2], v[3])};
             }
+        };
+        if (rblk < p.R) {
+            if (TS == 1 || th == 0) put(std::integral_constant<int, 0>{});
+            else put(std::integral_constant<int, 1>{});
         }
-        // rows 4g+i of this lane overflowed -> tell their S-layout lanes (row n)
-        const uint64_t big_mask = __ballot(big);
-        const bool row_big = (big_mask >> (n >> 2) * 16) & 0xffffull;  // any lane of quad n/4
-        const int srow = rblk + n;  // S-layout row of this lane
+        // fp16 partials: a normalised value past 65000 cannot be stored
+        // (only bf16 latent rows can be that large); flagged like an overshoot
+        big_mask[mb] = __ballot(!(vmax <= 65000.f));
+    }
+    if constexpr (TS == 2) {  // slice 0 writes the rows' (m, l): it needs the partner's overflow ballots
+        if (th == 1) {
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++)
+                if (lane == 0) big_x[rg * MB + mb] = big_mask[mb];
+        }
+        __syncthreads();
+        if (th == 1) return;
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) big_mask[mb] |= big_x[rg * MB + mb];
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+        // rows 4g+i of a lane overflowed -> tell their S-layout lanes (row n)
+        const bool row_big = (big_mask[mb] >> (n >> 2) * 16) & 0xffffull;  // any lane of quad n/4
+        const int srow = row0 + 16 * mb + n;  // S-layout row of this lane
         if (g == 0 && srow < p.R) {
-            // every weight is <= l: a sum past the headroom means some weight
-            // may have overflowed its 16-bit P
-            const bool ovf = !(l <= exp2f(TH)) || row_big;
+            // a weight past the headroom may have overflowed its 16-bit P
             const int64_t slot = ((int64_t)b * p.num_splits + s) * p.R + srow;
-            p.ws_ml[slot * 2 + 0] = ovf ? __builtin_nanf("") : m_ref[mb];
-            p.ws_ml[slot * 2 + 1] = l;
+            p.ws_ml[slot * 2 + 0] = (ovf[mb] || row_big) ? __builtin_nanf("") : mrow[mb];
+            p.ws_ml[slot * 2 + 1] = Lrow[mb];
         }
     }
 }
@@ -585,13 +712,16 @@ __global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
 
 // ------------------------------------------------------------------ launch
 
-int mla_rows_per_block(int variant) { return 64 * variant; }
+// variant 1: MB = 1, TS = 1 (64 rows); 2: MB = 2, TS = 1 (128 rows);
+// 3: MB = 2, TS = 2 (64 rows, 64-token tiles)
+int mla_rows_per_block(int variant) { return variant == 2 ? 128 : 64; }
+int mla_tile_tokens(int variant) { return variant == 3 ? 2 * kTT : kTT; }
 
-template <int MB, int QDT, int DT, int OUT_DT>
+template <int MB, int TS, int QDT, int DT, int OUT_DT>
 static hipError_t launch_mla_t(const MlaParams& p, hipStream_t st, KernelTimer* t) {
     const int grid = 8 * p.nrb * ((p.groups + 7) / 8);  // see the XCD mapping in the kernel
     timer_begin(t, "mla_decode", st);
-    hipLaunchKernelGGL((mla_decode_kernel<MB, QDT, DT>), dim3(grid), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((mla_decode_kernel<MB, TS, QDT, DT>), dim3(grid), dim3(256), 0, st, p);
     timer_end(t, "mla_decode", st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -601,24 +731,27 @@ static hipError_t launch_mla_t(const MlaParams& p, hipStream_t st, KernelTimer* 
     return hipGetLastError();
 }
 
-template <int MB, int QDT, int DT>
+template <int MB, int TS, int QDT, int DT>
 static hipError_t launch_mla_o(const MlaParams& p, int out_dt, hipStream_t st, KernelTimer* t) {
-    if (out_dt == DT_F32) return launch_mla_t<MB, QDT, DT, DT_F32>(p, st, t);
-    if (out_dt == DT_F16) return launch_mla_t<MB, QDT, DT, DT_F16>(p, st, t);
-    return launch_mla_t<MB, QDT, DT, DT_BF16>(p, st, t);
+    if (out_dt == DT_F32) return launch_mla_t<MB, TS, QDT, DT, DT_F32>(p, st, t);
+    if (out_dt == DT_F16) return launch_mla_t<MB, TS, QDT, DT, DT_F16>(p, st, t);
+    return launch_mla_t<MB, TS, QDT, DT, DT_BF16>(p, st, t);
+}
+
+template <int DT>
+static hipError_t launch_mla_v(const MlaParams& p, int variant, int q_dt, int out_dt, hipStream_t st,
+                               KernelTimer* t) {
+    // variants 2 and 3 (32 rows per wave) need 16-bit q (register budget)
+    if (q_dt == DT_F32) return launch_mla_o<1, 1, DT_F32, DT>(p, out_dt, st, t);
+    if (variant == 2) return launch_mla_o<2, 1, DT, DT>(p, out_dt, st, t);
+    if (variant == 3) return launch_mla_o<2, 2, DT, DT>(p, out_dt, st, t);
+    return launch_mla_o<1, 1, DT, DT>(p, out_dt, st, t);
 }
 
 hipError_t launch_mla_decode(const MlaParams& p, int variant, int q_dt, int lat_dt, int out_dt,
                              hipStream_t st, KernelTimer* t) {
-    // variant 2 (128 rows per workgroup) needs 16-bit q (register budget)
-    if (lat_dt == DT_F16) {
-        if (q_dt == DT_F32) return launch_mla_o<1, DT_F32, DT_F16>(p, out_dt, st, t);
-        if (variant == 2) return launch_mla_o<2, DT_F16, DT_F16>(p, out_dt, st, t);
-        return launch_mla_o<1, DT_F16, DT_F16>(p, out_dt, st, t);
-    }
-    if (q_dt == DT_F32) return launch_mla_o<1, DT_F32, DT_BF16>(p, out_dt, st, t);
-    if (variant == 2) return launch_mla_o<2, DT_BF16, DT_BF16>(p, out_dt, st, t);
-    return launch_mla_o<1, DT_BF16, DT_BF16>(p, out_dt, st, t);
+    if (lat_dt == DT_F16) return launch_mla_v<DT_F16>(p, variant, q_dt, out_dt, st, t);
+    return launch_mla_v<DT_BF16>(p, variant, q_dt, out_dt, st, t);
 }
 
 }  // namespace mugen_attn
