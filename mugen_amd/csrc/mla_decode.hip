@@ -140,7 +140,8 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     if (b < 0) return;  // grid padding past the last active split
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int n = lane & 15, g = lane >> 4;
     const int T = p.seq_lens[b];
     const int t_begin = s * p.chunk;
@@ -327,8 +328,12 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
         }
         // first P.L operands requested now, to land during the softmax
         constexpr int VPD = 6;
+        // TS = 2: slice 1 accumulates its O with the 16-column blocks rotated
+        // by 16 (register d holds column block (d + 16) % 32), so that the
+        // epilogue of both slices keeps registers 0..15 and hands over 16..31
+        const int rot = (TS == 2 && th == 1) ? 512 : 0;
         auto tr_load = [&](int d) {
-            const char* tp = tile + t_off[d & 3] + 128 * (d >> 2);
+            const char* tp = tile + t_off[d & 3] + 128 * (d >> 2) + (d < 16 ? rot : -rot);
             const u32x2_t lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(tp));
             const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(tp + 4 * kRowBytes));
             return u32x4_t{lo[0], lo[1], hi[0], hi[1]};
@@ -430,7 +435,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     // the headroom flag (every weight of a slice is <= its l).
     float c0[MB], c1[MB], mrow[MB], Lrow[MB];
     bool ovf[MB];
-    constexpr int DH = 32 / TS;  // 16-column blocks this wave stores (from th * DH)
+    constexpr int DH = 32 / TS;  // 16-column blocks this wave stores: registers 0..DH-1
     const f32x4_t* ox = nullptr;     // TS = 2: the partner's O for this wave's columns, in LDS
     uint64_t* big_x = nullptr;        // TS = 2: the partner's overflow ballots
     if constexpr (TS == 1) {
@@ -451,20 +456,14 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
         float2* xml = reinterpret_cast<float2*>(&ring[0] + RG * 2 * XB * 16);
         big_x = reinterpret_cast<uint64_t*>(&ring[0] + RG * 2 * XB * 16 + RG * 2 * MB * 16 * 8);
         f32x4_t* mine = xo + (rg * 2 + th) * XB;
-        // O columns are picked with compile-time indices (a runtime index
-        // would move the accumulator array out of registers)
-        auto give = [&](auto half) {
-            constexpr int D0 = decltype(half)::value * DH;
+        // registers 16..31 hold the partner's column blocks (see the rotation
+        // in the P.L loop); they go over, registers 0..15 stay
 #pragma unroll
-            for (int mb = 0; mb < MB; mb++)
+        for (int mb = 0; mb < MB; mb++) {
 #pragma unroll
-                for (int d = 0; d < DH; d++) mine[(mb * DH + d) * 64 + lane] = o[mb][D0 + d];
-        };
-        if (th == 0) give(std::integral_constant<int, 1>{});
-        else give(std::integral_constant<int, 0>{});
-#pragma unroll
-        for (int mb = 0; mb < MB; mb++)
+            for (int d = 0; d < DH; d++) mine[(mb * DH + d) * 64 + lane] = o[mb][DH + d];
             if (g == 0) xml[((rg * 2 + th) * MB + mb) * 16 + n] = make_float2(m_ref[mb], lrow[mb]);
+        }
         __syncthreads();
         ox = xo + (rg * 2 + 1 - th) * XB;
 #pragma unroll
@@ -494,21 +493,17 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
         }
         const int rblk = row0 + 16 * mb;  // first row of this 16-row block
         float vmax = 0.f;                 // largest |o/l| this lane stores
-        auto put = [&](auto half) {
-            constexpr int D0 = decltype(half)::value * DH;
-            u32x2_t* dst = reinterpret_cast<u32x2_t*>(p.ws_o) + blob_frag(p, b, s, rblk >> 4, D0, lane);
+        if (rblk < p.R) {
+            // registers 0..DH-1 = column blocks th*DH .. th*DH + DH-1
+            u32x2_t* dst = reinterpret_cast<u32x2_t*>(p.ws_o) + blob_frag(p, b, s, rblk >> 4, th * DH, lane);
 #pragma unroll
             for (int d = 0; d < DH; d++) {
-                f32x4_t v = o[mb][D0 + d] * f32x4_t{k0[0], k0[1], k0[2], k0[3]};
+                f32x4_t v = o[mb][d] * f32x4_t{k0[0], k0[1], k0[2], k0[3]};
                 if constexpr (TS == 2) v += ox[(mb * DH + d) * 64 + lane] * f32x4_t{k1[0], k1[1], k1[2], k1[3]};
                 vmax = fmaxf(vmax, fmaxf(fabsf(v[0]), fabsf(v[1])));
                 vmax = fmaxf(vmax, fmaxf(fabsf(v[2]), fabsf(v[3])));
                 dst[d * 64] = u32x2_t{pack2<DT_F16>(v[0], v[1]), pack2<DT_F16>(v[2], v[3])};
             }
-        };
-        if (rblk < p.R) {
-            if (TS == 1 || th == 0) put(std::integral_constant<int, 0>{});
-            else put(std::integral_constant<int, 1>{});
         }
         // fp16 partials: a normalised value past 65000 cannot be stored
         // (only bf16 latent rows can be that large); flagged like an overshoot
