@@ -36,6 +36,7 @@ PEAK_HBM_GBS = 8000.0     # MI355X HBM3E
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 METRIC = json.load(open(os.path.join(ROOT, "BASELINE.json")))["metric"]
 MLA_SCALE = 1.0 / math.sqrt(192.0)
+GRAPH_STEPS = 20  # steps per captured HIP graph in the timed region
 
 
 def seeded_lens(seed, n, lo, hi):
@@ -149,20 +150,43 @@ class Prefill(Case):
         mugen_amd.flash_prefill_attention(self.q, self.k, self.v, 0, out=self.out)
 
 
+def capture(case, n):
+    """HIP graph of n consecutive steps (captured on a side stream, as torch requires)."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(n):
+            case.step()
+    return g
+
+
 def time_case(case, steps, warmup, dev):
+    """Warm-up, then EXACTLY `steps` steps timed with events between two
+    synchronisations.  The steps run as replays of captured HIP graphs (up
+    to GRAPH_STEPS steps each): the GPU executes the same kernels on the same
+    resident inputs as an eager call, without the per-call Python/ctypes
+    launch cost (~13 us), which would otherwise be what the small cases
+    measure."""
     for _ in range(warmup):
         case.step()
+    torch.cuda.synchronize(dev)
+    per = min(GRAPH_STEPS, steps)
+    full, rest = divmod(steps, per)
+    graphs = [(capture(case, per), full)] + ([(capture(case, rest), 1)] if rest else [])
+    for g, _ in graphs:  # one untimed replay each (graph upload)
+        g.replay()
     torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(steps):
-        case.step()
+    for g, reps in graphs:
+        for _ in range(reps):
+            g.replay()
     e1.record()
     torch.cuda.synchronize(dev)
     wall_ms = (time.perf_counter() - t0) * 1e3
     ms = e0.elapsed_time(e1) / steps
-    # per-kernel durations (HIP events around each launch, on the launch stream)
+    # per-kernel durations (HIP events around each launch, on the launch
+    # stream; eager calls, so these include the launch gaps)
     _capi.timing_reset()
     _capi.timing_enable(True)
     for _ in range(steps):
@@ -253,7 +277,8 @@ def main():
             "data": "synthetic (seeded torch.randn: q ~N(0,1), latent ~N(0,0.5); ctx lens seeded U[1024,8192])",
             "config": {"workload": "mla_absorbed_decode_deepseek_v3", "batch": 8, "n_heads": 128, "q_len": 1,
                        "latent_dim": 576, "kv_rank": 512, "ctx_lens": [int(x) for x in head.lens],
-                       "max_ctx": 8192, "split_k": "auto", "out_dtype": "f32"}}
+                       "max_ctx": 8192, "split_k": "auto", "out_dtype": "f32",
+                       "timing": f"HIP-graph replays of {GRAPH_STEPS}-step captures, events on the launch stream"}}
     if h:
         line["value"] = h["rate"]
         line["ms_per_step"] = round(h["us_per_step"] / 1e3, 6)

@@ -164,10 +164,13 @@ static int explicit_chunk(int max_seq_len, int num_splits, int quantum, int max_
 
 // GQA decode: tokens per split (multiple of 64 = one 16-token block per wave);
 // ~2 resident 256-thread workgroups per CU over 256 CUs
+// GQA decode: a workgroup's 4 waves take 32-token blocks, so chunks are
+// multiples of 128 tokens; about 512 workgroups (two per CU) keep every CU
+// streaming while the split count -- the combine's work -- stays low.
 static int gqa_chunk(const mugen_attn_gqa_decode_args* a) {
-    if (a->num_splits > 0) return explicit_chunk(a->max_seq_len, a->num_splits, 64);
+    if (a->num_splits > 0) return explicit_chunk(a->max_seq_len, a->num_splits, 128);
     const int64_t work = planned_tokens(a->seq_lens_host, a->batch, a->max_seq_len) * a->n_kv_heads;
-    return plan_chunk(work, 512, 64, a->max_seq_len);
+    return plan_chunk(work, 512, 128, a->max_seq_len);
 }
 
 static int gqa_validate(const mugen_attn_gqa_decode_args* a) {

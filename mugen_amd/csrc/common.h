@@ -129,6 +129,27 @@ __device__ __forceinline__ float wave_xor(float v, int mask) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Reductions with the lane 16 / 32 apart, in every lane, on the VALU
+// (gfx950 v_permlane16_swap / v_permlane32_swap; no LDS round trip like
+// ds_bpermute).  With both operands = v the swap returns, per lane, v and
+// its partner in some order, so their sum / max is the pair's.
+__device__ __forceinline__ float sum_x32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_x32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_x16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_x16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // LDS transpose read (gfx950 ds_read_b64_tr_b16).  Within each 16-lane
 // group, lane i receives element (i % 4) of the 8-byte chunks addressed by
 // lanes 4r + i/4, r = 0..3: with lane (4r + c) pointing at row r, columns

@@ -6,17 +6,24 @@
 // fp32 accumulation.
 //
 // Design (HBM-bound: ~7 flop per K/V byte at the 7B shape):
-//  * one workgroup = (context split, kv head, sequence); all G = H/Hk query
-//    heads of the group are served from ONE read of the group's K/V rows
-//    (the Metal kernel re-reads them once per query head);
-//  * 4 waves per workgroup; wave w takes 16-token blocks w, w+4, ... of
-//    the split so the workgroup streams one contiguous token range;
-//  * S^T[16 tok x 16 heads] = K . Q^T on MFMA 16x16x32 (K rows are the A
-//    operand straight from global memory, Q^T stays in registers; heads
-//    beyond G are zero columns);
-//  * online softmax in registers (exp2 domain), probabilities to LDS;
-//  * P.V on VALU: V is read fully coalesced (LPT lanes x 8 B per token row)
-//    and each lane accumulates all G heads for its 4 dims;
+//  * one workgroup = (context split, kv head, sequence); all G = H/Hk
+//    (<= 16) query heads of the group are served from ONE read of the
+//    group's K/V rows (the Metal kernel re-reads them once per query head);
+//  * 4 waves; wave w takes 32-token blocks w, w+4, ... of the split and
+//    loads the next block's K and V into registers while computing the
+//    current one;
+//  * S^T[32 tok x 16 heads] = K . Q^T on MFMA 16x16x32: K rows are the A
+//    operand straight from global memory, read in the token permutation
+//    that leaves each lane 8 consecutive tokens of its head (A row m of
+//    block nb is token 8*(m/4) + 4*nb + m%4); Q^T stays in registers and
+//    heads >= G are zero columns whose weights are forced to 0;
+//  * O^T[D x 16 heads] += V^T . P^T on MFMA as well: P is the B operand
+//    straight from registers (fp16, or bf16 hi + lo for 16 significant
+//    bits), V^T the A operand, staged through a per-wave LDS buffer
+//    (XOR-swizzled rows) and read with ds_read_b64_tr_b16; each lane owns
+//    one head, so softmax factors never cross lanes;
+//  * online softmax in the exp2 domain with a lazy max (a head is re-based
+//    only when a weight would exceed 2^8);
 //  * the 4 waves merge (m, l, o) through LDS; with one split the result is
 //    normalised and stored, otherwise (m, l, o) partials go to the
 //    workspace and gqa_decode_combine merges them with fp32 log-sum-exp.
@@ -25,18 +32,35 @@
 
 namespace mugen_attn {
 
-template <int D, int GMAX, int DT, int OUT_DT>
-__global__ __launch_bounds__(256) void gqa_decode_kernel(GqaDecodeParams p) {
-    constexpr int KK = D / 32;     // MFMA k-steps per row
-    constexpr int LPT = D / 4;     // lanes per token row in the V layout
-    constexpr int TPI = 64 / LPT;  // token rows per V load instruction
-    constexpr int VI = 16 / TPI;   // V load instructions per 16-token block
+namespace {
 
-    __shared__ float p_lds[4][16][16];  // [wave][token][head]
-    __shared__ float a_lds[4][16];      // per-head rescale of the step
-    __shared__ float m_lds[4][16];
-    __shared__ float l_lds[4][16];
-    __shared__ float o_lds[4][GMAX][D];
+// 16-byte chunk c of staged V row r is stored at chunk c ^ vswz<D>(r): the
+// transpose reads of lane groups g, g+1 (rows 8g + r', r' < 4, chunks 2d,
+// 2d + 1) then hit distinct banks (rows of 128 B for D = 64, 256 B for 128)
+template <int D>
+__device__ constexpr int vswz(int r) {
+    if constexpr (D == 64)
+        return (((r >> 1) & 1) * 2) ^ (((r >> 3) & 1) * 4) ^ ((r >> 4) & 1);
+    else
+        return ((r & 1) * 2) ^ (((r >> 1) & 1) * 4) ^ (((r >> 3) & 1) * 8) ^ ((r >> 4) & 1);
+}
+
+}  // namespace
+
+template <int D, int DT, int OUT_DT>
+__global__ __launch_bounds__(256) void gqa_decode_kernel(GqaDecodeParams p) {
+    constexpr int KK = D / 32;           // MFMA k-steps of S
+    constexpr int DB = D / 16;           // 16-dim blocks of O^T
+    constexpr int RB = 2 * D;            // bytes per staged V row
+    constexpr int VL = 32 * RB / 1024;   // 16-byte V loads per lane per 32-token block
+    constexpr int RPL = 1024 / RB;       // V rows per load instruction
+    constexpr int NP = p_terms<DT>();
+    constexpr float kHeadroom = 8.f;
+    // per-wave V staging (32 rows), reused after the loop for the wave merge
+    constexpr int STAGE = 4 * 32 * RB;
+    constexpr int OROW = D + 4;  // merge rows padded: lanes n of one write land on distinct banks
+    constexpr int MERGE = 4 * 16 * OROW * 4 + 2 * 4 * 16 * 4;
+    __shared__ __attribute__((aligned(16))) char lds[STAGE > MERGE ? STAGE : MERGE];
 
     const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -62,131 +86,146 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(GqaDecodeParams p) {
         for (int kk = 0; kk < KK; kk++) qf[kk] = u32x4_t{0, 0, 0, 0};
     }
 
+    // block loads: K rows in the permuted order (A operand), V rows coalesced
+    const int kr0 = 8 * (n >> 2) + (n & 3);  // + 4nb
+    auto load_block = [&](int t0, u32x4_t (&kq)[2][KK], u32x4_t (&vq)[VL]) {
+#pragma unroll
+        for (int nb = 0; nb < 2; nb++) {
+            const int tk = min(t0 + kr0 + 4 * nb, t_end - 1);
+            const uint16_t* kp = kbase + (int64_t)tk * p.row_stride + 8 * g;
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++) kq[nb][kk] = load16(kp + 32 * kk);
+        }
+#pragma unroll
+        for (int j = 0; j < VL; j++) {
+            const int tv = min(t0 + j * RPL + lane / (RB / 16), t_end - 1);
+            vq[j] = load16(vbase + (int64_t)tv * p.row_stride + 8 * (lane % (RB / 16)));
+        }
+    };
+    // V staging: load j of lane l is row j*RPL + l/(RB/16), chunk l%(RB/16)
+    char* stage = &lds[w * 32 * RB];
+    uint32_t st_off[VL];
+#pragma unroll
+    for (int j = 0; j < VL; j++) {
+        const int r = j * RPL + lane / (RB / 16), c = lane % (RB / 16);
+        st_off[j] = r * RB + ((c ^ vswz<D>(r)) * 16);
+    }
+    // transpose reads: lane (g, n) reads row 8g + n/4 (+4), logical bytes
+    // 32d + 8(n%4) = chunk 2d + (n%4)/2, half n%2
+    const int tr = 8 * g + (n >> 2);
+    uint32_t t_off[DB];
+#pragma unroll
+    for (int d = 0; d < DB; d++)
+        t_off[d] = tr * RB + (((2 * d + ((n & 3) >> 1)) ^ vswz<D>(tr)) * 16) + 8 * (n & 1);
+
+    f32x4_t o[DB];  // lane (g, n): O[head n][16d + 4g + i]
+#pragma unroll
+    for (int d = 0; d < DB; d++) o[d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     float m_run = kNegInf;  // running max (log2 domain) of head n
-    float l_part = 0.f;     // this lane's share of the running sum
-    float o[GMAX][4];
-#pragma unroll
-    for (int h = 0; h < GMAX; h++) o[h][0] = o[h][1] = o[h][2] = o[h][3] = 0.f;
+    float l_part = 0.f;     // this lane's share of head n's sum
 
-    const int vp = lane / LPT;         // token sub-row of this lane in V loads
-    const int vd = (lane % LPT) * 4;   // first of the 4 dims this lane owns
+    u32x4_t kf[2][KK], kn[2][KK], vf[VL], vn[VL];
+    int t0 = t_begin + 32 * w;
+    if (t0 < t_end) load_block(t0, kf, vf);
+    for (; t0 < t_end; t0 += 128) {
+        const bool more = t0 + 128 < t_end;
+        if (more) load_block(t0 + 128, kn, vn);  // streams in during this block
 
-    for (int t0 = t_begin + 16 * w; t0 < t_end; t0 += 64) {
-        // loads first (K as MFMA A operand, V coalesced); clamp rows past
-        // the split end onto the last valid row: finite, and masked below
-        const int tk = min(t0 + n, t_end - 1);
-        const uint16_t* kp = kbase + (int64_t)tk * p.row_stride + 8 * g;
-        u32x4_t kf[KK];
+        // stage V (this wave's buffer: its previous reads are consumed)
 #pragma unroll
-        for (int kk = 0; kk < KK; kk++) kf[kk] = load16(kp + 32 * kk);
-        u32x2_t vf[VI];
+        for (int j = 0; j < VL; j++) *reinterpret_cast<u32x4_t*>(stage + st_off[j]) = vf[j];
+
+        f32x4_t sacc[2];
 #pragma unroll
-        for (int i = 0; i < VI; i++) {
-            const int tv = min(t0 + i * TPI + vp, t_end - 1);
-            vf[i] = load8(vbase + (int64_t)tv * p.row_stride + vd);
+        for (int nb = 0; nb < 2; nb++) {
+            f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++) acc = mfma16x16x32<DT>(kf[nb][kk], qf[kk], acc);
+            sacc[nb] = acc;
         }
-
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+        // lane (g, n): head n, tokens t0 + 8g + 4nb + i
+        float x[8];
+        float smax = kNegInf;
 #pragma unroll
-        for (int kk = 0; kk < KK; kk++) acc = mfma16x16x32<DT>(kf[kk], qf[kk], acc);
-
-        // acc[i] = score of token t0 + 4g + i for head n
-        float x[4];
-        float mt = kNegInf;
+        for (int nb = 0; nb < 2; nb++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            x[i] = (t0 + 4 * g + i < t_end) ? acc[i] * p.scale_log2 : kNegInf;
-            mt = fmaxf(mt, x[i]);
+            for (int i = 0; i < 4; i++) {
+                const float v = (t0 + 8 * g + 4 * nb + i < t_end) ? sacc[nb][i] * p.scale_log2 : kNegInf;
+                x[4 * nb + i] = v;
+                smax = fmaxf(smax, v);
+            }
+        if (__any(smax > m_run + kHeadroom)) {  // re-base head n (wave-uniform branch)
+            const float m_new = fmaxf(m_run, max_x32(max_x16(smax)));
+            if (m_new > m_run) {
+                const float alpha = fast_exp2(m_run - m_new);  // 0 while m_run = -inf
+                l_part *= alpha;
+#pragma unroll
+                for (int d = 0; d < DB; d++) o[d] *= alpha;
+                m_run = m_new;
+            }
         }
-        mt = fmaxf(mt, wave_xor(mt, 16));
-        mt = fmaxf(mt, wave_xor(mt, 32));
-        const float m_new = fmaxf(m_run, mt);  // finite: token t0 is valid
-        const float alpha = fast_exp2(m_run - m_new);
+        const float nm = (m_run == kNegInf || n >= G) ? 0.f : -m_run;
         float ps = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            x[i] = fast_exp2(x[i] - m_new);
-            ps += x[i];
+        for (int e = 0; e < 8; e++) {
+            x[e] = n < G ? fast_exp2(x[e] + nm) : 0.f;
+            ps += x[e];
         }
-        l_part = l_part * alpha + ps;
-        m_run = m_new;
+        l_part += ps;
+        u32x4_t pfr[NP];
+        split_p<DT, NP>(x, pfr);
 
-#pragma unroll
-        for (int i = 0; i < 4; i++) p_lds[w][4 * g + i][n] = x[i];
-        if (g == 0) a_lds[w][n] = alpha;
+        // O^T += V^T . P^T (staged rows visible to the wave's own reads)
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
 #pragma unroll
-        for (int h = 0; h < GMAX; h++) {
-            if (h < G) {
-                const float a = a_lds[w][h];
-                o[h][0] *= a; o[h][1] *= a; o[h][2] *= a; o[h][3] *= a;
-            }
-        }
+        for (int d = 0; d < DB; d++) {
+            const u32x2_t lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(stage + t_off[d]));
+            const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(stage + t_off[d] + 4 * RB));
+            const u32x4_t vt = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-        for (int i = 0; i < VI; i++) {
-            const int tl = i * TPI + vp;
-            const float v0 = lo_f32<DT>(vf[i][0]), v1 = hi_f32<DT>(vf[i][0]);
-            const float v2 = lo_f32<DT>(vf[i][1]), v3 = hi_f32<DT>(vf[i][1]);
-#pragma unroll
-            for (int h = 0; h < GMAX; h++) {
-                if (h < G) {
-                    const float pw = p_lds[w][tl][h];
-                    o[h][0] += pw * v0; o[h][1] += pw * v1;
-                    o[h][2] += pw * v2; o[h][3] += pw * v3;
-                }
-            }
+            for (int pp = 0; pp < NP; pp++) o[d] = mfma16x16x32<DT>(vt, pfr[pp], o[d]);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
-
-    // wave-level reductions: l over the 4 token groups, o over token sub-rows
-    l_part += wave_xor(l_part, 16);
-    l_part += wave_xor(l_part, 32);
+        if (more) {
 #pragma unroll
-    for (int h = 0; h < GMAX; h++) {
+            for (int nb = 0; nb < 2; nb++)
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            float v = o[h][c];
-            if (LPT <= 16) v += wave_xor(v, 16);
-            v += wave_xor(v, 32);
-            o[h][c] = v;
+                for (int kk = 0; kk < KK; kk++) kf[nb][kk] = kn[nb][kk];
+#pragma unroll
+            for (int j = 0; j < VL; j++) vf[j] = vn[j];
         }
     }
+
+    // ---- merge the 4 waves' (m, l, O) per head through LDS
+    l_part = sum_x32(sum_x16(l_part));
+    __syncthreads();  // staging buffers are free
+    float* o_lds = reinterpret_cast<float*>(&lds[0]);   // [4][16][OROW]
+    float* m_lds = o_lds + 4 * 16 * OROW;               // [4][16]
+    float* l_lds = m_lds + 4 * 16;                      // [4][16]
+#pragma unroll
+    for (int d = 0; d < DB; d++)
+        *reinterpret_cast<f32x4_t*>(&o_lds[(w * 16 + n) * OROW + 16 * d + 4 * g]) = o[d];
     if (g == 0) {
-        m_lds[w][n] = m_run;
-        l_lds[w][n] = l_part;
-    }
-    if (vp == 0) {
-#pragma unroll
-        for (int h = 0; h < GMAX; h++) {
-            if (h < G) {
-                o_lds[w][h][vd + 0] = o[h][0];
-                o_lds[w][h][vd + 1] = o[h][1];
-                o_lds[w][h][vd + 2] = o[h][2];
-                o_lds[w][h][vd + 3] = o[h][3];
-            }
-        }
+        m_lds[w * 16 + n] = m_run;
+        l_lds[w * 16 + n] = l_part;
     }
     __syncthreads();
-
-    // merge the 4 waves' (m, l, o) for each (head, dim)
     for (int idx = threadIdx.x; idx < G * D; idx += 256) {
         const int h = idx / D, d = idx - h * D;
         float M = kNegInf;
 #pragma unroll
-        for (int ww = 0; ww < 4; ww++) M = fmaxf(M, m_lds[ww][h]);
+        for (int ww = 0; ww < 4; ww++) M = fmaxf(M, m_lds[ww * 16 + h]);
         float L = 0.f, O = 0.f;
 #pragma unroll
         for (int ww = 0; ww < 4; ww++) {
-            const float mw = m_lds[ww][h];
+            const float mw = m_lds[ww * 16 + h];
             const float f = (mw == kNegInf) ? 0.f : fast_exp2(mw - M);
-            L += f * l_lds[ww][h];
-            O += f * o_lds[ww][h][d];
+            L += f * l_lds[ww * 16 + h];
+            O += f * o_lds[(ww * 16 + h) * OROW + d];
         }
         const int64_t bh = (int64_t)b * p.H + h0 + h;
         if (p.num_splits == 1) {
@@ -215,26 +254,29 @@ __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p
     const int64_t bh = (int64_t)b * p.H + h;
     const float inv = lse_weights(p.ws_ml + bh * p.num_splits * 2, 2, nact, f_lds, red_lds);
     const float* os = p.ws_o + bh * p.num_splits * D + d;
-    float O0 = 0.f, O1 = 0.f, O2 = 0.f, O3 = 0.f;
+    // 8 independent loads in flight per step
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     int s = 0;
-    for (; s + 4 <= nact; s += 4) {
-        O0 += f_lds[s] * os[(int64_t)s * D];
-        O1 += f_lds[s + 1] * os[(int64_t)(s + 1) * D];
-        O2 += f_lds[s + 2] * os[(int64_t)(s + 2) * D];
-        O3 += f_lds[s + 3] * os[(int64_t)(s + 3) * D];
+    for (; s + 8 <= nact; s += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = os[(int64_t)(s + j) * D];
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[j] += f_lds[s + j] * v[j];
     }
-    for (; s < nact; s++) O0 += f_lds[s] * os[(int64_t)s * D];
-    store_out<OUT_DT>(p.out, bh * D + d, ((O0 + O1) + (O2 + O3)) * inv);
+    for (; s < nact; s++) acc[0] += f_lds[s] * os[(int64_t)s * D];
+    const float O = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+    store_out<OUT_DT>(p.out, bh * D + d, O * inv);
 }
 
 // ------------------------------------------------------------------ launch
 
-template <int D, int GMAX, int DT, int OUT_DT>
+template <int D, int DT, int OUT_DT>
 static hipError_t launch_gqa_t(const GqaDecodeParams& p, int B, int Hk, hipStream_t st,
                                KernelTimer* timer) {
     dim3 grid(p.num_splits, Hk, B);
     timer_begin(timer, "gqa_decode", st);
-    hipLaunchKernelGGL((gqa_decode_kernel<D, GMAX, DT, OUT_DT>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gqa_decode_kernel<D, DT, OUT_DT>), grid, dim3(256), 0, st, p);
     timer_end(timer, "gqa_decode", st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.num_splits == 1) return e;
@@ -244,32 +286,21 @@ static hipError_t launch_gqa_t(const GqaDecodeParams& p, int B, int Hk, hipStrea
     return hipGetLastError();
 }
 
-template <int D, int GMAX, int DT>
+template <int D, int DT>
 static hipError_t launch_gqa_o(const GqaDecodeParams& p, int B, int Hk, int out_dt, hipStream_t st,
                                KernelTimer* t) {
     switch (out_dt) {
-        case DT_F32: return launch_gqa_t<D, GMAX, DT, DT_F32>(p, B, Hk, st, t);
-        case DT_F16: return launch_gqa_t<D, GMAX, DT, DT_F16>(p, B, Hk, st, t);
-        default: return launch_gqa_t<D, GMAX, DT, DT_BF16>(p, B, Hk, st, t);
+        case DT_F32: return launch_gqa_t<D, DT, DT_F32>(p, B, Hk, st, t);
+        case DT_F16: return launch_gqa_t<D, DT, DT_F16>(p, B, Hk, st, t);
+        default: return launch_gqa_t<D, DT, DT_BF16>(p, B, Hk, st, t);
     }
-}
-
-template <int D, int GMAX>
-static hipError_t launch_gqa_d(const GqaDecodeParams& p, int B, int Hk, int kv_dt, int out_dt,
-                               hipStream_t st, KernelTimer* t) {
-    if (kv_dt == DT_F16) return launch_gqa_o<D, GMAX, DT_F16>(p, B, Hk, out_dt, st, t);
-    return launch_gqa_o<D, GMAX, DT_BF16>(p, B, Hk, out_dt, st, t);
 }
 
 template <int D>
 static hipError_t launch_gqa_g(const GqaDecodeParams& p, int B, int Hk, int kv_dt, int out_dt,
                                hipStream_t st, KernelTimer* t) {
-    // GMAX sizes the per-lane accumulator array; G <= GMAX is masked
-    if (p.G <= 1) return launch_gqa_d<D, 1>(p, B, Hk, kv_dt, out_dt, st, t);
-    if (p.G <= 2) return launch_gqa_d<D, 2>(p, B, Hk, kv_dt, out_dt, st, t);
-    if (p.G <= 4) return launch_gqa_d<D, 4>(p, B, Hk, kv_dt, out_dt, st, t);
-    if (p.G <= 8) return launch_gqa_d<D, 8>(p, B, Hk, kv_dt, out_dt, st, t);
-    return launch_gqa_d<D, 16>(p, B, Hk, kv_dt, out_dt, st, t);
+    if (kv_dt == DT_F16) return launch_gqa_o<D, DT_F16>(p, B, Hk, out_dt, st, t);
+    return launch_gqa_o<D, DT_BF16>(p, B, Hk, out_dt, st, t);
 }
 
 hipError_t launch_gqa_decode(const GqaDecodeParams& p, int B, int Hk, int D, int kv_dt, int out_dt,

@@ -207,8 +207,7 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
             // re-base the row only when a weight would exceed 2^kHeadroom
             if (__any(smax * p.scale_log2 > m_run[mb] + kHeadroom)) {
                 float mt = smax * p.scale_log2;
-                mt = fmaxf(mt, wave_xor(mt, 16));
-                mt = fmaxf(mt, wave_xor(mt, 32));
+                mt = max_x32(max_x16(mt));
                 const float m_new = fmaxf(m_run[mb], mt);
                 if (m_new > m_run[mb]) {
                     const float alpha = fast_exp2(m_run[mb] - m_new);  // 0 when m_run = -inf
@@ -241,8 +240,7 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
         float l = l_part[mb];
-        l += wave_xor(l, 16);
-        l += wave_xor(l, 32);
+        l = sum_x32(sum_x16(l));
         l_part[mb] = l;
     }
     __syncthreads();  // every wave is done with the ring

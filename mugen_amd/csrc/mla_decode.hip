@@ -369,8 +369,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
                         mt = fmaxf(mt, vis ? sacc[mb][nb][i] * p.scale_log2 : kNegInf);
                     }
                 }
-                mt = fmaxf(mt, wave_xor(mt, 16));
-                mt = fmaxf(mt, wave_xor(mt, 32));
+                mt = max_x32(max_x16(mt));
                 if (m_ref[mb] == kNegInf) m_ref[mb] = mt;  // O of this row is still 0
             }
         }
@@ -426,8 +425,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
         float l = l_part[mb];
-        l += wave_xor(l, 16);
-        l += wave_xor(l, 32);
+        l = sum_x32(sum_x16(l));
         lrow[mb] = l;
     }
     // Per S-layout row n: weight c0 of this wave's O and c1 of the other
@@ -676,23 +674,29 @@ __global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
     auto h4 = [](u32x2_t v) {
         return f32x4_t{lo_f32<DT_F16>(v[0]), hi_f32<DT_F16>(v[0]), lo_f32<DT_F16>(v[1]), hi_f32<DT_F16>(v[1])};
     };
-    f32x4_t A0 = {0.f, 0.f, 0.f, 0.f}, A1 = A0, B0 = A0, B1 = A0;
+    // 8 splits (16 fragment loads) in flight per step: the merge is latency-bound
+    constexpr int U = 8;
+    f32x4_t A0 = {0.f, 0.f, 0.f, 0.f}, A1 = A0;
     int s = 0;
-    for (; s + 2 <= nact; s += 2) {
+    for (; s + U <= nact; s += U) {
+        u32x2_t fa[U], fb[U];
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            fa[j] = src[(s + j) * frag_st];
+            fb[j] = src[(s + j) * frag_st + 64];
+        }
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            const f32x4_t w = *reinterpret_cast<const f32x4_t*>(&wts[s + j][4 * g]);
+            A0 += w * h4(fa[j]);
+            A1 += w * h4(fb[j]);
+        }
+    }
+    for (; s < nact; s++) {
         const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(&wts[s][4 * g]);
-        const f32x4_t w1 = *reinterpret_cast<const f32x4_t*>(&wts[s + 1][4 * g]);
         A0 += w0 * h4(src[s * frag_st]);
         A1 += w0 * h4(src[s * frag_st + 64]);
-        B0 += w1 * h4(src[(s + 1) * frag_st]);
-        B1 += w1 * h4(src[(s + 1) * frag_st + 64]);
     }
-    if (s < nact) {
-        const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(&wts[s][4 * g]);
-        A0 += w0 * h4(src[s * frag_st]);
-        A1 += w0 * h4(src[s * frag_st + 64]);
-    }
-    A0 += B0;
-    A1 += B1;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int row = qb * 16 + 4 * g + i;

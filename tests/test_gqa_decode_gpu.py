@@ -54,8 +54,10 @@ def test_head_groups_and_edges(device, H, Hk, D, dtype):
 def test_split_count_invariance(device):
     c = C.gqa_decode_case(46, 2, 28, 4, 128, [3000, 1777], dtype=C.F16)
     outs = [run_gpu(c, device, C.F32, s) for s in (1, 0, 7, 40)]
+    # fp16 softmax weights on MFMA: each split rounds its own P (relative 2^-12)
     for o in outs[1:]:
-        np.testing.assert_allclose(o, outs[0], atol=2e-5, rtol=1e-4)
+        C.say(f"split invariance max diff {np.abs(o - outs[0]).max():.2e}")
+        np.testing.assert_allclose(o, outs[0], atol=1e-4, rtol=1e-3)
 
 
 def test_golden_fixture(device):
