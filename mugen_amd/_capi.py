@@ -80,11 +80,12 @@ def lib() -> ctypes.CDLL:
     """Load libmugen_attn.so; raise if it has not been built."""
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
+        path = os.environ.get("MUGEN_ATTN_LIB", LIB_PATH)  # alternative build (kernel comparisons)
+        if not os.path.exists(path):
             raise ImportError(
-                f"{LIB_PATH} not found: build it with `python -m mugen_amd.build` "
+                f"{path} not found: build it with `python -m mugen_amd.build` "
                 "(or __graft_entry__.build()); mugen_amd has no CPU fallback")
-        L = ctypes.CDLL(LIB_PATH)
+        L = ctypes.CDLL(path)
         L.mugen_attn_gqa_decode_workspace_size.argtypes = [ctypes.POINTER(GqaDecodeArgs)]
         L.mugen_attn_gqa_decode_workspace_size.restype = ctypes.c_size_t
         L.mugen_attn_gqa_decode.argtypes = [ctypes.POINTER(GqaDecodeArgs), _vp, ctypes.c_size_t, _vp]

@@ -7,6 +7,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
@@ -208,12 +209,18 @@ static size_t gqa_ws(const mugen_attn_gqa_decode_args* a, int chunk, int* splits
     return slots * (size_t)a->head_dim * 4 + slots * 2 * 4 + 256;
 }
 
-// MLA: 128-row workgroups (32 rows per wave) when there are enough rows and
-// q is 16-bit, else 64-row workgroups
+// MLA kernel variant (mla_decode.hip): fp32 q or at most 64 query rows ->
+// 1 (64-row workgroups, 16 rows per wave); otherwise 4 (64-row workgroups of
+// 8 waves, two per SIMD, 64-token tiles).  MUGEN_ATTN_MLA_VARIANT=1..4
+// overrides the choice (kernel comparisons); variants 2-4 need 16-bit q.
 static int mla_variant(const mugen_attn_mla_decode_args* a) {
     const int R = a->q_len * a->n_heads;
-    if (R <= 64 || a->q_dtype == DT_F32) return 1;
-    return 3;
+    const int dflt = (R <= 64 || a->q_dtype == DT_F32) ? 1 : 3;
+    if (const char* e = getenv("MUGEN_ATTN_MLA_VARIANT")) {
+        const int v = atoi(e);
+        if (v == 1 || (v >= 2 && v <= 4 && a->q_dtype != DT_F32)) return v;
+    }
+    return dflt;
 }
 
 // Active (sequence, split) groups for a chunk: exact from the host length

@@ -27,6 +27,25 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 enum { DT_F32 = MUGEN_ATTN_F32, DT_F16 = MUGEN_ATTN_F16, DT_BF16 = MUGEN_ATTN_BF16 };
 
+// Phase timestamps for development profiling, compiled only with
+// -DMUGEN_ATTN_TRACE (a single-translation-unit build that defines the
+// buffer): lane 0 of every wave stores the 100 MHz real-time counter of
+// numbered points (k < 16) of its kernel, indexed by workgroup and wave.
+#ifdef MUGEN_ATTN_TRACE
+extern __device__ uint64_t mugen_attn_trace[];
+#define MUGEN_TRACE(k)                                                                          \
+    do {                                                                                        \
+        if ((threadIdx.x & 63) == 0)                                                            \
+            mugen_attn_trace[(((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * \
+                                 (blockDim.x >> 6) * 16 + (threadIdx.x >> 6) * 16               \
+                             + (k)] = __builtin_amdgcn_s_memrealtime();                         \
+    } while (0)
+#else
+#define MUGEN_TRACE(k) \
+    do {               \
+    } while (0)
+#endif
+
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 

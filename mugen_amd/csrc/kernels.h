@@ -53,7 +53,7 @@ struct MlaParams {
     const uint16_t* lat;   // latent cache
     const int32_t* seq_lens;
     void* out;             // [B][q_len*H][512]
-    float* ws_o;           // [B][splits][nq][32][64] fp16x4 fragments of o/l (see blob_frag)
+    float* ws_o;           // [B][splits][nq][16][64] 16-byte pairs of fp16x4 fragments of o/l (see blob_pair)
     float* ws_ml;          // [B][splits][R][2]
     int B;
     int q_len;

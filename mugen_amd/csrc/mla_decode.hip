@@ -50,7 +50,7 @@ constexpr int kCD = kKR + kRD;          // 576 latent dims per token
 constexpr int kTT = 32;                 // tokens per LDS tile
 constexpr int kRowBytes = kCD * 2;      // 1152 B per latent row (72 x 16-byte chunks)
 constexpr int kTileBytes = kTT * kRowBytes;       // 36 KiB
-constexpr int kDmaPerWave = kTileBytes / 1024 / 4;  // 9 one-KiB DMA instructions per wave
+constexpr int kDmaPerTile = kTileBytes / 1024;    // 36 one-KiB DMA instructions per 32-token tile
 constexpr int kNBuf = 3;                // ring depth: two tiles in flight
 
 // LDS swizzle: 16-byte chunk c of tile row r is stored at chunk c ^ swz(r).
@@ -73,11 +73,13 @@ template <int DT>
 __device__ constexpr float headroom_log2() { return DT == DT_BF16 ? 64.f : 15.f; }
 
 // O partial blob (normalised o/l, fp16), in MFMA accumulator-fragment
-// order: for sequence b, split s and 16-row block q, the 4-element fragment
-//   (((b*S + s)*nq + q)*32 + d)*64 + lane
-// holds rows 16q + 4*(lane/16) + i (i = 0..3) at column 16d + lane%16.
-__device__ __forceinline__ int64_t blob_frag(const MlaParams& p, int b, int s, int q, int d, int lane) {
-    return ((((int64_t)b * p.num_splits + s) * p.nq + q) * 32 + d) * 64 + lane;
+// order.  For sequence b, split s and 16-row block q, the 16-byte unit
+//   (((b*S + s)*nq + q)*16 + dp)*64 + lane
+// holds the 4-element fragments of column blocks 2dp and 2dp+1 (8 bytes
+// each): rows 16q + 4*(lane/16) + i (i = 0..3) at column 16d + lane%16.  A
+// wave stores, and the combine loads, 1 KiB contiguous per instruction.
+__device__ __forceinline__ int64_t blob_pair(const MlaParams& p, int b, int s, int q, int dp, int lane) {
+    return ((((int64_t)b * p.num_splits + s) * p.nq + q) * 16 + dp) * 64 + lane;
 }
 
 // S-chain MFMA with a VGPR accumulator (FIRST: C = 0)
@@ -96,8 +98,8 @@ __device__ __forceinline__ void mfma_s(f32x4_t& acc, const u32x4_t& a, const u32
     }
 }
 
-template <int MB, int TS, int QDT, int DT>
-__global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
+template <int MB, int TS, int NW, int QDT, int DT>
+__global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
     constexpr int KS = kCD / 32;  // 18 k-steps over the 576 dims
     constexpr int NQ = (QDT == DT_F32) ? 2 : 1;
     constexpr float TH = headroom_log2<DT>();
@@ -109,35 +111,50 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     constexpr int TILE_T = kTT * TS;                 // tokens per tile
     constexpr int TILE_B = TILE_T * kRowBytes;       // bytes per tile
     constexpr int NBUF = TS == 1 ? kNBuf : 2;        // ring depth
-    constexpr int DPW = kDmaPerWave * TS;            // 1-KiB DMA ops per wave per tile
-    constexpr int RG = 4 / TS;                       // row groups (waves per token slice)
+    // NW = 4: one wave per SIMD (up to 512 registers per lane).  NW = 8
+    // (MB = 1): two waves per SIMD within 256 registers, so one wave's
+    // softmax, barrier and LDS waits overlap the other's MFMAs; a single
+    // wave cannot issue 16x16x32 MFMAs faster than about one per 18 clocks,
+    // two waves sharing a SIMD reach about one per 10.
+    static_assert(NW == 4 || (NW == 8 && MB == 1), "8-wave variant holds 16 rows per wave");
+    constexpr int DPW = kDmaPerTile * TS / NW;       // 1-KiB DMA ops per wave per tile
+    constexpr int RG = NW / TS;                      // row groups (waves per token slice)
+    constexpr int DSTRIDE = NW * 1024;               // LDS bytes between a wave's DMA ops
     __shared__ __attribute__((aligned(1024))) char ring[NBUF * TILE_B];
 
     // XCD-aware work mapping.  Workgroups are dealt to the 8 XCDs round-robin
     // by blockIdx.  A group = the nrb row blocks of one (sequence, split);
-    // they read the same latent tiles, so all of a group's row blocks go to
-    // one XCD (its L2 serves the tile to each), while consecutive groups go
-    // to different XCDs so every XCD gets an even share of the splits.
-    // Groups are numbered compactly over the ACTIVE splits only (sequence j
-    // contributes ceil(seq_lens[j] / chunk) of them), so a grid sized from
-    // the host's length hint has no idle workgroups and every XCD gets an
-    // even share in a single dispatch round.
+    // groups are numbered compactly over the ACTIVE splits (sequence j
+    // contributes ceil(seq_lens[j] / chunk) of them, in order), and each XCD
+    // takes a contiguous range of ceil(active / 8) groups.  So all row blocks
+    // of a group share one XCD's L2 for the latent tiles, consecutive splits
+    // of a sequence share it for the query rows (each sequence's q is fetched
+    // into one or two L2s, not all eight), and every XCD gets an even share.
+    // The grid is sized from the host's group count (exact with the length
+    // hint, an upper bound without); surplus workgroups exit at once.
     const int nxcd = 8;
     const int xcd = blockIdx.x % nxcd, slot = blockIdx.x / nxcd;
     const int nrb = p.nrb;
     const int rb = slot % nrb;
-    const int grp = (slot / nrb) * nxcd + xcd;  // active (sequence, split) group
+    int nact = 0;
+    for (int j = 0; j < p.B; j++) nact += (p.seq_lens[j] + p.chunk - 1) / p.chunk;  // uniform scalar loop
+    const int gpx = (nact + nxcd - 1) / nxcd;
+    const int gi = slot / nrb;
+    const int grp = xcd * gpx + gi;  // active (sequence, split) group
     int b = -1, s = 0;
-    for (int j = 0, acc = 0; j < p.B; j++) {  // uniform scalar loop over the batch
-        const int nsj = (p.seq_lens[j] + p.chunk - 1) / p.chunk;
-        if (grp < acc + nsj) {
-            b = j;
-            s = grp - acc;
-            break;
+    if (gi < gpx) {
+        for (int j = 0, acc = 0; j < p.B; j++) {
+            const int nsj = (p.seq_lens[j] + p.chunk - 1) / p.chunk;
+            if (grp < acc + nsj) {
+                b = j;
+                s = grp - acc;
+                break;
+            }
+            acc += nsj;
         }
-        acc += nsj;
     }
     if (b < 0) return;  // grid padding past the last active split
+    MUGEN_TRACE(0);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -157,23 +174,30 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     // (r, pc ^ swz(r)).  Offsets are clamped to the split's last valid byte,
     // so tokens past t_end read valid cache rows (masked later)
     const uint32_t ring_base = lds_addr(&ring[0]);
-    uint32_t dma_off[DPW];
-#pragma unroll
-    for (int k = 0; k < DPW; k++) {
-        const int slot = 64 * (w + 4 * k) + lane;
+    auto dma_offset = [&](int k) {
+        int ln = lane;
+        if constexpr (NW == 8) asm volatile("" : "+v"(ln));  // opaque: recomputed at each use, never hoisted and spilled
+        const int slot = 64 * (w + NW * k) + ln;
         const int r = slot / (kRowBytes / 16), pc = slot - r * (kRowBytes / 16);
-        dma_off[k] = (uint32_t)(r * kRowBytes + ((pc ^ swz(r)) * 16));
-    }
+        return (uint32_t)(r * kRowBytes + ((pc ^ swz(r)) * 16));
+    };
+    // NW = 4 keeps the offsets in registers; the 8-wave variant, at 256
+    // registers per lane, recomputes them at each DMA (a few VALU ops)
+    constexpr int NOFF = NW == 4 ? DPW : 1;
+    uint32_t dma_off_r[NOFF];
+#pragma unroll
+    for (int k = 0; k < NOFF; k++) dma_off_r[k] = dma_offset(k);
+    auto dma_off = [&](int k) { return NW == 4 ? dma_off_r[k < NOFF ? k : 0] : dma_offset(k); };
     auto issue = [&](int tt, int buf) {
         const uint16_t* tbase = lat + (int64_t)tt * kCD;  // wave-uniform
         const uint32_t lds0 = ring_base + buf * TILE_B + w * 1024;
         if (tt + TILE_T <= t_end) {  // whole tile valid: precomputed offsets
 #pragma unroll
-            for (int k = 0; k < DPW; k++) dma16s(lds0 + k * 4096, tbase, dma_off[k]);
+            for (int k = 0; k < DPW; k++) dma16s(lds0 + k * DSTRIDE, tbase, dma_off(k));
         } else {  // last tile of the split: clamp to its last valid chunk
             const uint32_t lim = (uint32_t)(t_end - tt) * kRowBytes - 16;
 #pragma unroll
-            for (int k = 0; k < DPW; k++) dma16s(lds0 + k * 4096, tbase, min(dma_off[k], lim));
+            for (int k = 0; k < DPW; k++) dma16s(lds0 + k * DSTRIDE, tbase, min(dma_off(k), lim));
         }
     };
 
@@ -189,14 +213,14 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
         const uint32_t qlim = (uint32_t)min(64, p.R - rb * 64) * kRowBytes - 16;
         const uint32_t q_lds = ring_base + TILE_B + w * 1024;
 #pragma unroll
-        for (int k = 0; k < DPW; k++) dma16s(q_lds + k * 4096, qrows, min(dma_off[k], qlim));
+        for (int k = 0; k < DPW; k++) dma16s(q_lds + k * DSTRIDE, qrows, min(dma_off(k), qlim));
         issue(t_begin, 0);
         vm_wait<DPW>();  // the query rows landed (tile 0 may still fly)
         lds_barrier();
         const char* qt = &ring[TILE_B];
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) {
-            const int r = rg * 32 + 16 * mb + n, row = rb * 64 + r;
+            const int r = rg * 16 * MB + 16 * mb + n, row = rb * 64 + r;
             const bool ok = row < p.R;
             teff[mb] = ok ? (T - p.q_len + row / p.H + 1) : T;
 #pragma unroll
@@ -249,6 +273,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     // understands: it then inserts no vmcnt(0) inside the tile loop (where
     // it would also drain the ring's in-flight DMA it cannot see)
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    MUGEN_TRACE(1);
 
     // S operand (A): row ar = 8*(n/4) + n%4 (+4nb), logical chunk 4ks + g.
     // swz(ar) does not depend on nb; (4ks + g) ^ h = 8*(ks/2) + ((4*(ks%2) + g) ^ h)
@@ -282,11 +307,24 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     }
     int buf = 0;
     for (int it = 0; it < ntiles; it++) {
+        if (it == 2) MUGEN_TRACE(6);
         if (NBUF > 2 && it + 1 < ntiles) vm_wait<DPW>();
         else vm_wait<0>();
         lds_barrier();  // tile `it` landed for every wave; the buffer of tile it-1 is free
-        if (it + NBUF - 1 < ntiles)
-            issue(t_begin + TILE_T * (it + NBUF - 1), buf == 0 ? NBUF - 1 : buf - 1);
+        if (it == 0) MUGEN_TRACE(2);
+        if (it == 2) MUGEN_TRACE(7);
+        // the next tile's DMA goes into the buffer freed by the barrier; its
+        // DPW instructions are spread over the S k-steps below, so the
+        // per-CU address unit works through them while the MFMAs run
+        // instead of holding up the wave's first MFMA behind all of them
+        const bool pf = it + NBUF - 1 < ntiles;
+        const int pf_tt = t_begin + TILE_T * (it + NBUF - 1);
+        const uint16_t* pf_src = lat + (int64_t)pf_tt * kCD;  // wave-uniform
+        const uint32_t pf_lds = ring_base + (buf == 0 ? NBUF - 1 : buf - 1) * TILE_B + w * 1024;
+        const uint32_t pf_lim = pf_tt + TILE_T <= t_end ? 0xFFFFFFFFu : (uint32_t)(t_end - pf_tt) * kRowBytes - 16;
+        auto issue_k = [&](int k) {
+            if (pf) dma16s(pf_lds + k * DSTRIDE, pf_src, min(dma_off(k), pf_lim));
+        };
         // this wave's 32-token slice of the tile (same swizzle: it ignores row bit 5)
         const char* tile = ring_bytes + buf * TILE_B + th * kTT * kRowBytes;
         buf = buf == NBUF - 1 ? 0 : buf + 1;
@@ -295,7 +333,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
         // ---- S^T = L . Q^T  (two 16-token blocks), VGPR accumulators.
         // Software-pipelined: operands of k-step ks+SPD are requested while
         // step ks runs, so each LDS read has ~2 steps of MFMA work to land.
-        constexpr int SPD = 3;
+        constexpr int SPD = NW == 8 ? 2 : 3;
         auto a_ptr = [&](int ks, int nb) {
             return reinterpret_cast<const u32x4_t*>(tile + ((ks & 1) ? a_off1 : a_off0) + 128 * (ks >> 1) +
                                                     4 * kRowBytes * nb);
@@ -325,9 +363,13 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
                 abuf[ks % SPD][0] = *a_ptr(ks + SPD, 0);
                 abuf[ks % SPD][1] = *a_ptr(ks + SPD, 1);
             }
+#pragma unroll
+            for (int k = 0; k < DPW; k++)
+                if ((k * KS) / DPW == ks) issue_k(k);
         }
+        if (it == 2) MUGEN_TRACE(11);
         // first P.L operands requested now, to land during the softmax
-        constexpr int VPD = 6;
+        constexpr int VPD = NW == 8 ? 4 : 6;
         // TS = 2: slice 1 accumulates its O with the 16-column blocks rotated
         // by 16 (register d holds column block (d + 16) % 32), so that the
         // epilogue of both slices keeps registers 0..15 and hands over 16..31
@@ -401,6 +443,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
         if (tt + kTT <= t_end && tt + kTT <= teff_min) weights(std::false_type{});
         else weights(std::true_type{});
 
+        if (it == 2) MUGEN_TRACE(12);
         // ---- O += P . L[:, 0:512]; B operand L[tt + 8g + j][16d + n], j < 8.
         // The schedule is pinned to [MFMA x MB][2 transpose reads of d+VPD]
         // so VPD steps of reads stay in flight behind the MFMAs.
@@ -413,6 +456,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
             __builtin_amdgcn_sched_group_barrier(0x008, MB, 0);
             if (d + VPD < 32) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
+        if (it == 2) MUGEN_TRACE(13);
     }
 
     // ---- epilogue: (m, l, o/l) partial of this split.  The normalised O is
@@ -421,6 +465,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     // contiguous per store instruction); m and l stay fp32.  A row whose
     // weights or normalised values left the 16-bit ranges is flagged (NaN m)
     // for the exact fp32 recompute in the combine kernel.
+    MUGEN_TRACE(3);
     float lrow[MB];  // S-layout row n: full sum of this wave's token slice
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
@@ -493,14 +538,21 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
         float vmax = 0.f;                 // largest |o/l| this lane stores
         if (rblk < p.R) {
             // registers 0..DH-1 = column blocks th*DH .. th*DH + DH-1
-            u32x2_t* dst = reinterpret_cast<u32x2_t*>(p.ws_o) + blob_frag(p, b, s, rblk >> 4, th * DH, lane);
+            u32x4_t* dst = reinterpret_cast<u32x4_t*>(p.ws_o) + blob_pair(p, b, s, rblk >> 4, (th * DH) >> 1, lane);
 #pragma unroll
-            for (int d = 0; d < DH; d++) {
-                f32x4_t v = o[mb][d] * f32x4_t{k0[0], k0[1], k0[2], k0[3]};
-                if constexpr (TS == 2) v += ox[(mb * DH + d) * 64 + lane] * f32x4_t{k1[0], k1[1], k1[2], k1[3]};
-                vmax = fmaxf(vmax, fmaxf(fabsf(v[0]), fabsf(v[1])));
-                vmax = fmaxf(vmax, fmaxf(fabsf(v[2]), fabsf(v[3])));
-                dst[d * 64] = u32x2_t{pack2<DT_F16>(v[0], v[1]), pack2<DT_F16>(v[2], v[3])};
+            for (int d = 0; d < DH; d += 2) {
+                uint32_t h[4];
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    f32x4_t v = o[mb][d + e] * f32x4_t{k0[0], k0[1], k0[2], k0[3]};
+                    if constexpr (TS == 2)
+                        v += ox[(mb * DH + d + e) * 64 + lane] * f32x4_t{k1[0], k1[1], k1[2], k1[3]};
+                    vmax = fmaxf(vmax, fmaxf(fabsf(v[0]), fabsf(v[1])));
+                    vmax = fmaxf(vmax, fmaxf(fabsf(v[2]), fabsf(v[3])));
+                    h[2 * e] = pack2<DT_F16>(v[0], v[1]);
+                    h[2 * e + 1] = pack2<DT_F16>(v[2], v[3]);
+                }
+                dst[(d >> 1) * 64] = u32x4_t{h[0], h[1], h[2], h[3]};
             }
         }
         // fp16 partials: a normalised value past 65000 cannot be stored
@@ -514,6 +566,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
                 if (lane == 0) big_x[rg * MB + mb] = big_mask[mb];
         }
         __syncthreads();
+        MUGEN_TRACE(4);
         if (th == 1) return;
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) big_mask[mb] |= big_x[rg * MB + mb];
@@ -530,6 +583,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
             p.ws_ml[slot * 2 + 1] = Lrow[mb];
         }
     }
+    MUGEN_TRACE(5);
 }
 
 // Exact fp32 recompute of one (row, split) partial, for rows the main kernel
@@ -588,7 +642,8 @@ __device__ void mla_recompute_split(const MlaParams& p, int b, int row, int s, f
     for (int k = 0; k < ncols; k++) {
         const int col = tid + k * nt;
         const int lane = 16 * ((row & 15) >> 2) + (col & 15);
-        blob[blob_frag(p, b, s, row >> 4, col >> 4, lane) * 4 + (row & 3)] = from_f32<DT_F16>(O[k] * inv);
+        const int d = col >> 4;
+        blob[blob_pair(p, b, s, row >> 4, d >> 1, lane) * 8 + (d & 1) * 4 + (row & 3)] = from_f32<DT_F16>(O[k] * inv);
     }
     if (tid == 0) {
         const int64_t slot = ((int64_t)b * p.num_splits + s) * p.R + row;
@@ -619,43 +674,62 @@ __global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
     const int64_t ml_st = (int64_t)p.R * 2;  // floats between splits of one row
     const float* ml0 = p.ws_ml + (int64_t)b * p.num_splits * p.R * 2;
 
-    // rare path: recompute (row, split) partials flagged with a NaN max
-    if (tid == 0) nflag = 0;
-    __syncthreads();
-    for (int k = tid; k < 16 * nact; k += 256) {
-        const int row = qb * 16 + (k & 15), s = k >> 4;
-        if (row < p.R && __builtin_isnan(ml0[s * ml_st + row * 2])) nflag = 1;
-    }
-    __syncthreads();
-    if (nflag) {
-        for (int k = 0; k < 16 * nact; k++) {
-            const int row = qb * 16 + (k & 15), s = k >> 4;
-            const bool flagged = row < p.R && __builtin_isnan(ml0[s * ml_st + row * 2]);
-            __syncthreads();
-            if (flagged) mla_recompute_split<QDT, DT>(p, b, row, s, x_lds, &red[0][0]);
-            __threadfence_block();
-            __syncthreads();
-        }
-    }
+    MUGEN_TRACE(8);
+    const int d0 = dg * 8 + dsub * 2;
+    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(p.ws_o) + blob_pair(p, b, 0, qb, d0 >> 1, lane);
+    const int64_t frag_st = (int64_t)p.nq * 16 * 64;  // 16-byte units between splits
+    // the first PF splits' fp16 fragments are requested before the split
+    // weights are known, so their latency overlaps the (m, l) reads
+    constexpr int PF = 16;
+    u32x4_t fa[PF];
+    auto prefetch = [&]() {
+#pragma unroll
+        for (int j = 0; j < PF; j++)
+            if (j < nact) fa[j] = src[j * frag_st];
+    };
+    prefetch();
 
-    // split weights: thread (row r = tid%16, split phase sl = tid/16)
-    {
-        const int r = tid & 15, sl = tid >> 4, row = qb * 16 + r;
-        const bool ok = row < p.R;
+    // split weights: thread (row r = tid%16, split phase sl = tid/16).  A
+    // NaN max marks a (row, split) the main kernel could not finish in 16
+    // bits; it is recomputed exactly (rare path), then the weights are redone.
+    const int r = tid & 15, sl = tid >> 4, row = qb * 16 + r;
+    const bool rok = row < p.R;
+    for (int pass = 0; pass < 2; pass++) {
+        if (tid == 0) nflag = 0;
         float mx = kNegInf;
-        for (int s = sl; s < nact; s += 16) mx = fmaxf(mx, ok ? ml0[s * ml_st + row * 2] : kNegInf);
+        bool bad = false;
+        for (int s = sl; s < nact; s += 16) {
+            const float m = rok ? ml0[s * ml_st + row * 2] : kNegInf;
+            bad |= __builtin_isnan(m);
+            mx = fmaxf(mx, m);
+        }
         red[sl][r] = mx;
         __syncthreads();
+        if (bad) nflag = 1;
         float M = kNegInf;
 #pragma unroll
         for (int j = 0; j < 16; j++) M = fmaxf(M, red[j][r]);
         __syncthreads();
+        if (nflag) {  // uniform: the flag was written before the barrier
+            for (int k = 0; k < 16 * nact; k++) {
+                const int rr = qb * 16 + (k & 15), ss = k >> 4;
+                const bool flagged = rr < p.R && __builtin_isnan(ml0[ss * ml_st + rr * 2]);
+                __syncthreads();
+                if (flagged) mla_recompute_split<QDT, DT>(p, b, rr, ss, x_lds, &red[0][0]);
+                __threadfence_block();
+                __syncthreads();
+            }
+            __threadfence();
+            __syncthreads();
+            prefetch();  // the recompute rewrote fragments
+            continue;
+        }
         float sum = 0.f;
         for (int s = sl; s < nact; s += 16) {
-            const float m = ok ? ml0[s * ml_st + row * 2] : kNegInf;
-            const float w = (m == kNegInf) ? 0.f : fast_exp2(m - M) * ml0[s * ml_st + row * 2 + 1];
-            wts[s][r] = w;
-            sum += w;
+            const float m = rok ? ml0[s * ml_st + row * 2] : kNegInf;
+            const float wgt = (m == kNegInf) ? 0.f : fast_exp2(m - M) * ml0[s * ml_st + row * 2 + 1];
+            wts[s][r] = wgt;
+            sum += wgt;
         }
         red[sl][r] = sum;
         __syncthreads();
@@ -666,61 +740,68 @@ __global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
             linv[tid] = L > 0.f ? 1.f / L : 0.f;
         }
         __syncthreads();
+        break;
     }
+    MUGEN_TRACE(9);
 
-    const int d0 = dg * 8 + dsub * 2;
-    const u32x2_t* src = reinterpret_cast<const u32x2_t*>(p.ws_o) + blob_frag(p, b, 0, qb, d0, lane);
-    const int64_t frag_st = (int64_t)p.nq * 32 * 64;  // fragments between splits
-    auto h4 = [](u32x2_t v) {
-        return f32x4_t{lo_f32<DT_F16>(v[0]), hi_f32<DT_F16>(v[0]), lo_f32<DT_F16>(v[1]), hi_f32<DT_F16>(v[1])};
+    auto h4 = [](uint32_t a, uint32_t b) {
+        return f32x4_t{lo_f32<DT_F16>(a), hi_f32<DT_F16>(a), lo_f32<DT_F16>(b), hi_f32<DT_F16>(b)};
     };
-    // 8 splits (16 fragment loads) in flight per step: the merge is latency-bound
-    constexpr int U = 8;
     f32x4_t A0 = {0.f, 0.f, 0.f, 0.f}, A1 = A0;
-    int s = 0;
-    for (; s + U <= nact; s += U) {
-        u32x2_t fa[U], fb[U];
 #pragma unroll
-        for (int j = 0; j < U; j++) {
-            fa[j] = src[(s + j) * frag_st];
-            fb[j] = src[(s + j) * frag_st + 64];
+    for (int j = 0; j < PF; j++) {
+        if (j < nact) {
+            const f32x4_t w = *reinterpret_cast<const f32x4_t*>(&wts[j][4 * g]);
+            A0 += w * h4(fa[j][0], fa[j][1]);
+            A1 += w * h4(fa[j][2], fa[j][3]);
         }
+    }
+    // sequences with more than PF splits: 8 splits (16 loads) in flight per step
+    constexpr int U = 8;
+    int s = PF;
+    for (; s + U <= nact; s += U) {
+        u32x4_t ga[U];
+#pragma unroll
+        for (int j = 0; j < U; j++) ga[j] = src[(s + j) * frag_st];
 #pragma unroll
         for (int j = 0; j < U; j++) {
             const f32x4_t w = *reinterpret_cast<const f32x4_t*>(&wts[s + j][4 * g]);
-            A0 += w * h4(fa[j]);
-            A1 += w * h4(fb[j]);
+            A0 += w * h4(ga[j][0], ga[j][1]);
+            A1 += w * h4(ga[j][2], ga[j][3]);
         }
     }
     for (; s < nact; s++) {
         const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(&wts[s][4 * g]);
-        A0 += w0 * h4(src[s * frag_st]);
-        A1 += w0 * h4(src[s * frag_st + 64]);
+        const u32x4_t v = src[s * frag_st];
+        A0 += w0 * h4(v[0], v[1]);
+        A1 += w0 * h4(v[2], v[3]);
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int row = qb * 16 + 4 * g + i;
-        if (row < p.R) {
+        const int orow = qb * 16 + 4 * g + i;
+        if (orow < p.R) {
             const float inv = linv[4 * g + i];
-            const int64_t base = ((int64_t)b * p.R + row) * kKR + 16 * d0 + n;
+            const int64_t base = ((int64_t)b * p.R + orow) * kKR + 16 * d0 + n;
             store_out<OUT_DT>(p.out, base, A0[i] * inv);
             store_out<OUT_DT>(p.out, base + 16, A1[i] * inv);
         }
     }
+    MUGEN_TRACE(10);
 }
 
 // ------------------------------------------------------------------ launch
 
 // variant 1: MB = 1, TS = 1 (64 rows); 2: MB = 2, TS = 1 (128 rows);
-// 3: MB = 2, TS = 2 (64 rows, 64-token tiles)
+// 3: MB = 2, TS = 2 (64 rows, 64-token tiles); 4: MB = 1, TS = 2, 8 waves
+// (64 rows, 64-token tiles, two waves per SIMD)
 int mla_rows_per_block(int variant) { return variant == 2 ? 128 : 64; }
-int mla_tile_tokens(int variant) { return variant == 3 ? 2 * kTT : kTT; }
+int mla_tile_tokens(int variant) { return variant >= 3 ? 2 * kTT : kTT; }
 
-template <int MB, int TS, int QDT, int DT, int OUT_DT>
+template <int MB, int TS, int NW, int QDT, int DT, int OUT_DT>
 static hipError_t launch_mla_t(const MlaParams& p, hipStream_t st, KernelTimer* t) {
     const int grid = 8 * p.nrb * ((p.groups + 7) / 8);  // see the XCD mapping in the kernel
     timer_begin(t, "mla_decode", st);
-    hipLaunchKernelGGL((mla_decode_kernel<MB, TS, QDT, DT>), dim3(grid), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((mla_decode_kernel<MB, TS, NW, QDT, DT>), dim3(grid), dim3(64 * NW), 0, st, p);
     timer_end(t, "mla_decode", st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -730,21 +811,22 @@ static hipError_t launch_mla_t(const MlaParams& p, hipStream_t st, KernelTimer* 
     return hipGetLastError();
 }
 
-template <int MB, int TS, int QDT, int DT>
+template <int MB, int TS, int NW, int QDT, int DT>
 static hipError_t launch_mla_o(const MlaParams& p, int out_dt, hipStream_t st, KernelTimer* t) {
-    if (out_dt == DT_F32) return launch_mla_t<MB, TS, QDT, DT, DT_F32>(p, st, t);
-    if (out_dt == DT_F16) return launch_mla_t<MB, TS, QDT, DT, DT_F16>(p, st, t);
-    return launch_mla_t<MB, TS, QDT, DT, DT_BF16>(p, st, t);
+    if (out_dt == DT_F32) return launch_mla_t<MB, TS, NW, QDT, DT, DT_F32>(p, st, t);
+    if (out_dt == DT_F16) return launch_mla_t<MB, TS, NW, QDT, DT, DT_F16>(p, st, t);
+    return launch_mla_t<MB, TS, NW, QDT, DT, DT_BF16>(p, st, t);
 }
 
 template <int DT>
 static hipError_t launch_mla_v(const MlaParams& p, int variant, int q_dt, int out_dt, hipStream_t st,
                                KernelTimer* t) {
     // variants 2 and 3 (32 rows per wave) need 16-bit q (register budget)
-    if (q_dt == DT_F32) return launch_mla_o<1, 1, DT_F32, DT>(p, out_dt, st, t);
-    if (variant == 2) return launch_mla_o<2, 1, DT, DT>(p, out_dt, st, t);
-    if (variant == 3) return launch_mla_o<2, 2, DT, DT>(p, out_dt, st, t);
-    return launch_mla_o<1, 1, DT, DT>(p, out_dt, st, t);
+    if (q_dt == DT_F32) return launch_mla_o<1, 1, 4, DT_F32, DT>(p, out_dt, st, t);
+    if (variant == 2) return launch_mla_o<2, 1, 4, DT, DT>(p, out_dt, st, t);
+    if (variant == 3) return launch_mla_o<2, 2, 4, DT, DT>(p, out_dt, st, t);
+    if (variant == 4) return launch_mla_o<1, 2, 8, DT, DT>(p, out_dt, st, t);
+    return launch_mla_o<1, 1, 4, DT, DT>(p, out_dt, st, t);
 }
 
 hipError_t launch_mla_decode(const MlaParams& p, int variant, int q_dt, int lat_dt, int out_dt,
