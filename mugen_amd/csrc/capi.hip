@@ -165,13 +165,43 @@ static int explicit_chunk(int max_seq_len, int num_splits, int quantum, int max_
 
 // GQA decode: tokens per split (multiple of 64 = one 16-token block per wave);
 // ~2 resident 256-thread workgroups per CU over 256 CUs
+// GQA decode work items for a chunk: sum over sequences of max(1,
+// ceil(T_b / chunk)) splits times the kv heads -- exact from the host length
+// hint, else the batch * max_seq_len upper bound.
+static int64_t gqa_items(const mugen_attn_gqa_decode_args* a, int chunk) {
+    const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
+    int64_t n = 0;
+    if (!a->seq_lens_host) {
+        n = (int64_t)a->batch * ceil_div(maxT, chunk);
+    } else {
+        for (int b = 0; b < a->batch; b++)
+            n += a->seq_lens_host[b] > 0 ? ceil_div(a->seq_lens_host[b], chunk) : 1;
+    }
+    return n * a->n_kv_heads;
+}
+
 // GQA decode: a workgroup's 4 waves take 32-token blocks, so chunks are
-// multiples of 128 tokens; about 512 workgroups (two per CU) keep every CU
-// streaming while the split count -- the combine's work -- stays low.
+// multiples of 128 tokens.  The kernel holds two 256-thread workgroups per
+// CU; the plan is the smallest chunk whose work list fits ONE dispatch round
+// of 512 workgroups (every CU streaming, no second round), with at most
+// kMaxSplits splits per sequence.
 static int gqa_chunk(const mugen_attn_gqa_decode_args* a) {
-    if (a->num_splits > 0) return explicit_chunk(a->max_seq_len, a->num_splits, 128);
-    const int64_t work = planned_tokens(a->seq_lens_host, a->batch, a->max_seq_len) * a->n_kv_heads;
-    return plan_chunk(work, 512, 128, a->max_seq_len);
+    constexpr int q = 128;
+    const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
+    if (a->num_splits > 0) return explicit_chunk(maxT, a->num_splits, q, kMaxSplits);
+    const int cmax = ceil_div(maxT, q) * q;
+    const int cmin = ceil_div(ceil_div(maxT, kMaxSplits), q) * q;
+    const int64_t budget = 512;
+    if (gqa_items(a, cmax) > budget) return cmax;  // one split per sequence already fills a round
+    int lo = cmin < q ? q : cmin, hi = cmax;       // items(c) is non-increasing in c
+    while (lo < hi) {
+        const int mid = ((lo + hi) / 2) / q * q;
+        if (mid <= lo) break;
+        if (gqa_items(a, mid) <= budget) hi = mid;
+        else lo = mid + q;
+    }
+    if (gqa_items(a, lo) > budget) lo = hi;
+    return lo;
 }
 
 static int gqa_validate(const mugen_attn_gqa_decode_args* a) {
@@ -200,6 +230,7 @@ static int gqa_validate(const mugen_attn_gqa_decode_args* a) {
     return MUGEN_ATTN_OK;
 }
 
+// workspace: fp32 partials [B][H][splits][D] and (m, l) [B][H][splits][2]
 static size_t gqa_ws(const mugen_attn_gqa_decode_args* a, int chunk, int* splits_out) {
     const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
     const int splits = ceil_div(maxT, chunk);
@@ -324,6 +355,8 @@ int mugen_attn_gqa_decode(const mugen_attn_gqa_decode_args* a, void* ws, size_t 
         return fail(MUGEN_ATTN_E_WORKSPACE, "gqa_decode: workspace of %zu bytes required, %zu given", need,
                     ws_bytes);
     GqaDecodeParams p{};
+    p.B = a->batch;
+    p.Hk = a->n_kv_heads;
     p.q = static_cast<const uint16_t*>(a->q);
     p.k = static_cast<const uint16_t*>(a->k_cache);
     p.v = static_cast<const uint16_t*>(a->v_cache);
@@ -343,7 +376,9 @@ int mugen_attn_gqa_decode(const mugen_attn_gqa_decode_args* a, void* ws, size_t 
         p.ws_o = base;
         p.ws_ml = base + slots * a->head_dim;
     }
-    hipError_t e = launch_gqa_decode(p, a->batch, a->n_kv_heads, a->head_dim, a->kv_dtype, a->out_dtype,
+    const int64_t nwg = gqa_items(a, chunk);
+    if (nwg > INT32_MAX) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode: too many work items");
+    hipError_t e = launch_gqa_decode(p, (int)nwg, a->head_dim, a->kv_dtype, a->out_dtype,
                                      static_cast<hipStream_t>(stream), active_timer());
     return hip_status(e, "gqa_decode launch");
 }

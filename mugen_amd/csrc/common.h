@@ -40,7 +40,17 @@ extern __device__ uint64_t mugen_attn_trace[];
                                  (blockDim.x >> 6) * 16 + (threadIdx.x >> 6) * 16               \
                              + (k)] = __builtin_amdgcn_s_memrealtime();                         \
     } while (0)
+#define MUGEN_TRACE_CLK(k)                                                                      \
+    do {                                                                                        \
+        if ((threadIdx.x & 63) == 0)                                                            \
+            mugen_attn_trace[(((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * \
+                                 (blockDim.x >> 6) * 16 + (threadIdx.x >> 6) * 16               \
+                             + (k)] = __builtin_readcyclecounter();                             \
+    } while (0)
 #else
+#define MUGEN_TRACE_CLK(k) \
+    do {                   \
+    } while (0)
 #define MUGEN_TRACE(k) \
     do {               \
     } while (0)

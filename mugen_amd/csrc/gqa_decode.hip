@@ -24,6 +24,9 @@
 //    one head, so softmax factors never cross lanes;
 //  * online softmax in the exp2 domain with a lazy max (a head is re-based
 //    only when a weight would exceed 2^8);
+//  * the grid is a compact list of the active (sequence, split, kv head)
+//    items -- max(1, ceil(T_b / chunk)) splits per sequence -- that the host
+//    planner sizes to one dispatch round (two workgroups per CU);
 //  * the 4 waves merge (m, l, o) through LDS; with one split the result is
 //    normalised and stored, otherwise (m, l, o) partials go to the
 //    workspace and gqa_decode_combine merges them with fp32 log-sum-exp.
@@ -62,13 +65,27 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(GqaDecodeParams p) {
     constexpr int MERGE = 4 * 16 * OROW * 4 + 2 * 4 * 16 * 4;
     __shared__ __attribute__((aligned(16))) char lds[STAGE > MERGE ? STAGE : MERGE];
 
-    const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    // compact work list: item r of sequence b is split r / Hk of kv head r % Hk
+    int b = -1, s = 0, kvh = 0;
+    for (int j = 0, r = blockIdx.x; j < p.B; j++) {  // uniform scalar loop over the batch
+        const int Tj = p.seq_lens[j];
+        const int nsj = Tj > 0 ? (Tj + p.chunk - 1) / p.chunk : 1;
+        if (r < nsj * p.Hk) {
+            b = j;
+            s = r / p.Hk;
+            kvh = r - s * p.Hk;
+            break;
+        }
+        r -= nsj * p.Hk;
+    }
+    if (b < 0) return;  // grid padding (sized from an upper bound)
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int T = p.seq_lens[b];
     const int t_begin = s * p.chunk;
     const int t_end = min(t_begin + p.chunk, T);
-    if (p.num_splits > 1 && t_begin >= T) return;  // empty split: combine skips it
+    if (p.num_splits > 1 && t_begin >= T) return;  // empty split (T <= 0): the combine skips it
+    MUGEN_TRACE(0);
     const int G = p.G;
     const int h0 = kvh * G;
 
@@ -200,6 +217,7 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(GqaDecodeParams p) {
         }
     }
 
+    MUGEN_TRACE(1);
     // ---- merge the 4 waves' (m, l, O) per head through LDS
     l_part = sum_x32(sum_x16(l_part));
     __syncthreads();  // staging buffers are free
@@ -239,6 +257,7 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(GqaDecodeParams p) {
             }
         }
     }
+    MUGEN_TRACE(2);
 }
 
 // Log-sum-exp merge of the split partials of one (sequence, head): the
@@ -249,6 +268,7 @@ __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p
     __shared__ float f_lds[kMaxSplits];
     __shared__ float red_lds[4];
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    MUGEN_TRACE(8);
     const int T = p.seq_lens[b];
     const int nact = min(p.num_splits, (T + p.chunk - 1) / p.chunk);
     const int64_t bh = (int64_t)b * p.H + h;
@@ -267,46 +287,44 @@ __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p
     for (; s < nact; s++) acc[0] += f_lds[s] * os[(int64_t)s * D];
     const float O = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
     store_out<OUT_DT>(p.out, bh * D + d, O * inv);
+    MUGEN_TRACE(9);
 }
 
 // ------------------------------------------------------------------ launch
 
 template <int D, int DT, int OUT_DT>
-static hipError_t launch_gqa_t(const GqaDecodeParams& p, int B, int Hk, hipStream_t st,
-                               KernelTimer* timer) {
-    dim3 grid(p.num_splits, Hk, B);
+static hipError_t launch_gqa_t(const GqaDecodeParams& p, int nwg, hipStream_t st, KernelTimer* timer) {
     timer_begin(timer, "gqa_decode", st);
-    hipLaunchKernelGGL((gqa_decode_kernel<D, DT, OUT_DT>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gqa_decode_kernel<D, DT, OUT_DT>), dim3(nwg), dim3(256), 0, st, p);
     timer_end(timer, "gqa_decode", st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.num_splits == 1) return e;
     timer_begin(timer, "gqa_decode_combine", st);
-    hipLaunchKernelGGL((gqa_decode_combine_kernel<D, OUT_DT>), dim3(p.H, B), dim3(D), 0, st, p);
+    hipLaunchKernelGGL((gqa_decode_combine_kernel<D, OUT_DT>), dim3(p.H, p.B), dim3(D), 0, st, p);
     timer_end(timer, "gqa_decode_combine", st);
     return hipGetLastError();
 }
 
 template <int D, int DT>
-static hipError_t launch_gqa_o(const GqaDecodeParams& p, int B, int Hk, int out_dt, hipStream_t st,
-                               KernelTimer* t) {
+static hipError_t launch_gqa_o(const GqaDecodeParams& p, int nwg, int out_dt, hipStream_t st, KernelTimer* t) {
     switch (out_dt) {
-        case DT_F32: return launch_gqa_t<D, DT, DT_F32>(p, B, Hk, st, t);
-        case DT_F16: return launch_gqa_t<D, DT, DT_F16>(p, B, Hk, st, t);
-        default: return launch_gqa_t<D, DT, DT_BF16>(p, B, Hk, st, t);
+        case DT_F32: return launch_gqa_t<D, DT, DT_F32>(p, nwg, st, t);
+        case DT_F16: return launch_gqa_t<D, DT, DT_F16>(p, nwg, st, t);
+        default: return launch_gqa_t<D, DT, DT_BF16>(p, nwg, st, t);
     }
 }
 
 template <int D>
-static hipError_t launch_gqa_g(const GqaDecodeParams& p, int B, int Hk, int kv_dt, int out_dt,
-                               hipStream_t st, KernelTimer* t) {
-    if (kv_dt == DT_F16) return launch_gqa_o<D, DT_F16>(p, B, Hk, out_dt, st, t);
-    return launch_gqa_o<D, DT_BF16>(p, B, Hk, out_dt, st, t);
+static hipError_t launch_gqa_g(const GqaDecodeParams& p, int nwg, int kv_dt, int out_dt, hipStream_t st,
+                               KernelTimer* t) {
+    if (kv_dt == DT_F16) return launch_gqa_o<D, DT_F16>(p, nwg, out_dt, st, t);
+    return launch_gqa_o<D, DT_BF16>(p, nwg, out_dt, st, t);
 }
 
-hipError_t launch_gqa_decode(const GqaDecodeParams& p, int B, int Hk, int D, int kv_dt, int out_dt,
-                             hipStream_t st, KernelTimer* t) {
-    if (D == 128) return launch_gqa_g<128>(p, B, Hk, kv_dt, out_dt, st, t);
-    return launch_gqa_g<64>(p, B, Hk, kv_dt, out_dt, st, t);
+hipError_t launch_gqa_decode(const GqaDecodeParams& p, int nwg, int D, int kv_dt, int out_dt, hipStream_t st,
+                             KernelTimer* t) {
+    if (D == 128) return launch_gqa_g<128>(p, nwg, kv_dt, out_dt, st, t);
+    return launch_gqa_g<64>(p, nwg, kv_dt, out_dt, st, t);
 }
 
 }  // namespace mugen_attn

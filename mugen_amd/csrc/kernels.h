@@ -18,6 +18,8 @@ struct GqaDecodeParams {
     void* out;
     float* ws_o;   // [B][H][splits][D]   unnormalised partial outputs
     float* ws_ml;  // [B][H][splits][2]   (max in log2 units, sum)
+    int B;
+    int Hk;
     int H;
     int G;           // query heads per kv head
     int row_stride;  // elements between consecutive tokens (Hk * D)
@@ -27,8 +29,9 @@ struct GqaDecodeParams {
     float scale_log2;  // softmax scale * log2(e)
 };
 
-hipError_t launch_gqa_decode(const GqaDecodeParams& p, int B, int Hk, int D, int kv_dt, int out_dt,
-                             hipStream_t st, KernelTimer* t);
+// nwg: workgroups of the compact work list (exact, or an upper bound)
+hipError_t launch_gqa_decode(const GqaDecodeParams& p, int nwg, int D, int kv_dt, int out_dt, hipStream_t st,
+                             KernelTimer* t);
 
 struct GqaPrefillParams {
     const uint16_t* q;

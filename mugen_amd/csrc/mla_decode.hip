@@ -313,6 +313,7 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
         lds_barrier();  // tile `it` landed for every wave; the buffer of tile it-1 is free
         if (it == 0) MUGEN_TRACE(2);
         if (it == 2) MUGEN_TRACE(7);
+        if (it == 2) MUGEN_TRACE_CLK(14);
         // the next tile's DMA goes into the buffer freed by the barrier; its
         // DPW instructions are spread over the S k-steps below, so the
         // per-CU address unit works through them while the MFMAs run
@@ -457,6 +458,7 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
             if (d + VPD < 32) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
         if (it == 2) MUGEN_TRACE(13);
+        if (it == 2) MUGEN_TRACE_CLK(15);
     }
 
     // ---- epilogue: (m, l, o/l) partial of this split.  The normalised O is
