@@ -588,6 +588,292 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
     MUGEN_TRACE(5);
 }
 
+// Warp-specialised variant (5): 8 waves, two per SIMD, 64 query rows per
+// workgroup, 32-token tiles.  Waves 0-3 ("S waves") each hold the q of 16
+// rows in registers, compute S^T = L . Q^T for the tile and its softmax
+// weights, and write P to LDS in the A-operand layout of P . V.  Waves 4-7
+// ("PV waves") each own a 128-column quarter of O for all 64 rows and
+// accumulate O += P . L[:, cols] from that P; they also move the tiles by
+// LDS DMA.  The S waves work on tile j while the PV waves consume tile
+// j - 1, so each SIMD runs one wave of each kind: the MFMA pipe is fed from
+// two instruction streams (one wave cannot issue MFMAs faster than about one
+// per 18 clocks; two reach about one per 10) and one wave's softmax, LDS
+// waits and barrier overlap the other's MFMAs.  Neither role holds both q
+// (72 registers for 16 rows) and O (128 for a 64 x 128 quarter), so a wave
+// fits the 256 registers of two waves per SIMD.
+//
+// LDS: a 4-slot ring of 32-token tiles (two tiles in flight, one read by the
+// S waves, one by the PV waves) and a double-buffered P.  One barrier per
+// tile: at barrier j the S waves have written P(j-1) and the PV waves have
+// finished tile j-2, whose slot then receives tile j+2.
+template <int DT>
+__global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
+    constexpr int KS = kCD / 32;          // 18 k-steps over the 576 dims
+    constexpr float TH = headroom_log2<DT>();
+    constexpr int NSLOT = 4;
+    constexpr int DPW = kDmaPerTile / 4;  // 9 one-KiB DMA ops per PV wave per tile
+    constexpr int PBUF = 4 * 64 * 16;     // one P buffer: 4 row blocks x 64 lanes x 16 B
+    __shared__ __attribute__((aligned(1024))) char ring[NSLOT * kTileBytes + 2 * PBUF];
+    __shared__ float2 ml_x[64];           // per row: (reference max, sum) from the S waves
+    __shared__ int ovf_x[64];
+    __shared__ uint64_t big_x[4][4];      // [PV wave][row block] overflow ballots
+
+    // work mapping: as mla_decode_kernel (XCD-blocked active groups)
+    const int nxcd = 8;
+    const int xcd = blockIdx.x % nxcd, slot = blockIdx.x / nxcd;
+    const int nrb = p.nrb;
+    const int rb = slot % nrb;
+    int nact = 0;
+    for (int j = 0; j < p.B; j++) nact += (p.seq_lens[j] + p.chunk - 1) / p.chunk;
+    const int gpx = (nact + nxcd - 1) / nxcd;
+    const int gi = slot / nrb;
+    const int grp = xcd * gpx + gi;
+    int b = -1, s = 0;
+    if (gi < gpx) {
+        for (int j = 0, acc = 0; j < p.B; j++) {
+            const int nsj = (p.seq_lens[j] + p.chunk - 1) / p.chunk;
+            if (grp < acc + nsj) {
+                b = j;
+                s = grp - acc;
+                break;
+            }
+            acc += nsj;
+        }
+    }
+    if (b < 0) return;
+    MUGEN_TRACE(0);
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool s_wave = w < 4;
+    const int wr = w & 3;  // S wave: row block; PV wave: column quarter
+    const int n = lane & 15, g = lane >> 4;
+    const int T = p.seq_lens[b];
+    const int t_begin = s * p.chunk;
+    const int t_end = min(t_begin + p.chunk, T);
+    const int ntiles = (t_end - t_begin + kTT - 1) / kTT;
+    const int row0 = rb * 64;  // first query row of the workgroup
+    const uint16_t* lat = p.lat + (int64_t)b * p.seq_stride;
+    const uint32_t ring_base = lds_addr(&ring[0]);
+    char* pbuf = &ring[NSLOT * kTileBytes];
+
+    // ---- PV waves: DMA of tile tt into slot sl (wave wr moves LDS chunks
+    // [64K, 64K+64) for K = wr + 4k; chunk (r, pc) holds source chunk
+    // (r, pc ^ swz(r)); the split's last tile is clamped to valid rows)
+    auto issue = [&](int tile_idx) {
+        const int tt = t_begin + kTT * tile_idx;
+        const uint16_t* src = lat + (int64_t)tt * kCD;
+        const uint32_t lds0 = ring_base + (tile_idx % NSLOT) * kTileBytes + wr * 1024;
+        const uint32_t lim = tt + kTT <= t_end ? 0xFFFFFFFFu : (uint32_t)(t_end - tt) * kRowBytes - 16;
+#pragma unroll
+        for (int k = 0; k < DPW; k++) {
+            const int sl = 64 * (wr + 4 * k) + lane;
+            const int r = sl / (kRowBytes / 16), pc = sl - r * (kRowBytes / 16);
+            dma16s(lds0 + k * 4096, src, min((uint32_t)(r * kRowBytes + ((pc ^ swz(r)) * 16)), lim));
+        }
+    };
+
+    if (s_wave) {
+        // ================================================== S waves
+        const int rowq = row0 + 16 * wr + n;  // S-layout row of this lane
+        const bool ok = rowq < p.R;
+        const int teff = ok ? (T - p.q_len + rowq / p.H + 1) : T;  // visible tokens of the row
+        u32x4_t qf[KS];
+        {
+            const uint16_t* qp = static_cast<const uint16_t*>(p.q) + ((int64_t)b * p.R + (ok ? rowq : 0)) * kCD + 8 * g;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) qf[ks] = ok ? load16(qp + 32 * ks) : u32x4_t{0, 0, 0, 0};
+        }
+        int teff_min = teff;
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) teff_min = min(teff_min, __shfl_xor(teff_min, m, 64));
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): q is in registers
+        MUGEN_TRACE(1);
+        const int ar0 = 8 * (n >> 2) + (n & 3);
+        const int hA = swz(ar0);
+        const uint32_t a_off0 = ar0 * kRowBytes + ((g ^ hA) * 16);
+        const uint32_t a_off1 = ar0 * kRowBytes + (((4 + g) ^ hA) * 16);
+        float m_ref = kNegInf, l_part = 0.f;
+
+        for (int j = 0; j <= ntiles; j++) {
+            if (j == 4) MUGEN_TRACE(6);
+            lds_barrier();  // B_j: tile j landed (the PV waves waited for it)
+            if (j == 4) MUGEN_TRACE(7);
+            if (j == ntiles) break;
+            const char* tile = &ring[(j % NSLOT) * kTileBytes];
+            const int tt = t_begin + kTT * j;
+            constexpr int SPD = 4;
+            auto a_ptr = [&](int ks, int nb) {
+                return reinterpret_cast<const u32x4_t*>(tile + ((ks & 1) ? a_off1 : a_off0) + 128 * (ks >> 1) +
+                                                        4 * kRowBytes * nb);
+            };
+            u32x4_t abuf[SPD][2];
+#pragma unroll
+            for (int q = 0; q < SPD; q++) {
+                abuf[q][0] = *a_ptr(q, 0);
+                abuf[q][1] = *a_ptr(q, 1);
+            }
+            f32x4_t sacc[2];
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+#pragma unroll
+                for (int nb = 0; nb < 2; nb++) {
+                    if (ks == 0) mfma_s<DT, true>(sacc[nb], abuf[ks % SPD][nb], qf[ks]);
+                    else mfma_s<DT, false>(sacc[nb], abuf[ks % SPD][nb], qf[ks]);
+                }
+                if (ks + SPD < KS) {
+                    abuf[ks % SPD][0] = *a_ptr(ks + SPD, 0);
+                    abuf[ks % SPD][1] = *a_ptr(ks + SPD, 1);
+                }
+            }
+            asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(sacc[0]), "+v"(sacc[1]));
+            if (j == 4) MUGEN_TRACE(11);
+            // softmax weights against the row's reference max (the max of its
+            // first visible tile); lane holds tokens tt + 8g + 4nb + i of row n
+            if (__any(m_ref == kNegInf)) {
+                float mt = kNegInf;
+#pragma unroll
+                for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int tok = tt + 8 * g + 4 * nb + i;
+                        mt = fmaxf(mt, (tok < t_end && tok < teff) ? sacc[nb][i] * p.scale_log2 : kNegInf);
+                    }
+                mt = max_x32(max_x16(mt));
+                if (m_ref == kNegInf) m_ref = mt;
+            }
+            const float mneg = (m_ref == kNegInf) ? 0.f : -m_ref;
+            const bool masked = !(tt + kTT <= t_end && tt + kTT <= teff_min);
+            float x[8];
+#pragma unroll
+            for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    float v = fmaf(sacc[nb][i], p.scale_log2, mneg);
+                    if (masked) {
+                        const int tok = tt + 8 * g + 4 * nb + i;
+                        v = (tok < t_end && tok < teff) ? v : kNegInf;
+                    }
+                    x[4 * nb + i] = fast_exp2(v);
+                }
+            l_part += ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
+            *reinterpret_cast<u32x4_t*>(pbuf + (j & 1) * PBUF + (wr * 64 + lane) * 16) =
+                u32x4_t{pack2<DT>(x[0], x[1]), pack2<DT>(x[2], x[3]), pack2<DT>(x[4], x[5]), pack2<DT>(x[6], x[7])};
+            if (j == 4) MUGEN_TRACE(12);
+        }
+        MUGEN_TRACE(3);
+        // epilogue 1: the row's (reference max, sum) and headroom flag for the PV waves
+        const float lrow = sum_x32(sum_x16(l_part));
+        if (g == 0) {
+            ml_x[16 * wr + n] = make_float2(m_ref, lrow);
+            ovf_x[16 * wr + n] = !(lrow <= exp2f(TH));
+        }
+        __syncthreads();  // E1
+        __syncthreads();  // E2: the PV waves stored o/l and their overflow ballots
+        uint64_t big = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) big |= big_x[q][wr];
+        const bool row_big = (big >> ((n >> 2) * 16)) & 0xffffull;
+        if (g == 0 && ok) {
+            const int64_t slot_ml = ((int64_t)b * p.num_splits + s) * p.R + rowq;
+            p.ws_ml[slot_ml * 2 + 0] = (ovf_x[16 * wr + n] || row_big) ? __builtin_nanf("") : m_ref;
+            p.ws_ml[slot_ml * 2 + 1] = lrow;
+        }
+        MUGEN_TRACE(5);
+    } else {
+        // ================================================== PV waves
+        issue(0);
+        if (ntiles > 1) issue(1);
+        // V operand (transpose reads): lane (i, g) of read hh reads row
+        // 8g + 4hh + i/4, logical bytes 32cb + 8*(i%4) (column block cb)
+        const int tr0 = 8 * g + (n >> 2);
+        const int hT = swz(tr0);
+        uint32_t t_off[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            t_off[q] = tr0 * kRowBytes + (((2 * q + ((n & 3) >> 1)) ^ hT) * 16) + 8 * (n & 1);
+        f32x4_t o[4][8];  // [row block][column block 8wr + d]
+#pragma unroll
+        for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+            for (int d = 0; d < 8; d++) o[mb][d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+        for (int j = 0; j <= ntiles; j++) {
+            // tile j must have landed for the S waves: this wave's DMAs
+            // complete in order and tile j+1 may still fly
+            if (j == 4) MUGEN_TRACE(6);
+            if (j + 1 < ntiles) vm_wait<DPW>();
+            else vm_wait<0>();
+            if (j == 4) MUGEN_TRACE(13);
+            lds_barrier();  // B_j
+            if (j == 0) MUGEN_TRACE(1);
+            if (j == 4) MUGEN_TRACE(7);
+            if (j + 2 < ntiles) issue(j + 2);  // into the slot of tile j-2, finished before B_j
+            if (j == 0) continue;
+            // O += P(j-1) . L(j-1)[:, 128wr .. +128]
+            const char* tile = &ring[((j - 1) % NSLOT) * kTileBytes];
+            const char* pb = pbuf + ((j - 1) & 1) * PBUF;
+            u32x4_t pa[4];
+#pragma unroll
+            for (int mb = 0; mb < 4; mb++) pa[mb] = *reinterpret_cast<const u32x4_t*>(pb + (mb * 64 + lane) * 16);
+            auto tr_load = [&](int d) {
+                const int cb = 8 * wr + d;
+                const char* tp = tile + t_off[cb & 3] + 128 * (cb >> 2);
+                const u32x2_t lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(tp));
+                const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(tp + 4 * kRowBytes));
+                return u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+            };
+            constexpr int VPD = 4;
+            u32x4_t vb[VPD];
+#pragma unroll
+            for (int q = 0; q < VPD; q++) vb[q] = tr_load(q);
+#pragma unroll
+            for (int d = 0; d < 8; d++) {
+                const u32x4_t bf = vb[d % VPD];
+                if (d + VPD < 8) vb[d % VPD] = tr_load(d + VPD);
+#pragma unroll
+                for (int mb = 0; mb < 4; mb++) o[mb][d] = mfma16x16x32<DT>(pa[mb], bf, o[mb][d]);
+            }
+            if (j == 4) MUGEN_TRACE(12);
+        }
+        MUGEN_TRACE(3);
+        __syncthreads();  // E1: the S waves published (max, sum, flag) per row
+        // epilogue: o/l in fp16, accumulator-fragment order (16-byte pairs
+        // of column blocks); rows whose normalised value does not fit fp16
+        // are flagged for the exact recompute
+#pragma unroll
+        for (int mb = 0; mb < 4; mb++) {
+            const int rblk = row0 + 16 * mb;
+            float k0[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float l = ml_x[16 * mb + 4 * g + i].y;
+                k0[i] = l > 0.f ? 1.f / l : 0.f;
+            }
+            float vmax = 0.f;
+            if (rblk < p.R) {
+                u32x4_t* dst = reinterpret_cast<u32x4_t*>(p.ws_o) + blob_pair(p, b, s, rblk >> 4, 4 * wr, lane);
+#pragma unroll
+                for (int d = 0; d < 8; d += 2) {
+                    uint32_t h[4];
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const f32x4_t v = o[mb][d + e] * f32x4_t{k0[0], k0[1], k0[2], k0[3]};
+                        vmax = fmaxf(vmax, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+                        h[2 * e] = pack2<DT_F16>(v[0], v[1]);
+                        h[2 * e + 1] = pack2<DT_F16>(v[2], v[3]);
+                    }
+                    dst[(d >> 1) * 64] = u32x4_t{h[0], h[1], h[2], h[3]};
+                }
+            }
+            const uint64_t bm = __ballot(!(vmax <= 65000.f));
+            if (lane == 0) big_x[wr][mb] = bm;
+        }
+        __syncthreads();  // E2
+        MUGEN_TRACE(5);
+    }
+}
+
 // Exact fp32 recompute of one (row, split) partial, for rows the main kernel
 // flagged: pass 1 finds the row max, pass 2 accumulates l and o, both over
 // batches of blockDim tokens (one token's 576-dim score per thread); each
@@ -795,9 +1081,10 @@ __global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
 
 // variant 1: MB = 1, TS = 1 (64 rows); 2: MB = 2, TS = 1 (128 rows);
 // 3: MB = 2, TS = 2 (64 rows, 64-token tiles); 4: MB = 1, TS = 2, 8 waves
-// (64 rows, 64-token tiles, two waves per SIMD)
+// (64 rows, 64-token tiles, two waves per SIMD); 5: warp-specialised
+// mla_decode_ws_kernel (64 rows, 32-token tiles)
 int mla_rows_per_block(int variant) { return variant == 2 ? 128 : 64; }
-int mla_tile_tokens(int variant) { return variant >= 3 ? 2 * kTT : kTT; }
+int mla_tile_tokens(int variant) { return (variant == 3 || variant == 4) ? 2 * kTT : kTT; }
 
 template <int MB, int TS, int NW, int QDT, int DT, int OUT_DT>
 static hipError_t launch_mla_t(const MlaParams& p, hipStream_t st, KernelTimer* t) {
@@ -811,6 +1098,27 @@ static hipError_t launch_mla_t(const MlaParams& p, hipStream_t st, KernelTimer* 
     hipLaunchKernelGGL((mla_decode_combine_kernel<QDT, DT, OUT_DT>), dim3(p.nq, 4, p.B), dim3(256), 0, st, p);
     timer_end(t, "mla_decode_combine", st);
     return hipGetLastError();
+}
+
+template <int DT, int OUT_DT>
+static hipError_t launch_mla_ws_t(const MlaParams& p, hipStream_t st, KernelTimer* t) {
+    const int grid = 8 * p.nrb * ((p.groups + 7) / 8);
+    timer_begin(t, "mla_decode", st);
+    hipLaunchKernelGGL((mla_decode_ws_kernel<DT>), dim3(grid), dim3(512), 0, st, p);
+    timer_end(t, "mla_decode", st);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    timer_begin(t, "mla_decode_combine", st);
+    hipLaunchKernelGGL((mla_decode_combine_kernel<DT, DT, OUT_DT>), dim3(p.nq, 4, p.B), dim3(256), 0, st, p);
+    timer_end(t, "mla_decode_combine", st);
+    return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t launch_mla_ws(const MlaParams& p, int out_dt, hipStream_t st, KernelTimer* t) {
+    if (out_dt == DT_F32) return launch_mla_ws_t<DT, DT_F32>(p, st, t);
+    if (out_dt == DT_F16) return launch_mla_ws_t<DT, DT_F16>(p, st, t);
+    return launch_mla_ws_t<DT, DT_BF16>(p, st, t);
 }
 
 template <int MB, int TS, int NW, int QDT, int DT>
@@ -828,6 +1136,7 @@ static hipError_t launch_mla_v(const MlaParams& p, int variant, int q_dt, int ou
     if (variant == 2) return launch_mla_o<2, 1, 4, DT, DT>(p, out_dt, st, t);
     if (variant == 3) return launch_mla_o<2, 2, 4, DT, DT>(p, out_dt, st, t);
     if (variant == 4) return launch_mla_o<1, 2, 8, DT, DT>(p, out_dt, st, t);
+    if (variant == 5) return launch_mla_ws<DT>(p, out_dt, st, t);
     return launch_mla_o<1, 1, 4, DT, DT>(p, out_dt, st, t);
 }
 

@@ -125,3 +125,35 @@ def test_host_length_hint_matches_no_hint(device):
     torch.cuda.synchronize()
     C.assert_close(a, C.mla_ref(c, nthreads=8), "no hint")
     C.assert_close(bb, C.mla_ref(c, nthreads=8), "hint")
+
+
+@pytest.mark.parametrize("variant", [2, 3, 4, 5])
+@pytest.mark.parametrize("B,q_len,H,lens", [
+    (2, 1, 128, [700, 33]),
+    (1, 5, 128, [4]),
+    (2, 2, 64, [700, 129]),
+    (3, 1, 96, [1, 300, 2050]),
+])
+def test_kernel_variants(device, monkeypatch, variant, B, q_len, H, lens):
+    # every 16-bit kernel variant, whichever one the planner would pick
+    monkeypatch.setenv("MUGEN_ATTN_MLA_VARIANT", str(variant))
+    c = C.mla_case(80 + H, B, q_len, H, lens, q_dtype=C.BF16, lat_dtype=C.BF16)
+    ref = C.mla_ref(c)
+    for splits in (0, 1, 4):
+        C.assert_close(run_gpu(c, device, C.F32, splits), ref, f"variant {variant} splits={splits}")
+
+
+@pytest.mark.parametrize("variant", [3, 5])
+def test_variant_overshoot_fallback(device, monkeypatch, variant):
+    # the exact-recompute flag path of the 16-bit variants (R = 128 rows)
+    monkeypatch.setenv("MUGEN_ATTN_MLA_VARIANT", str(variant))
+    c = C.mla_case(61, 2, 1, 128, [900, 300], q_dtype=C.BF16, lat_dtype=C.BF16)
+    lat = c["lat"].copy()
+    lat[0, 700, :] = 0.0
+    lat[0, 700, 0] = 1000.0
+    lat, latb = O.round_to(lat, C.BF16)
+    q = c["q"].copy()
+    q[:, :, :, 0] = np.abs(q[:, :, :, 0]) + 1.0
+    q, qb = O.round_to(q, C.BF16)
+    c2 = dict(c, lat=lat, latb=latb, q=q, qb=qb)
+    C.assert_close(run_gpu(c2, device, C.F32, 0), C.mla_ref(c2), f"variant {variant} overshoot")
