@@ -51,6 +51,7 @@ def randn(shape, std, dtype, gen, dev):
 class Case:
     name = ""
     kernel = ""          # dominant kernel's timing name
+    profile = None       # (kernel, workload) of its summaries under profiles/
     bound = "hbm"
     unit = "GB/s"
 
@@ -72,6 +73,8 @@ class MlaDecode(Case):
         self.sl = torch.from_numpy(self.lens).to(dev)
         self.max_T = max_T
         self.out = torch.empty((B, q_len, H, 512), dtype=torch.float32, device=dev)
+        self.profile = ("mla_decode", {"mla_decode_v3": "v3_b8_h128",
+                                       "mla_verify_v3": "verify_b4_q5_t32768"}.get(name, name))
         self.ws = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
         esz_q = self.q.element_size()
         self.bytes = float(self.lens.sum()) * 576 * self.lat.element_size() + B * q_len * H * (576 * esz_q + 512 * 4)
@@ -122,6 +125,7 @@ class GqaDecode(Case):
         self.sl = torch.from_numpy(self.lens).to(dev)
         self.max_T = max_T
         self.out = torch.empty((B, H, D), dtype=torch.float16, device=dev)
+        self.profile = ("gqa_decode", "qwen7b_b16_ragged" if B == 16 else name)
         self.ws = torch.empty(1 << 26, dtype=torch.uint8, device=dev)
         self.bytes = float(self.lens.sum()) * Hk * D * 2 * 2 + B * H * D * 2 * 2
         self.flops = 4.0 * H * D * float(self.lens.sum())
@@ -143,6 +147,7 @@ class Prefill(Case):
         self.k = randn((N, Hk, D), 1.0, torch.bfloat16, g, dev)
         self.v = randn((N, Hk, D), 1.0, torch.bfloat16, g, dev)
         self.out = torch.empty((N, H, D), dtype=torch.bfloat16, device=dev)
+        self.profile = ("gqa_prefill", "llama1b_n512")
         self.flops = 4.0 * H * D * N * (N + 1) / 2
         self.bytes = (N * H * D * 2) * 2 + N * Hk * D * 2 * 2
 
@@ -269,7 +274,8 @@ def main():
             rate=round(rate(c, t["ms_per_step"]), 2), unit=c.unit,
             kernel_rate=round(rate(c, t["kernel_ms"]), 2),
             frac_of_peak=round(rate(c, t["ms_per_step"]) / (PEAK_HBM_GBS if c.unit == "GB/s" else PEAK_BF16_TFLOPS), 4),
-            algorithmic_bytes=c.bytes, algorithmic_flops=c.flops)
+            algorithmic_bytes=c.bytes, algorithmic_flops=c.flops,
+            traffic=load_traffic(*c.profile) if c.profile else None)
 
     h = results.get(head.name) if head in cases else None
     line = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -287,7 +293,7 @@ def main():
         ach = kb / (h["kernel_us"] * 1e-6) / 1e9
         line["roofline"] = {"bound": "hbm", "kernel": "mla_decode", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS,
                             "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4),
-                            "traffic": load_traffic("mla_decode", "v3_b8_h128"),
+                            "traffic": h["traffic"],
                             "kernel_us": h["kernel_us"], "combine_us": h["combine_us"]}
         if not args.no_cpu:
             full_s, sample = head.cpu_sample()
