@@ -54,16 +54,19 @@ constexpr int kDmaPerTile = kTileBytes / 1024;    // 36 one-KiB DMA instructions
 constexpr int kNBuf = 3;                // ring depth: two tiles in flight
 
 // LDS swizzle: 16-byte chunk c of tile row r is stored at chunk c ^ swz(r).
-// gfx950 LDS serves 64 banks x 4 B per clock: 16 lanes of a b128 read or
-// 32 lanes of a b64 (transpose) read per cycle.  1152-byte rows put every
-// even row on bank 0 and every odd row on bank 32, so unswizzled the S
-// operand reads (rows 8*(n/4) + n%4 + 4nb) cost 8x and the transpose reads
-// (rows 8g + n/4 + 4hh) 4x their minimum.  This XOR of row bits 1, 3, 4
-// (found by exhaustive search over XOR swizzles against that bank model,
-// which reproduces measured conflict counts) makes both conflict-free; it
-// ignores row bit 2, so the nb / hh row offsets keep the same swizzle.
+// gfx950 LDS has 64 banks x 4 B.  Measured on the MI355X (bank-conflict
+// counters of single-pattern probes): a ds_read_b128 runs in four phases of
+// 16 lanes -- each 32-lane half split by the parity of its lane-quad index
+// (lanes 0-3, 12-15, 20-23, 24-27 share a phase) -- and a ds_read_b64 /
+// ds_read_b64_tr_b16 in two phases of 32 consecutive lanes.  1152-byte rows
+// put every even row on bank 0 and every odd row on bank 32, so unswizzled
+// the S operand reads (rows 8*(n/4) + n%4 + 4nb) cost 4x and the transpose
+// reads (rows 8g + n/4 + 4hh) 4x their minimum.  XOR of row bits 1 and 3
+// (an exhaustive search over XOR swizzles against that phase model) makes
+// both conflict-free; it ignores row bits 2, 4 and 5, so the nb / hh row
+// offsets and the token slices keep the same swizzle.
 __host__ __device__ constexpr int swz(int r) {
-    return (((r >> 1) & 1) * 2) ^ (((r >> 3) & 1) * 4) ^ ((r >> 4) & 1);
+    return (((r >> 1) & 1) * 2) ^ (((r >> 3) & 1) * 4);
 }
 
 // Reference-max headroom (log2 units): with the max fixed at the first
@@ -808,7 +811,9 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
             lds_barrier();  // B_j
             if (j == 0) MUGEN_TRACE(1);
             if (j == 4) MUGEN_TRACE(7);
+#ifndef WS_DEBUG_NO_DMA
             if (j + 2 < ntiles) issue(j + 2);  // into the slot of tile j-2, finished before B_j
+#endif
             if (j == 0) continue;
             // O += P(j-1) . L(j-1)[:, 128wr .. +128]
             const char* tile = &ring[((j - 1) % NSLOT) * kTileBytes];
