@@ -233,6 +233,9 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
             }
         }
     } else {
+    // the first tiles' DMA goes out before the q loads: both latencies overlap
+    issue(t_begin, 0);
+    if (ntiles > 1) issue(t_begin + TILE_T, 1);
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
         const int row = row0 + 16 * mb + n;
@@ -244,19 +247,21 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
             if constexpr (QDT == DT_F32) {
+                // two 16-byte loads (q is 16-byte aligned, qoff a multiple of 8)
                 const float* qp = static_cast<const float*>(p.q) + qoff + 32 * ks;
+                const f32x4_t q0 = *reinterpret_cast<const f32x4_t*>(qp);
+                const f32x4_t q1 = *reinterpret_cast<const f32x4_t*>(qp + 4);
                 float x[8];
 #pragma unroll
-                for (int j = 0; j < 8; j++) x[j] = ok ? qp[j] : 0.f;
-                uint32_t hi[4], lo[4];
-#pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const uint16_t h0 = from_f32<DT>(x[2 * j]), h1 = from_f32<DT>(x[2 * j + 1]);
-                    hi[j] = uint32_t(h0) | (uint32_t(h1) << 16);
-                    lo[j] = pack2<DT>(x[2 * j] - to_f32<DT>(h0), x[2 * j + 1] - to_f32<DT>(h1));
+                    x[j] = ok ? q0[j] : 0.f;
+                    x[4 + j] = ok ? q1[j] : 0.f;
                 }
-                qf[mb][0][ks] = u32x4_t{hi[0], hi[1], hi[2], hi[3]};
-                qf[mb][NQ - 1][ks] = u32x4_t{lo[0], lo[1], lo[2], lo[3]};
+                // hi = RNE 16-bit pack of the pair, lo = RNE pack of the residual
+                u32x4_t fr[2];
+                split_p<DT, 2>(x, fr);
+                qf[mb][0][ks] = fr[0];
+                qf[mb][NQ - 1][ks] = fr[1];
             } else {
                 const uint16_t* qp = static_cast<const uint16_t*>(p.q) + qoff + 32 * ks;
                 qf[mb][0][ks] = ok ? load16(qp) : u32x4_t{0, 0, 0, 0};
@@ -304,11 +309,7 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
     }
 
     const char* ring_bytes = &ring[0];
-    if constexpr (TS == 1) {  // (TS = 2 issued tile 0 with the query rows)
-        issue(t_begin, 0);
-        if (ntiles > 1) issue(t_begin + TILE_T, 1);
-    }
-    int buf = 0;
+    int buf = 0;  // (tiles 0 and 1 were issued with the query loads)
     for (int it = 0; it < ntiles; it++) {
         if (it == 2) MUGEN_TRACE(6);
         if (NBUF > 2 && it + 1 < ntiles) vm_wait<DPW>();
