@@ -241,15 +241,13 @@ static size_t gqa_ws(const mugen_attn_gqa_decode_args* a, int chunk, int* splits
 }
 
 // MLA kernel variant (mla_decode.hip): fp32 q or at most 64 query rows ->
-// 1 (64-row workgroups, 16 rows per wave); decode (q_len 1) -> 5 (warp-
-// specialised, two waves per SIMD); verify (q_len > 1) -> 3 (64-row
-// workgroups, 32 rows per wave, 64-token tiles), which keeps more MFMA work
-// per LDS byte where the 10+ row blocks per sequence make the kernel
-// compute-bound.  MUGEN_ATTN_MLA_VARIANT=1..5 overrides the choice (kernel
-// comparisons); variants 2-5 need 16-bit q.
+// 1 (64-row workgroups, 16 rows per wave); otherwise 5 (warp-specialised,
+// two waves per SIMD), which measures faster than the one-wave-per-SIMD
+// variants for both decode and verify.  MUGEN_ATTN_MLA_VARIANT=1..5
+// overrides the choice (kernel comparisons); variants 2-5 need 16-bit q.
 static int mla_variant(const mugen_attn_mla_decode_args* a) {
     const int R = a->q_len * a->n_heads;
-    const int dflt = (R <= 64 || a->q_dtype == DT_F32) ? 1 : (a->q_len == 1 ? 5 : 3);
+    const int dflt = (R <= 64 || a->q_dtype == DT_F32) ? 1 : 5;
     if (const char* e = getenv("MUGEN_ATTN_MLA_VARIANT")) {
         const int v = atoi(e);
         if (v == 1 || (v >= 2 && v <= 5 && a->q_dtype != DT_F32)) return v;
