@@ -192,6 +192,73 @@ int mugen_attn_mla_decode(const mugen_attn_mla_decode_args* args, void* workspac
                           size_t workspace_bytes, void* stream);
 
 /*
+ * MLA absorption and up-projection: the rest of cpu_mla_attention
+ * (transformer.cpp:2539-2623) around the latent core above, so that
+ *   mugen_attn_mla_absorb -> mugen_attn_mla_decode (q F32) -> mugen_attn_mla_project
+ * computes the reference operator from its own inputs (f16 q_data, the
+ * layer's attn_k_b / attn_v_b weights, the latent cache) to its f16 output.
+ *
+ * Weights keep the reference's GGUF block encodings, dequantised on the fly
+ * exactly as dequant_weight_row (transformer.cpp:2488-2534) does; the ids
+ * are GGML's (src/model/ggml_types.h:12-20):
+ *   F16  : kv_rank halfs per row;
+ *   Q8_0 : kv_rank/32 blocks of 34 bytes, f16 scale + 32 int8 (w = s*q);
+ *   Q4_0 : kv_rank/32 blocks of 18 bytes, f16 scale + 16 bytes; element j
+ *          of a block is low nibble of byte j (j < 16) or high nibble of
+ *          byte j-16, minus 8, times s.
+ * Weight rows start at row * row_bytes (no padding), byte-addressed.
+ */
+typedef enum {
+    MUGEN_ATTN_W_F16 = 1,
+    MUGEN_ATTN_W_Q4_0 = 2,
+    MUGEN_ATTN_W_Q8_0 = 8
+} mugen_attn_wtype;
+
+/*
+ * q_absorbed = q_nope x k_b, then q_rope appended (transformer.cpp:2556-2573):
+ *   q      [rows][n_heads][nope_dim + rope_dim]  F16 (the reference's q_data)
+ *   w_kb   attn_k_b: n_heads*nope_dim rows of kv_rank values (w_type)
+ *   q_abs  [rows][n_heads][kv_rank + rope_dim]   F32 (fp32 sums, as the
+ *          reference's float q_absorbed) or BF16
+ *   q_abs[r][h][d] = sum_i q[r][h][i] * k_b[h*nope_dim + i][d], d < kv_rank
+ * rows = batch * q_len.  Supported: nope_dim 128, rope_dim 64, kv_rank 512.
+ */
+typedef struct mugen_attn_mla_absorb_args {
+    const void* q;
+    const void* w_kb;
+    void* q_abs;
+    int32_t rows;
+    int32_t n_heads;
+    int32_t nope_dim;
+    int32_t rope_dim;
+    int32_t kv_rank;
+    int32_t w_type;    /* mugen_attn_wtype */
+    int32_t out_dtype; /* F32 or BF16 */
+} mugen_attn_mla_absorb_args;
+int mugen_attn_mla_absorb(const mugen_attn_mla_absorb_args* args, void* stream);
+
+/*
+ * out_h = out_comp x v_b^T (transformer.cpp:2610-2620):
+ *   o      [rows][n_heads][kv_rank]         F32 (mugen_attn_mla_decode's out)
+ *   w_vb   attn_v_b: n_heads*v_head_dim rows of kv_rank values (w_type)
+ *   out    [rows][n_heads][v_head_dim]      F16 (the reference's output) or F32
+ *   out[r][h][j] = sum_d o[r][h][d] * v_b[h*v_head_dim + j][d]
+ * Supported: kv_rank 512, v_head_dim 128.
+ */
+typedef struct mugen_attn_mla_project_args {
+    const void* o;
+    const void* w_vb;
+    void* out;
+    int32_t rows;
+    int32_t n_heads;
+    int32_t kv_rank;
+    int32_t v_head_dim;
+    int32_t w_type;    /* mugen_attn_wtype */
+    int32_t out_dtype; /* F16 or F32 */
+} mugen_attn_mla_project_args;
+int mugen_attn_mla_project(const mugen_attn_mla_project_args* args, void* stream);
+
+/*
  * scatter_kv: dst[offset + i] = src[i], i < count, 16-bit elements.
  * Replaces scatter_kv (kernel_sources.h:3018-3028) / make_scatter_kv_dp
  * (transformer.cpp:872-886): the per-token append of K/V rows or latent
@@ -211,7 +278,7 @@ const char* mugen_attn_version(void);
  * mugen_attn_timing_read synchronises on the recorded events and returns
  * the summed milliseconds and launch count of the kernel named `kernel`
  * ("gqa_decode", "gqa_decode_combine", "gqa_prefill", "mla_decode",
- * "mla_decode_combine", "scatter_kv").
+ * "mla_decode_combine", "mla_absorb", "mla_project", "scatter_kv").
  */
 int mugen_attn_timing_enable(int enable);
 int mugen_attn_timing_read(const char* kernel, double* total_ms, int64_t* launches);

@@ -18,6 +18,7 @@ E_WORKSPACE = -3
 E_HIP = -4
 
 F32, F16, BF16 = 0, 1, 2
+W_F16, W_Q4_0, W_Q8_0 = 1, 2, 8  # weight encodings (GGML type ids)
 
 # every symbol include/mugen_attn.h declares
 EXPORTS = (
@@ -26,6 +27,8 @@ EXPORTS = (
     "mugen_attn_gqa_prefill",
     "mugen_attn_mla_decode_workspace_size",
     "mugen_attn_mla_decode",
+    "mugen_attn_mla_absorb",
+    "mugen_attn_mla_project",
     "mugen_attn_scatter_kv",
     "mugen_attn_last_error",
     "mugen_attn_version",
@@ -67,6 +70,22 @@ class MlaDecodeArgs(ctypes.Structure):
     ]
 
 
+class MlaAbsorbArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", _vp), ("w_kb", _vp), ("q_abs", _vp),
+        ("rows", _i32), ("n_heads", _i32), ("nope_dim", _i32), ("rope_dim", _i32), ("kv_rank", _i32),
+        ("w_type", _i32), ("out_dtype", _i32),
+    ]
+
+
+class MlaProjectArgs(ctypes.Structure):
+    _fields_ = [
+        ("o", _vp), ("w_vb", _vp), ("out", _vp),
+        ("rows", _i32), ("n_heads", _i32), ("kv_rank", _i32), ("v_head_dim", _i32),
+        ("w_type", _i32), ("out_dtype", _i32),
+    ]
+
+
 class MugenAttnError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"[{code}] {msg}")
@@ -96,6 +115,10 @@ def lib() -> ctypes.CDLL:
         L.mugen_attn_mla_decode_workspace_size.restype = ctypes.c_size_t
         L.mugen_attn_mla_decode.argtypes = [ctypes.POINTER(MlaDecodeArgs), _vp, ctypes.c_size_t, _vp]
         L.mugen_attn_mla_decode.restype = ctypes.c_int
+        L.mugen_attn_mla_absorb.argtypes = [ctypes.POINTER(MlaAbsorbArgs), _vp]
+        L.mugen_attn_mla_absorb.restype = ctypes.c_int
+        L.mugen_attn_mla_project.argtypes = [ctypes.POINTER(MlaProjectArgs), _vp]
+        L.mugen_attn_mla_project.restype = ctypes.c_int
         L.mugen_attn_scatter_kv.argtypes = [_vp, _vp, ctypes.c_uint64, ctypes.c_uint64, _vp]
         L.mugen_attn_scatter_kv.restype = ctypes.c_int
         L.mugen_attn_last_error.restype = ctypes.c_char_p

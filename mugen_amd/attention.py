@@ -9,6 +9,9 @@ libmugen_attn.so.  Operator names follow the reference's seams:
                               (transformer.cpp:2441-2485, kernel_sources.h:2900-2999)
   flash_prefill_attention  <- flash_prefill_attention (kernel_sources.h:2769-2896)
   mla_attention            <- cpu_mla_attention latent core (transformer.cpp:2576-2608)
+  mla_absorb / mla_project <- cpu_mla_attention absorption and up-projection
+                              (transformer.cpp:2556-2573, 2610-2620)
+  mla_attention_full       <- cpu_mla_attention (transformer.cpp:2539-2623)
   scatter_kv               <- scatter_kv (kernel_sources.h:3018-3028)
 """
 from __future__ import annotations
@@ -167,6 +170,73 @@ def mla_attention(q: torch.Tensor, latent: torch.Tensor, seq_lens: torch.Tensor,
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _capi.check(L.mugen_attn_mla_decode(ctypes.byref(a), _ptr(workspace), ws_bytes, _stream(q.device)))
     return out
+
+
+_WT = {"f16": _capi.W_F16, "q8_0": _capi.W_Q8_0, "q4_0": _capi.W_Q4_0}
+
+
+def _wtype(w: torch.Tensor, w_type) -> int:
+    if w_type is None:
+        if w.dtype != torch.float16:
+            raise TypeError("block-encoded weights need w_type ('q8_0' / 'q4_0')")
+        return _capi.W_F16
+    return _WT[w_type] if isinstance(w_type, str) else int(w_type)
+
+
+def mla_absorb(q: torch.Tensor, w_kb: torch.Tensor, w_type=None, *, out: torch.Tensor | None = None,
+               out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """q_abs = [q_nope . k_b | q_rope] per head (transformer.cpp:2556-2573).
+
+    q f16 [..., H, 192]; w_kb = attn_k_b, H*128 rows of 512 in the GGML
+    encoding w_type ('f16' as a float16 tensor, 'q8_0' / 'q4_0' as uint8
+    bytes).  Returns [..., H, 576] in out_dtype (F32 or BF16)."""
+    _need_cuda(q, w_kb)
+    if q.dtype != torch.float16 or q.shape[-1] != 192:
+        raise ValueError("q must be float16 [..., H, 192]")
+    H = q.shape[-2]
+    rows = q.numel() // (H * 192)
+    if out is None:
+        out = torch.empty((*q.shape[:-1], 576), dtype=out_dtype, device=q.device)
+    a = _capi.MlaAbsorbArgs()
+    a.q, a.w_kb, a.q_abs = q.data_ptr(), w_kb.data_ptr(), out.data_ptr()
+    a.rows, a.n_heads, a.nope_dim, a.rope_dim, a.kv_rank = rows, H, 128, 64, 512
+    a.w_type, a.out_dtype = _wtype(w_kb, w_type), _dt(out.dtype)
+    _capi.check(_capi.lib().mugen_attn_mla_absorb(ctypes.byref(a), _stream(q.device)))
+    return out
+
+
+def mla_project(o: torch.Tensor, w_vb: torch.Tensor, w_type=None, *, out: torch.Tensor | None = None,
+                out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """out = o . v_b^T per head (transformer.cpp:2610-2620).
+
+    o f32 [..., H, 512]; w_vb = attn_v_b, H*128 rows of 512 (w_type as in
+    mla_absorb).  Returns [..., H, 128] in out_dtype (F16 or F32)."""
+    _need_cuda(o, w_vb)
+    if o.dtype != torch.float32 or o.shape[-1] != 512:
+        raise ValueError("o must be float32 [..., H, 512]")
+    H = o.shape[-2]
+    rows = o.numel() // (H * 512)
+    if out is None:
+        out = torch.empty((*o.shape[:-1], 128), dtype=out_dtype, device=o.device)
+    a = _capi.MlaProjectArgs()
+    a.o, a.w_vb, a.out = o.data_ptr(), w_vb.data_ptr(), out.data_ptr()
+    a.rows, a.n_heads, a.kv_rank, a.v_head_dim = rows, H, 512, 128
+    a.w_type, a.out_dtype = _wtype(w_vb, w_type), _dt(out.dtype)
+    _capi.check(_capi.lib().mugen_attn_mla_project(ctypes.byref(a), _stream(o.device)))
+    return out
+
+
+def mla_attention_full(q: torch.Tensor, w_kb: torch.Tensor, w_vb: torch.Tensor, latent: torch.Tensor,
+                       seq_lens: torch.Tensor, max_seq_len: int | None = None, w_type=None, *,
+                       scale: float = 1.0 / math.sqrt(192.0), num_splits: int = 0,
+                       seq_lens_host=None) -> torch.Tensor:
+    """cpu_mla_attention end to end (transformer.cpp:2539-2623): f16 q
+    [B,q_len,H,192] and f16 latent [B,max_T,576] in, f16 [B,q_len,H,128]
+    out, fp32 arithmetic throughout (the latent core runs with an fp32 q)."""
+    qa = mla_absorb(q, w_kb, w_type)
+    o = mla_attention(qa, latent, seq_lens, max_seq_len, scale=scale, num_splits=num_splits,
+                      seq_lens_host=seq_lens_host)
+    return mla_project(o, w_vb, w_type)
 
 
 # ------------------------------------------------------------------ scatter_kv

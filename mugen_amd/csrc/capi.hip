@@ -466,6 +466,53 @@ int mugen_attn_mla_decode(const mugen_attn_mla_decode_args* a, void* ws, size_t 
     return hip_status(e, "mla_decode launch");
 }
 
+static bool is_wtype(int w) { return w == W_F16 || w == W_Q8_0 || w == W_Q4_0; }
+
+// weight rows: F16 rows are read 16 bytes at a time, block rows 2 at a time
+static bool w_aligned(const void* w, int w_type) {
+    return ((uintptr_t)w & (w_type == W_F16 ? 15 : 1)) == 0;
+}
+
+int mugen_attn_mla_absorb(const mugen_attn_mla_absorb_args* a, void* stream) {
+    if (!a) return fail(MUGEN_ATTN_E_INVALID, "mla_absorb: null args");
+    if (a->rows < 0 || a->n_heads <= 0) return fail(MUGEN_ATTN_E_INVALID, "mla_absorb: bad rows/n_heads");
+    if (a->nope_dim != 128 || a->rope_dim != 64 || a->kv_rank != 512)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_absorb: nope/rope/kv_rank %d/%d/%d (supported: 128/64/512)",
+                    a->nope_dim, a->rope_dim, a->kv_rank);
+    if (!is_wtype(a->w_type)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_absorb: w_type %d", a->w_type);
+    if (a->out_dtype != DT_F32 && a->out_dtype != DT_BF16)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_absorb: out_dtype must be F32 or BF16");
+    if (a->rows == 0) return MUGEN_ATTN_OK;
+    if (!a->q || !a->w_kb || !a->q_abs) return fail(MUGEN_ATTN_E_INVALID, "mla_absorb: null pointer");
+    if (((uintptr_t)a->q & 1) || ((uintptr_t)a->q_abs & 3) || !w_aligned(a->w_kb, a->w_type))
+        return fail(MUGEN_ATTN_E_INVALID, "mla_absorb: misaligned q/q_abs/w_kb");
+    if ((int64_t)a->rows * a->n_heads > (1 << 24))
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_absorb: rows*n_heads too large");
+    MlaProjParams p{a->q, a->w_kb, a->q_abs, a->rows, a->n_heads};
+    return hip_status(launch_mla_absorb(p, a->w_type, a->out_dtype, static_cast<hipStream_t>(stream), active_timer()),
+                      "mla_absorb launch");
+}
+
+int mugen_attn_mla_project(const mugen_attn_mla_project_args* a, void* stream) {
+    if (!a) return fail(MUGEN_ATTN_E_INVALID, "mla_project: null args");
+    if (a->rows < 0 || a->n_heads <= 0) return fail(MUGEN_ATTN_E_INVALID, "mla_project: bad rows/n_heads");
+    if (a->kv_rank != 512 || a->v_head_dim != 128)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_project: kv_rank/v_head_dim %d/%d (supported: 512/128)",
+                    a->kv_rank, a->v_head_dim);
+    if (!is_wtype(a->w_type)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_project: w_type %d", a->w_type);
+    if (a->out_dtype != DT_F32 && a->out_dtype != DT_F16)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_project: out_dtype must be F16 or F32");
+    if (a->rows == 0) return MUGEN_ATTN_OK;
+    if (!a->o || !a->w_vb || !a->out) return fail(MUGEN_ATTN_E_INVALID, "mla_project: null pointer");
+    if (((uintptr_t)a->o & 15) || ((uintptr_t)a->out & 3) || !w_aligned(a->w_vb, a->w_type))
+        return fail(MUGEN_ATTN_E_INVALID, "mla_project: misaligned o/out/w_vb");
+    if ((int64_t)a->rows * a->n_heads > (1 << 24))
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_project: rows*n_heads too large");
+    MlaProjParams p{a->o, a->w_vb, a->out, a->rows, a->n_heads};
+    return hip_status(launch_mla_project(p, a->w_type, a->out_dtype, static_cast<hipStream_t>(stream), active_timer()),
+                      "mla_project launch");
+}
+
 int mugen_attn_scatter_kv(const void* src, void* dst, uint64_t offset, uint64_t count, void* stream) {
     if (count == 0) return MUGEN_ATTN_OK;
     if (!src || !dst) return fail(MUGEN_ATTN_E_INVALID, "scatter_kv: null pointer");

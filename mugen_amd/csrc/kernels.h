@@ -77,6 +77,18 @@ int mla_tile_tokens(int variant);
 hipError_t launch_mla_decode(const MlaParams& p, int variant, int q_dt, int lat_dt, int out_dt,
                              hipStream_t st, KernelTimer* t);
 
+// MLA absorption / up-projection (mla_proj.hip)
+enum { W_F16 = MUGEN_ATTN_W_F16, W_Q4_0 = MUGEN_ATTN_W_Q4_0, W_Q8_0 = MUGEN_ATTN_W_Q8_0 };
+struct MlaProjParams {
+    const void* in;   // absorb: q f16 [rows][H][nope+rope]; project: o f32 [rows][H][kv_rank]
+    const void* w;    // weight rows in the GGML block encoding
+    void* out;        // absorb: q_abs [rows][H][kv_rank+rope]; project: [rows][H][v_head]
+    int rows;
+    int H;
+};
+hipError_t launch_mla_absorb(const MlaProjParams& p, int w_type, int out_dt, hipStream_t st, KernelTimer* t);
+hipError_t launch_mla_project(const MlaProjParams& p, int w_type, int out_dt, hipStream_t st, KernelTimer* t);
+
 hipError_t launch_scatter_kv(const uint16_t* src, uint16_t* dst, uint64_t offset, uint64_t count,
                              hipStream_t st, KernelTimer* t);
 

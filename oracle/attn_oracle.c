@@ -26,6 +26,11 @@
  *                            multi-query (verify) rows follow the per-token
  *                            call seq_len = start_position + t + 1
  *                            (transformer.cpp:1325-1337).
+ *   oracle_dequant_row    <- dequant_weight_row, transformer.cpp:2488-2534
+ *   oracle_mla_absorb     <- q_absorbed = q_nope x k_b, transformer.cpp:2563-2573
+ *   oracle_mla_project    <- out_h = out_comp x v_b^T, transformer.cpp:2610-2620
+ *   (absorb + oracle_mla_attention + project = cpu_mla_attention,
+ *    transformer.cpp:2539-2623)
  *   oracle_scatter_kv     <- scatter_kv, src/metal/kernel_sources.h:3018-3028
  *
  * The summation orders above are kept (sequential fp32 sums, expf, divide
@@ -366,6 +371,105 @@ void oracle_mla_attention_f64(const float* q, const float* latent, const int32_t
     MLA_BODY(double, exp)
 }
 #undef OUT_T
+
+/* ------------------------------------------------------------------ */
+/* MLA absorption / up-projection (the rest of cpu_mla_attention)       */
+/* ------------------------------------------------------------------ */
+/*
+ * oracle_dequant_row <- dequant_weight_row, transformer.cpp:2488-2534.
+ * Weight types use the GGML ids of src/model/ggml_types.h:12-20:
+ *   F16  (1): K little-endian halfs per row;
+ *   Q8_0 (8): K/32 blocks of 34 bytes = f16 scale s + 32 int8 q; w = s * q;
+ *   Q4_0 (2): K/32 blocks of 18 bytes = f16 scale s + 16 bytes; element j
+ *             of a block is (low nibble of byte j) - 8 for j < 16 and
+ *             (high nibble of byte j-16) - 8 for j >= 16, times s.
+ * Any other type zero-fills the row (transformer.cpp:2530-2533).
+ */
+static size_t wrow_bytes(int type, int K) {
+    if (type == 1) return (size_t)K * 2;
+    if (type == 8) return (size_t)(K / 32) * 34;
+    if (type == 2) return (size_t)(K / 32) * 18;
+    return 0;
+}
+void oracle_dequant_row(const uint8_t* buf, int type, int64_t row, int K, float* out) {
+    const uint8_t* rp = buf + (size_t)row * wrow_bytes(type, K);
+    if (type == 1) {
+        for (int i = 0; i < K; i++) {
+            uint16_t h;
+            memcpy(&h, rp + 2 * i, 2);
+            out[i] = oracle_f16_to_f32(h);
+        }
+    } else if (type == 8) {
+        for (int b = 0; b < K / 32; b++) {
+            const uint8_t* blk = rp + (size_t)b * 34;
+            uint16_t sh;
+            memcpy(&sh, blk, 2);
+            float sc = oracle_f16_to_f32(sh);
+            for (int j = 0; j < 32; j++) out[b * 32 + j] = sc * (float)(int8_t)blk[2 + j];
+        }
+    } else if (type == 2) {
+        for (int b = 0; b < K / 32; b++) {
+            const uint8_t* blk = rp + (size_t)b * 18;
+            uint16_t sh;
+            memcpy(&sh, blk, 2);
+            float sc = oracle_f16_to_f32(sh);
+            for (int j = 0; j < 16; j++) {
+                out[b * 32 + j] = (float)((blk[2 + j] & 0x0F) - 8) * sc;
+                out[b * 32 + j + 16] = (float)((blk[2 + j] >> 4) - 8) * sc;
+            }
+        }
+    } else {
+        memset(out, 0, sizeof(float) * (size_t)K);
+    }
+}
+
+/*
+ * oracle_mla_absorb <- transformer.cpp:2563-2573: per query row r and head
+ * h, q_abs[d] = sum_i q_nope[i] * W_kb[h*nope + i][d] over i in order
+ * (terms with q_nope[i] == 0 skipped, as there), d < kv_rank; the q_rope
+ * part is appended unchanged.  q [rows][H][nope + rope] (f16 values),
+ * q_abs [rows][H][kv_rank + rope] fp32.
+ */
+void oracle_mla_absorb(const float* q, const uint8_t* w_kb, int w_type, float* q_abs, int rows, int H,
+                       int nope, int rope, int kv_rank) {
+    float* wrow = (float*)malloc(sizeof(float) * (size_t)kv_rank);
+    for (int64_t rh = 0; rh < (int64_t)rows * H; rh++) {
+        int h = (int)(rh % H);
+        const float* qn = q + rh * (nope + rope);
+        float* qa = q_abs + rh * (kv_rank + rope);
+        for (int d = 0; d < kv_rank; d++) qa[d] = 0.f;
+        for (int i = 0; i < nope; i++) {
+            float qi = qn[i];
+            if (qi == 0.0f) continue;
+            oracle_dequant_row(w_kb, w_type, (int64_t)h * nope + i, kv_rank, wrow);
+            for (int d = 0; d < kv_rank; d++) qa[d] += qi * wrow[d];
+        }
+        for (int j = 0; j < rope; j++) qa[kv_rank + j] = qn[nope + j];
+    }
+    free(wrow);
+}
+
+/*
+ * oracle_mla_project <- transformer.cpp:2610-2620: out[r][h][j] =
+ * sum_d o[r][h][d] * W_vb[h*v_head + j][d] (d in order), rounded to f16 as
+ * the reference's static_cast<f16> does; out_f16 holds the rounded values
+ * as floats.  o [rows][H][kv_rank] fp32.
+ */
+void oracle_mla_project(const float* o, const uint8_t* w_vb, int w_type, float* out_f16, int rows, int H,
+                        int kv_rank, int v_head) {
+    float* wrow = (float*)malloc(sizeof(float) * (size_t)kv_rank);
+    for (int64_t rh = 0; rh < (int64_t)rows * H; rh++) {
+        int h = (int)(rh % H);
+        const float* oc = o + rh * kv_rank;
+        for (int j = 0; j < v_head; j++) {
+            oracle_dequant_row(w_vb, w_type, (int64_t)h * v_head + j, kv_rank, wrow);
+            float val = 0.0f;
+            for (int d = 0; d < kv_rank; d++) val += oc[d] * wrow[d];
+            out_f16[rh * v_head + j] = oracle_f16_to_f32(oracle_f32_to_f16(val));
+        }
+    }
+    free(wrow);
+}
 
 /* ------------------------------------------------------------------ */
 /* scatter_kv: dst[offset + i] = src[i] for i < count (16-bit elements) */

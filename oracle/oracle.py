@@ -50,6 +50,9 @@ def lib():
         L.oracle_mla_attention_f32.argtypes = [P, P, P, P, i32, i32, i32, i32, i32, i64, f32, i32]
         L.oracle_mla_attention_f64.argtypes = [P, P, P, P, i32, i32, i32, i32, i32, i64, f32]
         L.oracle_scatter_kv.argtypes = [P, P, i64, i64]
+        L.oracle_dequant_row.argtypes = [P, i32, i64, i32, P]
+        L.oracle_mla_absorb.argtypes = [P, P, i32, P, i32, i32, i32, i32, i32]
+        L.oracle_mla_project.argtypes = [P, P, i32, P, i32, i32, i32, i32]
         L.oracle_num_threads.restype = ctypes.c_int
         _lib = L
     return _lib
@@ -150,6 +153,62 @@ def mla_attention(q, latent, seq_lens, q_len, H, scale, kv_rank=512, rope=64, se
         lib().oracle_mla_attention_f32(_p(q), _p(lat), _p(sl), _p(out), B, q_len, H, kv_rank, rope,
                                        seq_stride, scale, nthreads)
     return out
+
+
+# GGML weight type ids (src/model/ggml_types.h:12-20) accepted by the MLA
+# absorption / up-projection
+W_F16, W_Q4_0, W_Q8_0 = 1, 2, 8
+
+
+def wrow_bytes(w_type: int, K: int) -> int:
+    return {W_F16: 2 * K, W_Q8_0: K // 32 * 34, W_Q4_0: K // 32 * 18}[w_type]
+
+
+def dequant_rows(w: np.ndarray, w_type: int, K: int) -> np.ndarray:
+    """dequant_weight_row (transformer.cpp:2488-2534) applied to every row
+    of a [rows, row_bytes] uint8 buffer; returns [rows, K] fp32."""
+    w = np.ascontiguousarray(w, np.uint8)
+    rows = w.shape[0]
+    out = np.empty((rows, K), np.float32)
+    for r in range(rows):
+        lib().oracle_dequant_row(_p(w), w_type, r, K, _p(out[r]))
+    return out
+
+
+def mla_absorb(q, w_kb, w_type, H, nope=128, rope=64, kv_rank=512):
+    """q_absorbed = q_nope x k_b (transformer.cpp:2563-2573) ++ q_rope.
+    q [..., H, nope+rope] (f16 values as float32); w_kb [H*nope, row_bytes]
+    uint8.  Returns [..., H, kv_rank+rope] fp32."""
+    q = np.ascontiguousarray(q, np.float32)
+    lead = q.shape[:-2]
+    rows = int(np.prod(lead)) if lead else 1
+    out = np.empty(lead + (H, kv_rank + rope), np.float32)
+    lib().oracle_mla_absorb(_p(q), _p(np.ascontiguousarray(w_kb, np.uint8)), w_type, _p(out), rows, H, nope, rope,
+                            kv_rank)
+    return out
+
+
+def mla_project(o, w_vb, w_type, H, kv_rank=512, v_head=128):
+    """out_h = out_comp x v_b^T rounded to f16 (transformer.cpp:2610-2620).
+    o [..., H, kv_rank] fp32; w_vb [H*v_head, row_bytes] uint8.  Returns
+    [..., H, v_head] fp32 holding f16 values."""
+    o = np.ascontiguousarray(o, np.float32)
+    lead = o.shape[:-2]
+    rows = int(np.prod(lead)) if lead else 1
+    out = np.empty(lead + (H, v_head), np.float32)
+    lib().oracle_mla_project(_p(o), _p(np.ascontiguousarray(w_vb, np.uint8)), w_type, _p(out), rows, H, kv_rank,
+                             v_head)
+    return out
+
+
+def mla_full(q, w_kb, w_vb, w_type, latent, seq_lens, q_len, H, scale, nope=128, rope=64, kv_rank=512,
+             v_head=128, seq_stride=None, nthreads=1):
+    """cpu_mla_attention (transformer.cpp:2539-2623): absorb, latent core,
+    up-project.  q [B,q_len,H,nope+rope]; returns [B,q_len,H,v_head] (f16
+    values as float32)."""
+    qa = mla_absorb(q, w_kb, w_type, H, nope, rope, kv_rank)
+    o = mla_attention(qa, latent, seq_lens, q_len, H, scale, kv_rank, rope, seq_stride, nthreads=nthreads)
+    return mla_project(o, w_vb, w_type, H, kv_rank, v_head)
 
 
 def scatter_kv(src_bits, dst_bits, offset, count):

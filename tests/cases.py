@@ -115,3 +115,47 @@ def say(msg):
 def golden_path(name):
     import os
     return os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name)
+
+
+def make_weights(seed, rows, K, w_type, std=0.05):
+    """A [rows, row_bytes] uint8 weight buffer in a GGML encoding (F16, Q8_0,
+    Q4_0; transformer.cpp:2488-2534), seeded, with dequantised weights of
+    rms ~std as a quantiser would produce from N(0, std) weights: block
+    scales std/rms(quants) times a factor in [0.5, 1.5), rounded to f16,
+    quants uniform over their range (Q8_0 rms ~74, Q4_0 rms ~4.6)."""
+    if w_type == O.W_F16:
+        _, bits = O.round_to(O.randn(seed, (rows, K), 0.0, std), F16)
+        return np.ascontiguousarray(bits.view(np.uint8).reshape(rows, 2 * K))
+    nb = K // 32
+    qrms = 73.9 if w_type == O.W_Q8_0 else 4.61
+    jit = O.randint(seed, rows * nb, 0, 1023).astype(np.float32).reshape(rows, nb) / 1024 + 0.5
+    _, sbits = O.round_to(jit * np.float32(std / qrms), F16)
+    blk = 34 if w_type == O.W_Q8_0 else 18
+    out = np.zeros((rows, nb, blk), np.uint8)
+    out[:, :, 0:2] = sbits.reshape(rows, nb, 1).view(np.uint8).reshape(rows, nb, 2)
+    if w_type == O.W_Q8_0:
+        qs = O.randint(seed + 1, rows * nb * 32, -128, 127).astype(np.int8)
+        out[:, :, 2:] = qs.view(np.uint8).reshape(rows, nb, 32)
+    else:
+        qs = O.randint(seed + 1, rows * nb * 16, 0, 255).astype(np.uint8)
+        out[:, :, 2:] = qs.reshape(rows, nb, 16)
+    return np.ascontiguousarray(out.reshape(rows, nb * blk))
+
+
+def mla_full_case(seed, B, q_len, H, seq_lens, w_type, max_T=None, nope=128, rope=64, kv_rank=512, v_head=128):
+    """cpu_mla_attention inputs: f16 q [B,q_len,H,nope+rope], f16 latent,
+    k_b [H*nope, row], v_b [H*v_head, row] in w_type."""
+    seq_lens = np.asarray(seq_lens, np.int32)
+    if max_T is None:
+        max_T = int(seq_lens.max()) if seq_lens.size else 1
+    max_T = max(max_T, 1)
+    q, qb = O.round_to(O.randn(seed, (B, q_len, H, nope + rope)), F16)
+    lat, latb = O.round_to(O.randn(seed + 1000, (B, max_T, kv_rank + rope), 0.0, 0.5), F16)
+    return dict(B=B, q_len=q_len, H=H, max_T=max_T, seq_lens=seq_lens, w_type=w_type, q=q, qb=qb, lat=lat,
+                latb=latb, w_kb=make_weights(seed + 2000, H * nope, kv_rank, w_type),
+                w_vb=make_weights(seed + 3000, H * v_head, kv_rank, w_type))
+
+
+def mla_full_ref(c, nthreads=0):
+    return O.mla_full(c["q"], c["w_kb"], c["w_vb"], c["w_type"], c["lat"], c["seq_lens"], c["q_len"], c["H"],
+                      MLA_SCALE, nthreads=nthreads)

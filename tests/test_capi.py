@@ -157,3 +157,30 @@ def test_cpp_adapter_maps_status_to_expected(tmp_path):
         out = subprocess.run([str(exe)], capture_output=True, text=True)
         assert out.returncode == 0, out
         assert out.stdout.strip()
+
+
+def test_mla_absorb_project_validation():
+    L = _capi.lib()
+    a = _capi.MlaAbsorbArgs()
+    a.q = a.w_kb = a.q_abs = 0x1000
+    a.rows, a.n_heads, a.nope_dim, a.rope_dim, a.kv_rank = 4, 16, 128, 64, 512
+    a.w_type, a.out_dtype = _capi.W_Q8_0, _capi.F32
+    for field, val, code in [("nope_dim", 64, _capi.E_UNSUPPORTED), ("w_type", 3, _capi.E_UNSUPPORTED),
+                             ("out_dtype", _capi.F16, _capi.E_UNSUPPORTED), ("q", 0, _capi.E_INVALID),
+                             ("q", 0x1001, _capi.E_INVALID), ("n_heads", 0, _capi.E_INVALID)]:
+        b = _capi.MlaAbsorbArgs.from_buffer_copy(a)
+        setattr(b, field, val)
+        assert L.mugen_attn_mla_absorb(ctypes.byref(b), None) == code, field
+    b = _capi.MlaAbsorbArgs.from_buffer_copy(a)
+    b.w_type, b.w_kb = _capi.W_F16, 0x1002          # f16 rows are read 16 bytes at a time
+    assert L.mugen_attn_mla_absorb(ctypes.byref(b), None) == _capi.E_INVALID
+    b.rows = 0
+    assert L.mugen_attn_mla_absorb(ctypes.byref(b), None) == _capi.OK
+    p = _capi.MlaProjectArgs()
+    p.o = p.w_vb = p.out = 0x1000
+    p.rows, p.n_heads, p.kv_rank, p.v_head_dim, p.w_type, p.out_dtype = 4, 16, 512, 128, _capi.W_Q4_0, _capi.F16
+    for field, val, code in [("v_head_dim", 64, _capi.E_UNSUPPORTED), ("out_dtype", _capi.BF16, _capi.E_UNSUPPORTED),
+                             ("o", 0x1008, _capi.E_INVALID), ("w_vb", 0, _capi.E_INVALID)]:
+        b = _capi.MlaProjectArgs.from_buffer_copy(p)
+        setattr(b, field, val)
+        assert L.mugen_attn_mla_project(ctypes.byref(b), None) == code, field

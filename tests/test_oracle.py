@@ -232,3 +232,61 @@ def test_golden_fixtures_reproduce():
     out = O.mla_attention(fx["q"], lat, fx["seq_lens"], int(fx["q_len"]), int(fx["H"]), C.MLA_SCALE,
                           seq_stride=int(fx["max_T"]) * 576)
     np.testing.assert_array_equal(out, fx["out_f32"])
+
+
+def test_dequant_known_answers():
+    # F16: the row's halfs widened exactly
+    vals = np.array([1.0, -2.5, 0.000123, 65504.0] * 8, np.float16)
+    out = O.dequant_rows(vals.view(np.uint8).reshape(1, -1), O.W_F16, 32)
+    np.testing.assert_array_equal(out[0], vals.astype(np.float32))
+    # Q8_0: scale 0.5 (f16 0x3800) times the int8 quants
+    blk = np.zeros(34, np.uint8)
+    blk[0:2] = np.array([0x3800], np.uint16).view(np.uint8)
+    q = np.arange(-16, 16, dtype=np.int8) * 4
+    blk[2:] = q.view(np.uint8)
+    out = O.dequant_rows(blk.reshape(1, 34), O.W_Q8_0, 32)
+    np.testing.assert_array_equal(out[0], 0.5 * q.astype(np.float32))
+    # Q4_0: scale 2 (0x4000); byte j = (15 - j) << 4 | j -> element j is the
+    # low nibble (j - 8) * 2, element j + 16 the high nibble (7 - j) * 2
+    blk = np.zeros(18, np.uint8)
+    blk[0:2] = np.array([0x4000], np.uint16).view(np.uint8)
+    j = np.arange(16)
+    blk[2:] = ((15 - j) << 4 | j).astype(np.uint8)
+    out = O.dequant_rows(blk.reshape(1, 18), O.W_Q4_0, 32)
+    np.testing.assert_array_equal(out[0, :16], ((j - 8) * 2).astype(np.float32))
+    np.testing.assert_array_equal(out[0, 16:], ((7 - j) * 2).astype(np.float32))
+    # an unsupported type zero-fills (transformer.cpp:2530-2533)
+    np.testing.assert_array_equal(O.dequant_rows(blk.reshape(1, 18), 12, 32), np.zeros((1, 32), np.float32))
+
+
+@pytest.mark.parametrize("w_type", [O.W_F16, O.W_Q8_0, O.W_Q4_0])
+def test_absorb_and_project_vs_numpy(w_type):
+    H, nope, rope, kr, vh, rows = 3, 128, 64, 512, 128, 2
+    q, _ = O.round_to(O.randn(5, (rows, H, nope + rope)), C.F16)
+    q[0, 1, 7] = 0.0  # a skipped term
+    wkb = C.make_weights(6, H * nope, kr, w_type)
+    wvb = C.make_weights(7, H * vh, kr, w_type)
+    Wk = O.dequant_rows(wkb, w_type, kr).reshape(H, nope, kr).astype(np.float64)
+    Wv = O.dequant_rows(wvb, w_type, kr).reshape(H, vh, kr).astype(np.float64)
+    qa = O.mla_absorb(q, wkb, w_type, H)
+    ref = np.einsum("rhi,hid->rhd", q[..., :nope].astype(np.float64), Wk)
+    np.testing.assert_allclose(qa[..., :kr], ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
+    np.testing.assert_array_equal(qa[..., kr:], q[..., nope:])
+    o = O.randn(8, (rows, H, kr), 0.0, 0.3)
+    out = O.mla_project(o, wvb, w_type, H)
+    refo = np.einsum("rhd,hjd->rhj", o.astype(np.float64), Wv)
+    assert np.all(out == out.astype(np.float16).astype(np.float32))  # f16 values
+    np.testing.assert_allclose(out, refo, rtol=2e-3, atol=2e-3 * np.abs(refo).max())
+
+
+def test_mla_full_is_absorb_core_project():
+    # the composition against an fp64 brute force of the whole operator
+    c = C.mla_full_case(9, 2, 2, 4, [40, 17], O.W_Q8_0)
+    got = C.mla_full_ref(c)
+    Wk = O.dequant_rows(c["w_kb"], O.W_Q8_0, 512).reshape(4, 128, 512).astype(np.float64)
+    Wv = O.dequant_rows(c["w_vb"], O.W_Q8_0, 512).reshape(4, 128, 512).astype(np.float64)
+    q = c["q"].astype(np.float64)
+    qa = np.concatenate([np.einsum("bthi,hid->bthd", q[..., :128], Wk), q[..., 128:]], -1)
+    o = O.mla_attention_np64(qa, c["lat"], c["seq_lens"], 2, 4, C.MLA_SCALE)
+    ref = np.einsum("bthd,hjd->bthj", o, Wv)
+    np.testing.assert_allclose(got, ref, rtol=2e-3, atol=2e-3 * np.abs(ref).max())
