@@ -155,6 +155,56 @@ class Prefill(Case):
         mugen_amd.flash_prefill_attention(self.q, self.k, self.v, 0, out=self.out)
 
 
+class MlaFull(Case):
+    """cpu_mla_attention end to end (transformer.cpp:2539-2623): f16 q of
+    192 dims per head, absorption by attn_k_b, the latent core with the fp32
+    absorbed q over an f16 latent cache, up-projection by attn_v_b to f16,
+    weights in a GGML block encoding.  Bytes: both weight matrices, the
+    latent rows, q in, q_abs and o out and back, out."""
+    bound = "hbm"
+    kernel = "mla_decode"
+    extra_kernels = ("mla_absorb", "mla_project")
+
+    def __init__(self, dev, B, H, lens, max_T, w_type, seed, name):
+        self.name = name
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.lens = np.asarray(lens, np.int32)
+        self.w_type = w_type
+        self.q = randn((B, 1, H, 192), 1.0, torch.float16, g, dev)
+        self.lat = randn((B, max_T, 576), 0.5, torch.float16, g, dev)
+        self.sl = torch.from_numpy(self.lens).to(dev)
+        self.max_T = max_T
+        rb = {"f16": 1024, "q8_0": 544, "q4_0": 288}[w_type]
+        # weights as a quantiser writes them: random bytes with valid f16 block scales
+        wb = torch.randint(0, 256, (2, H * 128, rb), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+        if w_type == "f16":
+            wf = randn((2, H * 128, 512), 0.05, torch.float16, g, dev)
+            wb = wf.view(torch.uint8).reshape(2, H * 128, rb).contiguous()
+        else:
+            bb = 34 if w_type == "q8_0" else 18
+            sc = (torch.rand((2, H * 128, 16), generator=g, device=dev) * 1e-3 + 5e-4).to(torch.float16)
+            wb = wb.view(2, H * 128, 16, bb)
+            wb[..., 0:2] = sc.view(torch.uint8).view(2, H * 128, 16, 2)
+            wb = wb.reshape(2, H * 128, rb).contiguous()
+        self.w_kb = wb[0] if w_type != "f16" else wb[0].view(torch.float16)
+        self.w_vb = wb[1] if w_type != "f16" else wb[1].view(torch.float16)
+        self.qa = torch.empty((B, 1, H, 576), dtype=torch.float32, device=dev)
+        self.o = torch.empty((B, 1, H, 512), dtype=torch.float32, device=dev)
+        self.out = torch.empty((B, 1, H, 128), dtype=torch.float16, device=dev)
+        self.ws = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
+        self.profile = ("mla_full", name)
+        rows = B * H
+        self.bytes = (2.0 * H * 128 * rb + float(self.lens.sum()) * 576 * 2 + rows * 192 * 2
+                      + 2 * rows * 576 * 4 + 2 * rows * 512 * 4 + rows * 128 * 2)
+        self.flops = 2.0 * rows * 128 * 512 * 2 + 2.0 * H * (576 + 512) * float(self.lens.sum())
+
+    def step(self):
+        mugen_amd.mla_absorb(self.q, self.w_kb, self.w_type, out=self.qa)
+        mugen_amd.mla_attention(self.qa, self.lat, self.sl, self.max_T, scale=MLA_SCALE, out=self.o,
+                                workspace=self.ws, seq_lens_host=self.lens)
+        mugen_amd.mla_project(self.o, self.w_vb, self.w_type, out=self.out)
+
+
 def capture(case, n):
     """HIP graph of n consecutive steps (captured on a side stream, as torch requires)."""
     g = torch.cuda.CUDAGraph()
@@ -200,8 +250,12 @@ def time_case(case, steps, warmup, dev):
     _capi.timing_enable(False)
     k_ms, k_n = _capi.timing_read(case.kernel)
     c_ms, c_n = _capi.timing_read(case.kernel + "_combine")
+    extra = {}
+    for name in getattr(case, "extra_kernels", ()):
+        e_ms, e_n = _capi.timing_read(name)
+        extra[name + "_us"] = round(e_ms / max(e_n, 1) * 1e3, 3)
     return dict(ms_per_step=ms, wall_ms=wall_ms, kernel_ms=k_ms / max(k_n, 1),
-                combine_ms=(c_ms / c_n) if c_n else 0.0)
+                combine_ms=(c_ms / c_n) if c_n else 0.0, extra=extra)
 
 
 def rate(case, ms):
@@ -260,6 +314,7 @@ def main():
             GqaDecode(dev, 16, 28, 4, 128, seeded_lens(44, 16, 256, 4096), 4096, 44, "gqa_decode_qwen7b_b16"),
             Prefill(dev, 512, 32, 8, 64, 46, "gqa_prefill_llama1b"),
             MlaDecode(dev, 4, 128, 5, [32768] * 4, 32768, torch.bfloat16, torch.bfloat16, 47, "mla_verify_v3"),
+            MlaFull(dev, 8, 128, seeded_lens(45, 8, 1024, 8192), 8192, "q8_0", 48, "mla_full_v3_q8_0"),
         ]
     if args.only:
         cases = [c for c in cases if c.name == args.only]
@@ -275,7 +330,7 @@ def main():
             kernel_rate=round(rate(c, t["kernel_ms"]), 2),
             frac_of_peak=round(rate(c, t["ms_per_step"]) / (PEAK_HBM_GBS if c.unit == "GB/s" else PEAK_BF16_TFLOPS), 4),
             algorithmic_bytes=c.bytes, algorithmic_flops=c.flops,
-            traffic=load_traffic(*c.profile) if c.profile else None)
+            traffic=load_traffic(*c.profile) if c.profile else None, **t["extra"])
 
     h = results.get(head.name) if head in cases else None
     line = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,

@@ -4,17 +4,23 @@
 // the reference's GGUF block encodings (dequant_weight_row,
 // transformer.cpp:2488-2534: F16, Q8_0, Q4_0).
 //
-// At decode sizes (rows = batch * q_len of a few to a few tens) both are
+// At decode sizes (rows = batch * q_len, a few to a few tens) both are
 // skinny per-head GEMMs bound by the weight stream (16.8 MB per matrix per
-// layer in F16 at DeepSeek-V3 shape, 8.9 MB Q8_0, 4.7 MB Q4_0), so they run
-// as fp32 VALU dot products that read every weight element once per 16
-// rows, the reference's fp32 arithmetic:
-//  * absorb: workgroup = (head, 256 columns of kv_rank); thread = one
-//    column d; q_nope of up to 16 rows staged in LDS; the k-loop over the
-//    128 nope dims streams weight row h*128 + i (coalesced along d);
-//  * project: workgroup = (head, 16 output rows j); wave = 4 rows j; lane =
-//    8 consecutive kv_rank dims, so one weight row is one coalesced 1 KiB
-//    (F16) read; o of up to 16 rows in LDS; per-row wave reductions.
+// layer in F16 at DeepSeek-V3 shape, 8.9 MB Q8_0, 4.7 MB Q4_0).  Streaming
+// it at HBM rate needs most of the matrix in flight at once, so every lane
+// issues all of its weight loads before any arithmetic, keeps its slice of
+// the weights in registers, and loops over the rows against them (each
+// weight byte is read once for any number of rows).  Arithmetic is fp32 on
+// the VALU, as the reference's:
+//  * absorb: workgroup = (head, 256-column half of kv_rank), 8 waves; wave w
+//    holds nope rows 16w..16w+15, lane 4 consecutive columns; per 8-row
+//    chunk of q each lane sums its 16 rows, and the 8 waves' partials are
+//    added in LDS in a fixed order;
+//  * project: workgroup = (head, 32 output rows j), 4 waves of 8 rows j;
+//    lane = 8 consecutive kv_rank dims, so a wave's load of one weight row is
+//    one coalesced row; per 4 rows of o a lane forms 32 (row, j) partials
+//    over its 8 dims and a halving butterfly over the 64 lanes (32 + 1
+//    shuffles for the 32 sums) leaves each lane pair with one total.
 #include "common.h"
 #include "kernels.h"
 
@@ -22,154 +28,223 @@ namespace mugen_attn {
 
 namespace {
 
-constexpr int kRCH = 16;  // rows per pass (register accumulators / LDS rows)
-
 template <int WT>
 __host__ __device__ constexpr int wrow_bytes(int K) {
     return WT == W_F16 ? 2 * K : (WT == W_Q8_0 ? K / 32 * 34 : K / 32 * 18);
 }
 
-__device__ __forceinline__ float half_at(const uint8_t* p) {  // 2-byte aligned f16
-    return to_f32<DT_F16>(*reinterpret_cast<const uint16_t*>(p));
+__device__ __forceinline__ float half_bits(uint32_t b) {
+    return to_f32<DT_F16>(uint16_t(b & 0xffffu));
 }
 
-// element d of a dequantised weight row (dequant_weight_row)
-template <int WT>
-__device__ __forceinline__ float wval(const uint8_t* row, int d) {
+// Raw bits of N consecutive weights d0 .. d0+N-1 of one row (N = 4 or 8,
+// d0 a multiple of N), loaded with as few instructions as the encoding's
+// alignment allows; dequant() turns them into floats (dequant_weight_row).
+template <int WT, int N>
+struct WRaw {
+    uint32_t v[N / 2];  // F16: N halfs; Q8_0: N int8; Q4_0: N bytes whose low/high nibble is used
+    uint32_t s;         // block scale bits (unused for F16)
+};
+
+template <int WT, int N>
+__device__ __forceinline__ WRaw<WT, N> wload(const uint8_t* row, int d0) {
+    WRaw<WT, N> r{};
     if constexpr (WT == W_F16) {
-        return half_at(row + 2 * d);
-    } else if constexpr (WT == W_Q8_0) {
-        const uint8_t* blk = row + (d >> 5) * 34;
-        return half_at(blk) * (float)(int8_t)blk[2 + (d & 31)];
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(row + 2 * d0);  // 2N-byte aligned
+#pragma unroll
+        for (int e = 0; e < N / 2; e++) r.v[e] = p[e];
     } else {
-        const uint8_t* blk = row + (d >> 5) * 18;
-        const uint8_t byte = blk[2 + (d & 15)];
-        const int nib = (d & 16) ? (byte >> 4) : (byte & 15);
-        return (float)(nib - 8) * half_at(blk);
+        constexpr int BB = WT == W_Q8_0 ? 34 : 18;
+        const uint8_t* blk = row + (d0 >> 5) * BB;
+        const int off = WT == W_Q8_0 ? (d0 & 31) : (d0 & 15);  // byte offset of the first quant
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(blk + 2 + off);  // even: 2-byte loads
+        r.s = *reinterpret_cast<const uint16_t*>(blk);
+#pragma unroll
+        for (int e = 0; e < N / 2; e++) r.v[e] = p[e];
+    }
+    return r;
+}
+
+template <int WT, int N>
+__device__ __forceinline__ void dequant(const WRaw<WT, N>& r, int d0, float* w) {
+    if constexpr (WT == W_F16) {
+#pragma unroll
+        for (int e = 0; e < N / 2; e++) {
+            w[2 * e] = lo_f32<DT_F16>(r.v[e]);
+            w[2 * e + 1] = hi_f32<DT_F16>(r.v[e]);
+        }
+    } else if constexpr (WT == W_Q8_0) {
+        const float sc = half_bits(r.s);
+#pragma unroll
+        for (int e = 0; e < N / 2; e++) {
+            w[2 * e] = sc * (float)(int8_t)(r.v[e] & 0xff);
+            w[2 * e + 1] = sc * (float)(int8_t)((r.v[e] >> 8) & 0xff);
+        }
+    } else {
+        const float sc = half_bits(r.s);
+        const int sh = (d0 & 16) ? 4 : 0;  // elements 16..31 of a block: high nibbles
+#pragma unroll
+        for (int e = 0; e < N / 2; e++) {
+            w[2 * e] = (float)((int)((r.v[e] >> sh) & 15) - 8) * sc;
+            w[2 * e + 1] = (float)((int)((r.v[e] >> (8 + sh)) & 15) - 8) * sc;
+        }
     }
 }
 
-// elements d0 .. d0+7 of a dequantised row (d0 a multiple of 8)
-template <int WT>
-__device__ __forceinline__ void wval8(const uint8_t* row, int d0, float* w) {
-    if constexpr (WT == W_F16) {
-        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(row + 2 * d0);
+// one butterfly step over lane bit M: the lane keeps half of its M/2 live
+// values (the upper half if its bit M is set) plus its partner's copy of it
+template <int M>
+__device__ __forceinline__ void halve(float* x, int lane) {
+    constexpr int N = M / 2;
+    const bool up = (lane & M) != 0;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            w[2 * e] = lo_f32<DT_F16>(v[e]);
-            w[2 * e + 1] = hi_f32<DT_F16>(v[e]);
-        }
-    } else if constexpr (WT == W_Q8_0) {
-        const uint8_t* blk = row + (d0 >> 5) * 34;
-        const float s = half_at(blk);
-        const uint16_t* q2 = reinterpret_cast<const uint16_t*>(blk + 2 + (d0 & 31));  // even offset
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const uint16_t v = q2[e];
-            w[2 * e] = s * (float)(int8_t)(v & 0xff);
-            w[2 * e + 1] = s * (float)(int8_t)(v >> 8);
-        }
-    } else {
-        const uint8_t* blk = row + (d0 >> 5) * 18;
-        const float s = half_at(blk);
-        const int p = d0 & 31;  // 0, 8: low nibbles of bytes p..p+7; 16, 24: high nibbles of p-16..
-        const uint16_t* b2 = reinterpret_cast<const uint16_t*>(blk + 2 + (p & 15));
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const uint16_t v = b2[e];
-            const int lo = v & 0xff, hi = v >> 8;
-            const int n0 = (p & 16) ? (lo >> 4) : (lo & 15);
-            const int n1 = (p & 16) ? (hi >> 4) : (hi & 15);
-            w[2 * e] = (float)(n0 - 8) * s;
-            w[2 * e + 1] = (float)(n1 - 8) * s;
-        }
+    for (int t = 0; t < N; t++) {
+        const float keep = up ? x[t + N] : x[t];
+        const float give = up ? x[t] : x[t + N];
+        x[t] = keep + __shfl_xor(give, M, 64);
     }
 }
 
 }  // namespace
 
 template <int WT, int OUT_DT>
-__global__ __launch_bounds__(256) void mla_absorb_kernel(MlaProjParams p) {
-    constexpr int NOPE = 128, ROPE = 64, KR = 512;
-    __shared__ float qs[kRCH][NOPE];
-    const int h = blockIdx.x, tid = threadIdx.x;
-    const int d = blockIdx.y * 256 + tid;
+__global__ __launch_bounds__(512) void mla_absorb_kernel(MlaProjParams p) {
+    constexpr int NOPE = 128, ROPE = 64, KR = 512, RC = 8, IPW = 16;  // rows per chunk, nope rows per wave
+    __shared__ __attribute__((aligned(16))) float qs[RC][NOPE];
+    __shared__ __attribute__((aligned(16))) f32x4_t red[8][RC][64];  // [wave][row][lane] partials
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int d0 = blockIdx.y * 256 + 4 * lane;
     constexpr int RB = wrow_bytes<WT>(KR);
-    const uint8_t* wh = static_cast<const uint8_t*>(p.w) + (size_t)h * NOPE * RB;
+    const uint8_t* wrow = static_cast<const uint8_t*>(p.w) + ((size_t)h * NOPE + w * IPW) * RB;
+    WRaw<WT, 4> raw[IPW];
+#pragma unroll
+    for (int k = 0; k < IPW; k++) raw[k] = wload<WT, 4>(wrow + (size_t)k * RB, d0);
     const uint16_t* q = static_cast<const uint16_t*>(p.in);
-    for (int r0 = 0; r0 < p.rows; r0 += kRCH) {
-        const int nr = min(kRCH, p.rows - r0);
-        __syncthreads();
-        for (int k = tid; k < kRCH * NOPE; k += 256) {
+    for (int r0 = 0; r0 < p.rows; r0 += RC) {
+        const int nr = min(RC, p.rows - r0);
+        bool zero = false;  // a zero q term in a real row of the chunk
+        for (int k = tid; k < RC * NOPE; k += 512) {
             const int r = k / NOPE, i = k % NOPE;
-            qs[r][i] = r < nr ? to_f32<DT_F16>(q[((int64_t)(r0 + r) * p.H + h) * (NOPE + ROPE) + i]) : 0.f;
+            const float v = r < nr ? to_f32<DT_F16>(q[((int64_t)(r0 + r) * p.H + h) * (NOPE + ROPE) + i]) : 1.f;
+            zero |= v == 0.f;
+            qs[r][i] = r < nr ? v : 0.f;
         }
+        if (blockIdx.y == 0 && tid < RC * ROPE) {  // q_rope appended unchanged
+            const int r = tid / ROPE, c = tid % ROPE;
+            if (r < nr)
+                store_out<OUT_DT>(p.out, ((int64_t)(r0 + r) * p.H + h) * (KR + ROPE) + KR + c,
+                                  to_f32<DT_F16>(q[((int64_t)(r0 + r) * p.H + h) * (NOPE + ROPE) + NOPE + c]));
+        }
+        // The reference skips q == 0 terms; that differs from adding 0 * w
+        // only for a non-finite weight, so chunks without a zero q take the
+        // plain fma path.
+        const bool skip_zero = __syncthreads_or(zero);
+        f32x4_t acc[RC];
+        auto accumulate = [&](auto skip_tag) {
+            constexpr bool SKIP = decltype(skip_tag)::value;
+#pragma unroll
+            for (int r = 0; r < RC; r++) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k4 = 0; k4 < IPW; k4 += 4) {
+                float wv[4][4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) dequant<WT, 4>(raw[k4 + k], d0, wv[k]);
+#pragma unroll
+                for (int r = 0; r < RC; r++) {
+                    const f32x4_t qv = *reinterpret_cast<const f32x4_t*>(&qs[r][w * IPW + k4]);
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const float t = fmaf(qv[k], wv[k][e], acc[r][e]);
+                            acc[r][e] = (SKIP && qv[k] == 0.f) ? acc[r][e] : t;
+                        }
+                    }
+                }
+            }
+        };
+        if (skip_zero) accumulate(std::true_type{});
+        else accumulate(std::false_type{});
+#pragma unroll
+        for (int r = 0; r < RC; r++) red[w][r][lane] = acc[r];
         __syncthreads();
-        float acc[kRCH];
+        {   // thread (row r, lane l) adds the 8 waves' partials in wave order
+            const int r = tid >> 6, l = tid & 63;
+            f32x4_t t = red[0][r][l];
 #pragma unroll
-        for (int r = 0; r < kRCH; r++) acc[r] = 0.f;
-        for (int i0 = 0; i0 < NOPE; i0 += 8) {
-            float w[8];
+            for (int ww = 1; ww < 8; ww++) t += red[ww][r][l];
+            if (r < nr) {
+                const int64_t o = ((int64_t)(r0 + r) * p.H + h) * (KR + ROPE) + blockIdx.y * 256 + 4 * l;
+                if constexpr (OUT_DT == DT_F32) {
+                    *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.out) + o) = t;  // 16-byte aligned
+                } else {
 #pragma unroll
-            for (int e = 0; e < 8; e++) w[e] = wval<WT>(wh + (size_t)(i0 + e) * RB, d);
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-#pragma unroll
-                for (int r = 0; r < kRCH; r++) {
-                    const float qi = qs[r][i0 + e];
-                    acc[r] = qi != 0.f ? fmaf(qi, w[e], acc[r]) : acc[r];  // zero terms skipped, as the reference
+                    for (int e = 0; e < 4; e++) store_out<OUT_DT>(p.out, o + e, t[e]);
                 }
             }
         }
-#pragma unroll
-        for (int r = 0; r < kRCH; r++)
-            if (r < nr) store_out<OUT_DT>(p.out, ((int64_t)(r0 + r) * p.H + h) * (KR + ROPE) + d, acc[r]);
-        if (blockIdx.y == 0 && tid < ROPE) {  // q_rope appended unchanged
-            for (int r = 0; r < nr; r++)
-                store_out<OUT_DT>(p.out, ((int64_t)(r0 + r) * p.H + h) * (KR + ROPE) + KR + tid,
-                                  to_f32<DT_F16>(q[((int64_t)(r0 + r) * p.H + h) * (NOPE + ROPE) + NOPE + tid]));
-        }
+        __syncthreads();  // qs / red are rewritten by the next chunk
     }
 }
 
 template <int WT, int OUT_DT>
 __global__ __launch_bounds__(256) void mla_project_kernel(MlaProjParams p) {
-    constexpr int KR = 512, VH = 128;
-    __shared__ __attribute__((aligned(16))) float os[kRCH][KR];
+    constexpr int KR = 512, VH = 128, RC = 16, JW = 8;  // o rows staged per pass, output rows per wave
+    __shared__ __attribute__((aligned(16))) float os[RC][KR];
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int j0 = blockIdx.y * 16 + 4 * w;
+    const int j0 = blockIdx.y * 32 + JW * w;
+    const int d0 = 8 * lane;
     constexpr int RB = wrow_bytes<WT>(KR);
-    const uint8_t* wh = static_cast<const uint8_t*>(p.w) + (size_t)h * VH * RB;
+    const uint8_t* wrow = static_cast<const uint8_t*>(p.w) + ((size_t)h * VH + j0) * RB;
+    WRaw<WT, 8> raw[JW];
+#pragma unroll
+    for (int j = 0; j < JW; j++) raw[j] = wload<WT, 8>(wrow + (size_t)j * RB, d0);
+    float wv[JW][8];
+#pragma unroll
+    for (int j = 0; j < JW; j++) dequant<WT, 8>(raw[j], d0, wv[j]);
     const float* o = static_cast<const float*>(p.in);
-    for (int r0 = 0; r0 < p.rows; r0 += kRCH) {
-        const int nr = min(kRCH, p.rows - r0);
+    // after the butterfly, lane pair (2v, 2v+1) holds sum v = 8 * row + j
+    const int v = lane >> 1;
+    for (int r0 = 0; r0 < p.rows; r0 += RC) {
+        const int nr = min(RC, p.rows - r0);
         __syncthreads();
-        for (int k = tid; k < kRCH * KR / 4; k += 256) {
+        for (int k = tid; k < RC * KR / 4; k += 256) {
             const int r = k / (KR / 4), c4 = k % (KR / 4);
             *reinterpret_cast<f32x4_t*>(&os[r][4 * c4]) =
                 r < nr ? *reinterpret_cast<const f32x4_t*>(o + ((int64_t)(r0 + r) * p.H + h) * KR + 4 * c4)
                        : f32x4_t{0.f, 0.f, 0.f, 0.f};
         }
         __syncthreads();
+        for (int rs = 0; rs < nr; rs += 4) {
+            float x[32];  // x[8 * r + j]: rows rs..rs+3 x this wave's 8 output rows, over this lane's 8 dims
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++) {
-            const int j = j0 + jj;
-            float wv[8];
-            wval8<WT>(wh + (size_t)j * RB, 8 * lane, wv);
-            for (int r = 0; r < nr; r++) {
-                const f32x4_t a = *reinterpret_cast<const f32x4_t*>(&os[r][8 * lane]);
-                const f32x4_t b = *reinterpret_cast<const f32x4_t*>(&os[r][8 * lane + 4]);
-                float part = a[0] * wv[0];
-                part = fmaf(a[1], wv[1], part);
-                part = fmaf(a[2], wv[2], part);
-                part = fmaf(a[3], wv[3], part);
-                part = fmaf(b[0], wv[4], part);
-                part = fmaf(b[1], wv[5], part);
-                part = fmaf(b[2], wv[6], part);
-                part = fmaf(b[3], wv[7], part);
-                part = wave_sum(part);
-                if (lane == 0) store_out<OUT_DT>(p.out, ((int64_t)(r0 + r) * p.H + h) * VH + j, part);
+            for (int r = 0; r < 4; r++) {
+                const f32x4_t a = *reinterpret_cast<const f32x4_t*>(&os[rs + r][d0]);
+                const f32x4_t b = *reinterpret_cast<const f32x4_t*>(&os[rs + r][d0 + 4]);
+#pragma unroll
+                for (int j = 0; j < JW; j++) {
+                    float t = a[0] * wv[j][0];
+                    t = fmaf(a[1], wv[j][1], t);
+                    t = fmaf(a[2], wv[j][2], t);
+                    t = fmaf(a[3], wv[j][3], t);
+                    t = fmaf(b[0], wv[j][4], t);
+                    t = fmaf(b[1], wv[j][5], t);
+                    t = fmaf(b[2], wv[j][6], t);
+                    t = fmaf(b[3], wv[j][7], t);
+                    x[8 * r + j] = t;
+                }
             }
+            // halving butterfly: at lane bit m (32 .. 2) a lane keeps the half
+            // of its values selected by that bit and adds its partner's copy
+            halve<32>(x, lane);
+            halve<16>(x, lane);
+            halve<8>(x, lane);
+            halve<4>(x, lane);
+            halve<2>(x, lane);
+            const float tot = x[0] + __shfl_xor(x[0], 1, 64);
+            const int r = v >> 3, j = v & 7;
+            if ((lane & 1) == 0 && rs + r < nr)
+                store_out<OUT_DT>(p.out, ((int64_t)(r0 + rs + r) * p.H + h) * VH + j0 + j, tot);
         }
     }
 }
@@ -177,8 +252,8 @@ __global__ __launch_bounds__(256) void mla_project_kernel(MlaProjParams p) {
 template <int WT>
 static hipError_t launch_absorb_w(const MlaProjParams& p, int out_dt, hipStream_t st) {
     const dim3 grid(p.H, 512 / 256);
-    if (out_dt == DT_BF16) hipLaunchKernelGGL((mla_absorb_kernel<WT, DT_BF16>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((mla_absorb_kernel<WT, DT_F32>), grid, dim3(256), 0, st, p);
+    if (out_dt == DT_BF16) hipLaunchKernelGGL((mla_absorb_kernel<WT, DT_BF16>), grid, dim3(512), 0, st, p);
+    else hipLaunchKernelGGL((mla_absorb_kernel<WT, DT_F32>), grid, dim3(512), 0, st, p);
     return hipGetLastError();
 }
 
@@ -193,7 +268,7 @@ hipError_t launch_mla_absorb(const MlaProjParams& p, int w_type, int out_dt, hip
 
 template <int WT>
 static hipError_t launch_project_w(const MlaProjParams& p, int out_dt, hipStream_t st) {
-    const dim3 grid(p.H, 128 / 16);
+    const dim3 grid(p.H, 128 / 32);
     if (out_dt == DT_F16) hipLaunchKernelGGL((mla_project_kernel<WT, DT_F16>), grid, dim3(256), 0, st, p);
     else hipLaunchKernelGGL((mla_project_kernel<WT, DT_F32>), grid, dim3(256), 0, st, p);
     return hipGetLastError();
