@@ -156,14 +156,16 @@ class Prefill(Case):
 
 
 class MlaFull(Case):
-    """cpu_mla_attention end to end (transformer.cpp:2539-2623): f16 q of
-    192 dims per head, absorption by attn_k_b, the latent core with the fp32
-    absorbed q over an f16 latent cache, up-projection by attn_v_b to f16,
+    """The attention part of one MLA decode layer (transformer.cpp:3882-3995,
+    from the q / kv_a projections to the attention output): latent-cache
+    write of the new token (c_kv RMSNorm, k_rope YaRN RoPE, append), q RoPE
+    fused into absorption by attn_k_b, the latent core with the fp32
+    absorbed q over the f16 latent cache, up-projection by attn_v_b to f16,
     weights in a GGML block encoding.  Bytes: both weight matrices, the
-    latent rows, q in, q_abs and o out and back, out."""
+    latent rows read and written, q in, q_abs and o out and back, out."""
     bound = "hbm"
     kernel = "mla_decode"
-    extra_kernels = ("mla_absorb", "mla_project")
+    extra_kernels = ("mla_latent_write", "mla_absorb", "mla_project")
 
     def __init__(self, dev, B, H, lens, max_T, w_type, seed, name):
         self.name = name
@@ -192,14 +194,19 @@ class MlaFull(Case):
         self.o = torch.empty((B, 1, H, 512), dtype=torch.float32, device=dev)
         self.out = torch.empty((B, 1, H, 128), dtype=torch.float16, device=dev)
         self.ws = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
+        self.kv_a = randn((B, 576), 1.0, torch.float16, g, dev)
+        self.norm_w = randn((512,), 0.1, torch.float16, g, dev) + 1.0
+        self.pos = torch.from_numpy(self.lens - 1).to(dev)
+        self.rope = (10000.0, 40.0, 4096)
         self.profile = ("mla_full", name)
         rows = B * H
         self.bytes = (2.0 * H * 128 * rb + float(self.lens.sum()) * 576 * 2 + rows * 192 * 2
-                      + 2 * rows * 576 * 4 + 2 * rows * 512 * 4 + rows * 128 * 2)
+                      + 2 * rows * 576 * 4 + 2 * rows * 512 * 4 + rows * 128 * 2 + 2 * B * 576 * 2)
         self.flops = 2.0 * rows * 128 * 512 * 2 + 2.0 * H * (576 + 512) * float(self.lens.sum())
 
     def step(self):
-        mugen_amd.mla_absorb(self.q, self.w_kb, self.w_type, out=self.qa)
+        mugen_amd.mla_latent_write(self.kv_a, self.norm_w, self.pos, self.lat, rope=self.rope)
+        mugen_amd.mla_absorb(self.q, self.w_kb, self.w_type, out=self.qa, positions=self.pos, rope=self.rope)
         mugen_amd.mla_attention(self.qa, self.lat, self.sl, self.max_T, scale=MLA_SCALE, out=self.o,
                                 workspace=self.ws, seq_lens_host=self.lens)
         mugen_amd.mla_project(self.o, self.w_vb, self.w_type, out=self.out)
@@ -314,7 +321,7 @@ def main():
             GqaDecode(dev, 16, 28, 4, 128, seeded_lens(44, 16, 256, 4096), 4096, 44, "gqa_decode_qwen7b_b16"),
             Prefill(dev, 512, 32, 8, 64, 46, "gqa_prefill_llama1b"),
             MlaDecode(dev, 4, 128, 5, [32768] * 4, 32768, torch.bfloat16, torch.bfloat16, 47, "mla_verify_v3"),
-            MlaFull(dev, 8, 128, seeded_lens(45, 8, 1024, 8192), 8192, "q8_0", 48, "mla_full_v3_q8_0"),
+            MlaFull(dev, 8, 128, seeded_lens(45, 8, 1024, 8192), 8192, "q8_0", 48, "mla_layer_v3_q8_0"),
         ]
     if args.only:
         cases = [c for c in cases if c.name == args.only]

@@ -215,6 +215,18 @@ typedef enum {
 } mugen_attn_wtype;
 
 /*
+ * RoPE of the MLA path: NeoX pairs (i, i + rope_dim/2) with the YaRN
+ * frequencies of yarn_rope_freq (transformer.cpp:41-70; beta_fast 32,
+ * beta_slow 1), computed by the library on the host exactly as there.
+ * factor <= 1 means plain RoPE, 1 / theta^(2i/rope_dim).
+ */
+typedef struct mugen_attn_rope_params {
+    float theta;          /* rope_theta */
+    float factor;         /* rope_scaling_factor */
+    int32_t original_ctx; /* rope_original_ctx */
+} mugen_attn_rope_params;
+
+/*
  * q_absorbed = q_nope x k_b, then q_rope appended (transformer.cpp:2556-2573):
  *   q      [rows][n_heads][nope_dim + rope_dim]  F16 (the reference's q_data)
  *   w_kb   attn_k_b: n_heads*nope_dim rows of kv_rank values (w_type)
@@ -222,6 +234,9 @@ typedef enum {
  *          reference's float q_absorbed) or BF16
  *   q_abs[r][h][d] = sum_i q[r][h][i] * k_b[h*nope_dim + i][d], d < kv_rank
  * rows = batch * q_len.  Supported: nope_dim 128, rope_dim 64, kv_rank 512.
+ * With positions (device int32 [rows]) non-null, the appended q_rope is
+ * first rotated by the reference's q RoPE stage (transformer.cpp:3882-3921,
+ * f16 results) at positions[r]; q itself is not modified.
  */
 typedef struct mugen_attn_mla_absorb_args {
     const void* q;
@@ -234,6 +249,8 @@ typedef struct mugen_attn_mla_absorb_args {
     int32_t kv_rank;
     int32_t w_type;    /* mugen_attn_wtype */
     int32_t out_dtype; /* F32 or BF16 */
+    const int32_t* positions;    /* optional: RoPE q_rope at these positions */
+    mugen_attn_rope_params rope; /* used when positions is non-null */
 } mugen_attn_mla_absorb_args;
 int mugen_attn_mla_absorb(const mugen_attn_mla_absorb_args* args, void* stream);
 
@@ -259,6 +276,37 @@ typedef struct mugen_attn_mla_project_args {
 int mugen_attn_mla_project(const mugen_attn_mla_project_args* args, void* stream);
 
 /*
+ * Latent-cache writer (transformer.cpp:3930-3987): for each new token r,
+ *   c_kv = RMSNorm(kv_a[r][0:kv_rank]) * norm_w   (1/sqrt(mean(x^2) + eps))
+ *   k_rope = RoPE(kv_a[r][kv_rank:], positions[r])
+ * and [c_kv | k_rope] is written to row positions[r] of sequence
+ * r / rows_per_seq of the latent cache, replacing the reference's host
+ * round trip (read kv_a, normalise and rotate on the CPU, scatter_kv).
+ *   kv_a      [rows][kv_rank + rope_dim] F16 (the kv_a_mqa projection)
+ *   norm_w    [kv_rank] F16 (attn_kv_a_norm)
+ *   positions [rows] device int32; rows outside [0, max_seq_len) are skipped
+ *   latent    [n_seq][max_seq_len][kv_rank + rope_dim], seq_stride elements
+ *             apart; F16 (the reference's rounding) or BF16
+ * Supported: kv_rank 512, rope_dim 64.
+ */
+typedef struct mugen_attn_mla_latent_write_args {
+    const void* kv_a;
+    const void* norm_w;
+    const int32_t* positions;
+    void* latent;
+    int32_t rows;
+    int32_t rows_per_seq;
+    int32_t max_seq_len;
+    int32_t kv_rank;
+    int32_t rope_dim;
+    int32_t latent_dtype;
+    int64_t seq_stride;
+    float eps;
+    mugen_attn_rope_params rope;
+} mugen_attn_mla_latent_write_args;
+int mugen_attn_mla_latent_write(const mugen_attn_mla_latent_write_args* args, void* stream);
+
+/*
  * scatter_kv: dst[offset + i] = src[i], i < count, 16-bit elements.
  * Replaces scatter_kv (kernel_sources.h:3018-3028) / make_scatter_kv_dp
  * (transformer.cpp:872-886): the per-token append of K/V rows or latent
@@ -278,7 +326,7 @@ const char* mugen_attn_version(void);
  * mugen_attn_timing_read synchronises on the recorded events and returns
  * the summed milliseconds and launch count of the kernel named `kernel`
  * ("gqa_decode", "gqa_decode_combine", "gqa_prefill", "mla_decode",
- * "mla_decode_combine", "mla_absorb", "mla_project", "scatter_kv").
+ * "mla_decode_combine", "mla_absorb", "mla_project", "mla_latent_write", "scatter_kv").
  */
 int mugen_attn_timing_enable(int enable);
 int mugen_attn_timing_read(const char* kernel, double* total_ms, int64_t* launches);

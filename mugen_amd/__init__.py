@@ -5,8 +5,8 @@ HIP kernels behind the C ABI in include/mugen_attn.h (libmugen_attn.so).
 """
 from . import _capi
 from .attention import (attention_decode, flash_prefill_attention, mla_absorb, mla_attention,
-                        mla_attention_full, mla_project, scatter_kv)
+                        mla_attention_full, mla_latent_write, mla_project, scatter_kv)
 
 __all__ = ["attention_decode", "flash_prefill_attention", "mla_absorb", "mla_attention", "mla_attention_full",
-           "mla_project", "scatter_kv", "_capi"]
+           "mla_latent_write", "mla_project", "scatter_kv", "_capi"]
 __version__ = "0.1.0"

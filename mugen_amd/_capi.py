@@ -29,6 +29,7 @@ EXPORTS = (
     "mugen_attn_mla_decode",
     "mugen_attn_mla_absorb",
     "mugen_attn_mla_project",
+    "mugen_attn_mla_latent_write",
     "mugen_attn_scatter_kv",
     "mugen_attn_last_error",
     "mugen_attn_version",
@@ -70,11 +71,23 @@ class MlaDecodeArgs(ctypes.Structure):
     ]
 
 
+class RopeParams(ctypes.Structure):
+    _fields_ = [("theta", _f32), ("factor", _f32), ("original_ctx", _i32)]
+
+
 class MlaAbsorbArgs(ctypes.Structure):
     _fields_ = [
         ("q", _vp), ("w_kb", _vp), ("q_abs", _vp),
         ("rows", _i32), ("n_heads", _i32), ("nope_dim", _i32), ("rope_dim", _i32), ("kv_rank", _i32),
-        ("w_type", _i32), ("out_dtype", _i32),
+        ("w_type", _i32), ("out_dtype", _i32), ("positions", _vp), ("rope", RopeParams),
+    ]
+
+
+class MlaLatentWriteArgs(ctypes.Structure):
+    _fields_ = [
+        ("kv_a", _vp), ("norm_w", _vp), ("positions", _vp), ("latent", _vp),
+        ("rows", _i32), ("rows_per_seq", _i32), ("max_seq_len", _i32), ("kv_rank", _i32), ("rope_dim", _i32),
+        ("latent_dtype", _i32), ("seq_stride", _i64), ("eps", _f32), ("rope", RopeParams),
     ]
 
 
@@ -119,6 +132,8 @@ def lib() -> ctypes.CDLL:
         L.mugen_attn_mla_absorb.restype = ctypes.c_int
         L.mugen_attn_mla_project.argtypes = [ctypes.POINTER(MlaProjectArgs), _vp]
         L.mugen_attn_mla_project.restype = ctypes.c_int
+        L.mugen_attn_mla_latent_write.argtypes = [ctypes.POINTER(MlaLatentWriteArgs), _vp]
+        L.mugen_attn_mla_latent_write.restype = ctypes.c_int
         L.mugen_attn_scatter_kv.argtypes = [_vp, _vp, ctypes.c_uint64, ctypes.c_uint64, _vp]
         L.mugen_attn_scatter_kv.restype = ctypes.c_int
         L.mugen_attn_last_error.restype = ctypes.c_char_p

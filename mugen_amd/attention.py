@@ -12,6 +12,8 @@ libmugen_attn.so.  Operator names follow the reference's seams:
   mla_absorb / mla_project <- cpu_mla_attention absorption and up-projection
                               (transformer.cpp:2556-2573, 2610-2620)
   mla_attention_full       <- cpu_mla_attention (transformer.cpp:2539-2623)
+  mla_latent_write         <- c_kv RMSNorm + k_rope RoPE + latent append
+                              (transformer.cpp:3930-3987)
   scatter_kv               <- scatter_kv (kernel_sources.h:3018-3028)
 """
 from __future__ import annotations
@@ -183,13 +185,23 @@ def _wtype(w: torch.Tensor, w_type) -> int:
     return _WT[w_type] if isinstance(w_type, str) else int(w_type)
 
 
+def _rope(rope) -> _capi.RopeParams:
+    """(theta, factor, original_ctx) -> RopeParams; factor <= 1: plain RoPE."""
+    theta, factor, ctx = rope
+    return _capi.RopeParams(float(theta), float(factor), int(ctx))
+
+
 def mla_absorb(q: torch.Tensor, w_kb: torch.Tensor, w_type=None, *, out: torch.Tensor | None = None,
-               out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+               out_dtype: torch.dtype = torch.float32, positions: torch.Tensor | None = None,
+               rope=(10000.0, 0.0, 0)) -> torch.Tensor:
     """q_abs = [q_nope . k_b | q_rope] per head (transformer.cpp:2556-2573).
 
     q f16 [..., H, 192]; w_kb = attn_k_b, H*128 rows of 512 in the GGML
     encoding w_type ('f16' as a float16 tensor, 'q8_0' / 'q4_0' as uint8
-    bytes).  Returns [..., H, 576] in out_dtype (F32 or BF16)."""
+    bytes).  Returns [..., H, 576] in out_dtype (F32 or BF16).  With
+    positions (int32, one per row of q), q_rope is first rotated by the
+    reference's q RoPE stage (transformer.cpp:3882-3921) with
+    rope = (theta, yarn factor, original ctx)."""
     _need_cuda(q, w_kb)
     if q.dtype != torch.float16 or q.shape[-1] != 192:
         raise ValueError("q must be float16 [..., H, 192]")
@@ -201,6 +213,11 @@ def mla_absorb(q: torch.Tensor, w_kb: torch.Tensor, w_type=None, *, out: torch.T
     a.q, a.w_kb, a.q_abs = q.data_ptr(), w_kb.data_ptr(), out.data_ptr()
     a.rows, a.n_heads, a.nope_dim, a.rope_dim, a.kv_rank = rows, H, 128, 64, 512
     a.w_type, a.out_dtype = _wtype(w_kb, w_type), _dt(out.dtype)
+    if positions is not None:
+        _need_cuda(positions)
+        if positions.dtype != torch.int32 or positions.numel() != rows:
+            raise ValueError("positions must be int32 with one entry per row of q")
+        a.positions, a.rope = positions.data_ptr(), _rope(rope)
     _capi.check(_capi.lib().mugen_attn_mla_absorb(ctypes.byref(a), _stream(q.device)))
     return out
 
@@ -237,6 +254,33 @@ def mla_attention_full(q: torch.Tensor, w_kb: torch.Tensor, w_vb: torch.Tensor, 
     o = mla_attention(qa, latent, seq_lens, max_seq_len, scale=scale, num_splits=num_splits,
                       seq_lens_host=seq_lens_host)
     return mla_project(o, w_vb, w_type)
+
+
+def mla_latent_write(kv_a: torch.Tensor, norm_w: torch.Tensor, positions: torch.Tensor, latent: torch.Tensor,
+                     *, rows_per_seq: int = 1, eps: float = 1e-6, rope=(10000.0, 0.0, 0),
+                     max_seq_len: int | None = None) -> torch.Tensor:
+    """Latent-cache writer (transformer.cpp:3930-3987): RMSNorm(c_kv) * norm_w
+    and RoPE(k_rope) of each kv_a row [rows, 576] (f16), written to row
+    positions[r] of sequence r // rows_per_seq of latent [n_seq, max_T, 576]
+    (f16 or bf16).  rope = (theta, yarn factor, original ctx)."""
+    _need_cuda(kv_a, norm_w, positions, latent)
+    if kv_a.dtype != torch.float16 or norm_w.dtype != torch.float16 or kv_a.shape[-1] != 576:
+        raise ValueError("kv_a must be float16 [rows, 576] and norm_w float16 [512]")
+    if positions.dtype != torch.int32:
+        raise TypeError("positions must be int32")
+    rows = kv_a.numel() // 576
+    if positions.numel() != rows or latent.dim() != 3 or latent.shape[-1] != 576:
+        raise ValueError("positions must hold one entry per kv_a row; latent must be [n_seq, max_T, 576]")
+    a = _capi.MlaLatentWriteArgs()
+    a.kv_a, a.norm_w, a.positions, a.latent = kv_a.data_ptr(), norm_w.data_ptr(), positions.data_ptr(), latent.data_ptr()
+    a.rows, a.rows_per_seq = rows, int(rows_per_seq)
+    a.max_seq_len = int(latent.shape[1] if max_seq_len is None else max_seq_len)
+    a.kv_rank, a.rope_dim, a.latent_dtype = 512, 64, _dt(latent.dtype)
+    a.seq_stride, a.eps, a.rope = latent[0].numel(), float(eps), _rope(rope)
+    if (rows + a.rows_per_seq - 1) // a.rows_per_seq > latent.shape[0]:
+        raise ValueError("more sequences than latent has")
+    _capi.check(_capi.lib().mugen_attn_mla_latent_write(ctypes.byref(a), _stream(kv_a.device)))
+    return latent
 
 
 # ------------------------------------------------------------------ scatter_kv

@@ -10,6 +10,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
+#include <cmath>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -466,6 +468,40 @@ int mugen_attn_mla_decode(const mugen_attn_mla_decode_args* a, void* ws, size_t 
     return hip_status(e, "mla_decode launch");
 }
 
+// yarn_rope_freq (transformer.cpp:41-70) in the same float operations, so
+// the table matches the reference's frequencies bit for bit
+static RopeFreqs yarn_freqs(const mugen_attn_rope_params& r) {
+#pragma clang fp contract(off)
+    RopeFreqs out{};
+    constexpr int RD = 64;
+    const float pi_f = 3.14159265358979323846f;
+    for (int i = 0; i < RD / 2; i++) {
+        float freq = 1.0f / std::pow(r.theta, 2.0f * (float)i / (float)RD);
+        if (r.factor > 1.0f) {
+            const float log_base = std::log(r.theta);
+            const float ctx_f = (float)r.original_ctx;
+            float low = std::floor((float)RD * std::log(ctx_f / (32.0f * 2.0f * pi_f)) / (2.0f * log_base));
+            float high = std::ceil((float)RD * std::log(ctx_f / (1.0f * 2.0f * pi_f)) / (2.0f * log_base));
+            low = std::max(low, 0.0f);
+            high = std::min(high, (float)(RD / 2 - 1));
+            const float idx = (float)i;
+            if (idx > high) {
+                freq = freq / r.factor;
+            } else if (idx >= low) {
+                float ramp = (idx - low) / std::max(0.001f, high - low);
+                ramp = std::max(0.0f, std::min(1.0f, ramp));
+                freq = freq * (1.0f - ramp) + (freq / r.factor) * ramp;
+            }
+        }
+        out.f[i] = freq;
+    }
+    return out;
+}
+
+static bool rope_ok(const mugen_attn_rope_params& r) {
+    return std::isfinite(r.theta) && r.theta > 0.f && std::isfinite(r.factor) && (r.factor <= 1.f || r.original_ctx > 0);
+}
+
 static bool is_wtype(int w) { return w == W_F16 || w == W_Q8_0 || w == W_Q4_0; }
 
 // weight rows: F16 rows are read 16 bytes at a time, block rows 2 at a time
@@ -488,7 +524,9 @@ int mugen_attn_mla_absorb(const mugen_attn_mla_absorb_args* a, void* stream) {
         return fail(MUGEN_ATTN_E_INVALID, "mla_absorb: misaligned q/q_abs/w_kb");
     if ((int64_t)a->rows * a->n_heads > (1 << 24))
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_absorb: rows*n_heads too large");
-    MlaProjParams p{a->q, a->w_kb, a->q_abs, a->rows, a->n_heads};
+    if (a->positions && !rope_ok(a->rope)) return fail(MUGEN_ATTN_E_INVALID, "mla_absorb: bad rope parameters");
+    MlaProjParams p{a->q, a->w_kb, a->q_abs, a->rows, a->n_heads, a->positions, {}};
+    if (a->positions) p.freqs = yarn_freqs(a->rope);
     return hip_status(launch_mla_absorb(p, a->w_type, a->out_dtype, static_cast<hipStream_t>(stream), active_timer()),
                       "mla_absorb launch");
 }
@@ -508,9 +546,43 @@ int mugen_attn_mla_project(const mugen_attn_mla_project_args* a, void* stream) {
         return fail(MUGEN_ATTN_E_INVALID, "mla_project: misaligned o/out/w_vb");
     if ((int64_t)a->rows * a->n_heads > (1 << 24))
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_project: rows*n_heads too large");
-    MlaProjParams p{a->o, a->w_vb, a->out, a->rows, a->n_heads};
+    MlaProjParams p{a->o, a->w_vb, a->out, a->rows, a->n_heads, nullptr, {}};
     return hip_status(launch_mla_project(p, a->w_type, a->out_dtype, static_cast<hipStream_t>(stream), active_timer()),
                       "mla_project launch");
+}
+
+int mugen_attn_mla_latent_write(const mugen_attn_mla_latent_write_args* a, void* stream) {
+    if (!a) return fail(MUGEN_ATTN_E_INVALID, "mla_latent_write: null args");
+    if (a->kv_rank != 512 || a->rope_dim != 64)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_latent_write: kv_rank/rope_dim %d/%d (supported: 512/64)",
+                    a->kv_rank, a->rope_dim);
+    if (!is16(a->latent_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_latent_write: latent dtype must be F16/BF16");
+    if (a->rows < 0 || a->rows_per_seq <= 0 || a->max_seq_len <= 0)
+        return fail(MUGEN_ATTN_E_INVALID, "mla_latent_write: bad rows/rows_per_seq/max_seq_len");
+    if (!(a->eps >= 0.f) || !std::isfinite(a->eps)) return fail(MUGEN_ATTN_E_INVALID, "mla_latent_write: bad eps");
+    if (!rope_ok(a->rope)) return fail(MUGEN_ATTN_E_INVALID, "mla_latent_write: bad rope parameters");
+    if (a->rows == 0) return MUGEN_ATTN_OK;
+    if (!a->kv_a || !a->norm_w || !a->positions || !a->latent)
+        return fail(MUGEN_ATTN_E_INVALID, "mla_latent_write: null pointer");
+    const int n_seq = (a->rows + a->rows_per_seq - 1) / a->rows_per_seq;
+    if (n_seq > 1 && a->seq_stride < (int64_t)a->max_seq_len * 576)
+        return fail(MUGEN_ATTN_E_INVALID, "mla_latent_write: seq_stride smaller than max_seq_len*576");
+    if ((((uintptr_t)a->kv_a | (uintptr_t)a->norm_w | (uintptr_t)a->latent) & 15) || (a->seq_stride % 8))
+        return fail(MUGEN_ATTN_E_INVALID, "mla_latent_write: kv_a/norm_w/latent must be 16-byte aligned, "
+                    "seq_stride a multiple of 8");
+    LatentWriteParams p{};
+    p.kv_a = static_cast<const uint16_t*>(a->kv_a);
+    p.norm_w = static_cast<const uint16_t*>(a->norm_w);
+    p.positions = a->positions;
+    p.latent = static_cast<uint16_t*>(a->latent);
+    p.rows = a->rows;
+    p.rows_per_seq = a->rows_per_seq;
+    p.max_seq_len = a->max_seq_len;
+    p.seq_stride = a->seq_stride;
+    p.eps = a->eps;
+    p.freqs = yarn_freqs(a->rope);
+    return hip_status(launch_mla_latent_write(p, a->latent_dtype, static_cast<hipStream_t>(stream), active_timer()),
+                      "mla_latent_write launch");
 }
 
 int mugen_attn_scatter_kv(const void* src, void* dst, uint64_t offset, uint64_t count, void* stream) {

@@ -278,4 +278,19 @@ __device__ __forceinline__ u32x2_t load8(const void* p) {
     return *reinterpret_cast<const u32x2_t*>(p);
 }
 
+// ---------------------------------------------------------------- RoPE
+
+// One NeoX pair (x0 = dim i, x1 = dim i + 32) rotated by pos * freq as the
+// reference's float code does (transformer.cpp:3903-3917): angle rounded
+// to float, full-precision cosf / sinf, each output a product difference
+// with separately rounded products (contraction off, like the scalar host
+// loop), then rounded to f16 (the reference stores the result as f16).
+__device__ __forceinline__ void rope_pair_f16(float x0, float x1, int pos, float freq, uint16_t& y0, uint16_t& y1) {
+#pragma clang fp contract(off)
+    const float angle = (float)pos * freq;
+    const float cv = cosf(angle), sv = sinf(angle);
+    y0 = from_f32<DT_F16>(x0 * cv - x1 * sv);
+    y1 = from_f32<DT_F16>(x1 * cv + x0 * sv);
+}
+
 }  // namespace mugen_attn

@@ -6,6 +6,12 @@
 
 namespace mugen_attn {
 
+// YaRN frequencies of the 64 rope dims' 32 pairs, computed on the host
+// (yarn_rope_freq, transformer.cpp:41-70) and passed by value.
+struct RopeFreqs {
+    float f[32];
+};
+
 struct KernelTimer;  // defined in capi.hip
 void timer_begin(KernelTimer* t, const char* name, hipStream_t st);
 void timer_end(KernelTimer* t, const char* name, hipStream_t st);
@@ -85,9 +91,26 @@ struct MlaProjParams {
     void* out;        // absorb: q_abs [rows][H][kv_rank+rope]; project: [rows][H][v_head]
     int rows;
     int H;
+    const int32_t* positions;  // absorb: RoPE position of each row (null: q_rope copied as is)
+    RopeFreqs freqs;
 };
 hipError_t launch_mla_absorb(const MlaProjParams& p, int w_type, int out_dt, hipStream_t st, KernelTimer* t);
 hipError_t launch_mla_project(const MlaProjParams& p, int w_type, int out_dt, hipStream_t st, KernelTimer* t);
+
+// MLA latent-cache writer (mla_cache.hip)
+struct LatentWriteParams {
+    const uint16_t* kv_a;      // [rows][576] f16
+    const uint16_t* norm_w;    // [512] f16
+    const int32_t* positions;  // [rows]
+    uint16_t* latent;          // [n_seq][max_seq_len][576]
+    int rows;
+    int rows_per_seq;
+    int max_seq_len;
+    int64_t seq_stride;
+    float eps;
+    RopeFreqs freqs;
+};
+hipError_t launch_mla_latent_write(const LatentWriteParams& p, int latent_dt, hipStream_t st, KernelTimer* t);
 
 hipError_t launch_scatter_kv(const uint16_t* src, uint16_t* dst, uint64_t offset, uint64_t count,
                              hipStream_t st, KernelTimer* t);

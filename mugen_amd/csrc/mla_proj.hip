@@ -129,11 +129,19 @@ __global__ __launch_bounds__(512) void mla_absorb_kernel(MlaProjParams p) {
             zero |= v == 0.f;
             qs[r][i] = r < nr ? v : 0.f;
         }
-        if (blockIdx.y == 0 && tid < RC * ROPE) {  // q_rope appended unchanged
-            const int r = tid / ROPE, c = tid % ROPE;
-            if (r < nr)
-                store_out<OUT_DT>(p.out, ((int64_t)(r0 + r) * p.H + h) * (KR + ROPE) + KR + c,
-                                  to_f32<DT_F16>(q[((int64_t)(r0 + r) * p.H + h) * (NOPE + ROPE) + NOPE + c]));
+        if (blockIdx.y == 0 && tid < RC * ROPE / 2) {
+            // q_rope appended: as is, or with the reference's q RoPE stage
+            // (NeoX pairs c, c + 32, f16 results; transformer.cpp:3882-3921)
+            const int r = tid / (ROPE / 2), c = tid % (ROPE / 2);
+            if (r < nr) {
+                const uint16_t* qr = q + ((int64_t)(r0 + r) * p.H + h) * (NOPE + ROPE) + NOPE;
+                uint16_t y0 = qr[c], y1 = qr[c + ROPE / 2];
+                if (p.positions)
+                    rope_pair_f16(to_f32<DT_F16>(y0), to_f32<DT_F16>(y1), p.positions[r0 + r], p.freqs.f[c], y0, y1);
+                const int64_t o = ((int64_t)(r0 + r) * p.H + h) * (KR + ROPE) + KR + c;
+                store_out<OUT_DT>(p.out, o, to_f32<DT_F16>(y0));
+                store_out<OUT_DT>(p.out, o + ROPE / 2, to_f32<DT_F16>(y1));
+            }
         }
         // The reference skips q == 0 terms; that differs from adding 0 * w
         // only for a non-finite weight, so chunks without a zero q take the

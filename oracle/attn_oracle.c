@@ -31,6 +31,12 @@
  *   oracle_mla_project    <- out_h = out_comp x v_b^T, transformer.cpp:2610-2620
  *   (absorb + oracle_mla_attention + project = cpu_mla_attention,
  *    transformer.cpp:2539-2623)
+ *   oracle_yarn_rope_freq <- yarn_rope_freq, transformer.cpp:41-70
+ *   oracle_rope_neox_f16  <- q / k_rope NeoX RoPE, transformer.cpp:3903-3917,
+ *                            :3968-3980
+ *   oracle_mla_kv_prepare <- c_kv RMSNorm + k_rope RoPE, transformer.cpp:3935-3981
+ *   oracle_mla_latent_write <- prepare + scatter into the latent cache,
+ *                            transformer.cpp:3930-3987
  *   oracle_scatter_kv     <- scatter_kv, src/metal/kernel_sources.h:3018-3028
  *
  * The summation orders above are kept (sequential fp32 sums, expf, divide
@@ -469,6 +475,102 @@ void oracle_mla_project(const float* o, const uint8_t* w_vb, int w_type, float* 
         }
     }
     free(wrow);
+}
+
+/* ------------------------------------------------------------------ */
+/* MLA latent-cache writer and q RoPE                                  */
+/* ------------------------------------------------------------------ */
+/*
+ * oracle_yarn_rope_freq <- yarn_rope_freq, transformer.cpp:41-70: base
+ * frequency theta^(-2i/rope_dim) (powf), and for factor > 1 the YaRN
+ * correction with beta_fast 32 / beta_slow 1: dims below
+ * low = floor(d ln(ctx / (32 * 2 pi)) / (2 ln theta)) keep it, dims above
+ * high = ceil(d ln(ctx / (2 pi)) / (2 ln theta)) (clamped to d/2 - 1) take
+ * freq / factor, a linear ramp in between.  float arithmetic throughout,
+ * as there (std::pow / std::log / std::floor on floats).
+ */
+float oracle_yarn_rope_freq(int dim_idx, int rope_dim, float factor, int original_ctx, float theta) {
+    const float pi_f = 3.14159265358979323846f;
+    float freq = 1.0f / powf(theta, 2.0f * (float)dim_idx / (float)rope_dim);
+    if (factor <= 1.0f) return freq;
+    float log_base = logf(theta);
+    float ctx_f = (float)original_ctx;
+    float dim_f = (float)rope_dim;
+    float low = floorf(dim_f * logf(ctx_f / (32.0f * 2.0f * pi_f)) / (2.0f * log_base));
+    float high = ceilf(dim_f * logf(ctx_f / (1.0f * 2.0f * pi_f)) / (2.0f * log_base));
+    if (low < 0.0f) low = 0.0f;
+    if (high > (float)(rope_dim / 2 - 1)) high = (float)(rope_dim / 2 - 1);
+    float idx = (float)dim_idx;
+    if (idx < low) return freq;
+    if (idx > high) return freq / factor;
+    float span = high - low;
+    if (span < 0.001f) span = 0.001f;
+    float ramp = (idx - low) / span;
+    if (ramp < 0.0f) ramp = 0.0f;
+    if (ramp > 1.0f) ramp = 1.0f;
+    return freq * (1.0f - ramp) + (freq / factor) * ramp;
+}
+
+/*
+ * oracle_rope_neox_f16 <- the NeoX RoPE of transformer.cpp:3903-3917 (q)
+ * and :3968-3980 (k_rope): pairs (i, i + rope_dim/2), angle = pos * freq_i
+ * in float, x0' = x0 cos - x1 sin, x1' = x1 cos + x0 sin, each rounded to
+ * f16.  x holds rope_dim f16 bit patterns, rotated in place.
+ */
+void oracle_rope_neox_f16(uint16_t* x, int rope_dim, int pos, const float* freqs) {
+    int half = rope_dim / 2;
+    for (int i = 0; i < half; i++) {
+        float angle = (float)pos * freqs[i];
+        float cv = cosf(angle), sv = sinf(angle);
+        float x0 = oracle_f16_to_f32(x[i]);
+        float x1 = oracle_f16_to_f32(x[i + half]);
+        x[i] = oracle_f32_to_f16(x0 * cv - x1 * sv);
+        x[i + half] = oracle_f32_to_f16(x1 * cv + x0 * sv);
+    }
+}
+
+/*
+ * oracle_mla_kv_prepare <- transformer.cpp:3935-3981, one token: RMSNorm of
+ * c_kv = kva[0:kv_rank] (sequential float sum of squares, scale
+ * 1/sqrt(ss/kv_rank + eps), kva[i] = f16((kva[i] * scale) * w[i])), then
+ * the NeoX RoPE of k_rope = kva[kv_rank : kv_rank + rope_dim].  kva and
+ * norm_w are f16 bit patterns; kva is updated in place.
+ */
+void oracle_mla_kv_prepare(uint16_t* kva, const uint16_t* norm_w, int kv_rank, int rope_dim, float eps, int pos,
+                           const float* freqs) {
+    float ss = 0.0f;
+    for (int i = 0; i < kv_rank; i++) {
+        float v = oracle_f16_to_f32(kva[i]);
+        ss += v * v;
+    }
+    ss = 1.0f / sqrtf(ss / (float)kv_rank + eps);
+    for (int i = 0; i < kv_rank; i++) {
+        float v = oracle_f16_to_f32(kva[i]) * ss;
+        kva[i] = oracle_f32_to_f16(v * oracle_f16_to_f32(norm_w[i]));
+    }
+    oracle_rope_neox_f16(kva + kv_rank, rope_dim, pos, freqs);
+}
+
+/*
+ * oracle_mla_latent_write <- transformer.cpp:3930-3987 (prepare, then the
+ * scatter of :3982-3987 to cache offset pos * (kv_rank + rope_dim)) for
+ * `rows` tokens: token r belongs to sequence r / rows_per_seq and goes to
+ * row positions[r] of that sequence's cache (seq_stride elements apart).
+ * Rows whose position is outside [0, max_seq_len) are not written.
+ */
+void oracle_mla_latent_write(const uint16_t* kv_a, const uint16_t* norm_w, const int32_t* positions,
+                             uint16_t* cache, int rows, int rows_per_seq, int64_t seq_stride, int max_seq_len,
+                             int kv_rank, int rope_dim, float eps, const float* freqs) {
+    int C = kv_rank + rope_dim;
+    uint16_t* tmp = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)C);
+    for (int r = 0; r < rows; r++) {
+        int pos = positions[r];
+        if (pos < 0 || pos >= max_seq_len) continue;
+        memcpy(tmp, kv_a + (size_t)r * C, sizeof(uint16_t) * (size_t)C);
+        oracle_mla_kv_prepare(tmp, norm_w, kv_rank, rope_dim, eps, pos, freqs);
+        memcpy(cache + (int64_t)(r / rows_per_seq) * seq_stride + (int64_t)pos * C, tmp, sizeof(uint16_t) * (size_t)C);
+    }
+    free(tmp);
 }
 
 /* ------------------------------------------------------------------ */

@@ -53,6 +53,11 @@ def lib():
         L.oracle_dequant_row.argtypes = [P, i32, i64, i32, P]
         L.oracle_mla_absorb.argtypes = [P, P, i32, P, i32, i32, i32, i32, i32]
         L.oracle_mla_project.argtypes = [P, P, i32, P, i32, i32, i32, i32]
+        L.oracle_yarn_rope_freq.argtypes = [i32, i32, f32, i32, f32]
+        L.oracle_yarn_rope_freq.restype = f32
+        L.oracle_rope_neox_f16.argtypes = [P, i32, i32, P]
+        L.oracle_mla_kv_prepare.argtypes = [P, P, i32, i32, f32, i32, P]
+        L.oracle_mla_latent_write.argtypes = [P, P, P, P, i32, i32, i64, i32, i32, i32, f32, P]
         L.oracle_num_threads.restype = ctypes.c_int
         _lib = L
     return _lib
@@ -199,6 +204,53 @@ def mla_project(o, w_vb, w_type, H, kv_rank=512, v_head=128):
     lib().oracle_mla_project(_p(o), _p(np.ascontiguousarray(w_vb, np.uint8)), w_type, _p(out), rows, H, kv_rank,
                              v_head)
     return out
+
+
+def yarn_freqs(rope_dim=64, factor=0.0, original_ctx=0, theta=10000.0):
+    """yarn_rope_freq (transformer.cpp:41-70) for i < rope_dim/2, float32."""
+    return np.array([lib().oracle_yarn_rope_freq(i, rope_dim, factor, original_ctx, theta)
+                     for i in range(rope_dim // 2)], np.float32)
+
+
+def rope_neox_f16(x_bits, pos, freqs):
+    """NeoX RoPE of one f16 vector (transformer.cpp:3903-3917); uint16 bits in/out."""
+    x = np.ascontiguousarray(x_bits, np.uint16).copy()
+    lib().oracle_rope_neox_f16(_p(x), x.size, int(pos), _p(np.ascontiguousarray(freqs, np.float32)))
+    return x
+
+
+def rope_q_f16(q_bits, positions, freqs, nope=128):
+    """q rope stage (transformer.cpp:3882-3921): q [rows, H, nope+rope]
+    uint16 f16 bits; the rope part of every head of row r rotated by
+    positions[r]."""
+    q = np.ascontiguousarray(q_bits, np.uint16).copy()
+    rows = q.shape[0]
+    for r in range(rows):
+        for h in range(q.shape[1]):
+            q[r, h, nope:] = rope_neox_f16(q[r, h, nope:], positions[r], freqs)
+    return q
+
+
+def mla_kv_prepare(kva_bits, norm_w_bits, pos, freqs, eps, kv_rank=512, rope=64):
+    """c_kv RMSNorm + k_rope RoPE of one token (transformer.cpp:3935-3981)."""
+    x = np.ascontiguousarray(kva_bits, np.uint16).copy()
+    lib().oracle_mla_kv_prepare(_p(x), _p(np.ascontiguousarray(norm_w_bits, np.uint16)), kv_rank, rope,
+                                float(eps), int(pos), _p(np.ascontiguousarray(freqs, np.float32)))
+    return x
+
+
+def mla_latent_write(kv_a_bits, norm_w_bits, positions, cache_bits, rows_per_seq, max_seq_len, freqs, eps,
+                     kv_rank=512, rope=64):
+    """Latent-cache writer (transformer.cpp:3930-3987) for every row of
+    kv_a [rows, kv_rank+rope]; cache [n_seq, max_T, kv_rank+rope] uint16,
+    returned updated (a copy)."""
+    kv = np.ascontiguousarray(kv_a_bits, np.uint16)
+    cache = np.ascontiguousarray(cache_bits, np.uint16).copy()
+    pos = np.ascontiguousarray(positions, np.int32)
+    lib().oracle_mla_latent_write(_p(kv), _p(np.ascontiguousarray(norm_w_bits, np.uint16)), _p(pos), _p(cache),
+                                  kv.shape[0], rows_per_seq, cache[0].size, max_seq_len, kv_rank, rope, float(eps),
+                                  _p(np.ascontiguousarray(freqs, np.float32)))
+    return cache
 
 
 def mla_full(q, w_kb, w_vb, w_type, latent, seq_lens, q_len, H, scale, nope=128, rope=64, kv_rank=512,

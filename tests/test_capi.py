@@ -184,3 +184,24 @@ def test_mla_absorb_project_validation():
         b = _capi.MlaProjectArgs.from_buffer_copy(p)
         setattr(b, field, val)
         assert L.mugen_attn_mla_project(ctypes.byref(b), None) == code, field
+
+
+def test_latent_write_validation():
+    L = _capi.lib()
+    a = _capi.MlaLatentWriteArgs()
+    a.kv_a = a.norm_w = a.positions = a.latent = 0x1000
+    a.rows, a.rows_per_seq, a.max_seq_len, a.kv_rank, a.rope_dim = 4, 1, 64, 512, 64
+    a.latent_dtype, a.seq_stride, a.eps = _capi.F16, 64 * 576, 1e-6
+    a.rope = _capi.RopeParams(10000.0, 40.0, 4096)
+    for field, val, code in [("kv_rank", 256, _capi.E_UNSUPPORTED), ("latent_dtype", _capi.F32, _capi.E_UNSUPPORTED),
+                             ("rows_per_seq", 0, _capi.E_INVALID), ("seq_stride", 100, _capi.E_INVALID),
+                             ("latent", 0x1008, _capi.E_INVALID), ("positions", 0, _capi.E_INVALID),
+                             ("eps", float("nan"), _capi.E_INVALID)]:
+        b = _capi.MlaLatentWriteArgs.from_buffer_copy(a)
+        setattr(b, field, val)
+        assert L.mugen_attn_mla_latent_write(ctypes.byref(b), None) == code, field
+    b = _capi.MlaLatentWriteArgs.from_buffer_copy(a)
+    b.rope = _capi.RopeParams(10000.0, 40.0, 0)     # YaRN needs the original context
+    assert L.mugen_attn_mla_latent_write(ctypes.byref(b), None) == _capi.E_INVALID
+    b.rope, b.rows = _capi.RopeParams(10000.0, 0.0, 0), 0
+    assert L.mugen_attn_mla_latent_write(ctypes.byref(b), None) == _capi.OK

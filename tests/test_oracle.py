@@ -290,3 +290,95 @@ def test_mla_full_is_absorb_core_project():
     o = O.mla_attention_np64(qa, c["lat"], c["seq_lens"], 2, 4, C.MLA_SCALE)
     ref = np.einsum("bthd,hjd->bthj", o, Wv)
     np.testing.assert_allclose(got, ref, rtol=2e-3, atol=2e-3 * np.abs(ref).max())
+
+
+# ------------------------------------------------------------ latent-cache writer
+
+def _f16(x):
+    return np.asarray(x, np.float32).astype(np.float16)
+
+
+def _bits(x):
+    return _f16(x).view(np.uint16)
+
+
+def _vals(bits):
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float64)
+
+
+def test_yarn_freqs_closed_form_and_deepseek_v3_correction_range():
+    base = O.yarn_freqs(64, 0.0, 0, 10000.0)  # factor <= 1: theta^(-2i/d)
+    np.testing.assert_allclose(base, 10000.0 ** (-2.0 * np.arange(32) / 64), rtol=2e-6)
+    assert np.array_equal(O.yarn_freqs(64, 1.0, 4096, 10000.0), base)
+    # DeepSeek-V3 (theta 1e4, factor 40, original ctx 4096, beta 32 / 1): the
+    # YaRN correction range is dims [10, 23] -- below it the base frequency,
+    # above it base / 40, a linear ramp over 13 steps in between
+    v3 = O.yarn_freqs(64, 40.0, 4096, 10000.0)
+    ratio = v3.astype(np.float64) / base
+    i = np.arange(32)
+    expect = np.where(i <= 10, 1.0, np.where(i >= 23, 1 / 40, 1 - (i - 10) / 13 * (1 - 1 / 40)))
+    np.testing.assert_allclose(ratio, expect, rtol=1e-5)
+
+
+def test_rope_neox_known_rotation_pairing_and_identity():
+    freqs = O.yarn_freqs(64, 0.0, 0, 10000.0)   # freqs[0] = 1
+    x = np.zeros(64, np.float32)
+    x[0] = 1.0
+    for pos in (1, 2, 7):
+        y = _vals(O.rope_neox_f16(_bits(x), pos, freqs))
+        # NeoX pairs (i, i + 32): e_0 -> (cos p, sin p) in dims 0 and 32
+        assert abs(y[0] - np.cos(pos)) <= 2 ** -11 and abs(y[32] - np.sin(pos)) <= 2 ** -11
+        assert np.count_nonzero(y) == 2
+    r = np.asarray(O.randn(3, (64,)), np.float32)
+    assert np.array_equal(O.rope_neox_f16(_bits(r), 0, freqs), _bits(r))   # pos 0: identity
+
+
+def test_rope_neox_preserves_pair_norms_and_composes():
+    freqs = O.yarn_freqs(64, 40.0, 4096, 10000.0)
+    x = _bits(O.randn(4, (64,)))
+    xv = _vals(x)
+    y = _vals(O.rope_neox_f16(x, 1000, freqs))
+    n0 = np.hypot(xv[:32], xv[32:])
+    n1 = np.hypot(y[:32], y[32:])
+    np.testing.assert_allclose(n1, n0, rtol=2e-3, atol=1e-3)
+    # rotating by a then by b == rotating by a + b (up to f16 roundings)
+    ab = _vals(O.rope_neox_f16(O.rope_neox_f16(x, 300, freqs), 200, freqs))
+    np.testing.assert_allclose(ab, _vals(O.rope_neox_f16(x, 500, freqs)), atol=4e-3)
+    # against an fp64 rotation
+    ang = 1000.0 * freqs.astype(np.float64)
+    ref0 = xv[:32] * np.cos(ang) - xv[32:] * np.sin(ang)
+    ref1 = xv[32:] * np.cos(ang) + xv[:32] * np.sin(ang)
+    np.testing.assert_allclose(y, np.concatenate([ref0, ref1]), atol=3e-3)
+
+
+def test_kv_prepare_rmsnorm_closed_forms():
+    freqs = O.yarn_freqs(64, 0.0, 0, 10000.0)
+    kva = np.full(576, 2.0, np.float32)
+    w = np.full(512, 0.5, np.float32)
+    out = _vals(O.mla_kv_prepare(_bits(kva), _bits(w), 0, freqs, 1e-6))
+    np.testing.assert_allclose(out[:512], 0.5, rtol=1e-3)          # 2 / rms(2) * 0.5
+    assert np.all(out[512:] == 2.0)                                 # pos 0: k_rope unrotated
+    # random vector against an fp64 RMSNorm, weights applied per dim
+    v = _f16(O.randn(5, (576,))).astype(np.float32)
+    wv = _f16(np.linspace(0.5, 1.5, 512)).astype(np.float32)
+    out = _vals(O.mla_kv_prepare(_bits(v), _bits(wv), 37, freqs, 1e-6))
+    v64 = v[:512].astype(np.float64)
+    ref = v64 / np.sqrt(np.mean(v64 * v64) + 1e-6) * wv
+    np.testing.assert_allclose(out[:512], ref, rtol=2e-3, atol=1e-4)
+    np.testing.assert_array_equal(out[512:], _vals(O.rope_neox_f16(_bits(v[512:]), 37, freqs)))
+
+
+def test_latent_write_rows_sequences_and_bounds():
+    freqs = O.yarn_freqs(64, 40.0, 4096, 10000.0)
+    kv = _bits(O.randn(6, (6, 576)))
+    w = _bits(O.randn(7, (512,), 1.0, 0.1))
+    cache = np.zeros((3, 16, 576), np.uint16)
+    pos = np.array([3, 4, 0, 15, 16, -1], np.int32)     # 2 rows per sequence; the last two out of range
+    out = O.mla_latent_write(kv, w, pos, cache, 2, 16, freqs, 1e-6)
+    for r, p in enumerate(pos[:4]):
+        np.testing.assert_array_equal(out[r // 2, p], O.mla_kv_prepare(kv[r], w, p, freqs, 1e-6))
+    written = {(0, 3), (0, 4), (1, 0), (1, 15)}
+    for b in range(3):
+        for t in range(16):
+            if (b, t) not in written:
+                assert not out[b, t].any()
