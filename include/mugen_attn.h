@@ -107,6 +107,88 @@ int mugen_attn_gqa_decode(const mugen_attn_gqa_decode_args* args, void* workspac
                           size_t workspace_bytes, void* stream);
 
 /*
+ * 4-bit group KV store: the reference's KVCache format (kv_cache.cpp:11-98)
+ * on the GPU.  Per sequence (and layer), the quantised tokens [0, n_q4)
+ * are kept as groups of 32 consecutive values of the token's
+ * [n_kv_heads*head_dim] row, 20 bytes each: f16 scale, f16 min, 16 bytes of
+ * nibbles (value 2i low, 2i+1 high), value = f16(min + nibble * scale).
+ * The newest tokens stay f16 in a ring of `ring` rows (token t at slot
+ * t % ring), as the reference keeps its newest fp16_preserve_last tokens.
+ *   q4_k, q4_v      [n_seq][max_seq_len][n_kv_heads*head_dim/32][20 B],
+ *                   q4_seq_stride bytes apart (a multiple of 4)
+ *   ring_k, ring_v  [n_seq][ring][n_kv_heads*head_dim] F16,
+ *                   ring_seq_stride elements apart (a multiple of 8)
+ */
+typedef struct mugen_attn_kv_q4_store {
+    void* q4_k;
+    void* q4_v;
+    void* ring_k;
+    void* ring_v;
+    int64_t q4_seq_stride;
+    int64_t ring_seq_stride;
+    int32_t ring;
+    int32_t fp16_preserve_last; /* the reference's KVCacheConfig field (256 in the engine) */
+} mugen_attn_kv_q4_store;
+
+/*
+ * Append n_new tokens to each of n_seq sequences (KVCache::append,
+ * kv_cache.cpp:163-216, applied n_new times): the new rows go to the ring,
+ * and the tokens that leave the newest fp16_preserve_last are quantised
+ * (quantize_group, kv_cache.cpp:21-56, bit for bit).
+ *   k_new, v_new  [n_seq][n_new][n_kv_heads*head_dim] F16
+ *   seq_lens      device [n_seq]: tokens held before the append
+ *   n_q4          device [n_seq]: of which quantised (the store's state;
+ *                 seq_lens - n_q4 <= fp16_preserve_last, as appends keep it)
+ *   n_q4_out      device [n_seq]: quantised tokens after the append; must
+ *                 not alias n_q4 (every layer's call reads the same n_q4)
+ * Requires ring >= fp16_preserve_last + n_new; tokens at positions
+ * >= max_seq_len are dropped (the reference's append refuses them).
+ */
+typedef struct mugen_attn_kv_q4_append_args {
+    mugen_attn_kv_q4_store store;
+    const void* k_new;
+    const void* v_new;
+    const int32_t* seq_lens;
+    const int32_t* n_q4;
+    int32_t* n_q4_out;
+    int32_t n_seq;
+    int32_t n_new;
+    int32_t n_kv_heads;
+    int32_t head_dim;
+    int32_t max_seq_len;
+} mugen_attn_kv_q4_append_args;
+int mugen_attn_kv_q4_append(const mugen_attn_kv_q4_append_args* args, void* stream);
+
+/*
+ * GQA decode straight from the 4-bit store: cpu_attention
+ * (transformer.cpp:2441-2485) over the K/V that KVCache::read_k / read_v
+ * return (kv_cache.cpp:218-278) -- dequantised groups for t < n_q4[b], the
+ * f16 ring rows for the rest -- without materialising them: 320 bytes per
+ * token and kv head set instead of 1024 at n_kv_heads*head_dim = 512.
+ * Same rules as mugen_attn_gqa_decode (q F16; out F16/BF16/F32; split-K
+ * workspace from mugen_attn_gqa_decode_q4_workspace_size).
+ */
+typedef struct mugen_attn_gqa_decode_q4_args {
+    const void* q;
+    mugen_attn_kv_q4_store store;
+    const int32_t* seq_lens;
+    const int32_t* n_q4;
+    void* out;
+    int32_t batch;
+    int32_t n_heads;
+    int32_t n_kv_heads;
+    int32_t head_dim;
+    int32_t max_seq_len;
+    int32_t num_splits;
+    float scale;
+    int32_t out_dtype;
+    const int32_t* seq_lens_host;
+} mugen_attn_gqa_decode_q4_args;
+size_t mugen_attn_gqa_decode_q4_workspace_size(const mugen_attn_gqa_decode_q4_args* args);
+int mugen_attn_gqa_decode_q4(const mugen_attn_gqa_decode_q4_args* args, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/*
  * GQA causal prefill (flash attention) over one sequence.
  * Replaces flash_prefill_attention (kernel_sources.h:2769-2896) and
  * make_prefill_attention_dp (transformer.cpp:828-850); same buffers and
@@ -326,7 +408,7 @@ const char* mugen_attn_version(void);
  * mugen_attn_timing_read synchronises on the recorded events and returns
  * the summed milliseconds and launch count of the kernel named `kernel`
  * ("gqa_decode", "gqa_decode_combine", "gqa_prefill", "mla_decode",
- * "mla_decode_combine", "mla_absorb", "mla_project", "mla_latent_write", "scatter_kv").
+ * "mla_decode_combine", "mla_absorb", "mla_project", "mla_latent_write", "kv_q4_append", "scatter_kv").
  */
 int mugen_attn_timing_enable(int enable);
 int mugen_attn_timing_read(const char* kernel, double* total_ms, int64_t* launches);

@@ -25,6 +25,9 @@ EXPORTS = (
     "mugen_attn_gqa_decode_workspace_size",
     "mugen_attn_gqa_decode",
     "mugen_attn_gqa_prefill",
+    "mugen_attn_kv_q4_append",
+    "mugen_attn_gqa_decode_q4_workspace_size",
+    "mugen_attn_gqa_decode_q4",
     "mugen_attn_mla_decode_workspace_size",
     "mugen_attn_mla_decode",
     "mugen_attn_mla_absorb",
@@ -50,6 +53,28 @@ class GqaDecodeArgs(ctypes.Structure):
         ("batch", _i32), ("n_heads", _i32), ("n_kv_heads", _i32), ("head_dim", _i32),
         ("max_seq_len", _i32), ("num_splits", _i32), ("seq_stride", _i64), ("scale", _f32),
         ("kv_dtype", _i32), ("out_dtype", _i32), ("seq_lens_host", _vp),
+    ]
+
+
+class KvQ4Store(ctypes.Structure):
+    _fields_ = [
+        ("q4_k", _vp), ("q4_v", _vp), ("ring_k", _vp), ("ring_v", _vp),
+        ("q4_seq_stride", _i64), ("ring_seq_stride", _i64), ("ring", _i32), ("fp16_preserve_last", _i32),
+    ]
+
+
+class KvQ4AppendArgs(ctypes.Structure):
+    _fields_ = [
+        ("store", KvQ4Store), ("k_new", _vp), ("v_new", _vp), ("seq_lens", _vp), ("n_q4", _vp), ("n_q4_out", _vp),
+        ("n_seq", _i32), ("n_new", _i32), ("n_kv_heads", _i32), ("head_dim", _i32), ("max_seq_len", _i32),
+    ]
+
+
+class GqaDecodeQ4Args(ctypes.Structure):
+    _fields_ = [
+        ("q", _vp), ("store", KvQ4Store), ("seq_lens", _vp), ("n_q4", _vp), ("out", _vp),
+        ("batch", _i32), ("n_heads", _i32), ("n_kv_heads", _i32), ("head_dim", _i32), ("max_seq_len", _i32),
+        ("num_splits", _i32), ("scale", _f32), ("out_dtype", _i32), ("seq_lens_host", _vp),
     ]
 
 
@@ -122,6 +147,12 @@ def lib() -> ctypes.CDLL:
         L.mugen_attn_gqa_decode_workspace_size.restype = ctypes.c_size_t
         L.mugen_attn_gqa_decode.argtypes = [ctypes.POINTER(GqaDecodeArgs), _vp, ctypes.c_size_t, _vp]
         L.mugen_attn_gqa_decode.restype = ctypes.c_int
+        L.mugen_attn_kv_q4_append.argtypes = [ctypes.POINTER(KvQ4AppendArgs), _vp]
+        L.mugen_attn_kv_q4_append.restype = ctypes.c_int
+        L.mugen_attn_gqa_decode_q4_workspace_size.argtypes = [ctypes.POINTER(GqaDecodeQ4Args)]
+        L.mugen_attn_gqa_decode_q4_workspace_size.restype = ctypes.c_size_t
+        L.mugen_attn_gqa_decode_q4.argtypes = [ctypes.POINTER(GqaDecodeQ4Args), _vp, ctypes.c_size_t, _vp]
+        L.mugen_attn_gqa_decode_q4.restype = ctypes.c_int
         L.mugen_attn_gqa_prefill.argtypes = [ctypes.POINTER(GqaPrefillArgs), _vp]
         L.mugen_attn_gqa_prefill.restype = ctypes.c_int
         L.mugen_attn_mla_decode_workspace_size.argtypes = [ctypes.POINTER(MlaDecodeArgs)]

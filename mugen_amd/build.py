@@ -18,7 +18,8 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB_NAME = "libmugen_attn.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-SOURCES = ["capi.hip", "gqa_decode.hip", "gqa_prefill.hip", "mla_cache.hip", "mla_decode.hip", "mla_proj.hip"]
+SOURCES = ["capi.hip", "gqa_decode.hip", "gqa_prefill.hip", "kv_q4.hip", "mla_cache.hip", "mla_decode.hip",
+           "mla_proj.hip"]
 ARCH = "gfx950"
 
 

@@ -206,7 +206,7 @@ static int gqa_chunk(const mugen_attn_gqa_decode_args* a) {
     return lo;
 }
 
-static int gqa_validate(const mugen_attn_gqa_decode_args* a) {
+static int gqa_validate(const mugen_attn_gqa_decode_args* a, bool ring_store = false) {
     if (!a) return fail(MUGEN_ATTN_E_INVALID, "gqa_decode: null args");
     if (!a->q || !a->k_cache || !a->v_cache || !a->seq_lens || !a->out)
         return fail(MUGEN_ATTN_E_INVALID, "gqa_decode: null tensor pointer");
@@ -222,7 +222,7 @@ static int gqa_validate(const mugen_attn_gqa_decode_args* a) {
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode: head_dim %d (supported: 64, 128)", a->head_dim);
     if (!is16(a->kv_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode: kv_dtype must be F16 or BF16");
     if (!is_out(a->out_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode: bad out_dtype");
-    if (a->batch > 1 && a->seq_stride < (int64_t)a->max_seq_len * a->n_kv_heads * a->head_dim)
+    if (!ring_store && a->batch > 1 && a->seq_stride < (int64_t)a->max_seq_len * a->n_kv_heads * a->head_dim)
         return fail(MUGEN_ATTN_E_INVALID, "gqa_decode: seq_stride %lld smaller than max_seq_len*Hk*D",
                     (long long)a->seq_stride);
     if (((uintptr_t)a->q | (uintptr_t)a->k_cache | (uintptr_t)a->v_cache) & 15)
@@ -342,6 +342,139 @@ extern "C" {
 const char* mugen_attn_last_error(void) { return g_last_error.c_str(); }
 
 const char* mugen_attn_version(void) { return "mugen_attn 0.1.0 (gfx950, abi 1)"; }
+
+// ------------------------------------------------------------------ 4-bit store
+
+static int q4_store_validate(const mugen_attn_kv_q4_store& st, int n_seq, int vpt, int max_seq_len, const char* who) {
+    if (!st.q4_k || !st.q4_v || !st.ring_k || !st.ring_v) return fail(MUGEN_ATTN_E_INVALID, "%s: null store pointer", who);
+    if (st.ring <= 0 || st.fp16_preserve_last < 0) return fail(MUGEN_ATTN_E_INVALID, "%s: bad ring / fp16_preserve_last", who);
+    if (vpt % 32) return fail(MUGEN_ATTN_E_UNSUPPORTED, "%s: n_kv_heads*head_dim must be a multiple of 32", who);
+    const int64_t q4_row = (int64_t)vpt / 32 * 20;
+    if (n_seq > 1 && (st.q4_seq_stride < q4_row * max_seq_len || st.ring_seq_stride < (int64_t)st.ring * vpt))
+        return fail(MUGEN_ATTN_E_INVALID, "%s: sequence strides smaller than one store", who);
+    if ((((uintptr_t)st.q4_k | (uintptr_t)st.q4_v) & 3) || (st.q4_seq_stride & 3))
+        return fail(MUGEN_ATTN_E_INVALID, "%s: Q4 stores must be 4-byte aligned", who);
+    if ((((uintptr_t)st.ring_k | (uintptr_t)st.ring_v) & 15) || (st.ring_seq_stride % 8))
+        return fail(MUGEN_ATTN_E_INVALID, "%s: rings must be 16-byte aligned, strides multiples of 8", who);
+    return MUGEN_ATTN_OK;
+}
+
+int mugen_attn_kv_q4_append(const mugen_attn_kv_q4_append_args* a, void* stream) {
+    if (!a) return fail(MUGEN_ATTN_E_INVALID, "kv_q4_append: null args");
+    if (a->n_seq < 0 || a->n_new < 0 || a->n_kv_heads <= 0 || a->head_dim <= 0 || a->max_seq_len <= 0)
+        return fail(MUGEN_ATTN_E_INVALID, "kv_q4_append: bad sizes");
+    if (a->n_seq == 0 || a->n_new == 0) return MUGEN_ATTN_OK;
+    const int vpt = a->n_kv_heads * a->head_dim;
+    if (int rc = q4_store_validate(a->store, a->n_seq, vpt, a->max_seq_len, "kv_q4_append")) return rc;
+    if (!a->k_new || !a->v_new || !a->seq_lens || !a->n_q4 || !a->n_q4_out)
+        return fail(MUGEN_ATTN_E_INVALID, "kv_q4_append: null pointer");
+    if (a->n_q4_out == a->n_q4) return fail(MUGEN_ATTN_E_INVALID, "kv_q4_append: n_q4_out aliases n_q4");
+    if (a->store.ring < a->store.fp16_preserve_last + a->n_new)
+        return fail(MUGEN_ATTN_E_INVALID, "kv_q4_append: ring %d < fp16_preserve_last + n_new", a->store.ring);
+    if (((uintptr_t)a->k_new | (uintptr_t)a->v_new) & 15)
+        return fail(MUGEN_ATTN_E_INVALID, "kv_q4_append: k_new/v_new must be 16-byte aligned");
+    if ((int64_t)a->n_new * 2 > INT32_MAX || a->n_seq > 65535)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "kv_q4_append: too many tokens / sequences");
+    KvQ4AppendParams p{};
+    p.k_new = static_cast<const uint16_t*>(a->k_new);
+    p.v_new = static_cast<const uint16_t*>(a->v_new);
+    p.q4k = static_cast<uint8_t*>(a->store.q4_k);
+    p.q4v = static_cast<uint8_t*>(a->store.q4_v);
+    p.ring_k = static_cast<uint16_t*>(a->store.ring_k);
+    p.ring_v = static_cast<uint16_t*>(a->store.ring_v);
+    p.seq_lens = a->seq_lens;
+    p.n_q4 = a->n_q4;
+    p.n_q4_out = a->n_q4_out;
+    p.q4_seq_stride = a->store.q4_seq_stride;
+    p.ring_seq_stride = a->store.ring_seq_stride;
+    p.n_new = a->n_new;
+    p.vpt = vpt;
+    p.ring = a->store.ring;
+    p.preserve = a->store.fp16_preserve_last;
+    p.max_seq_len = a->max_seq_len;
+    return hip_status(launch_kv_q4_append(p, a->n_seq, static_cast<hipStream_t>(stream), active_timer()),
+                      "kv_q4_append launch");
+}
+
+// the f16 view of a 4-bit store decode for the shared planner / validation
+static mugen_attn_gqa_decode_args q4_as_gqa(const mugen_attn_gqa_decode_q4_args* a) {
+    mugen_attn_gqa_decode_args g{};
+    g.q = a->q;
+    g.k_cache = a->store.ring_k;
+    g.v_cache = a->store.ring_v;
+    g.seq_lens = a->seq_lens;
+    g.out = a->out;
+    g.batch = a->batch;
+    g.n_heads = a->n_heads;
+    g.n_kv_heads = a->n_kv_heads;
+    g.head_dim = a->head_dim;
+    g.max_seq_len = a->max_seq_len;
+    g.num_splits = a->num_splits;
+    g.seq_stride = a->store.ring_seq_stride;
+    g.scale = a->scale;
+    g.kv_dtype = DT_F16;
+    g.out_dtype = a->out_dtype;
+    g.seq_lens_host = a->seq_lens_host;
+    return g;
+}
+
+static int gqa_q4_validate(const mugen_attn_gqa_decode_q4_args* a) {
+    if (!a) return fail(MUGEN_ATTN_E_INVALID, "gqa_decode_q4: null args");
+    const mugen_attn_gqa_decode_args g = q4_as_gqa(a);
+    if (int rc = gqa_validate(&g, true)) return rc;
+    if (!a->n_q4) return fail(MUGEN_ATTN_E_INVALID, "gqa_decode_q4: null n_q4");
+    return q4_store_validate(a->store, a->batch, a->n_kv_heads * a->head_dim, a->max_seq_len, "gqa_decode_q4");
+}
+
+size_t mugen_attn_gqa_decode_q4_workspace_size(const mugen_attn_gqa_decode_q4_args* a) {
+    if (gqa_q4_validate(a) != MUGEN_ATTN_OK) return 0;
+    const mugen_attn_gqa_decode_args g = q4_as_gqa(a);
+    return gqa_ws(&g, gqa_chunk(&g), nullptr);
+}
+
+int mugen_attn_gqa_decode_q4(const mugen_attn_gqa_decode_q4_args* a, void* ws, size_t ws_bytes, void* stream) {
+    if (int rc = gqa_q4_validate(a)) return rc;
+    const mugen_attn_gqa_decode_args g = q4_as_gqa(a);
+    const int chunk = gqa_chunk(&g);
+    int splits = 1;
+    const size_t need = gqa_ws(&g, chunk, &splits);
+    if (need > 0 && (!ws || ws_bytes < need))
+        return fail(MUGEN_ATTN_E_WORKSPACE, "gqa_decode_q4: workspace of %zu bytes required, %zu given", need,
+                    ws_bytes);
+    GqaDecodeParams p{};
+    p.B = a->batch;
+    p.Hk = a->n_kv_heads;
+    p.q = static_cast<const uint16_t*>(a->q);
+    p.k = static_cast<const uint16_t*>(a->store.ring_k);
+    p.v = static_cast<const uint16_t*>(a->store.ring_v);
+    p.seq_lens = a->seq_lens;
+    p.out = a->out;
+    p.H = a->n_heads;
+    p.G = a->n_heads / a->n_kv_heads;
+    p.row_stride = a->n_kv_heads * a->head_dim;
+    p.chunk = chunk;
+    p.num_splits = splits;
+    p.seq_stride = a->store.ring_seq_stride;
+    const float scale = a->scale > 0.f ? a->scale : 1.f / sqrtf((float)a->head_dim);
+    p.scale_log2 = scale * kLog2e;
+    p.q4k = static_cast<const uint8_t*>(a->store.q4_k);
+    p.q4v = static_cast<const uint8_t*>(a->store.q4_v);
+    p.n_q4 = a->n_q4;
+    p.q4_seq_stride = a->store.q4_seq_stride;
+    p.q4_row_bytes = a->n_kv_heads * a->head_dim / 32 * 20;
+    p.ring = a->store.ring;
+    if (splits > 1) {
+        float* base = align256(ws);
+        const size_t slots = (size_t)a->batch * a->n_heads * splits;
+        p.ws_o = base;
+        p.ws_ml = base + slots * a->head_dim;
+    }
+    const int64_t nwg = gqa_items(&g, chunk);
+    if (nwg > INT32_MAX) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode_q4: too many work items");
+    return hip_status(launch_gqa_decode_q4(p, (int)nwg, a->head_dim, a->out_dtype, static_cast<hipStream_t>(stream),
+                                           active_timer()),
+                      "gqa_decode_q4 launch");
+}
 
 size_t mugen_attn_gqa_decode_workspace_size(const mugen_attn_gqa_decode_args* a) {
     if (gqa_validate(a) != MUGEN_ATTN_OK) return 0;

@@ -48,9 +48,26 @@ __device__ constexpr int vswz(int r) {
         return ((r & 1) * 2) ^ (((r >> 1) & 1) * 4) ^ (((r >> 3) & 1) * 8) ^ ((r >> 4) & 1);
 }
 
+// Eight values of a 20-byte 4-bit group (dequantize_group,
+// kv_cache.cpp:58-73): `sm` = the group's f16 scale (low half) and min
+// (high half), `nib` = the 4 bytes holding values 2i (low nibble) and 2i+1
+// (high nibble); each value f16(min + nibble * scale), product and sum
+// rounded separately as there.
+__device__ __forceinline__ u32x4_t dequant_q4x8(uint32_t sm, uint32_t nib) {
+#pragma clang fp contract(off)
+    const float sf = lo_f32<DT_F16>(sm), mf = hi_f32<DT_F16>(sm);
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t byte = (nib >> (8 * e)) & 0xffu;
+        w[e] = pack2<DT_F16>(mf + (float)(byte & 15u) * sf, mf + (float)(byte >> 4) * sf);
+    }
+    return u32x4_t{w[0], w[1], w[2], w[3]};
+}
+
 }  // namespace
 
-template <int D, int DT, int OUT_DT>
+template <int D, int DT, int OUT_DT, bool Q4 = false>
 __global__ __launch_bounds__(256) void gqa_decode_kernel(GqaDecodeParams p) {
     constexpr int KK = D / 32;           // MFMA k-steps of S
     constexpr int DB = D / 16;           // 16-dim blocks of O^T
@@ -91,6 +108,25 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(GqaDecodeParams p) {
 
     const uint16_t* kbase = p.k + (int64_t)b * p.seq_stride + (int64_t)kvh * D;
     const uint16_t* vbase = p.v + (int64_t)b * p.seq_stride + (int64_t)kvh * D;
+    // 4-bit store: tokens below nq are groups (group kvh*D/32 + c of a token
+    // row holds dims 32c .. 32c+31 of this kv head), the rest ring rows
+    const int nq = Q4 ? p.n_q4[b] : 0;
+    const uint8_t* q4kb = Q4 ? p.q4k + (int64_t)b * p.q4_seq_stride + (int64_t)kvh * (D / 32) * 20 : nullptr;
+    const uint8_t* q4vb = Q4 ? p.q4v + (int64_t)b * p.q4_seq_stride + (int64_t)kvh * (D / 32) * 20 : nullptr;
+    // 8 consecutive dims d0 (a multiple of 8) of token t
+    auto load8 = [&](const uint16_t* base, const uint8_t* q4base, int t, int d0) -> u32x4_t {
+        if constexpr (Q4) {
+            if (t < nq) {
+                const uint8_t* grp = q4base + (int64_t)t * p.q4_row_bytes + (d0 >> 5) * 20;
+                const uint32_t sm = *reinterpret_cast<const uint32_t*>(grp);
+                const uint32_t nib = *reinterpret_cast<const uint32_t*>(grp + 4 + ((d0 & 31) >> 1));
+                return dequant_q4x8(sm, nib);
+            }
+            return load16(base + (int64_t)(t % p.ring) * p.row_stride + d0);
+        } else {
+            return load16(base + (int64_t)t * p.row_stride + d0);
+        }
+    };
 
     // Q^T as the B operand: lane holds q[head n][32kk + 8g .. +8]
     u32x4_t qf[KK];
@@ -109,14 +145,13 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(GqaDecodeParams p) {
 #pragma unroll
         for (int nb = 0; nb < 2; nb++) {
             const int tk = min(t0 + kr0 + 4 * nb, t_end - 1);
-            const uint16_t* kp = kbase + (int64_t)tk * p.row_stride + 8 * g;
 #pragma unroll
-            for (int kk = 0; kk < KK; kk++) kq[nb][kk] = load16(kp + 32 * kk);
+            for (int kk = 0; kk < KK; kk++) kq[nb][kk] = load8(kbase, q4kb, tk, 32 * kk + 8 * g);
         }
 #pragma unroll
         for (int j = 0; j < VL; j++) {
             const int tv = min(t0 + j * RPL + lane / (RB / 16), t_end - 1);
-            vq[j] = load16(vbase + (int64_t)tv * p.row_stride + 8 * (lane % (RB / 16)));
+            vq[j] = load8(vbase, q4vb, tv, 8 * (lane % (RB / 16)));
         }
     };
     // V staging: load j of lane l is row j*RPL + l/(RB/16), chunk l%(RB/16)
@@ -292,10 +327,10 @@ __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p
 
 // ------------------------------------------------------------------ launch
 
-template <int D, int DT, int OUT_DT>
+template <int D, int DT, int OUT_DT, bool Q4 = false>
 static hipError_t launch_gqa_t(const GqaDecodeParams& p, int nwg, hipStream_t st, KernelTimer* timer) {
     timer_begin(timer, "gqa_decode", st);
-    hipLaunchKernelGGL((gqa_decode_kernel<D, DT, OUT_DT>), dim3(nwg), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gqa_decode_kernel<D, DT, OUT_DT, Q4>), dim3(nwg), dim3(256), 0, st, p);
     timer_end(timer, "gqa_decode", st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.num_splits == 1) return e;
@@ -325,6 +360,21 @@ hipError_t launch_gqa_decode(const GqaDecodeParams& p, int nwg, int D, int kv_dt
                              KernelTimer* t) {
     if (D == 128) return launch_gqa_g<128>(p, nwg, kv_dt, out_dt, st, t);
     return launch_gqa_g<64>(p, nwg, kv_dt, out_dt, st, t);
+}
+
+// 4-bit store: f16 values (the reference's format), fp16 MFMA
+template <int D>
+static hipError_t launch_gqa_q4_d(const GqaDecodeParams& p, int nwg, int out_dt, hipStream_t st, KernelTimer* t) {
+    switch (out_dt) {
+        case DT_F32: return launch_gqa_t<D, DT_F16, DT_F32, true>(p, nwg, st, t);
+        case DT_F16: return launch_gqa_t<D, DT_F16, DT_F16, true>(p, nwg, st, t);
+        default: return launch_gqa_t<D, DT_F16, DT_BF16, true>(p, nwg, st, t);
+    }
+}
+
+hipError_t launch_gqa_decode_q4(const GqaDecodeParams& p, int nwg, int D, int out_dt, hipStream_t st, KernelTimer* t) {
+    if (D == 128) return launch_gqa_q4_d<128>(p, nwg, out_dt, st, t);
+    return launch_gqa_q4_d<64>(p, nwg, out_dt, st, t);
 }
 
 }  // namespace mugen_attn

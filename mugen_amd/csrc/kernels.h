@@ -33,11 +33,42 @@ struct GqaDecodeParams {
     int num_splits;
     int64_t seq_stride;
     float scale_log2;  // softmax scale * log2(e)
+    // 4-bit group store (gqa_decode_q4): tokens [0, n_q4[b]) come from the
+    // 20-byte groups of q4k / q4v, the others from the f16 ring in k / v
+    // (token t at slot t % ring; seq_stride and row_stride describe the ring)
+    const uint8_t* q4k;
+    const uint8_t* q4v;
+    const int32_t* n_q4;
+    int64_t q4_seq_stride;  // bytes between sequences' Q4 stores
+    int q4_row_bytes;       // bytes per token (Hk * D / 32 groups of 20)
+    int ring;
 };
 
 // nwg: workgroups of the compact work list (exact, or an upper bound)
 hipError_t launch_gqa_decode(const GqaDecodeParams& p, int nwg, int D, int kv_dt, int out_dt, hipStream_t st,
                              KernelTimer* t);
+hipError_t launch_gqa_decode_q4(const GqaDecodeParams& p, int nwg, int D, int out_dt, hipStream_t st, KernelTimer* t);
+
+// 4-bit group store append (kv_q4.hip)
+struct KvQ4AppendParams {
+    const uint16_t* k_new;   // [n_seq][n_new][vpt]
+    const uint16_t* v_new;
+    uint8_t* q4k;
+    uint8_t* q4v;
+    uint16_t* ring_k;
+    uint16_t* ring_v;
+    const int32_t* seq_lens;
+    const int32_t* n_q4;
+    int32_t* n_q4_out;
+    int64_t q4_seq_stride;
+    int64_t ring_seq_stride;
+    int n_new;
+    int vpt;
+    int ring;
+    int preserve;
+    int max_seq_len;
+};
+hipError_t launch_kv_q4_append(const KvQ4AppendParams& p, int n_seq, hipStream_t st, KernelTimer* t);
 
 struct GqaPrefillParams {
     const uint16_t* q;

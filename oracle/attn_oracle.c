@@ -37,6 +37,10 @@
  *   oracle_mla_kv_prepare <- c_kv RMSNorm + k_rope RoPE, transformer.cpp:3935-3981
  *   oracle_mla_latent_write <- prepare + scatter into the latent cache,
  *                            transformer.cpp:3930-3987
+ *   oracle_q4_*           <- quantize_group / dequantize_group / *_token,
+ *                            src/core/memory/kv_cache.cpp:21-97
+ *   oracle_kvq4_read      <- KVCache::append + read_k / read_v,
+ *                            src/core/memory/kv_cache.cpp:163-278
  *   oracle_scatter_kv     <- scatter_kv, src/metal/kernel_sources.h:3018-3028
  *
  * The summation orders above are kept (sequential fp32 sums, expf, divide
@@ -571,6 +575,100 @@ void oracle_mla_latent_write(const uint16_t* kv_a, const uint16_t* norm_w, const
         memcpy(cache + (int64_t)(r / rows_per_seq) * seq_stride + (int64_t)pos * C, tmp, sizeof(uint16_t) * (size_t)C);
     }
     free(tmp);
+}
+
+/* ------------------------------------------------------------------ */
+/* 4-bit group KV store (kv_cache.cpp)                                 */
+/* ------------------------------------------------------------------ */
+/*
+ * oracle_q4_quantize_group <- quantize_group, kv_cache.cpp:21-56: a group
+ * of up to 32 f16 values (missing ones are 0 and take part in min / max)
+ * becomes 20 bytes: f16 scale = f16(range / 15) (0 when max == min), f16
+ * min, then 16 bytes whose low / high nibble holds value 2i / 2i+1 as
+ * min(15, roundf((v - min) / scale)) (all nibbles 0 when scale is 0).
+ */
+void oracle_q4_quantize_group(const uint16_t* src, uint8_t* dst, int count) {
+    float vals[32];
+    uint16_t bits[32];
+    for (int i = 0; i < 32; i++) {
+        bits[i] = i < count ? src[i] : 0;
+        vals[i] = oracle_f16_to_f32(bits[i]);
+    }
+    int lo = 0, hi = 0;
+    for (int i = 1; i < 32; i++) {
+        if (vals[i] < vals[lo]) lo = i;
+        if (vals[i] > vals[hi]) hi = i;
+    }
+    float range = vals[hi] - vals[lo];
+    uint16_t scale = range == 0.0f ? 0 : oracle_f32_to_f16(range / 15.0f);
+    uint16_t minv = bits[lo];
+    memcpy(dst, &scale, 2);
+    memcpy(dst + 2, &minv, 2);
+    float sf = oracle_f16_to_f32(scale), mf = oracle_f16_to_f32(minv);
+    for (int i = 0; i < 16; i++) {
+        uint8_t n0 = 0, n1 = 0;
+        if (sf > 0.0f) {
+            float a = roundf((vals[2 * i] - mf) / sf), b = roundf((vals[2 * i + 1] - mf) / sf);
+            n0 = (uint8_t)(a < 15.0f ? a : 15.0f);
+            n1 = (uint8_t)(b < 15.0f ? b : 15.0f);
+        }
+        dst[4 + i] = (uint8_t)((n1 << 4) | n0);
+    }
+}
+
+/*
+ * oracle_q4_dequantize_group <- dequantize_group, kv_cache.cpp:58-73:
+ * value 2i / 2i+1 = f16(min + nibble * scale), product and sum rounded
+ * separately.
+ */
+void oracle_q4_dequantize_group(const uint8_t* src, uint16_t* dst) {
+    uint16_t scale, minv;
+    memcpy(&scale, src, 2);
+    memcpy(&minv, src + 2, 2);
+    float sf = oracle_f16_to_f32(scale), mf = oracle_f16_to_f32(minv);
+    for (int i = 0; i < 16; i++) {
+        uint8_t packed = src[4 + i];
+        dst[2 * i] = oracle_f32_to_f16(mf + (float)(packed & 0x0F) * sf);
+        dst[2 * i + 1] = oracle_f32_to_f16(mf + (float)((packed >> 4) & 0x0F) * sf);
+    }
+}
+
+/* quantize_token / dequantize_token (kv_cache.cpp:75-97): groups of 32
+ * consecutive values of the token's [n_kv_heads * head_dim] row, the last
+ * one possibly short. */
+void oracle_q4_quantize_token(const uint16_t* src, uint8_t* dst, int vpt) {
+    for (int g = 0; g * 32 < vpt; g++) {
+        int cnt = vpt - g * 32 < 32 ? vpt - g * 32 : 32;
+        oracle_q4_quantize_group(src + g * 32, dst + g * 20, cnt);
+    }
+}
+void oracle_q4_dequantize_token(const uint8_t* src, uint16_t* dst, int vpt) {
+    uint16_t tmp[32];
+    for (int g = 0; g * 32 < vpt; g++) {
+        int cnt = vpt - g * 32 < 32 ? vpt - g * 32 : 32;
+        oracle_q4_dequantize_group(src + g * 20, tmp);
+        memcpy(dst + g * 32, tmp, sizeof(uint16_t) * (size_t)cnt);
+    }
+}
+
+/*
+ * oracle_kvq4_read <- KVCache::read_k / read_v (kv_cache.cpp:218-278) of a
+ * layer whose first n_q4 tokens were quantised on append (append,
+ * kv_cache.cpp:163-216: every token older than the newest
+ * fp16_preserve_last is quantised from its own f16 values): tokens < n_q4
+ * come back as dequant(quant(x)), the rest unchanged.  x [T][vpt] f16 bits.
+ */
+void oracle_kvq4_read(const uint16_t* x, uint16_t* out, int T, int vpt, int n_q4) {
+    uint8_t* q = (uint8_t*)malloc((size_t)((vpt + 31) / 32) * 20);
+    for (int t = 0; t < T; t++) {
+        if (t < n_q4) {
+            oracle_q4_quantize_token(x + (size_t)t * vpt, q, vpt);
+            oracle_q4_dequantize_token(q, out + (size_t)t * vpt, vpt);
+        } else {
+            memcpy(out + (size_t)t * vpt, x + (size_t)t * vpt, sizeof(uint16_t) * (size_t)vpt);
+        }
+    }
+    free(q);
 }
 
 /* ------------------------------------------------------------------ */

@@ -53,6 +53,11 @@ def lib():
         L.oracle_dequant_row.argtypes = [P, i32, i64, i32, P]
         L.oracle_mla_absorb.argtypes = [P, P, i32, P, i32, i32, i32, i32, i32]
         L.oracle_mla_project.argtypes = [P, P, i32, P, i32, i32, i32, i32]
+        L.oracle_q4_quantize_group.argtypes = [P, P, i32]
+        L.oracle_q4_dequantize_group.argtypes = [P, P]
+        L.oracle_q4_quantize_token.argtypes = [P, P, i32]
+        L.oracle_q4_dequantize_token.argtypes = [P, P, i32]
+        L.oracle_kvq4_read.argtypes = [P, P, i32, i32, i32]
         L.oracle_yarn_rope_freq.argtypes = [i32, i32, f32, i32, f32]
         L.oracle_yarn_rope_freq.restype = f32
         L.oracle_rope_neox_f16.argtypes = [P, i32, i32, P]
@@ -251,6 +256,50 @@ def mla_latent_write(kv_a_bits, norm_w_bits, positions, cache_bits, rows_per_seq
                                   kv.shape[0], rows_per_seq, cache[0].size, max_seq_len, kv_rank, rope, float(eps),
                                   _p(np.ascontiguousarray(freqs, np.float32)))
     return cache
+
+
+def q4_quantize_group(bits, count=None):
+    """quantize_group (kv_cache.cpp:21-56): up to 32 f16 bit patterns -> 20 bytes."""
+    src = np.zeros(32, np.uint16)
+    bits = np.asarray(bits, np.uint16)
+    src[:bits.size] = bits
+    out = np.zeros(20, np.uint8)
+    lib().oracle_q4_quantize_group(_p(src), _p(out), bits.size if count is None else count)
+    return out
+
+
+def q4_dequantize_group(group):
+    out = np.zeros(32, np.uint16)
+    lib().oracle_q4_dequantize_group(_p(np.ascontiguousarray(group, np.uint8)), _p(out))
+    return out
+
+
+def q4_quantize_tokens(bits):
+    """quantize_token for each row of [T, vpt] f16 bits -> [T, groups*20] bytes."""
+    x = np.ascontiguousarray(bits, np.uint16)
+    T, vpt = x.shape
+    out = np.zeros((T, (vpt + 31) // 32 * 20), np.uint8)
+    for t in range(T):
+        lib().oracle_q4_quantize_token(_p(x[t]), _p(out[t]), vpt)
+    return out
+
+
+def q4_dequantize_tokens(q, vpt):
+    q = np.ascontiguousarray(q, np.uint8)
+    out = np.zeros((q.shape[0], vpt), np.uint16)
+    for t in range(q.shape[0]):
+        lib().oracle_q4_dequantize_token(_p(q[t]), _p(out[t]), vpt)
+    return out
+
+
+def kvq4_read(bits, n_q4):
+    """KVCache::read_k / read_v of [T, vpt] f16 bits whose first n_q4 tokens
+    were quantised (kv_cache.cpp:163-278)."""
+    x = np.ascontiguousarray(bits, np.uint16)
+    T, vpt = x.shape
+    out = np.empty_like(x)
+    lib().oracle_kvq4_read(_p(x), _p(out), T, vpt, int(n_q4))
+    return out
 
 
 def mla_full(q, w_kb, w_vb, w_type, latent, seq_lens, q_len, H, scale, nope=128, rope=64, kv_rank=512,

@@ -205,3 +205,28 @@ def test_latent_write_validation():
     assert L.mugen_attn_mla_latent_write(ctypes.byref(b), None) == _capi.E_INVALID
     b.rope, b.rows = _capi.RopeParams(10000.0, 0.0, 0), 0
     assert L.mugen_attn_mla_latent_write(ctypes.byref(b), None) == _capi.OK
+
+
+def test_kv_q4_validation():
+    L = _capi.lib()
+    st = _capi.KvQ4Store(0x1000, 0x1000, 0x1000, 0x1000, 64 * 320, 300 * 512, 300, 256)
+    a = _capi.KvQ4AppendArgs()
+    a.store = st
+    a.k_new = a.v_new = a.seq_lens = a.n_q4 = 0x1000
+    a.n_q4_out = 0x2000
+    a.n_seq, a.n_new, a.n_kv_heads, a.head_dim, a.max_seq_len = 2, 8, 4, 128, 64
+    # every case below fails validation on the host (nothing is launched)
+    for field, val in [("n_q4_out", 0x1000), ("k_new", 0x1004), ("n_new", 45)]:
+        b = _capi.KvQ4AppendArgs.from_buffer_copy(a)
+        setattr(b, field, val)
+        assert L.mugen_attn_kv_q4_append(ctypes.byref(b), None) == _capi.E_INVALID, field
+    b = _capi.KvQ4AppendArgs.from_buffer_copy(a)
+    b.n_kv_heads, b.head_dim = 3, 10                                              # 30 values: not whole groups
+    assert L.mugen_attn_kv_q4_append(ctypes.byref(b), None) == _capi.E_UNSUPPORTED
+    d = _capi.GqaDecodeQ4Args()
+    d.q, d.store, d.seq_lens, d.n_q4, d.out = 0x1000, st, 0x1000, 0, 0x1000
+    d.batch, d.n_heads, d.n_kv_heads, d.head_dim, d.max_seq_len, d.out_dtype = 2, 28, 4, 128, 64, _capi.F16
+    assert L.mugen_attn_gqa_decode_q4(ctypes.byref(d), None, 0, None) == _capi.E_INVALID   # null n_q4
+    d.n_q4 = 0x1000
+    d.store.q4_k = 0x1002
+    assert L.mugen_attn_gqa_decode_q4(ctypes.byref(d), None, 0, None) == _capi.E_INVALID   # misaligned store

@@ -382,3 +382,64 @@ def test_latent_write_rows_sequences_and_bounds():
         for t in range(16):
             if (b, t) not in written:
                 assert not out[b, t].any()
+
+
+# ------------------------------------------------------------ 4-bit group KV store
+
+def test_q4_group_known_answers():
+    # values 0..15 twice: min 0, range 15 -> scale exactly 1, nibbles = values;
+    # value 2i in the low nibble of byte i, 2i+1 in the high one
+    v = np.concatenate([np.arange(16), np.arange(16)]).astype(np.float16)
+    g = O.q4_quantize_group(v.view(np.uint16))
+    assert g[0:2].view(np.float16)[0] == 1.0 and g[2:4].view(np.float16)[0] == 0.0
+    expect = [(int(v[2 * i + 1]) << 4) | int(v[2 * i]) for i in range(16)]
+    assert list(g[4:]) == expect
+    assert np.array_equal(O.q4_dequantize_group(g), v.view(np.uint16))     # exact round trip
+    # a constant group: scale 0, nibbles 0, every value comes back as the min
+    c = np.full(32, -3.25, np.float16)
+    gc = O.q4_quantize_group(c.view(np.uint16))
+    assert gc[0:2].view(np.float16)[0] == 0.0 and not gc[4:].any()
+    assert np.all(O.q4_dequantize_group(gc).view(np.float16) == -3.25)
+    # a short group: the zero padding takes part in min / max (all-positive
+    # values get min 0), round-half-away: (v - 0) / (30/15) = 2.5 -> 3
+    s = np.array([5.0, 30.0], np.float16)
+    gs = O.q4_quantize_group(s.view(np.uint16))
+    assert gs[0:2].view(np.float16)[0] == 2.0 and gs[2:4].view(np.float16)[0] == 0.0
+    assert gs[4] == (15 << 4) | 3 and not gs[5:].any()
+
+
+def _fill_token(vpt, base):
+    # the reference test's fill_token: f16(base + 0.01 i)
+    return (base + np.float32(0.01) * np.arange(vpt, dtype=np.float32)).astype(np.float16).view(np.uint16)
+
+
+def test_q4_store_reference_test_properties():
+    # test_kv_cache.cpp:128-177 (4 heads x 64, preserve 32, 128 tokens):
+    # quantised tokens within 10% relative, the fp16 tail exact
+    vpt, T, keep = 256, 128, 32
+    k = np.stack([_fill_token(vpt, 1.0 + 0.05 * t) for t in range(T)])
+    got = O.kvq4_read(k, T - keep)
+    kv, gv = k.view(np.float16).astype(np.float32), got.view(np.float16).astype(np.float32)
+    rel = np.abs(kv - gv) / np.maximum(np.abs(kv), 1e-6)
+    assert rel[:T - keep].max() < 0.10 and rel[:T - keep].max() > 0
+    assert np.array_equal(got[T - keep:], k[T - keep:])
+    # test_compression_ratio: 64 / 20 bytes per group of 32
+    assert O.q4_quantize_tokens(k[:1]).nbytes * 3.2 == vpt * 2
+
+
+def test_q4_error_bound_and_extremes():
+    # |x - deq(q(x))| <= scale / 2 (+ f16 rounding) per value; in every
+    # group the minimum gets nibble 0 and the maximum nibble 15
+    x = O.round_to(O.randn(61, (64, 512), 0.0, 2.0), C.F16)[1]
+    q = O.q4_quantize_tokens(x)
+    d = O.q4_dequantize_tokens(q, 512)
+    sc = q.reshape(64, 16, 20)[:, :, 0:2].copy().view(np.float16).astype(np.float32)[..., 0]
+    err = np.abs(x.view(np.float16).astype(np.float32) - d.view(np.float16).astype(np.float32)).reshape(64, 16, 32)
+    assert np.all(err <= sc[..., None] * 0.5 + 4e-3)
+    nib = q.reshape(64, 16, 20)[:, :, 4:]
+    nib = np.stack([nib & 15, nib >> 4], -1).reshape(64, 16, 32)
+    xv = x.view(np.float16).astype(np.float32).reshape(64, 16, 32)
+    rows = np.arange(64)[:, None]
+    grps = np.arange(16)[None, :]
+    assert np.all(nib[rows, grps, xv.argmin(-1)] == 0)
+    assert np.all(nib[rows, grps, xv.argmax(-1)] == 15)
