@@ -135,6 +135,47 @@ class GqaDecode(Case):
                                    seq_lens_host=self.lens)
 
 
+class GqaDecodeQ4(Case):
+    """GQA decode straight from the 4-bit group KV store (the reference's
+    KVCache format, kv_cache.cpp): tokens older than the newest 256 as
+    20-byte groups of 32 values, the newest 256 f16.  Bytes: the Q4 groups
+    and f16 rows actually read, q and out."""
+    bound = "hbm"
+    kernel = "gqa_decode"
+
+    def __init__(self, dev, B, H, Hk, D, lens, max_T, seed, name):
+        self.name = name
+        self.lens = np.asarray(lens, np.int32)
+        self.cache = mugen_amd.KVCacheQ4(1, B, Hk, D, max_seq_len=max_T, fp16_preserve_last=256, max_new=64,
+                                         device=dev)
+        c = self.cache
+        g = torch.Generator(device=dev).manual_seed(seed)
+        # fill the store directly: random groups with valid f16 scale / min
+        # for the quantised tokens, random f16 ring rows
+        q4 = torch.randint(0, 256, c.q4_k[0].shape, generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+        sm = (torch.rand(c.q4_k[0].shape[:2] + (c.vpt // 32, 2), generator=g, device=dev) * 0.1).to(torch.float16)
+        q4 = q4.view(B, max_T, c.vpt // 32, 20)
+        q4[..., 0:4] = sm.view(torch.uint8).view(B, max_T, c.vpt // 32, 4)
+        c.q4_k[0].copy_(q4.view_as(c.q4_k[0]))
+        c.q4_v[0].copy_(q4.view_as(c.q4_v[0]).flip(1))
+        c.ring_k[0].copy_(randn(c.ring_k[0].shape, 1.0, torch.float16, g, dev))
+        c.ring_v[0].copy_(randn(c.ring_v[0].shape, 1.0, torch.float16, g, dev))
+        c.seq_lens_host = self.lens.copy()
+        c.seq_lens.copy_(torch.from_numpy(self.lens))
+        nq = np.maximum(self.lens - 256, 0).astype(np.int32)
+        c.n_q4.copy_(torch.from_numpy(nq))
+        self.q = randn((B, H, D), 1.0, torch.float16, g, dev)
+        self.out = torch.empty((B, H, D), dtype=torch.float16, device=dev)
+        self.ws = torch.empty(1 << 26, dtype=torch.uint8, device=dev)
+        self.profile = ("gqa_decode_q4", name)
+        nf = self.lens - nq
+        self.bytes = 2.0 * (float(nq.sum()) * c.row_bytes + float(nf.sum()) * c.vpt * 2) + B * H * D * 2 * 2
+        self.flops = 4.0 * H * D * float(self.lens.sum())
+
+    def step(self):
+        self.cache.attention_decode(0, self.q, out=self.out, workspace=self.ws)
+
+
 class Prefill(Case):
     bound = "mfma"
     unit = "TFLOP/s"
@@ -319,6 +360,7 @@ def main():
             MlaDecode(dev, 1, 16, 1, [1024], 1024, torch.float32, torch.float16, 42, "mla_decode_v2lite"),
             GqaDecode(dev, 1, 28, 4, 128, [4096], 4096, 43, "gqa_decode_qwen7b_b1"),
             GqaDecode(dev, 16, 28, 4, 128, seeded_lens(44, 16, 256, 4096), 4096, 44, "gqa_decode_qwen7b_b16"),
+            GqaDecodeQ4(dev, 16, 28, 4, 128, seeded_lens(44, 16, 256, 4096), 4096, 44, "gqa_decode_q4_qwen7b_b16"),
             Prefill(dev, 512, 32, 8, 64, 46, "gqa_prefill_llama1b"),
             MlaDecode(dev, 4, 128, 5, [32768] * 4, 32768, torch.bfloat16, torch.bfloat16, 47, "mla_verify_v3"),
             MlaFull(dev, 8, 128, seeded_lens(45, 8, 1024, 8192), 8192, "q8_0", 48, "mla_layer_v3_q8_0"),

@@ -112,8 +112,9 @@ int mugen_attn_gqa_decode(const mugen_attn_gqa_decode_args* args, void* workspac
  * are kept as groups of 32 consecutive values of the token's
  * [n_kv_heads*head_dim] row, 20 bytes each: f16 scale, f16 min, 16 bytes of
  * nibbles (value 2i low, 2i+1 high), value = f16(min + nibble * scale).
- * The newest tokens stay f16 in a ring of `ring` rows (token t at slot
- * t % ring), as the reference keeps its newest fp16_preserve_last tokens.
+ * The newest tokens stay f16 in a ring of `ring` rows (a power of two;
+ * token t at slot t % ring), as the reference keeps its newest
+ * fp16_preserve_last tokens.
  *   q4_k, q4_v      [n_seq][max_seq_len][n_kv_heads*head_dim/32][20 B],
  *                   q4_seq_stride bytes apart (a multiple of 4)
  *   ring_k, ring_v  [n_seq][ring][n_kv_heads*head_dim] F16,

@@ -347,7 +347,8 @@ const char* mugen_attn_version(void) { return "mugen_attn 0.1.0 (gfx950, abi 1)"
 
 static int q4_store_validate(const mugen_attn_kv_q4_store& st, int n_seq, int vpt, int max_seq_len, const char* who) {
     if (!st.q4_k || !st.q4_v || !st.ring_k || !st.ring_v) return fail(MUGEN_ATTN_E_INVALID, "%s: null store pointer", who);
-    if (st.ring <= 0 || st.fp16_preserve_last < 0) return fail(MUGEN_ATTN_E_INVALID, "%s: bad ring / fp16_preserve_last", who);
+    if (st.ring <= 0 || (st.ring & (st.ring - 1)) || st.fp16_preserve_last < 0)
+        return fail(MUGEN_ATTN_E_INVALID, "%s: ring must be a power of two, fp16_preserve_last >= 0", who);
     if (vpt % 32) return fail(MUGEN_ATTN_E_UNSUPPORTED, "%s: n_kv_heads*head_dim must be a multiple of 32", who);
     const int64_t q4_row = (int64_t)vpt / 32 * 20;
     if (n_seq > 1 && (st.q4_seq_stride < q4_row * max_seq_len || st.ring_seq_stride < (int64_t)st.ring * vpt))

@@ -67,8 +67,9 @@ __device__ __forceinline__ u32x4_t dequant_q4x8(uint32_t sm, uint32_t nib) {
 
 }  // namespace
 
+// two waves per SIMD (the planner sizes the grid for two workgroups per CU)
 template <int D, int DT, int OUT_DT, bool Q4 = false>
-__global__ __launch_bounds__(256) void gqa_decode_kernel(GqaDecodeParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gqa_decode_kernel(GqaDecodeParams p) {
     constexpr int KK = D / 32;           // MFMA k-steps of S
     constexpr int DB = D / 16;           // 16-dim blocks of O^T
     constexpr int RB = 2 * D;            // bytes per staged V row
@@ -114,15 +115,16 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(GqaDecodeParams p) {
     const uint8_t* q4kb = Q4 ? p.q4k + (int64_t)b * p.q4_seq_stride + (int64_t)kvh * (D / 32) * 20 : nullptr;
     const uint8_t* q4vb = Q4 ? p.q4v + (int64_t)b * p.q4_seq_stride + (int64_t)kvh * (D / 32) * 20 : nullptr;
     // 8 consecutive dims d0 (a multiple of 8) of token t
+    // (32-bit offsets from the wave-uniform bases; the ring size is a power of two)
     auto load8 = [&](const uint16_t* base, const uint8_t* q4base, int t, int d0) -> u32x4_t {
         if constexpr (Q4) {
-            if (t < nq) {
-                const uint8_t* grp = q4base + (int64_t)t * p.q4_row_bytes + (d0 >> 5) * 20;
-                const uint32_t sm = *reinterpret_cast<const uint32_t*>(grp);
-                const uint32_t nib = *reinterpret_cast<const uint32_t*>(grp + 4 + ((d0 & 31) >> 1));
-                return dequant_q4x8(sm, nib);
+            if (t < nq) {  // raw (scale|min, nibbles): dequantised by unpack8 when the block is used
+                const uint32_t off = (uint32_t)t * (uint32_t)p.q4_row_bytes + (uint32_t)((d0 >> 5) * 20);
+                const uint32_t sm = *reinterpret_cast<const uint32_t*>(q4base + off);
+                const uint32_t nib = *reinterpret_cast<const uint32_t*>(q4base + off + 4 + ((d0 & 31) >> 1));
+                return u32x4_t{sm, nib, 0u, 0u};
             }
-            return load16(base + (int64_t)(t % p.ring) * p.row_stride + d0);
+            return load16(base + ((uint32_t)(t & (p.ring - 1)) * (uint32_t)p.row_stride + (uint32_t)d0));
         } else {
             return load16(base + (int64_t)t * p.row_stride + d0);
         }
@@ -176,12 +178,29 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(GqaDecodeParams p) {
     float m_run = kNegInf;  // running max (log2 domain) of head n
     float l_part = 0.f;     // this lane's share of head n's sum
 
+    // 4-bit store: the block's Q4 loads arrive raw and are expanded here,
+    // one block after they were issued, so the loads stay in flight
+    auto unpack_block = [&](int t0, u32x4_t (&kq)[2][KK], u32x4_t (&vq)[VL]) {
+        if constexpr (Q4) {
+#pragma unroll
+            for (int nb = 0; nb < 2; nb++) {
+                const bool q4 = min(t0 + kr0 + 4 * nb, t_end - 1) < nq;
+#pragma unroll
+                for (int kk = 0; kk < KK; kk++)
+                    if (q4) kq[nb][kk] = dequant_q4x8(kq[nb][kk][0], kq[nb][kk][1]);
+            }
+#pragma unroll
+            for (int j = 0; j < VL; j++)
+                if (min(t0 + j * RPL + lane / (RB / 16), t_end - 1) < nq) vq[j] = dequant_q4x8(vq[j][0], vq[j][1]);
+        }
+    };
     u32x4_t kf[2][KK], kn[2][KK], vf[VL], vn[VL];
     int t0 = t_begin + 32 * w;
     if (t0 < t_end) load_block(t0, kf, vf);
     for (; t0 < t_end; t0 += 128) {
         const bool more = t0 + 128 < t_end;
         if (more) load_block(t0 + 128, kn, vn);  // streams in during this block
+        unpack_block(t0, kf, vf);
 
         // stage V (this wave's buffer: its previous reads are consumed)
 #pragma unroll

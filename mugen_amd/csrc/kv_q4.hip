@@ -3,7 +3,8 @@
 //
 // Layout per sequence: Q4 groups of every quantised token at its absolute
 // position ([max_seq_len][vpt/32][20 B]) and an f16 ring of `ring` token
-// rows holding the newest ones (token t at slot t % ring).  Appending n_new
+// rows (a power of two) holding the newest ones (token t at slot
+// t % ring).  Appending n_new
 // tokens to a sequence holding T tokens of which n_q4 are quantised leaves
 // the newest fp16_preserve_last in f16 and quantises the ones that age out:
 // positions n_q4 .. n_q4 + q - 1 with q = max(0, T - n_q4 + n_new -
@@ -84,7 +85,7 @@ __global__ __launch_bounds__(64) void kv_q4_append_kernel(KvQ4AppendParams p) {
     if (job < p.n_new) {
         const int t = T + job;
         if (t < nq + q || t >= p.max_seq_len) return;  // quantised right away / past the cache
-        const int64_t slot = (int64_t)(t % p.ring) * p.vpt;
+        const int64_t slot = (int64_t)(t & (p.ring - 1)) * p.vpt;
         for (int i = 8 * lane; i < p.vpt; i += 8 * 64) {
             *reinterpret_cast<u32x4_t*>(rk + slot + i) = load16(knew + (int64_t)job * p.vpt + i);
             *reinterpret_cast<u32x4_t*>(rv + slot + i) = load16(vnew + (int64_t)job * p.vpt + i);
@@ -95,8 +96,8 @@ __global__ __launch_bounds__(64) void kv_q4_append_kernel(KvQ4AppendParams p) {
     if (j >= q) return;
     const int t = nq + j;
     if (t >= p.max_seq_len) return;
-    const uint16_t* ks = t < T ? rk + (int64_t)(t % p.ring) * p.vpt : knew + (int64_t)(t - T) * p.vpt;
-    const uint16_t* vs = t < T ? rv + (int64_t)(t % p.ring) * p.vpt : vnew + (int64_t)(t - T) * p.vpt;
+    const uint16_t* ks = t < T ? rk + (int64_t)(t & (p.ring - 1)) * p.vpt : knew + (int64_t)(t - T) * p.vpt;
+    const uint16_t* vs = t < T ? rv + (int64_t)(t & (p.ring - 1)) * p.vpt : vnew + (int64_t)(t - T) * p.vpt;
     const int groups = p.vpt / 32;
     const int64_t row = (int64_t)b * p.q4_seq_stride + (int64_t)t * groups * 20;
     for (int g = lane; g < groups; g += 64) {

@@ -38,7 +38,7 @@ class KVCacheQ4:
         if self.vpt % 32:
             raise ValueError("n_kv_heads * head_dim must be a multiple of 32")
         self.max_seq_len, self.preserve, self.max_new = max_seq_len, fp16_preserve_last, max_new
-        self.ring = fp16_preserve_last + max_new
+        self.ring = 1 << max(0, (fp16_preserve_last + max_new - 1).bit_length())  # a power of two
         self.row_bytes = self.vpt // 32 * 20
         dev = torch.device(device)
         self.q4_k = [torch.zeros((n_seq, max_seq_len, self.row_bytes), dtype=torch.uint8, device=dev)

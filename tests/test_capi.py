@@ -209,14 +209,14 @@ def test_latent_write_validation():
 
 def test_kv_q4_validation():
     L = _capi.lib()
-    st = _capi.KvQ4Store(0x1000, 0x1000, 0x1000, 0x1000, 64 * 320, 300 * 512, 300, 256)
+    st = _capi.KvQ4Store(0x1000, 0x1000, 0x1000, 0x1000, 64 * 320, 512 * 512, 512, 256)
     a = _capi.KvQ4AppendArgs()
     a.store = st
     a.k_new = a.v_new = a.seq_lens = a.n_q4 = 0x1000
     a.n_q4_out = 0x2000
     a.n_seq, a.n_new, a.n_kv_heads, a.head_dim, a.max_seq_len = 2, 8, 4, 128, 64
     # every case below fails validation on the host (nothing is launched)
-    for field, val in [("n_q4_out", 0x1000), ("k_new", 0x1004), ("n_new", 45)]:
+    for field, val in [("n_q4_out", 0x1000), ("k_new", 0x1004), ("n_new", 257)]:
         b = _capi.KvQ4AppendArgs.from_buffer_copy(a)
         setattr(b, field, val)
         assert L.mugen_attn_kv_q4_append(ctypes.byref(b), None) == _capi.E_INVALID, field
@@ -230,3 +230,5 @@ def test_kv_q4_validation():
     d.n_q4 = 0x1000
     d.store.q4_k = 0x1002
     assert L.mugen_attn_gqa_decode_q4(ctypes.byref(d), None, 0, None) == _capi.E_INVALID   # misaligned store
+    d.store.q4_k, d.store.ring = 0x1000, 300
+    assert L.mugen_attn_gqa_decode_q4(ctypes.byref(d), None, 0, None) == _capi.E_INVALID   # ring not a power of two

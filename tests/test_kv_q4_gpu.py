@@ -112,7 +112,7 @@ def oracle_decode(q_bits, k, v, seq_lens, n_q4, H, Hk, D):
 def test_decode_from_store_ragged(device, H, Hk, D, splits):
     # sequences entirely f16, entirely Q4, and mixed with the boundary
     # inside a 32-token block; one empty sequence
-    T, ring, preserve = 700, 300, 256
+    T, ring, preserve = 700, 512, 256
     lens = [700, 333, 1, 0, 450]
     n_q4 = [700 - 256, 333, 0, 0, 450 - 17]
     B = len(lens)
