@@ -167,7 +167,7 @@ class GqaDecodeQ4(Case):
         self.q = randn((B, H, D), 1.0, torch.float16, g, dev)
         self.out = torch.empty((B, H, D), dtype=torch.float16, device=dev)
         self.ws = torch.empty(1 << 26, dtype=torch.uint8, device=dev)
-        self.profile = ("gqa_decode_q4", name)
+        self.profile = ("gqa_decode_q4", "qwen7b_b16_ragged")
         nf = self.lens - nq
         self.bytes = 2.0 * (float(nq.sum()) * c.row_bytes + float(nf.sum()) * c.vpt * 2) + B * H * D * 2 * 2
         self.flops = 4.0 * H * D * float(self.lens.sum())
@@ -239,7 +239,7 @@ class MlaFull(Case):
         self.norm_w = randn((512,), 0.1, torch.float16, g, dev) + 1.0
         self.pos = torch.from_numpy(self.lens - 1).to(dev)
         self.rope = (10000.0, 40.0, 4096)
-        self.profile = ("mla_full", name)
+        self.profile = ("mla_layer", "v3_b8_q8_0")
         rows = B * H
         self.bytes = (2.0 * H * 128 * rb + float(self.lens.sum()) * 576 * 2 + rows * 192 * 2
                       + 2 * rows * 576 * 4 + 2 * rows * 512 * 4 + rows * 128 * 2 + 2 * B * 576 * 2)

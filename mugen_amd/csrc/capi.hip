@@ -170,14 +170,16 @@ static int explicit_chunk(int max_seq_len, int num_splits, int quantum, int max_
 // GQA decode work items for a chunk: sum over sequences of max(1,
 // ceil(T_b / chunk)) splits times the kv heads -- exact from the host length
 // hint, else the batch * max_seq_len upper bound.
-static int64_t gqa_items(const mugen_attn_gqa_decode_args* a, int chunk) {
+// extra: splits per sequence beyond ceil(T / chunk) (the 4-bit store splits
+// its f16 ring tokens separately: at most one more)
+static int64_t gqa_items(const mugen_attn_gqa_decode_args* a, int chunk, int extra = 0) {
     const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
     int64_t n = 0;
     if (!a->seq_lens_host) {
-        n = (int64_t)a->batch * ceil_div(maxT, chunk);
+        n = (int64_t)a->batch * (ceil_div(maxT, chunk) + extra);
     } else {
         for (int b = 0; b < a->batch; b++)
-            n += a->seq_lens_host[b] > 0 ? ceil_div(a->seq_lens_host[b], chunk) : 1;
+            n += a->seq_lens_host[b] > 0 ? ceil_div(a->seq_lens_host[b], chunk) + extra : 1;
     }
     return n * a->n_kv_heads;
 }
@@ -187,22 +189,22 @@ static int64_t gqa_items(const mugen_attn_gqa_decode_args* a, int chunk) {
 // CU; the plan is the smallest chunk whose work list fits ONE dispatch round
 // of 512 workgroups (every CU streaming, no second round), with at most
 // kMaxSplits splits per sequence.
-static int gqa_chunk(const mugen_attn_gqa_decode_args* a) {
+static int gqa_chunk(const mugen_attn_gqa_decode_args* a, int extra = 0) {
     constexpr int q = 128;
     const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
-    if (a->num_splits > 0) return explicit_chunk(maxT, a->num_splits, q, kMaxSplits);
+    if (a->num_splits > 0) return explicit_chunk(maxT, a->num_splits, q, kMaxSplits - 1);
     const int cmax = ceil_div(maxT, q) * q;
-    const int cmin = ceil_div(ceil_div(maxT, kMaxSplits), q) * q;
+    const int cmin = ceil_div(ceil_div(maxT, kMaxSplits - 1), q) * q;
     const int64_t budget = 512;
-    if (gqa_items(a, cmax) > budget) return cmax;  // one split per sequence already fills a round
-    int lo = cmin < q ? q : cmin, hi = cmax;       // items(c) is non-increasing in c
+    if (gqa_items(a, cmax, extra) > budget) return cmax;  // one split per sequence already fills a round
+    int lo = cmin < q ? q : cmin, hi = cmax;              // items(c) is non-increasing in c
     while (lo < hi) {
         const int mid = ((lo + hi) / 2) / q * q;
         if (mid <= lo) break;
-        if (gqa_items(a, mid) <= budget) hi = mid;
+        if (gqa_items(a, mid, extra) <= budget) hi = mid;
         else lo = mid + q;
     }
-    if (gqa_items(a, lo) > budget) lo = hi;
+    if (gqa_items(a, lo, extra) > budget) lo = hi;
     return lo;
 }
 
@@ -427,19 +429,30 @@ static int gqa_q4_validate(const mugen_attn_gqa_decode_q4_args* a) {
     return q4_store_validate(a->store, a->batch, a->n_kv_heads * a->head_dim, a->max_seq_len, "gqa_decode_q4");
 }
 
+// 4-bit store decode: the Q4 and f16-ring tokens of a sequence are split
+// separately (at most one split more than the f16 plan), and the partials
+// always go through the workspace and the combine
+static size_t gqa_q4_ws(const mugen_attn_gqa_decode_q4_args* a, int chunk, int* splits_out) {
+    const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
+    const int splits = ceil_div(maxT, chunk) + 1;
+    if (splits_out) *splits_out = splits;
+    const size_t slots = (size_t)a->batch * a->n_heads * splits;
+    return slots * (size_t)a->head_dim * 4 + slots * 2 * 4 + 256;
+}
+
 size_t mugen_attn_gqa_decode_q4_workspace_size(const mugen_attn_gqa_decode_q4_args* a) {
     if (gqa_q4_validate(a) != MUGEN_ATTN_OK) return 0;
     const mugen_attn_gqa_decode_args g = q4_as_gqa(a);
-    return gqa_ws(&g, gqa_chunk(&g), nullptr);
+    return gqa_q4_ws(a, gqa_chunk(&g, 1), nullptr);
 }
 
 int mugen_attn_gqa_decode_q4(const mugen_attn_gqa_decode_q4_args* a, void* ws, size_t ws_bytes, void* stream) {
     if (int rc = gqa_q4_validate(a)) return rc;
     const mugen_attn_gqa_decode_args g = q4_as_gqa(a);
-    const int chunk = gqa_chunk(&g);
-    int splits = 1;
-    const size_t need = gqa_ws(&g, chunk, &splits);
-    if (need > 0 && (!ws || ws_bytes < need))
+    const int chunk = gqa_chunk(&g, 1);
+    int splits = 2;
+    const size_t need = gqa_q4_ws(a, chunk, &splits);
+    if (!ws || ws_bytes < need)
         return fail(MUGEN_ATTN_E_WORKSPACE, "gqa_decode_q4: workspace of %zu bytes required, %zu given", need,
                     ws_bytes);
     GqaDecodeParams p{};
@@ -464,14 +477,15 @@ int mugen_attn_gqa_decode_q4(const mugen_attn_gqa_decode_q4_args* a, void* ws, s
     p.q4_seq_stride = a->store.q4_seq_stride;
     p.q4_row_bytes = a->n_kv_heads * a->head_dim / 32 * 20;
     p.ring = a->store.ring;
-    if (splits > 1) {
+    {
         float* base = align256(ws);
         const size_t slots = (size_t)a->batch * a->n_heads * splits;
         p.ws_o = base;
         p.ws_ml = base + slots * a->head_dim;
     }
-    const int64_t nwg = gqa_items(&g, chunk);
-    if (nwg > INT32_MAX) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode_q4: too many work items");
+    const int64_t nwg = gqa_items(&g, chunk, 1);  // + the ring splits
+    if (nwg > INT32_MAX / 2) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode_q4: too many work items");
+    p.per_xcd = (int)ceil_div(nwg, (int64_t)8);
     return hip_status(launch_gqa_decode_q4(p, (int)nwg, a->head_dim, a->out_dtype, static_cast<hipStream_t>(stream),
                                            active_timer()),
                       "gqa_decode_q4 launch");

@@ -51,18 +51,34 @@ __device__ constexpr int vswz(int r) {
 // Eight values of a 20-byte 4-bit group (dequantize_group,
 // kv_cache.cpp:58-73): `sm` = the group's f16 scale (low half) and min
 // (high half), `nib` = the 4 bytes holding values 2i (low nibble) and 2i+1
-// (high nibble); each value f16(min + nibble * scale), product and sum
-// rounded separately as there.
+// (high nibble); each value f16(min + nibble * scale).  nibble * scale is
+// exact in fp32 (4 x 11 significant bits), so one fma rounds exactly like
+// the reference's product-then-sum; the nibbles are masked into bytes and
+// converted with the byte-select conversions.
 __device__ __forceinline__ u32x4_t dequant_q4x8(uint32_t sm, uint32_t nib) {
-#pragma clang fp contract(off)
     const float sf = lo_f32<DT_F16>(sm), mf = hi_f32<DT_F16>(sm);
+    const uint32_t lo = nib & 0x0f0f0f0fu, hi = (nib >> 4) & 0x0f0f0f0fu;
     uint32_t w[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const uint32_t byte = (nib >> (8 * e)) & 0xffu;
-        w[e] = pack2<DT_F16>(mf + (float)(byte & 15u) * sf, mf + (float)(byte >> 4) * sf);
-    }
+    for (int e = 0; e < 4; e++)
+        w[e] = pack2<DT_F16>(fmaf((float)((lo >> (8 * e)) & 0xffu), sf, mf),
+                             fmaf((float)((hi >> (8 * e)) & 0xffu), sf, mf));
     return u32x4_t{w[0], w[1], w[2], w[3]};
+}
+
+// splits of sequence j in the compact work list: ceil(T / chunk) (at least
+// one), or for the 4-bit store those of the Q4 tokens plus those of the f16
+// ring tokens (at least one)
+template <bool Q4>
+__device__ __forceinline__ int splits_of(const GqaDecodeParams& p, int j) {
+    const int Tj = p.seq_lens[j];
+    if constexpr (Q4) {
+        const int nqj = min(p.n_q4[j], max(Tj, 0));
+        const int n = (nqj + p.chunk - 1) / p.chunk + (max(Tj - nqj, 0) + p.chunk - 1) / p.chunk;
+        return n > 0 ? n : 1;
+    } else {
+        return Tj > 0 ? (Tj + p.chunk - 1) / p.chunk : 1;
+    }
 }
 
 }  // namespace
@@ -85,9 +101,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 
     // compact work list: item r of sequence b is split r / Hk of kv head r % Hk
     int b = -1, s = 0, kvh = 0;
-    for (int j = 0, r = blockIdx.x; j < p.B; j++) {  // uniform scalar loop over the batch
-        const int Tj = p.seq_lens[j];
-        const int nsj = Tj > 0 ? (Tj + p.chunk - 1) / p.chunk : 1;
+    // 4-bit store: a kv head's 80-byte group run shares cache lines with its
+    // neighbours', so the kv heads of one (sequence, split) -- consecutive
+    // items -- go to one XCD (workgroups are dealt to the 8 XCDs round-robin
+    // by blockIdx): item = xcd * per_xcd + slot
+    const int item = (Q4 && p.per_xcd > 0) ? (int)(blockIdx.x % 8) * p.per_xcd + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+    for (int j = 0, r = item; j < p.B; j++) {  // uniform scalar loop over the batch
+        const int nsj = splits_of<Q4>(p, j);
         if (r < nsj * p.Hk) {
             b = j;
             s = r / p.Hk;
@@ -100,36 +120,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int T = p.seq_lens[b];
-    const int t_begin = s * p.chunk;
-    const int t_end = min(t_begin + p.chunk, T);
-    if (p.num_splits > 1 && t_begin >= T) return;  // empty split (T <= 0): the combine skips it
+    // 4-bit store: the Q4 tokens [0, n_q4) and the f16 ring tokens
+    // [n_q4, T) are split separately, so a split -- and every 32-token block
+    // of it -- holds one kind only (Q4 splits first)
+    const int nq = Q4 ? min(p.n_q4[b], max(T, 0)) : 0;
+    const int nsq = Q4 ? (nq + p.chunk - 1) / p.chunk : 0;
+    const bool q4_split = Q4 && s < nsq;
+    const int t_begin = q4_split || !Q4 ? s * p.chunk : nq + (s - nsq) * p.chunk;
+    const int t_end = min(t_begin + p.chunk, q4_split ? nq : T);
+    if (p.num_splits > 1 && t_begin >= t_end) return;  // empty split (T <= 0): the combine skips it
     MUGEN_TRACE(0);
     const int G = p.G;
     const int h0 = kvh * G;
 
     const uint16_t* kbase = p.k + (int64_t)b * p.seq_stride + (int64_t)kvh * D;
     const uint16_t* vbase = p.v + (int64_t)b * p.seq_stride + (int64_t)kvh * D;
-    // 4-bit store: tokens below nq are groups (group kvh*D/32 + c of a token
-    // row holds dims 32c .. 32c+31 of this kv head), the rest ring rows
-    const int nq = Q4 ? p.n_q4[b] : 0;
-    const uint8_t* q4kb = Q4 ? p.q4k + (int64_t)b * p.q4_seq_stride + (int64_t)kvh * (D / 32) * 20 : nullptr;
-    const uint8_t* q4vb = Q4 ? p.q4v + (int64_t)b * p.q4_seq_stride + (int64_t)kvh * (D / 32) * 20 : nullptr;
-    // 8 consecutive dims d0 (a multiple of 8) of token t
-    // (32-bit offsets from the wave-uniform bases; the ring size is a power of two)
-    auto load8 = [&](const uint16_t* base, const uint8_t* q4base, int t, int d0) -> u32x4_t {
-        if constexpr (Q4) {
-            if (t < nq) {  // raw (scale|min, nibbles): dequantised by unpack8 when the block is used
-                const uint32_t off = (uint32_t)t * (uint32_t)p.q4_row_bytes + (uint32_t)((d0 >> 5) * 20);
-                const uint32_t sm = *reinterpret_cast<const uint32_t*>(q4base + off);
-                const uint32_t nib = *reinterpret_cast<const uint32_t*>(q4base + off + 4 + ((d0 & 31) >> 1));
-                return u32x4_t{sm, nib, 0u, 0u};
-            }
-            return load16(base + ((uint32_t)(t & (p.ring - 1)) * (uint32_t)p.row_stride + (uint32_t)d0));
-        } else {
-            return load16(base + (int64_t)t * p.row_stride + d0);
-        }
+    // 4-bit store: tokens below nq are 20-byte groups (group kvh*D/32 + c of
+    // a token row holds dims 32c .. 32c+31 of this kv head), the rest f16
+    // ring rows (token t at slot t % ring, a power of two).  The Q4 rows are
+    // read through buffer resources (one per sequence: 32-bit offsets, one
+    // instruction per dword) and arrive raw; they are expanded one block
+    // later (unpack_block), so the loads stay in flight.
+    const int64_t q4sb = Q4 ? (int64_t)b * p.q4_seq_stride : 0;
+    const __amdgpu_buffer_rsrc_t rq4k =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(Q4 ? p.q4k + q4sb : nullptr), 0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rq4v =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(Q4 ? p.q4v + q4sb : nullptr), 0, 0x7fffffff, 0x00020000);
+    const uint32_t q4head = (uint32_t)kvh * (D / 32) * 20;
+    auto load_q4raw = [&](__amdgpu_buffer_rsrc_t r, int t, int d0) -> u32x4_t {
+        const int off = (int)((uint32_t)t * (uint32_t)p.q4_row_bytes + q4head + (uint32_t)((d0 >> 5) * 20));
+        const uint32_t sm = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+        const uint32_t nib = __builtin_amdgcn_raw_buffer_load_b32(r, off + 4 + ((d0 & 31) >> 1), 0, 0);
+        u32x4_t v;
+        v[0] = sm;
+        v[1] = nib;
+        return v;
     };
-
+    auto load_f16 = [&](const uint16_t* base, int t, int d0) -> u32x4_t {
+        if constexpr (Q4) return load16(base + ((uint32_t)(t & (p.ring - 1)) * (uint32_t)p.row_stride + (uint32_t)d0));
+        else return load16(base + (int64_t)t * p.row_stride + d0);
+    };
     // Q^T as the B operand: lane holds q[head n][32kk + 8g .. +8]
     u32x4_t qf[KK];
     if (n < G) {
@@ -143,17 +173,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 
     // block loads: K rows in the permuted order (A operand), V rows coalesced
     const int kr0 = 8 * (n >> 2) + (n & 3);  // + 4nb
-    auto load_block = [&](int t0, u32x4_t (&kq)[2][KK], u32x4_t (&vq)[VL]) {
+    // QB: this split's tokens are Q4 groups (a compile-time kind, so the
+    // main loop has no data-dependent branches around its loads and the
+    // prefetch's wait counts stay exact)
+    auto load_block = [&](int t0, u32x4_t (&kq)[2][KK], u32x4_t (&vq)[VL], auto qb_tag) {
+        constexpr bool QB = decltype(qb_tag)::value;
 #pragma unroll
         for (int nb = 0; nb < 2; nb++) {
             const int tk = min(t0 + kr0 + 4 * nb, t_end - 1);
 #pragma unroll
-            for (int kk = 0; kk < KK; kk++) kq[nb][kk] = load8(kbase, q4kb, tk, 32 * kk + 8 * g);
+            for (int kk = 0; kk < KK; kk++) {
+                const int d0 = 32 * kk + 8 * g;
+                kq[nb][kk] = QB ? load_q4raw(rq4k, tk, d0) : load_f16(kbase, tk, d0);
+            }
         }
 #pragma unroll
         for (int j = 0; j < VL; j++) {
             const int tv = min(t0 + j * RPL + lane / (RB / 16), t_end - 1);
-            vq[j] = load8(vbase, q4vb, tv, 8 * (lane % (RB / 16)));
+            const int d0 = 8 * (lane % (RB / 16));
+            vq[j] = QB ? load_q4raw(rq4v, tv, d0) : load_f16(vbase, tv, d0);
         }
     };
     // V staging: load j of lane l is row j*RPL + l/(RB/16), chunk l%(RB/16)
@@ -180,27 +218,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 
     // 4-bit store: the block's Q4 loads arrive raw and are expanded here,
     // one block after they were issued, so the loads stay in flight
-    auto unpack_block = [&](int t0, u32x4_t (&kq)[2][KK], u32x4_t (&vq)[VL]) {
-        if constexpr (Q4) {
+    auto unpack_block = [&](u32x4_t (&kq)[2][KK], u32x4_t (&vq)[VL], auto qb_tag) {
+        if constexpr (decltype(qb_tag)::value) {
 #pragma unroll
-            for (int nb = 0; nb < 2; nb++) {
-                const bool q4 = min(t0 + kr0 + 4 * nb, t_end - 1) < nq;
+            for (int nb = 0; nb < 2; nb++)
 #pragma unroll
-                for (int kk = 0; kk < KK; kk++)
-                    if (q4) kq[nb][kk] = dequant_q4x8(kq[nb][kk][0], kq[nb][kk][1]);
-            }
+                for (int kk = 0; kk < KK; kk++) kq[nb][kk] = dequant_q4x8(kq[nb][kk][0], kq[nb][kk][1]);
 #pragma unroll
-            for (int j = 0; j < VL; j++)
-                if (min(t0 + j * RPL + lane / (RB / 16), t_end - 1) < nq) vq[j] = dequant_q4x8(vq[j][0], vq[j][1]);
+            for (int j = 0; j < VL; j++) vq[j] = dequant_q4x8(vq[j][0], vq[j][1]);
         }
     };
+    auto main_loop = [&](auto qb_tag) {
     u32x4_t kf[2][KK], kn[2][KK], vf[VL], vn[VL];
     int t0 = t_begin + 32 * w;
-    if (t0 < t_end) load_block(t0, kf, vf);
+    if (t0 < t_end) load_block(t0, kf, vf, qb_tag);
     for (; t0 < t_end; t0 += 128) {
         const bool more = t0 + 128 < t_end;
-        if (more) load_block(t0 + 128, kn, vn);  // streams in during this block
-        unpack_block(t0, kf, vf);
+        if (more) load_block(t0 + 128, kn, vn, qb_tag);  // streams in during this block
+        unpack_block(kf, vf, qb_tag);
 
         // stage V (this wave's buffer: its previous reads are consumed)
 #pragma unroll
@@ -270,6 +305,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             for (int j = 0; j < VL; j++) vf[j] = vn[j];
         }
     }
+    };
+    if (q4_split) {
+        if constexpr (Q4) main_loop(std::true_type{});
+    } else {
+        main_loop(std::false_type{});
+    }
 
     MUGEN_TRACE(1);
     // ---- merge the 4 waves' (m, l, O) per head through LDS
@@ -324,7 +365,8 @@ __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     MUGEN_TRACE(8);
     const int T = p.seq_lens[b];
-    const int nact = min(p.num_splits, (T + p.chunk - 1) / p.chunk);
+    const int nact = p.n_q4 ? min(p.num_splits, T > 0 ? splits_of<true>(p, b) : 0)
+                            : min(p.num_splits, (T + p.chunk - 1) / p.chunk);
     const int64_t bh = (int64_t)b * p.H + h;
     const float inv = lse_weights(p.ws_ml + bh * p.num_splits * 2, 2, nact, f_lds, red_lds);
     const float* os = p.ws_o + bh * p.num_splits * D + d;
@@ -349,7 +391,8 @@ __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p
 template <int D, int DT, int OUT_DT, bool Q4 = false>
 static hipError_t launch_gqa_t(const GqaDecodeParams& p, int nwg, hipStream_t st, KernelTimer* timer) {
     timer_begin(timer, "gqa_decode", st);
-    hipLaunchKernelGGL((gqa_decode_kernel<D, DT, OUT_DT, Q4>), dim3(nwg), dim3(256), 0, st, p);
+    const int grid = (Q4 && p.per_xcd > 0) ? 8 * p.per_xcd : nwg;
+    hipLaunchKernelGGL((gqa_decode_kernel<D, DT, OUT_DT, Q4>), dim3(grid), dim3(256), 0, st, p);
     timer_end(timer, "gqa_decode", st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.num_splits == 1) return e;

@@ -42,6 +42,7 @@ struct GqaDecodeParams {
     int64_t q4_seq_stride;  // bytes between sequences' Q4 stores
     int q4_row_bytes;       // bytes per token (Hk * D / 32 groups of 20)
     int ring;
+    int per_xcd;            // 4-bit store: work items per XCD (0: blockIdx order)
 };
 
 // nwg: workgroups of the compact work list (exact, or an upper bound)
