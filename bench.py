@@ -288,8 +288,9 @@ def time_case(case, steps, warmup, dev):
     torch.cuda.synchronize(dev)
     wall_ms = (time.perf_counter() - t0) * 1e3
     ms = e0.elapsed_time(e1) / steps
-    # per-kernel durations (HIP events around each launch, on the launch
-    # stream; eager calls, so these include the launch gaps)
+    # per-kernel durations: the library launches each kernel with a start /
+    # stop event pair stamped at the kernel's own start and end, on the
+    # launch stream (hipExtLaunchKernelGGL)
     _capi.timing_reset()
     _capi.timing_enable(True)
     for _ in range(steps):

@@ -405,11 +405,13 @@ const char* mugen_attn_version(void);
 
 /*
  * Optional kernel timing (for benchmarks): when enabled, every compute call
- * brackets each kernel it launches with HIP events on the call's stream.
- * mugen_attn_timing_read synchronises on the recorded events and returns
- * the summed milliseconds and launch count of the kernel named `kernel`
- * ("gqa_decode", "gqa_decode_combine", "gqa_prefill", "mla_decode",
- * "mla_decode_combine", "mla_absorb", "mla_project", "mla_latent_write", "kv_q4_append", "scatter_kv").
+ * launches its kernels with a start / stop HIP event pair that the runtime
+ * stamps at each kernel's own start and end (hipExtLaunchKernelGGL), on the
+ * call's stream.  mugen_attn_timing_read synchronises on the recorded
+ * events and returns the summed milliseconds and launch count of the kernel
+ * named `kernel` ("gqa_decode", "gqa_decode_combine", "gqa_prefill",
+ * "mla_decode", "mla_decode_combine", "mla_absorb", "mla_project",
+ * "mla_latent_write", "kv_q4_append", "scatter_kv").
  */
 int mugen_attn_timing_enable(int enable);
 int mugen_attn_timing_read(const char* kernel, double* total_ms, int64_t* launches);

@@ -50,7 +50,6 @@ struct KernelTimer {
     std::vector<Pending> pending;
     std::vector<hipEvent_t> pool;
     std::unordered_map<std::string, std::pair<double, int64_t>> totals;
-    hipEvent_t open_a = nullptr;
 
     hipEvent_t get() {
         if (!pool.empty()) { hipEvent_t e = pool.back(); pool.pop_back(); return e; }
@@ -77,22 +76,20 @@ static KernelTimer g_timer;
 
 KernelTimer* active_timer() { return g_timer.enabled ? &g_timer : nullptr; }
 
-void timer_begin(KernelTimer* t, const char*, hipStream_t st) {
-    if (!t) return;
+bool timer_pair(KernelTimer* t, hipEvent_t* start, hipEvent_t* stop) {
+    if (!t) return false;
     std::lock_guard<std::mutex> lk(t->mu);
-    t->open_a = t->get();
-    if (t->open_a) (void)hipEventRecord(t->open_a, st);
+    *start = t->get();
+    *stop = t->get();
+    if (*start && *stop) return true;
+    if (*start) t->pool.push_back(*start);
+    if (*stop) t->pool.push_back(*stop);
+    return false;
 }
 
-void timer_end(KernelTimer* t, const char* name, hipStream_t st) {
-    if (!t) return;
+void timer_push(KernelTimer* t, const char* name, hipEvent_t start, hipEvent_t stop) {
     std::lock_guard<std::mutex> lk(t->mu);
-    if (!t->open_a) return;
-    hipEvent_t b = t->get();
-    if (!b) return;
-    (void)hipEventRecord(b, st);
-    t->pending.push_back({name, t->open_a, b});
-    t->open_a = nullptr;
+    t->pending.push_back({name, start, stop});
     if (t->pending.size() > 4096) t->drain();
 }
 
@@ -114,18 +111,14 @@ __global__ void scatter_kv16_kernel(const u32x4_t* __restrict__ src, u32x4_t* __
 hipError_t launch_scatter_kv(const uint16_t* src, uint16_t* dst, uint64_t offset, uint64_t count,
                              hipStream_t st, KernelTimer* t) {
     if (count == 0) return hipSuccess;
-    timer_begin(t, "scatter_kv", st);
     uint16_t* d = dst + offset;
     if ((((uintptr_t)src | (uintptr_t)d) & 15) == 0 && (count & 7) == 0) {
         const uint64_t n16 = count / 8;
-        hipLaunchKernelGGL(scatter_kv16_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, st,
-                           reinterpret_cast<const u32x4_t*>(src), reinterpret_cast<u32x4_t*>(d), n16);
-    } else {
-        hipLaunchKernelGGL(scatter_kv_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, st, src,
-                           dst, offset, count);
+        return launch_k(t, "scatter_kv", scatter_kv16_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), st,
+                        reinterpret_cast<const u32x4_t*>(src), reinterpret_cast<u32x4_t*>(d), n16);
     }
-    timer_end(t, "scatter_kv", st);
-    return hipGetLastError();
+    return launch_k(t, "scatter_kv", scatter_kv_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), st,
+                    static_cast<const uint16_t*>(src), dst, offset, count);
 }
 
 // ------------------------------------------------------------------ planning

@@ -390,16 +390,10 @@ __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p
 
 template <int D, int DT, int OUT_DT, bool Q4 = false>
 static hipError_t launch_gqa_t(const GqaDecodeParams& p, int nwg, hipStream_t st, KernelTimer* timer) {
-    timer_begin(timer, "gqa_decode", st);
     const int grid = (Q4 && p.per_xcd > 0) ? 8 * p.per_xcd : nwg;
-    hipLaunchKernelGGL((gqa_decode_kernel<D, DT, OUT_DT, Q4>), dim3(grid), dim3(256), 0, st, p);
-    timer_end(timer, "gqa_decode", st);
-    hipError_t e = hipGetLastError();
+    hipError_t e = launch_k(timer, "gqa_decode", gqa_decode_kernel<D, DT, OUT_DT, Q4>, dim3(grid), dim3(256), st, p);
     if (e != hipSuccess || p.num_splits == 1) return e;
-    timer_begin(timer, "gqa_decode_combine", st);
-    hipLaunchKernelGGL((gqa_decode_combine_kernel<D, OUT_DT>), dim3(p.H, p.B), dim3(D), 0, st, p);
-    timer_end(timer, "gqa_decode_combine", st);
-    return hipGetLastError();
+    return launch_k(timer, "gqa_decode_combine", gqa_decode_combine_kernel<D, OUT_DT>, dim3(p.H, p.B), dim3(D), st, p);
 }
 
 template <int D, int DT>

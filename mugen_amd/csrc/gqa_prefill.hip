@@ -300,10 +300,7 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
 template <int D, int MB, int DT, int OUT_DT>
 static hipError_t launch_pf_t(const GqaPrefillParams& p, int Hk, hipStream_t st, KernelTimer* t) {
     dim3 grid((p.N + 15) / 16, Hk);
-    timer_begin(t, "gqa_prefill", st);
-    hipLaunchKernelGGL((gqa_prefill_kernel<D, MB, DT, OUT_DT>), grid, dim3(64 * kWaves), 0, st, p);
-    timer_end(t, "gqa_prefill", st);
-    return hipGetLastError();
+    return launch_k(t, "gqa_prefill", gqa_prefill_kernel<D, MB, DT, OUT_DT>, grid, dim3(64 * kWaves), st, p);
 }
 
 template <int D, int MB, int DT>

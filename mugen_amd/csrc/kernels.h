@@ -1,6 +1,7 @@
 // kernels.h -- internal kernel parameter blocks and launchers (not ABI).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -13,8 +14,24 @@ struct RopeFreqs {
 };
 
 struct KernelTimer;  // defined in capi.hip
-void timer_begin(KernelTimer* t, const char* name, hipStream_t st);
-void timer_end(KernelTimer* t, const char* name, hipStream_t st);
+// Per-kernel timing (mugen_attn_timing_*): when enabled, launches go through
+// hipExtLaunchKernelGGL with a start / stop event pair that the runtime
+// stamps at the kernel's own start and end (no launch gap included).
+bool timer_pair(KernelTimer* t, hipEvent_t* start, hipEvent_t* stop);
+void timer_push(KernelTimer* t, const char* name, hipEvent_t start, hipEvent_t stop);
+
+template <typename... KArgs, typename... Args>
+hipError_t launch_k(KernelTimer* t, const char* name, void (*kernel)(KArgs...), dim3 grid, dim3 block,
+                    hipStream_t st, Args... args) {
+    hipEvent_t a = nullptr, b = nullptr;
+    if (timer_pair(t, &a, &b)) {
+        hipExtLaunchKernelGGL(kernel, grid, block, 0, st, a, b, 0, args...);
+        timer_push(t, name, a, b);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, 0, st, args...);
+    }
+    return hipGetLastError();
+}
 
 struct GqaDecodeParams {
     const uint16_t* q;

@@ -107,11 +107,7 @@ __global__ __launch_bounds__(64) void kv_q4_append_kernel(KvQ4AppendParams p) {
 }
 
 hipError_t launch_kv_q4_append(const KvQ4AppendParams& p, int n_seq, hipStream_t st, KernelTimer* t) {
-    timer_begin(t, "kv_q4_append", st);
-    hipLaunchKernelGGL(kv_q4_append_kernel, dim3(2 * p.n_new, n_seq), dim3(64), 0, st, p);
-    hipError_t e = hipGetLastError();
-    timer_end(t, "kv_q4_append", st);
-    return e;
+    return launch_k(t, "kv_q4_append", kv_q4_append_kernel, dim3(2 * p.n_new, n_seq), dim3(64), st, p);
 }
 
 }  // namespace mugen_attn

@@ -70,12 +70,9 @@ __global__ __launch_bounds__(64) void mla_latent_write_kernel(LatentWriteParams 
 }
 
 hipError_t launch_mla_latent_write(const LatentWriteParams& p, int latent_dt, hipStream_t st, KernelTimer* t) {
-    timer_begin(t, "mla_latent_write", st);
-    if (latent_dt == DT_BF16) hipLaunchKernelGGL(mla_latent_write_kernel<DT_BF16>, dim3(p.rows), dim3(64), 0, st, p);
-    else hipLaunchKernelGGL(mla_latent_write_kernel<DT_F16>, dim3(p.rows), dim3(64), 0, st, p);
-    hipError_t e = hipGetLastError();
-    timer_end(t, "mla_latent_write", st);
-    return e;
+    if (latent_dt == DT_BF16)
+        return launch_k(t, "mla_latent_write", mla_latent_write_kernel<DT_BF16>, dim3(p.rows), dim3(64), st, p);
+    return launch_k(t, "mla_latent_write", mla_latent_write_kernel<DT_F16>, dim3(p.rows), dim3(64), st, p);
 }
 
 }  // namespace mugen_attn

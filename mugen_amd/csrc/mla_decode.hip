@@ -1095,29 +1095,19 @@ int mla_tile_tokens(int variant) { return (variant == 3 || variant == 4) ? 2 * k
 template <int MB, int TS, int NW, int QDT, int DT, int OUT_DT>
 static hipError_t launch_mla_t(const MlaParams& p, hipStream_t st, KernelTimer* t) {
     const int grid = 8 * p.nrb * ((p.groups + 7) / 8);  // see the XCD mapping in the kernel
-    timer_begin(t, "mla_decode", st);
-    hipLaunchKernelGGL((mla_decode_kernel<MB, TS, NW, QDT, DT>), dim3(grid), dim3(64 * NW), 0, st, p);
-    timer_end(t, "mla_decode", st);
-    hipError_t e = hipGetLastError();
+    hipError_t e = launch_k(t, "mla_decode", mla_decode_kernel<MB, TS, NW, QDT, DT>, dim3(grid), dim3(64 * NW), st, p);
     if (e != hipSuccess) return e;
-    timer_begin(t, "mla_decode_combine", st);
-    hipLaunchKernelGGL((mla_decode_combine_kernel<QDT, DT, OUT_DT>), dim3(p.nq, 4, p.B), dim3(256), 0, st, p);
-    timer_end(t, "mla_decode_combine", st);
-    return hipGetLastError();
+    return launch_k(t, "mla_decode_combine", mla_decode_combine_kernel<QDT, DT, OUT_DT>, dim3(p.nq, 4, p.B),
+                    dim3(256), st, p);
 }
 
 template <int DT, int OUT_DT>
 static hipError_t launch_mla_ws_t(const MlaParams& p, hipStream_t st, KernelTimer* t) {
     const int grid = 8 * p.nrb * ((p.groups + 7) / 8);
-    timer_begin(t, "mla_decode", st);
-    hipLaunchKernelGGL((mla_decode_ws_kernel<DT>), dim3(grid), dim3(512), 0, st, p);
-    timer_end(t, "mla_decode", st);
-    hipError_t e = hipGetLastError();
+    hipError_t e = launch_k(t, "mla_decode", mla_decode_ws_kernel<DT>, dim3(grid), dim3(512), st, p);
     if (e != hipSuccess) return e;
-    timer_begin(t, "mla_decode_combine", st);
-    hipLaunchKernelGGL((mla_decode_combine_kernel<DT, DT, OUT_DT>), dim3(p.nq, 4, p.B), dim3(256), 0, st, p);
-    timer_end(t, "mla_decode_combine", st);
-    return hipGetLastError();
+    return launch_k(t, "mla_decode_combine", mla_decode_combine_kernel<DT, DT, OUT_DT>, dim3(p.nq, 4, p.B),
+                    dim3(256), st, p);
 }
 
 template <int DT>

@@ -258,37 +258,29 @@ __global__ __launch_bounds__(256) void mla_project_kernel(MlaProjParams p) {
 }
 
 template <int WT>
-static hipError_t launch_absorb_w(const MlaProjParams& p, int out_dt, hipStream_t st) {
+static hipError_t launch_absorb_w(const MlaProjParams& p, int out_dt, hipStream_t st, KernelTimer* t) {
     const dim3 grid(p.H, 512 / 256);
-    if (out_dt == DT_BF16) hipLaunchKernelGGL((mla_absorb_kernel<WT, DT_BF16>), grid, dim3(512), 0, st, p);
-    else hipLaunchKernelGGL((mla_absorb_kernel<WT, DT_F32>), grid, dim3(512), 0, st, p);
-    return hipGetLastError();
+    if (out_dt == DT_BF16) return launch_k(t, "mla_absorb", mla_absorb_kernel<WT, DT_BF16>, grid, dim3(512), st, p);
+    return launch_k(t, "mla_absorb", mla_absorb_kernel<WT, DT_F32>, grid, dim3(512), st, p);
 }
 
 hipError_t launch_mla_absorb(const MlaProjParams& p, int w_type, int out_dt, hipStream_t st, KernelTimer* t) {
-    timer_begin(t, "mla_absorb", st);
-    hipError_t e = w_type == W_F16 ? launch_absorb_w<W_F16>(p, out_dt, st)
-                 : w_type == W_Q8_0 ? launch_absorb_w<W_Q8_0>(p, out_dt, st)
-                                    : launch_absorb_w<W_Q4_0>(p, out_dt, st);
-    timer_end(t, "mla_absorb", st);
-    return e;
+    return w_type == W_F16 ? launch_absorb_w<W_F16>(p, out_dt, st, t)
+         : w_type == W_Q8_0 ? launch_absorb_w<W_Q8_0>(p, out_dt, st, t)
+                            : launch_absorb_w<W_Q4_0>(p, out_dt, st, t);
 }
 
 template <int WT>
-static hipError_t launch_project_w(const MlaProjParams& p, int out_dt, hipStream_t st) {
+static hipError_t launch_project_w(const MlaProjParams& p, int out_dt, hipStream_t st, KernelTimer* t) {
     const dim3 grid(p.H, 128 / 32);
-    if (out_dt == DT_F16) hipLaunchKernelGGL((mla_project_kernel<WT, DT_F16>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((mla_project_kernel<WT, DT_F32>), grid, dim3(256), 0, st, p);
-    return hipGetLastError();
+    if (out_dt == DT_F16) return launch_k(t, "mla_project", mla_project_kernel<WT, DT_F16>, grid, dim3(256), st, p);
+    return launch_k(t, "mla_project", mla_project_kernel<WT, DT_F32>, grid, dim3(256), st, p);
 }
 
 hipError_t launch_mla_project(const MlaProjParams& p, int w_type, int out_dt, hipStream_t st, KernelTimer* t) {
-    timer_begin(t, "mla_project", st);
-    hipError_t e = w_type == W_F16 ? launch_project_w<W_F16>(p, out_dt, st)
-                 : w_type == W_Q8_0 ? launch_project_w<W_Q8_0>(p, out_dt, st)
-                                    : launch_project_w<W_Q4_0>(p, out_dt, st);
-    timer_end(t, "mla_project", st);
-    return e;
+    return w_type == W_F16 ? launch_project_w<W_F16>(p, out_dt, st, t)
+         : w_type == W_Q8_0 ? launch_project_w<W_Q8_0>(p, out_dt, st, t)
+                            : launch_project_w<W_Q4_0>(p, out_dt, st, t);
 }
 
 }  // namespace mugen_attn
