@@ -390,6 +390,44 @@ typedef struct mugen_attn_mla_latent_write_args {
 int mugen_attn_mla_latent_write(const mugen_attn_mla_latent_write_args* args, void* stream);
 
 /*
+ * Decode-step helpers for captured HIP graphs.  The reference caches its
+ * whole decode step as one dispatch chain ("mega-chain",
+ * transformer.cpp:3734-3833) and patches pos / kv_offset / seq_len into the
+ * cached constants before each step.  Here those values live in device
+ * memory, so a captured graph of a step's calls replays unchanged:
+ *
+ * kv_append replaces the two scatter_kv dispatches of a step
+ * (transformer.cpp:3749-3754): row j of sequence b's new K and V goes to
+ * position seq_lens[b] + j of its cache (rows past max_seq_len are dropped).
+ *   k_new, v_new      [n_seq][n_new][n_kv_heads*head_dim] (16-bit)
+ *   k_cache, v_cache  [n_seq][max_seq_len][n_kv_heads*head_dim],
+ *                     seq_stride elements apart
+ *   seq_lens          device [n_seq]: tokens held before the append
+ */
+typedef struct mugen_attn_kv_append_args {
+    const void* k_new;
+    const void* v_new;
+    void* k_cache;
+    void* v_cache;
+    const int32_t* seq_lens;
+    int64_t seq_stride;
+    int32_t n_seq;
+    int32_t n_new;
+    int32_t row;           /* n_kv_heads * head_dim, a multiple of 8 */
+    int32_t max_seq_len;
+} mugen_attn_kv_append_args;
+int mugen_attn_kv_append(const mugen_attn_kv_append_args* args, void* stream);
+
+/*
+ * seq_lens[b] = min(seq_lens[b] + n, max_seq_len) for b < count, on the
+ * device (KVCache::advance_seq_len, kv_cache.cpp:355-357); with n_q4
+ * non-null also n_q4[b] = n_q4_next[b] (commits a 4-bit store append).
+ * Run once per step after every layer's calls.
+ */
+int mugen_attn_seq_advance(int32_t* seq_lens, int32_t n, int32_t count, int32_t max_seq_len, int32_t* n_q4,
+                           const int32_t* n_q4_next, void* stream);
+
+/*
  * scatter_kv: dst[offset + i] = src[i], i < count, 16-bit elements.
  * Replaces scatter_kv (kernel_sources.h:3018-3028) / make_scatter_kv_dp
  * (transformer.cpp:872-886): the per-token append of K/V rows or latent
@@ -411,7 +449,8 @@ const char* mugen_attn_version(void);
  * events and returns the summed milliseconds and launch count of the kernel
  * named `kernel` ("gqa_decode", "gqa_decode_combine", "gqa_prefill",
  * "mla_decode", "mla_decode_combine", "mla_absorb", "mla_project",
- * "mla_latent_write", "kv_q4_append", "scatter_kv").
+ * "mla_latent_write", "kv_q4_append", "kv_append", "seq_advance",
+ * "scatter_kv").
  */
 int mugen_attn_timing_enable(int enable);
 int mugen_attn_timing_read(const char* kernel, double* total_ms, int64_t* launches);

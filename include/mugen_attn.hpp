@@ -76,5 +76,30 @@ inline Status mla_decode(const mugen_attn_mla_decode_args& a, void* ws, size_t w
 inline Status scatter_kv(const void* src, void* dst, uint64_t offset, uint64_t count, void* stream) {
     return check(mugen_attn_scatter_kv(src, dst, offset, count, stream));
 }
+inline Status mla_absorb(const mugen_attn_mla_absorb_args& a, void* stream) {
+    return check(mugen_attn_mla_absorb(&a, stream));
+}
+inline Status mla_project(const mugen_attn_mla_project_args& a, void* stream) {
+    return check(mugen_attn_mla_project(&a, stream));
+}
+inline Status mla_latent_write(const mugen_attn_mla_latent_write_args& a, void* stream) {
+    return check(mugen_attn_mla_latent_write(&a, stream));
+}
+inline Status kv_q4_append(const mugen_attn_kv_q4_append_args& a, void* stream) {
+    return check(mugen_attn_kv_q4_append(&a, stream));
+}
+inline size_t gqa_decode_q4_workspace_size(const mugen_attn_gqa_decode_q4_args& a) {
+    return mugen_attn_gqa_decode_q4_workspace_size(&a);
+}
+inline Status gqa_decode_q4(const mugen_attn_gqa_decode_q4_args& a, void* ws, size_t ws_bytes, void* stream) {
+    return check(mugen_attn_gqa_decode_q4(&a, ws, ws_bytes, stream));
+}
+inline Status kv_append(const mugen_attn_kv_append_args& a, void* stream) {
+    return check(mugen_attn_kv_append(&a, stream));
+}
+inline Status seq_advance(int32_t* seq_lens, int32_t n, int32_t count, int32_t max_seq_len, void* stream,
+                          int32_t* n_q4 = nullptr, const int32_t* n_q4_next = nullptr) {
+    return check(mugen_attn_seq_advance(seq_lens, n, count, max_seq_len, n_q4, n_q4_next, stream));
+}
 
 }  // namespace mugen_attn

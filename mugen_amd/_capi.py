@@ -33,6 +33,8 @@ EXPORTS = (
     "mugen_attn_mla_absorb",
     "mugen_attn_mla_project",
     "mugen_attn_mla_latent_write",
+    "mugen_attn_kv_append",
+    "mugen_attn_seq_advance",
     "mugen_attn_scatter_kv",
     "mugen_attn_last_error",
     "mugen_attn_version",
@@ -75,6 +77,13 @@ class GqaDecodeQ4Args(ctypes.Structure):
         ("q", _vp), ("store", KvQ4Store), ("seq_lens", _vp), ("n_q4", _vp), ("out", _vp),
         ("batch", _i32), ("n_heads", _i32), ("n_kv_heads", _i32), ("head_dim", _i32), ("max_seq_len", _i32),
         ("num_splits", _i32), ("scale", _f32), ("out_dtype", _i32), ("seq_lens_host", _vp),
+    ]
+
+
+class KvAppendArgs(ctypes.Structure):
+    _fields_ = [
+        ("k_new", _vp), ("v_new", _vp), ("k_cache", _vp), ("v_cache", _vp), ("seq_lens", _vp),
+        ("seq_stride", _i64), ("n_seq", _i32), ("n_new", _i32), ("row", _i32), ("max_seq_len", _i32),
     ]
 
 
@@ -165,6 +174,10 @@ def lib() -> ctypes.CDLL:
         L.mugen_attn_mla_project.restype = ctypes.c_int
         L.mugen_attn_mla_latent_write.argtypes = [ctypes.POINTER(MlaLatentWriteArgs), _vp]
         L.mugen_attn_mla_latent_write.restype = ctypes.c_int
+        L.mugen_attn_kv_append.argtypes = [ctypes.POINTER(KvAppendArgs), _vp]
+        L.mugen_attn_kv_append.restype = ctypes.c_int
+        L.mugen_attn_seq_advance.argtypes = [_vp, _i32, _i32, _i32, _vp, _vp, _vp]
+        L.mugen_attn_seq_advance.restype = ctypes.c_int
         L.mugen_attn_scatter_kv.argtypes = [_vp, _vp, ctypes.c_uint64, ctypes.c_uint64, _vp]
         L.mugen_attn_scatter_kv.restype = ctypes.c_int
         L.mugen_attn_last_error.restype = ctypes.c_char_p

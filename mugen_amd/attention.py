@@ -283,6 +283,36 @@ def mla_latent_write(kv_a: torch.Tensor, norm_w: torch.Tensor, positions: torch.
     return latent
 
 
+# ------------------------------------------------------------------ decode-step helpers
+
+def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+              seq_lens: torch.Tensor) -> None:
+    """Write row j of each sequence's new K / V ([B, n_new, Hk, d] or
+    [B, n_new, Hk*d]) at position seq_lens[b] + j of the caches
+    ([B, max_T, Hk, d]): the two scatter_kv dispatches of a decode step
+    (transformer.cpp:3749-3754) with the offset read on the device."""
+    _need_cuda(k_new, v_new, k_cache, v_cache, seq_lens)
+    B, n_new = k_new.shape[0], k_new.shape[1]
+    row = k_new[0, 0].numel()
+    if k_cache[0, 0].numel() != row or v_new.shape != k_new.shape or k_cache.shape != v_cache.shape:
+        raise ValueError("k_new / v_new rows must match the caches' rows")
+    a = _capi.KvAppendArgs()
+    a.k_new, a.v_new, a.k_cache, a.v_cache = k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr()
+    a.seq_lens, a.seq_stride = seq_lens.data_ptr(), k_cache[0].numel()
+    a.n_seq, a.n_new, a.row, a.max_seq_len = B, n_new, row, k_cache.shape[1]
+    _capi.check(_capi.lib().mugen_attn_kv_append(ctypes.byref(a), _stream(k_new.device)))
+
+
+def seq_advance(seq_lens: torch.Tensor, n: int, max_seq_len: int, n_q4: torch.Tensor | None = None,
+                n_q4_next: torch.Tensor | None = None) -> None:
+    """seq_lens += n on the device, capped at max_seq_len (and n_q4 = n_q4_next)."""
+    _need_cuda(seq_lens)
+    if seq_lens.dtype != torch.int32:
+        raise TypeError("seq_lens must be int32")
+    _capi.check(_capi.lib().mugen_attn_seq_advance(_ptr(seq_lens), int(n), seq_lens.numel(), int(max_seq_len),
+                                                    _ptr(n_q4), _ptr(n_q4_next), _stream(seq_lens.device)))
+
+
 # ------------------------------------------------------------------ scatter_kv
 
 def scatter_kv(src: torch.Tensor, dst: torch.Tensor, offset: int) -> torch.Tensor:

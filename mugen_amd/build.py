@@ -18,8 +18,8 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB_NAME = "libmugen_attn.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-SOURCES = ["capi.hip", "gqa_decode.hip", "gqa_prefill.hip", "kv_q4.hip", "mla_cache.hip", "mla_decode.hip",
-           "mla_proj.hip"]
+SOURCES = ["capi.hip", "engine.hip", "gqa_decode.hip", "gqa_prefill.hip", "kv_q4.hip", "mla_cache.hip",
+           "mla_decode.hip", "mla_proj.hip"]
 ARCH = "gfx950"
 
 
@@ -63,7 +63,27 @@ def build(verbose: bool = False) -> str:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH}")
+    build_selftest(verbose)
     return LIB_PATH
+
+
+SELFTEST = os.path.join(HERE, "engine_selftest")
+
+
+def build_selftest(verbose: bool = False) -> str:
+    """The C++ provider check (engine_selftest.cpp, run by the GPU tests),
+    linked against the in-tree library."""
+    tmp = SELFTEST + ".tmp"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-O2", "-std=c++20", "-I", INCLUDE,
+           os.path.join(HERE, "engine_selftest.cpp"), "-o", tmp, "-L", HERE, "-lmugen_attn",
+           "-Wl,-rpath,$ORIGIN", "-Wno-unused-command-line-argument"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"engine_selftest build failed:\n{r.stderr}")
+    os.replace(tmp, SELFTEST)
+    if verbose:
+        print(f"built {SELFTEST}")
+    return SELFTEST
 
 
 if __name__ == "__main__":

@@ -726,6 +726,44 @@ int mugen_attn_mla_latent_write(const mugen_attn_mla_latent_write_args* a, void*
                       "mla_latent_write launch");
 }
 
+int mugen_attn_kv_append(const mugen_attn_kv_append_args* a, void* stream) {
+    if (!a) return fail(MUGEN_ATTN_E_INVALID, "kv_append: null args");
+    if (a->n_seq < 0 || a->n_new < 0 || a->row <= 0 || a->max_seq_len <= 0)
+        return fail(MUGEN_ATTN_E_INVALID, "kv_append: bad sizes");
+    if (a->n_seq == 0 || a->n_new == 0) return MUGEN_ATTN_OK;
+    if (!a->k_new || !a->v_new || !a->k_cache || !a->v_cache || !a->seq_lens)
+        return fail(MUGEN_ATTN_E_INVALID, "kv_append: null pointer");
+    if (a->row % 8) return fail(MUGEN_ATTN_E_UNSUPPORTED, "kv_append: row must be a multiple of 8");
+    if (a->n_seq > 1 && a->seq_stride < (int64_t)a->max_seq_len * a->row)
+        return fail(MUGEN_ATTN_E_INVALID, "kv_append: seq_stride smaller than max_seq_len*row");
+    if ((((uintptr_t)a->k_new | (uintptr_t)a->v_new | (uintptr_t)a->k_cache | (uintptr_t)a->v_cache) & 15) ||
+        (a->seq_stride % 8))
+        return fail(MUGEN_ATTN_E_INVALID, "kv_append: buffers must be 16-byte aligned, seq_stride a multiple of 8");
+    if (a->n_seq > 65535) return fail(MUGEN_ATTN_E_UNSUPPORTED, "kv_append: too many sequences");
+    KvAppendParams p{};
+    p.k_new = static_cast<const uint16_t*>(a->k_new);
+    p.v_new = static_cast<const uint16_t*>(a->v_new);
+    p.k_cache = static_cast<uint16_t*>(a->k_cache);
+    p.v_cache = static_cast<uint16_t*>(a->v_cache);
+    p.seq_lens = a->seq_lens;
+    p.seq_stride = a->seq_stride;
+    p.row = a->row;
+    p.n_new = a->n_new;
+    p.max_seq_len = a->max_seq_len;
+    return hip_status(launch_kv_append(p, a->n_seq, static_cast<hipStream_t>(stream), active_timer()),
+                      "kv_append launch");
+}
+
+int mugen_attn_seq_advance(int32_t* seq_lens, int32_t n, int32_t count, int32_t max_seq_len, int32_t* n_q4,
+                           const int32_t* n_q4_next, void* stream) {
+    if (count == 0) return MUGEN_ATTN_OK;
+    if (!seq_lens || count < 0 || max_seq_len <= 0 || (n_q4 && !n_q4_next) || (n_q4 && n_q4 == n_q4_next))
+        return fail(MUGEN_ATTN_E_INVALID, "seq_advance: bad arguments");
+    return hip_status(launch_seq_advance(seq_lens, n, count, max_seq_len, n_q4, n_q4_next,
+                                         static_cast<hipStream_t>(stream), active_timer()),
+                      "seq_advance launch");
+}
+
 int mugen_attn_scatter_kv(const void* src, void* dst, uint64_t offset, uint64_t count, void* stream) {
     if (count == 0) return MUGEN_ATTN_OK;
     if (!src || !dst) return fail(MUGEN_ATTN_E_INVALID, "scatter_kv: null pointer");

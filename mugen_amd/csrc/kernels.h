@@ -161,6 +161,22 @@ struct LatentWriteParams {
 };
 hipError_t launch_mla_latent_write(const LatentWriteParams& p, int latent_dt, hipStream_t st, KernelTimer* t);
 
+// decode-step helpers (engine.hip)
+struct KvAppendParams {
+    const uint16_t* k_new;  // [n_seq][n_new][row]
+    const uint16_t* v_new;
+    uint16_t* k_cache;      // [n_seq][max_seq_len][row], seq_stride elements apart
+    uint16_t* v_cache;
+    const int32_t* seq_lens;
+    int64_t seq_stride;
+    int row;                // Hk * D
+    int n_new;
+    int max_seq_len;
+};
+hipError_t launch_kv_append(const KvAppendParams& p, int n_seq, hipStream_t st, KernelTimer* t);
+hipError_t launch_seq_advance(int32_t* seq_lens, int n, int count, int max_seq_len, int32_t* n_q4,
+                              const int32_t* n_q4_next, hipStream_t st, KernelTimer* t);
+
 hipError_t launch_scatter_kv(const uint16_t* src, uint16_t* dst, uint64_t offset, uint64_t count,
                              hipStream_t st, KernelTimer* t);
 

@@ -1,0 +1,286 @@
+// engine_selftest.cpp -- checks the C++ attention provider
+// (include/mugen_attn_engine.hpp) on the GPU: a multi-layer decode loop run
+// eagerly and the same loop replayed from one captured StepGraph must give
+// bit-identical outputs at every step (same kernels, same inputs), while the
+// device-side lengths advance by one per step inside the graph.
+//
+// Built by mugen_amd/build.py next to libmugen_attn.so; run by
+// tests/test_engine_gpu.py.  Prints PASS / FAIL lines; exit status 0 only
+// if every check passed.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "mugen_attn_engine.hpp"
+
+namespace {
+
+using mugen_attn::Status;
+
+// deterministic inputs: splitmix64 -> uniform in [-a, a) -> f16 bits
+struct Rng {
+    uint64_t s;
+    explicit Rng(uint64_t seed) : s(seed) {}
+    uint64_t next() {
+        uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    }
+    float uni(float a) { return a * (2.0f * (float)((next() >> 40) * (1.0 / 16777216.0)) - 1.0f); }
+};
+
+std::vector<uint16_t> f16_rand(Rng& r, size_t n, float a) {
+    std::vector<uint16_t> v(n);
+    for (auto& x : v) {
+        _Float16 h = (_Float16)r.uni(a);
+        std::memcpy(&x, &h, 2);
+    }
+    return v;
+}
+
+int failures = 0;
+
+bool ok(const Status& st, const char* what) {
+    if (st) return true;
+    std::printf("FAIL %s: %s\n", what, st.error().c_str());
+    failures++;
+    return false;
+}
+
+bool hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return true;
+    std::printf("FAIL %s: %s\n", what, hipGetErrorString(e));
+    failures++;
+    return false;
+}
+
+struct Dev {
+    void* p = nullptr;
+    size_t n = 0;
+    explicit Dev(size_t bytes) : n(bytes) { hip(hipMalloc(&p, bytes), "hipMalloc"); }
+    ~Dev() { (void)hipFree(p); }
+    void put(const void* h, hipStream_t st) { hip(hipMemcpyAsync(p, h, n, hipMemcpyHostToDevice, st), "upload"); }
+    std::vector<uint8_t> get(hipStream_t st) const {
+        std::vector<uint8_t> h(n);
+        hip(hipMemcpyAsync(h.data(), p, n, hipMemcpyDeviceToHost, st), "download");
+        hip(hipStreamSynchronize(st), "sync");
+        return h;
+    }
+};
+
+bool finite_f16(const std::vector<uint8_t>& b) {
+    for (size_t i = 0; i + 1 < b.size(); i += 2) {
+        uint16_t x;
+        std::memcpy(&x, &b[i], 2);
+        if ((x & 0x7c00u) == 0x7c00u) return false;
+    }
+    return true;
+}
+
+void check_lengths(const int32_t* dev_after, const std::vector<int32_t>& want, hipStream_t st, const char* what) {
+    std::vector<int32_t> got(want.size());
+    hip(hipMemcpyAsync(got.data(), dev_after, sizeof(int32_t) * got.size(), hipMemcpyDeviceToHost, st), "lengths");
+    hip(hipStreamSynchronize(st), "sync");
+    if (got != want) {
+        std::printf("FAIL %s: device lengths", what);
+        for (size_t i = 0; i < got.size(); i++) std::printf(" %d/%d", got[i], want[i]);
+        std::printf("\n");
+        failures++;
+    }
+}
+
+// ---------------------------------------------------------------- GQA
+
+void gqa_test(hipStream_t st) {
+    mugen_attn::GqaShape s;
+    s.n_layers = 3;
+    s.batch = 3;
+    s.n_heads = 28;
+    s.n_kv_heads = 4;
+    s.head_dim = 128;
+    s.max_seq_len = 1024;
+    const std::vector<int32_t> lens0 = {700, 1, 300};
+    const int steps = 5;
+    std::printf("gqa provider: layers %d batch %d H %d Hk %d d %d steps %d\n", s.n_layers, s.batch, s.n_heads,
+                s.n_kv_heads, s.head_dim, steps);
+    std::fflush(stdout);
+    std::unique_ptr<mugen_attn::GqaAttention> eager, graphed;
+    if (!ok(mugen_attn::GqaAttention::create(s, &eager), "create eager")) return;
+    if (!ok(mugen_attn::GqaAttention::create(s, &graphed), "create graphed")) return;
+    const size_t row = (size_t)s.n_kv_heads * s.head_dim;
+    const size_t cache = (size_t)s.batch * s.max_seq_len * row * 2;
+    Rng r(1);
+    for (int L = 0; L < s.n_layers; L++) {  // the context already held
+        auto k = f16_rand(r, cache / 2, 1.0f);
+        auto v = f16_rand(r, cache / 2, 1.0f);
+        for (auto* a : {eager.get(), graphed.get()}) {
+            hip(hipMemcpyAsync(a->k_cache(L), k.data(), cache, hipMemcpyHostToDevice, st), "K init");
+            hip(hipMemcpyAsync(a->v_cache(L), v.data(), cache, hipMemcpyHostToDevice, st), "V init");
+        }
+        hip(hipStreamSynchronize(st), "sync");
+    }
+    ok(eager->set_lengths(lens0, st), "eager lengths");
+    ok(graphed->set_lengths(lens0, st), "graphed lengths");
+    // fixed per-layer input / output buffers (the graph captures their addresses)
+    std::vector<std::unique_ptr<Dev>> q, kn, vn, oe, og;
+    const size_t qb = (size_t)s.batch * s.n_heads * s.head_dim * 2, kb = (size_t)s.batch * row * 2;
+    for (int L = 0; L < s.n_layers; L++) {
+        q.emplace_back(new Dev(qb));
+        kn.emplace_back(new Dev(kb));
+        vn.emplace_back(new Dev(kb));
+        oe.emplace_back(new Dev(qb));
+        og.emplace_back(new Dev(qb));
+    }
+    mugen_attn::StepGraph graph;
+    auto body = [&](hipStream_t str) -> Status {
+        for (int L = 0; L < s.n_layers; L++)
+            if (auto rr = graphed->decode_layer(L, q[L]->p, kn[L]->p, vn[L]->p, og[L]->p, str); !rr) return rr;
+        return graphed->advance(str);
+    };
+    if (!ok(graph.capture(st, body), "capture")) return;
+    for (int step = 0; step < steps; step++) {
+        Rng ri(100 + step);
+        for (int L = 0; L < s.n_layers; L++) {  // the step's new inputs, uploaded outside the graph
+            auto hq = f16_rand(ri, qb / 2, 1.0f), hk = f16_rand(ri, kb / 2, 1.0f), hv = f16_rand(ri, kb / 2, 1.0f);
+            q[L]->put(hq.data(), st);
+            kn[L]->put(hk.data(), st);
+            vn[L]->put(hv.data(), st);
+            hip(hipStreamSynchronize(st), "sync");
+        }
+        for (int L = 0; L < s.n_layers; L++)
+            ok(eager->decode_layer(L, q[L]->p, kn[L]->p, vn[L]->p, oe[L]->p, st), "eager decode");
+        ok(eager->advance(st), "eager advance");
+        hip(hipStreamSynchronize(st), "sync");
+        ok(graph.replay(st), "replay");
+        hip(hipStreamSynchronize(st), "sync");
+        for (int L = 0; L < s.n_layers; L++) {
+            const auto a = oe[L]->get(st), b = og[L]->get(st);
+            if (a != b || !finite_f16(a)) {
+                std::printf("FAIL gqa step %d layer %d: graph replay differs from the eager call\n", step, L);
+                failures++;
+            }
+        }
+        std::vector<int32_t> want(lens0);  // the next step's post-append lengths
+        for (auto& x : want) x += step + 2;
+        check_lengths(eager->lengths_after(), want, st, "gqa eager");
+        check_lengths(graphed->lengths_after(), want, st, "gqa graphed");
+    }
+    std::printf("gqa provider done\n");
+}
+
+// ---------------------------------------------------------------- MLA
+
+void mla_test(hipStream_t st) {
+    mugen_attn::MlaShape s;
+    s.n_layers = 2;
+    s.batch = 2;
+    s.n_heads = 16;
+    s.max_seq_len = 512;
+    s.rope = mugen_attn_rope_params{10000.f, 40.f, 4096};
+    const std::vector<int32_t> lens0 = {300, 5};
+    const int steps = 4;
+    std::printf("mla provider: layers %d batch %d H %d steps %d\n", s.n_layers, s.batch, s.n_heads, steps);
+    std::fflush(stdout);
+    std::unique_ptr<mugen_attn::MlaAttention> eager, graphed;
+    if (!ok(mugen_attn::MlaAttention::create(s, &eager), "create eager")) return;
+    if (!ok(mugen_attn::MlaAttention::create(s, &graphed), "create graphed")) return;
+    Rng r(2);
+    const size_t lat = (size_t)s.batch * s.max_seq_len * 576 * 2;
+    std::vector<std::unique_ptr<Dev>> norm, wkb, wvb;
+    std::vector<mugen_attn::MlaLayerWeights> w(s.n_layers);
+    for (int L = 0; L < s.n_layers; L++) {
+        auto c = f16_rand(r, lat / 2, 0.5f);
+        for (auto* a : {eager.get(), graphed.get()})
+            hip(hipMemcpyAsync(a->latent(L), c.data(), lat, hipMemcpyHostToDevice, st), "latent init");
+        auto hn = f16_rand(r, 512, 0.2f);
+        for (auto& x : hn) {  // weights near 1
+            _Float16 h;
+            std::memcpy(&h, &x, 2);
+            h = (_Float16)(1.0f + (float)h);
+            std::memcpy(&x, &h, 2);
+        }
+        auto hk = f16_rand(r, (size_t)s.n_heads * 128 * 512, 0.08f), hv = f16_rand(r, (size_t)s.n_heads * 128 * 512, 0.08f);
+        norm.emplace_back(new Dev(512 * 2));
+        wkb.emplace_back(new Dev(hk.size() * 2));
+        wvb.emplace_back(new Dev(hv.size() * 2));
+        norm[L]->put(hn.data(), st);
+        wkb[L]->put(hk.data(), st);
+        wvb[L]->put(hv.data(), st);
+        hip(hipStreamSynchronize(st), "sync");
+        w[L].kv_a_norm = norm[L]->p;
+        w[L].w_kb = wkb[L]->p;
+        w[L].w_vb = wvb[L]->p;
+        w[L].w_type = MUGEN_ATTN_W_F16;
+    }
+    ok(eager->set_lengths(lens0, st), "eager lengths");
+    ok(graphed->set_lengths(lens0, st), "graphed lengths");
+    std::vector<std::unique_ptr<Dev>> q, kva, oe, og;
+    const size_t qb = (size_t)s.batch * s.n_heads * 192 * 2, kb = (size_t)s.batch * 576 * 2,
+                 ob = (size_t)s.batch * s.n_heads * 128 * 2;
+    for (int L = 0; L < s.n_layers; L++) {
+        q.emplace_back(new Dev(qb));
+        kva.emplace_back(new Dev(kb));
+        oe.emplace_back(new Dev(ob));
+        og.emplace_back(new Dev(ob));
+    }
+    mugen_attn::StepGraph graph;
+    auto body = [&](hipStream_t str) -> Status {
+        for (int L = 0; L < s.n_layers; L++)
+            if (auto rr = graphed->decode_layer(L, w[L], q[L]->p, kva[L]->p, og[L]->p, str); !rr) return rr;
+        return graphed->advance(str);
+    };
+    if (!ok(graph.capture(st, body), "capture")) return;
+    for (int step = 0; step < steps; step++) {
+        Rng ri(200 + step);
+        for (int L = 0; L < s.n_layers; L++) {
+            auto hq = f16_rand(ri, qb / 2, 1.0f), hk = f16_rand(ri, kb / 2, 1.0f);
+            q[L]->put(hq.data(), st);
+            kva[L]->put(hk.data(), st);
+            hip(hipStreamSynchronize(st), "sync");
+        }
+        for (int L = 0; L < s.n_layers; L++)
+            ok(eager->decode_layer(L, w[L], q[L]->p, kva[L]->p, oe[L]->p, st), "eager decode");
+        ok(eager->advance(st), "eager advance");
+        hip(hipStreamSynchronize(st), "sync");
+        ok(graph.replay(st), "replay");
+        hip(hipStreamSynchronize(st), "sync");
+        for (int L = 0; L < s.n_layers; L++) {
+            const auto a = oe[L]->get(st), b = og[L]->get(st);
+            if (a != b || !finite_f16(a)) {
+                std::printf("FAIL mla step %d layer %d: graph replay differs from the eager call\n", step, L);
+                failures++;
+            }
+            // the latent rows written this step agree as well
+            std::vector<uint8_t> le(lat), lg(lat);
+            hip(hipMemcpyAsync(le.data(), eager->latent(L), lat, hipMemcpyDeviceToHost, st), "latent");
+            hip(hipMemcpyAsync(lg.data(), graphed->latent(L), lat, hipMemcpyDeviceToHost, st), "latent");
+            hip(hipStreamSynchronize(st), "sync");
+            if (le != lg) {
+                std::printf("FAIL mla step %d layer %d: latent caches differ\n", step, L);
+                failures++;
+            }
+        }
+        std::vector<int32_t> want(lens0);  // the next step's post-append lengths
+        for (auto& x : want) x += step + 2;
+        check_lengths(eager->lengths_after(), want, st, "mla eager");
+        check_lengths(graphed->lengths_after(), want, st, "mla graphed");
+    }
+    std::printf("mla provider done\n");
+}
+
+}  // namespace
+
+int main() {
+    hipStream_t st;
+    if (!hip(hipStreamCreate(&st), "hipStreamCreate")) return 1;
+    gqa_test(st);
+    mla_test(st);
+    (void)hipStreamSynchronize(st);
+    (void)hipStreamDestroy(st);
+    std::printf(failures ? "FAIL (%d)\n" : "PASS\n", failures);
+    return failures ? 1 : 0;
+}

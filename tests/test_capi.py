@@ -232,3 +232,33 @@ def test_kv_q4_validation():
     assert L.mugen_attn_gqa_decode_q4(ctypes.byref(d), None, 0, None) == _capi.E_INVALID   # misaligned store
     d.store.q4_k, d.store.ring = 0x1000, 300
     assert L.mugen_attn_gqa_decode_q4(ctypes.byref(d), None, 0, None) == _capi.E_INVALID   # ring not a power of two
+
+
+def test_engine_header_compiles(tmp_path):
+    """include/mugen_attn_engine.hpp (the C++ provider) compiles as C++20 and
+    C++23 host code against the HIP runtime headers."""
+    import shutil
+    import subprocess
+    cxx = shutil.which("g++")
+    if cxx is None or not os.path.isdir("/opt/rocm/include"):
+        pytest.skip("no host C++ compiler / ROCm headers")
+    src = tmp_path / "engine.cpp"
+    src.write_text('#include "mugen_attn_engine.hpp"\n'
+                   "int main() { mugen_attn::GqaShape s; mugen_attn::StepGraph g; return s.n_layers; }\n")
+    for std in ("c++20", "c++23"):
+        subprocess.run([cxx, f"-std={std}", "-Wall", "-Werror", "-D__HIP_PLATFORM_AMD__", "-c", str(src),
+                        "-I", os.path.join(ROOT, "include"), "-I", "/opt/rocm/include", "-o",
+                        str(tmp_path / f"engine_{std}.o")], check=True)
+
+
+def test_kv_append_and_seq_advance_validation():
+    L = _capi.lib()
+    a = _capi.KvAppendArgs()
+    a.k_new = a.v_new = a.k_cache = a.v_cache = a.seq_lens = 0x1000
+    a.seq_stride, a.n_seq, a.n_new, a.row, a.max_seq_len = 64 * 512, 2, 1, 512, 64
+    for field, val in [("row", 12), ("seq_stride", 100), ("k_cache", 0x1004), ("seq_lens", 0)]:
+        b = _capi.KvAppendArgs.from_buffer_copy(a)
+        setattr(b, field, val)
+        assert L.mugen_attn_kv_append(ctypes.byref(b), None) in (_capi.E_INVALID, _capi.E_UNSUPPORTED), field
+    assert L.mugen_attn_seq_advance(None, 1, 4, 64, None, None, None) == _capi.E_INVALID
+    assert L.mugen_attn_seq_advance(None, 1, 0, 64, None, None, None) == _capi.OK

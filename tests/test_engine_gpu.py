@@ -1,0 +1,88 @@
+"""The engine hook: a decode step's attention calls captured once into a
+HIP graph and replayed step after step, every per-step value (positions,
+lengths) read from device memory -- the counterpart of the reference's
+cached mega-chain (transformer.cpp:3734-3833), which patches pos /
+kv_offset / seq_len into its cached dispatches before each step.
+
+* test_cpp_provider_selftest: the C++ provider (include/mugen_attn_engine.hpp)
+  replays a captured multi-layer GQA and MLA step bit-identically to eager
+  calls (mugen_amd/engine_selftest.cpp);
+* test_step_graph_replays_match_oracle: a captured step (kv_append +
+  decode per layer + seq_advance) replayed several times, with eager uploads
+  and synchronisations between replays, each replay checked against the
+  oracle at that step's lengths."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+import mugen_amd
+from oracle import oracle as O
+from tests import cases as C
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_cpp_provider_selftest(device):
+    exe = os.path.join(ROOT, "mugen_amd", "engine_selftest")
+    assert os.path.exists(exe), "engine_selftest is built by mugen_amd/build.py"
+    C.say("engine_selftest (C++ provider, captured step vs eager)")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    print(r.stdout[-4000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and r.stdout.strip().endswith("PASS"), r.stdout[-2000:]
+
+
+def test_step_graph_replays_match_oracle(device):
+    n_layers, B, H, Hk, D, max_T = 2, 3, 28, 4, 128, 600
+    lens = np.array([400, 1, 77], np.int32)
+    steps = 4
+    row = Hk * D
+    K = [O.round_to(O.randn(300 + l, (B, max_T, row)), C.F16)[1] for l in range(n_layers)]
+    V = [O.round_to(O.randn(400 + l, (B, max_T, row)), C.F16)[1] for l in range(n_layers)]
+    kc = [C.to_dev(k, C.F16, device).view(B, max_T, Hk, D) for k in K]
+    vc = [C.to_dev(v, C.F16, device).view(B, max_T, Hk, D) for v in V]
+    seq = torch.from_numpy(np.concatenate([lens, lens + 1])).to(device)   # [before | after] the append
+    q_in = [torch.empty((B, H, D), dtype=torch.float16, device=device) for _ in range(n_layers)]
+    k_in = [torch.empty((B, 1, row), dtype=torch.float16, device=device) for _ in range(n_layers)]
+    v_in = [torch.empty((B, 1, row), dtype=torch.float16, device=device) for _ in range(n_layers)]
+    out = [torch.empty((B, H, D), dtype=torch.float32, device=device) for _ in range(n_layers)]
+    ws = [torch.empty(1 << 24, dtype=torch.uint8, device=device) for _ in range(n_layers)]
+
+    def step():
+        for l in range(n_layers):
+            mugen_amd.kv_append(k_in[l], v_in[l], kc[l], vc[l], seq[:B])
+            mugen_amd.attention_decode(q_in[l], kc[l], vc[l], seq[B:], max_T, out=out[l], workspace=ws[l])
+        mugen_amd.seq_advance(seq, 1, max_T)
+
+    C.say(f"captured GQA step: layers {n_layers} batch {B} lens {list(lens)}")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    torch.cuda.synchronize()
+    assert seq.cpu().tolist() == list(lens) + list(lens + 1)  # capture ran nothing
+    for t in range(steps):
+        qs, ks, vs = [], [], []
+        for l in range(n_layers):   # this step's inputs, uploaded eagerly
+            qb = O.round_to(O.randn(500 + 10 * t + l, (B, H, D)), C.F16)[1]
+            kb = O.round_to(O.randn(600 + 10 * t + l, (B, 1, row)), C.F16)[1]
+            vb = O.round_to(O.randn(700 + 10 * t + l, (B, 1, row)), C.F16)[1]
+            q_in[l].copy_(C.to_dev(qb, C.F16, device))
+            k_in[l].copy_(C.to_dev(kb, C.F16, device))
+            v_in[l].copy_(C.to_dev(vb, C.F16, device))
+            qs.append(qb)
+            for b in range(B):      # the host mirror of the append
+                K[l][b, lens[b]] = kb[b, 0]
+                V[l][b, lens[b]] = vb[b, 0]
+        torch.cuda.synchronize()
+        C.say(f"replay {t}: lens after append {list(lens + 1)}")
+        g.replay()
+        torch.cuda.synchronize()
+        lens = lens + 1
+        assert seq.cpu().tolist() == list(lens) + list(lens + 1)
+        f = lambda x: x.view(np.float16).astype(np.float32)
+        for l in range(n_layers):
+            ref = O.gqa_attention(f(qs[l]), f(K[l]), f(V[l]), lens, H, Hk, D, max_T * row, nthreads=8)
+            C.assert_close(out[l].cpu().numpy(), ref, f"replay {t} layer {l}")
