@@ -138,34 +138,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     // 4-bit store: tokens below nq are 20-byte groups (group kvh*D/32 + c of
     // a token row holds dims 32c .. 32c+31 of this kv head), the rest f16
     // ring rows (token t at slot t % ring, a power of two).  The Q4 rows are
-    // read through buffer resources (one per sequence: 32-bit offsets, one
-    // instruction per dword) and arrive raw; they are expanded one block
-    // later (unpack_block), so the loads stay in flight.
+    // read through buffer resources (one per sequence, 32-bit offsets) a
+    // whole group run per load, arrive raw and are expanded one block later
+    // (unpack_block), so the loads stay in flight:
+    //  * K: in a Q4 split the S contraction runs over a permuted dim order --
+    //    in MFMA k-step kk lane (g, n) supplies dims 8*KK*g + 8kk .. +7, so
+    //    a lane's dims are one contiguous run of 8*KK inside one group, and q
+    //    is loaded in the same order (S = K.Q^T is unchanged).  Per token a
+    //    lane reads the group's (scale|min) dword and its 4*KK nibble bytes:
+    //    two loads instead of 2*KK;
+    //  * V: a lane reads whole groups (dword + 16 bytes) and writes their 32
+    //    dequantised values to the staging rows itself.
     const int64_t q4sb = Q4 ? (int64_t)b * p.q4_seq_stride : 0;
     const __amdgpu_buffer_rsrc_t rq4k =
         __builtin_amdgcn_make_buffer_rsrc((void*)(Q4 ? p.q4k + q4sb : nullptr), 0, 0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t rq4v =
         __builtin_amdgcn_make_buffer_rsrc((void*)(Q4 ? p.q4v + q4sb : nullptr), 0, 0x7fffffff, 0x00020000);
     const uint32_t q4head = (uint32_t)kvh * (D / 32) * 20;
-    auto load_q4raw = [&](__amdgpu_buffer_rsrc_t r, int t, int d0) -> u32x4_t {
-        const int off = (int)((uint32_t)t * (uint32_t)p.q4_row_bytes + q4head + (uint32_t)((d0 >> 5) * 20));
-        const uint32_t sm = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-        const uint32_t nib = __builtin_amdgcn_raw_buffer_load_b32(r, off + 4 + ((d0 & 31) >> 1), 0, 0);
-        u32x4_t v;
-        v[0] = sm;
-        v[1] = nib;
-        return v;
+    // byte offset of group gq (of this kv head) of token t
+    auto q4_off = [&](int t, int gq) -> int {
+        return (int)((uint32_t)t * (uint32_t)p.q4_row_bytes + q4head + (uint32_t)(gq * 20));
     };
+    constexpr int NGV = D / 64;  // V groups per lane per 32-token block
     auto load_f16 = [&](const uint16_t* base, int t, int d0) -> u32x4_t {
         if constexpr (Q4) return load16(base + ((uint32_t)(t & (p.ring - 1)) * (uint32_t)p.row_stride + (uint32_t)d0));
         else return load16(base + (int64_t)t * p.row_stride + d0);
     };
-    // Q^T as the B operand: lane holds q[head n][32kk + 8g .. +8]
+    // Q^T as the B operand: lane holds q[head n][32kk + 8g .. +8] (Q4
+    // splits: q[head n][8*KK*g + 8kk .. +8], the permuted order above)
     u32x4_t qf[KK];
     if (n < G) {
         const uint16_t* qp = p.q + ((int64_t)b * p.H + h0 + n) * D;
 #pragma unroll
-        for (int kk = 0; kk < KK; kk++) qf[kk] = load16(qp + 32 * kk + 8 * g);
+        for (int kk = 0; kk < KK; kk++) qf[kk] = load16(qp + (q4_split ? 8 * KK * g + 8 * kk : 32 * kk + 8 * g));
     } else {
 #pragma unroll
         for (int kk = 0; kk < KK; kk++) qf[kk] = u32x4_t{0, 0, 0, 0};
@@ -178,20 +183,45 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     // prefetch's wait counts stay exact)
     auto load_block = [&](int t0, u32x4_t (&kq)[2][KK], u32x4_t (&vq)[VL], auto qb_tag) {
         constexpr bool QB = decltype(qb_tag)::value;
+        if constexpr (QB) {
+            // K: kq[nb][0] = the lane's 4*KK nibble bytes, kq[nb][1][0] = (scale|min)
+            const int d0 = 8 * KK * g;
 #pragma unroll
-        for (int nb = 0; nb < 2; nb++) {
-            const int tk = min(t0 + kr0 + 4 * nb, t_end - 1);
-#pragma unroll
-            for (int kk = 0; kk < KK; kk++) {
-                const int d0 = 32 * kk + 8 * g;
-                kq[nb][kk] = QB ? load_q4raw(rq4k, tk, d0) : load_f16(kbase, tk, d0);
+            for (int nb = 0; nb < 2; nb++) {
+                const int tk = min(t0 + kr0 + 4 * nb, t_end - 1);
+                const int off = q4_off(tk, d0 >> 5);
+                const int noff = off + 4 + ((d0 & 31) >> 1);
+                if constexpr (KK == 4) {
+                    kq[nb][0] = __builtin_amdgcn_raw_buffer_load_b128(rq4k, noff, 0, 0);
+                } else {
+                    const auto h = __builtin_amdgcn_raw_buffer_load_b64(rq4k, noff, 0, 0);
+                    kq[nb][0][0] = h[0];
+                    kq[nb][0][1] = h[1];
+                }
+                kq[nb][1][0] = __builtin_amdgcn_raw_buffer_load_b32(rq4k, off, 0, 0);
             }
-        }
+            // V: group G = lane + 64i of the block (row G / (D/32), group G % (D/32)):
+            // vq[2i] = its 16 nibble bytes, vq[2i+1][0] = its (scale|min)
 #pragma unroll
-        for (int j = 0; j < VL; j++) {
-            const int tv = min(t0 + j * RPL + lane / (RB / 16), t_end - 1);
-            const int d0 = 8 * (lane % (RB / 16));
-            vq[j] = QB ? load_q4raw(rq4v, tv, d0) : load_f16(vbase, tv, d0);
+            for (int i = 0; i < NGV; i++) {
+                const int G = lane + 64 * i;
+                const int tv = min(t0 + G / (D / 32), t_end - 1);
+                const int off = q4_off(tv, G % (D / 32));
+                vq[2 * i] = __builtin_amdgcn_raw_buffer_load_b128(rq4v, off + 4, 0, 0);
+                vq[2 * i + 1][0] = __builtin_amdgcn_raw_buffer_load_b32(rq4v, off, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int nb = 0; nb < 2; nb++) {
+                const int tk = min(t0 + kr0 + 4 * nb, t_end - 1);
+#pragma unroll
+                for (int kk = 0; kk < KK; kk++) kq[nb][kk] = load_f16(kbase, tk, 32 * kk + 8 * g);
+            }
+#pragma unroll
+            for (int j = 0; j < VL; j++) {
+                const int tv = min(t0 + j * RPL + lane / (RB / 16), t_end - 1);
+                vq[j] = load_f16(vbase, tv, 8 * (lane % (RB / 16)));
+            }
         }
     };
     // V staging: load j of lane l is row j*RPL + l/(RB/16), chunk l%(RB/16)
@@ -200,7 +230,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
     for (int j = 0; j < VL; j++) {
         const int r = j * RPL + lane / (RB / 16), c = lane % (RB / 16);
-        st_off[j] = r * RB + ((c ^ vswz<D>(r)) * 16);
+        // Q4 splits: chunk j % 4 of the lane's group j / 4 (see load_block)
+        const int G = lane + 64 * (j >> 2);
+        const int rq = G / (D / 32), cq = 4 * (G % (D / 32)) + (j & 3);
+        st_off[j] = q4_split ? rq * RB + ((cq ^ vswz<D>(rq)) * 16) : r * RB + ((c ^ vswz<D>(r)) * 16);
     }
     // transpose reads: lane (g, n) reads row 8g + n/4 (+4), logical bytes
     // 32d + 8(n%4) = chunk 2d + (n%4)/2, half n%2
@@ -221,11 +254,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     auto unpack_block = [&](u32x4_t (&kq)[2][KK], u32x4_t (&vq)[VL], auto qb_tag) {
         if constexpr (decltype(qb_tag)::value) {
 #pragma unroll
-            for (int nb = 0; nb < 2; nb++)
+            for (int nb = 0; nb < 2; nb++) {
+                const u32x4_t nib = kq[nb][0];
+                const uint32_t sm = kq[nb][1][0];
 #pragma unroll
-                for (int kk = 0; kk < KK; kk++) kq[nb][kk] = dequant_q4x8(kq[nb][kk][0], kq[nb][kk][1]);
+                for (int kk = 0; kk < KK; kk++) kq[nb][kk] = dequant_q4x8(sm, nib[kk]);
+            }
 #pragma unroll
-            for (int j = 0; j < VL; j++) vq[j] = dequant_q4x8(vq[j][0], vq[j][1]);
+            for (int i = NGV - 1; i >= 0; i--) {
+                const u32x4_t nib = vq[2 * i];
+                const uint32_t sm = vq[2 * i + 1][0];
+#pragma unroll
+                for (int c = 0; c < 4; c++) vq[4 * i + c] = dequant_q4x8(sm, nib[c]);
+            }
         }
     };
     auto main_loop = [&](auto qb_tag) {
