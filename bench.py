@@ -262,16 +262,27 @@ def capture(case, n):
     return g
 
 
+WARMUP_MIN_S = 0.3  # untimed GPU work before timing: clocks settle
+
+
 def time_case(case, steps, warmup, dev):
     """Warm-up, then EXACTLY `steps` steps timed with events between two
-    synchronisations.  The steps run as replays of captured HIP graphs (up
-    to GRAPH_STEPS steps each): the GPU executes the same kernels on the same
-    resident inputs as an eager call, without the per-call Python/ctypes
-    launch cost (~13 us), which would otherwise be what the small cases
-    measure."""
+    synchronisations.  Warm-up is `warmup` untimed steps, continued (still
+    untimed) until at least WARMUP_MIN_S of wall time has passed: the first
+    workload measured in a fresh process otherwise runs ~8% slower than the
+    same kernels a second later (the GPU's clocks ramp up).  The steps run as
+    replays of captured HIP graphs (up to GRAPH_STEPS steps each): the GPU
+    executes the same kernels on the same resident inputs as an eager call,
+    without the per-call Python/ctypes launch cost (~13 us), which would
+    otherwise be what the small cases measure."""
+    t_w = time.perf_counter()
     for _ in range(warmup):
         case.step()
     torch.cuda.synchronize(dev)
+    while time.perf_counter() - t_w < WARMUP_MIN_S:
+        for _ in range(20):
+            case.step()
+        torch.cuda.synchronize(dev)
     per = min(GRAPH_STEPS, steps)
     full, rest = divmod(steps, per)
     graphs = [(capture(case, per), full)] + ([(capture(case, rest), 1)] if rest else [])
