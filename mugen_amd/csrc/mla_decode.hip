@@ -691,7 +691,7 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
         int teff_min = teff;
 #pragma unroll
         for (int m = 1; m < 64; m <<= 1) teff_min = min(teff_min, __shfl_xor(teff_min, m, 64));
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): q is in registers
+        // q is waited for chunk by chunk in the first tile's k-loop
         MUGEN_TRACE(1);
         const int ar0 = 8 * (n >> 2) + (n & 3);
         const int hA = swz(ar0);
@@ -720,6 +720,17 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
             f32x4_t sacc[2];
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
+                // first tile: wait for q chunk ks only (the 18 q loads are the
+                // S wave's only vector-memory operations before this loop)
+                if (j == 0) {
+                    switch (KS - 1 - ks) {  // ks is a constant after unrolling: one s_waitcnt
+#define MLA_VMW(N) case N: vm_wait<N>(); break;
+                        MLA_VMW(0) MLA_VMW(1) MLA_VMW(2) MLA_VMW(3) MLA_VMW(4) MLA_VMW(5) MLA_VMW(6) MLA_VMW(7)
+                        MLA_VMW(8) MLA_VMW(9) MLA_VMW(10) MLA_VMW(11) MLA_VMW(12) MLA_VMW(13) MLA_VMW(14)
+                        MLA_VMW(15) MLA_VMW(16) MLA_VMW(17)
+#undef MLA_VMW
+                    }
+                }
 #pragma unroll
                 for (int nb = 0; nb < 2; nb++) {
                     if (ks == 0) mfma_s<DT, true>(sacc[nb], abuf[ks % SPD][nb], qf[ks]);
