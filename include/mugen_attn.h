@@ -319,7 +319,10 @@ typedef struct mugen_attn_rope_params {
  * rows = batch * q_len.  Supported: nope_dim 128, rope_dim 64, kv_rank 512.
  * With positions (device int32 [rows]) non-null, the appended q_rope is
  * first rotated by the reference's q RoPE stage (transformer.cpp:3882-3921,
- * f16 results) at positions[r]; q itself is not modified.
+ * f16 results) at positions[r]; q itself is not modified.  With positions
+ * null and seq_base non-null, row r's position is
+ * seq_base[r / rows_per_seq] + r % rows_per_seq (the tokens a sequence
+ * appends in one step: a captured graph replays it unchanged).
  */
 typedef struct mugen_attn_mla_absorb_args {
     const void* q;
@@ -333,7 +336,9 @@ typedef struct mugen_attn_mla_absorb_args {
     int32_t w_type;    /* mugen_attn_wtype */
     int32_t out_dtype; /* F32 or BF16 */
     const int32_t* positions;    /* optional: RoPE q_rope at these positions */
-    mugen_attn_rope_params rope; /* used when positions is non-null */
+    mugen_attn_rope_params rope; /* used when positions or seq_base is non-null */
+    const int32_t* seq_base;     /* optional, with positions null: see above */
+    int32_t rows_per_seq;        /* rows per sequence for seq_base (q_len) */
 } mugen_attn_mla_absorb_args;
 int mugen_attn_mla_absorb(const mugen_attn_mla_absorb_args* args, void* stream);
 
@@ -367,7 +372,9 @@ int mugen_attn_mla_project(const mugen_attn_mla_project_args* args, void* stream
  * round trip (read kv_a, normalise and rotate on the CPU, scatter_kv).
  *   kv_a      [rows][kv_rank + rope_dim] F16 (the kv_a_mqa projection)
  *   norm_w    [kv_rank] F16 (attn_kv_a_norm)
- *   positions [rows] device int32; rows outside [0, max_seq_len) are skipped
+ *   positions [rows] device int32; rows outside [0, max_seq_len) are skipped;
+ *             or null with seq_base (device int32 [n_seq]): row r goes to
+ *             seq_base[r / rows_per_seq] + r % rows_per_seq
  *   latent    [n_seq][max_seq_len][kv_rank + rope_dim], seq_stride elements
  *             apart; F16 (the reference's rounding) or BF16
  * Supported: kv_rank 512, rope_dim 64.
@@ -386,6 +393,7 @@ typedef struct mugen_attn_mla_latent_write_args {
     int64_t seq_stride;
     float eps;
     mugen_attn_rope_params rope;
+    const int32_t* seq_base; /* used when positions is null */
 } mugen_attn_mla_latent_write_args;
 int mugen_attn_mla_latent_write(const mugen_attn_mla_latent_write_args* args, void* stream);
 

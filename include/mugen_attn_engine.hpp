@@ -27,6 +27,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <memory>
 #include <string>
@@ -176,6 +177,7 @@ public:
                                     "GqaAttention::set_lengths");
             !r)
             return r;
+        host_lens_ = lens;
         return detail::hip_ok(hipStreamSynchronize(st), "GqaAttention::set_lengths");
     }
 
@@ -201,8 +203,52 @@ public:
         return gqa_decode(d, ws_.ptr, ws_.bytes, st);
     }
 
-    // End of a step: every length += n (device side, capturable).
+    // Prompt of n_tokens for sequence 0 (batch 1), one layer: append its K / V
+    // rows at the current length, then causal flash attention over the cache
+    // (make_prefill_attention_dp, transformer.cpp:828-850, :1915).  Uses the
+    // host copy of the length, so it is not for captured steps; call
+    // advance(st, n_tokens) after the last layer.
+    //   q [n_tokens][H][d], k_new / v_new [n_tokens][Hk*d], out [n_tokens][H][d]
+    Status prefill_layer(int L, const void* q, const void* k_new, const void* v_new, void* out, int n_tokens,
+                         hipStream_t st) {
+        if (L < 0 || L >= s_.n_layers) return fail("GqaAttention::prefill_layer: bad layer");
+        if (s_.batch != 1) return fail("GqaAttention::prefill_layer: one sequence (batch 1)");
+        const int start = host_lens_.empty() ? 0 : host_lens_[0];
+        if (start + n_tokens > s_.max_seq_len) return fail("GqaAttention::prefill_layer: prompt past max_seq_len");
+        mugen_attn_kv_append_args ap{};
+        ap.k_new = k_new;
+        ap.v_new = v_new;
+        ap.k_cache = k_[L].ptr;
+        ap.v_cache = v_[L].ptr;
+        ap.seq_lens = before();
+        ap.seq_stride = (int64_t)s_.max_seq_len * s_.n_kv_heads * s_.head_dim;
+        ap.n_seq = 1;
+        ap.n_new = n_tokens;
+        ap.row = s_.n_kv_heads * s_.head_dim;
+        ap.max_seq_len = s_.max_seq_len;
+        if (auto r = kv_append(ap, st); !r) return r;
+        mugen_attn_gqa_prefill_args pf{};
+        pf.q = q;
+        pf.k = k_[L].ptr;
+        pf.v = v_[L].ptr;
+        pf.out = out;
+        pf.n_tokens = n_tokens;
+        pf.n_heads = s_.n_heads;
+        pf.n_kv_heads = s_.n_kv_heads;
+        pf.head_dim = s_.head_dim;
+        pf.kv_len = start + n_tokens;
+        pf.start_pos = start;
+        pf.causal = 1;
+        pf.scale = s_.scale;
+        pf.dtype = s_.kv_dtype;
+        pf.out_dtype = s_.out_dtype;
+        return gqa_prefill(pf, st);
+    }
+
+    // End of a step: every length += n (device side, capturable; the host
+    // copy used by prefill_layer follows).
     Status advance(hipStream_t st, int n = 1) {
+        for (auto& x : host_lens_) x = std::min(x + n, s_.max_seq_len);
         return seq_advance(static_cast<int32_t*>(lens_.ptr), n, 2 * s_.batch, s_.max_seq_len, st);
     }
 
@@ -237,6 +283,7 @@ private:
     GqaShape s_;
     std::vector<detail::DeviceBuffer> k_, v_;
     detail::DeviceBuffer lens_, ws_;
+    std::vector<int32_t> host_lens_;
 };
 
 // ---------------------------------------------------------------- MLA
@@ -246,6 +293,7 @@ struct MlaShape {
     int batch = 1;
     int n_heads = 0;          // 128 (V3), 16 (V2-Lite)
     int max_seq_len = 0;
+    int q_len = 1;            // tokens per sequence per step: 1 decode, > 1 speculative verify
     float scale = 0.f;        // 1/sqrt(qk_nope + qk_rope), transformer.cpp:2550
     float rms_norm_eps = 1e-6f;
     mugen_attn_rope_params rope{10000.f, 0.f, 0};
@@ -274,7 +322,8 @@ public:
             if (auto r = a->lat_[L].alloc((size_t)s.batch * s.max_seq_len * 576 * 2, "MlaAttention latent"); !r)
                 return r;
         if (auto r = a->lens_.alloc(sizeof(int32_t) * 2 * s.batch, "MlaAttention lengths"); !r) return r;
-        const size_t rows = (size_t)s.batch * s.n_heads;
+        if (s.q_len <= 0) return fail("MlaAttention: q_len must be > 0");
+        const size_t rows = (size_t)s.batch * s.q_len * s.n_heads;
         if (auto r = a->qabs_.alloc(rows * 576 * 4, "MlaAttention q_abs"); !r) return r;
         if (auto r = a->o_.alloc(rows * 512 * 4, "MlaAttention o"); !r) return r;
         mugen_attn_mla_decode_args m = a->core_args(0);
@@ -288,8 +337,8 @@ public:
 
     Status set_lengths(const std::vector<int32_t>& lens, hipStream_t st) {
         if ((int)lens.size() != s_.batch) return fail("MlaAttention::set_lengths: one length per sequence");
-        std::vector<int32_t> both(lens);  // [before | after]: a step appends one token and attends to it
-        for (int32_t x : lens) both.push_back(x + 1);
+        std::vector<int32_t> both(lens);  // [before | after]: a step appends q_len tokens and attends to them
+        for (int32_t x : lens) both.push_back(x + s_.q_len);
         // from pageable host memory: wait for the copy before `both` goes away
         if (auto r = detail::hip_ok(hipMemcpyAsync(lens_.ptr, both.data(), sizeof(int32_t) * both.size(),
                                                    hipMemcpyHostToDevice, st),
@@ -299,20 +348,22 @@ public:
         return detail::hip_ok(hipStreamSynchronize(st), "MlaAttention::set_lengths");
     }
 
-    // One layer of a decode step (one new token per sequence):
-    //   q    [batch][H][192] f16 (buf_mla_q, before its RoPE)
-    //   kv_a [batch][576]    f16 (buf_mla_kv_a, before RMSNorm / RoPE)
-    //   out  [batch][H][128] f16 (the attention output fed to wo)
+    // One layer of a step: q_len new tokens per sequence (1 for decode; the
+    // draft tokens of a speculative verify otherwise, causal among them --
+    // the reference's per-token calls, transformer.cpp:1325-1337):
+    //   q    [batch][q_len][H][192] f16 (buf_mla_q, before its RoPE)
+    //   kv_a [batch][q_len][576]    f16 (buf_mla_kv_a, before RMSNorm / RoPE)
+    //   out  [batch][q_len][H][128] f16 (the attention output fed to wo)
     Status decode_layer(int L, const MlaLayerWeights& w, const void* q, const void* kv_a, void* out,
                         hipStream_t st) {
         if (L < 0 || L >= s_.n_layers) return fail("MlaAttention::decode_layer: bad layer");
         mugen_attn_mla_latent_write_args lw{};
         lw.kv_a = kv_a;
         lw.norm_w = w.kv_a_norm;
-        lw.positions = before();  // the new token's position = tokens held before it
+        lw.seq_base = before();  // token j of sequence b goes to before[b] + j
         lw.latent = lat_[L].ptr;
-        lw.rows = s_.batch;
-        lw.rows_per_seq = 1;
+        lw.rows = s_.batch * s_.q_len;
+        lw.rows_per_seq = s_.q_len;
         lw.max_seq_len = s_.max_seq_len;
         lw.kv_rank = 512;
         lw.rope_dim = 64;
@@ -325,14 +376,15 @@ public:
         ab.q = q;
         ab.w_kb = w.w_kb;
         ab.q_abs = qabs_.ptr;
-        ab.rows = s_.batch;
+        ab.rows = s_.batch * s_.q_len;
         ab.n_heads = s_.n_heads;
         ab.nope_dim = 128;
         ab.rope_dim = 64;
         ab.kv_rank = 512;
         ab.w_type = w.w_type;
         ab.out_dtype = MUGEN_ATTN_F32;
-        ab.positions = before();
+        ab.seq_base = before();
+        ab.rows_per_seq = s_.q_len;
         ab.rope = s_.rope;
         if (auto r = mla_absorb(ab, st); !r) return r;
         const mugen_attn_mla_decode_args m = core_args(L);
@@ -341,7 +393,7 @@ public:
         pr.o = o_.ptr;
         pr.w_vb = w.w_vb;
         pr.out = out;
-        pr.rows = s_.batch;
+        pr.rows = s_.batch * s_.q_len;
         pr.n_heads = s_.n_heads;
         pr.kv_rank = 512;
         pr.v_head_dim = 128;
@@ -350,6 +402,9 @@ public:
         return mla_project(pr, st);
     }
 
+    // End of a step: every length += n, the tokens kept (q_len for decode;
+    // the accepted ones after a verify -- the others are overwritten by the
+    // next step's writes).  Device side, capturable.
     Status advance(hipStream_t st, int n = 1) {
         return seq_advance(static_cast<int32_t*>(lens_.ptr), n, 2 * s_.batch, s_.max_seq_len, st);
     }
@@ -368,7 +423,7 @@ private:
         m.seq_lens = lengths_after();
         m.out = o_.ptr;
         m.batch = s_.batch;
-        m.q_len = 1;
+        m.q_len = s_.q_len;
         m.n_heads = s_.n_heads;
         m.kv_rank = 512;
         m.rope_dim = 64;

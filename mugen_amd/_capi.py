@@ -114,6 +114,7 @@ class MlaAbsorbArgs(ctypes.Structure):
         ("q", _vp), ("w_kb", _vp), ("q_abs", _vp),
         ("rows", _i32), ("n_heads", _i32), ("nope_dim", _i32), ("rope_dim", _i32), ("kv_rank", _i32),
         ("w_type", _i32), ("out_dtype", _i32), ("positions", _vp), ("rope", RopeParams),
+        ("seq_base", _vp), ("rows_per_seq", _i32),
     ]
 
 
@@ -122,6 +123,7 @@ class MlaLatentWriteArgs(ctypes.Structure):
         ("kv_a", _vp), ("norm_w", _vp), ("positions", _vp), ("latent", _vp),
         ("rows", _i32), ("rows_per_seq", _i32), ("max_seq_len", _i32), ("kv_rank", _i32), ("rope_dim", _i32),
         ("latent_dtype", _i32), ("seq_stride", _i64), ("eps", _f32), ("rope", RopeParams),
+        ("seq_base", _vp),
     ]
 
 

@@ -193,7 +193,7 @@ def _rope(rope) -> _capi.RopeParams:
 
 def mla_absorb(q: torch.Tensor, w_kb: torch.Tensor, w_type=None, *, out: torch.Tensor | None = None,
                out_dtype: torch.dtype = torch.float32, positions: torch.Tensor | None = None,
-               rope=(10000.0, 0.0, 0)) -> torch.Tensor:
+               rope=(10000.0, 0.0, 0), seq_base: torch.Tensor | None = None, rows_per_seq: int = 1) -> torch.Tensor:
     """q_abs = [q_nope . k_b | q_rope] per head (transformer.cpp:2556-2573).
 
     q f16 [..., H, 192]; w_kb = attn_k_b, H*128 rows of 512 in the GGML
@@ -201,7 +201,9 @@ def mla_absorb(q: torch.Tensor, w_kb: torch.Tensor, w_type=None, *, out: torch.T
     bytes).  Returns [..., H, 576] in out_dtype (F32 or BF16).  With
     positions (int32, one per row of q), q_rope is first rotated by the
     reference's q RoPE stage (transformer.cpp:3882-3921) with
-    rope = (theta, yarn factor, original ctx)."""
+    rope = (theta, yarn factor, original ctx).  With seq_base (int32
+    [n_seq]) instead of positions, row r is rotated at
+    seq_base[r // rows_per_seq] + r % rows_per_seq."""
     _need_cuda(q, w_kb)
     if q.dtype != torch.float16 or q.shape[-1] != 192:
         raise ValueError("q must be float16 [..., H, 192]")
@@ -218,6 +220,11 @@ def mla_absorb(q: torch.Tensor, w_kb: torch.Tensor, w_type=None, *, out: torch.T
         if positions.dtype != torch.int32 or positions.numel() != rows:
             raise ValueError("positions must be int32 with one entry per row of q")
         a.positions, a.rope = positions.data_ptr(), _rope(rope)
+    elif seq_base is not None:
+        _need_cuda(seq_base)
+        if seq_base.dtype != torch.int32:
+            raise TypeError("seq_base must be int32")
+        a.seq_base, a.rows_per_seq, a.rope = seq_base.data_ptr(), int(rows_per_seq), _rope(rope)
     _capi.check(_capi.lib().mugen_attn_mla_absorb(ctypes.byref(a), _stream(q.device)))
     return out
 
@@ -256,23 +263,33 @@ def mla_attention_full(q: torch.Tensor, w_kb: torch.Tensor, w_vb: torch.Tensor, 
     return mla_project(o, w_vb, w_type)
 
 
-def mla_latent_write(kv_a: torch.Tensor, norm_w: torch.Tensor, positions: torch.Tensor, latent: torch.Tensor,
+def mla_latent_write(kv_a: torch.Tensor, norm_w: torch.Tensor, positions: torch.Tensor | None, latent: torch.Tensor,
                      *, rows_per_seq: int = 1, eps: float = 1e-6, rope=(10000.0, 0.0, 0),
-                     max_seq_len: int | None = None) -> torch.Tensor:
+                     max_seq_len: int | None = None, seq_base: torch.Tensor | None = None) -> torch.Tensor:
     """Latent-cache writer (transformer.cpp:3930-3987): RMSNorm(c_kv) * norm_w
     and RoPE(k_rope) of each kv_a row [rows, 576] (f16), written to row
     positions[r] of sequence r // rows_per_seq of latent [n_seq, max_T, 576]
-    (f16 or bf16).  rope = (theta, yarn factor, original ctx)."""
-    _need_cuda(kv_a, norm_w, positions, latent)
+    (f16 or bf16).  rope = (theta, yarn factor, original ctx).  With
+    positions None, row r goes to seq_base[r // rows_per_seq] +
+    r % rows_per_seq."""
+    _need_cuda(kv_a, norm_w, latent)
     if kv_a.dtype != torch.float16 or norm_w.dtype != torch.float16 or kv_a.shape[-1] != 576:
         raise ValueError("kv_a must be float16 [rows, 576] and norm_w float16 [512]")
-    if positions.dtype != torch.int32:
-        raise TypeError("positions must be int32")
+    pos = positions if positions is not None else seq_base
+    if pos is None:
+        raise ValueError("positions or seq_base is required")
+    _need_cuda(pos)
+    if pos.dtype != torch.int32:
+        raise TypeError("positions / seq_base must be int32")
     rows = kv_a.numel() // 576
-    if positions.numel() != rows or latent.dim() != 3 or latent.shape[-1] != 576:
+    if (positions is not None and positions.numel() != rows) or latent.dim() != 3 or latent.shape[-1] != 576:
         raise ValueError("positions must hold one entry per kv_a row; latent must be [n_seq, max_T, 576]")
     a = _capi.MlaLatentWriteArgs()
-    a.kv_a, a.norm_w, a.positions, a.latent = kv_a.data_ptr(), norm_w.data_ptr(), positions.data_ptr(), latent.data_ptr()
+    a.kv_a, a.norm_w, a.latent = kv_a.data_ptr(), norm_w.data_ptr(), latent.data_ptr()
+    if positions is not None:
+        a.positions = positions.data_ptr()
+    else:
+        a.seq_base = seq_base.data_ptr()
     a.rows, a.rows_per_seq = rows, int(rows_per_seq)
     a.max_seq_len = int(latent.shape[1] if max_seq_len is None else max_seq_len)
     a.kv_rank, a.rope_dim, a.latent_dtype = 512, 64, _dt(latent.dtype)

@@ -665,9 +665,13 @@ int mugen_attn_mla_absorb(const mugen_attn_mla_absorb_args* a, void* stream) {
         return fail(MUGEN_ATTN_E_INVALID, "mla_absorb: misaligned q/q_abs/w_kb");
     if ((int64_t)a->rows * a->n_heads > (1 << 24))
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_absorb: rows*n_heads too large");
-    if (a->positions && !rope_ok(a->rope)) return fail(MUGEN_ATTN_E_INVALID, "mla_absorb: bad rope parameters");
-    MlaProjParams p{a->q, a->w_kb, a->q_abs, a->rows, a->n_heads, a->positions, {}};
-    if (a->positions) p.freqs = yarn_freqs(a->rope);
+    const bool rope = a->positions || a->seq_base;
+    if (rope && !rope_ok(a->rope)) return fail(MUGEN_ATTN_E_INVALID, "mla_absorb: bad rope parameters");
+    if (!a->positions && a->seq_base && a->rows_per_seq <= 0)
+        return fail(MUGEN_ATTN_E_INVALID, "mla_absorb: rows_per_seq must be > 0 with seq_base");
+    MlaProjParams p{a->q, a->w_kb, a->q_abs, a->rows, a->n_heads, a->positions, {}, a->positions ? nullptr : a->seq_base,
+                    a->rows_per_seq > 0 ? a->rows_per_seq : 1};
+    if (rope) p.freqs = yarn_freqs(a->rope);
     return hip_status(launch_mla_absorb(p, a->w_type, a->out_dtype, static_cast<hipStream_t>(stream), active_timer()),
                       "mla_absorb launch");
 }
@@ -687,7 +691,7 @@ int mugen_attn_mla_project(const mugen_attn_mla_project_args* a, void* stream) {
         return fail(MUGEN_ATTN_E_INVALID, "mla_project: misaligned o/out/w_vb");
     if ((int64_t)a->rows * a->n_heads > (1 << 24))
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_project: rows*n_heads too large");
-    MlaProjParams p{a->o, a->w_vb, a->out, a->rows, a->n_heads, nullptr, {}};
+    MlaProjParams p{a->o, a->w_vb, a->out, a->rows, a->n_heads, nullptr, {}, nullptr, 1};
     return hip_status(launch_mla_project(p, a->w_type, a->out_dtype, static_cast<hipStream_t>(stream), active_timer()),
                       "mla_project launch");
 }
@@ -703,7 +707,7 @@ int mugen_attn_mla_latent_write(const mugen_attn_mla_latent_write_args* a, void*
     if (!(a->eps >= 0.f) || !std::isfinite(a->eps)) return fail(MUGEN_ATTN_E_INVALID, "mla_latent_write: bad eps");
     if (!rope_ok(a->rope)) return fail(MUGEN_ATTN_E_INVALID, "mla_latent_write: bad rope parameters");
     if (a->rows == 0) return MUGEN_ATTN_OK;
-    if (!a->kv_a || !a->norm_w || !a->positions || !a->latent)
+    if (!a->kv_a || !a->norm_w || (!a->positions && !a->seq_base) || !a->latent)
         return fail(MUGEN_ATTN_E_INVALID, "mla_latent_write: null pointer");
     const int n_seq = (a->rows + a->rows_per_seq - 1) / a->rows_per_seq;
     if (n_seq > 1 && a->seq_stride < (int64_t)a->max_seq_len * 576)
@@ -715,6 +719,7 @@ int mugen_attn_mla_latent_write(const mugen_attn_mla_latent_write_args* a, void*
     p.kv_a = static_cast<const uint16_t*>(a->kv_a);
     p.norm_w = static_cast<const uint16_t*>(a->norm_w);
     p.positions = a->positions;
+    p.seq_base = a->positions ? nullptr : a->seq_base;
     p.latent = static_cast<uint16_t*>(a->latent);
     p.rows = a->rows;
     p.rows_per_seq = a->rows_per_seq;

@@ -282,6 +282,13 @@ __device__ __forceinline__ u32x2_t load8(const void* p) {
 
 // ---------------------------------------------------------------- RoPE
 
+// position of row r: positions[r], or (positions null) the r % rows_per_seq
+// -th new token of sequence r / rows_per_seq, appended at seq_base[seq]
+__device__ __forceinline__ int row_position(const int32_t* positions, const int32_t* seq_base, int rows_per_seq,
+                                            int r) {
+    return positions ? positions[r] : seq_base[r / rows_per_seq] + r % rows_per_seq;
+}
+
 // One NeoX pair (x0 = dim i, x1 = dim i + 32) rotated by pos * freq as the
 // reference's float code does (transformer.cpp:3903-3917): angle rounded
 // to float, full-precision cosf / sinf, each output a product difference

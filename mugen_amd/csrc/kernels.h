@@ -140,8 +140,10 @@ struct MlaProjParams {
     void* out;        // absorb: q_abs [rows][H][kv_rank+rope]; project: [rows][H][v_head]
     int rows;
     int H;
-    const int32_t* positions;  // absorb: RoPE position of each row (null: q_rope copied as is)
+    const int32_t* positions;  // absorb: RoPE position of each row (null: see seq_base)
     RopeFreqs freqs;
+    const int32_t* seq_base;   // absorb, positions null: row r at seq_base[r / rows_per_seq] + r % rows_per_seq
+    int rows_per_seq;
 };
 hipError_t launch_mla_absorb(const MlaProjParams& p, int w_type, int out_dt, hipStream_t st, KernelTimer* t);
 hipError_t launch_mla_project(const MlaProjParams& p, int w_type, int out_dt, hipStream_t st, KernelTimer* t);
@@ -150,7 +152,8 @@ hipError_t launch_mla_project(const MlaProjParams& p, int w_type, int out_dt, hi
 struct LatentWriteParams {
     const uint16_t* kv_a;      // [rows][576] f16
     const uint16_t* norm_w;    // [512] f16
-    const int32_t* positions;  // [rows]
+    const int32_t* positions;  // [rows], or null: seq_base[r / rows_per_seq] + r % rows_per_seq
+    const int32_t* seq_base;
     uint16_t* latent;          // [n_seq][max_seq_len][576]
     int rows;
     int rows_per_seq;

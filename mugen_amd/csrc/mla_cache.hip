@@ -22,7 +22,7 @@ __global__ __launch_bounds__(64) void mla_latent_write_kernel(LatentWriteParams 
 #pragma clang fp contract(off)
     constexpr int KR = 512, ROPE = 64, C = KR + ROPE;
     const int r = blockIdx.x, lane = threadIdx.x;
-    const int pos = p.positions[r];
+    const int pos = row_position(p.positions, p.seq_base, p.rows_per_seq, r);
     if (pos < 0 || pos >= p.max_seq_len) return;  // outside the cache: not written
     const uint16_t* src = p.kv_a + (int64_t)r * C;
     uint16_t* dst = p.latent + (int64_t)(r / p.rows_per_seq) * p.seq_stride + (int64_t)pos * C;

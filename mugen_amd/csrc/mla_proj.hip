@@ -136,8 +136,9 @@ __global__ __launch_bounds__(512) void mla_absorb_kernel(MlaProjParams p) {
             if (r < nr) {
                 const uint16_t* qr = q + ((int64_t)(r0 + r) * p.H + h) * (NOPE + ROPE) + NOPE;
                 uint16_t y0 = qr[c], y1 = qr[c + ROPE / 2];
-                if (p.positions)
-                    rope_pair_f16(to_f32<DT_F16>(y0), to_f32<DT_F16>(y1), p.positions[r0 + r], p.freqs.f[c], y0, y1);
+                if (p.positions || p.seq_base)
+                    rope_pair_f16(to_f32<DT_F16>(y0), to_f32<DT_F16>(y1),
+                                  row_position(p.positions, p.seq_base, p.rows_per_seq, r0 + r), p.freqs.f[c], y0, y1);
                 const int64_t o = ((int64_t)(r0 + r) * p.H + h) * (KR + ROPE) + KR + c;
                 store_out<OUT_DT>(p.out, o, to_f32<DT_F16>(y0));
                 store_out<OUT_DT>(p.out, o + ROPE / 2, to_f32<DT_F16>(y1));

@@ -2,13 +2,16 @@
 // (include/mugen_attn_engine.hpp) on the GPU: a multi-layer decode loop run
 // eagerly and the same loop replayed from one captured StepGraph must give
 // bit-identical outputs at every step (same kernels, same inputs), while the
-// device-side lengths advance by one per step inside the graph.
+// device-side lengths advance by one per step inside the graph (q_len per
+// step for an MLA verify step).  A prompt chunk through prefill_layer is
+// checked against a direct causal prefill over the same context.
 //
 // Built by mugen_amd/build.py next to libmugen_attn.so; run by
 // tests/test_engine_gpu.py.  Prints PASS / FAIL lines; exit status 0 only
 // if every check passed.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -174,16 +177,18 @@ void gqa_test(hipStream_t st) {
 
 // ---------------------------------------------------------------- MLA
 
-void mla_test(hipStream_t st) {
+void mla_test(hipStream_t st, int q_len) {
     mugen_attn::MlaShape s;
     s.n_layers = 2;
     s.batch = 2;
     s.n_heads = 16;
     s.max_seq_len = 512;
+    s.q_len = q_len;
     s.rope = mugen_attn_rope_params{10000.f, 40.f, 4096};
     const std::vector<int32_t> lens0 = {300, 5};
     const int steps = 4;
-    std::printf("mla provider: layers %d batch %d H %d steps %d\n", s.n_layers, s.batch, s.n_heads, steps);
+    std::printf("mla provider: layers %d batch %d H %d q_len %d steps %d\n", s.n_layers, s.batch, s.n_heads, q_len,
+                steps);
     std::fflush(stdout);
     std::unique_ptr<mugen_attn::MlaAttention> eager, graphed;
     if (!ok(mugen_attn::MlaAttention::create(s, &eager), "create eager")) return;
@@ -219,8 +224,8 @@ void mla_test(hipStream_t st) {
     ok(eager->set_lengths(lens0, st), "eager lengths");
     ok(graphed->set_lengths(lens0, st), "graphed lengths");
     std::vector<std::unique_ptr<Dev>> q, kva, oe, og;
-    const size_t qb = (size_t)s.batch * s.n_heads * 192 * 2, kb = (size_t)s.batch * 576 * 2,
-                 ob = (size_t)s.batch * s.n_heads * 128 * 2;
+    const size_t rows = (size_t)s.batch * q_len;
+    const size_t qb = rows * s.n_heads * 192 * 2, kb = rows * 576 * 2, ob = rows * s.n_heads * 128 * 2;
     for (int L = 0; L < s.n_layers; L++) {
         q.emplace_back(new Dev(qb));
         kva.emplace_back(new Dev(kb));
@@ -231,7 +236,7 @@ void mla_test(hipStream_t st) {
     auto body = [&](hipStream_t str) -> Status {
         for (int L = 0; L < s.n_layers; L++)
             if (auto rr = graphed->decode_layer(L, w[L], q[L]->p, kva[L]->p, og[L]->p, str); !rr) return rr;
-        return graphed->advance(str);
+        return graphed->advance(str, q_len);
     };
     if (!ok(graph.capture(st, body), "capture")) return;
     for (int step = 0; step < steps; step++) {
@@ -244,7 +249,7 @@ void mla_test(hipStream_t st) {
         }
         for (int L = 0; L < s.n_layers; L++)
             ok(eager->decode_layer(L, w[L], q[L]->p, kva[L]->p, oe[L]->p, st), "eager decode");
-        ok(eager->advance(st), "eager advance");
+        ok(eager->advance(st, q_len), "eager advance");
         hip(hipStreamSynchronize(st), "sync");
         ok(graph.replay(st), "replay");
         hip(hipStreamSynchronize(st), "sync");
@@ -265,11 +270,85 @@ void mla_test(hipStream_t st) {
             }
         }
         std::vector<int32_t> want(lens0);  // the next step's post-append lengths
-        for (auto& x : want) x += step + 2;
+        for (auto& x : want) x += q_len * (step + 2);
         check_lengths(eager->lengths_after(), want, st, "mla eager");
         check_lengths(graphed->lengths_after(), want, st, "mla graphed");
     }
     std::printf("mla provider done\n");
+}
+
+// ---------------------------------------------------------------- GQA prefill
+
+// A prompt chunk appended to a held context through prefill_layer: the cache
+// rows [start, start + N) must hold the chunk's K / V, and the output must be
+// the causal prefill over context + chunk computed directly from a buffer
+// assembled on the host; afterwards a decode step continues from start + N.
+void gqa_prefill_test(hipStream_t st) {
+    mugen_attn::GqaShape s;
+    s.n_layers = 1;
+    s.batch = 1;
+    s.n_heads = 32;
+    s.n_kv_heads = 8;
+    s.head_dim = 128;
+    s.max_seq_len = 1024;
+    const int start = 200, n = 77;
+    std::printf("gqa prefill provider: H %d Hk %d d %d start %d chunk %d\n", s.n_heads, s.n_kv_heads, s.head_dim,
+                start, n);
+    std::fflush(stdout);
+    std::unique_ptr<mugen_attn::GqaAttention> a;
+    if (!ok(mugen_attn::GqaAttention::create(s, &a), "create")) return;
+    const size_t row = (size_t)s.n_kv_heads * s.head_dim, cache = (size_t)s.max_seq_len * row * 2;
+    Rng r(3);
+    auto k = f16_rand(r, cache / 2, 1.0f), v = f16_rand(r, cache / 2, 1.0f);
+    hip(hipMemcpyAsync(a->k_cache(0), k.data(), cache, hipMemcpyHostToDevice, st), "K init");
+    hip(hipMemcpyAsync(a->v_cache(0), v.data(), cache, hipMemcpyHostToDevice, st), "V init");
+    ok(a->set_lengths({start}, st), "lengths");
+    const size_t qb = (size_t)n * s.n_heads * s.head_dim * 2, kb = (size_t)n * row * 2;
+    auto hq = f16_rand(r, qb / 2, 1.0f), hk = f16_rand(r, kb / 2, 1.0f), hv = f16_rand(r, kb / 2, 1.0f);
+    Dev q(qb), kn(kb), vn(kb), out(qb), ref(qb), kc((size_t)(start + n) * row * 2), vc((size_t)(start + n) * row * 2);
+    q.put(hq.data(), st);
+    kn.put(hk.data(), st);
+    vn.put(hv.data(), st);
+    // the context + chunk, assembled on the host
+    std::vector<uint16_t> kall(k.begin(), k.begin() + (size_t)start * row), vall(v.begin(), v.begin() + (size_t)start * row);
+    kall.insert(kall.end(), hk.begin(), hk.end());
+    vall.insert(vall.end(), hv.begin(), hv.end());
+    kc.put(kall.data(), st);
+    vc.put(vall.data(), st);
+    hip(hipStreamSynchronize(st), "sync");
+    ok(a->prefill_layer(0, q.p, kn.p, vn.p, out.p, n, st), "prefill_layer");
+    mugen_attn_gqa_prefill_args pf{};
+    pf.q = q.p;
+    pf.k = kc.p;
+    pf.v = vc.p;
+    pf.out = ref.p;
+    pf.n_tokens = n;
+    pf.n_heads = s.n_heads;
+    pf.n_kv_heads = s.n_kv_heads;
+    pf.head_dim = s.head_dim;
+    pf.kv_len = start + n;
+    pf.start_pos = start;
+    pf.causal = 1;
+    pf.dtype = MUGEN_ATTN_F16;
+    pf.out_dtype = MUGEN_ATTN_F16;
+    ok(mugen_attn::gqa_prefill(pf, st), "direct prefill");
+    const auto o = out.get(st), o_ref = ref.get(st);
+    if (o != o_ref || !finite_f16(o)) {
+        std::printf("FAIL gqa prefill: provider output differs from the direct prefill\n");
+        failures++;
+    }
+    std::vector<uint16_t> kgot(cache / 2), vgot(cache / 2);
+    hip(hipMemcpyAsync(kgot.data(), a->k_cache(0), cache, hipMemcpyDeviceToHost, st), "K read");
+    hip(hipMemcpyAsync(vgot.data(), a->v_cache(0), cache, hipMemcpyDeviceToHost, st), "V read");
+    hip(hipStreamSynchronize(st), "sync");
+    if (!std::equal(kall.begin(), kall.end(), kgot.begin()) || !std::equal(vall.begin(), vall.end(), vgot.begin()) ||
+        !std::equal(k.begin() + kall.size(), k.end(), kgot.begin() + kall.size())) {
+        std::printf("FAIL gqa prefill: cache rows not where the chunk belongs\n");
+        failures++;
+    }
+    ok(a->advance(st, n), "advance");
+    check_lengths(a->lengths_after(), {start + n + 1}, st, "gqa prefill");
+    std::printf("gqa prefill provider done\n");
 }
 
 }  // namespace
@@ -278,7 +357,9 @@ int main() {
     hipStream_t st;
     if (!hip(hipStreamCreate(&st), "hipStreamCreate")) return 1;
     gqa_test(st);
-    mla_test(st);
+    mla_test(st, 1);
+    mla_test(st, 3);
+    gqa_prefill_test(st);
     (void)hipStreamSynchronize(st);
     (void)hipStreamDestroy(st);
     std::printf(failures ? "FAIL (%d)\n" : "PASS\n", failures);

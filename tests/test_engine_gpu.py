@@ -88,10 +88,13 @@ def test_step_graph_replays_match_oracle(device):
             C.assert_close(out[l].cpu().numpy(), ref, f"replay {t} layer {l}")
 
 
-def test_mla_step_graph_replays_match_oracle(device):
-    # a captured MLA decode step (latent write -> absorb with q RoPE ->
-    # fp32-q core -> projection, then the device-side length advance),
-    # replayed with fresh inputs and checked against the oracle's chain
+@pytest.mark.parametrize("q_len", [1, 3])
+def test_mla_step_graph_replays_match_oracle(device, q_len):
+    # a captured MLA step (latent write -> absorb with q RoPE -> fp32-q core
+    # -> projection, then the device-side length advance), replayed with
+    # fresh inputs and checked against the oracle's chain.  q_len 1 is a
+    # decode step; q_len 3 a speculative verify step, whose token j of
+    # sequence b sits at seq_base[b] + j (the before-lengths on the device).
     B, H, max_T, w_type = 2, 16, 256, O.W_Q8_0
     rope = (10000.0, 40.0, 4096)
     freqs = O.yarn_freqs(64, rope[1], rope[2], rope[0])
@@ -103,40 +106,41 @@ def test_mla_step_graph_replays_match_oracle(device):
     lat = C.to_dev(latb, C.F16, device)
     wk, wv = torch.from_numpy(w_kb).to(device), torch.from_numpy(w_vb).to(device)
     nd = C.to_dev(norm, C.F16, device)
-    seq = torch.from_numpy(np.concatenate([lens, lens + 1])).to(device)   # [before | after]
-    q_in = torch.empty((B, 1, H, 192), dtype=torch.float16, device=device)
-    kv_in = torch.empty((B, 576), dtype=torch.float16, device=device)
-    qa = torch.empty((B, 1, H, 576), dtype=torch.float32, device=device)
-    o = torch.empty((B, 1, H, 512), dtype=torch.float32, device=device)
-    out = torch.empty((B, 1, H, 128), dtype=torch.float16, device=device)
+    seq = torch.from_numpy(np.concatenate([lens, lens + q_len])).to(device)   # [before | after]
+    q_in = torch.empty((B, q_len, H, 192), dtype=torch.float16, device=device)
+    kv_in = torch.empty((B * q_len, 576), dtype=torch.float16, device=device)
+    qa = torch.empty((B, q_len, H, 576), dtype=torch.float32, device=device)
+    o = torch.empty((B, q_len, H, 512), dtype=torch.float32, device=device)
+    out = torch.empty((B, q_len, H, 128), dtype=torch.float16, device=device)
     ws = torch.empty(1 << 24, dtype=torch.uint8, device=device)
 
     def step():
-        mugen_amd.mla_latent_write(kv_in, nd, seq[:B], lat, rope=rope)
-        mugen_amd.mla_absorb(q_in, wk, "q8_0", out=qa, positions=seq[:B], rope=rope)
+        mugen_amd.mla_latent_write(kv_in, nd, None, lat, rope=rope, rows_per_seq=q_len, seq_base=seq[:B])
+        mugen_amd.mla_absorb(q_in, wk, "q8_0", out=qa, rope=rope, seq_base=seq[:B], rows_per_seq=q_len)
         mugen_amd.mla_attention(qa, lat, seq[B:], max_T, scale=C.MLA_SCALE, out=o, workspace=ws)
         mugen_amd.mla_project(o, wv, "q8_0", out=out)
-        mugen_amd.seq_advance(seq, 1, max_T)
+        mugen_amd.seq_advance(seq, q_len, max_T)
 
-    C.say(f"captured MLA step: batch {B} H {H} lens {list(lens)}")
+    C.say(f"captured MLA step: batch {B} q_len {q_len} H {H} lens {list(lens)}")
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         step()
     torch.cuda.synchronize()
     cache = latb.copy()
     for t in range(3):
-        qb = O.round_to(O.randn(810 + t, (B, 1, H, 192)), C.F16)[1]
-        kvb = O.round_to(O.randn(820 + t, (B, 576)), C.F16)[1]
+        qb = O.round_to(O.randn(810 + t, (B, q_len, H, 192)), C.F16)[1]
+        kvb = O.round_to(O.randn(820 + t, (B * q_len, 576)), C.F16)[1]
         q_in.copy_(C.to_dev(qb, C.F16, device))
         kv_in.copy_(C.to_dev(kvb, C.F16, device))
         torch.cuda.synchronize()
-        C.say(f"MLA replay {t}: positions {list(lens)}")
+        C.say(f"MLA replay {t}: positions {list(lens)} + [0, {q_len})")
         g.replay()
         torch.cuda.synchronize()
-        cache = O.mla_latent_write(kvb, norm, lens, cache, 1, max_T, freqs, 1e-6)
-        qr = O.rope_q_f16(qb.reshape(B, H, 192), lens, freqs).reshape(B, 1, H, 192)
-        lens = lens + 1
+        pos = (lens[:, None] + np.arange(q_len, dtype=np.int32)[None, :]).reshape(-1).astype(np.int32)
+        cache = O.mla_latent_write(kvb, norm, pos, cache, q_len, max_T, freqs, 1e-6)
+        qr = O.rope_q_f16(qb.reshape(B * q_len, H, 192), pos, freqs).reshape(B, q_len, H, 192)
+        lens = lens + q_len
         f = lambda x: x.view(np.float16).astype(np.float32)
-        ref = O.mla_full(f(qr), w_kb, w_vb, w_type, f(cache), lens, 1, H, C.MLA_SCALE, nthreads=8)
+        ref = O.mla_full(f(qr), w_kb, w_vb, w_type, f(cache), lens, q_len, H, C.MLA_SCALE, nthreads=8)
         C.assert_close(out.float().cpu().numpy(), ref, f"MLA replay {t}")
-        assert seq.cpu().tolist() == list(lens) + list(lens + 1)
+        assert seq.cpu().tolist() == list(lens) + list(lens + q_len)

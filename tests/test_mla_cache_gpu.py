@@ -139,3 +139,29 @@ def test_writer_then_full_operator(device):
     out = mugen_amd.mla_project(o, wv, "q8_0")
     torch.cuda.synchronize()
     C.assert_close(out.float().cpu().numpy(), ref, "writer + full operator")
+
+
+def test_seq_base_positions_match_explicit_positions(device):
+    # rows_per_seq tokens per sequence at seq_base[b] + j: the same bytes as
+    # passing those positions explicitly (writer and absorb's q RoPE)
+    B, q_len, H, T = 3, 4, 16, 128
+    base = np.array([10, 0, 120], np.int32)          # the last sequence runs past the cache
+    pos = (base[:, None] + np.arange(q_len)[None, :]).reshape(-1).astype(np.int32)
+    kv = O.randn(91, (B * q_len, 576))
+    w = O.randn(92, (512,), 1.0, 0.1)
+    _, cache = O.round_to(O.randn(93, (B, T, 576), 0.0, 0.5), C.F16)
+    C.say("seq_base positions")
+    a = C.to_dev(cache, C.F16, device)
+    b = C.to_dev(cache, C.F16, device)
+    kvd, wd = f16_bits_dev(kv, device), f16_bits_dev(w, device)
+    mugen_amd.mla_latent_write(kvd, wd, torch.from_numpy(pos).to(device), a, rows_per_seq=q_len, rope=V3_ROPE)
+    mugen_amd.mla_latent_write(kvd, wd, None, b, rows_per_seq=q_len, rope=V3_ROPE,
+                               seq_base=torch.from_numpy(base).to(device))
+    q = f16_bits_dev(O.randn(94, (B * q_len, H, 192)), device)
+    wk = torch.from_numpy(C.make_weights(95, H * 128, 512, O.W_F16)).to(device).view(torch.float16)
+    qa = mugen_amd.mla_absorb(q, wk, "f16", positions=torch.from_numpy(pos).to(device), rope=V3_ROPE)
+    qb = mugen_amd.mla_absorb(q, wk, "f16", seq_base=torch.from_numpy(base).to(device), rows_per_seq=q_len,
+                              rope=V3_ROPE)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert torch.equal(qa, qb)
