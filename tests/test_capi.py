@@ -176,6 +176,9 @@ def test_mla_absorb_project_validation():
     assert L.mugen_attn_mla_absorb(ctypes.byref(b), None) == _capi.E_INVALID
     b.rows = 0
     assert L.mugen_attn_mla_absorb(ctypes.byref(b), None) == _capi.OK
+    b = _capi.MlaAbsorbArgs.from_buffer_copy(a)      # device seq_base positions need tokens per sequence
+    b.seq_base, b.rows_per_seq = 0x1000, 0
+    assert L.mugen_attn_mla_absorb(ctypes.byref(b), None) == _capi.E_INVALID
     p = _capi.MlaProjectArgs()
     p.o = p.w_vb = p.out = 0x1000
     p.rows, p.n_heads, p.kv_rank, p.v_head_dim, p.w_type, p.out_dtype = 4, 16, 512, 128, _capi.W_Q4_0, _capi.F16
@@ -205,6 +208,12 @@ def test_latent_write_validation():
     assert L.mugen_attn_mla_latent_write(ctypes.byref(b), None) == _capi.E_INVALID
     b.rope, b.rows = _capi.RopeParams(10000.0, 0.0, 0), 0
     assert L.mugen_attn_mla_latent_write(ctypes.byref(b), None) == _capi.OK
+    b = _capi.MlaLatentWriteArgs.from_buffer_copy(a)  # seq_base replaces positions; one of them is needed
+    b.positions, b.seq_base = 0, 0x1000
+    b.rows = 0
+    assert L.mugen_attn_mla_latent_write(ctypes.byref(b), None) == _capi.OK
+    b.seq_base, b.rows = 0, 4
+    assert L.mugen_attn_mla_latent_write(ctypes.byref(b), None) == _capi.E_INVALID
 
 
 def test_kv_q4_validation():
