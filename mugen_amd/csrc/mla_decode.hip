@@ -987,23 +987,39 @@ __global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
     // weights are known, so their latency overlaps the (m, l) reads
     constexpr int PF = 16;
     u32x4_t fa[PF];
-    auto prefetch = [&]() {
+    auto prefetch = [&]() {  // unconditional (clamped) loads keep the wait counts exact
 #pragma unroll
-        for (int j = 0; j < PF; j++)
-            if (j < nact) fa[j] = src[j * frag_st];
+        for (int j = 0; j < PF; j++) fa[j] = src[max(0, min(j, nact - 1)) * frag_st];
     };
-    prefetch();
-
-    // split weights: thread (row r = tid%16, split phase sl = tid/16).  A
+    // split weights: thread (row r = tid%16, split phase sl = tid/16).  The
+    // (m, l) of splits sl and sl + 16 are loaded once, ahead of the
+    // fragments; further splits are read from the workspace in the loops.  A
     // NaN max marks a (row, split) the main kernel could not finish in 16
     // bits; it is recomputed exactly (rare path), then the weights are redone.
     const int r = tid & 15, sl = tid >> 4, row = qb * 16 + r;
     const bool rok = row < p.R;
+    constexpr int MLC = 2;
+    f32x2v_t mlc[MLC];
+    auto load_ml = [&]() {
+#pragma unroll
+        for (int k = 0; k < MLC; k++) {
+            const int s = sl + 16 * k;
+            mlc[k] = (rok && s < nact) ? *reinterpret_cast<const f32x2v_t*>(ml0 + s * ml_st + row * 2)
+                                       : f32x2v_t{kNegInf, 0.f};
+        }
+    };
+    load_ml();
+    prefetch();
     for (int pass = 0; pass < 2; pass++) {
         if (tid == 0) nflag = 0;
         float mx = kNegInf;
         bool bad = false;
-        for (int s = sl; s < nact; s += 16) {
+#pragma unroll
+        for (int k = 0; k < MLC; k++) {
+            bad |= __builtin_isnan(mlc[k][0]);
+            mx = fmaxf(mx, mlc[k][0]);
+        }
+        for (int s = sl + 16 * MLC; s < nact; s += 16) {
             const float m = rok ? ml0[s * ml_st + row * 2] : kNegInf;
             bad |= __builtin_isnan(m);
             mx = fmaxf(mx, m);
@@ -1026,11 +1042,21 @@ __global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
             }
             __threadfence();
             __syncthreads();
-            prefetch();  // the recompute rewrote fragments
+            load_ml();  // the recompute rewrote (m, l) and fragments
+            prefetch();
             continue;
         }
         float sum = 0.f;
-        for (int s = sl; s < nact; s += 16) {
+#pragma unroll
+        for (int k = 0; k < MLC; k++) {
+            const int s = sl + 16 * k;
+            if (s < nact) {
+                const float wgt = (mlc[k][0] == kNegInf) ? 0.f : fast_exp2(mlc[k][0] - M) * mlc[k][1];
+                wts[s][r] = wgt;
+                sum += wgt;
+            }
+        }
+        for (int s = sl + 16 * MLC; s < nact; s += 16) {
             const float m = rok ? ml0[s * ml_st + row * 2] : kNegInf;
             const float wgt = (m == kNegInf) ? 0.f : fast_exp2(m - M) * ml0[s * ml_st + row * 2 + 1];
             wts[s][r] = wgt;
