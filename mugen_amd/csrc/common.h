@@ -211,11 +211,15 @@ __device__ __forceinline__ float wave_sum(float v) {
 // no split saw a token).  All threads of the block must call it.
 constexpr int kMaxSplits = 4096;
 constexpr int kMaxMlaSplits = 512;  // MLA combine keeps per-row split weights in LDS
-__device__ __forceinline__ float lse_weights(const float* ml, int64_t ml_stride, int nact, float* f_lds,
-                                             float* red_lds) {
+// Split weights of a log-sum-exp merge: f_lds[s] = 2^(m_s - M), returns
+// 1 / sum_s f_s * l_s.  (m0, l0) is the (m, l) pair of split threadIdx.x,
+// loaded by the caller (so that its latency can overlap other loads); the
+// splits beyond blockDim.x are read here.
+__device__ __forceinline__ float lse_weights(const float* ml, int64_t ml_stride, int nact, float m0, float l0,
+                                             float* f_lds, float* red_lds) {
     const int tid = threadIdx.x, nw = blockDim.x >> 6, w = tid >> 6;
-    float mloc = kNegInf;
-    for (int s = tid; s < nact; s += blockDim.x) mloc = fmaxf(mloc, ml[s * ml_stride]);
+    float mloc = m0;
+    for (int s = tid + blockDim.x; s < nact; s += blockDim.x) mloc = fmaxf(mloc, ml[s * ml_stride]);
     mloc = wave_max(mloc);
     if ((tid & 63) == 0) red_lds[w] = mloc;
     __syncthreads();
@@ -223,7 +227,12 @@ __device__ __forceinline__ float lse_weights(const float* ml, int64_t ml_stride,
     for (int i = 1; i < nw; i++) M = fmaxf(M, red_lds[i]);
     __syncthreads();
     float lloc = 0.f;
-    for (int s = tid; s < nact; s += blockDim.x) {
+    if (tid < nact) {
+        const float f = (m0 == kNegInf) ? 0.f : fast_exp2(m0 - M);
+        f_lds[tid] = f;
+        lloc = f * l0;
+    }
+    for (int s = tid + blockDim.x; s < nact; s += blockDim.x) {
         const float m = ml[s * ml_stride];
         const float f = (m == kNegInf) ? 0.f : fast_exp2(m - M);
         f_lds[s] = f;

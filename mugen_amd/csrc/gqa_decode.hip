@@ -397,8 +397,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 }
 
 // Log-sum-exp merge of the split partials of one (sequence, head): the
-// split weights are computed in parallel, then each thread sums its dim
-// over the splits with independent (unrolled) loads.
+// split weights are computed in parallel while the first splits' partials
+// are already in flight, then each thread sums its dim over the splits with
+// independent (unrolled) loads.
 template <int D, int OUT_DT>
 __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p) {
     __shared__ float f_lds[kMaxSplits];
@@ -409,11 +410,20 @@ __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p
     const int nact = p.n_q4 ? min(p.num_splits, T > 0 ? splits_of<true>(p, b) : 0)
                             : min(p.num_splits, (T + p.chunk - 1) / p.chunk);
     const int64_t bh = (int64_t)b * p.H + h;
-    const float inv = lse_weights(p.ws_ml + bh * p.num_splits * 2, 2, nact, f_lds, red_lds);
+    const float* ml = p.ws_ml + bh * p.num_splits * 2;
     const float* os = p.ws_o + bh * p.num_splits * D + d;
-    // 8 independent loads in flight per step
+    // this thread's split (m, l), then the first 8 splits' partials (clamped,
+    // unconditional loads), all in flight before the weights are formed
+    const float m0 = d < nact ? ml[2 * d] : kNegInf, l0 = d < nact ? ml[2 * d + 1] : 0.f;
+    float v0[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) v0[j] = os[(int64_t)max(0, min(j, nact - 1)) * D];
+    const float inv = lse_weights(ml, 2, nact, m0, l0, f_lds, red_lds);
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    int s = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+        if (j < nact) acc[j] = f_lds[j] * v0[j];
+    int s = 8;
     for (; s + 8 <= nact; s += 8) {
         float v[8];
 #pragma unroll
