@@ -283,6 +283,17 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
 }
 
+// Write-through vector stores (sc0 sc1) for large split partials: each line goes
+// through L2 to the memory-side cache when it is written, instead of staying
+// dirty until the end-of-kernel L2 writeback, which otherwise sits between
+// the split kernel and the merge kernel that reads the partials.
+__device__ __forceinline__ void store_wt(u32x4_t* p, u32x4_t v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_wt(float* p, float v) {
+    asm volatile("global_store_dword %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
+}
+
 __device__ __forceinline__ u32x4_t load16(const void* p) {
     return *reinterpret_cast<const u32x4_t*>(p);
 }

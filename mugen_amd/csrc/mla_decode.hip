@@ -791,8 +791,8 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
         const bool row_big = (big >> ((n >> 2) * 16)) & 0xffffull;
         if (g == 0 && ok) {
             const int64_t slot_ml = ((int64_t)b * p.num_splits + s) * p.R + rowq;
-            p.ws_ml[slot_ml * 2 + 0] = (ovf_x[16 * wr + n] || row_big) ? __builtin_nanf("") : m_ref;
-            p.ws_ml[slot_ml * 2 + 1] = lrow;
+            store_wt(&p.ws_ml[slot_ml * 2 + 0], (ovf_x[16 * wr + n] || row_big) ? __builtin_nanf("") : m_ref);
+            store_wt(&p.ws_ml[slot_ml * 2 + 1], lrow);
         }
         MUGEN_TRACE(5);
     } else {
@@ -880,7 +880,7 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
                         h[2 * e] = pack2<DT_F16>(v[0], v[1]);
                         h[2 * e + 1] = pack2<DT_F16>(v[2], v[3]);
                     }
-                    dst[(d >> 1) * 64] = u32x4_t{h[0], h[1], h[2], h[3]};
+                    store_wt(&dst[(d >> 1) * 64], u32x4_t{h[0], h[1], h[2], h[3]});
                 }
             }
             const uint64_t bm = __ballot(!(vmax <= 65000.f));
