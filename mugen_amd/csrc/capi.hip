@@ -244,10 +244,10 @@ static size_t gqa_ws(const mugen_attn_gqa_decode_args* a, int chunk, int* splits
 // overrides the choice (kernel comparisons); variants 2-5 need 16-bit q.
 static int mla_variant(const mugen_attn_mla_decode_args* a) {
     const int R = a->q_len * a->n_heads;
-    const int dflt = (R <= 64 || a->q_dtype == DT_F32) ? 1 : 5;
+    const int dflt = (R <= 64 && a->q_dtype != DT_F32) ? 1 : 5;
     if (const char* e = getenv("MUGEN_ATTN_MLA_VARIANT")) {
         const int v = atoi(e);
-        if (v == 1 || (v >= 2 && v <= 5 && a->q_dtype != DT_F32)) return v;
+        if (v == 1 || v == 5 || (v >= 2 && v <= 4 && a->q_dtype != DT_F32)) return v;
     }
     return dflt;
 }

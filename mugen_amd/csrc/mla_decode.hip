@@ -610,9 +610,13 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
 // S waves, one by the PV waves) and a double-buffered P.  One barrier per
 // tile: at barrier j the S waves have written P(j-1) and the PV waves have
 // finished tile j-2, whose slot then receives tile j+2.
-template <int DT>
+template <int QDT, int DT>
 __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
     constexpr int KS = kCD / 32;          // 18 k-steps over the 576 dims
+    // fp32 q: each S wave holds q as hi + lo 16-bit parts (RNE split) and
+    // issues two MFMAs per k-step, so S carries ~2^-16 relative q error
+    // instead of 2^-8 / 2^-11
+    constexpr int NQ = (QDT == DT_F32) ? 2 : 1;
     constexpr float TH = headroom_log2<DT>();
     constexpr int NSLOT = 4;
     constexpr int DPW = kDmaPerTile / 4;  // 9 one-KiB DMA ops per PV wave per tile
@@ -682,11 +686,28 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
         const int rowq = row0 + 16 * wr + n;  // S-layout row of this lane
         const bool ok = rowq < p.R;
         const int teff = ok ? (T - p.q_len + rowq / p.H + 1) : T;  // visible tokens of the row
-        u32x4_t qf[KS];
-        {
+        u32x4_t qf[NQ][KS];
+        if constexpr (QDT == DT_F32) {
+            const float* qp = static_cast<const float*>(p.q) + ((int64_t)b * p.R + (ok ? rowq : 0)) * kCD + 8 * g;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                const f32x4_t q0 = *reinterpret_cast<const f32x4_t*>(qp + 32 * ks);
+                const f32x4_t q1 = *reinterpret_cast<const f32x4_t*>(qp + 32 * ks + 4);
+                float x[8];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    x[e] = ok ? q0[e] : 0.f;
+                    x[4 + e] = ok ? q1[e] : 0.f;
+                }
+                u32x4_t fr[2];
+                split_p<DT, 2>(x, fr);
+                qf[0][ks] = fr[0];
+                qf[1][ks] = fr[1];
+            }
+        } else {
             const uint16_t* qp = static_cast<const uint16_t*>(p.q) + ((int64_t)b * p.R + (ok ? rowq : 0)) * kCD + 8 * g;
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) qf[ks] = ok ? load16(qp + 32 * ks) : u32x4_t{0, 0, 0, 0};
+            for (int ks = 0; ks < KS; ks++) qf[0][ks] = ok ? load16(qp + 32 * ks) : u32x4_t{0, 0, 0, 0};
         }
         int teff_min = teff;
 #pragma unroll
@@ -722,7 +743,7 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
             for (int ks = 0; ks < KS; ks++) {
                 // first tile: wait for q chunk ks only (the 18 q loads are the
                 // S wave's only vector-memory operations before this loop)
-                if (j == 0) {
+                if (QDT != DT_F32 && j == 0) {  // (fp32 q was waited for by its split)
                     switch (KS - 1 - ks) {  // ks is a constant after unrolling: one s_waitcnt
 #define MLA_VMW(N) case N: vm_wait<N>(); break;
                         MLA_VMW(0) MLA_VMW(1) MLA_VMW(2) MLA_VMW(3) MLA_VMW(4) MLA_VMW(5) MLA_VMW(6) MLA_VMW(7)
@@ -732,10 +753,12 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
                     }
                 }
 #pragma unroll
-                for (int nb = 0; nb < 2; nb++) {
-                    if (ks == 0) mfma_s<DT, true>(sacc[nb], abuf[ks % SPD][nb], qf[ks]);
-                    else mfma_s<DT, false>(sacc[nb], abuf[ks % SPD][nb], qf[ks]);
-                }
+                for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+                    for (int qq = 0; qq < NQ; qq++) {
+                        if (ks == 0 && qq == 0) mfma_s<DT, true>(sacc[nb], abuf[ks % SPD][nb], qf[qq][ks]);
+                        else mfma_s<DT, false>(sacc[nb], abuf[ks % SPD][nb], qf[qq][ks]);
+                    }
                 if (ks + SPD < KS) {
                     abuf[ks % SPD][0] = *a_ptr(ks + SPD, 0);
                     abuf[ks % SPD][1] = *a_ptr(ks + SPD, 1);
@@ -1138,20 +1161,20 @@ static hipError_t launch_mla_t(const MlaParams& p, hipStream_t st, KernelTimer* 
                     dim3(256), st, p);
 }
 
-template <int DT, int OUT_DT>
+template <int QDT, int DT, int OUT_DT>
 static hipError_t launch_mla_ws_t(const MlaParams& p, hipStream_t st, KernelTimer* t) {
     const int grid = 8 * p.nrb * ((p.groups + 7) / 8);
-    hipError_t e = launch_k(t, "mla_decode", mla_decode_ws_kernel<DT>, dim3(grid), dim3(512), st, p);
+    hipError_t e = launch_k(t, "mla_decode", mla_decode_ws_kernel<QDT, DT>, dim3(grid), dim3(512), st, p);
     if (e != hipSuccess) return e;
-    return launch_k(t, "mla_decode_combine", mla_decode_combine_kernel<DT, DT, OUT_DT>, dim3(p.nq, 4, p.B),
+    return launch_k(t, "mla_decode_combine", mla_decode_combine_kernel<QDT, DT, OUT_DT>, dim3(p.nq, 4, p.B),
                     dim3(256), st, p);
 }
 
-template <int DT>
+template <int QDT, int DT>
 static hipError_t launch_mla_ws(const MlaParams& p, int out_dt, hipStream_t st, KernelTimer* t) {
-    if (out_dt == DT_F32) return launch_mla_ws_t<DT, DT_F32>(p, st, t);
-    if (out_dt == DT_F16) return launch_mla_ws_t<DT, DT_F16>(p, st, t);
-    return launch_mla_ws_t<DT, DT_BF16>(p, st, t);
+    if (out_dt == DT_F32) return launch_mla_ws_t<QDT, DT, DT_F32>(p, st, t);
+    if (out_dt == DT_F16) return launch_mla_ws_t<QDT, DT, DT_F16>(p, st, t);
+    return launch_mla_ws_t<QDT, DT, DT_BF16>(p, st, t);
 }
 
 template <int MB, int TS, int NW, int QDT, int DT>
@@ -1164,12 +1187,14 @@ static hipError_t launch_mla_o(const MlaParams& p, int out_dt, hipStream_t st, K
 template <int DT>
 static hipError_t launch_mla_v(const MlaParams& p, int variant, int q_dt, int out_dt, hipStream_t st,
                                KernelTimer* t) {
-    // variants 2 and 3 (32 rows per wave) need 16-bit q (register budget)
-    if (q_dt == DT_F32) return launch_mla_o<1, 1, 4, DT_F32, DT>(p, out_dt, st, t);
+    // variants 2-4 need 16-bit q (register budget); fp32 q runs variant 1 or 5
+    if (q_dt == DT_F32)
+        return variant == 5 ? launch_mla_ws<DT_F32, DT>(p, out_dt, st, t)
+                            : launch_mla_o<1, 1, 4, DT_F32, DT>(p, out_dt, st, t);
     if (variant == 2) return launch_mla_o<2, 1, 4, DT, DT>(p, out_dt, st, t);
     if (variant == 3) return launch_mla_o<2, 2, 4, DT, DT>(p, out_dt, st, t);
     if (variant == 4) return launch_mla_o<1, 2, 8, DT, DT>(p, out_dt, st, t);
-    if (variant == 5) return launch_mla_ws<DT>(p, out_dt, st, t);
+    if (variant == 5) return launch_mla_ws<DT, DT>(p, out_dt, st, t);
     return launch_mla_o<1, 1, 4, DT, DT>(p, out_dt, st, t);
 }
 

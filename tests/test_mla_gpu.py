@@ -143,6 +143,37 @@ def test_kernel_variants(device, monkeypatch, variant, B, q_len, H, lens):
         C.assert_close(run_gpu(c, device, C.F32, splits), ref, f"variant {variant} splits={splits}")
 
 
+@pytest.mark.parametrize("variant", [1, 5])
+@pytest.mark.parametrize("B,q_len,H,lens,ldt", [
+    (2, 1, 128, [700, 33], C.BF16),
+    (2, 3, 128, [3, 100], C.F16),
+    (3, 1, 96, [1, 300, 2050], C.F16),
+    (1, 1, 16, [1024], C.F16),
+])
+def test_fp32_q_variants(device, monkeypatch, variant, B, q_len, H, lens, ldt):
+    # fp32 q (the absorbed q of the full operator): the hi + lo split in the
+    # 4-wave and the warp-specialised kernels
+    monkeypatch.setenv("MUGEN_ATTN_MLA_VARIANT", str(variant))
+    c = C.mla_case(90 + H, B, q_len, H, lens, q_dtype=C.F32, lat_dtype=ldt)
+    ref = C.mla_ref(c)
+    for splits in (0, 1, 4):
+        C.assert_close(run_gpu(c, device, C.F32, splits), ref, f"fp32 q variant {variant} splits={splits}")
+
+
+def test_fp32_q_overshoot_fallback(device, monkeypatch):
+    # the exact-recompute path with fp32 q in the warp-specialised kernel
+    monkeypatch.setenv("MUGEN_ATTN_MLA_VARIANT", "5")
+    c = C.mla_case(62, 2, 1, 128, [900, 300], q_dtype=C.F32, lat_dtype=C.F16)
+    lat = c["lat"].copy()
+    lat[0, 700, :] = 0.0
+    lat[0, 700, 0] = 300.0
+    lat, latb = O.round_to(lat, C.F16)
+    q = c["q"].copy()
+    q[:, :, :, 0] = np.abs(q[:, :, :, 0]) + 1.0
+    c2 = dict(c, lat=lat, latb=latb, q=q)
+    C.assert_close(run_gpu(c2, device, C.F32, 0), C.mla_ref(c2), "fp32 q overshoot")
+
+
 @pytest.mark.parametrize("variant", [3, 5])
 def test_variant_overshoot_fallback(device, monkeypatch, variant):
     # the exact-recompute flag path of the 16-bit variants (R = 128 rows)
