@@ -110,6 +110,32 @@ class MlaDecode(Case):
         full_s = elapsed * total_rows_tok / done_rows_tok
         return full_s, f"{nseq} of {self.B} sequences (all {self.H} heads), scaled by row-tokens"
 
+    def cpu_extras(self, threads):
+        """Context for the single-thread baseline: (i) the same core with
+        `threads` workers over (sequence, head), timed on the first two
+        sequences and scaled by row-tokens; (ii) the per-head q_nope
+        absorption of cpu_mla_attention (transformer.cpp:2563-2573) for all
+        B*H rows against f16 W_UK, single thread."""
+        from oracle import oracle as O
+        elapsed, done = 0.0, 0.0
+        for b in range(min(2, self.B)):
+            q = self.q[b:b + 1].float().cpu().numpy()
+            T = int(self.lens[b])
+            lat = self.lat[b:b + 1, :T].float().cpu().numpy()
+            t0 = time.perf_counter()
+            O.mla_attention(q, lat, [T], self.q_len, self.H, MLA_SCALE, seq_stride=T * 576, nthreads=threads)
+            elapsed += time.perf_counter() - t0
+            done += self.H * sum(T - self.q_len + i + 1 for i in range(self.q_len))
+        total = self.H * sum(int(T) - self.q_len + i + 1 for T in self.lens for i in range(self.q_len))
+        mt_s = elapsed * total / done
+        rng = np.random.default_rng(7)
+        w = (rng.standard_normal((self.H * 128, 512)) * 0.05).astype(np.float16).view(np.uint8)
+        qn = rng.standard_normal((self.B, self.q_len, self.H, 192)).astype(np.float16).astype(np.float32)
+        t0 = time.perf_counter()
+        O.mla_absorb(qn, w, O.W_F16, self.H)
+        absorb_s = time.perf_counter() - t0
+        return mt_s, absorb_s
+
 
 class GqaDecode(Case):
     bound = "hbm"
@@ -188,7 +214,7 @@ class Prefill(Case):
         self.k = randn((N, Hk, D), 1.0, torch.bfloat16, g, dev)
         self.v = randn((N, Hk, D), 1.0, torch.bfloat16, g, dev)
         self.out = torch.empty((N, H, D), dtype=torch.bfloat16, device=dev)
-        self.profile = ("gqa_prefill", "llama1b_n512")
+        self.profile = ("gqa_prefill", "llama1b_n512" if N == 512 else f"qwen7b_n{N}")
         self.flops = 4.0 * H * D * N * (N + 1) / 2
         self.bytes = (N * H * D * 2) * 2 + N * Hk * D * 2 * 2
 
@@ -334,6 +360,35 @@ def load_traffic(kernel, workload):
     return None
 
 
+def measured_peaks(dev):
+    """Practical ceilings next to the datasheet peaks, measured in this run:
+    a library bf16 GEMM (8192^3, hipBLASLt through torch.matmul) and a 1 GiB
+    device-to-device copy (read + write bytes), event-timed after warm-up."""
+    def timed(fn, reps):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / reps
+    n = 8192
+    a = torch.randn((n, n), dtype=torch.bfloat16, device=dev)
+    b = torch.randn((n, n), dtype=torch.bfloat16, device=dev)
+    c = torch.empty((n, n), dtype=torch.bfloat16, device=dev)
+    gemm_s = timed(lambda: torch.matmul(a, b, out=c), 20)
+    del a, b, c
+    x = torch.empty(1 << 29, dtype=torch.float16, device=dev)
+    y = torch.empty_like(x)
+    copy_s = timed(lambda: y.copy_(x), 20)
+    del x, y
+    return {"gemm_bf16_tflops": round(2.0 * n ** 3 / gemm_s / 1e12, 1), "gemm_shape": [n, n, n],
+            "copy_gbs": round(2.0 * (1 << 30) / copy_s / 1e9, 1), "copy_bytes": 1 << 30}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -374,6 +429,7 @@ def main():
             GqaDecode(dev, 16, 28, 4, 128, seeded_lens(44, 16, 256, 4096), 4096, 44, "gqa_decode_qwen7b_b16"),
             GqaDecodeQ4(dev, 16, 28, 4, 128, seeded_lens(44, 16, 256, 4096), 4096, 44, "gqa_decode_q4_qwen7b_b16"),
             Prefill(dev, 512, 32, 8, 64, 46, "gqa_prefill_llama1b"),
+            Prefill(dev, 8192, 28, 4, 128, 49, "gqa_prefill_qwen7b_n8192"),
             MlaDecode(dev, 4, 128, 5, [32768] * 4, 32768, torch.bfloat16, torch.bfloat16, 47, "mla_verify_v3"),
             MlaFull(dev, 8, 128, seeded_lens(45, 8, 1024, 8192), 8192, "q8_0", 48, "mla_layer_v3_q8_0"),
         ]
@@ -416,6 +472,13 @@ def main():
             line["cpu_baseline"] = {"value": round(head.bytes / full_s / 1e9, 4), "unit": "GB/s", "cores": 1,
                                     "kind": "port", "us_per_layer_step": round(full_s * 1e6, 1),
                                     "sample": sample, "host_cores_available": os.cpu_count()}
+            threads = min(16, os.cpu_count() or 1)  # the GPU box's CPU share
+            mt_s, absorb_s = head.cpu_extras(threads)
+            line["cpu_baseline"]["threaded"] = {"value": round(head.bytes / mt_s / 1e9, 4), "unit": "GB/s",
+                                                "cores": threads, "us_per_layer_step": round(mt_s * 1e6, 1),
+                                                "sample": "sequences 0-1, scaled by row-tokens"}
+            line["cpu_baseline"]["absorb_us_per_layer_step"] = round(absorb_s * 1e6, 1)
+    line["measured_peaks"] = measured_peaks(dev)
     line["configs"] = results
     print(json.dumps(line))
 
