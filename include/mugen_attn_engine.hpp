@@ -286,6 +286,165 @@ private:
     std::vector<int32_t> host_lens_;
 };
 
+// ---------------------------------------------------------------- GQA, 4-bit store
+
+struct GqaQ4Shape {
+    int n_layers = 0;
+    int batch = 1;
+    int n_heads = 0;
+    int n_kv_heads = 0;
+    int head_dim = 0;
+    int max_seq_len = 0;
+    int fp16_preserve_last = 256;  // KVCacheConfig (the engine's value)
+    int max_new = 64;              // most tokens one append_layer call adds per sequence
+    int out_dtype = MUGEN_ATTN_F16;
+    float scale = 0.f;             // 0: 1/sqrt(head_dim)
+};
+
+// The same step interface over the reference's 4-bit group KV store
+// (KVCache with quantize_4bit, transformer.cpp:3374-3377; kv_cache.cpp:
+// 163-278): per layer and sequence, tokens older than the newest
+// fp16_preserve_last as 20-byte groups of 32 values, the newest in an f16
+// ring.  decode_layer appends the step's rows (quantising the tokens that
+// leave the ring) and attends straight from the store; the lengths and the
+// quantised counts live on the device, so a captured step replays as is.
+class GqaAttentionQ4 {
+public:
+    static Status create(const GqaQ4Shape& s, std::unique_ptr<GqaAttentionQ4>* out) {
+        if (s.n_layers <= 0 || s.batch <= 0 || s.max_seq_len <= 0 || s.fp16_preserve_last < 0 || s.max_new <= 0)
+            return fail("GqaAttentionQ4: n_layers, batch, max_seq_len, max_new must be > 0");
+        const int vpt = s.n_kv_heads * s.head_dim;
+        if (vpt <= 0 || vpt % 32) return fail("GqaAttentionQ4: n_kv_heads * head_dim must be a multiple of 32");
+        std::unique_ptr<GqaAttentionQ4> a(new GqaAttentionQ4(s));
+        a->ring_ = 1;
+        while (a->ring_ < s.fp16_preserve_last + s.max_new) a->ring_ <<= 1;  // a power of two
+        a->row_bytes_ = vpt / 32 * 20;
+        const size_t q4 = (size_t)s.batch * s.max_seq_len * a->row_bytes_;
+        const size_t ring = (size_t)s.batch * a->ring_ * vpt * 2;
+        a->q4k_.resize(s.n_layers);
+        a->q4v_.resize(s.n_layers);
+        a->rk_.resize(s.n_layers);
+        a->rv_.resize(s.n_layers);
+        for (int L = 0; L < s.n_layers; L++) {
+            if (auto r = a->q4k_[L].alloc(q4, "GqaAttentionQ4 K groups"); !r) return r;
+            if (auto r = a->q4v_[L].alloc(q4, "GqaAttentionQ4 V groups"); !r) return r;
+            if (auto r = a->rk_[L].alloc(ring, "GqaAttentionQ4 K ring"); !r) return r;
+            if (auto r = a->rv_[L].alloc(ring, "GqaAttentionQ4 V ring"); !r) return r;
+        }
+        // lens_: [before | after] as GqaAttention; q4_: [n_q4 | n_q4 after the step's append]
+        if (auto r = a->lens_.alloc(sizeof(int32_t) * 2 * s.batch, "GqaAttentionQ4 lengths"); !r) return r;
+        if (auto r = a->q4n_.alloc(sizeof(int32_t) * 2 * s.batch, "GqaAttentionQ4 quantised counts"); !r) return r;
+        mugen_attn_gqa_decode_q4_args d = a->decode_args(0, nullptr, nullptr);
+        d.q = d.out = a->rk_[0].ptr;  // placeholders: only the shape matters for the size
+        if (auto r = a->ws_.alloc(gqa_decode_q4_workspace_size(d), "GqaAttentionQ4 workspace"); !r) return r;
+        *out = std::move(a);
+        return Status{};
+    }
+
+    // Set every sequence's length for an EMPTY store (a new conversation:
+    // 0), or for one whose rows the caller filled to that length through
+    // append_layer.  Outside any captured step; waits for the copy.
+    Status set_lengths(const std::vector<int32_t>& lens, hipStream_t st) {
+        if ((int)lens.size() != s_.batch) return fail("GqaAttentionQ4::set_lengths: one length per sequence");
+        std::vector<int32_t> both(lens), q4(lens.size());
+        for (int32_t x : lens) both.push_back(x + 1);
+        for (size_t i = 0; i < lens.size(); i++) q4[i] = std::max(0, lens[i] - s_.fp16_preserve_last);
+        q4.insert(q4.end(), q4.begin(), q4.end());
+        if (auto r = detail::hip_ok(hipMemcpyAsync(lens_.ptr, both.data(), sizeof(int32_t) * both.size(),
+                                                   hipMemcpyHostToDevice, st),
+                                    "GqaAttentionQ4::set_lengths");
+            !r)
+            return r;
+        if (auto r = detail::hip_ok(hipMemcpyAsync(q4n_.ptr, q4.data(), sizeof(int32_t) * q4.size(),
+                                                   hipMemcpyHostToDevice, st),
+                                    "GqaAttentionQ4::set_lengths");
+            !r)
+            return r;
+        return detail::hip_ok(hipStreamSynchronize(st), "GqaAttentionQ4::set_lengths");
+    }
+
+    // KVCache::append of n_new (<= max_new) tokens per sequence to one layer,
+    // without attention (a prompt's rows, fed in chunks); after every layer
+    // of the chunk: advance(st, n_new).  k_new / v_new [batch][n_new][Hk*d].
+    Status append_layer(int L, const void* k_new, const void* v_new, int n_new, hipStream_t st) {
+        if (L < 0 || L >= s_.n_layers) return fail("GqaAttentionQ4::append_layer: bad layer");
+        if (n_new <= 0 || n_new > s_.max_new) return fail("GqaAttentionQ4::append_layer: 0 < n_new <= max_new");
+        mugen_attn_kv_q4_append_args ap{};
+        ap.store = store(L);
+        ap.k_new = k_new;
+        ap.v_new = v_new;
+        ap.seq_lens = before();
+        ap.n_q4 = static_cast<const int32_t*>(q4n_.ptr);
+        ap.n_q4_out = static_cast<int32_t*>(q4n_.ptr) + s_.batch;
+        ap.n_seq = s_.batch;
+        ap.n_new = n_new;
+        ap.n_kv_heads = s_.n_kv_heads;
+        ap.head_dim = s_.head_dim;
+        ap.max_seq_len = s_.max_seq_len;
+        return kv_q4_append(ap, st);
+    }
+
+    // One layer of a decode step: append the token's K / V, then cpu_attention
+    // over the store including it.  q [batch][H][d], k_new / v_new
+    // [batch][Hk*d], out [batch][H][d].
+    Status decode_layer(int L, const void* q, const void* k_new, const void* v_new, void* out, hipStream_t st) {
+        if (auto r = append_layer(L, k_new, v_new, 1, st); !r) return r;
+        const mugen_attn_gqa_decode_q4_args d = decode_args(L, q, out);
+        return gqa_decode_q4(d, ws_.ptr, ws_.bytes, st);
+    }
+
+    // End of a step (or of an appended chunk): lengths += n and the
+    // quantised counts take the appends' result (device side, capturable).
+    Status advance(hipStream_t st, int n = 1) {
+        int32_t* lens = static_cast<int32_t*>(lens_.ptr);
+        int32_t* q4 = static_cast<int32_t*>(q4n_.ptr);
+        if (auto r = seq_advance(lens, n, s_.batch, s_.max_seq_len, st, q4, q4 + s_.batch); !r) return r;
+        return seq_advance(lens + s_.batch, n, s_.batch, s_.max_seq_len, st);
+    }
+
+    mugen_attn_kv_q4_store store(int L) const {
+        mugen_attn_kv_q4_store k{};
+        k.q4_k = q4k_[L].ptr;
+        k.q4_v = q4v_[L].ptr;
+        k.ring_k = rk_[L].ptr;
+        k.ring_v = rv_[L].ptr;
+        k.q4_seq_stride = (int64_t)s_.max_seq_len * row_bytes_;
+        k.ring_seq_stride = (int64_t)ring_ * s_.n_kv_heads * s_.head_dim;
+        k.ring = ring_;
+        k.fp16_preserve_last = s_.fp16_preserve_last;
+        return k;
+    }
+    const int32_t* lengths_after() const { return static_cast<const int32_t*>(lens_.ptr) + s_.batch; }
+    const int32_t* quantised() const { return static_cast<const int32_t*>(q4n_.ptr); }
+    const GqaQ4Shape& shape() const { return s_; }
+
+private:
+    explicit GqaAttentionQ4(const GqaQ4Shape& s) : s_(s) {}
+    const int32_t* before() const { return static_cast<const int32_t*>(lens_.ptr); }
+    mugen_attn_gqa_decode_q4_args decode_args(int L, const void* q, void* out) const {
+        mugen_attn_gqa_decode_q4_args d{};
+        d.q = q;
+        d.store = store(L);
+        d.seq_lens = lengths_after();
+        d.n_q4 = static_cast<const int32_t*>(q4n_.ptr) + s_.batch;  // the state after this step's append
+        d.out = out;
+        d.batch = s_.batch;
+        d.n_heads = s_.n_heads;
+        d.n_kv_heads = s_.n_kv_heads;
+        d.head_dim = s_.head_dim;
+        d.max_seq_len = s_.max_seq_len;
+        d.scale = s_.scale;
+        d.out_dtype = s_.out_dtype;
+        d.seq_lens_host = nullptr;  // planned for max_seq_len: one plan serves every step
+        return d;
+    }
+
+    GqaQ4Shape s_;
+    int ring_ = 0, row_bytes_ = 0;
+    std::vector<detail::DeviceBuffer> q4k_, q4v_, rk_, rv_;
+    detail::DeviceBuffer lens_, q4n_, ws_;
+};
+
 // ---------------------------------------------------------------- MLA
 
 struct MlaShape {

@@ -4,7 +4,8 @@
 // bit-identical outputs at every step (same kernels, same inputs), while the
 // device-side lengths advance by one per step inside the graph (q_len per
 // step for an MLA verify step).  A prompt chunk through prefill_layer is
-// checked against a direct causal prefill over the same context.
+// checked against a direct causal prefill over the same context, and the
+// 4-bit store provider's replayed steps against eager ones.
 //
 // Built by mugen_amd/build.py next to libmugen_attn.so; run by
 // tests/test_engine_gpu.py.  Prints PASS / FAIL lines; exit status 0 only
@@ -277,6 +278,147 @@ void mla_test(hipStream_t st, int q_len) {
     std::printf("mla provider done\n");
 }
 
+// ---------------------------------------------------------------- GQA, 4-bit store
+
+float max_abs_diff_f16(const std::vector<uint8_t>& a, const std::vector<uint8_t>& b) {
+    float m = 0.f;
+    for (size_t i = 0; i + 1 < a.size(); i += 2) {
+        _Float16 x, y;
+        std::memcpy(&x, &a[i], 2);
+        std::memcpy(&y, &b[i], 2);
+        m = std::max(m, std::fabs((float)x - (float)y));
+    }
+    return m;
+}
+
+// A context appended in chunks, then decode steps eager and replayed from
+// one captured graph (bit-identical, lengths and quantised counts advancing
+// on the device); a store that quantises nothing (preserve >= length) must
+// agree with the f16 provider fed the same tokens.
+void gqa_q4_test(hipStream_t st) {
+    mugen_attn::GqaQ4Shape s;
+    s.n_layers = 2;
+    s.batch = 2;
+    s.n_heads = 28;
+    s.n_kv_heads = 4;
+    s.head_dim = 128;
+    s.max_seq_len = 512;
+    s.fp16_preserve_last = 16;
+    s.max_new = 32;
+    const std::vector<int32_t> lens0 = {0, 5};
+    const int chunks = 3, steps = 4;
+    std::printf("gqa q4 provider: layers %d batch %d preserve %d chunks %d steps %d\n", s.n_layers, s.batch,
+                s.fp16_preserve_last, chunks, steps);
+    std::fflush(stdout);
+    mugen_attn::GqaQ4Shape s_wide = s;  // nothing quantised: compared with the f16 provider
+    s_wide.fp16_preserve_last = 256;
+    mugen_attn::GqaShape sf;
+    sf.n_layers = s.n_layers;
+    sf.batch = s.batch;
+    sf.n_heads = s.n_heads;
+    sf.n_kv_heads = s.n_kv_heads;
+    sf.head_dim = s.head_dim;
+    sf.max_seq_len = s.max_seq_len;
+    std::unique_ptr<mugen_attn::GqaAttentionQ4> eager, graphed, wide;
+    std::unique_ptr<mugen_attn::GqaAttention> f16;
+    if (!ok(mugen_attn::GqaAttentionQ4::create(s, &eager), "create eager")) return;
+    if (!ok(mugen_attn::GqaAttentionQ4::create(s, &graphed), "create graphed")) return;
+    if (!ok(mugen_attn::GqaAttentionQ4::create(s_wide, &wide), "create wide")) return;
+    if (!ok(mugen_attn::GqaAttention::create(sf, &f16), "create f16")) return;
+    for (auto* a : {eager.get(), graphed.get(), wide.get()}) ok(a->set_lengths(lens0, st), "q4 lengths");
+    ok(f16->set_lengths(lens0, st), "f16 lengths");
+    const size_t row = (size_t)s.n_kv_heads * s.head_dim;
+    Rng r(4);
+    {   // the context: chunks of max_new tokens per sequence, every layer
+        Dev kc((size_t)s.batch * s.max_new * row * 2), vc((size_t)s.batch * s.max_new * row * 2);
+        Dev k1((size_t)s.max_new * row * 2), v1((size_t)s.max_new * row * 2);
+        for (int c = 0; c < chunks; c++) {
+            for (int L = 0; L < s.n_layers; L++) {
+                auto hk = f16_rand(r, kc.n / 2, 1.0f), hv = f16_rand(r, vc.n / 2, 1.0f);
+                kc.put(hk.data(), st);
+                vc.put(hv.data(), st);
+                for (auto* a : {eager.get(), graphed.get(), wide.get()})
+                    ok(a->append_layer(L, kc.p, vc.p, s.max_new, st), "q4 append");
+                // the f16 provider takes the same rows (sequence-major [batch][n_new][row])
+                mugen_attn_kv_append_args ap{};
+                ap.k_new = kc.p;
+                ap.v_new = vc.p;
+                ap.k_cache = f16->k_cache(L);
+                ap.v_cache = f16->v_cache(L);
+                ap.seq_lens = f16->lengths_after() - s.batch;
+                ap.seq_stride = (int64_t)s.max_seq_len * row;
+                ap.n_seq = s.batch;
+                ap.n_new = s.max_new;
+                ap.row = (int)row;
+                ap.max_seq_len = s.max_seq_len;
+                ok(mugen_attn::kv_append(ap, st), "f16 append");
+                hip(hipStreamSynchronize(st), "sync");
+            }
+            for (auto* a : {eager.get(), graphed.get(), wide.get()}) ok(a->advance(st, s.max_new), "q4 advance");
+            ok(f16->advance(st, s.max_new), "f16 advance");
+        }
+    }
+    std::vector<std::unique_ptr<Dev>> q, kn, vn, oe, og, ow, of;
+    const size_t qb = (size_t)s.batch * s.n_heads * s.head_dim * 2, kb = (size_t)s.batch * row * 2;
+    for (int L = 0; L < s.n_layers; L++) {
+        q.emplace_back(new Dev(qb));
+        kn.emplace_back(new Dev(kb));
+        vn.emplace_back(new Dev(kb));
+        oe.emplace_back(new Dev(qb));
+        og.emplace_back(new Dev(qb));
+        ow.emplace_back(new Dev(qb));
+        of.emplace_back(new Dev(qb));
+    }
+    mugen_attn::StepGraph graph;
+    auto body = [&](hipStream_t str) -> Status {
+        for (int L = 0; L < s.n_layers; L++)
+            if (auto rr = graphed->decode_layer(L, q[L]->p, kn[L]->p, vn[L]->p, og[L]->p, str); !rr) return rr;
+        return graphed->advance(str);
+    };
+    if (!ok(graph.capture(st, body), "q4 capture")) return;
+    for (int step = 0; step < steps; step++) {
+        Rng ri(300 + step);
+        for (int L = 0; L < s.n_layers; L++) {
+            auto hq = f16_rand(ri, qb / 2, 1.0f), hk = f16_rand(ri, kb / 2, 1.0f), hv = f16_rand(ri, kb / 2, 1.0f);
+            q[L]->put(hq.data(), st);
+            kn[L]->put(hk.data(), st);
+            vn[L]->put(hv.data(), st);
+            hip(hipStreamSynchronize(st), "sync");
+        }
+        for (int L = 0; L < s.n_layers; L++) {
+            ok(eager->decode_layer(L, q[L]->p, kn[L]->p, vn[L]->p, oe[L]->p, st), "q4 eager decode");
+            ok(wide->decode_layer(L, q[L]->p, kn[L]->p, vn[L]->p, ow[L]->p, st), "q4 wide decode");
+            ok(f16->decode_layer(L, q[L]->p, kn[L]->p, vn[L]->p, of[L]->p, st), "f16 decode");
+        }
+        ok(eager->advance(st), "q4 eager advance");
+        ok(wide->advance(st), "q4 wide advance");
+        ok(f16->advance(st), "f16 advance");
+        hip(hipStreamSynchronize(st), "sync");
+        ok(graph.replay(st), "q4 replay");
+        hip(hipStreamSynchronize(st), "sync");
+        for (int L = 0; L < s.n_layers; L++) {
+            const auto a = oe[L]->get(st), b = og[L]->get(st), w = ow[L]->get(st), f = of[L]->get(st);
+            if (a != b || !finite_f16(a)) {
+                std::printf("FAIL gqa q4 step %d layer %d: graph replay differs from the eager call\n", step, L);
+                failures++;
+            }
+            const float d = max_abs_diff_f16(w, f);
+            if (!(d <= 2e-3f)) {
+                std::printf("FAIL gqa q4 step %d layer %d: unquantised store vs f16 provider max-abs %g\n", step, L,
+                            d);
+                failures++;
+            }
+        }
+        std::vector<int32_t> want(lens0), wq4;
+        for (auto& x : want) x += chunks * s.max_new + step + 2;
+        check_lengths(eager->lengths_after(), want, st, "gqa q4 eager");
+        check_lengths(graphed->lengths_after(), want, st, "gqa q4 graphed");
+        for (int32_t x : want) wq4.push_back(std::max(0, x - 1 - s.fp16_preserve_last));
+        check_lengths(graphed->quantised(), wq4, st, "gqa q4 quantised counts");
+    }
+    std::printf("gqa q4 provider done\n");
+}
+
 // ---------------------------------------------------------------- GQA prefill
 
 // A prompt chunk appended to a held context through prefill_layer: the cache
@@ -360,6 +502,7 @@ int main() {
     mla_test(st, 1);
     mla_test(st, 3);
     gqa_prefill_test(st);
+    gqa_q4_test(st);
     (void)hipStreamSynchronize(st);
     (void)hipStreamDestroy(st);
     std::printf(failures ? "FAIL (%d)\n" : "PASS\n", failures);
