@@ -288,13 +288,14 @@ def capture(case, n):
     return g
 
 
-WARMUP_MIN_S = 0.3  # untimed GPU work before timing: clocks settle
+WARMUP_MIN_S = 0.5  # untimed GPU work before timing: clocks settle
 
 
 def time_case(case, steps, warmup, dev):
     """Warm-up, then EXACTLY `steps` steps timed with events between two
     synchronisations.  Warm-up is `warmup` untimed steps, continued (still
-    untimed) until at least WARMUP_MIN_S of wall time has passed: the first
+    untimed, as back-to-back replays of the captured graphs that keep the GPU
+    busy) until at least WARMUP_MIN_S of wall time has passed: the first
     workload measured in a fresh process otherwise runs ~8% slower than the
     same kernels a second later (the GPU's clocks ramp up).  The steps run as
     replays of captured HIP graphs (up to GRAPH_STEPS steps each): the GPU
@@ -305,16 +306,16 @@ def time_case(case, steps, warmup, dev):
     for _ in range(warmup):
         case.step()
     torch.cuda.synchronize(dev)
-    while time.perf_counter() - t_w < WARMUP_MIN_S:
-        for _ in range(20):
-            case.step()
-        torch.cuda.synchronize(dev)
     per = min(GRAPH_STEPS, steps)
     full, rest = divmod(steps, per)
     graphs = [(capture(case, per), full)] + ([(capture(case, rest), 1)] if rest else [])
     for g, _ in graphs:  # one untimed replay each (graph upload)
         g.replay()
     torch.cuda.synchronize(dev)
+    while time.perf_counter() - t_w < WARMUP_MIN_S:
+        for _ in range(4):
+            graphs[0][0].replay()
+        torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
