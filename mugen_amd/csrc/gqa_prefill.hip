@@ -295,6 +295,279 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
     }
 }
 
+// ------------------------------------------------------------------ warp-specialised variant
+//
+// For long prompts the kernel above is bound neither by MFMA issue nor by
+// LDS bandwidth but by its serial per-tile chain: the two waves of a SIMD
+// run their MFMA and softmax phases in lock step (one barrier per tile).
+// This variant gives the two phases to different waves, as the MLA decode
+// kernel does:
+//  * workgroup = (16-token query block, kv head, slice of NS = 4 or 8 heads
+//    of the group); blocks are numbered longest-first across all kv heads
+//    and slices;
+//  * waves 0..NS-1 ("S waves"): head NS*slice + w: S^T = K . Q^T for a 32-key
+//    tile (the same operand layouts as above with one key half), causal
+//    mask, lazy-max softmax, and P (hi + lo for bf16) written to LDS in the
+//    B-operand layout of the PV product, with the row's re-base factor when
+//    its max moved;
+//  * the last 4 waves ("PV waves"): output columns [D/4 * (w-NS), +D/4) of
+//    the NS heads: O^T += V^T . P^T for the previous tile, after applying that
+//    tile's re-base factors, and the K / V tile DMA into a 4-slot ring;
+//  * one barrier per tile: at barrier j tile j has landed, the S waves have
+//    written P(j-1), and the PV waves have finished tile j-2, whose slot
+//    then receives tile j+2.
+template <int D, int NS, int DT, int OUT_DT>
+__global__ __launch_bounds__(64 * (NS + 4)) void gqa_prefill_ws_kernel(GqaPrefillParams p, int nqb, int nslice,
+                                                                       int Hk) {
+    constexpr int TK = 32;                      // keys per tile
+    constexpr int KK = D / 32;                  // k-steps of S over head_dim
+    constexpr int DB = D / 16;                  // 16-wide output column blocks
+    constexpr int DBW = DB / 4;                 // column blocks per PV wave
+    constexpr int RB = D * 2;                   // bytes per tile row
+    constexpr int CR = D / 8;                   // 16-byte chunks per row
+    constexpr int MAT = TK * RB;                // bytes of one K or V tile
+    constexpr int SLOT = 2 * MAT;
+    constexpr int NSLOT = 4;                    // NSLOT - 2 tiles in flight
+    constexpr int DPW = 2 * MAT / 1024 / 4;     // 1-KiB DMA ops per PV wave per tile (K and V)
+    constexpr int NP = p_terms<DT>();
+    constexpr int PB = NS * NP * 64 * 16;       // one P buffer: NS heads x NP terms x 64 lanes x 16 B
+    static_assert(DPW >= 2 && DPW % 2 == 0 && DBW >= 1, "tile split");
+    __shared__ __attribute__((aligned(1024))) char ring[NSLOT * SLOT + 2 * PB];
+    __shared__ float alpha_x[2][NS][16];        // per P buffer: re-base factor of (head, query)
+    __shared__ int resc_x[2][NS];               // per P buffer: head's factors apply
+    __shared__ float linv_x[NS][16];
+    constexpr float kHeadroom = 8.f;
+
+    // longest-first over (query block, kv head, slice)
+    const int lin = blockIdx.x;
+    const int per_qb = Hk * nslice;
+    const int qb = nqb - 1 - lin / per_qb;
+    const int kvh = (lin / nslice) % Hk;
+    const int slice = lin % nslice;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool s_wave = w < NS;
+    const int wr = s_wave ? w : w - NS;         // S wave: head of the slice; PV wave: column quarter
+    const int n = lane & 15, g = lane >> 4;
+    const int t0 = qb * 16;
+    const int G = p.G;
+    const int nh = min(NS, G - NS * slice);     // heads of this slice
+    int kend = p.kv_len;
+    if (p.causal) kend = min(kend, p.start_pos + min(t0 + 16, p.N));
+    const int ntiles = (kend + TK - 1) / TK;
+    const uint32_t ring_base = lds_addr(&ring[0]);
+    char* pbuf = &ring[NSLOT * SLOT];
+
+    if (s_wave) {
+        // ================================================== S waves
+        const bool hok = wr < nh;
+        const int hg = NS * slice + (hok ? wr : 0);
+        const int tok = min(t0 + n, p.N - 1);
+        u32x4_t qf[KK];
+        const uint16_t* qp = p.q + ((int64_t)tok * p.H + kvh * G + hg) * D + 8 * g;
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++) qf[kk] = load16(qp + 32 * kk);
+        const int row_lim = p.causal ? min(p.start_pos + t0 + n + 1, p.kv_len) : p.kv_len;
+        const int mask_from = p.causal ? min(p.start_pos + t0 + 1, p.kv_len) : p.kv_len;
+        // K operand (A): tile row 8(n/4) + n%4 (+4nb), logical chunk g + 4kk
+        const int ar = 8 * (n >> 2) + (n & 3);
+        uint32_t a_off[KK];
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++) a_off[kk] = ar * RB + (((g + 4 * kk) ^ pf_swz<D>(ar)) * 16);
+        float m_run = kNegInf, l_part = 0.f;
+        for (int j = 0; j <= ntiles; j++) {
+            if (j == 8) MUGEN_TRACE(0);
+            lds_barrier();  // B_j: tile j landed
+            if (j == 8) MUGEN_TRACE(1);
+            if (j == 16) MUGEN_TRACE(5);
+            if (j == ntiles) break;
+            if (!hok) continue;
+            const char* tile = &ring[(j % NSLOT) * SLOT];
+            const int kt = j * TK;
+            u32x4_t af[2][KK];
+#pragma unroll
+            for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+                for (int kk = 0; kk < KK; kk++)
+                    af[nb][kk] = *reinterpret_cast<const u32x4_t*>(tile + a_off[kk] + nb * 4 * RB);
+            float s[8];
+#pragma unroll
+            for (int nb = 0; nb < 2; nb++) {
+                f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < KK; kk++) acc = mfma16x16x32<DT>(af[nb][kk], qf[kk], acc);
+#pragma unroll
+                for (int i = 0; i < 4; i++) s[4 * nb + i] = acc[i];
+            }
+            // lane: query t0+n, keys kt + 8g + 4nb + i
+            if (kt + TK > mask_from) {
+                const int key0 = kt + 8 * g;
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++)
+                    if (key0 + jj >= row_lim) s[jj] = kNegInf;
+            }
+            if (j == 8) MUGEN_TRACE(2);
+            float smax = s[0];
+#pragma unroll
+            for (int jj = 1; jj < 8; jj++) smax = fmaxf(smax, s[jj]);
+            float alpha = 1.f;
+            const bool rebase = __any(smax * p.scale_log2 > m_run + kHeadroom);
+            if (rebase) {
+                const float mt = max_x32(max_x16(smax * p.scale_log2));
+                const float m_new = fmaxf(m_run, mt);
+                if (m_new > m_run) {
+                    alpha = fast_exp2(m_run - m_new);  // 0 when m_run = -inf
+                    l_part *= alpha;
+                    m_run = m_new;
+                }
+            }
+            const float nm = m_run == kNegInf ? 0.f : -m_run;
+            float x[8];
+            float ps = 0.f;
+#pragma unroll
+            for (int jj = 0; jj < 8; jj++) {
+                x[jj] = fast_exp2(fmaf(s[jj], p.scale_log2, nm));
+                ps += x[jj];
+            }
+            l_part += ps;
+            u32x4_t pfr[NP];
+            split_p<DT, NP>(x, pfr);
+            char* pb = pbuf + (j & 1) * PB;
+#pragma unroll
+            for (int pp = 0; pp < NP; pp++)
+                *reinterpret_cast<u32x4_t*>(pb + ((wr * NP + pp) * 64 + lane) * 16) = pfr[pp];
+            if (g == 0) alpha_x[j & 1][wr][n] = alpha;
+            if (lane == 0) resc_x[j & 1][wr] = rebase ? 1 : 0;
+            if (j == 8) MUGEN_TRACE(3);
+        }
+        const float l = sum_x32(sum_x16(l_part));
+        if (g == 0) linv_x[wr][n] = l > 0.f ? 1.f / l : 0.f;
+        __syncthreads();  // E: 1/l published
+    } else {
+        // ================================================== PV waves
+        const uint16_t* kb = p.k + (int64_t)kvh * D;
+        const uint16_t* vb = p.v + (int64_t)kvh * D;
+        const int rs_bytes = p.row_stride * 2;
+        // DMA op k of this wave moves K / V chunks [64(wr + 4k), +64) of the
+        // tile: chunk slot s = row s / CR, physical chunk s % CR, holding
+        // logical chunk (s % CR) ^ pf_swz(row); rows past kend are clamped
+        int dma_row[DPW / 2];
+        uint32_t dma_col[DPW / 2];
+#pragma unroll
+        for (int k = 0; k < DPW / 2; k++) {
+            const int slot = 64 * (wr + 4 * k) + lane;
+            const int r = slot / CR, pc = slot % CR;
+            dma_row[k] = r;
+            dma_col[k] = (uint32_t)((pc ^ pf_swz<D>(r)) * 16);
+        }
+        auto issue = [&](int it) {
+            const int kt = it * TK;
+            const uint32_t lds0 = ring_base + (it % NSLOT) * SLOT + wr * 1024;
+#pragma unroll
+            for (int k = 0; k < DPW / 2; k++) {
+                const uint32_t off = (uint32_t)min(kt + dma_row[k], kend - 1) * rs_bytes + dma_col[k];
+                dma16s(lds0 + k * 4096, kb, off);
+                dma16s(lds0 + MAT + k * 4096, vb, off);
+            }
+        };
+        for (int it = 0; it < min(ntiles, NSLOT - 2); it++) issue(it);
+        // V operand (A, transpose reads): tile row 8g + n/4 (+4), logical
+        // bytes 32d + 8(n%4) = chunk 2d + (n%4)/2, half n%2
+        const int tr = 8 * g + (n >> 2);
+        uint32_t t_off[DBW];
+#pragma unroll
+        for (int dd = 0; dd < DBW; dd++) {
+            const int d = wr * DBW + dd;
+            t_off[dd] = MAT + tr * RB + (((2 * d + ((n & 3) >> 1)) ^ pf_swz<D>(tr)) * 16) + 8 * (n & 1);
+        }
+        f32x4_t o[NS][DBW];
+#pragma unroll
+        for (int h = 0; h < NS; h++)
+#pragma unroll
+            for (int dd = 0; dd < DBW; dd++) o[h][dd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j <= ntiles; j++) {
+            // tile j landed before B_j: the tiles issued after it are
+            // j+1 .. min(j + NSLOT - 3, ntiles - 1), DPW operations each
+            if (j == 8) MUGEN_TRACE(0);
+            switch (min(NSLOT - 3, max(ntiles - 1 - j, 0))) {  // one s_waitcnt
+#define PF_VMW(C) case C: vm_wait<C * DPW>(); break;
+                PF_VMW(0) PF_VMW(1) PF_VMW(2) PF_VMW(3) PF_VMW(4) PF_VMW(5)
+#undef PF_VMW
+            }
+            static_assert(NSLOT - 3 <= 5, "wait cases");
+            if (j == 8) MUGEN_TRACE(4);
+            lds_barrier();  // B_j
+            if (j == 8) MUGEN_TRACE(1);
+            if (j == 16) MUGEN_TRACE(5);
+            if (j + NSLOT - 2 < ntiles) issue(j + NSLOT - 2);  // into the slot of tile j-2
+            if (j == 0) continue;
+            const int jp = j - 1;
+            const char* tile = &ring[(jp % NSLOT) * SLOT];
+            const char* pb = pbuf + (jp & 1) * PB;
+            u32x4_t vf[DBW];
+#pragma unroll
+            for (int dd = 0; dd < DBW; dd++) {
+                const u32x2_t lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(tile + t_off[dd]));
+                const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(tile + t_off[dd] + 4 * RB));
+                vf[dd] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+            }
+            // four heads at a time: their factors and P in one LDS round trip,
+            // then independent MFMAs back to back
+#pragma unroll
+            for (int h0 = 0; h0 < NS; h0 += 4) {
+                u32x4_t pf[4][NP];
+                float a[4];
+                int rs[4];
+#pragma unroll
+                for (int hh = 0; hh < 4; hh++) {
+                    rs[hh] = resc_x[jp & 1][h0 + hh];
+                    a[hh] = alpha_x[jp & 1][h0 + hh][n];
+#pragma unroll
+                    for (int pp = 0; pp < NP; pp++)
+                        pf[hh][pp] = *reinterpret_cast<const u32x4_t*>(pb + (((h0 + hh) * NP + pp) * 64 + lane) * 16);
+                }
+#pragma unroll
+                for (int hh = 0; hh < 4; hh++)
+                    if (h0 + hh < nh && rs[hh]) {
+#pragma unroll
+                        for (int dd = 0; dd < DBW; dd++) o[h0 + hh][dd] *= a[hh];
+                    }
+                // (heads past nh accumulate stale P; their sums are never stored)
+#pragma unroll
+                for (int pp = 0; pp < NP; pp++)
+#pragma unroll
+                    for (int hh = 0; hh < 4; hh++)
+#pragma unroll
+                        for (int dd = 0; dd < DBW; dd++)
+                            o[h0 + hh][dd] = mfma16x16x32<DT>(vf[dd], pf[hh][pp], o[h0 + hh][dd]);
+            }
+            if (j == 8) MUGEN_TRACE(3);
+        }
+        __syncthreads();  // E: the S waves' 1/l
+        // lane (g, n): O[query t0+n][16d + 4g + i]
+        const int tok = t0 + n;
+        if (tok < p.N) {
+#pragma unroll
+            for (int h = 0; h < NS; h++) {
+                if (h >= nh) continue;
+                const float inv = linv_x[h][n];
+                const int64_t base = ((int64_t)tok * p.H + kvh * G + NS * slice + h) * D + 4 * g;
+#pragma unroll
+                for (int dd = 0; dd < DBW; dd++) {
+                    const int d = wr * DBW + dd;
+                    const f32x4_t r = o[h][dd] * inv;
+                    if constexpr (OUT_DT == DT_F32) {
+                        *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.out) + base + 16 * d) = r;
+                    } else {
+                        *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.out) + base + 16 * d) =
+                            u32x2_t{pack2<OUT_DT>(r[0], r[1]), pack2<OUT_DT>(r[2], r[3])};
+                    }
+                }
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------ launch
 
 template <int D, int MB, int DT, int OUT_DT>
@@ -324,8 +597,35 @@ static hipError_t launch_pf_g(const GqaPrefillParams& p, int Hk, int dt, int out
     return launch_pf_d<D, 2>(p, Hk, dt, out_dt, st, t);
 }
 
-hipError_t launch_gqa_prefill(const GqaPrefillParams& p, int Hk, int D, int dt, int out_dt,
+template <int D, int DT, int OUT_DT>
+static hipError_t launch_pf_ws_t(const GqaPrefillParams& p, int Hk, hipStream_t st, KernelTimer* t) {
+    const int nqb = (p.N + 15) / 16;
+    if (p.G <= 4)
+        return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 4, DT, OUT_DT>, dim3(nqb * Hk * ((p.G + 3) / 4)),
+                        dim3(64 * 8), st, p, nqb, (p.G + 3) / 4, Hk);
+    const int nslice = (p.G + 7) / 8;
+    return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 8, DT, OUT_DT>, dim3(nqb * Hk * nslice), dim3(64 * 12),
+                    st, p, nqb, nslice, Hk);
+}
+
+template <int D, int DT>
+static hipError_t launch_pf_ws_o(const GqaPrefillParams& p, int Hk, int out_dt, hipStream_t st, KernelTimer* t) {
+    if (out_dt == DT_F32) return launch_pf_ws_t<D, DT, DT_F32>(p, Hk, st, t);
+    if (out_dt == DT_F16) return launch_pf_ws_t<D, DT, DT_F16>(p, Hk, st, t);
+    return launch_pf_ws_t<D, DT, DT_BF16>(p, Hk, st, t);
+}
+
+template <int D>
+static hipError_t launch_pf_ws(const GqaPrefillParams& p, int Hk, int dt, int out_dt, hipStream_t st,
+                               KernelTimer* t) {
+    if (dt == DT_F16) return launch_pf_ws_o<D, DT_F16>(p, Hk, out_dt, st, t);
+    return launch_pf_ws_o<D, DT_BF16>(p, Hk, out_dt, st, t);
+}
+
+hipError_t launch_gqa_prefill(const GqaPrefillParams& p, int Hk, int D, int dt, int out_dt, int variant,
                               hipStream_t st, KernelTimer* t) {
+    if (variant == 2) return D == 128 ? launch_pf_ws<128>(p, Hk, dt, out_dt, st, t)
+                                      : launch_pf_ws<64>(p, Hk, dt, out_dt, st, t);
     if (D == 128) return launch_pf_g<128>(p, Hk, dt, out_dt, st, t);
     return launch_pf_g<64>(p, Hk, dt, out_dt, st, t);
 }

@@ -103,7 +103,9 @@ struct GqaPrefillParams {
     float scale_log2;
 };
 
-hipError_t launch_gqa_prefill(const GqaPrefillParams& p, int Hk, int D, int dt, int out_dt,
+// variant 1: one (query block, kv head) per workgroup, every wave doing S,
+// softmax and PV; 2: warp-specialised S / PV waves (long prompts)
+hipError_t launch_gqa_prefill(const GqaPrefillParams& p, int Hk, int D, int dt, int out_dt, int variant,
                               hipStream_t st, KernelTimer* t);
 
 struct MlaParams {

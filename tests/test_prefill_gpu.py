@@ -55,3 +55,25 @@ def test_golden_fixture(device):
     c = dict(N=int(fx["N"]), H=int(fx["H"]), Hk=int(fx["Hk"]), D=int(fx["D"]), start=int(fx["start"]),
              dtype=int(fx["dtype"]), qb=fx["qb"], kb=fx["kb"], vb=fx["vb"])
     C.assert_close(run_gpu(c, device, C.F32), fx["out_f64"], "golden prefill_small")
+
+
+@pytest.mark.parametrize("N,H,Hk,D,start,dtype", [
+    (512, 32, 8, 64, 0, C.BF16), (40, 28, 4, 128, 100, C.F16), (200, 8, 1, 128, 300, C.BF16),
+    (65, 12, 3, 64, 0, C.F16), (300, 28, 4, 128, 0, C.BF16), (33, 16, 2, 64, 5, C.BF16),
+])
+def test_warp_specialised_variant(device, monkeypatch, N, H, Hk, D, start, dtype):
+    # the S / PV warp-specialised kernel (4 or 8 heads per block, G = 1, 4, 7,
+    # 8), against the same oracle
+    monkeypatch.setenv("MUGEN_ATTN_PREFILL_VARIANT", "2")
+    c = C.prefill_case(70 + N, N, H, Hk, D, start, dtype)
+    C.assert_close(run_gpu(c, device, C.F32), C.prefill_ref(c), f"ws prefill N={N} start={start}")
+
+
+def test_warp_specialised_non_causal(device, monkeypatch):
+    monkeypatch.setenv("MUGEN_ATTN_PREFILL_VARIANT", "2")
+    c = C.prefill_case(52, 33, 14, 2, 128, 0, C.BF16)
+    from oracle import oracle as O
+    ref = O.gqa_attention(c["q"], c["k"].reshape(1, c["kv_len"], 2, 128).repeat(33, 0),
+                          c["v"].reshape(1, c["kv_len"], 2, 128).repeat(33, 0), [c["kv_len"]] * 33, 14, 2, 128,
+                          c["kv_len"] * 2 * 128)
+    C.assert_close(run_gpu(c, device, C.F32, causal=False), ref, "ws non-causal")
