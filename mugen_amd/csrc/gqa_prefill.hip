@@ -511,27 +511,30 @@ __global__ __launch_bounds__(64 * (NS + 4)) void gqa_prefill_ws_kernel(GqaPrefil
                 const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(tile + t_off[dd] + 4 * RB));
                 vf[dd] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
             }
-            // four heads at a time: their factors and P in one LDS round trip,
-            // then independent MFMAs back to back
+            // re-base (rare after the first tiles): one uniform test for the
+            // tile, the factors read only when some head moved its max (a head
+            // that did not has factor 1)
+            int any_rs = 0;
+#pragma unroll
+            for (int h = 0; h < NS; h++) any_rs |= resc_x[jp & 1][h];
+            if (__builtin_amdgcn_readfirstlane(any_rs)) {
+#pragma unroll
+                for (int h = 0; h < NS; h++) {
+                    const float a = h < nh ? alpha_x[jp & 1][h][n] : 1.f;
+#pragma unroll
+                    for (int dd = 0; dd < DBW; dd++) o[h][dd] *= a;
+                }
+            }
+            // four heads at a time: their P in one LDS round trip, then
+            // independent MFMAs back to back
 #pragma unroll
             for (int h0 = 0; h0 < NS; h0 += 4) {
                 u32x4_t pf[4][NP];
-                float a[4];
-                int rs[4];
 #pragma unroll
-                for (int hh = 0; hh < 4; hh++) {
-                    rs[hh] = resc_x[jp & 1][h0 + hh];
-                    a[hh] = alpha_x[jp & 1][h0 + hh][n];
+                for (int hh = 0; hh < 4; hh++)
 #pragma unroll
                     for (int pp = 0; pp < NP; pp++)
                         pf[hh][pp] = *reinterpret_cast<const u32x4_t*>(pb + (((h0 + hh) * NP + pp) * 64 + lane) * 16);
-                }
-#pragma unroll
-                for (int hh = 0; hh < 4; hh++)
-                    if (h0 + hh < nh && rs[hh]) {
-#pragma unroll
-                        for (int dd = 0; dd < DBW; dd++) o[h0 + hh][dd] *= a[hh];
-                    }
                 // (heads past nh accumulate stale P; their sums are never stored)
 #pragma unroll
                 for (int pp = 0; pp < NP; pp++)
