@@ -561,7 +561,9 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     p.causal = a->causal ? 1 : 0;
     const float scale = a->scale > 0.f ? a->scale : 1.f / sqrtf((float)a->head_dim);
     p.scale_log2 = scale * kLog2e;
-    int variant = 1;
+    // the warp-specialised kernel where it measured faster: 1024..4096-token
+    // prompts (at 512 tokens and at 8192 the per-block kernel is ahead)
+    int variant = (a->n_tokens >= 1024 && a->n_tokens <= 4096) ? 2 : 1;
     if (const char* e = getenv("MUGEN_ATTN_PREFILL_VARIANT")) variant = atoi(e) == 2 ? 2 : 1;
     hipError_t e = launch_gqa_prefill(p, a->n_kv_heads, a->head_dim, a->dtype, a->out_dtype, variant,
                                       static_cast<hipStream_t>(stream), active_timer());

@@ -310,8 +310,8 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
 //    mask, lazy-max softmax, and P (hi + lo for bf16) written to LDS in the
 //    B-operand layout of the PV product, with the row's re-base factor when
 //    its max moved;
-//  * the last 4 waves ("PV waves"): output columns [D/4 * (w-NS), +D/4) of
-//    the NS heads: O^T += V^T . P^T for the previous tile, after applying that
+//  * the last 4 waves ("PV waves"): NS/4 heads each, every output column:
+//    O^T += V^T . P^T for the previous tile, after applying that
 //    tile's re-base factors, and the K / V tile DMA into a 4-slot ring;
 //  * one barrier per tile: at barrier j tile j has landed, the S waves have
 //    written P(j-1), and the PV waves have finished tile j-2, whose slot
@@ -474,21 +474,22 @@ __global__ __launch_bounds__(64 * (NS + 4)) void gqa_prefill_ws_kernel(GqaPrefil
         // V operand (A, transpose reads): tile row 8g + n/4 (+4), logical
         // bytes 32d + 8(n%4) = chunk 2d + (n%4)/2, half n%2
         const int tr = 8 * g + (n >> 2);
-        uint32_t t_off[DBW];
+        uint32_t t_off[DB];
 #pragma unroll
-        for (int dd = 0; dd < DBW; dd++) {
-            const int d = wr * DBW + dd;
-            t_off[dd] = MAT + tr * RB + (((2 * d + ((n & 3) >> 1)) ^ pf_swz<D>(tr)) * 16) + 8 * (n & 1);
-        }
-        f32x4_t o[NS][DBW];
+        for (int d = 0; d < DB; d++)
+            t_off[d] = MAT + tr * RB + (((2 * d + ((n & 3) >> 1)) ^ pf_swz<D>(tr)) * 16) + 8 * (n & 1);
+        // this wave's heads: HPW consecutive heads of the slice, every column
+        constexpr int HPW = NS / 4;
+        const int hb = wr * HPW;
+        f32x4_t o[HPW][DB];
 #pragma unroll
-        for (int h = 0; h < NS; h++)
+        for (int hh = 0; hh < HPW; hh++)
 #pragma unroll
-            for (int dd = 0; dd < DBW; dd++) o[h][dd] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            for (int d = 0; d < DB; d++) o[hh][d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         for (int j = 0; j <= ntiles; j++) {
+            if (j == 8) MUGEN_TRACE(0);
             // tile j landed before B_j: the tiles issued after it are
             // j+1 .. min(j + NSLOT - 3, ntiles - 1), DPW operations each
-            if (j == 8) MUGEN_TRACE(0);
             switch (min(NSLOT - 3, max(ntiles - 1 - j, 0))) {  // one s_waitcnt
 #define PF_VMW(C) case C: vm_wait<C * DPW>(); break;
                 PF_VMW(0) PF_VMW(1) PF_VMW(2) PF_VMW(3) PF_VMW(4) PF_VMW(5)
@@ -504,46 +505,40 @@ __global__ __launch_bounds__(64 * (NS + 4)) void gqa_prefill_ws_kernel(GqaPrefil
             const int jp = j - 1;
             const char* tile = &ring[(jp % NSLOT) * SLOT];
             const char* pb = pbuf + (jp & 1) * PB;
-            u32x4_t vf[DBW];
+            // this wave's heads' P, then the V^T fragments, in flight together
+            u32x4_t pf[HPW][NP];
 #pragma unroll
-            for (int dd = 0; dd < DBW; dd++) {
-                const u32x2_t lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(tile + t_off[dd]));
-                const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(tile + t_off[dd] + 4 * RB));
-                vf[dd] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
-            }
-            // re-base (rare after the first tiles): one uniform test for the
-            // tile, the factors read only when some head moved its max (a head
-            // that did not has factor 1)
-            int any_rs = 0;
-#pragma unroll
-            for (int h = 0; h < NS; h++) any_rs |= resc_x[jp & 1][h];
-            if (__builtin_amdgcn_readfirstlane(any_rs)) {
-#pragma unroll
-                for (int h = 0; h < NS; h++) {
-                    const float a = h < nh ? alpha_x[jp & 1][h][n] : 1.f;
-#pragma unroll
-                    for (int dd = 0; dd < DBW; dd++) o[h][dd] *= a;
-                }
-            }
-            // four heads at a time: their P in one LDS round trip, then
-            // independent MFMAs back to back
-#pragma unroll
-            for (int h0 = 0; h0 < NS; h0 += 4) {
-                u32x4_t pf[4][NP];
-#pragma unroll
-                for (int hh = 0; hh < 4; hh++)
-#pragma unroll
-                    for (int pp = 0; pp < NP; pp++)
-                        pf[hh][pp] = *reinterpret_cast<const u32x4_t*>(pb + (((h0 + hh) * NP + pp) * 64 + lane) * 16);
-                // (heads past nh accumulate stale P; their sums are never stored)
+            for (int hh = 0; hh < HPW; hh++)
 #pragma unroll
                 for (int pp = 0; pp < NP; pp++)
+                    pf[hh][pp] = *reinterpret_cast<const u32x4_t*>(pb + (((hb + hh) * NP + pp) * 64 + lane) * 16);
+            u32x4_t vf[DB];
 #pragma unroll
-                    for (int hh = 0; hh < 4; hh++)
-#pragma unroll
-                        for (int dd = 0; dd < DBW; dd++)
-                            o[h0 + hh][dd] = mfma16x16x32<DT>(vf[dd], pf[hh][pp], o[h0 + hh][dd]);
+            for (int d = 0; d < DB; d++) {
+                const u32x2_t lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(tile + t_off[d]));
+                const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(tile + t_off[d] + 4 * RB));
+                vf[d] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
             }
+            // re-base (rare after the first tiles): the factors are read only
+            // when one of this wave's heads moved its max (factor 1 otherwise)
+            int any_rs = 0;
+#pragma unroll
+            for (int hh = 0; hh < HPW; hh++) any_rs |= resc_x[jp & 1][hb + hh];
+            if (__builtin_amdgcn_readfirstlane(any_rs)) {
+#pragma unroll
+                for (int hh = 0; hh < HPW; hh++) {
+                    const float a = hb + hh < nh ? alpha_x[jp & 1][hb + hh][n] : 1.f;
+#pragma unroll
+                    for (int d = 0; d < DB; d++) o[hh][d] *= a;
+                }
+            }
+            // (heads past nh accumulate stale P; their sums are never stored)
+#pragma unroll
+            for (int pp = 0; pp < NP; pp++)
+#pragma unroll
+                for (int d = 0; d < DB; d++)
+#pragma unroll
+                    for (int hh = 0; hh < HPW; hh++) o[hh][d] = mfma16x16x32<DT>(vf[d], pf[hh][pp], o[hh][d]);
             if (j == 8) MUGEN_TRACE(3);
         }
         __syncthreads();  // E: the S waves' 1/l
@@ -551,14 +546,13 @@ __global__ __launch_bounds__(64 * (NS + 4)) void gqa_prefill_ws_kernel(GqaPrefil
         const int tok = t0 + n;
         if (tok < p.N) {
 #pragma unroll
-            for (int h = 0; h < NS; h++) {
-                if (h >= nh) continue;
-                const float inv = linv_x[h][n];
-                const int64_t base = ((int64_t)tok * p.H + kvh * G + NS * slice + h) * D + 4 * g;
+            for (int hh = 0; hh < HPW; hh++) {
+                if (hb + hh >= nh) continue;
+                const float inv = linv_x[hb + hh][n];
+                const int64_t base = ((int64_t)tok * p.H + kvh * G + NS * slice + hb + hh) * D + 4 * g;
 #pragma unroll
-                for (int dd = 0; dd < DBW; dd++) {
-                    const int d = wr * DBW + dd;
-                    const f32x4_t r = o[h][dd] * inv;
+                for (int d = 0; d < DB; d++) {
+                    const f32x4_t r = o[hh][d] * inv;
                     if constexpr (OUT_DT == DT_F32) {
                         *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.out) + base + 16 * d) = r;
                     } else {

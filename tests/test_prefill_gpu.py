@@ -34,6 +34,7 @@ def test_llama1b_config(device):
 @pytest.mark.parametrize("N,H,Hk,D,start,dtype", [
     (1, 8, 2, 64, 0, C.F16), (17, 4, 4, 128, 0, C.BF16), (40, 28, 4, 128, 100, C.F16),
     (100, 16, 2, 64, 7, C.BF16), (65, 12, 3, 64, 0, C.F16), (200, 8, 1, 128, 300, C.BF16),
+    (1100, 8, 2, 128, 50, C.BF16),  # a length the planner gives the warp-specialised kernel
 ])
 def test_shapes_and_offsets(device, N, H, Hk, D, start, dtype):
     c = C.prefill_case(50 + N, N, H, Hk, D, start, dtype)
@@ -61,7 +62,7 @@ def test_golden_fixture(device):
     (512, 32, 8, 64, 0, C.BF16), (40, 28, 4, 128, 100, C.F16), (200, 8, 1, 128, 300, C.BF16),
     (65, 12, 3, 64, 0, C.F16), (300, 28, 4, 128, 0, C.BF16), (33, 16, 2, 64, 5, C.BF16),
 ])
-def test_warp_specialised_variant(device, monkeypatch, N, H, Hk, D, start, dtype):
+def test_warp_specialised_variant(device, monkeypatch, N, H, Hk, D, start, dtype):  # forced on short prompts
     # the S / PV warp-specialised kernel (4 or 8 heads per block, G = 1, 4, 7,
     # 8), against the same oracle
     monkeypatch.setenv("MUGEN_ATTN_PREFILL_VARIANT", "2")
