@@ -310,28 +310,28 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
 //    mask, lazy-max softmax, and P (hi + lo for bf16) written to LDS in the
 //    B-operand layout of the PV product, with the row's re-base factor when
 //    its max moved;
-//  * the last 4 waves ("PV waves"): NS/4 heads each, every output column:
+//  * the last NPV = 4 or 8 waves ("PV waves"): NS/NPV heads each, every
+//    output column:
 //    O^T += V^T . P^T for the previous tile, after applying that
 //    tile's re-base factors, and the K / V tile DMA into a 4-slot ring;
 //  * one barrier per tile: at barrier j tile j has landed, the S waves have
 //    written P(j-1), and the PV waves have finished tile j-2, whose slot
 //    then receives tile j+2.
-template <int D, int NS, int DT, int OUT_DT>
-__global__ __launch_bounds__(64 * (NS + 4)) void gqa_prefill_ws_kernel(GqaPrefillParams p, int nqb, int nslice,
-                                                                       int Hk) {
+template <int D, int NS, int NPV, int DT, int OUT_DT>
+__global__ __launch_bounds__(64 * (NS + NPV)) void gqa_prefill_ws_kernel(GqaPrefillParams p, int nqb, int nslice,
+                                                                         int Hk) {
     constexpr int TK = 32;                      // keys per tile
     constexpr int KK = D / 32;                  // k-steps of S over head_dim
     constexpr int DB = D / 16;                  // 16-wide output column blocks
-    constexpr int DBW = DB / 4;                 // column blocks per PV wave
     constexpr int RB = D * 2;                   // bytes per tile row
     constexpr int CR = D / 8;                   // 16-byte chunks per row
     constexpr int MAT = TK * RB;                // bytes of one K or V tile
     constexpr int SLOT = 2 * MAT;
     constexpr int NSLOT = 4;                    // NSLOT - 2 tiles in flight
-    constexpr int DPW = 2 * MAT / 1024 / 4;     // 1-KiB DMA ops per PV wave per tile (K and V)
+    constexpr int DPW = 2 * MAT / 1024 / NPV;   // 1-KiB DMA ops per PV wave per tile (K and V)
     constexpr int NP = p_terms<DT>();
     constexpr int PB = NS * NP * 64 * 16;       // one P buffer: NS heads x NP terms x 64 lanes x 16 B
-    static_assert(DPW >= 2 && DPW % 2 == 0 && DBW >= 1, "tile split");
+    static_assert(DPW >= 2 && DPW % 2 == 0 && NS % NPV == 0, "tile split");
     __shared__ __attribute__((aligned(1024))) char ring[NSLOT * SLOT + 2 * PB];
     __shared__ float alpha_x[2][NS][16];        // per P buffer: re-base factor of (head, query)
     __shared__ int resc_x[2][NS];               // per P buffer: head's factors apply
@@ -448,14 +448,14 @@ __global__ __launch_bounds__(64 * (NS + 4)) void gqa_prefill_ws_kernel(GqaPrefil
         const uint16_t* kb = p.k + (int64_t)kvh * D;
         const uint16_t* vb = p.v + (int64_t)kvh * D;
         const int rs_bytes = p.row_stride * 2;
-        // DMA op k of this wave moves K / V chunks [64(wr + 4k), +64) of the
+        // DMA op k of this wave moves K / V chunks [64(wr + NPV k), +64) of the
         // tile: chunk slot s = row s / CR, physical chunk s % CR, holding
         // logical chunk (s % CR) ^ pf_swz(row); rows past kend are clamped
         int dma_row[DPW / 2];
         uint32_t dma_col[DPW / 2];
 #pragma unroll
         for (int k = 0; k < DPW / 2; k++) {
-            const int slot = 64 * (wr + 4 * k) + lane;
+            const int slot = 64 * (wr + NPV * k) + lane;
             const int r = slot / CR, pc = slot % CR;
             dma_row[k] = r;
             dma_col[k] = (uint32_t)((pc ^ pf_swz<D>(r)) * 16);
@@ -466,8 +466,8 @@ __global__ __launch_bounds__(64 * (NS + 4)) void gqa_prefill_ws_kernel(GqaPrefil
 #pragma unroll
             for (int k = 0; k < DPW / 2; k++) {
                 const uint32_t off = (uint32_t)min(kt + dma_row[k], kend - 1) * rs_bytes + dma_col[k];
-                dma16s(lds0 + k * 4096, kb, off);
-                dma16s(lds0 + MAT + k * 4096, vb, off);
+                dma16s(lds0 + k * NPV * 1024, kb, off);
+                dma16s(lds0 + MAT + k * NPV * 1024, vb, off);
             }
         };
         for (int it = 0; it < min(ntiles, NSLOT - 2); it++) issue(it);
@@ -479,7 +479,7 @@ __global__ __launch_bounds__(64 * (NS + 4)) void gqa_prefill_ws_kernel(GqaPrefil
         for (int d = 0; d < DB; d++)
             t_off[d] = MAT + tr * RB + (((2 * d + ((n & 3) >> 1)) ^ pf_swz<D>(tr)) * 16) + 8 * (n & 1);
         // this wave's heads: HPW consecutive heads of the slice, every column
-        constexpr int HPW = NS / 4;
+        constexpr int HPW = NS / NPV;
         const int hb = wr * HPW;
         f32x4_t o[HPW][DB];
 #pragma unroll
@@ -598,11 +598,14 @@ template <int D, int DT, int OUT_DT>
 static hipError_t launch_pf_ws_t(const GqaPrefillParams& p, int Hk, hipStream_t st, KernelTimer* t) {
     const int nqb = (p.N + 15) / 16;
     if (p.G <= 4)
-        return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 4, DT, OUT_DT>, dim3(nqb * Hk * ((p.G + 3) / 4)),
+        return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 4, 4, DT, OUT_DT>, dim3(nqb * Hk * ((p.G + 3) / 4)),
                         dim3(64 * 8), st, p, nqb, (p.G + 3) / 4, Hk);
     const int nslice = (p.G + 7) / 8;
-    return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 8, DT, OUT_DT>, dim3(nqb * Hk * nslice), dim3(64 * 12),
-                    st, p, nqb, nslice, Hk);
+    // 8-head blocks keep 4 PV waves (2 heads each): 8 PV waves (one head
+    // each, 16-wave blocks) measured no faster
+    constexpr int NPV = 4;
+    return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 8, NPV, DT, OUT_DT>, dim3(nqb * Hk * nslice),
+                    dim3(64 * (8 + NPV)), st, p, nqb, nslice, Hk);
 }
 
 template <int D, int DT>
