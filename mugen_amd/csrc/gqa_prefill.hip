@@ -317,9 +317,9 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
 //  * one barrier per tile: at barrier j tile j has landed, the S waves have
 //    written P(j-1), and the PV waves have finished tile j-2, whose slot
 //    then receives tile j+2.
-template <int D, int NS, int NPV, int DT, int OUT_DT>
-__global__ __launch_bounds__(64 * (NS + NPV)) void gqa_prefill_ws_kernel(GqaPrefillParams p, int nqb, int nslice,
-                                                                         int Hk) {
+template <int D, int NS, int SMB, int NPV, int DT, int OUT_DT>
+__global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(GqaPrefillParams p, int nqb,
+                                                                               int nslice, int Hk) {
     constexpr int TK = 32;                      // keys per tile
     constexpr int KK = D / 32;                  // k-steps of S over head_dim
     constexpr int DB = D / 16;                  // 16-wide output column blocks
@@ -346,8 +346,9 @@ __global__ __launch_bounds__(64 * (NS + NPV)) void gqa_prefill_ws_kernel(GqaPref
     const int slice = lin % nslice;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const bool s_wave = w < NS;
-    const int wr = s_wave ? w : w - NS;         // S wave: head of the slice; PV wave: column quarter
+    constexpr int NSW = NS / SMB;               // S waves, SMB heads each
+    const bool s_wave = w < NSW;
+    const int wr = s_wave ? w : w - NSW;        // S wave index; PV wave index
     const int n = lane & 15, g = lane >> 4;
     const int t0 = qb * 16;
     const int G = p.G;
@@ -360,13 +361,19 @@ __global__ __launch_bounds__(64 * (NS + NPV)) void gqa_prefill_ws_kernel(GqaPref
 
     if (s_wave) {
         // ================================================== S waves
-        const bool hok = wr < nh;
-        const int hg = NS * slice + (hok ? wr : 0);
-        const int tok = min(t0 + n, p.N - 1);
-        u32x4_t qf[KK];
-        const uint16_t* qp = p.q + ((int64_t)tok * p.H + kvh * G + hg) * D + 8 * g;
+        // heads wr*SMB .. +SMB-1 of the slice share each K fragment read
+        bool hok[SMB];
+        u32x4_t qf[SMB][KK];
 #pragma unroll
-        for (int kk = 0; kk < KK; kk++) qf[kk] = load16(qp + 32 * kk);
+        for (int mb = 0; mb < SMB; mb++) {
+            const int hs = wr * SMB + mb;
+            hok[mb] = hs < nh;
+            const int tok = min(t0 + n, p.N - 1);
+            const uint16_t* qp =
+                p.q + ((int64_t)tok * p.H + kvh * G + NS * slice + (hok[mb] ? hs : 0)) * D + 8 * g;
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++) qf[mb][kk] = load16(qp + 32 * kk);
+        }
         const int row_lim = p.causal ? min(p.start_pos + t0 + n + 1, p.kv_len) : p.kv_len;
         const int mask_from = p.causal ? min(p.start_pos + t0 + 1, p.kv_len) : p.kv_len;
         // K operand (A): tile row 8(n/4) + n%4 (+4nb), logical chunk g + 4kk
@@ -374,14 +381,19 @@ __global__ __launch_bounds__(64 * (NS + NPV)) void gqa_prefill_ws_kernel(GqaPref
         uint32_t a_off[KK];
 #pragma unroll
         for (int kk = 0; kk < KK; kk++) a_off[kk] = ar * RB + (((g + 4 * kk) ^ pf_swz<D>(ar)) * 16);
-        float m_run = kNegInf, l_part = 0.f;
+        float m_run[SMB], l_part[SMB];
+#pragma unroll
+        for (int mb = 0; mb < SMB; mb++) {
+            m_run[mb] = kNegInf;
+            l_part[mb] = 0.f;
+        }
         for (int j = 0; j <= ntiles; j++) {
             if (j == 8) MUGEN_TRACE(0);
             lds_barrier();  // B_j: tile j landed
             if (j == 8) MUGEN_TRACE(1);
             if (j == 16) MUGEN_TRACE(5);
             if (j == ntiles) break;
-            if (!hok) continue;
+            if (!hok[0]) continue;
             const char* tile = &ring[(j % NSLOT) * SLOT];
             const int kt = j * TK;
             u32x4_t af[2][KK];
@@ -390,58 +402,69 @@ __global__ __launch_bounds__(64 * (NS + NPV)) void gqa_prefill_ws_kernel(GqaPref
 #pragma unroll
                 for (int kk = 0; kk < KK; kk++)
                     af[nb][kk] = *reinterpret_cast<const u32x4_t*>(tile + a_off[kk] + nb * 4 * RB);
-            float s[8];
+            float sv[SMB][8];
 #pragma unroll
-            for (int nb = 0; nb < 2; nb++) {
-                f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+            for (int mb = 0; mb < SMB; mb++)
 #pragma unroll
-                for (int kk = 0; kk < KK; kk++) acc = mfma16x16x32<DT>(af[nb][kk], qf[kk], acc);
+                for (int nb = 0; nb < 2; nb++) {
+                    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int i = 0; i < 4; i++) s[4 * nb + i] = acc[i];
-            }
-            // lane: query t0+n, keys kt + 8g + 4nb + i
-            if (kt + TK > mask_from) {
-                const int key0 = kt + 8 * g;
+                    for (int kk = 0; kk < KK; kk++) acc = mfma16x16x32<DT>(af[nb][kk], qf[mb][kk], acc);
 #pragma unroll
-                for (int jj = 0; jj < 8; jj++)
-                    if (key0 + jj >= row_lim) s[jj] = kNegInf;
-            }
-            if (j == 8) MUGEN_TRACE(2);
-            float smax = s[0];
-#pragma unroll
-            for (int jj = 1; jj < 8; jj++) smax = fmaxf(smax, s[jj]);
-            float alpha = 1.f;
-            const bool rebase = __any(smax * p.scale_log2 > m_run + kHeadroom);
-            if (rebase) {
-                const float mt = max_x32(max_x16(smax * p.scale_log2));
-                const float m_new = fmaxf(m_run, mt);
-                if (m_new > m_run) {
-                    alpha = fast_exp2(m_run - m_new);  // 0 when m_run = -inf
-                    l_part *= alpha;
-                    m_run = m_new;
+                    for (int i = 0; i < 4; i++) sv[mb][4 * nb + i] = acc[i];
                 }
-            }
-            const float nm = m_run == kNegInf ? 0.f : -m_run;
-            float x[8];
-            float ps = 0.f;
+            if (j == 8) MUGEN_TRACE(2);
 #pragma unroll
-            for (int jj = 0; jj < 8; jj++) {
-                x[jj] = fast_exp2(fmaf(s[jj], p.scale_log2, nm));
-                ps += x[jj];
-            }
-            l_part += ps;
-            u32x4_t pfr[NP];
-            split_p<DT, NP>(x, pfr);
-            char* pb = pbuf + (j & 1) * PB;
+            for (int mb = 0; mb < SMB; mb++) {
+                if (!hok[mb]) continue;
+                const int hs = wr * SMB + mb;
+                float* s = sv[mb];
+                // lane: query t0+n, keys kt + 8g + 4nb + i
+                if (kt + TK > mask_from) {
+                    const int key0 = kt + 8 * g;
 #pragma unroll
-            for (int pp = 0; pp < NP; pp++)
-                *reinterpret_cast<u32x4_t*>(pb + ((wr * NP + pp) * 64 + lane) * 16) = pfr[pp];
-            if (g == 0) alpha_x[j & 1][wr][n] = alpha;
-            if (lane == 0) resc_x[j & 1][wr] = rebase ? 1 : 0;
+                    for (int jj = 0; jj < 8; jj++)
+                        if (key0 + jj >= row_lim) s[jj] = kNegInf;
+                }
+                float smax = s[0];
+#pragma unroll
+                for (int jj = 1; jj < 8; jj++) smax = fmaxf(smax, s[jj]);
+                float alpha = 1.f;
+                const bool rebase = __any(smax * p.scale_log2 > m_run[mb] + kHeadroom);
+                if (rebase) {
+                    const float mt = max_x32(max_x16(smax * p.scale_log2));
+                    const float m_new = fmaxf(m_run[mb], mt);
+                    if (m_new > m_run[mb]) {
+                        alpha = fast_exp2(m_run[mb] - m_new);  // 0 when m_run = -inf
+                        l_part[mb] *= alpha;
+                        m_run[mb] = m_new;
+                    }
+                }
+                const float nm = m_run[mb] == kNegInf ? 0.f : -m_run[mb];
+                float x[8];
+                float ps = 0.f;
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++) {
+                    x[jj] = fast_exp2(fmaf(s[jj], p.scale_log2, nm));
+                    ps += x[jj];
+                }
+                l_part[mb] += ps;
+                u32x4_t pfr[NP];
+                split_p<DT, NP>(x, pfr);
+                char* pb = pbuf + (j & 1) * PB;
+#pragma unroll
+                for (int pp = 0; pp < NP; pp++)
+                    *reinterpret_cast<u32x4_t*>(pb + ((hs * NP + pp) * 64 + lane) * 16) = pfr[pp];
+                if (g == 0) alpha_x[j & 1][hs][n] = alpha;
+                if (lane == 0) resc_x[j & 1][hs] = rebase ? 1 : 0;
+            }
             if (j == 8) MUGEN_TRACE(3);
         }
-        const float l = sum_x32(sum_x16(l_part));
-        if (g == 0) linv_x[wr][n] = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+        for (int mb = 0; mb < SMB; mb++) {
+            const float l = sum_x32(sum_x16(l_part[mb]));
+            if (g == 0) linv_x[wr * SMB + mb][n] = l > 0.f ? 1.f / l : 0.f;
+        }
         __syncthreads();  // E: 1/l published
     } else {
         // ================================================== PV waves
@@ -598,14 +621,18 @@ template <int D, int DT, int OUT_DT>
 static hipError_t launch_pf_ws_t(const GqaPrefillParams& p, int Hk, hipStream_t st, KernelTimer* t) {
     const int nqb = (p.N + 15) / 16;
     if (p.G <= 4)
-        return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 4, 4, DT, OUT_DT>, dim3(nqb * Hk * ((p.G + 3) / 4)),
+        return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 4, 1, 4, DT, OUT_DT>, dim3(nqb * Hk * ((p.G + 3) / 4)),
                         dim3(64 * 8), st, p, nqb, (p.G + 3) / 4, Hk);
     const int nslice = (p.G + 7) / 8;
     // 8-head blocks keep 4 PV waves (2 heads each): 8 PV waves (one head
     // each, 16-wave blocks) measured no faster
     constexpr int NPV = 4;
-    return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 8, NPV, DT, OUT_DT>, dim3(nqb * Hk * nslice),
-                    dim3(64 * (8 + NPV)), st, p, nqb, nslice, Hk);
+    // one head per S wave (two S waves per SIMD overlap each other's MFMA
+    // and softmax phases); two heads per S wave, which halves the K reads
+    // per row, measured slower (859 against 804 us at 7B N = 8192)
+    constexpr int SMB = 1;
+    return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 8, SMB, NPV, DT, OUT_DT>, dim3(nqb * Hk * nslice),
+                    dim3(64 * (8 / SMB + NPV)), st, p, nqb, nslice, Hk);
 }
 
 template <int D, int DT>
