@@ -430,6 +430,7 @@ def main():
             GqaDecode(dev, 16, 28, 4, 128, seeded_lens(44, 16, 256, 4096), 4096, 44, "gqa_decode_qwen7b_b16"),
             GqaDecodeQ4(dev, 16, 28, 4, 128, seeded_lens(44, 16, 256, 4096), 4096, 44, "gqa_decode_q4_qwen7b_b16"),
             Prefill(dev, 512, 32, 8, 64, 46, "gqa_prefill_llama1b"),
+            Prefill(dev, 2048, 28, 4, 128, 50, "gqa_prefill_qwen7b_n2048"),
             Prefill(dev, 8192, 28, 4, 128, 49, "gqa_prefill_qwen7b_n8192"),
             MlaDecode(dev, 4, 128, 5, [32768] * 4, 32768, torch.bfloat16, torch.bfloat16, 47, "mla_verify_v3"),
             MlaFull(dev, 8, 128, seeded_lens(45, 8, 1024, 8192), 8192, "q8_0", 48, "mla_layer_v3_q8_0"),
