@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define MUGEN_ATTN_ABI_VERSION 1
+#define MUGEN_ATTN_ABI_VERSION 2
 
 /* status codes */
 #define MUGEN_ATTN_OK 0
@@ -75,7 +75,10 @@ typedef enum {
  *
  *   kv head of query head h = h / (n_heads / n_kv_heads)   (transformer.cpp:2452)
  *   scale <= 0 selects 1/sqrt(head_dim)                     (transformer.cpp:2444)
- *   max_seq_len: host-side upper bound of seq_lens (sizes the split-K grid)
+ *   max_seq_len (> 0): tokens each sequence's cache holds; sizes the split-K
+ *            grid and workspace.  Device lengths are clamped to
+ *            [0, max_seq_len], so a bad length never reads past the cache or
+ *            writes past the workspace
  *   num_splits: 0 = automatic; otherwise the context-split count (>= 1)
  *
  * Supported: head_dim in {64, 128}; n_heads / n_kv_heads in [1, 16];
@@ -220,7 +223,13 @@ typedef struct mugen_attn_gqa_prefill_args {
     float scale;
     int32_t dtype;
     int32_t out_dtype;
+    /* 0 = automatic; MUGEN_ATTN_PREFILL_KERNEL_BLOCK / _WS force one kernel
+     * (same results within rounding; for kernel comparisons) */
+    int32_t kernel;
 } mugen_attn_gqa_prefill_args;
+
+#define MUGEN_ATTN_PREFILL_KERNEL_BLOCK 1 /* one (16-token block, kv head) per workgroup */
+#define MUGEN_ATTN_PREFILL_KERNEL_WS 2    /* warp-specialised S / PV waves */
 
 int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* args, void* stream);
 
@@ -237,7 +246,8 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* args, void* stream
  *           kv_rank + rope_dim (c_kv then k_rope), the reference's
  *           buf_kv_compressed layout (transformer.cpp:3397-3407)
  *   seq_lens device int32 [batch]: cache length INCLUDING the q_len new
- *           tokens; query i sees seq_len - q_len + i + 1 tokens
+ *           tokens; query i sees seq_len - q_len + i + 1 tokens; clamped to
+ *           [0, max_seq_len] (max_seq_len > 0: the cache's rows per sequence)
  *   out     [batch][q_len][n_heads][kv_rank]  o = sum_t p_t c_t[0:kv_rank]
  *   scale   must be > 0 (the reference uses 1/sqrt(qk_nope + qk_rope),
  *           transformer.cpp:2550; 1/sqrt(192) for DeepSeek V2/V3)
@@ -268,7 +278,13 @@ typedef struct mugen_attn_mla_decode_args {
      * the device value (normally equal; a larger value only costs idle
      * workgroups).  NULL sizes the grid for batch * max_seq_len. */
     const int32_t* seq_lens_host;
+    /* 0 = automatic; MUGEN_ATTN_MLA_KERNEL_ROWS / _WS force
+     * one kernel (same results within rounding; for kernel comparisons) */
+    int32_t kernel;
 } mugen_attn_mla_decode_args;
+
+#define MUGEN_ATTN_MLA_KERNEL_ROWS 1 /* 4 waves of 16 rows (16-bit q, <= 64 rows by default) */
+#define MUGEN_ATTN_MLA_KERNEL_WS 2   /* warp-specialised S / P.L waves */
 
 size_t mugen_attn_mla_decode_workspace_size(const mugen_attn_mla_decode_args* args);
 int mugen_attn_mla_decode(const mugen_attn_mla_decode_args* args, void* workspace,

@@ -19,6 +19,8 @@ E_HIP = -4
 
 F32, F16, BF16 = 0, 1, 2
 W_F16, W_Q4_0, W_Q8_0 = 1, 2, 8  # weight encodings (GGML type ids)
+MLA_KERNEL_ROWS, MLA_KERNEL_WS = 1, 2  # mugen_attn_mla_decode_args.kernel
+PREFILL_KERNEL_BLOCK, PREFILL_KERNEL_WS = 1, 2  # mugen_attn_gqa_prefill_args.kernel
 
 # every symbol include/mugen_attn.h declares
 EXPORTS = (
@@ -92,7 +94,7 @@ class GqaPrefillArgs(ctypes.Structure):
         ("q", _vp), ("k", _vp), ("v", _vp), ("out", _vp),
         ("n_tokens", _i32), ("n_heads", _i32), ("n_kv_heads", _i32), ("head_dim", _i32),
         ("kv_len", _i32), ("start_pos", _i32), ("causal", _i32), ("scale", _f32),
-        ("dtype", _i32), ("out_dtype", _i32),
+        ("dtype", _i32), ("out_dtype", _i32), ("kernel", _i32),
     ]
 
 
@@ -102,6 +104,7 @@ class MlaDecodeArgs(ctypes.Structure):
         ("batch", _i32), ("q_len", _i32), ("n_heads", _i32), ("kv_rank", _i32), ("rope_dim", _i32),
         ("max_seq_len", _i32), ("num_splits", _i32), ("seq_stride", _i64), ("scale", _f32),
         ("q_dtype", _i32), ("latent_dtype", _i32), ("out_dtype", _i32), ("seq_lens_host", _vp),
+        ("kernel", _i32),
     ]
 
 

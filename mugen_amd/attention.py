@@ -108,9 +108,11 @@ def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
 
 def flash_prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, start_pos: int = 0, *,
                             causal: bool = True, out: torch.Tensor | None = None,
-                            out_dtype: torch.dtype | None = None, scale: float = 0.0) -> torch.Tensor:
+                            out_dtype: torch.dtype | None = None, scale: float = 0.0,
+                            kernel: int = 0) -> torch.Tensor:
     """Causal GQA prefill.  q [N,H,D]; k/v [kv_len,Hk,D] (cache incl. the new
-    tokens); token i sees keys [0, start_pos+i].  Returns out [N,H,D]."""
+    tokens); token i sees keys [0, start_pos+i].  Returns out [N,H,D].
+    kernel: 0 automatic, PREFILL_KERNEL_BLOCK / PREFILL_KERNEL_WS force one."""
     _need_cuda(q, k, v)
     N, H, D = q.shape
     kv_len, Hk, Dk = k.shape
@@ -122,14 +124,14 @@ def flash_prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, s
     a.q, a.k, a.v, a.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
     a.n_tokens, a.n_heads, a.n_kv_heads, a.head_dim = N, H, Hk, D
     a.kv_len, a.start_pos, a.causal, a.scale = kv_len, int(start_pos), 1 if causal else 0, float(scale)
-    a.dtype, a.out_dtype = _dt(q.dtype), _dt(out.dtype)
+    a.dtype, a.out_dtype, a.kernel = _dt(q.dtype), _dt(out.dtype), int(kernel)
     _capi.check(_capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), _stream(q.device)))
     return out
 
 
 # ------------------------------------------------------------------ MLA
 
-def mla_args(q, latent, seq_lens, out, max_seq_len, scale, num_splits=0):
+def mla_args(q, latent, seq_lens, out, max_seq_len, scale, num_splits=0, kernel=0):
     B, q_len, H, C = q.shape
     a = _capi.MlaDecodeArgs()
     a.q, a.latent, a.seq_lens, a.out = q.data_ptr(), latent.data_ptr(), seq_lens.data_ptr(), out.data_ptr()
@@ -138,6 +140,7 @@ def mla_args(q, latent, seq_lens, out, max_seq_len, scale, num_splits=0):
     a.seq_stride = latent[0].numel()
     a.scale = float(scale)
     a.q_dtype, a.latent_dtype, a.out_dtype = _dt(q.dtype), _dt(latent.dtype), _dt(out.dtype)
+    a.kernel = int(kernel)
     return a
 
 
@@ -145,11 +148,12 @@ def mla_attention(q: torch.Tensor, latent: torch.Tensor, seq_lens: torch.Tensor,
                   max_seq_len: int | None = None, *, scale: float = 1.0 / math.sqrt(192.0),
                   out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32,
                   num_splits: int = 0, workspace: torch.Tensor | None = None,
-                  seq_lens_host=None) -> torch.Tensor:
+                  seq_lens_host=None, kernel: int = 0) -> torch.Tensor:
     """MLA absorbed attention (decode: q_len 1; verify: q_len > 1, causal).
 
     q [B,q_len,H,576] (q_nope.W_UK ++ q_rope); latent [B,max_T,576];
     seq_lens int32 [B] = cache length incl. the q_len new tokens.
+    kernel: 0 automatic, MLA_KERNEL_ROWS / MLA_KERNEL_WS force one.
     Returns out [B,q_len,H,512]."""
     _need_cuda(q, latent, seq_lens)
     if q.dim() != 4 or latent.dim() != 3 or latent.shape[-1] != q.shape[-1]:
@@ -161,7 +165,7 @@ def mla_attention(q: torch.Tensor, latent: torch.Tensor, seq_lens: torch.Tensor,
     B, q_len, H, _ = q.shape
     if out is None:
         out = torch.empty((B, q_len, H, 512), dtype=out_dtype, device=q.device)
-    a = mla_args(q, latent, seq_lens, out, max_seq_len, scale, num_splits)
+    a = mla_args(q, latent, seq_lens, out, max_seq_len, scale, num_splits, kernel)
     hl = _host_lens(seq_lens_host)
     if hl is not None:
         a.seq_lens_host = hl.ctypes.data

@@ -128,15 +128,6 @@ static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b)
 static bool is16(int dt) { return dt == DT_F16 || dt == DT_BF16; }
 static bool is_out(int dt) { return dt == DT_F32 || dt == DT_F16 || dt == DT_BF16; }
 
-// Token count the planner balances: the sum of the host hint when given,
-// else batch * max_seq_len.
-static int64_t planned_tokens(const int32_t* host_lens, int batch, int max_seq_len) {
-    if (!host_lens) return (int64_t)batch * (max_seq_len > 0 ? max_seq_len : 1);
-    int64_t t = 0;
-    for (int b = 0; b < batch; b++) t += host_lens[b] > 0 ? host_lens[b] : 0;
-    return t > 0 ? t : 1;
-}
-
 // Tokens per split for a workgroup count target; rounded to `quantum`, and
 // large enough that no more than kMaxSplits splits cover max_seq_len.
 static int plan_chunk(int64_t tokens_x_groups, int target_wgs, int quantum, int max_seq_len,
@@ -171,8 +162,10 @@ static int64_t gqa_items(const mugen_attn_gqa_decode_args* a, int chunk, int ext
     if (!a->seq_lens_host) {
         n = (int64_t)a->batch * (ceil_div(maxT, chunk) + extra);
     } else {
-        for (int b = 0; b < a->batch; b++)
-            n += a->seq_lens_host[b] > 0 ? ceil_div(a->seq_lens_host[b], chunk) + extra : 1;
+        for (int b = 0; b < a->batch; b++) {
+            const int T = std::min(a->seq_lens_host[b], maxT);  // the kernels clamp to max_seq_len too
+            n += T > 0 ? ceil_div(T, chunk) + extra : 1;
+        }
     }
     return n * a->n_kv_heads;
 }
@@ -205,8 +198,8 @@ static int gqa_validate(const mugen_attn_gqa_decode_args* a, bool ring_store = f
     if (!a) return fail(MUGEN_ATTN_E_INVALID, "gqa_decode: null args");
     if (!a->q || !a->k_cache || !a->v_cache || !a->seq_lens || !a->out)
         return fail(MUGEN_ATTN_E_INVALID, "gqa_decode: null tensor pointer");
-    if (a->batch <= 0 || a->n_heads <= 0 || a->n_kv_heads <= 0 || a->max_seq_len < 0 || a->num_splits < 0)
-        return fail(MUGEN_ATTN_E_INVALID, "gqa_decode: batch/heads must be > 0, max_seq_len/num_splits >= 0");
+    if (a->batch <= 0 || a->n_heads <= 0 || a->n_kv_heads <= 0 || a->max_seq_len <= 0 || a->num_splits < 0)
+        return fail(MUGEN_ATTN_E_INVALID, "gqa_decode: batch/heads/max_seq_len must be > 0, num_splits >= 0");
     if (a->n_heads % a->n_kv_heads)
         return fail(MUGEN_ATTN_E_INVALID, "gqa_decode: n_heads %d not a multiple of n_kv_heads %d", a->n_heads,
                     a->n_kv_heads);
@@ -237,19 +230,14 @@ static size_t gqa_ws(const mugen_attn_gqa_decode_args* a, int chunk, int* splits
     return slots * (size_t)a->head_dim * 4 + slots * 2 * 4 + 256;
 }
 
-// MLA kernel variant (mla_decode.hip): fp32 q or at most 64 query rows ->
-// 1 (64-row workgroups, 16 rows per wave); otherwise 5 (warp-specialised,
-// two waves per SIMD), which measures faster than the one-wave-per-SIMD
-// variants for both decode and verify.  MUGEN_ATTN_MLA_VARIANT=1..5
-// overrides the choice (kernel comparisons); variants 2-5 need 16-bit q.
-static int mla_variant(const mugen_attn_mla_decode_args* a) {
+// MLA kernel (mla_decode.hip): 16-bit q with at most 64 query rows -> the
+// "rows" kernel (4 waves of 16 rows, one per SIMD); everything else -> the
+// warp-specialised kernel (two waves per SIMD), which measures faster for
+// fp32 q and for the wide decode / verify shapes.  args->kernel forces one.
+static int mla_kernel(const mugen_attn_mla_decode_args* a) {
+    if (a->kernel == MUGEN_ATTN_MLA_KERNEL_ROWS || a->kernel == MUGEN_ATTN_MLA_KERNEL_WS) return a->kernel;
     const int R = a->q_len * a->n_heads;
-    const int dflt = (R <= 64 && a->q_dtype != DT_F32) ? 1 : 5;
-    if (const char* e = getenv("MUGEN_ATTN_MLA_VARIANT")) {
-        const int v = atoi(e);
-        if (v == 1 || v == 5 || (v >= 2 && v <= 4 && a->q_dtype != DT_F32)) return v;
-    }
-    return dflt;
+    return (R <= 64 && a->q_dtype != DT_F32) ? MUGEN_ATTN_MLA_KERNEL_ROWS : MUGEN_ATTN_MLA_KERNEL_WS;
 }
 
 // Active (sequence, split) groups for a chunk: exact from the host length
@@ -257,7 +245,10 @@ static int mla_variant(const mugen_attn_mla_decode_args* a) {
 static int64_t mla_groups(const mugen_attn_mla_decode_args* a, int chunk) {
     if (!a->seq_lens_host) return (int64_t)a->batch * ceil_div(a->max_seq_len > 0 ? a->max_seq_len : 1, chunk);
     int64_t g = 0;
-    for (int b = 0; b < a->batch; b++) g += a->seq_lens_host[b] > 0 ? ceil_div(a->seq_lens_host[b], chunk) : 0;
+    for (int b = 0; b < a->batch; b++) {
+        const int T = std::min(a->seq_lens_host[b], a->max_seq_len);  // the kernels clamp to max_seq_len too
+        g += T > 0 ? ceil_div(T, chunk) : 0;
+    }
     return g;
 }
 
@@ -266,11 +257,11 @@ static int64_t mla_groups(const mugen_attn_mla_decode_args* a, int chunk) {
 // ring fill, partial store) on top of ~1.8 us per 32-token tile.  The plan:
 // the smallest chunk (multiple of 32) whose nrb * active groups fit ONE
 // dispatch round of 256 CUs -- maximum parallelism, no second round.
-static int mla_chunk(const mugen_attn_mla_decode_args* a, int variant) {
-    const int q = mla_tile_tokens(variant);  // chunks are whole tiles
+static int mla_chunk(const mugen_attn_mla_decode_args* a, int kernel) {
+    const int q = mla_tile_tokens(kernel);  // chunks are whole tiles
     if (a->num_splits > 0) return explicit_chunk(a->max_seq_len, a->num_splits, q, kMaxMlaSplits);
     const int R = a->q_len * a->n_heads;
-    const int64_t nrb = ceil_div(R, mla_rows_per_block(variant));
+    const int64_t nrb = ceil_div(R, mla_rows_per_block(kernel));
     const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
     const int cmax = ceil_div(maxT, q) * q;
     const int cmin = ceil_div(ceil_div(maxT, kMaxMlaSplits), q) * q;
@@ -291,8 +282,8 @@ static int mla_validate(const mugen_attn_mla_decode_args* a) {
     if (!a) return fail(MUGEN_ATTN_E_INVALID, "mla_decode: null args");
     if (!a->q || !a->latent || !a->seq_lens || !a->out)
         return fail(MUGEN_ATTN_E_INVALID, "mla_decode: null tensor pointer");
-    if (a->batch <= 0 || a->q_len <= 0 || a->n_heads <= 0 || a->max_seq_len < 0 || a->num_splits < 0)
-        return fail(MUGEN_ATTN_E_INVALID, "mla_decode: batch/q_len/n_heads must be > 0");
+    if (a->batch <= 0 || a->q_len <= 0 || a->n_heads <= 0 || a->max_seq_len <= 0 || a->num_splits < 0)
+        return fail(MUGEN_ATTN_E_INVALID, "mla_decode: batch/q_len/n_heads/max_seq_len must be > 0");
     if (a->kv_rank != 512 || a->rope_dim != 64)
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_decode: kv_rank %d / rope_dim %d (supported: 512 / 64)",
                     a->kv_rank, a->rope_dim);
@@ -310,6 +301,8 @@ static int mla_validate(const mugen_attn_mla_decode_args* a) {
         return fail(MUGEN_ATTN_E_INVALID, "mla_decode: seq_stride must be a multiple of 8 elements");
     if ((int64_t)a->q_len * a->n_heads > (1 << 20))
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_decode: q_len*n_heads too large");
+    if (a->kernel < 0 || a->kernel > MUGEN_ATTN_MLA_KERNEL_WS)
+        return fail(MUGEN_ATTN_E_INVALID, "mla_decode: kernel %d (0 auto, 1 rows, 2 warp-specialised)", a->kernel);
     return MUGEN_ATTN_OK;
 }
 
@@ -336,7 +329,7 @@ extern "C" {
 
 const char* mugen_attn_last_error(void) { return g_last_error.c_str(); }
 
-const char* mugen_attn_version(void) { return "mugen_attn 0.1.0 (gfx950, abi 1)"; }
+const char* mugen_attn_version(void) { return "mugen_attn 0.2.0 (gfx950, abi 2)"; }
 
 // ------------------------------------------------------------------ 4-bit store
 
@@ -470,6 +463,7 @@ int mugen_attn_gqa_decode_q4(const mugen_attn_gqa_decode_q4_args* a, void* ws, s
     p.q4_seq_stride = a->store.q4_seq_stride;
     p.q4_row_bytes = a->n_kv_heads * a->head_dim / 32 * 20;
     p.ring = a->store.ring;
+    p.max_T = a->max_seq_len;
     {
         float* base = align256(ws);
         const size_t slots = (size_t)a->batch * a->n_heads * splits;
@@ -514,6 +508,7 @@ int mugen_attn_gqa_decode(const mugen_attn_gqa_decode_args* a, void* ws, size_t 
     p.seq_stride = a->seq_stride;
     const float scale = a->scale > 0.f ? a->scale : 1.f / sqrtf((float)a->head_dim);
     p.scale_log2 = scale * kLog2e;
+    p.max_T = a->max_seq_len;
     if (splits > 1) {
         float* base = align256(ws);
         const size_t slots = (size_t)a->batch * a->n_heads * splits;
@@ -538,6 +533,8 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     if (a->head_dim != 64 && a->head_dim != 128)
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: head_dim %d (supported: 64, 128)", a->head_dim);
     if (!is16(a->dtype) || !is_out(a->out_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: dtype");
+    if (a->kernel < 0 || a->kernel > MUGEN_ATTN_PREFILL_KERNEL_WS)
+        return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: kernel %d (0 auto, 1 per-block, 2 warp-specialised)", a->kernel);
     if (((uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->v | (uintptr_t)a->out) & 15)
         return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: q/k/v/out must be 16-byte aligned");
     if (a->n_tokens == 0) return MUGEN_ATTN_OK;
@@ -562,25 +559,26 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     const float scale = a->scale > 0.f ? a->scale : 1.f / sqrtf((float)a->head_dim);
     p.scale_log2 = scale * kLog2e;
     // the warp-specialised kernel where it measured faster: 1024..4096-token
-    // prompts (at 512 tokens and at 8192 the per-block kernel is ahead)
-    int variant = (a->n_tokens >= 1024 && a->n_tokens <= 4096) ? 2 : 1;
-    if (const char* e = getenv("MUGEN_ATTN_PREFILL_VARIANT")) variant = atoi(e) == 2 ? 2 : 1;
-    hipError_t e = launch_gqa_prefill(p, a->n_kv_heads, a->head_dim, a->dtype, a->out_dtype, variant,
+    // prompts (at 512 tokens and at 8192 the per-block kernel is ahead);
+    // args->kernel forces one
+    int kernel = (a->n_tokens >= 1024 && a->n_tokens <= 4096) ? MUGEN_ATTN_PREFILL_KERNEL_WS
+                                                               : MUGEN_ATTN_PREFILL_KERNEL_BLOCK;
+    if (a->kernel == MUGEN_ATTN_PREFILL_KERNEL_BLOCK || a->kernel == MUGEN_ATTN_PREFILL_KERNEL_WS) kernel = a->kernel;
+    hipError_t e = launch_gqa_prefill(p, a->n_kv_heads, a->head_dim, a->dtype, a->out_dtype, kernel,
                                       static_cast<hipStream_t>(stream), active_timer());
     return hip_status(e, "gqa_prefill launch");
 }
 
 size_t mugen_attn_mla_decode_workspace_size(const mugen_attn_mla_decode_args* a) {
     if (mla_validate(a) != MUGEN_ATTN_OK) return 0;
-    const int v = mla_variant(a);
-    return mla_ws(a, mla_chunk(a, v), nullptr);
+    return mla_ws(a, mla_chunk(a, mla_kernel(a)), nullptr);
 }
 
 int mugen_attn_mla_decode(const mugen_attn_mla_decode_args* a, void* ws, size_t ws_bytes, void* stream) {
     int rc = mla_validate(a);
     if (rc) return rc;
-    const int variant = mla_variant(a);
-    const int chunk = mla_chunk(a, variant);
+    const int kernel = mla_kernel(a);
+    const int chunk = mla_chunk(a, kernel);
     int splits = 1;
     const size_t need = mla_ws(a, chunk, &splits);
     if (!ws || ws_bytes < need)
@@ -595,11 +593,12 @@ int mugen_attn_mla_decode(const mugen_attn_mla_decode_args* a, void* ws, size_t 
     p.H = a->n_heads;
     p.B = a->batch;
     p.R = a->q_len * a->n_heads;
-    p.nrb = ceil_div(p.R, mla_rows_per_block(variant));
+    p.nrb = ceil_div(p.R, mla_rows_per_block(kernel));
     p.nq = ceil_div(p.R, 16);
     p.groups = (int)mla_groups(a, chunk);
     p.chunk = chunk;
     p.num_splits = splits;
+    p.max_T = a->max_seq_len;
     p.seq_stride = a->seq_stride;
     p.scale_log2 = a->scale * kLog2e;
     {
@@ -608,7 +607,7 @@ int mugen_attn_mla_decode(const mugen_attn_mla_decode_args* a, void* ws, size_t 
         p.ws_o = base;
         p.ws_ml = base + sb * (size_t)p.nq * 16 * 512 / 2;  // after the fp16 O blob
     }
-    hipError_t e = launch_mla_decode(p, variant, a->q_dtype, a->latent_dtype, a->out_dtype,
+    hipError_t e = launch_mla_decode(p, kernel, a->q_dtype, a->latent_dtype, a->out_dtype,
                                      static_cast<hipStream_t>(stream), active_timer());
     return hip_status(e, "mla_decode launch");
 }

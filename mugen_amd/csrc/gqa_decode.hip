@@ -71,7 +71,7 @@ __device__ __forceinline__ u32x4_t dequant_q4x8(uint32_t sm, uint32_t nib) {
 // ring tokens (at least one)
 template <bool Q4>
 __device__ __forceinline__ int splits_of(const GqaDecodeParams& p, int j) {
-    const int Tj = p.seq_lens[j];
+    const int Tj = clamp_len(p.seq_lens[j], p.max_T);
     if constexpr (Q4) {
         const int nqj = min(p.n_q4[j], max(Tj, 0));
         const int n = (nqj + p.chunk - 1) / p.chunk + (max(Tj - nqj, 0) + p.chunk - 1) / p.chunk;
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     if (b < 0) return;  // grid padding (sized from an upper bound)
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
-    const int T = p.seq_lens[b];
+    const int T = clamp_len(p.seq_lens[b], p.max_T);
     // 4-bit store: the Q4 tokens [0, n_q4) and the f16 ring tokens
     // [n_q4, T) are split separately, so a split -- and every 32-token block
     // of it -- holds one kind only (Q4 splits first)
@@ -406,7 +406,7 @@ __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p
     __shared__ float red_lds[4];
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     MUGEN_TRACE(8);
-    const int T = p.seq_lens[b];
+    const int T = clamp_len(p.seq_lens[b], p.max_T);
     const int nact = p.n_q4 ? min(p.num_splits, T > 0 ? splits_of<true>(p, b) : 0)
                             : min(p.num_splits, (T + p.chunk - 1) / p.chunk);
     const int64_t bh = (int64_t)b * p.H + h;

@@ -60,6 +60,7 @@ struct GqaDecodeParams {
     int q4_row_bytes;       // bytes per token (Hk * D / 32 groups of 20)
     int ring;
     int per_xcd;            // 4-bit store: work items per XCD (0: blockIdx order)
+    int max_T;              // device lengths are clamped to [0, max_T] (the caches' size)
 };
 
 // nwg: workgroups of the compact work list (exact, or an upper bound)
@@ -103,9 +104,10 @@ struct GqaPrefillParams {
     float scale_log2;
 };
 
-// variant 1: one (query block, kv head) per workgroup, every wave doing S,
-// softmax and PV; 2: warp-specialised S / PV waves (long prompts)
-hipError_t launch_gqa_prefill(const GqaPrefillParams& p, int Hk, int D, int dt, int out_dt, int variant,
+// kernel 1 (MUGEN_ATTN_PREFILL_KERNEL_BLOCK): one (query block, kv head) per
+// workgroup, every wave doing S, softmax and PV; 2 (_WS): warp-specialised
+// S / PV waves
+hipError_t launch_gqa_prefill(const GqaPrefillParams& p, int Hk, int D, int dt, int out_dt, int kernel,
                               hipStream_t st, KernelTimer* t);
 
 struct MlaParams {
@@ -124,14 +126,21 @@ struct MlaParams {
     int groups;            // active (sequence, split) groups the grid covers (upper bound)
     int chunk;
     int num_splits;
+    int max_T;             // device lengths are clamped to [0, max_T] (the cache's size)
     int64_t seq_stride;
     float scale_log2;
 };
 
-// query rows of one MLA workgroup, and tokens per LDS tile, of a variant (1..3)
-int mla_rows_per_block(int variant);
-int mla_tile_tokens(int variant);
-hipError_t launch_mla_decode(const MlaParams& p, int variant, int q_dt, int lat_dt, int out_dt,
+// every kernel reads a sequence's length through this clamp: a device value
+// past the cache (or negative) never indexes outside the cache or the
+// workspace that the host sized from max_T
+__device__ __forceinline__ int clamp_len(int t, int max_T) { return min(max(t, 0), max_T); }
+
+// query rows of one MLA workgroup, and tokens per LDS tile, of a kernel
+// (MUGEN_ATTN_MLA_KERNEL_ROWS or _WS)
+int mla_rows_per_block(int kernel);
+int mla_tile_tokens(int kernel);
+hipError_t launch_mla_decode(const MlaParams& p, int kernel, int q_dt, int lat_dt, int out_dt,
                              hipStream_t st, KernelTimer* t);
 
 // MLA absorption / up-projection (mla_proj.hip)

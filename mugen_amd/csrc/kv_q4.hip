@@ -75,9 +75,12 @@ __device__ __forceinline__ void quantize_group32(const uint16_t* src, uint8_t* d
 
 __global__ __launch_bounds__(64) void kv_q4_append_kernel(KvQ4AppendParams p) {
     const int b = blockIdx.y, job = blockIdx.x, lane = threadIdx.x;
-    const int T = p.seq_lens[b], nq = p.n_q4[b];
+    // lengths clamped to the store: a device value past max_seq_len (or
+    // negative) never indexes outside it
+    const int T = clamp_len(p.seq_lens[b], p.max_seq_len), nq = clamp_len(p.n_q4[b], T);
     const int q = max(0, T - nq + p.n_new - p.preserve);
-    if (job == 0 && lane == 0) p.n_q4_out[b] = nq + q;
+    // tokens at positions >= max_seq_len are dropped, so they are not counted
+    if (job == 0 && lane == 0) p.n_q4_out[b] = min(nq + q, p.max_seq_len);
     const uint16_t* knew = p.k_new + (int64_t)b * p.n_new * p.vpt;
     const uint16_t* vnew = p.v_new + (int64_t)b * p.n_new * p.vpt;
     uint16_t* rk = p.ring_k + (int64_t)b * p.ring_seq_stride;

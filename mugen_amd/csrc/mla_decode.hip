@@ -10,15 +10,11 @@
 // Design: all heads share one latent row, so attention is a pair of dense
 // contractions, S = Q[rows x 576] . L^T and O = P . L[:, 0:512], run on
 // MFMA 16x16x32 (bf16 or fp16 in, fp32 accumulate):
-//  * workgroup = (block of 64*MB query rows, context split, sequence); 4
-//    waves, each owning 16*MB rows.  MB = 2 (32 rows per wave) halves the
-//    LDS bytes per MFMA flop versus 16 rows: every latent fragment read from
-//    LDS feeds two MFMAs.  Q of the wave's rows stays in VGPRs (B operand of
-//    S^T = L . Q^T); O[rows x 512] is accumulated in AGPRs;
-//  * the S MFMAs are issued from inline asm with VGPR accumulators so that
-//    the 256-register O accumulator alone owns the AGPR file (the compiler
-//    would otherwise put both in AGPRs and spill);
-//  * latent tiles of 32 tokens stream into a 3-deep LDS ring by direct
+//  * workgroup = (64 query rows, context split, sequence).  Two kernels:
+//    "rows" (mla_decode_kernel: 4 waves of 16 rows, each doing S, softmax
+//    and P.L for its rows; small 16-bit-q problems) and the warp-specialised
+//    mla_decode_ws_kernel (S waves and P.L waves, everything else);
+//  * latent tiles of 32 tokens stream into an LDS ring by direct
 //    global->LDS DMA (global_load_lds_dwordx4), two tiles in flight; rows
 //    are XOR-swizzled in 16-byte chunks so both MFMA operand reads are
 //    bank-conflict free;
@@ -101,29 +97,21 @@ __device__ __forceinline__ void mfma_s(f32x4_t& acc, const u32x4_t& a, const u32
     }
 }
 
-template <int MB, int TS, int NW, int QDT, int DT>
-__global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
+// Kernel "rows" (16-bit q, at most 64 query rows: small-head decode):
+// workgroup = (64 query rows, context split, sequence), 4 waves of 16
+// rows, one wave per SIMD.  Each wave keeps the q of its rows in VGPRs (B
+// operand of S^T = L . Q^T) and its 16 x 512 O in AGPRs; the S MFMAs are
+// issued from inline asm with VGPR accumulators so that the O accumulator
+// alone owns the AGPR file.
+template <int QDT, int DT>
+__global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     constexpr int KS = kCD / 32;  // 18 k-steps over the 576 dims
     constexpr int NQ = (QDT == DT_F32) ? 2 : 1;
     constexpr float TH = headroom_log2<DT>();
-    // TS = 1: the 4 waves split the rows of a 32-token tile (3-deep ring).
-    // TS = 2: 64-token tiles (2-deep ring); wave w takes rows of group w%2
-    // and the 32-token half w/2 of every tile, and the two halves of a row
-    // group are merged at the end -- half the rows per workgroup for the
-    // same MFMA work, so half the split partials and query loads.
-    constexpr int TILE_T = kTT * TS;                 // tokens per tile
-    constexpr int TILE_B = TILE_T * kRowBytes;       // bytes per tile
-    constexpr int NBUF = TS == 1 ? kNBuf : 2;        // ring depth
-    // NW = 4: one wave per SIMD (up to 512 registers per lane).  NW = 8
-    // (MB = 1): two waves per SIMD within 256 registers, so one wave's
-    // softmax, barrier and LDS waits overlap the other's MFMAs; a single
-    // wave cannot issue 16x16x32 MFMAs faster than about one per 18 clocks,
-    // two waves sharing a SIMD reach about one per 10.
-    static_assert(NW == 4 || (NW == 8 && MB == 1), "8-wave variant holds 16 rows per wave");
-    constexpr int DPW = kDmaPerTile * TS / NW;       // 1-KiB DMA ops per wave per tile
-    constexpr int RG = NW / TS;                      // row groups (waves per token slice)
-    constexpr int DSTRIDE = NW * 1024;               // LDS bytes between a wave's DMA ops
-    __shared__ __attribute__((aligned(1024))) char ring[NBUF * TILE_B];
+    constexpr int NW = 4;                      // waves, one per SIMD
+    constexpr int DPW = kDmaPerTile / NW;      // 1-KiB DMA ops per wave per tile
+    constexpr int DSTRIDE = NW * 1024;         // LDS bytes between a wave's DMA ops
+    __shared__ __attribute__((aligned(1024))) char ring[kNBuf * kTileBytes];
 
     // XCD-aware work mapping.  Workgroups are dealt to the 8 XCDs round-robin
     // by blockIdx.  A group = the nrb row blocks of one (sequence, split);
@@ -140,14 +128,14 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
     const int nrb = p.nrb;
     const int rb = slot % nrb;
     int nact = 0;
-    for (int j = 0; j < p.B; j++) nact += (p.seq_lens[j] + p.chunk - 1) / p.chunk;  // uniform scalar loop
+    for (int j = 0; j < p.B; j++) nact += (clamp_len(p.seq_lens[j], p.max_T) + p.chunk - 1) / p.chunk;  // uniform scalar loop
     const int gpx = (nact + nxcd - 1) / nxcd;
     const int gi = slot / nrb;
     const int grp = xcd * gpx + gi;  // active (sequence, split) group
     int b = -1, s = 0;
     if (gi < gpx) {
         for (int j = 0, acc = 0; j < p.B; j++) {
-            const int nsj = (p.seq_lens[j] + p.chunk - 1) / p.chunk;
+            const int nsj = (clamp_len(p.seq_lens[j], p.max_T) + p.chunk - 1) / p.chunk;
             if (grp < acc + nsj) {
                 b = j;
                 s = grp - acc;
@@ -163,13 +151,11 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int n = lane & 15, g = lane >> 4;
-    const int T = p.seq_lens[b];
+    const int T = clamp_len(p.seq_lens[b], p.max_T);
     const int t_begin = s * p.chunk;
     const int t_end = min(t_begin + p.chunk, T);
-    const int ntiles = (t_end - t_begin + TILE_T - 1) / TILE_T;
-
-    const int rg = w % RG, th = w / RG;  // row group, token slice of each tile
-    const int row0 = rb * (RG * 16 * MB) + rg * (16 * MB);
+    const int ntiles = (t_end - t_begin + kTT - 1) / kTT;
+    const int row0 = rb * 64 + w * 16;
     const uint16_t* lat = p.lat + (int64_t)b * p.seq_stride;
 
     // ---- tile staging by LDS DMA: wave w fills LDS chunks [64K, 64K+64) of
@@ -177,73 +163,38 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
     // (r, pc ^ swz(r)).  Offsets are clamped to the split's last valid byte,
     // so tokens past t_end read valid cache rows (masked later)
     const uint32_t ring_base = lds_addr(&ring[0]);
-    auto dma_offset = [&](int k) {
-        int ln = lane;
-        if constexpr (NW == 8) asm volatile("" : "+v"(ln));  // opaque: recomputed at each use, never hoisted and spilled
-        const int slot = 64 * (w + NW * k) + ln;
-        const int r = slot / (kRowBytes / 16), pc = slot - r * (kRowBytes / 16);
-        return (uint32_t)(r * kRowBytes + ((pc ^ swz(r)) * 16));
-    };
-    // NW = 4 keeps the offsets in registers; the 8-wave variant, at 256
-    // registers per lane, recomputes them at each DMA (a few VALU ops)
-    constexpr int NOFF = NW == 4 ? DPW : 1;
-    uint32_t dma_off_r[NOFF];
+    uint32_t dma_off[DPW];
 #pragma unroll
-    for (int k = 0; k < NOFF; k++) dma_off_r[k] = dma_offset(k);
-    auto dma_off = [&](int k) { return NW == 4 ? dma_off_r[k < NOFF ? k : 0] : dma_offset(k); };
+    for (int k = 0; k < DPW; k++) {
+        const int sl = 64 * (w + NW * k) + lane;
+        const int r = sl / (kRowBytes / 16), pc = sl - r * (kRowBytes / 16);
+        dma_off[k] = (uint32_t)(r * kRowBytes + ((pc ^ swz(r)) * 16));
+    }
     auto issue = [&](int tt, int buf) {
         const uint16_t* tbase = lat + (int64_t)tt * kCD;  // wave-uniform
-        const uint32_t lds0 = ring_base + buf * TILE_B + w * 1024;
-        if (tt + TILE_T <= t_end) {  // whole tile valid: precomputed offsets
+        const uint32_t lds0 = ring_base + buf * kTileBytes + w * 1024;
+        if (tt + kTT <= t_end) {  // whole tile valid: precomputed offsets
 #pragma unroll
-            for (int k = 0; k < DPW; k++) dma16s(lds0 + k * DSTRIDE, tbase, dma_off(k));
+            for (int k = 0; k < DPW; k++) dma16s(lds0 + k * DSTRIDE, tbase, dma_off[k]);
         } else {  // last tile of the split: clamp to its last valid chunk
             const uint32_t lim = (uint32_t)(t_end - tt) * kRowBytes - 16;
 #pragma unroll
-            for (int k = 0; k < DPW; k++) dma16s(lds0 + k * DSTRIDE, tbase, min(dma_off(k), lim));
+            for (int k = 0; k < DPW; k++) dma16s(lds0 + k * DSTRIDE, tbase, min(dma_off[k], lim));
         }
     };
 
-    // ---- Q^T fragments (B operand): lane holds Q[row0+16mb+n][32ks+8g .. +8]
-    u32x4_t qf[MB][NQ][KS];
-    int teff[MB];  // visible tokens of this lane's S-row
-    if constexpr (TS == 2) {
-        // the workgroup's 64 query rows (contiguous in q) arrive by LDS DMA
-        // in ring buffer 1, laid out and swizzled like latent rows, ahead of
-        // tile 0; both token slices of a row group then read them from LDS
-        static_assert(TS == 1 || QDT != DT_F32, "token-sliced variant takes 16-bit q");
-        const uint16_t* qrows = static_cast<const uint16_t*>(p.q) + ((int64_t)b * p.R + rb * 64) * kCD;
-        const uint32_t qlim = (uint32_t)min(64, p.R - rb * 64) * kRowBytes - 16;
-        const uint32_t q_lds = ring_base + TILE_B + w * 1024;
-#pragma unroll
-        for (int k = 0; k < DPW; k++) dma16s(q_lds + k * DSTRIDE, qrows, min(dma_off(k), qlim));
-        issue(t_begin, 0);
-        vm_wait<DPW>();  // the query rows landed (tile 0 may still fly)
-        lds_barrier();
-        const char* qt = &ring[TILE_B];
-#pragma unroll
-        for (int mb = 0; mb < MB; mb++) {
-            const int r = rg * 16 * MB + 16 * mb + n, row = rb * 64 + r;
-            const bool ok = row < p.R;
-            teff[mb] = ok ? (T - p.q_len + row / p.H + 1) : T;
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-                const u32x4_t v = *reinterpret_cast<const u32x4_t*>(qt + r * kRowBytes + (((4 * ks + g) ^ swz(r)) * 16));
-                qf[mb][0][ks] = ok ? v : u32x4_t{0, 0, 0, 0};
-            }
-        }
-    } else {
-    // the first tiles' DMA goes out before the q loads: both latencies overlap
+    // ---- Q^T fragments (B operand): lane holds Q[row0+n][32ks+8g .. +8].
+    // The first tiles' DMA goes out before the q loads: both latencies overlap
     issue(t_begin, 0);
-    if (ntiles > 1) issue(t_begin + TILE_T, 1);
-#pragma unroll
-    for (int mb = 0; mb < MB; mb++) {
-        const int row = row0 + 16 * mb + n;
-        const bool ok = row < p.R;
-        // rows past R (padding of the last row block) have q = 0 and are
-        // treated as visible everywhere; their output is never stored
-        teff[mb] = ok ? (T - p.q_len + row / p.H + 1) : T;
-        const int64_t qoff = ((int64_t)b * p.R + (ok ? row : 0)) * kCD + 8 * g;
+    if (ntiles > 1) issue(t_begin + kTT, 1);
+    u32x4_t qf[NQ][KS];
+    const int row = row0 + n;
+    const bool row_ok = row < p.R;
+    // rows past R (padding of the last row block) have q = 0 and are
+    // treated as visible everywhere; their output is never stored
+    const int teff = row_ok ? (T - p.q_len + row / p.H + 1) : T;  // visible tokens of this lane's S-row
+    {
+        const int64_t qoff = ((int64_t)b * p.R + (row_ok ? row : 0)) * kCD + 8 * g;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
             if constexpr (QDT == DT_F32) {
@@ -254,26 +205,22 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
                 float x[8];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    x[j] = ok ? q0[j] : 0.f;
-                    x[4 + j] = ok ? q1[j] : 0.f;
+                    x[j] = row_ok ? q0[j] : 0.f;
+                    x[4 + j] = row_ok ? q1[j] : 0.f;
                 }
                 // hi = RNE 16-bit pack of the pair, lo = RNE pack of the residual
                 u32x4_t fr[2];
                 split_p<DT, 2>(x, fr);
-                qf[mb][0][ks] = fr[0];
-                qf[mb][NQ - 1][ks] = fr[1];
+                qf[0][ks] = fr[0];
+                qf[NQ - 1][ks] = fr[1];
             } else {
                 const uint16_t* qp = static_cast<const uint16_t*>(p.q) + qoff + 32 * ks;
-                qf[mb][0][ks] = ok ? load16(qp) : u32x4_t{0, 0, 0, 0};
+                qf[0][ks] = row_ok ? load16(qp) : u32x4_t{0, 0, 0, 0};
             }
         }
     }
-    }
-
     // smallest visible length over the wave's rows: tiles below it need no mask
-    int teff_min = teff[0];
-#pragma unroll
-    for (int mb = 1; mb < MB; mb++) teff_min = min(teff_min, teff[mb]);
+    int teff_min = teff;
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) teff_min = min(teff_min, __shfl_xor(teff_min, m, 64));
 
@@ -298,47 +245,37 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
     for (int j = 0; j < 4; j++)
         t_off[j] = tr0 * kRowBytes + (((2 * j + ((n & 3) >> 1)) ^ hT) * 16) + 8 * (n & 1);
 
-    f32x4_t o[MB][32];
-    float m_ref[MB], l_part[MB];  // reference max (log2 units) and partial sum
+    f32x4_t o[32];
+    float m_ref = kNegInf, l_part = 0.f;  // reference max (log2 units) and partial sum
 #pragma unroll
-    for (int mb = 0; mb < MB; mb++) {
-        m_ref[mb] = kNegInf;
-        l_part[mb] = 0.f;
-#pragma unroll
-        for (int d = 0; d < 32; d++) o[mb][d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int d = 0; d < 32; d++) o[d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     const char* ring_bytes = &ring[0];
     int buf = 0;  // (tiles 0 and 1 were issued with the query loads)
     for (int it = 0; it < ntiles; it++) {
-        if (it == 2) MUGEN_TRACE(6);
-        if (NBUF > 2 && it + 1 < ntiles) vm_wait<DPW>();
+        if (it + 1 < ntiles) vm_wait<DPW>();
         else vm_wait<0>();
         lds_barrier();  // tile `it` landed for every wave; the buffer of tile it-1 is free
-        if (it == 0) MUGEN_TRACE(2);
-        if (it == 2) MUGEN_TRACE(7);
-        if (it == 2) MUGEN_TRACE_CLK(14);
         // the next tile's DMA goes into the buffer freed by the barrier; its
         // DPW instructions are spread over the S k-steps below, so the
         // per-CU address unit works through them while the MFMAs run
         // instead of holding up the wave's first MFMA behind all of them
-        const bool pf = it + NBUF - 1 < ntiles;
-        const int pf_tt = t_begin + TILE_T * (it + NBUF - 1);
+        const bool pf = it + kNBuf - 1 < ntiles;
+        const int pf_tt = t_begin + kTT * (it + kNBuf - 1);
         const uint16_t* pf_src = lat + (int64_t)pf_tt * kCD;  // wave-uniform
-        const uint32_t pf_lds = ring_base + (buf == 0 ? NBUF - 1 : buf - 1) * TILE_B + w * 1024;
-        const uint32_t pf_lim = pf_tt + TILE_T <= t_end ? 0xFFFFFFFFu : (uint32_t)(t_end - pf_tt) * kRowBytes - 16;
+        const uint32_t pf_lds = ring_base + (buf == 0 ? kNBuf - 1 : buf - 1) * kTileBytes + w * 1024;
+        const uint32_t pf_lim = pf_tt + kTT <= t_end ? 0xFFFFFFFFu : (uint32_t)(t_end - pf_tt) * kRowBytes - 16;
         auto issue_k = [&](int k) {
-            if (pf) dma16s(pf_lds + k * DSTRIDE, pf_src, min(dma_off(k), pf_lim));
+            if (pf) dma16s(pf_lds + k * DSTRIDE, pf_src, min(dma_off[k], pf_lim));
         };
-        // this wave's 32-token slice of the tile (same swizzle: it ignores row bit 5)
-        const char* tile = ring_bytes + buf * TILE_B + th * kTT * kRowBytes;
-        buf = buf == NBUF - 1 ? 0 : buf + 1;
-        const int tt = t_begin + TILE_T * it + th * kTT;
+        const char* tile = ring_bytes + buf * kTileBytes;
+        buf = buf == kNBuf - 1 ? 0 : buf + 1;
+        const int tt = t_begin + kTT * it;
 
         // ---- S^T = L . Q^T  (two 16-token blocks), VGPR accumulators.
         // Software-pipelined: operands of k-step ks+SPD are requested while
         // step ks runs, so each LDS read has ~2 steps of MFMA work to land.
-        constexpr int SPD = NW == 8 ? 2 : 3;
+        constexpr int SPD = 3;
         auto a_ptr = [&](int ks, int nb) {
             return reinterpret_cast<const u32x4_t*>(tile + ((ks & 1) ? a_off1 : a_off0) + 128 * (ks >> 1) +
                                                     4 * kRowBytes * nb);
@@ -349,19 +286,16 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
             abuf[j][0] = *a_ptr(j, 0);
             abuf[j][1] = *a_ptr(j, 1);
         }
-        f32x4_t sacc[MB][2];
+        f32x4_t sacc[2];
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
 #pragma unroll
             for (int nb = 0; nb < 2; nb++) {
                 const u32x4_t a = abuf[ks % SPD][nb];
 #pragma unroll
-                for (int mb = 0; mb < MB; mb++) {
-#pragma unroll
-                    for (int qq = 0; qq < NQ; qq++) {
-                        if (ks == 0 && qq == 0) mfma_s<DT, true>(sacc[mb][nb], a, qf[mb][qq][ks]);
-                        else mfma_s<DT, false>(sacc[mb][nb], a, qf[mb][qq][ks]);
-                    }
+                for (int qq = 0; qq < NQ; qq++) {
+                    if (ks == 0 && qq == 0) mfma_s<DT, true>(sacc[nb], a, qf[qq][ks]);
+                    else mfma_s<DT, false>(sacc[nb], a, qf[qq][ks]);
                 }
             }
             if (ks + SPD < KS) {
@@ -372,15 +306,10 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
             for (int k = 0; k < DPW; k++)
                 if ((k * KS) / DPW == ks) issue_k(k);
         }
-        if (it == 2) MUGEN_TRACE(11);
         // first P.L operands requested now, to land during the softmax
-        constexpr int VPD = NW == 8 ? 4 : 6;
-        // TS = 2: slice 1 accumulates its O with the 16-column blocks rotated
-        // by 16 (register d holds column block (d + 16) % 32), so that the
-        // epilogue of both slices keeps registers 0..15 and hands over 16..31
-        const int rot = (TS == 2 && th == 1) ? 512 : 0;
+        constexpr int VPD = 6;
         auto tr_load = [&](int d) {
-            const char* tp = tile + t_off[d & 3] + 128 * (d >> 2) + (d < 16 ? rot : -rot);
+            const char* tp = tile + t_off[d & 3] + 128 * (d >> 2);
             const u32x2_t lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(tp));
             const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(tp + 4 * kRowBytes));
             return u32x4_t{lo[0], lo[1], hi[0], hi[1]};
@@ -388,11 +317,12 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
         u32x4_t bbuf[VPD];
 #pragma unroll
         for (int j = 0; j < VPD; j++) bbuf[j] = tr_load(j);
-        // the asm MFMAs are hidden from the hazard recognizer: wait out their
-        // pipeline before the VALU reads the results
-#pragma unroll
-        for (int mb = 0; mb < MB; mb++)
-            asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(sacc[mb][0]), "+v"(sacc[mb][1]));
+        // The asm MFMAs are hidden from the compiler's hazard recognizer.  A
+        // VALU read of an MFMA result must wait for the MFMA to complete: a
+        // 16x16x32 MFMA (8 passes) writes its accumulator up to 18 cycles
+        // after issue, so 19 wait states (s_nop 7, 7, 3 = 8 + 8 + 4 - 1)
+        // precede the softmax's first read of sacc.
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(sacc[0]), "+v"(sacc[1]));
 
         // ---- softmax weights; lane holds tokens tt + 8g + (4nb + i) of row n.
         // A row's reference max is the max of its first visible tile (a
@@ -400,69 +330,55 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
         // none yet); afterwards each weight is exp2(s*scale*log2e - m_ref),
         // one fma + one exp2, and only edge tiles (split end, causal rows)
         // pay for masking.
-        bool fresh = false;
+        if (__any(m_ref == kNegInf)) {
+            float mt = kNegInf;
 #pragma unroll
-        for (int mb = 0; mb < MB; mb++) fresh |= (m_ref[mb] == kNegInf);
-        if (__any(fresh)) {
+            for (int nb = 0; nb < 2; nb++) {
 #pragma unroll
-            for (int mb = 0; mb < MB; mb++) {
-                float mt = kNegInf;
-#pragma unroll
-                for (int nb = 0; nb < 2; nb++) {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int tok = tt + 8 * g + 4 * nb + i;
-                        const bool vis = tok < t_end && tok < teff[mb];
-                        mt = fmaxf(mt, vis ? sacc[mb][nb][i] * p.scale_log2 : kNegInf);
-                    }
+                for (int i = 0; i < 4; i++) {
+                    const int tok = tt + 8 * g + 4 * nb + i;
+                    const bool vis = tok < t_end && tok < teff;
+                    mt = fmaxf(mt, vis ? sacc[nb][i] * p.scale_log2 : kNegInf);
                 }
-                mt = max_x32(max_x16(mt));
-                if (m_ref[mb] == kNegInf) m_ref[mb] = mt;  // O of this row is still 0
             }
+            mt = max_x32(max_x16(mt));
+            if (m_ref == kNegInf) m_ref = mt;  // O of this row is still 0
         }
-        u32x4_t pfrag[MB];
+        u32x4_t pfrag;
         auto weights = [&](auto masked_tag) {
             constexpr bool MASKED = decltype(masked_tag)::value;
+            const float mneg = (m_ref == kNegInf) ? 0.f : -m_ref;
+            float x[8];
 #pragma unroll
-            for (int mb = 0; mb < MB; mb++) {
-                const float mneg = (m_ref[mb] == kNegInf) ? 0.f : -m_ref[mb];
-                float x[8];
+            for (int nb = 0; nb < 2; nb++) {
 #pragma unroll
-                for (int nb = 0; nb < 2; nb++) {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        float v = fmaf(sacc[mb][nb][i], p.scale_log2, mneg);
-                        if constexpr (MASKED) {
-                            const int tok = tt + 8 * g + 4 * nb + i;
-                            v = (tok < t_end && tok < teff[mb]) ? v : kNegInf;
-                        }
-                        x[4 * nb + i] = fast_exp2(v);
+                for (int i = 0; i < 4; i++) {
+                    float v = fmaf(sacc[nb][i], p.scale_log2, mneg);
+                    if constexpr (MASKED) {
+                        const int tok = tt + 8 * g + 4 * nb + i;
+                        v = (tok < t_end && tok < teff) ? v : kNegInf;
                     }
+                    x[4 * nb + i] = fast_exp2(v);
                 }
-                l_part[mb] += ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
-                pfrag[mb] = u32x4_t{pack2<DT>(x[0], x[1]), pack2<DT>(x[2], x[3]),
-                                    pack2<DT>(x[4], x[5]), pack2<DT>(x[6], x[7])};
             }
+            l_part += ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
+            pfrag = u32x4_t{pack2<DT>(x[0], x[1]), pack2<DT>(x[2], x[3]), pack2<DT>(x[4], x[5]), pack2<DT>(x[6], x[7])};
         };
         // wave-uniform: interior tiles (the common case) carry no mask
         if (tt + kTT <= t_end && tt + kTT <= teff_min) weights(std::false_type{});
         else weights(std::true_type{});
 
-        if (it == 2) MUGEN_TRACE(12);
         // ---- O += P . L[:, 0:512]; B operand L[tt + 8g + j][16d + n], j < 8.
-        // The schedule is pinned to [MFMA x MB][2 transpose reads of d+VPD]
-        // so VPD steps of reads stay in flight behind the MFMAs.
+        // The schedule is pinned to [MFMA][2 transpose reads of d+VPD] so
+        // VPD steps of reads stay in flight behind the MFMAs.
 #pragma unroll
         for (int d = 0; d < 32; d++) {
             const u32x4_t bf = bbuf[d % VPD];
             if (d + VPD < 32) bbuf[d % VPD] = tr_load(d + VPD);
-#pragma unroll
-            for (int mb = 0; mb < MB; mb++) o[mb][d] = mfma16x16x32<DT>(pfrag[mb], bf, o[mb][d]);
-            __builtin_amdgcn_sched_group_barrier(0x008, MB, 0);
+            o[d] = mfma16x16x32<DT>(pfrag, bf, o[d]);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             if (d + VPD < 32) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
-        if (it == 2) MUGEN_TRACE(13);
-        if (it == 2) MUGEN_TRACE_CLK(15);
     }
 
     // ---- epilogue: (m, l, o/l) partial of this split.  The normalised O is
@@ -472,127 +388,44 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_kernel(MlaParams p) {
     // weights or normalised values left the 16-bit ranges is flagged (NaN m)
     // for the exact fp32 recompute in the combine kernel.
     MUGEN_TRACE(3);
-    float lrow[MB];  // S-layout row n: full sum of this wave's token slice
+    const float lrow = sum_x32(sum_x16(l_part));  // S-layout row n: the split's full sum
+    const float c0 = lrow > 0.f ? 1.f / lrow : 0.f;
+    const bool ovf = !(lrow <= exp2f(TH));  // every weight is <= l
+    float k0[4];  // the factors of O rows 4g+i
 #pragma unroll
-    for (int mb = 0; mb < MB; mb++) {
-        float l = l_part[mb];
-        l = sum_x32(sum_x16(l));
-        lrow[mb] = l;
-    }
-    // Per S-layout row n: weight c0 of this wave's O and c1 of the other
-    // token slice's O in the normalised merge, the merged (max, sum), and
-    // the headroom flag (every weight of a slice is <= its l).
-    float c0[MB], c1[MB], mrow[MB], Lrow[MB];
-    bool ovf[MB];
-    constexpr int DH = 32 / TS;  // 16-column blocks this wave stores: registers 0..DH-1
-    const f32x4_t* ox = nullptr;     // TS = 2: the partner's O for this wave's columns, in LDS
-    uint64_t* big_x = nullptr;        // TS = 2: the partner's overflow ballots
-    if constexpr (TS == 1) {
+    for (int i = 0; i < 4; i++) k0[i] = __shfl(c0, 4 * g + i, 64);
+    float vmax = 0.f;  // largest |o/l| this lane stores
+    if (row0 < p.R) {
+        u32x4_t* dst = reinterpret_cast<u32x4_t*>(p.ws_o) + blob_pair(p, b, s, row0 >> 4, 0, lane);
 #pragma unroll
-        for (int mb = 0; mb < MB; mb++) {
-            c0[mb] = lrow[mb] > 0.f ? 1.f / lrow[mb] : 0.f;
-            c1[mb] = 0.f;
-            mrow[mb] = m_ref[mb];
-            Lrow[mb] = lrow[mb];
-            ovf[mb] = !(lrow[mb] <= exp2f(TH));
-        }
-    } else {
-        // the two token slices of a row group swap the O columns the other
-        // one stores (16 blocks each), plus (m, l), through LDS
-        __syncthreads();  // every wave is done with the ring (its DMA has landed)
-        constexpr int XB = MB * 16 * 64;  // f32x4 per (row group, slice) area
-        f32x4_t* xo = reinterpret_cast<f32x4_t*>(&ring[0]);
-        float2* xml = reinterpret_cast<float2*>(&ring[0] + RG * 2 * XB * 16);
-        big_x = reinterpret_cast<uint64_t*>(&ring[0] + RG * 2 * XB * 16 + RG * 2 * MB * 16 * 8);
-        f32x4_t* mine = xo + (rg * 2 + th) * XB;
-        // registers 16..31 hold the partner's column blocks (see the rotation
-        // in the P.L loop); they go over, registers 0..15 stay
+        for (int d = 0; d < 32; d += 2) {
+            uint32_t h[4];
 #pragma unroll
-        for (int mb = 0; mb < MB; mb++) {
-#pragma unroll
-            for (int d = 0; d < DH; d++) mine[(mb * DH + d) * 64 + lane] = o[mb][DH + d];
-            if (g == 0) xml[((rg * 2 + th) * MB + mb) * 16 + n] = make_float2(m_ref[mb], lrow[mb]);
-        }
-        __syncthreads();
-        ox = xo + (rg * 2 + 1 - th) * XB;
-#pragma unroll
-        for (int mb = 0; mb < MB; mb++) {
-            const float2 v1 = xml[((rg * 2 + 1 - th) * MB + mb) * 16 + n];
-            const float m0 = m_ref[mb], l0 = lrow[mb], m1 = v1.x, l1 = v1.y;
-            const float M = fmaxf(m0, m1);
-            const float a0 = m0 == kNegInf ? 0.f : fast_exp2(m0 - M);
-            const float a1 = m1 == kNegInf ? 0.f : fast_exp2(m1 - M);
-            const float L = a0 * l0 + a1 * l1;
-            const float inv = L > 0.f ? 1.f / L : 0.f;
-            c0[mb] = a0 * inv;
-            c1[mb] = a1 * inv;
-            mrow[mb] = M;
-            Lrow[mb] = L;
-            ovf[mb] = !(l0 <= exp2f(TH)) || !(l1 <= exp2f(TH));
-        }
-    }
-    uint64_t big_mask[MB];
-#pragma unroll
-    for (int mb = 0; mb < MB; mb++) {
-        float k0[4], k1[4];  // the factors of O rows 4g+i
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            k0[i] = __shfl(c0[mb], 4 * g + i, 64);
-            if constexpr (TS == 2) k1[i] = __shfl(c1[mb], 4 * g + i, 64);
-        }
-        const int rblk = row0 + 16 * mb;  // first row of this 16-row block
-        float vmax = 0.f;                 // largest |o/l| this lane stores
-        if (rblk < p.R) {
-            // registers 0..DH-1 = column blocks th*DH .. th*DH + DH-1
-            u32x4_t* dst = reinterpret_cast<u32x4_t*>(p.ws_o) + blob_pair(p, b, s, rblk >> 4, (th * DH) >> 1, lane);
-#pragma unroll
-            for (int d = 0; d < DH; d += 2) {
-                uint32_t h[4];
-#pragma unroll
-                for (int e = 0; e < 2; e++) {
-                    f32x4_t v = o[mb][d + e] * f32x4_t{k0[0], k0[1], k0[2], k0[3]};
-                    if constexpr (TS == 2)
-                        v += ox[(mb * DH + d + e) * 64 + lane] * f32x4_t{k1[0], k1[1], k1[2], k1[3]};
-                    vmax = fmaxf(vmax, fmaxf(fabsf(v[0]), fabsf(v[1])));
-                    vmax = fmaxf(vmax, fmaxf(fabsf(v[2]), fabsf(v[3])));
-                    h[2 * e] = pack2<DT_F16>(v[0], v[1]);
-                    h[2 * e + 1] = pack2<DT_F16>(v[2], v[3]);
-                }
-                dst[(d >> 1) * 64] = u32x4_t{h[0], h[1], h[2], h[3]};
+            for (int e = 0; e < 2; e++) {
+                const f32x4_t v = o[d + e] * f32x4_t{k0[0], k0[1], k0[2], k0[3]};
+                vmax = fmaxf(vmax, fmaxf(fabsf(v[0]), fabsf(v[1])));
+                vmax = fmaxf(vmax, fmaxf(fabsf(v[2]), fabsf(v[3])));
+                h[2 * e] = pack2<DT_F16>(v[0], v[1]);
+                h[2 * e + 1] = pack2<DT_F16>(v[2], v[3]);
             }
+            dst[(d >> 1) * 64] = u32x4_t{h[0], h[1], h[2], h[3]};
         }
-        // fp16 partials: a normalised value past 65000 cannot be stored
-        // (only bf16 latent rows can be that large); flagged like an overshoot
-        big_mask[mb] = __ballot(!(vmax <= 65000.f));
     }
-    if constexpr (TS == 2) {  // slice 0 writes the rows' (m, l): it needs the partner's overflow ballots
-        if (th == 1) {
-#pragma unroll
-            for (int mb = 0; mb < MB; mb++)
-                if (lane == 0) big_x[rg * MB + mb] = big_mask[mb];
-        }
-        __syncthreads();
-        MUGEN_TRACE(4);
-        if (th == 1) return;
-#pragma unroll
-        for (int mb = 0; mb < MB; mb++) big_mask[mb] |= big_x[rg * MB + mb];
-    }
-#pragma unroll
-    for (int mb = 0; mb < MB; mb++) {
-        // rows 4g+i of a lane overflowed -> tell their S-layout lanes (row n)
-        const bool row_big = (big_mask[mb] >> (n >> 2) * 16) & 0xffffull;  // any lane of quad n/4
-        const int srow = row0 + 16 * mb + n;  // S-layout row of this lane
-        if (g == 0 && srow < p.R) {
-            // a weight past the headroom may have overflowed its 16-bit P
-            const int64_t slot = ((int64_t)b * p.num_splits + s) * p.R + srow;
-            p.ws_ml[slot * 2 + 0] = (ovf[mb] || row_big) ? __builtin_nanf("") : mrow[mb];
-            p.ws_ml[slot * 2 + 1] = Lrow[mb];
-        }
+    // fp16 partials: a normalised value past 65000 cannot be stored (only
+    // bf16 latent rows can be that large); flagged like an overshoot
+    const uint64_t big_mask = __ballot(!(vmax <= 65000.f));
+    // rows 4g+i of a lane overflowed -> tell their S-layout lanes (row n)
+    const bool row_big = (big_mask >> (n >> 2) * 16) & 0xffffull;  // any lane of quad n/4
+    if (g == 0 && row_ok) {
+        // a weight past the headroom may have overflowed its 16-bit P
+        const int64_t slot_ml = ((int64_t)b * p.num_splits + s) * p.R + row;
+        p.ws_ml[slot_ml * 2 + 0] = (ovf || row_big) ? __builtin_nanf("") : m_ref;
+        p.ws_ml[slot_ml * 2 + 1] = lrow;
     }
     MUGEN_TRACE(5);
 }
 
-// Warp-specialised variant (5): 8 waves, two per SIMD, 64 query rows per
+// Warp-specialised kernel: 8 waves, two per SIMD, 64 query rows per
 // workgroup, 32-token tiles.  Waves 0-3 ("S waves") each hold the q of 16
 // rows in registers, compute S^T = L . Q^T for the tile and its softmax
 // weights, and write P to LDS in the A-operand layout of P . V.  Waves 4-7
@@ -632,14 +465,14 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
     const int nrb = p.nrb;
     const int rb = slot % nrb;
     int nact = 0;
-    for (int j = 0; j < p.B; j++) nact += (p.seq_lens[j] + p.chunk - 1) / p.chunk;
+    for (int j = 0; j < p.B; j++) nact += (clamp_len(p.seq_lens[j], p.max_T) + p.chunk - 1) / p.chunk;
     const int gpx = (nact + nxcd - 1) / nxcd;
     const int gi = slot / nrb;
     const int grp = xcd * gpx + gi;
     int b = -1, s = 0;
     if (gi < gpx) {
         for (int j = 0, acc = 0; j < p.B; j++) {
-            const int nsj = (p.seq_lens[j] + p.chunk - 1) / p.chunk;
+            const int nsj = (clamp_len(p.seq_lens[j], p.max_T) + p.chunk - 1) / p.chunk;
             if (grp < acc + nsj) {
                 b = j;
                 s = grp - acc;
@@ -656,7 +489,7 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
     const bool s_wave = w < 4;
     const int wr = w & 3;  // S wave: row block; PV wave: column quarter
     const int n = lane & 15, g = lane >> 4;
-    const int T = p.seq_lens[b];
+    const int T = clamp_len(p.seq_lens[b], p.max_T);
     const int t_begin = s * p.chunk;
     const int t_end = min(t_begin + p.chunk, T);
     const int ntiles = (t_end - t_begin + kTT - 1) / kTT;
@@ -846,9 +679,7 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
             lds_barrier();  // B_j
             if (j == 0) MUGEN_TRACE(1);
             if (j == 4) MUGEN_TRACE(7);
-#ifndef WS_DEBUG_NO_DMA
             if (j + 2 < ntiles) issue(j + 2);  // into the slot of tile j-2, finished before B_j
-#endif
             if (j == 0) continue;
             // O += P(j-1) . L(j-1)[:, 128wr .. +128]
             const char* tile = &ring[((j - 1) % NSLOT) * kTileBytes];
@@ -923,7 +754,7 @@ __device__ void mla_recompute_split(const MlaParams& p, int b, int row, int s, f
     const int tid = threadIdx.x, nt = blockDim.x, nw = nt >> 6;
     constexpr int kMaxCols = 8;  // 512 / 64: at least one wave per workgroup
     const int ncols = kKR / nt;
-    const int T = p.seq_lens[b];
+    const int T = clamp_len(p.seq_lens[b], p.max_T);
     const int teff = T - p.q_len + row / p.H + 1;
     const int t_begin = s * p.chunk;
     const int t_end = min(min(t_begin + p.chunk, T), teff);
@@ -997,7 +828,7 @@ __global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
     const int qb = blockIdx.x, dg = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, dsub = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
-    const int T = p.seq_lens[b];
+    const int T = clamp_len(p.seq_lens[b], p.max_T);
     const int nact = min(p.num_splits, (T + p.chunk - 1) / p.chunk);
     const int64_t ml_st = (int64_t)p.R * 2;  // floats between splits of one row
     const float* ml0 = p.ws_ml + (int64_t)b * p.num_splits * p.R * 2;
@@ -1145,63 +976,41 @@ __global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
 
 // ------------------------------------------------------------------ launch
 
-// variant 1: MB = 1, TS = 1 (64 rows); 2: MB = 2, TS = 1 (128 rows);
-// 3: MB = 2, TS = 2 (64 rows, 64-token tiles); 4: MB = 1, TS = 2, 8 waves
-// (64 rows, 64-token tiles, two waves per SIMD); 5: warp-specialised
-// mla_decode_ws_kernel (64 rows, 32-token tiles)
-int mla_rows_per_block(int variant) { return variant == 2 ? 128 : 64; }
-int mla_tile_tokens(int variant) { return (variant == 3 || variant == 4) ? 2 * kTT : kTT; }
-
-template <int MB, int TS, int NW, int QDT, int DT, int OUT_DT>
-static hipError_t launch_mla_t(const MlaParams& p, hipStream_t st, KernelTimer* t) {
-    const int grid = 8 * p.nrb * ((p.groups + 7) / 8);  // see the XCD mapping in the kernel
-    hipError_t e = launch_k(t, "mla_decode", mla_decode_kernel<MB, TS, NW, QDT, DT>, dim3(grid), dim3(64 * NW), st, p);
-    if (e != hipSuccess) return e;
-    return launch_k(t, "mla_decode_combine", mla_decode_combine_kernel<QDT, DT, OUT_DT>, dim3(p.nq, 4, p.B),
-                    dim3(256), st, p);
-}
+// kernel 1: mla_decode_kernel ("rows", 16-bit q with at most 64 rows);
+// kernel 2: mla_decode_ws_kernel (warp-specialised, every other case).
+// Both take 64 query rows per workgroup and 32-token tiles.
+int mla_rows_per_block(int) { return 64; }
+int mla_tile_tokens(int) { return kTT; }
 
 template <int QDT, int DT, int OUT_DT>
-static hipError_t launch_mla_ws_t(const MlaParams& p, hipStream_t st, KernelTimer* t) {
-    const int grid = 8 * p.nrb * ((p.groups + 7) / 8);
-    hipError_t e = launch_k(t, "mla_decode", mla_decode_ws_kernel<QDT, DT>, dim3(grid), dim3(512), st, p);
+static hipError_t launch_mla_t(const MlaParams& p, int kernel, hipStream_t st, KernelTimer* t) {
+    const int grid = 8 * p.nrb * ((p.groups + 7) / 8);  // see the XCD mapping in the kernels
+    hipError_t e = kernel == 1
+                       ? launch_k(t, "mla_decode", mla_decode_kernel<QDT, DT>, dim3(grid), dim3(256), st, p)
+                       : launch_k(t, "mla_decode", mla_decode_ws_kernel<QDT, DT>, dim3(grid), dim3(512), st, p);
     if (e != hipSuccess) return e;
     return launch_k(t, "mla_decode_combine", mla_decode_combine_kernel<QDT, DT, OUT_DT>, dim3(p.nq, 4, p.B),
                     dim3(256), st, p);
 }
 
 template <int QDT, int DT>
-static hipError_t launch_mla_ws(const MlaParams& p, int out_dt, hipStream_t st, KernelTimer* t) {
-    if (out_dt == DT_F32) return launch_mla_ws_t<QDT, DT, DT_F32>(p, st, t);
-    if (out_dt == DT_F16) return launch_mla_ws_t<QDT, DT, DT_F16>(p, st, t);
-    return launch_mla_ws_t<QDT, DT, DT_BF16>(p, st, t);
-}
-
-template <int MB, int TS, int NW, int QDT, int DT>
-static hipError_t launch_mla_o(const MlaParams& p, int out_dt, hipStream_t st, KernelTimer* t) {
-    if (out_dt == DT_F32) return launch_mla_t<MB, TS, NW, QDT, DT, DT_F32>(p, st, t);
-    if (out_dt == DT_F16) return launch_mla_t<MB, TS, NW, QDT, DT, DT_F16>(p, st, t);
-    return launch_mla_t<MB, TS, NW, QDT, DT, DT_BF16>(p, st, t);
+static hipError_t launch_mla_o(const MlaParams& p, int kernel, int out_dt, hipStream_t st, KernelTimer* t) {
+    if (out_dt == DT_F32) return launch_mla_t<QDT, DT, DT_F32>(p, kernel, st, t);
+    if (out_dt == DT_F16) return launch_mla_t<QDT, DT, DT_F16>(p, kernel, st, t);
+    return launch_mla_t<QDT, DT, DT_BF16>(p, kernel, st, t);
 }
 
 template <int DT>
-static hipError_t launch_mla_v(const MlaParams& p, int variant, int q_dt, int out_dt, hipStream_t st,
+static hipError_t launch_mla_q(const MlaParams& p, int kernel, int q_dt, int out_dt, hipStream_t st,
                                KernelTimer* t) {
-    // variants 2-4 need 16-bit q (register budget); fp32 q runs variant 1 or 5
-    if (q_dt == DT_F32)
-        return variant == 5 ? launch_mla_ws<DT_F32, DT>(p, out_dt, st, t)
-                            : launch_mla_o<1, 1, 4, DT_F32, DT>(p, out_dt, st, t);
-    if (variant == 2) return launch_mla_o<2, 1, 4, DT, DT>(p, out_dt, st, t);
-    if (variant == 3) return launch_mla_o<2, 2, 4, DT, DT>(p, out_dt, st, t);
-    if (variant == 4) return launch_mla_o<1, 2, 8, DT, DT>(p, out_dt, st, t);
-    if (variant == 5) return launch_mla_ws<DT, DT>(p, out_dt, st, t);
-    return launch_mla_o<1, 1, 4, DT, DT>(p, out_dt, st, t);
+    if (q_dt == DT_F32) return launch_mla_o<DT_F32, DT>(p, kernel, out_dt, st, t);
+    return launch_mla_o<DT, DT>(p, kernel, out_dt, st, t);
 }
 
-hipError_t launch_mla_decode(const MlaParams& p, int variant, int q_dt, int lat_dt, int out_dt,
+hipError_t launch_mla_decode(const MlaParams& p, int kernel, int q_dt, int lat_dt, int out_dt,
                              hipStream_t st, KernelTimer* t) {
-    if (lat_dt == DT_F16) return launch_mla_v<DT_F16>(p, variant, q_dt, out_dt, st, t);
-    return launch_mla_v<DT_BF16>(p, variant, q_dt, out_dt, st, t);
+    if (lat_dt == DT_F16) return launch_mla_q<DT_F16>(p, kernel, q_dt, out_dt, st, t);
+    return launch_mla_q<DT_BF16>(p, kernel, q_dt, out_dt, st, t);
 }
 
 }  // namespace mugen_attn

@@ -493,6 +493,221 @@ void gqa_prefill_test(hipStream_t st) {
     std::printf("gqa prefill provider done\n");
 }
 
+
+// ---------------------------------------------------------------- prompts in a batch
+
+// A prompt for sequence 1 of a batch of 2 through GqaAttention and through
+// GqaAttentionQ4 (whose prefill attends over its f16 caches, as the
+// reference's prefill does whichever path decodes): both equal a direct
+// prefill over the assembled context, sequence 0 is untouched, and the
+// lengths advance for sequence 1 only.
+void prefill_batch_test(hipStream_t st) {
+    mugen_attn::GqaShape s;
+    s.n_layers = 1;
+    s.batch = 2;
+    s.n_heads = 28;
+    s.n_kv_heads = 4;
+    s.head_dim = 128;
+    s.max_seq_len = 512;
+    mugen_attn::GqaQ4Shape s4;
+    s4.n_layers = 1;
+    s4.batch = 2;
+    s4.n_heads = 28;
+    s4.n_kv_heads = 4;
+    s4.head_dim = 128;
+    s4.max_seq_len = 512;
+    s4.fp16_preserve_last = 16;
+    s4.max_new = 64;
+    const int n = 48, chunks = 3;
+    std::printf("prompt in a batch: H %d Hk %d d %d, %d chunks of %d for sequence 1\n", s.n_heads, s.n_kv_heads,
+                s.head_dim, chunks, n);
+    std::fflush(stdout);
+    std::unique_ptr<mugen_attn::GqaAttention> a;
+    std::unique_ptr<mugen_attn::GqaAttentionQ4> a4;
+    if (!ok(mugen_attn::GqaAttention::create(s, &a), "create")) return;
+    if (!ok(mugen_attn::GqaAttentionQ4::create(s4, &a4), "create q4")) return;
+    const size_t row = (size_t)s.n_kv_heads * s.head_dim;
+    const size_t seq_bytes = (size_t)s.max_seq_len * row * 2;
+    Rng r(7);
+    auto k0 = f16_rand(r, seq_bytes / 2, 1.0f), v0 = f16_rand(r, seq_bytes / 2, 1.0f);  // sequence 0's cache
+    hip(hipMemcpyAsync(a->k_cache(0), k0.data(), seq_bytes, hipMemcpyHostToDevice, st), "K0");
+    hip(hipMemcpyAsync(a->v_cache(0), v0.data(), seq_bytes, hipMemcpyHostToDevice, st), "V0");
+    ok(a->set_lengths({100, 0}, st), "lengths");
+    ok(a4->set_lengths({0, 0}, st), "q4 lengths");
+    const size_t qb = (size_t)n * s.n_heads * s.head_dim * 2, kb = (size_t)n * row * 2;
+    Dev q(qb), kn(kb), vn(kb), out(qb), out4(qb), ref(qb), kc((size_t)chunks * n * row * 2),
+        vc((size_t)chunks * n * row * 2);
+    std::vector<uint16_t> kall, vall;
+    for (int c = 0; c < chunks; c++) {
+        auto hq = f16_rand(r, qb / 2, 1.0f), hk = f16_rand(r, kb / 2, 1.0f), hv = f16_rand(r, kb / 2, 1.0f);
+        q.put(hq.data(), st);
+        kn.put(hk.data(), st);
+        vn.put(hv.data(), st);
+        kall.insert(kall.end(), hk.begin(), hk.end());
+        vall.insert(vall.end(), hv.begin(), hv.end());
+        hip(hipStreamSynchronize(st), "sync");
+        ok(a->prefill_layer(0, 1, q.p, kn.p, vn.p, out.p, n, st), "prefill_layer seq 1");
+        ok(a4->prefill_layer(0, 1, q.p, kn.p, vn.p, out4.p, n, st), "q4 prefill_layer seq 1");
+        // direct prefill over the context so far
+        hip(hipMemcpyAsync(kc.p, kall.data(), kall.size() * 2, hipMemcpyHostToDevice, st), "kc");
+        hip(hipMemcpyAsync(vc.p, vall.data(), vall.size() * 2, hipMemcpyHostToDevice, st), "vc");
+        mugen_attn_gqa_prefill_args pf{};
+        pf.q = q.p;
+        pf.k = kc.p;
+        pf.v = vc.p;
+        pf.out = ref.p;
+        pf.n_tokens = n;
+        pf.n_heads = s.n_heads;
+        pf.n_kv_heads = s.n_kv_heads;
+        pf.head_dim = s.head_dim;
+        pf.kv_len = (c + 1) * n;
+        pf.start_pos = c * n;
+        pf.causal = 1;
+        pf.dtype = MUGEN_ATTN_F16;
+        pf.out_dtype = MUGEN_ATTN_F16;
+        ok(mugen_attn::gqa_prefill(pf, st), "direct prefill");
+        const auto o = out.get(st), o4 = out4.get(st), o_ref = ref.get(st);
+        if (o != o_ref || o4 != o_ref || !finite_f16(o)) {
+            std::printf("FAIL prompt chunk %d: provider outputs differ from the direct prefill\n", c);
+            failures++;
+        }
+        ok(a->advance_sequence(1, n, st), "advance_sequence");
+        ok(a4->advance_sequence(1, n, st), "q4 advance_sequence");
+    }
+    std::vector<uint16_t> kgot(seq_bytes / 2);
+    hip(hipMemcpyAsync(kgot.data(), a->k_cache(0), seq_bytes, hipMemcpyDeviceToHost, st), "K0 read");
+    hip(hipStreamSynchronize(st), "sync");
+    if (kgot != k0) {
+        std::printf("FAIL prompt in a batch: sequence 0's cache changed\n");
+        failures++;
+    }
+    check_lengths(a->lengths_after(), {101, chunks * n + 1}, st, "prompt in a batch");
+    check_lengths(a4->lengths_after(), {1, chunks * n + 1}, st, "q4 prompt in a batch");
+    // the store quantised what left its f16 window (preserve 16)
+    check_lengths(a4->quantised(), {0, chunks * n - s4.fp16_preserve_last}, st, "q4 quantised count");
+    std::printf("prompt in a batch done\n");
+}
+
+// MLA prompt: one prefill_layer call over n tokens equals the reference's
+// token-by-token path (n decode steps of q_len 1): the same latent rows,
+// outputs within the parity tolerance.
+void mla_prefill_test(hipStream_t st) {
+    mugen_attn::MlaShape s;
+    s.n_layers = 1;
+    s.batch = 1;
+    s.n_heads = 16;
+    s.max_seq_len = 256;
+    s.q_len = 1;
+    s.max_prefill = 64;
+    s.rope = mugen_attn_rope_params{10000.f, 40.f, 4096};
+    const int start = 20, n = 40;
+    std::printf("mla prompt: H %d start %d n %d\n", s.n_heads, start, n);
+    std::fflush(stdout);
+    std::unique_ptr<mugen_attn::MlaAttention> pre, step;
+    if (!ok(mugen_attn::MlaAttention::create(s, &pre), "create prefill")) return;
+    if (!ok(mugen_attn::MlaAttention::create(s, &step), "create stepwise")) return;
+    Rng r(9);
+    const size_t lat = (size_t)s.max_seq_len * 576 * 2;
+    auto c = f16_rand(r, lat / 2, 0.5f);
+    for (auto* a : {pre.get(), step.get()})
+        hip(hipMemcpyAsync(a->latent(0), c.data(), lat, hipMemcpyHostToDevice, st), "latent init");
+    auto hn = f16_rand(r, 512, 0.2f);
+    for (auto& x : hn) {
+        _Float16 h;
+        std::memcpy(&h, &x, 2);
+        h = (_Float16)(1.0f + (float)h);
+        std::memcpy(&x, &h, 2);
+    }
+    auto hk = f16_rand(r, (size_t)s.n_heads * 128 * 512, 0.08f), hv = f16_rand(r, (size_t)s.n_heads * 128 * 512, 0.08f);
+    Dev norm(512 * 2), wkb(hk.size() * 2), wvb(hv.size() * 2);
+    norm.put(hn.data(), st);
+    wkb.put(hk.data(), st);
+    wvb.put(hv.data(), st);
+    mugen_attn::MlaLayerWeights w;
+    w.kv_a_norm = norm.p;
+    w.w_kb = wkb.p;
+    w.w_vb = wvb.p;
+    w.w_type = MUGEN_ATTN_W_F16;
+    ok(pre->set_lengths({start}, st), "lengths");
+    ok(step->set_lengths({start}, st), "lengths");
+    const size_t qrow = (size_t)s.n_heads * 192 * 2, orow = (size_t)s.n_heads * 128 * 2;
+    auto hq = f16_rand(r, n * qrow / 2, 1.0f), hkv = f16_rand(r, (size_t)n * 576, 1.0f);
+    Dev q(n * qrow), kva((size_t)n * 576 * 2), out(n * orow), q1(qrow), kva1(576 * 2), out1(orow);
+    q.put(hq.data(), st);
+    kva.put(hkv.data(), st);
+    ok(pre->prefill_layer(0, 0, w, q.p, kva.p, out.p, n, st), "prefill_layer");
+    ok(pre->advance_sequence(0, n, st), "advance_sequence");
+    const auto o_pre = out.get(st);
+    float worst = 0.f;
+    for (int t = 0; t < n; t++) {
+        hip(hipMemcpyAsync(q1.p, hq.data() + t * qrow / 2, qrow, hipMemcpyHostToDevice, st), "q_t");
+        hip(hipMemcpyAsync(kva1.p, hkv.data() + (size_t)t * 576, 576 * 2, hipMemcpyHostToDevice, st), "kv_a_t");
+        ok(step->decode_layer(0, w, q1.p, kva1.p, out1.p, st), "decode_layer");
+        ok(step->advance(st, 1), "advance");
+        const auto o1 = out1.get(st);
+        std::vector<uint8_t> ot(o_pre.begin() + t * orow, o_pre.begin() + (t + 1) * orow);
+        worst = std::max(worst, max_abs_diff_f16(ot, o1));
+    }
+    if (!(worst <= 2e-3f) || !finite_f16(o_pre)) {
+        std::printf("FAIL mla prompt: prefill vs token-by-token max-abs %g\n", worst);
+        failures++;
+    }
+    std::vector<uint8_t> lp(lat), ls(lat);
+    hip(hipMemcpyAsync(lp.data(), pre->latent(0), lat, hipMemcpyDeviceToHost, st), "latent");
+    hip(hipMemcpyAsync(ls.data(), step->latent(0), lat, hipMemcpyDeviceToHost, st), "latent");
+    hip(hipStreamSynchronize(st), "sync");
+    if (lp != ls) {
+        std::printf("FAIL mla prompt: latent caches differ\n");
+        failures++;
+    }
+    check_lengths(pre->lengths_after(), {start + n + 1}, st, "mla prompt");
+    std::printf("mla prompt done (max-abs %g)\n", worst);
+}
+
+// Lengths outside the caches are refused (the reference's KVCache::append
+// refuses a token once the cache is full), and a new provider starts empty.
+void bounds_test(hipStream_t st) {
+    std::printf("length bounds\n");
+    std::fflush(stdout);
+    mugen_attn::GqaShape s;
+    s.n_layers = 1;
+    s.batch = 1;
+    s.n_heads = 8;
+    s.n_kv_heads = 2;
+    s.head_dim = 64;
+    s.max_seq_len = 64;
+    std::unique_ptr<mugen_attn::GqaAttention> a;
+    if (!ok(mugen_attn::GqaAttention::create(s, &a), "create")) return;
+    check_lengths(a->lengths_after(), {1}, st, "fresh provider");
+    if (a->set_lengths({64}, st) || a->set_lengths({-1}, st)) {
+        std::printf("FAIL bounds: set_lengths accepted a length without room for the step\n");
+        failures++;
+    }
+    ok(a->set_lengths({63}, st), "set_lengths max - 1");
+    Dev q(8 * 64 * 2), kn(2 * 64 * 2), vn(2 * 64 * 2), out(8 * 64 * 2);
+    ok(a->decode_layer(0, q.p, kn.p, vn.p, out.p, st), "last token");
+    ok(a->advance(st), "advance to full");
+    if (a->decode_layer(0, q.p, kn.p, vn.p, out.p, st) || a->advance(st)) {
+        std::printf("FAIL bounds: a full cache accepted another token\n");
+        failures++;
+    }
+    mugen_attn::MlaShape m;
+    m.n_layers = 1;
+    m.batch = 2;
+    m.n_heads = 16;
+    m.max_seq_len = 64;
+    m.q_len = 5;
+    std::unique_ptr<mugen_attn::MlaAttention> ma;
+    if (!ok(mugen_attn::MlaAttention::create(m, &ma), "create mla")) return;
+    check_lengths(ma->lengths_after(), {5, 5}, st, "fresh mla provider");
+    if (ma->set_lengths({60, 0}, st)) {
+        std::printf("FAIL bounds: MLA set_lengths accepted a length without room for q_len tokens\n");
+        failures++;
+    }
+    ok(ma->set_lengths({59, 0}, st), "mla set_lengths max - q_len");
+    std::printf("length bounds done\n");
+}
+
 }  // namespace
 
 int main() {
@@ -503,6 +718,9 @@ int main() {
     mla_test(st, 3);
     gqa_prefill_test(st);
     gqa_q4_test(st);
+    prefill_batch_test(st);
+    mla_prefill_test(st);
+    bounds_test(st);
     (void)hipStreamSynchronize(st);
     (void)hipStreamDestroy(st);
     std::printf(failures ? "FAIL (%d)\n" : "PASS\n", failures);

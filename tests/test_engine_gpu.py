@@ -6,8 +6,10 @@ kv_offset / seq_len into its cached dispatches before each step.
 
 * test_cpp_provider_selftest: the C++ provider (include/mugen_attn_engine.hpp)
   replays captured multi-layer GQA, 4-bit-store GQA and MLA (decode and
-  verify) steps bit-identically to eager calls, and a prompt chunk through
-  prefill_layer matches a direct prefill (mugen_amd/engine_selftest.cpp);
+  verify) steps bit-identically to eager calls; prompt chunks through
+  prefill_layer (one sequence of a batch, both GQA providers) match a direct
+  prefill; an MLA prompt in one call matches the token-by-token path; and
+  lengths past the caches are refused (mugen_amd/engine_selftest.cpp);
 * test_step_graph_replays_match_oracle: a captured step (kv_append +
   decode per layer + seq_advance) replayed several times, with eager uploads
   and synchronisations between replays, each replay checked against the
@@ -34,7 +36,8 @@ def test_cpp_provider_selftest(device):
     r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
     print(r.stdout[-4000:], r.stderr[-2000:], flush=True)
     assert r.returncode == 0 and r.stdout.strip().endswith("PASS"), r.stdout[-2000:]
-    for part in ("gqa provider done", "mla provider done", "gqa prefill provider done", "gqa q4 provider done"):
+    for part in ("gqa provider done", "mla provider done", "gqa prefill provider done", "gqa q4 provider done",
+                 "prompt in a batch done", "mla prompt done", "length bounds done"):
         assert part in r.stdout, part
 
 

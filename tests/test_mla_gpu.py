@@ -5,22 +5,23 @@ import pytest
 import torch
 
 import mugen_amd
+from mugen_amd import _capi
 from oracle import oracle as O
 from tests import cases as C
 
 pytestmark = pytest.mark.gpu
 
 
-def run_gpu(c, device, out_dtype=C.F32, num_splits=0, seq_lens=None, q=None):
+def run_gpu(c, device, out_dtype=C.F32, num_splits=0, seq_lens=None, q=None, kernel=0):
     sl_np = c["seq_lens"] if seq_lens is None else np.asarray(seq_lens, np.int32)
     C.say(f"mla B={c['B']} q_len={c['q_len']} H={c['H']} maxT={c['max_T']} q={c['q_dtype']} "
-          f"lat={c['lat_dtype']} out={out_dtype} splits={num_splits} lens={list(sl_np)[:8]}")
+          f"lat={c['lat_dtype']} out={out_dtype} splits={num_splits} kernel={kernel} lens={list(sl_np)[:8]}")
     if q is None:
         q = C.to_dev(c["q"] if c["q_dtype"] == C.F32 else c["qb"], c["q_dtype"], device)
     lat = C.to_dev(c["latb"], c["lat_dtype"], device)
     sl = torch.from_numpy(sl_np).to(device)
     out = mugen_amd.mla_attention(q, lat, sl, c["max_T"], scale=C.MLA_SCALE,
-                                  out_dtype=C.torch_dtype(out_dtype), num_splits=num_splits)
+                                  out_dtype=C.torch_dtype(out_dtype), num_splits=num_splits, kernel=kernel)
     torch.cuda.synchronize()
     return out.float().cpu().numpy()
 
@@ -41,20 +42,28 @@ def test_v3_decode_config(device):
     C.assert_close(run_gpu(c, device), ref, "v3 decode")
 
 
-def test_v3_verify_config_sampled_heads_and_causal_consistency(device):
-    # B=4, q_len=5, H=128, T=32768; the oracle checks a head sample,
+def test_v3_verify_config_and_causal_consistency(device):
+    # B=4, q_len=5, H=128, T=32768; the oracle checks every head,
     # and every verify row must equal a decode call at seq_len T-5+i+1
     T = 32768
     c = C.mla_case(46, 4, 5, 128, [T] * 4, q_dtype=C.BF16, lat_dtype=C.BF16)
     got = run_gpu(c, device)
-    heads = [0, 1, 63, 64, 127]
-    ref = C.mla_ref(c, nthreads=8, heads=heads)
-    C.assert_close(got[:, :, heads, :], ref, "v3 verify (sampled heads)")
+    ref = C.mla_ref(c, nthreads=16)  # all 128 heads (~180 GFLOP in the oracle)
+    C.assert_close(got, ref, "v3 verify (all heads)")
     qdev = C.to_dev(c["qb"], C.BF16, device)
     for i in range(5):
         qi = qdev[:, i:i + 1].contiguous()
         dec = run_gpu(dict(c, q_len=1), device, seq_lens=[T - 5 + i + 1] * 4, q=qi)
         np.testing.assert_allclose(got[:, i:i + 1], dec, atol=5e-4, rtol=1e-3)
+
+
+@pytest.mark.parametrize("q_len,start", [(64, 0), (64, 300), (512, 0), (512, 300)])
+def test_v2lite_prompt_prefill(device, q_len, start):
+    # a prompt of q_len tokens in one verify-shaped call: the reference runs
+    # cpu_mla_attention once per prompt token at seq_len = start + t + 1
+    # (transformer.cpp:1325-1337).  V2-Lite heads, fp32 absorbed q, f16 latent
+    c = C.mla_case(300 + q_len + start, 1, q_len, 16, [start + q_len], q_dtype=C.F32, lat_dtype=C.F16)
+    C.assert_close(run_gpu(c, device), C.mla_ref(c, nthreads=16), f"v2-lite prompt {q_len} at {start}")
 
 
 @pytest.mark.parametrize("B,q_len,H,lens,qdt,ldt", [
@@ -127,42 +136,39 @@ def test_host_length_hint_matches_no_hint(device):
     C.assert_close(bb, C.mla_ref(c, nthreads=8), "hint")
 
 
-@pytest.mark.parametrize("variant", [2, 3, 4, 5])
+@pytest.mark.parametrize("kernel", [_capi.MLA_KERNEL_ROWS, _capi.MLA_KERNEL_WS])
 @pytest.mark.parametrize("B,q_len,H,lens", [
     (2, 1, 128, [700, 33]),
     (1, 5, 128, [4]),
     (2, 2, 64, [700, 129]),
     (3, 1, 96, [1, 300, 2050]),
 ])
-def test_kernel_variants(device, monkeypatch, variant, B, q_len, H, lens):
-    # every 16-bit kernel variant, whichever one the planner would pick
-    monkeypatch.setenv("MUGEN_ATTN_MLA_VARIANT", str(variant))
+def test_kernel_variants(device, kernel, B, q_len, H, lens):
+    # both 16-bit-q kernels, whichever one the planner would pick
     c = C.mla_case(80 + H, B, q_len, H, lens, q_dtype=C.BF16, lat_dtype=C.BF16)
     ref = C.mla_ref(c)
     for splits in (0, 1, 4):
-        C.assert_close(run_gpu(c, device, C.F32, splits), ref, f"variant {variant} splits={splits}")
+        C.assert_close(run_gpu(c, device, C.F32, splits, kernel=kernel), ref, f"kernel {kernel} splits={splits}")
 
 
-@pytest.mark.parametrize("variant", [1, 5])
+@pytest.mark.parametrize("kernel", [_capi.MLA_KERNEL_ROWS, _capi.MLA_KERNEL_WS])
 @pytest.mark.parametrize("B,q_len,H,lens,ldt", [
     (2, 1, 128, [700, 33], C.BF16),
     (2, 3, 128, [3, 100], C.F16),
     (3, 1, 96, [1, 300, 2050], C.F16),
     (1, 1, 16, [1024], C.F16),
 ])
-def test_fp32_q_variants(device, monkeypatch, variant, B, q_len, H, lens, ldt):
+def test_fp32_q_variants(device, kernel, B, q_len, H, lens, ldt):
     # fp32 q (the absorbed q of the full operator): the hi + lo split in the
     # 4-wave and the warp-specialised kernels
-    monkeypatch.setenv("MUGEN_ATTN_MLA_VARIANT", str(variant))
     c = C.mla_case(90 + H, B, q_len, H, lens, q_dtype=C.F32, lat_dtype=ldt)
     ref = C.mla_ref(c)
     for splits in (0, 1, 4):
-        C.assert_close(run_gpu(c, device, C.F32, splits), ref, f"fp32 q variant {variant} splits={splits}")
+        C.assert_close(run_gpu(c, device, C.F32, splits, kernel=kernel), ref, f"fp32 q kernel {kernel} splits={splits}")
 
 
-def test_fp32_q_overshoot_fallback(device, monkeypatch):
+def test_fp32_q_overshoot_fallback(device):
     # the exact-recompute path with fp32 q in the warp-specialised kernel
-    monkeypatch.setenv("MUGEN_ATTN_MLA_VARIANT", "5")
     c = C.mla_case(62, 2, 1, 128, [900, 300], q_dtype=C.F32, lat_dtype=C.F16)
     lat = c["lat"].copy()
     lat[0, 700, :] = 0.0
@@ -171,13 +177,12 @@ def test_fp32_q_overshoot_fallback(device, monkeypatch):
     q = c["q"].copy()
     q[:, :, :, 0] = np.abs(q[:, :, :, 0]) + 1.0
     c2 = dict(c, lat=lat, latb=latb, q=q)
-    C.assert_close(run_gpu(c2, device, C.F32, 0), C.mla_ref(c2), "fp32 q overshoot")
+    C.assert_close(run_gpu(c2, device, C.F32, 0, kernel=_capi.MLA_KERNEL_WS), C.mla_ref(c2), "fp32 q overshoot")
 
 
-@pytest.mark.parametrize("variant", [3, 5])
-def test_variant_overshoot_fallback(device, monkeypatch, variant):
-    # the exact-recompute flag path of the 16-bit variants (R = 128 rows)
-    monkeypatch.setenv("MUGEN_ATTN_MLA_VARIANT", str(variant))
+@pytest.mark.parametrize("kernel", [_capi.MLA_KERNEL_ROWS, _capi.MLA_KERNEL_WS])
+def test_variant_overshoot_fallback(device, kernel):
+    # the exact-recompute flag path of both 16-bit-q kernels (R = 128 rows)
     c = C.mla_case(61, 2, 1, 128, [900, 300], q_dtype=C.BF16, lat_dtype=C.BF16)
     lat = c["lat"].copy()
     lat[0, 700, :] = 0.0
@@ -187,4 +192,4 @@ def test_variant_overshoot_fallback(device, monkeypatch, variant):
     q[:, :, :, 0] = np.abs(q[:, :, :, 0]) + 1.0
     q, qb = O.round_to(q, C.BF16)
     c2 = dict(c, lat=lat, latb=latb, q=q, qb=qb)
-    C.assert_close(run_gpu(c2, device, C.F32, 0), C.mla_ref(c2), f"variant {variant} overshoot")
+    C.assert_close(run_gpu(c2, device, C.F32, 0, kernel=kernel), C.mla_ref(c2), f"kernel {kernel} overshoot")

@@ -5,20 +5,21 @@ import pytest
 import torch
 
 import mugen_amd
+from mugen_amd import _capi
 from tests import cases as C
 
 pytestmark = pytest.mark.gpu
 
 
-def run_gpu(c, device, out_dtype=None, causal=True):
+def run_gpu(c, device, out_dtype=None, causal=True, kernel=0):
     out_dtype = c["dtype"] if out_dtype is None else out_dtype
     C.say(f"prefill N={c['N']} H={c['H']} Hk={c['Hk']} D={c['D']} start={c['start']} dtype={c['dtype']} "
-          f"out={out_dtype} causal={causal}")
+          f"out={out_dtype} causal={causal} kernel={kernel}")
     q = C.to_dev(c["qb"], c["dtype"], device)
     k = C.to_dev(c["kb"], c["dtype"], device)
     v = C.to_dev(c["vb"], c["dtype"], device)
     out = mugen_amd.flash_prefill_attention(q, k, v, c["start"], causal=causal,
-                                            out_dtype=C.torch_dtype(out_dtype))
+                                            out_dtype=C.torch_dtype(out_dtype), kernel=kernel)
     torch.cuda.synchronize()
     return out.float().cpu().numpy()
 
@@ -39,6 +40,14 @@ def test_llama1b_config(device):
 def test_shapes_and_offsets(device, N, H, Hk, D, start, dtype):
     c = C.prefill_case(50 + N, N, H, Hk, D, start, dtype)
     C.assert_close(run_gpu(c, device, C.F32), C.prefill_ref(c), f"prefill N={N} start={start}")
+
+
+@pytest.mark.parametrize("dtype", [C.F16, C.BF16])
+def test_default_routed_ws_16bit_out(device, dtype):
+    # 1024..4096 tokens route to the warp-specialised kernel by default; G = 7
+    # (Qwen2.5-7B heads) and the 16-bit output store
+    c = C.prefill_case(57, 1100, 28, 4, 128, 0, dtype)
+    C.assert_close(run_gpu(c, device, dtype), C.prefill_ref(c, nthreads=8), f"default-routed ws out={dtype}")
 
 
 def test_non_causal(device):
@@ -62,19 +71,20 @@ def test_golden_fixture(device):
     (512, 32, 8, 64, 0, C.BF16), (40, 28, 4, 128, 100, C.F16), (200, 8, 1, 128, 300, C.BF16),
     (65, 12, 3, 64, 0, C.F16), (300, 28, 4, 128, 0, C.BF16), (33, 16, 2, 64, 5, C.BF16),
 ])
-def test_warp_specialised_variant(device, monkeypatch, N, H, Hk, D, start, dtype):  # forced on short prompts
+def test_warp_specialised_variant(device, N, H, Hk, D, start, dtype):  # forced on short prompts
     # the S / PV warp-specialised kernel (4 or 8 heads per block, G = 1, 4, 7,
-    # 8), against the same oracle
-    monkeypatch.setenv("MUGEN_ATTN_PREFILL_VARIANT", "2")
+    # 8), against the same oracle, with fp32 and 16-bit outputs
     c = C.prefill_case(70 + N, N, H, Hk, D, start, dtype)
-    C.assert_close(run_gpu(c, device, C.F32), C.prefill_ref(c), f"ws prefill N={N} start={start}")
+    ref = C.prefill_ref(c)
+    for odt in (C.F32, dtype):
+        C.assert_close(run_gpu(c, device, odt, kernel=_capi.PREFILL_KERNEL_WS), ref,
+                       f"ws prefill N={N} start={start} out={odt}")
 
 
-def test_warp_specialised_non_causal(device, monkeypatch):
-    monkeypatch.setenv("MUGEN_ATTN_PREFILL_VARIANT", "2")
+def test_warp_specialised_non_causal(device):
     c = C.prefill_case(52, 33, 14, 2, 128, 0, C.BF16)
     from oracle import oracle as O
     ref = O.gqa_attention(c["q"], c["k"].reshape(1, c["kv_len"], 2, 128).repeat(33, 0),
                           c["v"].reshape(1, c["kv_len"], 2, 128).repeat(33, 0), [c["kv_len"]] * 33, 14, 2, 128,
                           c["kv_len"] * 2 * 128)
-    C.assert_close(run_gpu(c, device, C.F32, causal=False), ref, "ws non-causal")
+    C.assert_close(run_gpu(c, device, C.F32, causal=False, kernel=_capi.PREFILL_KERNEL_WS), ref, "ws non-causal")
