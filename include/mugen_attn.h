@@ -291,6 +291,22 @@ int mugen_attn_mla_decode(const mugen_attn_mla_decode_args* args, void* workspac
                           size_t workspace_bytes, void* stream);
 
 /*
+ * mugen_attn_mla_decode without a workspace argument and without any
+ * allocation: the split partials go to a fixed device scratch that the
+ * library holds per GPU (MUGEN_ATTN_MLA_SCRATCH_BYTES, until the process
+ * ends).  No counterpart in the reference: this entry point is for callers
+ * that cannot allocate -- code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  Same arguments, semantics and results
+ * as mugen_attn_mla_decode; a call whose workspace size
+ * (mugen_attn_mla_decode_workspace_size) exceeds the scratch fails with
+ * MUGEN_ATTN_E_WORKSPACE.  Every call on one GPU shares that GPU's scratch:
+ * calls that overlap on one GPU (two streams, two threads) race; serialise
+ * them on one stream.  Nothing in the scratch needs clearing between calls.
+ */
+#define MUGEN_ATTN_MLA_SCRATCH_BYTES (32u << 20) /* 32 MiB: DeepSeek-V3 decode B8 needs 23 MiB */
+int mugen_attn_mla_decode_noalloc(const mugen_attn_mla_decode_args* args, void* stream);
+
+/*
  * MLA absorption and up-projection: the rest of cpu_mla_attention
  * (transformer.cpp:2539-2623) around the latent core above, so that
  *   mugen_attn_mla_absorb -> mugen_attn_mla_decode (q F32) -> mugen_attn_mla_project

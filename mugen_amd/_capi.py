@@ -21,6 +21,7 @@ F32, F16, BF16 = 0, 1, 2
 W_F16, W_Q4_0, W_Q8_0 = 1, 2, 8  # weight encodings (GGML type ids)
 MLA_KERNEL_ROWS, MLA_KERNEL_WS = 1, 2  # mugen_attn_mla_decode_args.kernel
 PREFILL_KERNEL_BLOCK, PREFILL_KERNEL_WS = 1, 2  # mugen_attn_gqa_prefill_args.kernel
+MLA_SCRATCH_BYTES = 32 << 20  # MUGEN_ATTN_MLA_SCRATCH_BYTES: the fixed scratch of mugen_attn_mla_decode_noalloc
 
 # every symbol include/mugen_attn.h declares
 EXPORTS = (
@@ -32,6 +33,7 @@ EXPORTS = (
     "mugen_attn_gqa_decode_q4",
     "mugen_attn_mla_decode_workspace_size",
     "mugen_attn_mla_decode",
+    "mugen_attn_mla_decode_noalloc",
     "mugen_attn_mla_absorb",
     "mugen_attn_mla_project",
     "mugen_attn_mla_latent_write",
@@ -173,6 +175,8 @@ def lib() -> ctypes.CDLL:
         L.mugen_attn_mla_decode_workspace_size.restype = ctypes.c_size_t
         L.mugen_attn_mla_decode.argtypes = [ctypes.POINTER(MlaDecodeArgs), _vp, ctypes.c_size_t, _vp]
         L.mugen_attn_mla_decode.restype = ctypes.c_int
+        L.mugen_attn_mla_decode_noalloc.argtypes = [ctypes.POINTER(MlaDecodeArgs), _vp]
+        L.mugen_attn_mla_decode_noalloc.restype = ctypes.c_int
         L.mugen_attn_mla_absorb.argtypes = [ctypes.POINTER(MlaAbsorbArgs), _vp]
         L.mugen_attn_mla_absorb.restype = ctypes.c_int
         L.mugen_attn_mla_project.argtypes = [ctypes.POINTER(MlaProjectArgs), _vp]

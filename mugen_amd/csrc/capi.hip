@@ -574,9 +574,12 @@ size_t mugen_attn_mla_decode_workspace_size(const mugen_attn_mla_decode_args* a)
     return mla_ws(a, mla_chunk(a, mla_kernel(a)), nullptr);
 }
 
-int mugen_attn_mla_decode(const mugen_attn_mla_decode_args* a, void* ws, size_t ws_bytes, void* stream) {
-    int rc = mla_validate(a);
-    if (rc) return rc;
+}  // extern "C"
+
+// The MLA decode call behind both entry points: `ws` is the caller's
+// workspace or the library's fixed scratch.
+static int mla_decode_impl(const mugen_attn_mla_decode_args* a, void* ws, size_t ws_bytes, void* stream,
+                           KernelTimer* timer) {
     const int kernel = mla_kernel(a);
     const int chunk = mla_chunk(a, kernel);
     int splits = 1;
@@ -608,8 +611,59 @@ int mugen_attn_mla_decode(const mugen_attn_mla_decode_args* a, void* ws, size_t 
         p.ws_ml = base + sb * (size_t)p.nq * 16 * 512 / 2;  // after the fp16 O blob
     }
     hipError_t e = launch_mla_decode(p, kernel, a->q_dtype, a->latent_dtype, a->out_dtype,
-                                     static_cast<hipStream_t>(stream), active_timer());
+                                     static_cast<hipStream_t>(stream), timer);
     return hip_status(e, "mla_decode launch");
+}
+
+// Fixed device scratch of mugen_attn_mla_decode_noalloc: every GPU the
+// library runs on holds its own copy of this array until the process ends.
+// Host code must not use the array's name as a device address (it is a
+// host-side stand-in): the per-device address comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+static __device__ __align__(256) char mla_scratch[MUGEN_ATTN_MLA_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+static int scratch_for_current_device(void** out) {
+    int dev = -1;
+    if (int rc = hip_status(hipGetDevice(&dev), "mla_decode_noalloc: hipGetDevice")) return rc;
+    if (dev < 0 || dev >= kMaxDevices) return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_decode_noalloc: device %d", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        if (int rc = hip_status(hipGetSymbolAddress(&ptr, HIP_SYMBOL(mla_scratch)),
+                                "mla_decode_noalloc: hipGetSymbolAddress"))
+            return rc;
+        if (!ptr) return fail(MUGEN_ATTN_E_HIP, "mla_decode_noalloc: no scratch address");
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return MUGEN_ATTN_OK;
+}
+
+extern "C" {
+
+int mugen_attn_mla_decode(const mugen_attn_mla_decode_args* a, void* ws, size_t ws_bytes, void* stream) {
+    if (int rc = mla_validate(a)) return rc;
+    return mla_decode_impl(a, ws, ws_bytes, stream, active_timer());
+}
+
+int mugen_attn_mla_decode_noalloc(const mugen_attn_mla_decode_args* a, void* stream) {
+    if (int rc = mla_validate(a)) return rc;
+    const size_t need = mla_ws(a, mla_chunk(a, mla_kernel(a)), nullptr);
+    if (need > (size_t)MUGEN_ATTN_MLA_SCRATCH_BYTES)
+        return fail(MUGEN_ATTN_E_WORKSPACE,
+                    "mla_decode_noalloc: the call needs %zu bytes of scratch, the fixed scratch holds %zu "
+                    "(use mugen_attn_mla_decode with a workspace)",
+                    need, (size_t)MUGEN_ATTN_MLA_SCRATCH_BYTES);
+    void* ws = nullptr;
+    if (int rc = scratch_for_current_device(&ws)) return rc;
+    // no event timing here: this entry point creates nothing
+    return mla_decode_impl(a, ws, MUGEN_ATTN_MLA_SCRATCH_BYTES, stream, nullptr);
 }
 
 // yarn_rope_freq (transformer.cpp:41-70) in the same float operations, so
