@@ -252,9 +252,11 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* args, void* stream
  *   scale   must be > 0 (the reference uses 1/sqrt(qk_nope + qk_rope),
  *           transformer.cpp:2550; 1/sqrt(192) for DeepSeek V2/V3)
  *
- * Supported: kv_rank 512, rope_dim 64; latent dtype F16 or BF16; q dtype
- * F32 (split into two 16-bit halves, fp32-accurate) or equal to the latent
- * dtype; out_dtype F32, F16 or BF16.
+ * Supported: kv_rank 512, rope_dim 64; latent dtype F16 or BF16 (bf16
+ * latent values must lie within +-65504, the f16 range: the split partials
+ * are f16, and values beyond it come out as inf); q dtype F32 (split into
+ * two 16-bit halves, fp32-accurate) or equal to the latent dtype;
+ * out_dtype F32, F16 or BF16.
  */
 typedef struct mugen_attn_mla_decode_args {
     const void* q;

@@ -27,6 +27,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x2v_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
 
 enum { DT_F32 = MUGEN_ATTN_F32, DT_F16 = MUGEN_ATTN_F16, DT_BF16 = MUGEN_ATTN_BF16 };
 

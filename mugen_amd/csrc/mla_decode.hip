@@ -24,11 +24,11 @@
 //    never leaves registers;
 //  * the P.L B operand (8 tokens of one latent dim per lane) comes from the
 //    row-major tile through two ds_read_b64_tr_b16 transpose reads;
-//  * softmax in the exp2 domain against a reference max fixed at each row's
-//    first visible tile: later weights may exceed 1 (bf16 P keeps fp32's
-//    exponent range), so O is never rescaled.  A row whose score overshoots
-//    the reference by the dtype's headroom is flagged (NaN max) and the
-//    combine kernel recomputes that (row, split) exactly in fp32;
+//  * softmax in the exp2 domain against a reference max set at each row's
+//    first visible tile: later weights may exceed 1, so O is normally never
+//    rescaled.  Only a score more than the weights' headroom above the
+//    reference (rare) moves the row's reference up to that tile's max and
+//    scales the row's sum and O by 2^(old - new) ("lazy re-base");
 //  * every workgroup writes its split's (m, l) in fp32 and the normalised
 //    o/l (a convex combination of latent rows) in fp16, in accumulator-
 //    fragment order; mla_decode_combine merges the splits of a row with
@@ -65,9 +65,9 @@ __host__ __device__ constexpr int swz(int r) {
     return (((r >> 1) & 1) * 2) ^ (((r >> 3) & 1) * 4);
 }
 
-// Reference-max headroom (log2 units): with the max fixed at the first
-// visible tile, later weights may reach 2^TH.  bf16 P keeps fp32's exponent
-// range (O stays far from fp32 overflow); fp16 P tops out at 65504.
+// Reference-max headroom (log2 units): weights up to 2^TH are kept against
+// a row's reference; a larger score re-bases the row.  bf16 P keeps fp32's
+// exponent range (O stays far from fp32 overflow); fp16 P tops out at 65504.
 template <int DT>
 __device__ constexpr float headroom_log2() { return DT == DT_BF16 ? 64.f : 15.f; }
 
@@ -81,28 +81,10 @@ __device__ __forceinline__ int64_t blob_pair(const MlaParams& p, int b, int s, i
     return ((((int64_t)b * p.num_splits + s) * p.nq + q) * 16 + dp) * 64 + lane;
 }
 
-// S-chain MFMA with a VGPR accumulator (FIRST: C = 0)
-template <int DT, bool FIRST>
-__device__ __forceinline__ void mfma_s(f32x4_t& acc, const u32x4_t& a, const u32x4_t& b) {
-    if constexpr (FIRST) {
-        if constexpr (DT == DT_BF16)
-            asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b));
-        else
-            asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b));
-    } else {
-        if constexpr (DT == DT_BF16)
-            asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
-        else
-            asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
-    }
-}
-
 // Kernel "rows" (16-bit q, at most 64 query rows: small-head decode):
 // workgroup = (64 query rows, context split, sequence), 4 waves of 16
-// rows, one wave per SIMD.  Each wave keeps the q of its rows in VGPRs (B
-// operand of S^T = L . Q^T) and its 16 x 512 O in AGPRs; the S MFMAs are
-// issued from inline asm with VGPR accumulators so that the O accumulator
-// alone owns the AGPR file.
+// rows, one wave per SIMD.  Each wave keeps the q of its rows in registers
+// (B operand of S^T = L . Q^T) and its 16 x 512 O accumulator.
 template <int QDT, int DT>
 __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     constexpr int KS = kCD / 32;  // 18 k-steps over the 576 dims
@@ -293,10 +275,8 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
             for (int nb = 0; nb < 2; nb++) {
                 const u32x4_t a = abuf[ks % SPD][nb];
 #pragma unroll
-                for (int qq = 0; qq < NQ; qq++) {
-                    if (ks == 0 && qq == 0) mfma_s<DT, true>(sacc[nb], a, qf[qq][ks]);
-                    else mfma_s<DT, false>(sacc[nb], a, qf[qq][ks]);
-                }
+                for (int qq = 0; qq < NQ; qq++)
+                    sacc[nb] = mfma16x16x32<DT>(a, qf[qq][ks], (ks == 0 && qq == 0) ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sacc[nb]);
             }
             if (ks + SPD < KS) {
                 abuf[ks % SPD][0] = *a_ptr(ks + SPD, 0);
@@ -305,6 +285,8 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
 #pragma unroll
             for (int k = 0; k < DPW; k++)
                 if ((k * KS) / DPW == ks) issue_k(k);
+            // keep each step's reads SPD steps ahead of their MFMAs
+            __builtin_amdgcn_sched_barrier(0);
         }
         // first P.L operands requested now, to land during the softmax
         constexpr int VPD = 6;
@@ -317,12 +299,6 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
         u32x4_t bbuf[VPD];
 #pragma unroll
         for (int j = 0; j < VPD; j++) bbuf[j] = tr_load(j);
-        // The asm MFMAs are hidden from the compiler's hazard recognizer.  A
-        // VALU read of an MFMA result must wait for the MFMA to complete: a
-        // 16x16x32 MFMA (8 passes) writes its accumulator up to 18 cycles
-        // after issue, so 19 wait states (s_nop 7, 7, 3 = 8 + 8 + 4 - 1)
-        // precede the softmax's first read of sacc.
-        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(sacc[0]), "+v"(sacc[1]));
 
         // ---- softmax weights; lane holds tokens tt + 8g + (4nb + i) of row n.
         // A row's reference max is the max of its first visible tile (a
@@ -344,11 +320,10 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
             mt = max_x32(max_x16(mt));
             if (m_ref == kNegInf) m_ref = mt;  // O of this row is still 0
         }
-        u32x4_t pfrag;
-        auto weights = [&](auto masked_tag) {
+        const float mneg = (m_ref == kNegInf) ? 0.f : -m_ref;
+        float x[8];  // scores relative to the reference (log2 units), then weights
+        auto rel = [&](auto masked_tag) {
             constexpr bool MASKED = decltype(masked_tag)::value;
-            const float mneg = (m_ref == kNegInf) ? 0.f : -m_ref;
-            float x[8];
 #pragma unroll
             for (int nb = 0; nb < 2; nb++) {
 #pragma unroll
@@ -358,15 +333,40 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
                         const int tok = tt + 8 * g + 4 * nb + i;
                         v = (tok < t_end && tok < teff) ? v : kNegInf;
                     }
-                    x[4 * nb + i] = fast_exp2(v);
+                    x[4 * nb + i] = v;
                 }
             }
-            l_part += ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
-            pfrag = u32x4_t{pack2<DT>(x[0], x[1]), pack2<DT>(x[2], x[3]), pack2<DT>(x[4], x[5]), pack2<DT>(x[6], x[7])};
         };
         // wave-uniform: interior tiles (the common case) carry no mask
-        if (tt + kTT <= t_end && tt + kTT <= teff_min) weights(std::false_type{});
-        else weights(std::true_type{});
+        if (tt + kTT <= t_end && tt + kTT <= teff_min) rel(std::false_type{});
+        else rel(std::true_type{});
+        // Lazy re-base (rare): a score more than TH above its row's
+        // reference would overflow the 16-bit weights, so the row's
+        // reference moves up to the tile's max and its sum and O so far
+        // scale by alpha = 2^(old - new)
+        bool over = false;
+#pragma unroll
+        for (int e = 0; e < 8; e++) over |= x[e] > TH;
+        if (__any(over)) {  // wave-uniform
+            float mt = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+            mt = max_x32(max_x16(mt));
+            const float shift = fmaxf(mt, 0.f);
+            const float alpha = fast_exp2(-shift);
+            m_ref += shift;
+            l_part *= alpha;
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] -= shift;
+            f32x4_t a4;  // the factors of O rows 4g+i
+#pragma unroll
+            for (int i = 0; i < 4; i++) a4[i] = __shfl(alpha, 4 * g + i, 64);
+#pragma unroll
+            for (int d = 0; d < 32; d++) o[d] *= a4;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[e] = fast_exp2(x[e]);
+        l_part += ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
+        const u32x4_t pfrag =
+            u32x4_t{pack2<DT>(x[0], x[1]), pack2<DT>(x[2], x[3]), pack2<DT>(x[4], x[5]), pack2<DT>(x[6], x[7])};
 
         // ---- O += P . L[:, 0:512]; B operand L[tt + 8g + j][16d + n], j < 8.
         // The schedule is pinned to [MFMA][2 transpose reads of d+VPD] so
@@ -382,19 +382,15 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     }
 
     // ---- epilogue: (m, l, o/l) partial of this split.  The normalised O is
-    // a convex combination of latent rows and goes out as fp16 in
-    // accumulator-fragment order (4 rows x 1 column per lane, 512 B
-    // contiguous per store instruction); m and l stay fp32.  A row whose
-    // weights or normalised values left the 16-bit ranges is flagged (NaN m)
-    // for the exact fp32 recompute in the combine kernel.
+    // a convex combination of latent rows (within their f16 range) and goes
+    // out as fp16 in accumulator-fragment order (4 rows x 1 column per lane,
+    // 512 B contiguous per store instruction); m and l stay fp32.
     MUGEN_TRACE(3);
     const float lrow = sum_x32(sum_x16(l_part));  // S-layout row n: the split's full sum
     const float c0 = lrow > 0.f ? 1.f / lrow : 0.f;
-    const bool ovf = !(lrow <= exp2f(TH));  // every weight is <= l
     float k0[4];  // the factors of O rows 4g+i
 #pragma unroll
     for (int i = 0; i < 4; i++) k0[i] = __shfl(c0, 4 * g + i, 64);
-    float vmax = 0.f;  // largest |o/l| this lane stores
     if (row0 < p.R) {
         u32x4_t* dst = reinterpret_cast<u32x4_t*>(p.ws_o) + blob_pair(p, b, s, row0 >> 4, 0, lane);
 #pragma unroll
@@ -403,23 +399,15 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
 #pragma unroll
             for (int e = 0; e < 2; e++) {
                 const f32x4_t v = o[d + e] * f32x4_t{k0[0], k0[1], k0[2], k0[3]};
-                vmax = fmaxf(vmax, fmaxf(fabsf(v[0]), fabsf(v[1])));
-                vmax = fmaxf(vmax, fmaxf(fabsf(v[2]), fabsf(v[3])));
                 h[2 * e] = pack2<DT_F16>(v[0], v[1]);
                 h[2 * e + 1] = pack2<DT_F16>(v[2], v[3]);
             }
             dst[(d >> 1) * 64] = u32x4_t{h[0], h[1], h[2], h[3]};
         }
     }
-    // fp16 partials: a normalised value past 65000 cannot be stored (only
-    // bf16 latent rows can be that large); flagged like an overshoot
-    const uint64_t big_mask = __ballot(!(vmax <= 65000.f));
-    // rows 4g+i of a lane overflowed -> tell their S-layout lanes (row n)
-    const bool row_big = (big_mask >> (n >> 2) * 16) & 0xffffull;  // any lane of quad n/4
     if (g == 0 && row_ok) {
-        // a weight past the headroom may have overflowed its 16-bit P
         const int64_t slot_ml = ((int64_t)b * p.num_splits + s) * p.R + row;
-        p.ws_ml[slot_ml * 2 + 0] = (ovf || row_big) ? __builtin_nanf("") : m_ref;
+        p.ws_ml[slot_ml * 2 + 0] = m_ref;
         p.ws_ml[slot_ml * 2 + 1] = lrow;
     }
     MUGEN_TRACE(5);
@@ -456,8 +444,8 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
     constexpr int PBUF = 4 * 64 * 16;     // one P buffer: 4 row blocks x 64 lanes x 16 B
     __shared__ __attribute__((aligned(1024))) char ring[NSLOT * kTileBytes + 2 * PBUF];
     __shared__ float2 ml_x[64];           // per row: (reference max, sum) from the S waves
-    __shared__ int ovf_x[64];
-    __shared__ uint64_t big_x[4][4];      // [PV wave][row block] overflow ballots
+    __shared__ __attribute__((aligned(16))) float rs_alpha[2][64];  // per tile parity and row: O's re-base factor
+    __shared__ __attribute__((aligned(16))) int rs_flag[2][4];  // per tile parity and S wave: any row re-based
 
     // work mapping: as mla_decode_kernel (XCD-blocked active groups)
     const int nxcd = 8;
@@ -545,6 +533,7 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
         int teff_min = teff;
 #pragma unroll
         for (int m = 1; m < 64; m <<= 1) teff_min = min(teff_min, __shfl_xor(teff_min, m, 64));
+        teff_min = __builtin_amdgcn_readfirstlane(teff_min);  // wave-uniform: the mask test branches on it
         // q is waited for chunk by chunk in the first tile's k-loop
         MUGEN_TRACE(1);
         const int ar0 = 8 * (n >> 2) + (n & 3);
@@ -589,15 +578,17 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
                 for (int nb = 0; nb < 2; nb++)
 #pragma unroll
                     for (int qq = 0; qq < NQ; qq++) {
-                        if (ks == 0 && qq == 0) mfma_s<DT, true>(sacc[nb], abuf[ks % SPD][nb], qf[qq][ks]);
-                        else mfma_s<DT, false>(sacc[nb], abuf[ks % SPD][nb], qf[qq][ks]);
+                        sacc[nb] = mfma16x16x32<DT>(abuf[ks % SPD][nb], qf[qq][ks],
+                                                    (ks == 0 && qq == 0) ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sacc[nb]);
                     }
                 if (ks + SPD < KS) {
                     abuf[ks % SPD][0] = *a_ptr(ks + SPD, 0);
                     abuf[ks % SPD][1] = *a_ptr(ks + SPD, 1);
                 }
+                // keep each step's reads SPD steps ahead of their MFMAs (the
+                // scheduler would otherwise sink them next to their use)
+                __builtin_amdgcn_sched_barrier(0);
             }
-            asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(sacc[0]), "+v"(sacc[1]));
             if (j == 4) MUGEN_TRACE(11);
             // softmax weights against the row's reference max (the max of its
             // first visible tile); lane holds tokens tt + 8g + 4nb + i of row n
@@ -614,40 +605,61 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
                 if (m_ref == kNegInf) m_ref = mt;
             }
             const float mneg = (m_ref == kNegInf) ? 0.f : -m_ref;
-            const bool masked = !(tt + kTT <= t_end && tt + kTT <= teff_min);
-            float x[8];
+            float x[8];  // scores relative to the reference (log2 units), then weights
+            auto rel = [&](auto masked_tag) {
+                constexpr bool MASKED = decltype(masked_tag)::value;
 #pragma unroll
-            for (int nb = 0; nb < 2; nb++)
+                for (int nb = 0; nb < 2; nb++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    float v = fmaf(sacc[nb][i], p.scale_log2, mneg);
-                    if (masked) {
-                        const int tok = tt + 8 * g + 4 * nb + i;
-                        v = (tok < t_end && tok < teff) ? v : kNegInf;
+                    for (int i = 0; i < 4; i++) {
+                        float v = fmaf(sacc[nb][i], p.scale_log2, mneg);
+                        if constexpr (MASKED) {
+                            const int tok = tt + 8 * g + 4 * nb + i;
+                            v = (tok < t_end && tok < teff) ? v : kNegInf;
+                        }
+                        x[4 * nb + i] = v;
                     }
-                    x[4 * nb + i] = fast_exp2(v);
-                }
+            };
+            // wave-uniform branch: interior tiles (the common case) carry no mask
+            if (tt + kTT <= t_end && tt + kTT <= teff_min) rel(std::false_type{});
+            else rel(std::true_type{});
+            // Lazy re-base: a score more than TH above its row's reference
+            // would overflow the 16-bit weights, so the row's reference moves
+            // up to the tile's max: its weights and sum so far scale by
+            // alpha = 2^(old - new), and the PV waves scale the row's O by
+            // the same alpha before they add this tile (rare: only scores
+            // that climb far above the first tile's take this branch)
+            bool over = false;
+#pragma unroll
+            for (int e = 0; e < 8; e++) over |= x[e] > TH;
+            const bool rebase = __any(over);  // wave-uniform
+            if (rebase) {
+                float mt = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+                mt = max_x32(max_x16(mt));            // the row's tile max, relative to its reference
+                const float shift = fmaxf(mt, 0.f);  // rows under their reference keep it
+                const float alpha = fast_exp2(-shift);
+                m_ref += shift;
+                l_part *= alpha;
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[e] -= shift;
+                if (g == 0) rs_alpha[j & 1][16 * wr + n] = alpha;
+            }
+            if (lane == 0) rs_flag[j & 1][wr] = rebase ? 1 : 0;
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] = fast_exp2(x[e]);
             l_part += ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
             *reinterpret_cast<u32x4_t*>(pbuf + (j & 1) * PBUF + (wr * 64 + lane) * 16) =
                 u32x4_t{pack2<DT>(x[0], x[1]), pack2<DT>(x[2], x[3]), pack2<DT>(x[4], x[5]), pack2<DT>(x[6], x[7])};
             if (j == 4) MUGEN_TRACE(12);
         }
         MUGEN_TRACE(3);
-        // epilogue 1: the row's (reference max, sum) and headroom flag for the PV waves
+        // epilogue 1: the row's (reference max, sum) for the PV waves
         const float lrow = sum_x32(sum_x16(l_part));
-        if (g == 0) {
-            ml_x[16 * wr + n] = make_float2(m_ref, lrow);
-            ovf_x[16 * wr + n] = !(lrow <= exp2f(TH));
-        }
+        if (g == 0) ml_x[16 * wr + n] = make_float2(m_ref, lrow);
         __syncthreads();  // E1
-        __syncthreads();  // E2: the PV waves stored o/l and their overflow ballots
-        uint64_t big = 0;
-#pragma unroll
-        for (int q = 0; q < 4; q++) big |= big_x[q][wr];
-        const bool row_big = (big >> ((n >> 2) * 16)) & 0xffffull;
         if (g == 0 && ok) {
             const int64_t slot_ml = ((int64_t)b * p.num_splits + s) * p.R + rowq;
-            store_wt(&p.ws_ml[slot_ml * 2 + 0], (ovf_x[16 * wr + n] || row_big) ? __builtin_nanf("") : m_ref);
+            store_wt(&p.ws_ml[slot_ml * 2 + 0], m_ref);
             store_wt(&p.ws_ml[slot_ml * 2 + 1], lrow);
         }
         MUGEN_TRACE(5);
@@ -684,9 +696,23 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
             // O += P(j-1) . L(j-1)[:, 128wr .. +128]
             const char* tile = &ring[((j - 1) % NSLOT) * kTileBytes];
             const char* pb = pbuf + ((j - 1) & 1) * PBUF;
+            // the S waves re-based some rows for tile j-1 (rare): their O
+            // scales by the rows' factors before this tile is added
+            const i32x4_t fl = *reinterpret_cast<const i32x4_t*>(&rs_flag[(j - 1) & 1][0]);
             u32x4_t pa[4];
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) pa[mb] = *reinterpret_cast<const u32x4_t*>(pb + (mb * 64 + lane) * 16);
+            if (__builtin_amdgcn_readfirstlane(fl[0] | fl[1] | fl[2] | fl[3])) {
+#pragma unroll
+                for (int mb = 0; mb < 4; mb++) {
+                    // row block mb belongs to S wave mb; only a wave that
+                    // re-based wrote this tile's factors
+                    if (!__builtin_amdgcn_readfirstlane(fl[mb])) continue;
+                    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(&rs_alpha[(j - 1) & 1][16 * mb + 4 * g]);
+#pragma unroll
+                    for (int d = 0; d < 8; d++) o[mb][d] *= a;
+                }
+            }
             auto tr_load = [&](int d) {
                 const int cb = 8 * wr + d;
                 const char* tp = tile + t_off[cb & 3] + 128 * (cb >> 2);
@@ -708,10 +734,9 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
             if (j == 4) MUGEN_TRACE(12);
         }
         MUGEN_TRACE(3);
-        __syncthreads();  // E1: the S waves published (max, sum, flag) per row
+        __syncthreads();  // E1: the S waves published (max, sum) per row
         // epilogue: o/l in fp16, accumulator-fragment order (16-byte pairs
-        // of column blocks); rows whose normalised value does not fit fp16
-        // are flagged for the exact recompute
+        // of column blocks)
 #pragma unroll
         for (int mb = 0; mb < 4; mb++) {
             const int rblk = row0 + 16 * mb;
@@ -721,7 +746,6 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
                 const float l = ml_x[16 * mb + 4 * g + i].y;
                 k0[i] = l > 0.f ? 1.f / l : 0.f;
             }
-            float vmax = 0.f;
             if (rblk < p.R) {
                 u32x4_t* dst = reinterpret_cast<u32x4_t*>(p.ws_o) + blob_pair(p, b, s, rblk >> 4, 4 * wr, lane);
 #pragma unroll
@@ -730,84 +754,14 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
 #pragma unroll
                     for (int e = 0; e < 2; e++) {
                         const f32x4_t v = o[mb][d + e] * f32x4_t{k0[0], k0[1], k0[2], k0[3]};
-                        vmax = fmaxf(vmax, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
                         h[2 * e] = pack2<DT_F16>(v[0], v[1]);
                         h[2 * e + 1] = pack2<DT_F16>(v[2], v[3]);
                     }
                     store_wt(&dst[(d >> 1) * 64], u32x4_t{h[0], h[1], h[2], h[3]});
                 }
             }
-            const uint64_t bm = __ballot(!(vmax <= 65000.f));
-            if (lane == 0) big_x[wr][mb] = bm;
         }
-        __syncthreads();  // E2
         MUGEN_TRACE(5);
-    }
-}
-
-// Exact fp32 recompute of one (row, split) partial, for rows the main kernel
-// flagged: pass 1 finds the row max, pass 2 accumulates l and o, both over
-// batches of blockDim tokens (one token's 576-dim score per thread); each
-// thread then owns 512/blockDim output columns.
-template <int QDT, int DT>
-__device__ void mla_recompute_split(const MlaParams& p, int b, int row, int s, float* x_lds, float* red_lds) {
-    const int tid = threadIdx.x, nt = blockDim.x, nw = nt >> 6;
-    constexpr int kMaxCols = 8;  // 512 / 64: at least one wave per workgroup
-    const int ncols = kKR / nt;
-    const int T = clamp_len(p.seq_lens[b], p.max_T);
-    const int teff = T - p.q_len + row / p.H + 1;
-    const int t_begin = s * p.chunk;
-    const int t_end = min(min(t_begin + p.chunk, T), teff);
-    const uint16_t* lat = p.lat + (int64_t)b * p.seq_stride;
-    auto qval = [&](int d) -> float {
-        const int64_t i = ((int64_t)b * p.R + row) * kCD + d;
-        if constexpr (QDT == DT_F32) return static_cast<const float*>(p.q)[i];
-        else return to_f32<DT>(static_cast<const uint16_t*>(p.q)[i]);
-    };
-    auto score = [&](int t) -> float {
-        const uint16_t* c = lat + (int64_t)t * kCD;
-        float acc = 0.f;
-        for (int d = 0; d < kCD; d++) acc += qval(d) * to_f32<DT>(c[d]);
-        return acc * p.scale_log2;
-    };
-    float M = kNegInf;
-    for (int t0 = t_begin; t0 < t_end; t0 += nt) {
-        const int t = t0 + tid;
-        float v = wave_max(t < t_end ? score(t) : kNegInf);
-        if ((tid & 63) == 0) red_lds[tid >> 6] = v;
-        __syncthreads();
-        for (int w = 0; w < nw; w++) M = fmaxf(M, red_lds[w]);
-        __syncthreads();
-    }
-    float L = 0.f;
-    float O[kMaxCols] = {};
-    for (int t0 = t_begin; t0 < t_end; t0 += nt) {
-        const int t = t0 + tid;
-        x_lds[tid] = t < t_end ? fast_exp2(score(t) - M) : 0.f;
-        __syncthreads();
-        const int cnt = min(nt, t_end - t0);
-        for (int j = 0; j < cnt; j++) {
-            const float pw = x_lds[j];
-            L += pw;
-            const uint16_t* c = lat + (int64_t)(t0 + j) * kCD;
-            for (int k = 0; k < ncols; k++) O[k] += pw * to_f32<DT>(c[tid + k * nt]);
-        }
-        __syncthreads();
-    }
-    // normalised, fp16, fragment order; fp32 values beyond fp16 cannot come
-    // from a convex combination of finite 16-bit latent rows
-    uint16_t* blob = reinterpret_cast<uint16_t*>(p.ws_o);
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    for (int k = 0; k < ncols; k++) {
-        const int col = tid + k * nt;
-        const int lane = 16 * ((row & 15) >> 2) + (col & 15);
-        const int d = col >> 4;
-        blob[blob_pair(p, b, s, row >> 4, d >> 1, lane) * 8 + (d & 1) * 4 + (row & 3)] = from_f32<DT_F16>(O[k] * inv);
-    }
-    if (tid == 0) {
-        const int64_t slot = ((int64_t)b * p.num_splits + s) * p.R + row;
-        p.ws_ml[slot * 2 + 0] = M;
-        p.ws_ml[slot * 2 + 1] = L;
     }
 }
 
@@ -817,14 +771,11 @@ __device__ void mla_recompute_split(const MlaParams& p, int b, int row, int s, f
 // parallel); then lane l of wave w reads, per split, the fp16 fragments
 // (4 rows x 1 column) of column blocks 2w, 2w+1 -- the order the main
 // kernel wrote, 512 B contiguous per wave -- and accumulates in fp32.
-// Rows the main kernel flagged are recomputed first.
-template <int QDT, int DT, int OUT_DT>
+template <int OUT_DT>
 __global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
     __shared__ __attribute__((aligned(16))) float wts[kMaxMlaSplits][16];
     __shared__ float red[16][16];
     __shared__ float linv[16];
-    __shared__ float x_lds[256];
-    __shared__ int nflag;
     const int qb = blockIdx.x, dg = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, dsub = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
@@ -847,86 +798,53 @@ __global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
     };
     // split weights: thread (row r = tid%16, split phase sl = tid/16).  The
     // (m, l) of splits sl and sl + 16 are loaded once, ahead of the
-    // fragments; further splits are read from the workspace in the loops.  A
-    // NaN max marks a (row, split) the main kernel could not finish in 16
-    // bits; it is recomputed exactly (rare path), then the weights are redone.
+    // fragments; further splits are read from the workspace in the loops.
     const int r = tid & 15, sl = tid >> 4, row = qb * 16 + r;
     const bool rok = row < p.R;
     constexpr int MLC = 2;
     f32x2v_t mlc[MLC];
-    auto load_ml = [&]() {
 #pragma unroll
-        for (int k = 0; k < MLC; k++) {
-            const int s = sl + 16 * k;
-            mlc[k] = (rok && s < nact) ? *reinterpret_cast<const f32x2v_t*>(ml0 + s * ml_st + row * 2)
-                                       : f32x2v_t{kNegInf, 0.f};
-        }
-    };
-    load_ml();
+    for (int k = 0; k < MLC; k++) {
+        const int s = sl + 16 * k;
+        mlc[k] = (rok && s < nact) ? *reinterpret_cast<const f32x2v_t*>(ml0 + s * ml_st + row * 2)
+                                   : f32x2v_t{kNegInf, 0.f};
+    }
     prefetch();
-    for (int pass = 0; pass < 2; pass++) {
-        if (tid == 0) nflag = 0;
-        float mx = kNegInf;
-        bool bad = false;
+    float mx = kNegInf;
 #pragma unroll
-        for (int k = 0; k < MLC; k++) {
-            bad |= __builtin_isnan(mlc[k][0]);
-            mx = fmaxf(mx, mlc[k][0]);
-        }
-        for (int s = sl + 16 * MLC; s < nact; s += 16) {
-            const float m = rok ? ml0[s * ml_st + row * 2] : kNegInf;
-            bad |= __builtin_isnan(m);
-            mx = fmaxf(mx, m);
-        }
-        red[sl][r] = mx;
-        __syncthreads();
-        if (bad) nflag = 1;
-        float M = kNegInf;
+    for (int k = 0; k < MLC; k++) mx = fmaxf(mx, mlc[k][0]);
+    for (int s = sl + 16 * MLC; s < nact; s += 16) mx = fmaxf(mx, rok ? ml0[s * ml_st + row * 2] : kNegInf);
+    red[sl][r] = mx;
+    __syncthreads();
+    float M = kNegInf;
 #pragma unroll
-        for (int j = 0; j < 16; j++) M = fmaxf(M, red[j][r]);
-        __syncthreads();
-        if (nflag) {  // uniform: the flag was written before the barrier
-            for (int k = 0; k < 16 * nact; k++) {
-                const int rr = qb * 16 + (k & 15), ss = k >> 4;
-                const bool flagged = rr < p.R && __builtin_isnan(ml0[ss * ml_st + rr * 2]);
-                __syncthreads();
-                if (flagged) mla_recompute_split<QDT, DT>(p, b, rr, ss, x_lds, &red[0][0]);
-                __threadfence_block();
-                __syncthreads();
-            }
-            __threadfence();
-            __syncthreads();
-            load_ml();  // the recompute rewrote (m, l) and fragments
-            prefetch();
-            continue;
-        }
-        float sum = 0.f;
+    for (int j = 0; j < 16; j++) M = fmaxf(M, red[j][r]);
+    __syncthreads();
+    float sum = 0.f;
 #pragma unroll
-        for (int k = 0; k < MLC; k++) {
-            const int s = sl + 16 * k;
-            if (s < nact) {
-                const float wgt = (mlc[k][0] == kNegInf) ? 0.f : fast_exp2(mlc[k][0] - M) * mlc[k][1];
-                wts[s][r] = wgt;
-                sum += wgt;
-            }
-        }
-        for (int s = sl + 16 * MLC; s < nact; s += 16) {
-            const float m = rok ? ml0[s * ml_st + row * 2] : kNegInf;
-            const float wgt = (m == kNegInf) ? 0.f : fast_exp2(m - M) * ml0[s * ml_st + row * 2 + 1];
+    for (int k = 0; k < MLC; k++) {
+        const int s = sl + 16 * k;
+        if (s < nact) {
+            const float wgt = (mlc[k][0] == kNegInf) ? 0.f : fast_exp2(mlc[k][0] - M) * mlc[k][1];
             wts[s][r] = wgt;
             sum += wgt;
         }
-        red[sl][r] = sum;
-        __syncthreads();
-        if (tid < 16) {
-            float L = 0.f;
-#pragma unroll
-            for (int j = 0; j < 16; j++) L += red[j][tid];
-            linv[tid] = L > 0.f ? 1.f / L : 0.f;
-        }
-        __syncthreads();
-        break;
     }
+    for (int s = sl + 16 * MLC; s < nact; s += 16) {
+        const float m = rok ? ml0[s * ml_st + row * 2] : kNegInf;
+        const float wgt = (m == kNegInf) ? 0.f : fast_exp2(m - M) * ml0[s * ml_st + row * 2 + 1];
+        wts[s][r] = wgt;
+        sum += wgt;
+    }
+    red[sl][r] = sum;
+    __syncthreads();
+    if (tid < 16) {
+        float L = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) L += red[j][tid];
+        linv[tid] = L > 0.f ? 1.f / L : 0.f;
+    }
+    __syncthreads();
     MUGEN_TRACE(9);
 
     auto h4 = [](uint32_t a, uint32_t b) {
@@ -989,7 +907,7 @@ static hipError_t launch_mla_t(const MlaParams& p, int kernel, hipStream_t st, K
                        ? launch_k(t, "mla_decode", mla_decode_kernel<QDT, DT>, dim3(grid), dim3(256), st, p)
                        : launch_k(t, "mla_decode", mla_decode_ws_kernel<QDT, DT>, dim3(grid), dim3(512), st, p);
     if (e != hipSuccess) return e;
-    return launch_k(t, "mla_decode_combine", mla_decode_combine_kernel<QDT, DT, OUT_DT>, dim3(p.nq, 4, p.B),
+    return launch_k(t, "mla_decode_combine", mla_decode_combine_kernel<OUT_DT>, dim3(p.nq, 4, p.B),
                     dim3(256), st, p);
 }
 

@@ -104,9 +104,9 @@ def test_golden_fixture(device):
 
 @pytest.mark.parametrize("ldt,big", [(C.F16, 300.0), (C.BF16, 1000.0)])
 @pytest.mark.parametrize("splits", [0, 1])
-def test_late_score_overshoot_uses_exact_fallback(device, ldt, big, splits):
+def test_late_score_overshoot_rebases(device, ldt, big, splits):
     # a token far into the context scores far above every token of the first
-    # tile (beyond the weights' headroom): the flagged rows are recomputed
+    # tile (beyond the weights' headroom): the rows re-base in the kernel
     c = C.mla_case(60, 2, 2, 16, [900, 300], q_dtype=ldt, lat_dtype=ldt)
     lat = c["lat"].copy()
     lat[0, 700, :] = 0.0
@@ -167,8 +167,8 @@ def test_fp32_q_variants(device, kernel, B, q_len, H, lens, ldt):
         C.assert_close(run_gpu(c, device, C.F32, splits, kernel=kernel), ref, f"fp32 q kernel {kernel} splits={splits}")
 
 
-def test_fp32_q_overshoot_fallback(device):
-    # the exact-recompute path with fp32 q in the warp-specialised kernel
+def test_fp32_q_overshoot_rebases(device):
+    # the re-base path with fp32 q in the warp-specialised kernel
     c = C.mla_case(62, 2, 1, 128, [900, 300], q_dtype=C.F32, lat_dtype=C.F16)
     lat = c["lat"].copy()
     lat[0, 700, :] = 0.0
@@ -181,8 +181,8 @@ def test_fp32_q_overshoot_fallback(device):
 
 
 @pytest.mark.parametrize("kernel", [_capi.MLA_KERNEL_ROWS, _capi.MLA_KERNEL_WS])
-def test_variant_overshoot_fallback(device, kernel):
-    # the exact-recompute flag path of both 16-bit-q kernels (R = 128 rows)
+def test_kernel_overshoot_rebases(device, kernel):
+    # the re-base path of both 16-bit-q kernels (R = 128 rows)
     c = C.mla_case(61, 2, 1, 128, [900, 300], q_dtype=C.BF16, lat_dtype=C.BF16)
     lat = c["lat"].copy()
     lat[0, 700, :] = 0.0
@@ -193,3 +193,22 @@ def test_variant_overshoot_fallback(device, kernel):
     q, qb = O.round_to(q, C.BF16)
     c2 = dict(c, lat=lat, latb=latb, q=q, qb=qb)
     C.assert_close(run_gpu(c2, device, C.F32, 0, kernel=kernel), C.mla_ref(c2), f"kernel {kernel} overshoot")
+
+
+@pytest.mark.parametrize("kernel", [_capi.MLA_KERNEL_ROWS, _capi.MLA_KERNEL_WS])
+@pytest.mark.parametrize("q_len", [1, 3])
+def test_climbing_scores_rebase_every_tile(device, kernel, q_len):
+    # latent dim 0 grows 5 per token, so a row's scores climb ~11.5 nats per
+    # 32-token tile: past the f16 weights' headroom every tile, the rows
+    # re-base again and again (the last tokens dominate)
+    c = C.mla_case(63, 2, q_len, 16, [1000, 333], q_dtype=C.F16, lat_dtype=C.F16)
+    lat = c["lat"].copy()
+    lat[:, :, 0] = 5.0 * np.arange(lat.shape[1])[None, :]
+    lat, latb = O.round_to(lat, C.F16)
+    q = c["q"].copy()
+    q[:, :, :, 0] = 1.0
+    q, qb = O.round_to(q, C.F16)
+    c2 = dict(c, lat=lat, latb=latb, q=q, qb=qb)
+    ref = C.mla_ref(c2)
+    for splits in (0, 1, 5):
+        C.assert_close(run_gpu(c2, device, C.F32, splits, kernel=kernel), ref, f"climbing kernel {kernel} splits={splits}")
