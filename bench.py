@@ -87,8 +87,9 @@ class MlaDecode(Case):
         self.sl = torch.from_numpy(self.lens).to(dev)
         self.max_T = max_T
         self.out = torch.empty((B, q_len, H, 512), dtype=torch.float32, device=dev)
-        self.profile = ("mla_decode", {"mla_decode_v3": "v3_b8_h128",
-                                       "mla_verify_v3": "verify_b4_q5_t32768"}.get(name, name))
+        self.profile = ("mla_decode", {"mla_decode_v3": "v3_b8_h128", "mla_decode_v2lite": "v2lite_b1_h16",
+                                       "mla_verify_v3": "verify_b4_q5_t32768",
+                                       "mla_prefill_v2lite_n512": "prefill_v2lite_n512"}.get(name, name))
         self.ws = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
         esz_q = self.q.element_size()
         self.bytes = float(self.lens.sum()) * 576 * self.lat.element_size() + B * q_len * H * (576 * esz_q + 512 * 4)
@@ -165,7 +166,7 @@ class GqaDecode(Case):
         self.sl = torch.from_numpy(self.lens).to(dev)
         self.max_T = max_T
         self.out = torch.empty((B, H, D), dtype=torch.float16, device=dev)
-        self.profile = ("gqa_decode", "qwen7b_b16_ragged" if B == 16 else name)
+        self.profile = ("gqa_decode", "qwen7b_b16_ragged" if B == 16 else "qwen7b_b1_t4096")
         self.ws = torch.empty(1 << 26, dtype=torch.uint8, device=dev)
         self.bytes = float(self.lens.sum()) * Hk * D * 2 * 2 + B * H * D * 2 * 2
         self.flops = 4.0 * H * D * float(self.lens.sum())
@@ -462,6 +463,9 @@ def main():
             Prefill(dev, 2048, 28, 4, 128, 50, "gqa_prefill_qwen7b_n2048"),
             Prefill(dev, 8192, 28, 4, 128, 49, "gqa_prefill_qwen7b_n8192"),
             MlaDecode(dev, 4, 128, 5, [32768] * 4, 32768, torch.bfloat16, torch.bfloat16, 47, "mla_verify_v3"),
+            # a 512-token prompt of V2-Lite in one verify-shaped call (the
+            # reference runs cpu_mla_attention once per prompt token)
+            MlaDecode(dev, 1, 16, 512, [512], 512, torch.float32, torch.float16, 51, "mla_prefill_v2lite_n512"),
             MlaFull(dev, 8, 128, seeded_lens(45, 8, 1024, 8192), 8192, "q8_0", 48, "mla_layer_v3_q8_0"),
             MlaDecode(dev, 8, 128, 1, seeded_lens(45, 8, 1024, 8192), 8192, torch.bfloat16, torch.bfloat16, 45,
                       "mla_decode_v3_fallback_1pct", fallback_rows=1),

@@ -35,7 +35,7 @@ def _run(case):
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("name", ["mla_decode_v3", "mla_decode_v2lite", "mla_verify_v3",
+@pytest.mark.parametrize("name", ["mla_decode_v3", "mla_decode_v2lite", "mla_verify_v3", "mla_prefill_v2lite_n512",
                                   "mla_decode_v3_fallback_1pct", "mla_decode_v3_fallback_10pct"])
 def test_mla_workloads(device, name):
     lens45 = bench.seeded_lens(45, 8, 1024, 8192)
@@ -46,6 +46,8 @@ def test_mla_workloads(device, name):
                                                      42, name),
         "mla_verify_v3": lambda: bench.MlaDecode(device, 4, 128, 5, [32768] * 4, 32768, torch.bfloat16,
                                                  torch.bfloat16, 47, name),
+        "mla_prefill_v2lite_n512": lambda: bench.MlaDecode(device, 1, 16, 512, [512], 512, torch.float32,
+                                                           torch.float16, 51, name),
         "mla_decode_v3_fallback_1pct": lambda: bench.MlaDecode(device, 8, 128, 1, lens45, 8192, torch.bfloat16,
                                                                torch.bfloat16, 45, name, fallback_rows=1),
         "mla_decode_v3_fallback_10pct": lambda: bench.MlaDecode(device, 8, 128, 1, lens45, 8192, torch.bfloat16,
