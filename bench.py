@@ -249,12 +249,13 @@ class MlaFull(Case):
     kernel = "mla_decode"
     extra_kernels = ("mla_latent_write", "mla_absorb", "mla_project")
 
-    def __init__(self, dev, B, H, lens, max_T, w_type, seed, name):
+    def __init__(self, dev, B, H, lens, max_T, w_type, seed, name, q_len=1, profile=("mla_layer", "v3_b8_q8_0")):
         self.name = name
         g = torch.Generator(device=dev).manual_seed(seed)
         self.lens = np.asarray(lens, np.int32)
         self.w_type = w_type
-        self.q = randn((B, 1, H, 192), 1.0, torch.float16, g, dev)
+        self.q_len = q_len
+        self.q = randn((B, q_len, H, 192), 1.0, torch.float16, g, dev)
         self.lat = randn((B, max_T, 576), 0.5, torch.float16, g, dev)
         self.sl = torch.from_numpy(self.lens).to(dev)
         self.max_T = max_T
@@ -272,22 +273,28 @@ class MlaFull(Case):
             wb = wb.reshape(2, H * 128, rb).contiguous()
         self.w_kb = wb[0] if w_type != "f16" else wb[0].view(torch.float16)
         self.w_vb = wb[1] if w_type != "f16" else wb[1].view(torch.float16)
-        self.qa = torch.empty((B, 1, H, 576), dtype=torch.float32, device=dev)
-        self.o = torch.empty((B, 1, H, 512), dtype=torch.float32, device=dev)
-        self.out = torch.empty((B, 1, H, 128), dtype=torch.float16, device=dev)
+        self.qa = torch.empty((B, q_len, H, 576), dtype=torch.float32, device=dev)
+        self.o = torch.empty((B, q_len, H, 512), dtype=torch.float32, device=dev)
+        self.out = torch.empty((B, q_len, H, 128), dtype=torch.float16, device=dev)
         self.ws = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
-        self.kv_a = randn((B, 576), 1.0, torch.float16, g, dev)
+        self.kv_a = randn((B * q_len, 576), 1.0, torch.float16, g, dev)
         self.norm_w = randn((512,), 0.1, torch.float16, g, dev) + 1.0
-        self.pos = torch.from_numpy(self.lens - 1).to(dev)
+        # the step's new tokens sit at the end of each sequence
+        pos = (self.lens[:, None] - q_len + np.arange(q_len)[None, :]).astype(np.int32).reshape(-1)
+        self.pos = torch.from_numpy(pos).to(dev)
         self.rope = (10000.0, 40.0, 4096)
-        self.profile = ("mla_layer", "v3_b8_q8_0")
-        rows = B * H
+        self.profile = profile
+        rows = B * q_len * H
         self.bytes = (2.0 * H * 128 * rb + float(self.lens.sum()) * 576 * 2 + rows * 192 * 2
-                      + 2 * rows * 576 * 4 + 2 * rows * 512 * 4 + rows * 128 * 2 + 2 * B * 576 * 2)
-        self.flops = 2.0 * rows * 128 * 512 * 2 + 2.0 * H * (576 + 512) * float(self.lens.sum())
+                      + 2 * rows * 576 * 4 + 2 * rows * 512 * 4 + rows * 128 * 2 + 2 * B * q_len * 576 * 2)
+        vis = sum(int(T) - q_len + i + 1 for T in self.lens for i in range(q_len))
+        self.flops = 2.0 * rows * 128 * 512 * 2 + 2.0 * H * (576 + 512) * vis
+        if q_len > 1:
+            self.bound, self.unit = "mfma", "TFLOP/s"
 
     def step(self):
-        mugen_amd.mla_latent_write(self.kv_a, self.norm_w, self.pos, self.lat, rope=self.rope)
+        mugen_amd.mla_latent_write(self.kv_a, self.norm_w, self.pos, self.lat, rows_per_seq=self.q_len,
+                                   rope=self.rope)
         mugen_amd.mla_absorb(self.q, self.w_kb, self.w_type, out=self.qa, positions=self.pos, rope=self.rope)
         mugen_amd.mla_attention(self.qa, self.lat, self.sl, self.max_T, scale=MLA_SCALE, out=self.o,
                                 workspace=self.ws, seq_lens_host=self.lens)
@@ -467,6 +474,9 @@ def main():
             # reference runs cpu_mla_attention once per prompt token)
             MlaDecode(dev, 1, 16, 512, [512], 512, torch.float32, torch.float16, 51, "mla_prefill_v2lite_n512"),
             MlaFull(dev, 8, 128, seeded_lens(45, 8, 1024, 8192), 8192, "q8_0", 48, "mla_layer_v3_q8_0"),
+            # the same layer over a 512-token V2-Lite prompt in one step
+            MlaFull(dev, 1, 16, [512], 512, "q8_0", 52, "mla_layer_prefill_v2lite_n512", q_len=512,
+                    profile=("mla_layer", "prefill_v2lite_n512_q8_0")),
             MlaDecode(dev, 8, 128, 1, seeded_lens(45, 8, 1024, 8192), 8192, torch.bfloat16, torch.bfloat16, 45,
                       "mla_decode_v3_fallback_1pct", fallback_rows=1),
             MlaDecode(dev, 8, 128, 1, seeded_lens(45, 8, 1024, 8192), 8192, torch.bfloat16, torch.bfloat16, 45,

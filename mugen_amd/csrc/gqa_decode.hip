@@ -396,12 +396,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     MUGEN_TRACE(2);
 }
 
-// Log-sum-exp merge of the split partials of one (sequence, head): the
-// split weights are computed in parallel while the first splits' partials
-// are already in flight, then each thread sums its dim over the splits with
-// independent (unrolled) loads.
+// Log-sum-exp merge of the split partials of one (sequence, head); thread d
+// owns output dim d.
+//  * up to 64 splits (every decode plan at 7B-class shapes): each wave
+//    reads all (m, l) pairs (lane s holds split s) and forms the weights with
+//    wave reductions, while the first kPre splits' partials are already in
+//    flight -- one memory round trip, no block barrier;
+//  * more splits: the weights are formed block-wide in LDS (lse_weights),
+//    then the partials are summed 8 splits at a time.
 template <int D, int OUT_DT>
 __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p) {
+    constexpr int kPre = 32;
     __shared__ float f_lds[kMaxSplits];
     __shared__ float red_lds[4];
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
@@ -412,26 +417,55 @@ __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p
     const int64_t bh = (int64_t)b * p.H + h;
     const float* ml = p.ws_ml + bh * p.num_splits * 2;
     const float* os = p.ws_o + bh * p.num_splits * D + d;
-    // this thread's split (m, l), then the first 8 splits' partials (clamped,
-    // unconditional loads), all in flight before the weights are formed
-    const float m0 = d < nact ? ml[2 * d] : kNegInf, l0 = d < nact ? ml[2 * d + 1] : 0.f;
-    float v0[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++) v0[j] = os[(int64_t)max(0, min(j, nact - 1)) * D];
-    const float inv = lse_weights(ml, 2, nact, m0, l0, f_lds, red_lds);
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float inv;
+    if (nact <= 64) {
+        const int lane = d & 63;
+        float* fw = &f_lds[(d >> 6) * 64];  // this wave's weights
+        const float ms = lane < nact ? ml[2 * lane] : kNegInf;
+        const float ls = lane < nact ? ml[2 * lane + 1] : 0.f;
+        float v[kPre];  // clamped, unconditional loads: exact wait counts
 #pragma unroll
-    for (int j = 0; j < 8; j++)
-        if (j < nact) acc[j] = f_lds[j] * v0[j];
-    int s = 8;
-    for (; s + 8 <= nact; s += 8) {
-        float v[8];
+        for (int j = 0; j < kPre; j++) v[j] = os[(int64_t)max(0, min(j, nact - 1)) * D];
+        const float M = wave_max(ms);
+        const float f = (ms == kNegInf) ? 0.f : fast_exp2(ms - M);
+        const float L = wave_sum(f * ls);
+        inv = L > 0.f ? 1.f / L : 0.f;
+        fw[lane] = f;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = os[(int64_t)(s + j) * D];
+        for (int j = 0; j < kPre; j++)
+            if (j < nact) acc[j & 7] += fw[j] * v[j];
+        for (int s = kPre; s < nact; s += 8) {
+            float u[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) acc[j] += f_lds[s + j] * v[j];
+            for (int j = 0; j < 8; j++) u[j] = os[(int64_t)min(s + j, nact - 1) * D];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (s + j < nact) acc[j] += fw[s + j] * u[j];
+        }
+    } else {
+        // this thread's split (m, l), then the first 8 splits' partials,
+        // all in flight before the weights are formed
+        const float m0 = d < nact ? ml[2 * d] : kNegInf, l0 = d < nact ? ml[2 * d + 1] : 0.f;
+        float v0[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v0[j] = os[(int64_t)j * D];
+        inv = lse_weights(ml, 2, nact, m0, l0, f_lds, red_lds);
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[j] = f_lds[j] * v0[j];
+        int s = 8;
+        for (; s + 8 <= nact; s += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = os[(int64_t)(s + j) * D];
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[j] += f_lds[s + j] * v[j];
+        }
+        for (; s < nact; s++) acc[0] += f_lds[s] * os[(int64_t)s * D];
     }
-    for (; s < nact; s++) acc[0] += f_lds[s] * os[(int64_t)s * D];
     const float O = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
     store_out<OUT_DT>(p.out, bh * D + d, O * inv);
     MUGEN_TRACE(9);

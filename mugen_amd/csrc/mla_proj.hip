@@ -26,6 +26,9 @@
 
 namespace mugen_attn {
 
+// rows (batch * q_len) from which absorb / project run on MFMA
+constexpr int kProjMfmaRows = 64;
+
 namespace {
 
 template <int WT>
@@ -258,8 +261,205 @@ __global__ __launch_bounds__(256) void mla_project_kernel(MlaProjParams p) {
     }
 }
 
+// ---------------------------------------------------------------- MFMA forms
+//
+// At prompt sizes (rows = q_len * batch of 64 and more) the products are
+// real GEMMs (per head: rows x 128 x 512) and the weight stream is no longer
+// the bound; they run on bf16 MFMA with fp32-level accuracy:
+//  * each fp32 (or f16) operand value x is split into bf16 hi = rne(x) and
+//    lo = rne(x - hi) (16 significant bits; an f16 value splits exactly),
+//    and every product is formed as hi.hi + hi.lo + lo.hi with fp32
+//    accumulation -- the dropped lo.lo term and the rounding of lo leave a
+//    relative error of ~2^-16 per product;
+//  * the reference skips zero q terms (transformer.cpp:2567); that differs
+//    from adding 0 * w only for a non-finite weight, which a GGUF attn_k_b /
+//    attn_v_b does not hold.
+// Row counts below kProjMfmaRows keep the weight-streaming VALU kernels
+// above.
+
+// absorb: workgroup = (head, 128-column quarter of kv_rank, row group);
+// the quarter's weights (128 nope rows x 128 columns) are dequantised once
+// into LDS as bf16 hi / lo planes, rows XOR-swizzled in 16-byte chunks so
+// the transpose reads (ds_read_b64_tr_b16) that form the A operand
+// W^T[column][nope] are conflict-free.  Q^T_abs = W^T . q^T: wave w owns
+// columns 32w .. 32w+31 of the quarter and 64 rows at a time; q (f16) is
+// the B operand straight from global memory (8 consecutive nope dims per
+// lane).  Lane (g, n) ends with 4 consecutive columns of row n: one 16-byte
+// store.
+template <int WT, int OUT_DT>
+__global__ __launch_bounds__(256) void mla_absorb_mfma_kernel(MlaProjParams p) {
+    constexpr int NOPE = 128, ROPE = 64, KR = 512, CQ = 128, RB = CQ * 2;  // LDS row bytes per plane
+    constexpr int WRB = wrow_bytes<WT>(KR);
+    __shared__ __attribute__((aligned(16))) char wl[2][NOPE * RB];  // [hi|lo][nope row][128 columns]
+    const int h = blockIdx.x, cq = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    auto swz = [](int r) { return ((r & 1) * 2) ^ (((r >> 1) & 1) * 4) ^ (((r >> 3) & 1) * 8) ^ ((r >> 4) & 1); };
+    {   // dequantise the quarter: 128 rows x 16 chunks of 8 columns
+        const uint8_t* wh = static_cast<const uint8_t*>(p.w) + (size_t)h * NOPE * WRB;
+#pragma unroll 2
+        for (int job = tid; job < NOPE * 16; job += 256) {
+            const int k = job >> 4, c8 = job & 15;
+            const int d0 = cq * CQ + 8 * c8;
+            const WRaw<WT, 8> raw = wload<WT, 8>(wh + (size_t)k * WRB, d0);
+            float x[8];
+            dequant<WT, 8>(raw, d0, x);
+            u32x4_t fr[2];
+            split_p<DT_BF16, 2>(x, fr);
+            const int off = k * RB + ((c8 ^ swz(k)) * 16);
+            *reinterpret_cast<u32x4_t*>(&wl[0][off]) = fr[0];
+            *reinterpret_cast<u32x4_t*>(&wl[1][off]) = fr[1];
+        }
+    }
+    // transpose-read offsets: lane (g, n) reads rows 8g + n/4 (+4) of a
+    // k-step, column chunk 2cb + (n%4)/2 of its wave's 32 columns
+    const int tr = 8 * g + (n >> 2);
+    uint32_t t_off[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++)
+        t_off[cb] = tr * RB + (((4 * w + 2 * cb + ((n & 3) >> 1)) ^ swz(tr)) * 16) + 8 * (n & 1);
+    __syncthreads();
+    const uint16_t* q = static_cast<const uint16_t*>(p.in);
+    for (int r0 = blockIdx.z * 64; r0 < p.rows; r0 += gridDim.z * 64) {
+        if (cq == 0) {
+            // q_rope appended: as is, or rotated by the reference's q RoPE
+            // stage (NeoX pairs c, c + 32, f16 results)
+            for (int job = tid; job < 64 * ROPE / 2; job += 256) {
+                const int r = r0 + job / (ROPE / 2), c = job % (ROPE / 2);
+                if (r < p.rows) {
+                    const uint16_t* qr = q + ((int64_t)r * p.H + h) * (NOPE + ROPE) + NOPE;
+                    uint16_t y0 = qr[c], y1 = qr[c + ROPE / 2];
+                    if (p.positions || p.seq_base)
+                        rope_pair_f16(to_f32<DT_F16>(y0), to_f32<DT_F16>(y1),
+                                      row_position(p.positions, p.seq_base, p.rows_per_seq, r), p.freqs.f[c], y0, y1);
+                    const int64_t o = ((int64_t)r * p.H + h) * (KR + ROPE) + KR + c;
+                    store_out<OUT_DT>(p.out, o, to_f32<DT_F16>(y0));
+                    store_out<OUT_DT>(p.out, o + ROPE / 2, to_f32<DT_F16>(y1));
+                }
+            }
+        }
+        f32x4_t acc[2][4];
+#pragma unroll
+        for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++) acc[cb][rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < NOPE / 32; kk++) {
+            u32x4_t qf[4][2];  // row block rb: q[row n][32kk + 8g .. +7] as bf16 hi / lo
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++) {
+                const int r = min(r0 + 16 * rb + n, p.rows - 1);
+                const u32x4_t v = load16(q + ((int64_t)r * p.H + h) * (NOPE + ROPE) + 32 * kk + 8 * g);
+                float x[8];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    x[2 * e] = lo_f32<DT_F16>(v[e]);
+                    x[2 * e + 1] = hi_f32<DT_F16>(v[e]);
+                }
+                split_p<DT_BF16, 2>(x, qf[rb]);
+            }
+#pragma unroll
+            for (int cb = 0; cb < 2; cb++) {
+                u32x4_t wf[2];
+#pragma unroll
+                for (int pl = 0; pl < 2; pl++) {
+                    const char* base = &wl[pl][32 * kk * RB + t_off[cb]];
+                    const u32x2_t lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(base));
+                    const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(base + 4 * RB));
+                    wf[pl] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+                }
+#pragma unroll
+                for (int rb = 0; rb < 4; rb++) {
+                    acc[cb][rb] = mfma16x16x32<DT_BF16>(wf[0], qf[rb][0], acc[cb][rb]);
+                    acc[cb][rb] = mfma16x16x32<DT_BF16>(wf[0], qf[rb][1], acc[cb][rb]);
+                    acc[cb][rb] = mfma16x16x32<DT_BF16>(wf[1], qf[rb][0], acc[cb][rb]);
+                }
+            }
+        }
+        // lane (g, n): columns 32w + 16cb + 4g .. +3 of row r0 + 16rb + n
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++) {
+            const int r = r0 + 16 * rb + n;
+            if (r >= p.rows) continue;
+#pragma unroll
+            for (int cb = 0; cb < 2; cb++) {
+                const int64_t o = ((int64_t)r * p.H + h) * (KR + ROPE) + cq * CQ + 32 * w + 16 * cb + 4 * g;
+                if constexpr (OUT_DT == DT_F32) {
+                    *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.out) + o) = acc[cb][rb];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) store_out<OUT_DT>(p.out, o + e, acc[cb][rb][e]);
+                }
+            }
+        }
+    }
+}
+
+// project: workgroup = (head, 64 rows, half of the 128 output rows j);
+// out^T = W_v . o^T: wave w owns 16 rows of o and the half's 4 j blocks.
+// Both operands come straight from global memory with 8 consecutive
+// kv_rank dims per lane: a weight row j (the A operand, dequantised and
+// split) and a row of o (the B operand, fp32 split).  Lane (g, n) ends
+// with j .. j+3 of row n: one 8-byte (f16) or 16-byte (fp32) store.
+template <int WT, int OUT_DT>
+__global__ __launch_bounds__(256) void mla_project_mfma_kernel(MlaProjParams p) {
+    constexpr int KR = 512, VH = 128, JB = 4;  // j blocks of 16 per workgroup
+    constexpr int WRB = wrow_bytes<WT>(KR);
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int j0 = blockIdx.z * (16 * JB);
+    const int r = blockIdx.y * 64 + 16 * w + n;
+    const int rc = min(r, p.rows - 1);
+    const uint8_t* wh = static_cast<const uint8_t*>(p.w) + ((size_t)h * VH + j0 + n) * WRB;
+    const float* orow = static_cast<const float*>(p.in) + ((int64_t)rc * p.H + h) * KR + 8 * g;
+    f32x4_t acc[JB];
+#pragma unroll
+    for (int jb = 0; jb < JB; jb++) acc[jb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+    for (int kk = 0; kk < KR / 32; kk++) {
+        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(orow + 32 * kk);
+        const f32x4_t b = *reinterpret_cast<const f32x4_t*>(orow + 32 * kk + 4);
+        WRaw<WT, 8> raw[JB];
+#pragma unroll
+        for (int jb = 0; jb < JB; jb++) raw[jb] = wload<WT, 8>(wh + (size_t)(16 * jb) * WRB, 32 * kk + 8 * g);
+        const float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        u32x4_t of[2];
+        split_p<DT_BF16, 2>(x, of);
+#pragma unroll
+        for (int jb = 0; jb < JB; jb++) {
+            float wv[8];
+            dequant<WT, 8>(raw[jb], 32 * kk + 8 * g, wv);
+            u32x4_t wf[2];
+            split_p<DT_BF16, 2>(wv, wf);
+            acc[jb] = mfma16x16x32<DT_BF16>(wf[0], of[0], acc[jb]);
+            acc[jb] = mfma16x16x32<DT_BF16>(wf[0], of[1], acc[jb]);
+            acc[jb] = mfma16x16x32<DT_BF16>(wf[1], of[0], acc[jb]);
+        }
+    }
+    if (r >= p.rows) return;
+#pragma unroll
+    for (int jb = 0; jb < JB; jb++) {
+        const int64_t o = ((int64_t)r * p.H + h) * VH + j0 + 16 * jb + 4 * g;
+        if constexpr (OUT_DT == DT_F32) {
+            *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.out) + o) = acc[jb];
+        } else {
+            const uint32_t lo = pack2<OUT_DT>(acc[jb][0], acc[jb][1]), hi = pack2<OUT_DT>(acc[jb][2], acc[jb][3]);
+            *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.out) + o) = u32x2_t{lo, hi};
+        }
+    }
+}
+
 template <int WT>
 static hipError_t launch_absorb_w(const MlaProjParams& p, int out_dt, hipStream_t st, KernelTimer* t) {
+    if (p.rows >= kProjMfmaRows) {
+        // row groups of 64: enough workgroups for ~two per CU, each group
+        // of a workgroup reusing its dequantised quarter
+        const int groups = (p.rows + 63) / 64;
+        const int per = std::max(1, 512 / (p.H * 4));
+        const dim3 grid(p.H, 4, std::min(groups, per));
+        if (out_dt == DT_BF16)
+            return launch_k(t, "mla_absorb", mla_absorb_mfma_kernel<WT, DT_BF16>, grid, dim3(256), st, p);
+        return launch_k(t, "mla_absorb", mla_absorb_mfma_kernel<WT, DT_F32>, grid, dim3(256), st, p);
+    }
     const dim3 grid(p.H, 512 / 256);
     if (out_dt == DT_BF16) return launch_k(t, "mla_absorb", mla_absorb_kernel<WT, DT_BF16>, grid, dim3(512), st, p);
     return launch_k(t, "mla_absorb", mla_absorb_kernel<WT, DT_F32>, grid, dim3(512), st, p);
@@ -273,6 +473,12 @@ hipError_t launch_mla_absorb(const MlaProjParams& p, int w_type, int out_dt, hip
 
 template <int WT>
 static hipError_t launch_project_w(const MlaProjParams& p, int out_dt, hipStream_t st, KernelTimer* t) {
+    if (p.rows >= kProjMfmaRows) {
+        const dim3 grid(p.H, (p.rows + 63) / 64, 2);
+        if (out_dt == DT_F16)
+            return launch_k(t, "mla_project", mla_project_mfma_kernel<WT, DT_F16>, grid, dim3(256), st, p);
+        return launch_k(t, "mla_project", mla_project_mfma_kernel<WT, DT_F32>, grid, dim3(256), st, p);
+    }
     const dim3 grid(p.H, 128 / 32);
     if (out_dt == DT_F16) return launch_k(t, "mla_project", mla_project_kernel<WT, DT_F16>, grid, dim3(256), st, p);
     return launch_k(t, "mla_project", mla_project_kernel<WT, DT_F32>, grid, dim3(256), st, p);

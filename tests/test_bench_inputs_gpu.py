@@ -1,6 +1,7 @@
 """The benchmark's own timed inputs, checked against the oracle: every
 bench.py workload (headline MLA V3 decode, V2-Lite, verify, GQA decode,
-4-bit store decode, prefill, the fallback-cost workloads) is built exactly
+4-bit store decode, prefill, the fallback-cost workloads, both MLA layer
+workloads) is built exactly
 as bench.py builds it (seeded torch draws, its context lengths), run once,
 and compared with the CPU oracle on the same bytes.  So the numbers bench.py
 reports come from inputs whose results are parity-checked.  (The two longest
@@ -106,18 +107,23 @@ def test_prefill_workloads(device, name, N, H, Hk, D, seed):
     C.assert_close(_f32(c.out[:n]), ref, name)
 
 
-def test_mla_layer_workload(device):
+@pytest.mark.parametrize("name", ["mla_layer_v3_q8_0", "mla_layer_prefill_v2lite_n512"])
+def test_mla_layer_workload(device, name):
     from tests.test_mla_cache_gpu import assert_f16_match
-    c = bench.MlaFull(device, 8, 128, bench.seeded_lens(45, 8, 1024, 8192), 8192, "q8_0", 48, "mla_layer_v3_q8_0")
-    lat0 = _bits(c.lat).copy()  # the latent before the step writes the new token's row
+    if name == "mla_layer_v3_q8_0":
+        c = bench.MlaFull(device, 8, 128, bench.seeded_lens(45, 8, 1024, 8192), 8192, "q8_0", 48, name)
+    else:
+        c = bench.MlaFull(device, 1, 16, [512], 512, "q8_0", 52, name, q_len=512)
+    B, q_len, H = c.q.shape[0], c.q_len, c.q.shape[2]
+    lat0 = _bits(c.lat).copy()  # the latent before the step writes the new tokens' rows
     _run(c)
     freqs = O.yarn_freqs(64, c.rope[1], c.rope[2], c.rope[0])
-    pos = (c.lens - 1).astype(np.int32)
-    lat_ref = O.mla_latent_write(_bits(c.kv_a), _bits(c.norm_w), pos, lat0, 1, 8192, freqs, 1e-6)
+    pos = c.pos.cpu().numpy().astype(np.int32)
+    lat_ref = O.mla_latent_write(_bits(c.kv_a), _bits(c.norm_w), pos, lat0, q_len, c.max_T, freqs, 1e-6)
     got = _bits(c.lat)
-    rows = np.arange(8)
-    assert_f16_match(got[rows, pos], lat_ref[rows, pos], "latent rows written by the step")
-    q = O.rope_q_f16(_bits(c.q).reshape(8, 128, 192), pos, freqs).reshape(8, 1, 128, 192)
+    seq = np.repeat(np.arange(B), q_len)
+    assert_f16_match(got[seq, pos], lat_ref[seq, pos], "latent rows written by the step")
+    q = O.rope_q_f16(_bits(c.q).reshape(B * q_len, H, 192), pos, freqs).reshape(B, q_len, H, 192)
     ref = O.mla_full(O.bits_to_f32(q, C.F16), c.w_kb.cpu().numpy(), c.w_vb.cpu().numpy(), O.W_Q8_0,
-                     O.bits_to_f32(lat_ref, C.F16), c.lens, 1, 128, bench.MLA_SCALE, nthreads=16)
-    C.assert_close(_f32(c.out), ref, "mla_layer_v3_q8_0")
+                     O.bits_to_f32(lat_ref, C.F16), c.lens, q_len, H, bench.MLA_SCALE, nthreads=16)
+    C.assert_close(_f32(c.out), ref, name)

@@ -28,8 +28,12 @@ def qdev(qb, device):
     return C.to_dev(qb, C.F16, device)
 
 
+# rows >= 64 take the MFMA forms (bf16 hi / lo splits), fewer the VALU kernels
+ROWS_H = [(1, 16), (8, 128), (37, 3), (64, 16), (77, 3), (512, 16)]
+
+
 @pytest.mark.parametrize("w_type", WTYPES)
-@pytest.mark.parametrize("rows,H", [(1, 16), (8, 128), (37, 3)])
+@pytest.mark.parametrize("rows,H", ROWS_H)
 def test_absorb(device, w_type, rows, H):
     q, qb = O.round_to(O.randn(100 + rows, (rows, H, 192)), C.F16)
     q[0, 0, :40] = 0.0          # zero terms, skipped by the reference
@@ -47,7 +51,7 @@ def test_absorb(device, w_type, rows, H):
 
 
 @pytest.mark.parametrize("w_type", WTYPES)
-@pytest.mark.parametrize("rows,H", [(1, 16), (8, 128), (37, 3)])
+@pytest.mark.parametrize("rows,H", ROWS_H)
 def test_project(device, w_type, rows, H):
     o = O.randn(300 + rows, (rows, H, 512), 0.0, 0.3)
     w = C.make_weights(400 + H, H * 128, 512, w_type)
@@ -66,6 +70,7 @@ def test_project(device, w_type, rows, H):
     (1, 1, 16, [1024]),          # configs[0] shape (V2-Lite heads) end to end
     (3, 2, 20, [2, 700, 129]),
     (2, 5, 128, [1500, 5]),      # verify rows, V3 heads
+    (1, 64, 16, [300]),          # a prompt chunk: absorb / project on MFMA
 ])
 def test_full_operator(device, w_type, B, q_len, H, lens):
     c = C.mla_full_case(500 + H + q_len, B, q_len, H, lens, w_type)
@@ -77,6 +82,25 @@ def test_full_operator(device, w_type, B, q_len, H, lens):
     torch.cuda.synchronize()
     assert got.dtype == torch.float16 and got.shape == (B, q_len, H, 128)
     C.assert_close(got.float().cpu().numpy(), C.mla_full_ref(c, nthreads=8), f"mla full {WNAME[w_type]}")
+
+
+def test_absorb_rope_matches_across_forms(device):
+    """The q RoPE stage of the MFMA form (100 rows) equals the VALU form's
+    (the same rows absorbed 8 at a time) bit for bit, and q_abs agrees."""
+    rows, H = 100, 16
+    q, qb = O.round_to(O.randn(77, (rows, H, 192)), C.F16)
+    w = C.make_weights(78, H * 128, 512, O.W_Q8_0)
+    pos = torch.arange(900, 900 + rows, dtype=torch.int32, device=device)
+    rope = (10000.0, 40.0, 4096)
+    C.say("absorb rope MFMA vs VALU forms")
+    qd, wd = qdev(qb, device), wdev(w, O.W_Q8_0, device)
+    big = mugen_amd.mla_absorb(qd, wd, "q8_0", positions=pos, rope=rope)
+    parts = [mugen_amd.mla_absorb(qd[i:i + 8], wd, "q8_0", positions=pos[i:i + 8], rope=rope)
+             for i in range(0, rows, 8)]
+    small = torch.cat(parts)
+    torch.cuda.synchronize()
+    assert torch.equal(big[..., 512:], small[..., 512:])
+    C.assert_close(big[..., :512].cpu().numpy(), small[..., :512].cpu().numpy(), "q_abs MFMA vs VALU")
 
 
 def test_zero_rows_is_a_no_op(device):
