@@ -294,15 +294,35 @@ __global__ __launch_bounds__(256) void mla_absorb_mfma_kernel(MlaProjParams p) {
     const int h = blockIdx.x, cq = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
     auto swz = [](int r) { return ((r & 1) * 2) ^ (((r >> 1) & 1) * 4) ^ (((r >> 3) & 1) * 8) ^ ((r >> 4) & 1); };
-    {   // dequantise the quarter: 128 rows x 16 chunks of 8 columns
+    MUGEN_TRACE(0);
+    const uint16_t* q = static_cast<const uint16_t*>(p.in);
+    // q of row block rb, k-step kk: lane (g, n) holds q[row n][32kk + 8g .. +7]
+    u32x4_t qraw[4][NOPE / 32];
+    auto load_q = [&](int r0) {
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++) {
+            const int r = min(r0 + 16 * rb + n, p.rows - 1);
+#pragma unroll
+            for (int kk = 0; kk < NOPE / 32; kk++)
+                qraw[rb][kk] = load16(q + ((int64_t)r * p.H + h) * (NOPE + ROPE) + 32 * kk + 8 * g);
+        }
+    };
+    load_q(blockIdx.z * 64);  // in flight during the dequantisation
+    {   // dequantise the quarter: 128 rows x 16 chunks of 8 columns, all
+        // of a thread's loads issued before any conversion
         const uint8_t* wh = static_cast<const uint8_t*>(p.w) + (size_t)h * NOPE * WRB;
-#pragma unroll 2
-        for (int job = tid; job < NOPE * 16; job += 256) {
-            const int k = job >> 4, c8 = job & 15;
-            const int d0 = cq * CQ + 8 * c8;
-            const WRaw<WT, 8> raw = wload<WT, 8>(wh + (size_t)k * WRB, d0);
+        constexpr int JOBS = NOPE * 16 / 256;
+        WRaw<WT, 8> raw[JOBS];
+#pragma unroll
+        for (int i = 0; i < JOBS; i++) {
+            const int job = tid + 256 * i, k = job >> 4, c8 = job & 15;
+            raw[i] = wload<WT, 8>(wh + (size_t)k * WRB, cq * CQ + 8 * c8);
+        }
+#pragma unroll
+        for (int i = 0; i < JOBS; i++) {
+            const int job = tid + 256 * i, k = job >> 4, c8 = job & 15;
             float x[8];
-            dequant<WT, 8>(raw, d0, x);
+            dequant<WT, 8>(raw[i], cq * CQ + 8 * c8, x);
             u32x4_t fr[2];
             split_p<DT_BF16, 2>(x, fr);
             const int off = k * RB + ((c8 ^ swz(k)) * 16);
@@ -317,14 +337,18 @@ __global__ __launch_bounds__(256) void mla_absorb_mfma_kernel(MlaProjParams p) {
 #pragma unroll
     for (int cb = 0; cb < 2; cb++)
         t_off[cb] = tr * RB + (((4 * w + 2 * cb + ((n & 3) >> 1)) ^ swz(tr)) * 16) + 8 * (n & 1);
+    MUGEN_TRACE(1);
     __syncthreads();
-    const uint16_t* q = static_cast<const uint16_t*>(p.in);
+    MUGEN_TRACE(2);
     for (int r0 = blockIdx.z * 64; r0 < p.rows; r0 += gridDim.z * 64) {
-        if (cq == 0) {
-            // q_rope appended: as is, or rotated by the reference's q RoPE
-            // stage (NeoX pairs c, c + 32, f16 results)
-            for (int job = tid; job < 64 * ROPE / 2; job += 256) {
-                const int r = r0 + job / (ROPE / 2), c = job % (ROPE / 2);
+        if (r0 != blockIdx.z * 64) load_q(r0);
+        {   // q_rope appended: as is, or rotated by the reference's q RoPE
+            // stage (NeoX pairs c, c + 32, f16 results); the 4 quarter
+            // workgroups of a row group take 16 of its rows each
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int job = tid + 256 * i;
+                const int r = r0 + 16 * cq + (job >> 5), c = job & 31;
                 if (r < p.rows) {
                     const uint16_t* qr = q + ((int64_t)r * p.H + h) * (NOPE + ROPE) + NOPE;
                     uint16_t y0 = qr[c], y1 = qr[c + ROPE / 2];
@@ -337,6 +361,7 @@ __global__ __launch_bounds__(256) void mla_absorb_mfma_kernel(MlaProjParams p) {
                 }
             }
         }
+        MUGEN_TRACE(3);
         f32x4_t acc[2][4];
 #pragma unroll
         for (int cb = 0; cb < 2; cb++)
@@ -347,8 +372,7 @@ __global__ __launch_bounds__(256) void mla_absorb_mfma_kernel(MlaProjParams p) {
             u32x4_t qf[4][2];  // row block rb: q[row n][32kk + 8g .. +7] as bf16 hi / lo
 #pragma unroll
             for (int rb = 0; rb < 4; rb++) {
-                const int r = min(r0 + 16 * rb + n, p.rows - 1);
-                const u32x4_t v = load16(q + ((int64_t)r * p.H + h) * (NOPE + ROPE) + 32 * kk + 8 * g);
+                const u32x4_t v = qraw[rb][kk];
                 float x[8];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
@@ -375,6 +399,7 @@ __global__ __launch_bounds__(256) void mla_absorb_mfma_kernel(MlaProjParams p) {
                 }
             }
         }
+        MUGEN_TRACE(4);
         // lane (g, n): columns 32w + 16cb + 4g .. +3 of row r0 + 16rb + n
 #pragma unroll
         for (int rb = 0; rb < 4; rb++) {
@@ -392,58 +417,104 @@ __global__ __launch_bounds__(256) void mla_absorb_mfma_kernel(MlaProjParams p) {
             }
         }
     }
+    MUGEN_TRACE(5);
 }
 
-// project: workgroup = (head, 64 rows, half of the 128 output rows j);
-// out^T = W_v . o^T: wave w owns 16 rows of o and the half's 4 j blocks.
-// Both operands come straight from global memory with 8 consecutive
-// kv_rank dims per lane: a weight row j (the A operand, dequantised and
-// split) and a row of o (the B operand, fp32 split).  Lane (g, n) ends
-// with j .. j+3 of row n: one 8-byte (f16) or 16-byte (fp32) store.
+// project: workgroup = (head, half of the 128 output rows j, row group);
+// out^T = W_v . o^T.  The half's weights (64 rows j x 512 kv_rank) are
+// dequantised once into LDS as bf16 hi / lo planes (16-byte chunk c of row
+// j at chunk c ^ (j % 16): the 16 rows a phase of ds_read_b128 touches
+// land on distinct banks) and read as the A operand, 8 consecutive kv_rank
+// dims of a row j per lane.  o (fp32) is the B operand straight from
+// global memory, split into bf16 hi / lo, loaded kPf k-steps ahead.  Wave
+// w owns 16 rows of o and the half's 4 j blocks; lane (g, n) ends with
+// j .. j+3 of row n: one 8-byte (f16) or 16-byte (fp32) store.
 template <int WT, int OUT_DT>
 __global__ __launch_bounds__(256) void mla_project_mfma_kernel(MlaProjParams p) {
-    constexpr int KR = 512, VH = 128, JB = 4;  // j blocks of 16 per workgroup
+    constexpr int KR = 512, VH = 128, JH = 64, JB = JH / 16, RB = KR * 2, kPf = 4, KS = KR / 32;
     constexpr int WRB = wrow_bytes<WT>(KR);
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    __shared__ __attribute__((aligned(16))) char wl[2][JH * RB];  // [hi|lo][j][512]
+    const int h = blockIdx.x, jh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
-    const int j0 = blockIdx.z * (16 * JB);
-    const int r = blockIdx.y * 64 + 16 * w + n;
-    const int rc = min(r, p.rows - 1);
-    const uint8_t* wh = static_cast<const uint8_t*>(p.w) + ((size_t)h * VH + j0 + n) * WRB;
-    const float* orow = static_cast<const float*>(p.in) + ((int64_t)rc * p.H + h) * KR + 8 * g;
-    f32x4_t acc[JB];
+    const float* o = static_cast<const float*>(p.in);
+    f32x4_t ob[kPf][2];  // o[row n][32kk + 8g .. +7] of the next kPf k-steps
+    auto load_o = [&](int r0, int kk, f32x4_t (&dst)[2]) {
+        const int r = min(r0 + 16 * w + n, p.rows - 1);
+        const float* src = o + ((int64_t)r * p.H + h) * KR + 32 * kk + 8 * g;
+        dst[0] = *reinterpret_cast<const f32x4_t*>(src);
+        dst[1] = *reinterpret_cast<const f32x4_t*>(src + 4);
+    };
 #pragma unroll
-    for (int jb = 0; jb < JB; jb++) acc[jb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 2
-    for (int kk = 0; kk < KR / 32; kk++) {
-        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(orow + 32 * kk);
-        const f32x4_t b = *reinterpret_cast<const f32x4_t*>(orow + 32 * kk + 4);
-        WRaw<WT, 8> raw[JB];
+    for (int i = 0; i < kPf; i++) load_o(blockIdx.z * 64, i, ob[i]);
+    {   // dequantise the half: 64 rows x 64 chunks of 8 dims, 16 per
+        // thread in two batches of 8 (a batch's loads issued together)
+        const uint8_t* wh = static_cast<const uint8_t*>(p.w) + ((size_t)h * VH + jh * JH) * WRB;
+        constexpr int JOBS = 8;
+#pragma unroll 1
+        for (int j0 = 0; j0 < JH * 64; j0 += 256 * JOBS) {
+            WRaw<WT, 8> raw[JOBS];
 #pragma unroll
-        for (int jb = 0; jb < JB; jb++) raw[jb] = wload<WT, 8>(wh + (size_t)(16 * jb) * WRB, 32 * kk + 8 * g);
-        const float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-        u32x4_t of[2];
-        split_p<DT_BF16, 2>(x, of);
+            for (int i = 0; i < JOBS; i++) {
+                const int job = j0 + tid + 256 * i, j = job >> 6, c = job & 63;
+                raw[i] = wload<WT, 8>(wh + (size_t)j * WRB, 8 * c);
+            }
 #pragma unroll
-        for (int jb = 0; jb < JB; jb++) {
-            float wv[8];
-            dequant<WT, 8>(raw[jb], 32 * kk + 8 * g, wv);
-            u32x4_t wf[2];
-            split_p<DT_BF16, 2>(wv, wf);
-            acc[jb] = mfma16x16x32<DT_BF16>(wf[0], of[0], acc[jb]);
-            acc[jb] = mfma16x16x32<DT_BF16>(wf[0], of[1], acc[jb]);
-            acc[jb] = mfma16x16x32<DT_BF16>(wf[1], of[0], acc[jb]);
+            for (int i = 0; i < JOBS; i++) {
+                const int job = j0 + tid + 256 * i, j = job >> 6, c = job & 63;
+                float x[8];
+                dequant<WT, 8>(raw[i], 8 * c, x);
+                u32x4_t fr[2];
+                split_p<DT_BF16, 2>(x, fr);
+                const int off = j * RB + ((c ^ (j & 15)) * 16);
+                *reinterpret_cast<u32x4_t*>(&wl[0][off]) = fr[0];
+                *reinterpret_cast<u32x4_t*>(&wl[1][off]) = fr[1];
+            }
         }
     }
-    if (r >= p.rows) return;
+    __syncthreads();
+    for (int r0 = blockIdx.z * 64; r0 < p.rows; r0 += gridDim.z * 64) {
+        if (r0 != blockIdx.z * 64) {
 #pragma unroll
-    for (int jb = 0; jb < JB; jb++) {
-        const int64_t o = ((int64_t)r * p.H + h) * VH + j0 + 16 * jb + 4 * g;
-        if constexpr (OUT_DT == DT_F32) {
-            *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.out) + o) = acc[jb];
-        } else {
-            const uint32_t lo = pack2<OUT_DT>(acc[jb][0], acc[jb][1]), hi = pack2<OUT_DT>(acc[jb][2], acc[jb][3]);
-            *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.out) + o) = u32x2_t{lo, hi};
+            for (int i = 0; i < kPf; i++) load_o(r0, i, ob[i]);
+        }
+        f32x4_t acc[JB];
+#pragma unroll
+        for (int jb = 0; jb < JB; jb++) acc[jb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+        for (int k0 = 0; k0 < KS; k0 += kPf) {
+#pragma unroll
+            for (int i = 0; i < kPf; i++) {
+                const int kk = k0 + i;
+                const f32x4_t a = ob[i][0], b = ob[i][1];
+                if (kk + kPf < KS) load_o(r0, kk + kPf, ob[i]);
+                const float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+                u32x4_t of[2];
+                split_p<DT_BF16, 2>(x, of);
+#pragma unroll
+                for (int jb = 0; jb < JB; jb++) {
+                    const int j = 16 * jb + n;
+                    const int off = j * RB + (((4 * kk + g) ^ n) * 16);
+                    const u32x4_t whi = *reinterpret_cast<const u32x4_t*>(&wl[0][off]);
+                    const u32x4_t wlo = *reinterpret_cast<const u32x4_t*>(&wl[1][off]);
+                    acc[jb] = mfma16x16x32<DT_BF16>(whi, of[0], acc[jb]);
+                    acc[jb] = mfma16x16x32<DT_BF16>(whi, of[1], acc[jb]);
+                    acc[jb] = mfma16x16x32<DT_BF16>(wlo, of[0], acc[jb]);
+                }
+            }
+        }
+        const int r = r0 + 16 * w + n;
+        if (r < p.rows) {
+#pragma unroll
+            for (int jb = 0; jb < JB; jb++) {
+                const int64_t oo = ((int64_t)r * p.H + h) * VH + jh * JH + 16 * jb + 4 * g;
+                if constexpr (OUT_DT == DT_F32) {
+                    *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.out) + oo) = acc[jb];
+                } else {
+                    const uint32_t lo = pack2<OUT_DT>(acc[jb][0], acc[jb][1]);
+                    const uint32_t hi = pack2<OUT_DT>(acc[jb][2], acc[jb][3]);
+                    *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.out) + oo) = u32x2_t{lo, hi};
+                }
+            }
         }
     }
 }
@@ -474,7 +545,9 @@ hipError_t launch_mla_absorb(const MlaProjParams& p, int w_type, int out_dt, hip
 template <int WT>
 static hipError_t launch_project_w(const MlaProjParams& p, int out_dt, hipStream_t st, KernelTimer* t) {
     if (p.rows >= kProjMfmaRows) {
-        const dim3 grid(p.H, (p.rows + 63) / 64, 2);
+        const int groups = (p.rows + 63) / 64;
+        const int per = std::max(1, 256 / (p.H * 2));
+        const dim3 grid(p.H, 2, std::min(groups, per));
         if (out_dt == DT_F16)
             return launch_k(t, "mla_project", mla_project_mfma_kernel<WT, DT_F16>, grid, dim3(256), st, p);
         return launch_k(t, "mla_project", mla_project_mfma_kernel<WT, DT_F32>, grid, dim3(256), st, p);

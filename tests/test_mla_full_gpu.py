@@ -103,6 +103,26 @@ def test_absorb_rope_matches_across_forms(device):
     C.assert_close(big[..., :512].cpu().numpy(), small[..., :512].cpu().numpy(), "q_abs MFMA vs VALU")
 
 
+@pytest.mark.parametrize("w_type", [O.W_Q8_0, O.W_Q4_0])
+def test_two_byte_aligned_weights(device, w_type):
+    """Block-encoded weights need only 2-byte alignment, also in the MFMA
+    forms (96 rows)."""
+    rows, H = 96, 4
+    q, qb = O.round_to(O.randn(91, (rows, H, 192)), C.F16)
+    w = C.make_weights(92, H * 128, 512, w_type)
+    buf = torch.zeros(w.size + 2, dtype=torch.uint8, device=device)
+    buf[2:] = torch.from_numpy(w.reshape(-1)).to(device)
+    wd = buf[2:].view(w.shape)
+    assert wd.data_ptr() % 4 == 2
+    C.say(f"absorb / project with 2-byte aligned {WNAME[w_type]} weights")
+    got = mugen_amd.mla_absorb(qdev(qb, device), wd, WNAME[w_type])
+    o = O.randn(93, (rows, H, 512), 0.0, 0.3)
+    gp = mugen_amd.mla_project(torch.from_numpy(o).to(device), wd, WNAME[w_type], out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    C.assert_close(got.cpu().numpy(), O.mla_absorb(q, w, w_type, H), "absorb, 2-byte aligned weights")
+    C.assert_close(gp.cpu().numpy(), O.mla_project(o, w, w_type, H), "project, 2-byte aligned weights")
+
+
 def test_zero_rows_is_a_no_op(device):
     q = torch.empty((0, 4, 192), dtype=torch.float16, device=device)
     w = torch.zeros((4 * 128, 512), dtype=torch.float16, device=device)
