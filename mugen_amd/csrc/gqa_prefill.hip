@@ -56,7 +56,7 @@ __host__ __device__ constexpr int pf_swz(int r) {
 
 }  // namespace
 
-template <int D, int MB, int DT, int OUT_DT>
+template <int D, int MB, int DT, int OUT_DT, int TPB>
 __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
     constexpr int KK = D / 32;                 // k-steps of S over head_dim
     constexpr int DB = D / 16;                 // 16-wide output column blocks
@@ -66,7 +66,8 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
     constexpr int DPW = 2 * MAT / 1024 / kWaves;  // 1-KiB DMA ops per wave per tile (K and V)
     constexpr int NP = p_terms<DT>();
     static_assert(DPW >= 2 && DPW % 2 == 0, "tile split");
-    __shared__ __attribute__((aligned(16))) char ring[kNBuf][2 * MAT];
+    constexpr int NB = TPB == 1 ? kNBuf : 2 * TPB;  // ring slots
+    __shared__ __attribute__((aligned(16))) char ring[NB][2 * MAT];
 
     const int qb = gridDim.x - 1 - blockIdx.x;  // longest rows first
     const int kvh = blockIdx.y;
@@ -75,6 +76,7 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
     const int n = lane & 15, g = lane >> 4;
     const int t0 = qb * 16;
     const int G = p.G;
+    MUGEN_TRACE(0);
 
     // keys visible to the last token of the block; this lane's row limit
     int kend = p.kv_len;
@@ -102,7 +104,7 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
     const uint16_t* vb = p.v + (int64_t)kvh * D;
     auto issue = [&](int it) {
         const int kt = it * kKT;
-        const uint32_t lds0 = ring_base + (it % kNBuf) * (2 * MAT) + w * 1024;
+        const uint32_t lds0 = ring_base + (it % NB) * (2 * MAT) + w * 1024;
 #pragma unroll
         for (int k = 0; k < DPW / 2; k++) {
             const uint32_t off = (uint32_t)min(kt + dma_row[k], kend - 1) * rs_bytes + dma_col[k];
@@ -110,7 +112,10 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
             dma16s(lds0 + MAT + k * kWaves * 1024, vb, off);
         }
     };
-    for (int it = 0; it < min(ntiles, kNBuf - 1); it++) issue(it);
+    // TPB = 1: three tiles in flight, one barrier per tile.  TPB > 1: TPB
+    // tiles per barrier (the later tiles' operands are read during the
+    // first tile's MFMAs), TPB tiles in flight in a ring of 2 TPB slots
+    for (int it = 0; it < min(ntiles, TPB == 1 ? kNBuf - 1 : TPB); it++) issue(it);
 
     // Q^T fragments: lane holds q[token t0+n][head][32kk + 8g .. +8]
     u32x4_t qf[MB][KK];
@@ -125,6 +130,7 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
         for (int kk = 0; kk < KK; kk++) qf[mb][kk] = load16(qp + 32 * kk);
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no compiler waits inside the loop
+    MUGEN_TRACE(1);
 
     // K operand (A): row 32kh + 8(n/4) + n%4 (+4nb), logical chunk g + 4kk
     const int ar = 32 * kh + 8 * (n >> 2) + (n & 3);
@@ -153,33 +159,25 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
     // lazy max: weights may grow to 2^kHeadroom before the row is re-based
     constexpr float kHeadroom = 8.f;
 
-    for (int it = 0; it < ntiles; it++) {
-        // tiles issued after `it`: min(ntiles - 1, it + kNBuf - 2) - it
-        const int after = min(ntiles - 1, it + kNBuf - 2) - it;
-        if (after >= 2) vm_wait<2 * DPW>();
-        else if (after == 1) vm_wait<DPW>();
-        else vm_wait<0>();
-        lds_barrier();  // tile `it` landed for all waves; tile it-1's buffer is free
-        if (it + kNBuf - 1 < ntiles) issue(it + kNBuf - 1);
-        const char* tile = &ring[it % kNBuf][0];
-        const int kt = it * kKT;
-        const bool need_mask = kt + kKT > mask_from;
-
-        // K operand fragments, shared by the MB heads
-        u32x4_t af[2][KK];
+    // operands of one tile: K fragments (A, shared by the MB heads) and the
+    // V transpose fragments
+    auto load_ops = [&](int it, u32x4_t (&af)[2][KK], u32x4_t (&vf)[DB]) {
+        const char* tile = &ring[it % NB][0];
 #pragma unroll
         for (int nb = 0; nb < 2; nb++)
 #pragma unroll
             for (int kk = 0; kk < KK; kk++)
                 af[nb][kk] = *reinterpret_cast<const u32x4_t*>(tile + a_off[kk] + nb * 4 * RB);
-        u32x4_t vf[DB];
 #pragma unroll
         for (int d = 0; d < DB; d++) {
             const u32x2_t lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(tile + t_off[d]));
             const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(tile + t_off[d] + 4 * RB));
             vf[d] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
         }
-
+    };
+    auto compute = [&](int it, const u32x4_t (&af)[2][KK], const u32x4_t (&vf)[DB]) {
+        const int kt = it * kKT;
+        const bool need_mask = kt + kKT > mask_from;
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) {
             if (!head_ok[mb]) continue;
@@ -236,8 +234,41 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
 #pragma unroll
                 for (int pp = 0; pp < NP; pp++) o[mb][d] = mfma16x16x32<DT>(vf[d], pfr[pp], o[mb][d]);
         }
+    };
+
+    if constexpr (TPB == 1) {
+        for (int it = 0; it < ntiles; it++) {
+            // tiles issued after `it`: min(ntiles - 1, it + kNBuf - 2) - it
+            const int after = min(ntiles - 1, it + kNBuf - 2) - it;
+            if (after >= 2) vm_wait<2 * DPW>();
+            else if (after == 1) vm_wait<DPW>();
+            else vm_wait<0>();
+            lds_barrier();  // tile `it` landed for all waves; tile it-1's buffer is free
+            if (it + kNBuf - 1 < ntiles) issue(it + kNBuf - 1);
+            u32x4_t af[2][KK], vf[DB];
+            load_ops(it, af, vf);
+            compute(it, af, vf);
+        }
+    } else {
+        for (int it = 0; it < ntiles; it += TPB) {
+            vm_wait<0>();   // tiles it .. it+TPB-1 (everything issued) landed
+            if (it == 0) MUGEN_TRACE(4);
+            lds_barrier();  // ... for all waves; the slots of the previous TPB tiles are free
+            if (it == 0) MUGEN_TRACE(5);
+#pragma unroll
+            for (int k = 0; k < TPB; k++)
+                if (it + TPB + k < ntiles) issue(it + TPB + k);
+            u32x4_t af[TPB][2][KK], vf[TPB][DB];
+#pragma unroll
+            for (int k = 0; k < TPB; k++)
+                if (it + k < ntiles) load_ops(it + k, af[k], vf[k]);
+#pragma unroll
+            for (int k = 0; k < TPB; k++)
+                if (it + k < ntiles) compute(it + k, af[k], vf[k]);
+        }
     }
 
+    MUGEN_TRACE(2);
     // ---- merge the two key halves: waves 4..7 hand (m, l, O) to waves 0..3
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
@@ -293,6 +324,7 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
             }
         }
     }
+    MUGEN_TRACE(3);
 }
 
 // ------------------------------------------------------------------ warp-specialised variant
@@ -593,7 +625,11 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
 template <int D, int MB, int DT, int OUT_DT>
 static hipError_t launch_pf_t(const GqaPrefillParams& p, int Hk, hipStream_t st, KernelTimer* t) {
     dim3 grid((p.N + 15) / 16, Hk);
-    return launch_k(t, "gqa_prefill", gqa_prefill_kernel<D, MB, DT, OUT_DT>, grid, dim3(64 * kWaves), st, p);
+    // head_dim 64: two tiles per barrier (Llama-3.2-1B N = 512: 8.7 -> 8.0-8.2
+    // us; four per barrier, in an 8-slot ring, measured the same); head_dim
+    // 128 keeps one (the second tile's operands would not fit in registers)
+    constexpr int TPB = D == 64 ? 2 : 1;
+    return launch_k(t, "gqa_prefill", gqa_prefill_kernel<D, MB, DT, OUT_DT, TPB>, grid, dim3(64 * kWaves), st, p);
 }
 
 template <int D, int MB, int DT>
