@@ -136,7 +136,11 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     const int T = clamp_len(p.seq_lens[b], p.max_T);
     const int t_begin = s * p.chunk;
     const int t_end = min(t_begin + p.chunk, T);
-    const int ntiles = (t_end - t_begin + kTT - 1) / kTT;
+    // tiles past the last visible token of the workgroup's last row (a
+    // causal prompt's early rows) are not walked; a split that no row of
+    // the workgroup sees stores an empty partial (m = -inf, l = 0, o = 0)
+    const int t_stop = min(t_end, max(t_begin, T - p.q_len + min(rb * 64 + 63, p.R - 1) / p.H + 1));
+    const int ntiles = (t_stop - t_begin + kTT - 1) / kTT;
     const int row0 = rb * 64 + w * 16;
     const uint16_t* lat = p.lat + (int64_t)b * p.seq_stride;
 
@@ -167,7 +171,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
 
     // ---- Q^T fragments (B operand): lane holds Q[row0+n][32ks+8g .. +8].
     // The first tiles' DMA goes out before the q loads: both latencies overlap
-    issue(t_begin, 0);
+    if (ntiles > 0) issue(t_begin, 0);
     if (ntiles > 1) issue(t_begin + kTT, 1);
     u32x4_t qf[NQ][KS];
     const int row = row0 + n;
@@ -480,8 +484,12 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
     const int T = clamp_len(p.seq_lens[b], p.max_T);
     const int t_begin = s * p.chunk;
     const int t_end = min(t_begin + p.chunk, T);
-    const int ntiles = (t_end - t_begin + kTT - 1) / kTT;
     const int row0 = rb * 64;  // first query row of the workgroup
+    // tiles past the last visible token of the workgroup's last row (a
+    // causal prompt's early rows) are not walked; a split that no row of
+    // the workgroup sees stores an empty partial (m = -inf, l = 0, o = 0)
+    const int t_stop = min(t_end, max(t_begin, T - p.q_len + min(row0 + 63, p.R - 1) / p.H + 1));
+    const int ntiles = (t_stop - t_begin + kTT - 1) / kTT;
     const uint16_t* lat = p.lat + (int64_t)b * p.seq_stride;
     const uint32_t ring_base = lds_addr(&ring[0]);
     char* pbuf = &ring[NSLOT * kTileBytes];
@@ -665,7 +673,7 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
         MUGEN_TRACE(5);
     } else {
         // ================================================== PV waves
-        issue(0);
+        if (ntiles > 0) issue(0);
         if (ntiles > 1) issue(1);
         // V operand (transpose reads): lane (i, g) of read hh reads row
         // 8g + 4hh + i/4, logical bytes 32cb + 8*(i%4) (column block cb)
