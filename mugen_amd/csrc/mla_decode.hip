@@ -81,6 +81,40 @@ __device__ __forceinline__ int64_t blob_pair(const MlaParams& p, int b, int s, i
     return ((((int64_t)b * p.num_splits + s) * p.nq + q) * 16 + dp) * 64 + lane;
 }
 
+// XCD-aware work mapping, shared by both kernels.  Workgroups are dealt to
+// the 8 XCDs round-robin by blockIdx.  The work units are the (sequence,
+// split, 64-row block) triples of the ACTIVE splits (sequence j contributes
+// ceil(seq_lens[j] / chunk) splits, in order), numbered group-major: unit =
+// (sequence, split) group * nrb + row block.  Each XCD takes a contiguous
+// range of ceil(units / 8), so the row blocks of a group share one XCD's L2
+// for the latent tiles (a group straddles two XCDs at most at a range
+// boundary), consecutive splits of a sequence share it for the query rows,
+// and every XCD gets an even share, also with fewer groups than XCDs (a long
+// prompt: many row blocks, few splits).  The grid is sized from the host's
+// group count (exact with the length hint, an upper bound without); surplus
+// workgroups exit at once.
+__device__ __forceinline__ bool mla_map(const MlaParams& p, int& b, int& s, int& rb) {
+    const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
+    int nact = 0;
+    for (int j = 0; j < p.B; j++) nact += (clamp_len(p.seq_lens[j], p.max_T) + p.chunk - 1) / p.chunk;  // uniform scalar loop
+    const int units = nact * p.nrb;
+    const int upx = (units + 7) / 8;
+    const int unit = xcd * upx + slot;
+    if (slot >= upx || unit >= units) return false;
+    const int grp = unit / p.nrb;
+    rb = unit - grp * p.nrb;
+    for (int j = 0, acc = 0; j < p.B; j++) {
+        const int nsj = (clamp_len(p.seq_lens[j], p.max_T) + p.chunk - 1) / p.chunk;
+        if (grp < acc + nsj) {
+            b = j;
+            s = grp - acc;
+            return true;
+        }
+        acc += nsj;
+    }
+    return false;
+}
+
 // Kernel "rows" (16-bit q, at most 64 query rows: small-head decode):
 // workgroup = (64 query rows, context split, sequence), 4 waves of 16
 // rows, one wave per SIMD.  Each wave keeps the q of its rows in registers
@@ -95,38 +129,8 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
     constexpr int DSTRIDE = NW * 1024;         // LDS bytes between a wave's DMA ops
     __shared__ __attribute__((aligned(1024))) char ring[kNBuf * kTileBytes];
 
-    // XCD-aware work mapping.  Workgroups are dealt to the 8 XCDs round-robin
-    // by blockIdx.  A group = the nrb row blocks of one (sequence, split);
-    // groups are numbered compactly over the ACTIVE splits (sequence j
-    // contributes ceil(seq_lens[j] / chunk) of them, in order), and each XCD
-    // takes a contiguous range of ceil(active / 8) groups.  So all row blocks
-    // of a group share one XCD's L2 for the latent tiles, consecutive splits
-    // of a sequence share it for the query rows (each sequence's q is fetched
-    // into one or two L2s, not all eight), and every XCD gets an even share.
-    // The grid is sized from the host's group count (exact with the length
-    // hint, an upper bound without); surplus workgroups exit at once.
-    const int nxcd = 8;
-    const int xcd = blockIdx.x % nxcd, slot = blockIdx.x / nxcd;
-    const int nrb = p.nrb;
-    const int rb = slot % nrb;
-    int nact = 0;
-    for (int j = 0; j < p.B; j++) nact += (clamp_len(p.seq_lens[j], p.max_T) + p.chunk - 1) / p.chunk;  // uniform scalar loop
-    const int gpx = (nact + nxcd - 1) / nxcd;
-    const int gi = slot / nrb;
-    const int grp = xcd * gpx + gi;  // active (sequence, split) group
-    int b = -1, s = 0;
-    if (gi < gpx) {
-        for (int j = 0, acc = 0; j < p.B; j++) {
-            const int nsj = (clamp_len(p.seq_lens[j], p.max_T) + p.chunk - 1) / p.chunk;
-            if (grp < acc + nsj) {
-                b = j;
-                s = grp - acc;
-                break;
-            }
-            acc += nsj;
-        }
-    }
-    if (b < 0) return;  // grid padding past the last active split
+    int b, s, rb;
+    if (!mla_map(p, b, s, rb)) return;  // grid padding past the last active unit
     MUGEN_TRACE(0);
 
     const int tid = threadIdx.x;
@@ -451,29 +455,8 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
     __shared__ __attribute__((aligned(16))) float rs_alpha[2][64];  // per tile parity and row: O's re-base factor
     __shared__ __attribute__((aligned(16))) int rs_flag[2][4];  // per tile parity and S wave: any row re-based
 
-    // work mapping: as mla_decode_kernel (XCD-blocked active groups)
-    const int nxcd = 8;
-    const int xcd = blockIdx.x % nxcd, slot = blockIdx.x / nxcd;
-    const int nrb = p.nrb;
-    const int rb = slot % nrb;
-    int nact = 0;
-    for (int j = 0; j < p.B; j++) nact += (clamp_len(p.seq_lens[j], p.max_T) + p.chunk - 1) / p.chunk;
-    const int gpx = (nact + nxcd - 1) / nxcd;
-    const int gi = slot / nrb;
-    const int grp = xcd * gpx + gi;
-    int b = -1, s = 0;
-    if (gi < gpx) {
-        for (int j = 0, acc = 0; j < p.B; j++) {
-            const int nsj = (clamp_len(p.seq_lens[j], p.max_T) + p.chunk - 1) / p.chunk;
-            if (grp < acc + nsj) {
-                b = j;
-                s = grp - acc;
-                break;
-            }
-            acc += nsj;
-        }
-    }
-    if (b < 0) return;
+    int b, s, rb;
+    if (!mla_map(p, b, s, rb)) return;
     MUGEN_TRACE(0);
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -910,7 +893,7 @@ int mla_tile_tokens(int) { return kTT; }
 
 template <int QDT, int DT, int OUT_DT>
 static hipError_t launch_mla_t(const MlaParams& p, int kernel, hipStream_t st, KernelTimer* t) {
-    const int grid = 8 * p.nrb * ((p.groups + 7) / 8);  // see the XCD mapping in the kernels
+    const int grid = 8 * ((p.nrb * p.groups + 7) / 8);  // see mla_map
     hipError_t e = kernel == 1
                        ? launch_k(t, "mla_decode", mla_decode_kernel<QDT, DT>, dim3(grid), dim3(256), st, p)
                        : launch_k(t, "mla_decode", mla_decode_ws_kernel<QDT, DT>, dim3(grid), dim3(512), st, p);
