@@ -327,12 +327,12 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
     MUGEN_TRACE(3);
 }
 
-// ------------------------------------------------------------------ warp-specialised variant
+// ------------------------------------------------------------------ warp-specialised kernel
 //
 // For long prompts the kernel above is bound neither by MFMA issue nor by
 // LDS bandwidth but by its serial per-tile chain: the two waves of a SIMD
 // run their MFMA and softmax phases in lock step (one barrier per tile).
-// This variant gives the two phases to different waves, as the MLA decode
+// This kernel gives the two phases to different waves, as the MLA decode
 // kernel does:
 //  * workgroup = (16-token query block, kv head, slice of NS = 4 or 8 heads
 //    of the group); blocks are numbered longest-first across all kv heads
@@ -685,9 +685,9 @@ static hipError_t launch_pf_ws(const GqaPrefillParams& p, int Hk, int dt, int ou
     return launch_pf_ws_o<D, DT_BF16>(p, Hk, out_dt, st, t);
 }
 
-hipError_t launch_gqa_prefill(const GqaPrefillParams& p, int Hk, int D, int dt, int out_dt, int variant,
+hipError_t launch_gqa_prefill(const GqaPrefillParams& p, int Hk, int D, int dt, int out_dt, int kernel,
                               hipStream_t st, KernelTimer* t) {
-    if (variant == 2) return D == 128 ? launch_pf_ws<128>(p, Hk, dt, out_dt, st, t)
+    if (kernel == 2) return D == 128 ? launch_pf_ws<128>(p, Hk, dt, out_dt, st, t)
                                       : launch_pf_ws<64>(p, Hk, dt, out_dt, st, t);
     if (D == 128) return launch_pf_g<128>(p, Hk, dt, out_dt, st, t);
     return launch_pf_g<64>(p, Hk, dt, out_dt, st, t);
