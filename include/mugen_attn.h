@@ -205,8 +205,10 @@ int mugen_attn_gqa_decode_q4(const mugen_attn_gqa_decode_q4_args* args, void* wo
  *   token i attends to keys [0, start_pos + i]   (kernel_sources.h:2796)
  *   causal = 0 lets every token see all kv_len keys.
  *
- * Supported: head_dim in {64, 128}; n_heads / n_kv_heads in [1, 8];
- * dtype F16 or BF16 for q/k/v; out_dtype F16/BF16/F32.  No workspace.
+ * Supported: head_dim in {64, 128}; n_heads / n_kv_heads in [1, 16] (more
+ * than 8 runs on the warp-specialised kernel; forcing the per-block kernel
+ * there is refused); dtype F16 or BF16 for q/k/v; out_dtype F16/BF16/F32.
+ * No workspace.
  */
 typedef struct mugen_attn_gqa_prefill_args {
     const void* q;

@@ -529,8 +529,10 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     if (a->n_tokens < 0 || a->n_heads <= 0 || a->n_kv_heads <= 0 || a->kv_len < 0 || a->start_pos < 0)
         return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: negative size");
     if (a->n_heads % a->n_kv_heads) return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: n_heads % n_kv_heads != 0");
-    if (a->n_heads / a->n_kv_heads > 8)
-        return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: n_heads/n_kv_heads > 8");
+    if (a->n_heads / a->n_kv_heads > 16)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: n_heads/n_kv_heads > 16");
+    if (a->n_heads / a->n_kv_heads > 8 && a->kernel == MUGEN_ATTN_PREFILL_KERNEL_BLOCK)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: the per-block kernel serves at most 8 heads per kv head");
     if (a->head_dim != 64 && a->head_dim != 128)
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: head_dim %d (supported: 64, 128)", a->head_dim);
     if (!is16(a->dtype) || !is_out(a->out_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: dtype");
@@ -560,10 +562,11 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     const float scale = a->scale > 0.f ? a->scale : 1.f / sqrtf((float)a->head_dim);
     p.scale_log2 = scale * kLog2e;
     // the warp-specialised kernel where it measured faster: 1024..4096-token
-    // prompts (at 512 tokens and at 8192 the per-block kernel is ahead);
+    // prompts (at 512 tokens and at 8192 the per-block kernel is ahead), and
+    // for more than 8 heads per kv head (it takes them in slices of 8);
     // args->kernel forces one
-    int kernel = (a->n_tokens >= 1024 && a->n_tokens <= 4096) ? MUGEN_ATTN_PREFILL_KERNEL_WS
-                                                               : MUGEN_ATTN_PREFILL_KERNEL_BLOCK;
+    int kernel = (a->n_tokens >= 1024 && a->n_tokens <= 4096) || p.G > 8 ? MUGEN_ATTN_PREFILL_KERNEL_WS
+                                                                         : MUGEN_ATTN_PREFILL_KERNEL_BLOCK;
     if (a->kernel == MUGEN_ATTN_PREFILL_KERNEL_BLOCK || a->kernel == MUGEN_ATTN_PREFILL_KERNEL_WS) kernel = a->kernel;
     hipError_t e = launch_gqa_prefill(p, a->n_kv_heads, a->head_dim, a->dtype, a->out_dtype, kernel,
                                       static_cast<hipStream_t>(stream), active_timer());

@@ -107,6 +107,12 @@ def test_prefill_rejects_bad_args():
     assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.E_UNSUPPORTED
     a.head_dim, a.n_tokens = 64, 0
     assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.OK  # nothing to do
+    a.n_heads, a.n_kv_heads = 32, 1  # 32 heads per kv head
+    assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.E_UNSUPPORTED
+    a.n_kv_heads, a.kernel = 2, _capi.PREFILL_KERNEL_BLOCK  # 16 per kv head: the per-block kernel cannot
+    assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.E_UNSUPPORTED
+    a.kernel = 0
+    assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.OK
 
 
 def test_scatter_kv_validation():

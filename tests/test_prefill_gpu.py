@@ -88,3 +88,16 @@ def test_warp_specialised_non_causal(device):
                           c["v"].reshape(1, c["kv_len"], 2, 128).repeat(33, 0), [c["kv_len"]] * 33, 14, 2, 128,
                           c["kv_len"] * 2 * 128)
     C.assert_close(run_gpu(c, device, C.F32, causal=False, kernel=_capi.PREFILL_KERNEL_WS), ref, "ws non-causal")
+
+
+@pytest.mark.parametrize("N,H,Hk,D,start,dtype", [(300, 32, 2, 128, 40, C.BF16), (129, 24, 2, 64, 0, C.F16),
+                                                  (70, 16, 1, 128, 5, C.F16)])
+def test_more_than_8_heads_per_kv_head(device, N, H, Hk, D, start, dtype):
+    # 12 / 16 query heads per kv head: the warp-specialised kernel in slices of 8
+    c = C.prefill_case(60 + H, N, H, Hk, D, start, dtype)
+    ref = C.prefill_ref(c, nthreads=8)
+    C.assert_close(run_gpu(c, device, C.F32), ref, f"prefill G={H // Hk}")
+    C.assert_close(run_gpu(c, device, C.F32, kernel=_capi.PREFILL_KERNEL_WS), ref, f"prefill G={H // Hk} forced")
+    with pytest.raises(_capi.MugenAttnError):
+        run_gpu(c, device, C.F32, kernel=_capi.PREFILL_KERNEL_BLOCK)
+
