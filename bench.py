@@ -240,14 +240,14 @@ class Prefill(Case):
 class MlaFull(Case):
     """The attention part of one MLA decode layer (transformer.cpp:3882-3995,
     from the q / kv_a projections to the attention output): latent-cache
-    write of the new token (c_kv RMSNorm, k_rope YaRN RoPE, append), q RoPE
-    fused into absorption by attn_k_b, the latent core with the fp32
+    write of the new token (c_kv RMSNorm, k_rope YaRN RoPE, append) and q
+    RoPE fused into absorption by attn_k_b (one launch at decode sizes), the latent core with the fp32
     absorbed q over the f16 latent cache, up-projection by attn_v_b to f16,
     weights in a GGML block encoding.  Bytes: both weight matrices, the
     latent rows read and written, q in, q_abs and o out and back, out."""
     bound = "hbm"
     kernel = "mla_decode"
-    extra_kernels = ("mla_latent_write", "mla_absorb", "mla_project")
+    extra_kernels = ("mla_prepare", "mla_latent_write", "mla_absorb", "mla_project")
 
     def __init__(self, dev, B, H, lens, max_T, w_type, seed, name, q_len=1, profile=("mla_layer", "v3_b8_q8_0")):
         self.name = name
@@ -293,9 +293,9 @@ class MlaFull(Case):
             self.bound, self.unit = "mfma", "TFLOP/s"
 
     def step(self):
-        mugen_amd.mla_latent_write(self.kv_a, self.norm_w, self.pos, self.lat, rows_per_seq=self.q_len,
-                                   rope=self.rope)
-        mugen_amd.mla_absorb(self.q, self.w_kb, self.w_type, out=self.qa, positions=self.pos, rope=self.rope)
+        # latent write + absorption: one launch at decode sizes
+        mugen_amd.mla_prepare(self.kv_a, self.norm_w, self.pos, self.lat, self.q, self.w_kb, self.w_type,
+                              q_abs=self.qa, rows_per_seq=self.q_len, rope=self.rope)
         mugen_amd.mla_attention(self.qa, self.lat, self.sl, self.max_T, scale=MLA_SCALE, out=self.o,
                                 workspace=self.ws, seq_lens_host=self.lens)
         mugen_amd.mla_project(self.o, self.w_vb, self.w_type, out=self.out)

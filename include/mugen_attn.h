@@ -434,6 +434,20 @@ typedef struct mugen_attn_mla_latent_write_args {
 int mugen_attn_mla_latent_write(const mugen_attn_mla_latent_write_args* args, void* stream);
 
 /*
+ * The two independent stages that precede the latent core in one call:
+ * the latent write of the step's new tokens (as mugen_attn_mla_latent_write,
+ * transformer.cpp:3930-3987) and the absorption of their queries (as
+ * mugen_attn_mla_absorb, transformer.cpp:2563-2573 with the q RoPE of
+ * :3882-3921).  Results are identical to the two calls.  At decode sizes
+ * (absorb rows < 64) both run in ONE kernel launch, which removes a launch
+ * from the layer step; at prompt sizes they run as the two launches.  The
+ * absorption must not read the latent rows being written (it does not: it
+ * reads q and W_UK only).  Either args' rows may be 0.
+ */
+int mugen_attn_mla_prepare(const mugen_attn_mla_latent_write_args* latent_write,
+                           const mugen_attn_mla_absorb_args* absorb, void* stream);
+
+/*
  * Decode-step helpers for captured HIP graphs.  The reference caches its
  * whole decode step as one dispatch chain ("mega-chain",
  * transformer.cpp:3734-3833) and patches pos / kv_offset / seq_len into the

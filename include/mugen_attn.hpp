@@ -85,6 +85,10 @@ inline Status mla_project(const mugen_attn_mla_project_args& a, void* stream) {
 inline Status mla_latent_write(const mugen_attn_mla_latent_write_args& a, void* stream) {
     return check(mugen_attn_mla_latent_write(&a, stream));
 }
+inline Status mla_prepare(const mugen_attn_mla_latent_write_args& lw, const mugen_attn_mla_absorb_args& ab,
+                          void* stream) {
+    return check(mugen_attn_mla_prepare(&lw, &ab, stream));
+}
 inline Status kv_q4_append(const mugen_attn_kv_q4_append_args& a, void* stream) {
     return check(mugen_attn_kv_q4_append(&a, stream));
 }

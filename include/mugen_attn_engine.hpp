@@ -772,7 +772,7 @@ private:
     const int32_t* before() const { return static_cast<const int32_t*>(lens_.ptr); }
     int64_t seq_stride() const { return (int64_t)s_.max_seq_len * 576; }
 
-    // latent write -> absorb (q RoPE fused) -> core -> projection for
+    // latent write + absorb (q RoPE fused) -> core -> projection for
     // sequences [seq, seq + n_seq), rows_per_seq tokens each, the core
     // attending over `core_lens` (device, the lengths including the new rows)
     Status layer(int L, const MlaLayerWeights& w, const void* q, const void* kv_a, void* out, int seq, int n_seq,
@@ -792,7 +792,6 @@ private:
         lw.seq_stride = seq_stride();
         lw.eps = s_.rms_norm_eps;
         lw.rope = s_.rope;
-        if (auto r = mla_latent_write(lw, st); !r) return r;
         mugen_attn_mla_absorb_args ab{};
         ab.q = q;
         ab.w_kb = w.w_kb;
@@ -807,7 +806,8 @@ private:
         ab.seq_base = before() + seq;
         ab.rows_per_seq = rows_per_seq;
         ab.rope = s_.rope;
-        if (auto r = mla_absorb(ab, st); !r) return r;
+        // the latent write and the absorption in one launch (decode sizes)
+        if (auto r = mla_prepare(lw, ab, st); !r) return r;
         mugen_attn_mla_decode_args m = core_args(L, n_seq, rows_per_seq, core_lens);
         m.latent = lat;
         if (auto r = mla_decode(m, ws_.ptr, ws_.bytes, st); !r) return r;

@@ -37,6 +37,7 @@ EXPORTS = (
     "mugen_attn_mla_absorb",
     "mugen_attn_mla_project",
     "mugen_attn_mla_latent_write",
+    "mugen_attn_mla_prepare",
     "mugen_attn_kv_append",
     "mugen_attn_seq_advance",
     "mugen_attn_scatter_kv",
@@ -183,6 +184,8 @@ def lib() -> ctypes.CDLL:
         L.mugen_attn_mla_project.restype = ctypes.c_int
         L.mugen_attn_mla_latent_write.argtypes = [ctypes.POINTER(MlaLatentWriteArgs), _vp]
         L.mugen_attn_mla_latent_write.restype = ctypes.c_int
+        L.mugen_attn_mla_prepare.argtypes = [ctypes.POINTER(MlaLatentWriteArgs), ctypes.POINTER(MlaAbsorbArgs), _vp]
+        L.mugen_attn_mla_prepare.restype = ctypes.c_int
         L.mugen_attn_kv_append.argtypes = [ctypes.POINTER(KvAppendArgs), _vp]
         L.mugen_attn_kv_append.restype = ctypes.c_int
         L.mugen_attn_seq_advance.argtypes = [_vp, _i32, _i32, _i32, _vp, _vp, _vp]

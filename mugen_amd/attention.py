@@ -195,19 +195,8 @@ def _rope(rope) -> _capi.RopeParams:
     return _capi.RopeParams(float(theta), float(factor), int(ctx))
 
 
-def mla_absorb(q: torch.Tensor, w_kb: torch.Tensor, w_type=None, *, out: torch.Tensor | None = None,
-               out_dtype: torch.dtype = torch.float32, positions: torch.Tensor | None = None,
-               rope=(10000.0, 0.0, 0), seq_base: torch.Tensor | None = None, rows_per_seq: int = 1) -> torch.Tensor:
-    """q_abs = [q_nope . k_b | q_rope] per head (transformer.cpp:2556-2573).
-
-    q f16 [..., H, 192]; w_kb = attn_k_b, H*128 rows of 512 in the GGML
-    encoding w_type ('f16' as a float16 tensor, 'q8_0' / 'q4_0' as uint8
-    bytes).  Returns [..., H, 576] in out_dtype (F32 or BF16).  With
-    positions (int32, one per row of q), q_rope is first rotated by the
-    reference's q RoPE stage (transformer.cpp:3882-3921) with
-    rope = (theta, yarn factor, original ctx).  With seq_base (int32
-    [n_seq]) instead of positions, row r is rotated at
-    seq_base[r // rows_per_seq] + r % rows_per_seq."""
+def _absorb_args(q, w_kb, w_type, out, out_dtype, positions, rope, seq_base, rows_per_seq):
+    """The absorb call's ABI arguments (validated) and its output tensor."""
     _need_cuda(q, w_kb)
     if q.dtype != torch.float16 or q.shape[-1] != 192:
         raise ValueError("q must be float16 [..., H, 192]")
@@ -229,6 +218,23 @@ def mla_absorb(q: torch.Tensor, w_kb: torch.Tensor, w_type=None, *, out: torch.T
         if seq_base.dtype != torch.int32:
             raise TypeError("seq_base must be int32")
         a.seq_base, a.rows_per_seq, a.rope = seq_base.data_ptr(), int(rows_per_seq), _rope(rope)
+    return a, out
+
+
+def mla_absorb(q: torch.Tensor, w_kb: torch.Tensor, w_type=None, *, out: torch.Tensor | None = None,
+               out_dtype: torch.dtype = torch.float32, positions: torch.Tensor | None = None,
+               rope=(10000.0, 0.0, 0), seq_base: torch.Tensor | None = None, rows_per_seq: int = 1) -> torch.Tensor:
+    """q_abs = [q_nope . k_b | q_rope] per head (transformer.cpp:2556-2573).
+
+    q f16 [..., H, 192]; w_kb = attn_k_b, H*128 rows of 512 in the GGML
+    encoding w_type ('f16' as a float16 tensor, 'q8_0' / 'q4_0' as uint8
+    bytes).  Returns [..., H, 576] in out_dtype (F32 or BF16).  With
+    positions (int32, one per row of q), q_rope is first rotated by the
+    reference's q RoPE stage (transformer.cpp:3882-3921) with
+    rope = (theta, yarn factor, original ctx).  With seq_base (int32
+    [n_seq]) instead of positions, row r is rotated at
+    seq_base[r // rows_per_seq] + r % rows_per_seq."""
+    a, out = _absorb_args(q, w_kb, w_type, out, out_dtype, positions, rope, seq_base, rows_per_seq)
     _capi.check(_capi.lib().mugen_attn_mla_absorb(ctypes.byref(a), _stream(q.device)))
     return out
 
@@ -267,15 +273,8 @@ def mla_attention_full(q: torch.Tensor, w_kb: torch.Tensor, w_vb: torch.Tensor, 
     return mla_project(o, w_vb, w_type)
 
 
-def mla_latent_write(kv_a: torch.Tensor, norm_w: torch.Tensor, positions: torch.Tensor | None, latent: torch.Tensor,
-                     *, rows_per_seq: int = 1, eps: float = 1e-6, rope=(10000.0, 0.0, 0),
-                     max_seq_len: int | None = None, seq_base: torch.Tensor | None = None) -> torch.Tensor:
-    """Latent-cache writer (transformer.cpp:3930-3987): RMSNorm(c_kv) * norm_w
-    and RoPE(k_rope) of each kv_a row [rows, 576] (f16), written to row
-    positions[r] of sequence r // rows_per_seq of latent [n_seq, max_T, 576]
-    (f16 or bf16).  rope = (theta, yarn factor, original ctx).  With
-    positions None, row r goes to seq_base[r // rows_per_seq] +
-    r % rows_per_seq."""
+def _latent_args(kv_a, norm_w, positions, latent, rows_per_seq, eps, rope, max_seq_len, seq_base):
+    """The latent write's ABI arguments (validated)."""
     _need_cuda(kv_a, norm_w, latent)
     if kv_a.dtype != torch.float16 or norm_w.dtype != torch.float16 or kv_a.shape[-1] != 576:
         raise ValueError("kv_a must be float16 [rows, 576] and norm_w float16 [512]")
@@ -300,8 +299,33 @@ def mla_latent_write(kv_a: torch.Tensor, norm_w: torch.Tensor, positions: torch.
     a.seq_stride, a.eps, a.rope = latent[0].numel(), float(eps), _rope(rope)
     if (rows + a.rows_per_seq - 1) // a.rows_per_seq > latent.shape[0]:
         raise ValueError("more sequences than latent has")
+    return a
+
+
+def mla_latent_write(kv_a: torch.Tensor, norm_w: torch.Tensor, positions: torch.Tensor | None, latent: torch.Tensor,
+                     *, rows_per_seq: int = 1, eps: float = 1e-6, rope=(10000.0, 0.0, 0),
+                     max_seq_len: int | None = None, seq_base: torch.Tensor | None = None) -> torch.Tensor:
+    """Latent-cache writer (transformer.cpp:3930-3987): RMSNorm(c_kv) * norm_w
+    and RoPE(k_rope) of each kv_a row [rows, 576] (f16), written to row
+    positions[r] of sequence r // rows_per_seq of latent [n_seq, max_T, 576]
+    (f16 or bf16).  rope = (theta, yarn factor, original ctx).  With
+    positions None, row r goes to seq_base[r // rows_per_seq] +
+    r % rows_per_seq."""
+    a = _latent_args(kv_a, norm_w, positions, latent, rows_per_seq, eps, rope, max_seq_len, seq_base)
     _capi.check(_capi.lib().mugen_attn_mla_latent_write(ctypes.byref(a), _stream(kv_a.device)))
     return latent
+
+
+def mla_prepare(kv_a: torch.Tensor, norm_w: torch.Tensor, positions: torch.Tensor, latent: torch.Tensor,
+                q: torch.Tensor, w_kb: torch.Tensor, w_type=None, *, q_abs: torch.Tensor | None = None,
+                rows_per_seq: int = 1, eps: float = 1e-6, rope=(10000.0, 0.0, 0)) -> torch.Tensor:
+    """mla_latent_write(kv_a, norm_w, positions, latent) and mla_absorb(q,
+    w_kb, positions=positions) in one call (one kernel launch at decode
+    sizes; results identical to the two calls).  Returns q_abs (F32)."""
+    lw = _latent_args(kv_a, norm_w, positions, latent, rows_per_seq, eps, rope, None, None)
+    ab, q_abs = _absorb_args(q, w_kb, w_type, q_abs, torch.float32, positions, rope, None, 1)
+    _capi.check(_capi.lib().mugen_attn_mla_prepare(ctypes.byref(lw), ctypes.byref(ab), _stream(q.device)))
+    return q_abs
 
 
 # ------------------------------------------------------------------ decode-step helpers

@@ -711,7 +711,8 @@ static bool w_aligned(const void* w, int w_type) {
     return ((uintptr_t)w & (w_type == W_F16 ? 15 : 1)) == 0;
 }
 
-int mugen_attn_mla_absorb(const mugen_attn_mla_absorb_args* a, void* stream) {
+// validation and kernel parameters of an absorption (rows == 0: nothing to do)
+static int absorb_params(const mugen_attn_mla_absorb_args* a, MlaProjParams* p) {
     if (!a) return fail(MUGEN_ATTN_E_INVALID, "mla_absorb: null args");
     if (a->rows < 0 || a->n_heads <= 0) return fail(MUGEN_ATTN_E_INVALID, "mla_absorb: bad rows/n_heads");
     if (a->nope_dim != 128 || a->rope_dim != 64 || a->kv_rank != 512)
@@ -720,6 +721,7 @@ int mugen_attn_mla_absorb(const mugen_attn_mla_absorb_args* a, void* stream) {
     if (!is_wtype(a->w_type)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_absorb: w_type %d", a->w_type);
     if (a->out_dtype != DT_F32 && a->out_dtype != DT_BF16)
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_absorb: out_dtype must be F32 or BF16");
+    *p = MlaProjParams{};
     if (a->rows == 0) return MUGEN_ATTN_OK;
     if (!a->q || !a->w_kb || !a->q_abs) return fail(MUGEN_ATTN_E_INVALID, "mla_absorb: null pointer");
     if (((uintptr_t)a->q & 1) || ((uintptr_t)a->q_abs & 3) || !w_aligned(a->w_kb, a->w_type))
@@ -730,9 +732,16 @@ int mugen_attn_mla_absorb(const mugen_attn_mla_absorb_args* a, void* stream) {
     if (rope && !rope_ok(a->rope)) return fail(MUGEN_ATTN_E_INVALID, "mla_absorb: bad rope parameters");
     if (!a->positions && a->seq_base && a->rows_per_seq <= 0)
         return fail(MUGEN_ATTN_E_INVALID, "mla_absorb: rows_per_seq must be > 0 with seq_base");
-    MlaProjParams p{a->q, a->w_kb, a->q_abs, a->rows, a->n_heads, a->positions, {}, a->positions ? nullptr : a->seq_base,
-                    a->rows_per_seq > 0 ? a->rows_per_seq : 1};
-    if (rope) p.freqs = yarn_freqs(a->rope);
+    *p = MlaProjParams{a->q, a->w_kb, a->q_abs, a->rows, a->n_heads, a->positions, {},
+                       a->positions ? nullptr : a->seq_base, a->rows_per_seq > 0 ? a->rows_per_seq : 1};
+    if (rope) p->freqs = yarn_freqs(a->rope);
+    return MUGEN_ATTN_OK;
+}
+
+int mugen_attn_mla_absorb(const mugen_attn_mla_absorb_args* a, void* stream) {
+    MlaProjParams p;
+    if (int rc = absorb_params(a, &p)) return rc;
+    if (p.rows == 0) return MUGEN_ATTN_OK;
     return hip_status(launch_mla_absorb(p, a->w_type, a->out_dtype, static_cast<hipStream_t>(stream), active_timer()),
                       "mla_absorb launch");
 }
@@ -757,7 +766,8 @@ int mugen_attn_mla_project(const mugen_attn_mla_project_args* a, void* stream) {
                       "mla_project launch");
 }
 
-int mugen_attn_mla_latent_write(const mugen_attn_mla_latent_write_args* a, void* stream) {
+// validation and kernel parameters of a latent write (rows == 0: nothing to do)
+static int latent_params(const mugen_attn_mla_latent_write_args* a, LatentWriteParams* p) {
     if (!a) return fail(MUGEN_ATTN_E_INVALID, "mla_latent_write: null args");
     if (a->kv_rank != 512 || a->rope_dim != 64)
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_latent_write: kv_rank/rope_dim %d/%d (supported: 512/64)",
@@ -767,6 +777,7 @@ int mugen_attn_mla_latent_write(const mugen_attn_mla_latent_write_args* a, void*
         return fail(MUGEN_ATTN_E_INVALID, "mla_latent_write: bad rows/rows_per_seq/max_seq_len");
     if (!(a->eps >= 0.f) || !std::isfinite(a->eps)) return fail(MUGEN_ATTN_E_INVALID, "mla_latent_write: bad eps");
     if (!rope_ok(a->rope)) return fail(MUGEN_ATTN_E_INVALID, "mla_latent_write: bad rope parameters");
+    *p = LatentWriteParams{};
     if (a->rows == 0) return MUGEN_ATTN_OK;
     if (!a->kv_a || !a->norm_w || (!a->positions && !a->seq_base) || !a->latent)
         return fail(MUGEN_ATTN_E_INVALID, "mla_latent_write: null pointer");
@@ -776,20 +787,38 @@ int mugen_attn_mla_latent_write(const mugen_attn_mla_latent_write_args* a, void*
     if ((((uintptr_t)a->kv_a | (uintptr_t)a->norm_w | (uintptr_t)a->latent) & 15) || (a->seq_stride % 8))
         return fail(MUGEN_ATTN_E_INVALID, "mla_latent_write: kv_a/norm_w/latent must be 16-byte aligned, "
                     "seq_stride a multiple of 8");
-    LatentWriteParams p{};
-    p.kv_a = static_cast<const uint16_t*>(a->kv_a);
-    p.norm_w = static_cast<const uint16_t*>(a->norm_w);
-    p.positions = a->positions;
-    p.seq_base = a->positions ? nullptr : a->seq_base;
-    p.latent = static_cast<uint16_t*>(a->latent);
-    p.rows = a->rows;
-    p.rows_per_seq = a->rows_per_seq;
-    p.max_seq_len = a->max_seq_len;
-    p.seq_stride = a->seq_stride;
-    p.eps = a->eps;
-    p.freqs = yarn_freqs(a->rope);
+    p->kv_a = static_cast<const uint16_t*>(a->kv_a);
+    p->norm_w = static_cast<const uint16_t*>(a->norm_w);
+    p->positions = a->positions;
+    p->seq_base = a->positions ? nullptr : a->seq_base;
+    p->latent = static_cast<uint16_t*>(a->latent);
+    p->rows = a->rows;
+    p->rows_per_seq = a->rows_per_seq;
+    p->max_seq_len = a->max_seq_len;
+    p->seq_stride = a->seq_stride;
+    p->eps = a->eps;
+    p->freqs = yarn_freqs(a->rope);
+    return MUGEN_ATTN_OK;
+}
+
+int mugen_attn_mla_latent_write(const mugen_attn_mla_latent_write_args* a, void* stream) {
+    LatentWriteParams p;
+    if (int rc = latent_params(a, &p)) return rc;
+    if (p.rows == 0) return MUGEN_ATTN_OK;
     return hip_status(launch_mla_latent_write(p, a->latent_dtype, static_cast<hipStream_t>(stream), active_timer()),
                       "mla_latent_write launch");
+}
+
+int mugen_attn_mla_prepare(const mugen_attn_mla_latent_write_args* lw, const mugen_attn_mla_absorb_args* ab,
+                           void* stream) {
+    LatentWriteParams pl;
+    MlaProjParams pa;
+    if (int rc = latent_params(lw, &pl)) return rc;
+    if (int rc = absorb_params(ab, &pa)) return rc;
+    if (pl.rows == 0 && pa.rows == 0) return MUGEN_ATTN_OK;
+    return hip_status(launch_mla_prepare(pa, pl, ab->w_type, ab->out_dtype, lw->latent_dtype,
+                                         static_cast<hipStream_t>(stream), active_timer()),
+                      "mla_prepare launch");
 }
 
 int mugen_attn_kv_append(const mugen_attn_kv_append_args* a, void* stream) {

@@ -174,6 +174,9 @@ struct LatentWriteParams {
     RopeFreqs freqs;
 };
 hipError_t launch_mla_latent_write(const LatentWriteParams& p, int latent_dt, hipStream_t st, KernelTimer* t);
+// latent write + absorption in one launch at decode sizes (mla_proj.hip)
+hipError_t launch_mla_prepare(const MlaProjParams& pa, const LatentWriteParams& pl, int w_type, int out_dt,
+                              int lat_dt, hipStream_t st, KernelTimer* t);
 
 // decode-step helpers (engine.hip)
 struct KvAppendParams {

@@ -23,6 +23,7 @@
 //    shuffles for the 32 sums) leaves each lane pair with one total.
 #include "common.h"
 #include "kernels.h"
+#include "mla_latent.h"
 
 namespace mugen_attn {
 
@@ -110,13 +111,14 @@ __device__ __forceinline__ void halve(float* x, int lane) {
 
 }  // namespace
 
+// one absorb workgroup (512 threads): head h, 256-column half `half`
 template <int WT, int OUT_DT>
-__global__ __launch_bounds__(512) void mla_absorb_kernel(MlaProjParams p) {
+__device__ __forceinline__ void absorb_block(const MlaProjParams& p, int h, int half) {
     constexpr int NOPE = 128, ROPE = 64, KR = 512, RC = 8, IPW = 16;  // rows per chunk, nope rows per wave
     __shared__ __attribute__((aligned(16))) float qs[RC][NOPE];
     __shared__ __attribute__((aligned(16))) f32x4_t red[8][RC][64];  // [wave][row][lane] partials
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int d0 = blockIdx.y * 256 + 4 * lane;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int d0 = half * 256 + 4 * lane;
     constexpr int RB = wrow_bytes<WT>(KR);
     const uint8_t* wrow = static_cast<const uint8_t*>(p.w) + ((size_t)h * NOPE + w * IPW) * RB;
     WRaw<WT, 4> raw[IPW];
@@ -132,7 +134,7 @@ __global__ __launch_bounds__(512) void mla_absorb_kernel(MlaProjParams p) {
             zero |= v == 0.f;
             qs[r][i] = r < nr ? v : 0.f;
         }
-        if (blockIdx.y == 0 && tid < RC * ROPE / 2) {
+        if (half == 0 && tid < RC * ROPE / 2) {
             // q_rope appended: as is, or with the reference's q RoPE stage
             // (NeoX pairs c, c + 32, f16 results; transformer.cpp:3882-3921)
             const int r = tid / (ROPE / 2), c = tid % (ROPE / 2);
@@ -186,7 +188,7 @@ __global__ __launch_bounds__(512) void mla_absorb_kernel(MlaProjParams p) {
 #pragma unroll
             for (int ww = 1; ww < 8; ww++) t += red[ww][r][l];
             if (r < nr) {
-                const int64_t o = ((int64_t)(r0 + r) * p.H + h) * (KR + ROPE) + blockIdx.y * 256 + 4 * l;
+                const int64_t o = ((int64_t)(r0 + r) * p.H + h) * (KR + ROPE) + half * 256 + 4 * l;
                 if constexpr (OUT_DT == DT_F32) {
                     *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.out) + o) = t;  // 16-byte aligned
                 } else {
@@ -197,6 +199,26 @@ __global__ __launch_bounds__(512) void mla_absorb_kernel(MlaProjParams p) {
         }
         __syncthreads();  // qs / red are rewritten by the next chunk
     }
+}
+
+template <int WT, int OUT_DT>
+__global__ __launch_bounds__(512) void mla_absorb_kernel(MlaProjParams p) {
+    absorb_block<WT, OUT_DT>(p, blockIdx.x, blockIdx.y);
+}
+
+// One launch for the two independent stages before the latent core at decode
+// sizes: workgroups [0, 2H) absorb (head, column half), the rest write the
+// new tokens' latent rows, one wave per token.  Saves the writer's own launch
+// (the layer step's kernels run back to back).
+template <int WT, int OUT_DT, int LDT>
+__global__ __launch_bounds__(512) void mla_prepare_kernel(MlaProjParams pa, LatentWriteParams pl) {
+    const int nab = 2 * pa.H;
+    if ((int)blockIdx.x < nab) {
+        absorb_block<WT, OUT_DT>(pa, blockIdx.x % pa.H, blockIdx.x / pa.H);
+        return;
+    }
+    const int r = ((int)blockIdx.x - nab) * 8 + (int)(threadIdx.x >> 6);
+    if (r < pl.rows) latent_write_row<LDT>(pl, r, threadIdx.x & 63);
 }
 
 template <int WT, int OUT_DT>
@@ -540,6 +562,35 @@ hipError_t launch_mla_absorb(const MlaProjParams& p, int w_type, int out_dt, hip
     return w_type == W_F16 ? launch_absorb_w<W_F16>(p, out_dt, st, t)
          : w_type == W_Q8_0 ? launch_absorb_w<W_Q8_0>(p, out_dt, st, t)
                             : launch_absorb_w<W_Q4_0>(p, out_dt, st, t);
+}
+
+template <int WT, int OUT_DT>
+static hipError_t launch_prepare_o(const MlaProjParams& pa, const LatentWriteParams& pl, int lat_dt, hipStream_t st,
+                                   KernelTimer* t) {
+    const dim3 grid(2 * pa.H + (pl.rows + 7) / 8);
+    if (lat_dt == DT_BF16)
+        return launch_k(t, "mla_prepare", mla_prepare_kernel<WT, OUT_DT, DT_BF16>, grid, dim3(512), st, pa, pl);
+    return launch_k(t, "mla_prepare", mla_prepare_kernel<WT, OUT_DT, DT_F16>, grid, dim3(512), st, pa, pl);
+}
+
+template <int WT>
+static hipError_t launch_prepare_w(const MlaProjParams& pa, const LatentWriteParams& pl, int out_dt, int lat_dt,
+                                   hipStream_t st, KernelTimer* t) {
+    if (out_dt == DT_BF16) return launch_prepare_o<WT, DT_BF16>(pa, pl, lat_dt, st, t);
+    return launch_prepare_o<WT, DT_F32>(pa, pl, lat_dt, st, t);
+}
+
+hipError_t launch_mla_prepare(const MlaProjParams& pa, const LatentWriteParams& pl, int w_type, int out_dt,
+                              int lat_dt, hipStream_t st, KernelTimer* t) {
+    if (pa.rows >= kProjMfmaRows || pa.rows == 0 || pl.rows == 0) {
+        // prompt sizes (the absorb MFMA form) or one stage empty: two launches
+        if (pl.rows > 0)
+            if (hipError_t e = launch_mla_latent_write(pl, lat_dt, st, t); e != hipSuccess) return e;
+        return pa.rows > 0 ? launch_mla_absorb(pa, w_type, out_dt, st, t) : hipSuccess;
+    }
+    return w_type == W_F16 ? launch_prepare_w<W_F16>(pa, pl, out_dt, lat_dt, st, t)
+         : w_type == W_Q8_0 ? launch_prepare_w<W_Q8_0>(pa, pl, out_dt, lat_dt, st, t)
+                            : launch_prepare_w<W_Q4_0>(pa, pl, out_dt, lat_dt, st, t);
 }
 
 template <int WT>

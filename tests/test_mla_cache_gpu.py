@@ -165,3 +165,29 @@ def test_seq_base_positions_match_explicit_positions(device):
     torch.cuda.synchronize()
     assert torch.equal(a, b)
     assert torch.equal(qa, qb)
+
+
+@pytest.mark.parametrize("ldt", [C.F16, C.BF16])
+@pytest.mark.parametrize("B,q_len,H", [(8, 1, 128), (2, 3, 16), (1, 100, 16)])
+def test_prepare_equals_separate_calls(device, ldt, B, q_len, H):
+    """mla_prepare (one launch at decode sizes, two at prompt sizes) writes
+    the same latent rows and q_abs as mla_latent_write + mla_absorb."""
+    rows = B * q_len
+    g = torch.Generator(device=device).manual_seed(70 + rows)
+    kv_a = torch.randn((rows, 576), generator=g, device=device).half()
+    norm_w = (torch.randn((512,), generator=g, device=device) * 0.1 + 1.0).half()
+    q = torch.randn((B, q_len, H, 192), generator=g, device=device).half()
+    w = torch.from_numpy(C.make_weights(71, H * 128, 512, O.W_Q8_0)).to(device)
+    pos = torch.tensor([[100 * b + 7 + i for i in range(q_len)] for b in range(B)], dtype=torch.int32,
+                       device=device).reshape(-1)
+    rope = (10000.0, 40.0, 4096)
+    C.say(f"mla_prepare B={B} q_len={q_len} H={H} latent={ldt}")
+    lat1 = torch.zeros((B, 512, 576), dtype=C.torch_dtype(ldt), device=device)
+    lat2 = lat1.clone()
+    mugen_amd.mla_latent_write(kv_a, norm_w, pos, lat1, rows_per_seq=q_len, rope=rope)
+    qa1 = mugen_amd.mla_absorb(q, w, "q8_0", positions=pos, rope=rope)
+    qa2 = mugen_amd.mla_prepare(kv_a, norm_w, pos, lat2, q, w, "q8_0", rows_per_seq=q_len, rope=rope)
+    torch.cuda.synchronize()
+    assert torch.equal(lat1.view(torch.int16), lat2.view(torch.int16))
+    assert torch.equal(qa1.view(torch.int32), qa2.view(torch.int32))
+
