@@ -602,7 +602,11 @@ static int mla_decode_impl(const mugen_attn_mla_decode_args* a, void* ws, size_t
     p.R = a->q_len * a->n_heads;
     p.nrb = ceil_div(p.R, mla_rows_per_block(kernel));
     p.nq = ceil_div(p.R, 16);
-    p.groups = (int)mla_groups(a, chunk);
+    const int64_t groups = mla_groups(a, chunk);
+    // the kernels number (group, row block) units and the grid in 32 bits
+    if (groups * p.nrb > (int64_t)1 << 30)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_decode: batch * splits * row blocks too large");
+    p.groups = (int)groups;
     p.chunk = chunk;
     p.num_splits = splits;
     p.max_T = a->max_seq_len;
