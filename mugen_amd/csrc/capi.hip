@@ -207,8 +207,10 @@ static int gqa_validate(const mugen_attn_gqa_decode_args* a, bool ring_store = f
     if (a->n_heads / a->n_kv_heads > 16)
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode: n_heads/n_kv_heads = %d > 16",
                     a->n_heads / a->n_kv_heads);
-    if (a->head_dim != 64 && a->head_dim != 128)
-        return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode: head_dim %d (supported: 64, 128)", a->head_dim);
+    if (ring_store ? (a->head_dim != 64 && a->head_dim != 128)
+                   : (a->head_dim < 8 || a->head_dim > 128 || a->head_dim % 8))
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "%s: head_dim %d (supported: %s)", ring_store ? "gqa_decode_q4" : "gqa_decode",
+                    a->head_dim, ring_store ? "64, 128" : "multiples of 8 up to 128");
     if (!is16(a->kv_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode: kv_dtype must be F16 or BF16");
     if (!is_out(a->out_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode: bad out_dtype");
     if (!ring_store && a->batch > 1 && a->seq_stride < (int64_t)a->max_seq_len * a->n_kv_heads * a->head_dim)
@@ -221,14 +223,20 @@ static int gqa_validate(const mugen_attn_gqa_decode_args* a, bool ring_store = f
     return MUGEN_ATTN_OK;
 }
 
+// The decode and prefill kernels are built for head_dim 64 and 128; a
+// smaller head_dim (a multiple of 8) runs on the next one up, its extra
+// dims masked (q zero, outputs not stored).
+static int padded_head_dim(int head_dim) { return head_dim <= 64 ? 64 : 128; }
+
 // workspace: fp32 partials [B][H][splits][D] and (m, l) [B][H][splits][2]
+// (D = the padded head_dim)
 static size_t gqa_ws(const mugen_attn_gqa_decode_args* a, int chunk, int* splits_out) {
     const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
     const int splits = ceil_div(maxT, chunk);
     if (splits_out) *splits_out = splits;
     if (splits <= 1) return 0;
     const size_t slots = (size_t)a->batch * a->n_heads * splits;
-    return slots * (size_t)a->head_dim * 4 + slots * 2 * 4 + 256;
+    return slots * (size_t)padded_head_dim(a->head_dim) * 4 + slots * 2 * 4 + 256;
 }
 
 // MLA kernel (mla_decode.hip): 16-bit q with at most 64 query rows -> the
@@ -424,7 +432,7 @@ static size_t gqa_q4_ws(const mugen_attn_gqa_decode_q4_args* a, int chunk, int* 
     const int splits = ceil_div(maxT, chunk) + 1;
     if (splits_out) *splits_out = splits;
     const size_t slots = (size_t)a->batch * a->n_heads * splits;
-    return slots * (size_t)a->head_dim * 4 + slots * 2 * 4 + 256;
+    return slots * (size_t)padded_head_dim(a->head_dim) * 4 + slots * 2 * 4 + 256;
 }
 
 size_t mugen_attn_gqa_decode_q4_workspace_size(const mugen_attn_gqa_decode_q4_args* a) {
@@ -452,6 +460,7 @@ int mugen_attn_gqa_decode_q4(const mugen_attn_gqa_decode_q4_args* a, void* ws, s
     p.out = a->out;
     p.H = a->n_heads;
     p.G = a->n_heads / a->n_kv_heads;
+    p.hd = a->head_dim;
     p.row_stride = a->n_kv_heads * a->head_dim;
     p.chunk = chunk;
     p.num_splits = splits;
@@ -469,7 +478,7 @@ int mugen_attn_gqa_decode_q4(const mugen_attn_gqa_decode_q4_args* a, void* ws, s
         float* base = align256(ws);
         const size_t slots = (size_t)a->batch * a->n_heads * splits;
         p.ws_o = base;
-        p.ws_ml = base + slots * a->head_dim;
+        p.ws_ml = base + slots * padded_head_dim(a->head_dim);
     }
     const int64_t nwg = gqa_items(&g, chunk, 1);  // + the ring splits
     if (nwg > INT32_MAX / 2) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode_q4: too many work items");
@@ -503,6 +512,7 @@ int mugen_attn_gqa_decode(const mugen_attn_gqa_decode_args* a, void* ws, size_t 
     p.out = a->out;
     p.H = a->n_heads;
     p.G = a->n_heads / a->n_kv_heads;
+    p.hd = a->head_dim;
     p.row_stride = a->n_kv_heads * a->head_dim;
     p.chunk = chunk;
     p.num_splits = splits;
@@ -514,11 +524,11 @@ int mugen_attn_gqa_decode(const mugen_attn_gqa_decode_args* a, void* ws, size_t 
         float* base = align256(ws);
         const size_t slots = (size_t)a->batch * a->n_heads * splits;
         p.ws_o = base;
-        p.ws_ml = base + slots * a->head_dim;
+        p.ws_ml = base + slots * padded_head_dim(a->head_dim);
     }
     const int64_t nwg = gqa_items(a, chunk);
     if (nwg > INT32_MAX) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode: too many work items");
-    hipError_t e = launch_gqa_decode(p, (int)nwg, a->head_dim, a->kv_dtype, a->out_dtype,
+    hipError_t e = launch_gqa_decode(p, (int)nwg, padded_head_dim(a->head_dim), a->kv_dtype, a->out_dtype,
                                      static_cast<hipStream_t>(stream), active_timer());
     return hip_status(e, "gqa_decode launch");
 }
@@ -533,8 +543,9 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: n_heads/n_kv_heads > 16");
     if (a->n_heads / a->n_kv_heads > 8 && a->kernel == MUGEN_ATTN_PREFILL_KERNEL_BLOCK)
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: the per-block kernel serves at most 8 heads per kv head");
-    if (a->head_dim != 64 && a->head_dim != 128)
-        return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: head_dim %d (supported: 64, 128)", a->head_dim);
+    if (a->head_dim < 8 || a->head_dim > 128 || a->head_dim % 8)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: head_dim %d (supported: multiples of 8 up to 128)",
+                    a->head_dim);
     if (!is16(a->dtype) || !is_out(a->out_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: dtype");
     if (a->kernel < 0 || a->kernel > MUGEN_ATTN_PREFILL_KERNEL_WS)
         return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: kernel %d (0 auto, 1 per-block, 2 warp-specialised)", a->kernel);
@@ -555,6 +566,7 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     p.N = a->n_tokens;
     p.H = a->n_heads;
     p.G = a->n_heads / a->n_kv_heads;
+    p.hd = a->head_dim;
     p.row_stride = a->n_kv_heads * a->head_dim;
     p.kv_len = a->kv_len;
     p.start_pos = a->start_pos;
@@ -568,7 +580,7 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     int kernel = (a->n_tokens >= 1024 && a->n_tokens <= 4096) || p.G > 8 ? MUGEN_ATTN_PREFILL_KERNEL_WS
                                                                          : MUGEN_ATTN_PREFILL_KERNEL_BLOCK;
     if (a->kernel == MUGEN_ATTN_PREFILL_KERNEL_BLOCK || a->kernel == MUGEN_ATTN_PREFILL_KERNEL_WS) kernel = a->kernel;
-    hipError_t e = launch_gqa_prefill(p, a->n_kv_heads, a->head_dim, a->dtype, a->out_dtype, kernel,
+    hipError_t e = launch_gqa_prefill(p, a->n_kv_heads, padded_head_dim(a->head_dim), a->dtype, a->out_dtype, kernel,
                                       static_cast<hipStream_t>(stream), active_timer());
     return hip_status(e, "gqa_prefill launch");
 }

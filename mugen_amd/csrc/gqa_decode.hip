@@ -84,7 +84,8 @@ __device__ __forceinline__ int splits_of(const GqaDecodeParams& p, int j) {
 }  // namespace
 
 // two waves per SIMD (the planner sizes the grid for two workgroups per CU)
-template <int D, int DT, int OUT_DT, bool Q4 = false>
+// PAD: head_dim p.hd < D (dims past it masked); otherwise p.hd == D
+template <int D, int DT, int OUT_DT, bool Q4 = false, bool PAD = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gqa_decode_kernel(GqaDecodeParams p) {
     constexpr int KK = D / 32;           // MFMA k-steps of S
     constexpr int DB = D / 16;           // 16-dim blocks of O^T
@@ -133,8 +134,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     const int G = p.G;
     const int h0 = kvh * G;
 
-    const uint16_t* kbase = p.k + (int64_t)b * p.seq_stride + (int64_t)kvh * D;
-    const uint16_t* vbase = p.v + (int64_t)b * p.seq_stride + (int64_t)kvh * D;
+    // head_dim hd below the kernel's D: q's dims >= hd are zero, and the K / V
+    // loads of those dims re-read dims (x mod hd) of the same head and token
+    // (finite cache values: they meet q's zeros in S, and O's columns >= hd
+    // are never stored), so every lane's loads stay uniform and in bounds
+    const int hd = PAD ? p.hd : D;
+    auto dim_alias = [&](int x) {
+        if constexpr (PAD) return x < hd ? x : x % hd;
+        else return x;
+    };
+    const uint16_t* kbase = p.k + (int64_t)b * p.seq_stride + (int64_t)kvh * hd;
+    const uint16_t* vbase = p.v + (int64_t)b * p.seq_stride + (int64_t)kvh * hd;
     // 4-bit store: tokens below nq are 20-byte groups (group kvh*D/32 + c of
     // a token row holds dims 32c .. 32c+31 of this kv head), the rest f16
     // ring rows (token t at slot t % ring, a power of two).  The Q4 rows are
@@ -168,9 +178,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     // splits: q[head n][8*KK*g + 8kk .. +8], the permuted order above)
     u32x4_t qf[KK];
     if (n < G) {
-        const uint16_t* qp = p.q + ((int64_t)b * p.H + h0 + n) * D;
+        const uint16_t* qp = p.q + ((int64_t)b * p.H + h0 + n) * hd;
 #pragma unroll
-        for (int kk = 0; kk < KK; kk++) qf[kk] = load16(qp + (q4_split ? 8 * KK * g + 8 * kk : 32 * kk + 8 * g));
+        for (int kk = 0; kk < KK; kk++) {
+            const int dq = q4_split ? 8 * KK * g + 8 * kk : 32 * kk + 8 * g;  // (4-bit store: hd == D)
+            qf[kk] = (!PAD || dq < hd) ? load16(qp + dq) : u32x4_t{0, 0, 0, 0};
+        }
     } else {
 #pragma unroll
         for (int kk = 0; kk < KK; kk++) qf[kk] = u32x4_t{0, 0, 0, 0};
@@ -178,6 +191,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 
     // block loads: K rows in the permuted order (A operand), V rows coalesced
     const int kr0 = 8 * (n >> 2) + (n & 3);  // + 4nb
+    int kd[KK];  // the lane's K dims per k-step, and its V dim
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++) kd[kk] = dim_alias(32 * kk + 8 * g);
+    const int vd = dim_alias(8 * (lane % (RB / 16)));
     // QB: this split's tokens are Q4 groups (a compile-time kind, so the
     // main loop has no data-dependent branches around its loads and the
     // prefetch's wait counts stay exact)
@@ -215,12 +232,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             for (int nb = 0; nb < 2; nb++) {
                 const int tk = min(t0 + kr0 + 4 * nb, t_end - 1);
 #pragma unroll
-                for (int kk = 0; kk < KK; kk++) kq[nb][kk] = load_f16(kbase, tk, 32 * kk + 8 * g);
+                for (int kk = 0; kk < KK; kk++) kq[nb][kk] = load_f16(kbase, tk, PAD ? kd[kk] : 32 * kk + 8 * g);
             }
 #pragma unroll
             for (int j = 0; j < VL; j++) {
                 const int tv = min(t0 + j * RPL + lane / (RB / 16), t_end - 1);
-                vq[j] = load_f16(vbase, tv, 8 * (lane % (RB / 16)));
+                vq[j] = load_f16(vbase, tv, PAD ? vd : 8 * (lane % (RB / 16)));
             }
         }
     };
@@ -383,7 +400,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         }
         const int64_t bh = (int64_t)b * p.H + h0 + h;
         if (p.num_splits == 1) {
-            store_out<OUT_DT>(p.out, bh * D + d, L > 0.f ? O / L : 0.f);
+            if (!PAD || d < hd) store_out<OUT_DT>(p.out, bh * hd + d, L > 0.f ? O / L : 0.f);
         } else {
             const int64_t slot = bh * p.num_splits + s;
             p.ws_o[slot * D + d] = O;
@@ -404,7 +421,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 //    flight -- one memory round trip, no block barrier;
 //  * more splits: the weights are formed block-wide in LDS (lse_weights),
 //    then the partials are summed 8 splits at a time.
-template <int D, int OUT_DT>
+template <int D, int OUT_DT, bool PAD>
 __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p) {
     constexpr int kPre = 32;
     __shared__ float f_lds[kMaxSplits];
@@ -467,7 +484,8 @@ __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p
         for (; s < nact; s++) acc[0] += f_lds[s] * os[(int64_t)s * D];
     }
     const float O = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
-    store_out<OUT_DT>(p.out, bh * D + d, O * inv);
+    const int hd = PAD ? p.hd : D;
+    if (!PAD || d < hd) store_out<OUT_DT>(p.out, bh * hd + d, O * inv);
     MUGEN_TRACE(9);
 }
 
@@ -476,9 +494,16 @@ __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p
 template <int D, int DT, int OUT_DT, bool Q4 = false>
 static hipError_t launch_gqa_t(const GqaDecodeParams& p, int nwg, hipStream_t st, KernelTimer* timer) {
     const int grid = (Q4 && p.per_xcd > 0) ? 8 * p.per_xcd : nwg;
-    hipError_t e = launch_k(timer, "gqa_decode", gqa_decode_kernel<D, DT, OUT_DT, Q4>, dim3(grid), dim3(256), st, p);
+    hipError_t e = (!Q4 && p.hd != D)
+                       ? launch_k(timer, "gqa_decode", gqa_decode_kernel<D, DT, OUT_DT, false, true>, dim3(grid),
+                                  dim3(256), st, p)
+                       : launch_k(timer, "gqa_decode", gqa_decode_kernel<D, DT, OUT_DT, Q4>, dim3(grid), dim3(256), st, p);
     if (e != hipSuccess || p.num_splits == 1) return e;
-    return launch_k(timer, "gqa_decode_combine", gqa_decode_combine_kernel<D, OUT_DT>, dim3(p.H, p.B), dim3(D), st, p);
+    if (!Q4 && p.hd != D)
+        return launch_k(timer, "gqa_decode_combine", gqa_decode_combine_kernel<D, OUT_DT, true>, dim3(p.H, p.B),
+                        dim3(D), st, p);
+    return launch_k(timer, "gqa_decode_combine", gqa_decode_combine_kernel<D, OUT_DT, false>, dim3(p.H, p.B), dim3(D),
+                    st, p);
 }
 
 template <int D, int DT>

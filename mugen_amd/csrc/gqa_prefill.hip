@@ -54,10 +54,21 @@ __host__ __device__ constexpr int pf_swz(int r) {
         return ((r & 1) * 2) ^ (((r >> 1) & 1) * 4) ^ (((r >> 3) & 1) * 8);
 }
 
+// Logical 16-byte chunk c of a D-wide tile row holds dims 8c .. 8c+7; with
+// head_dim hd < D the chunks at and past hd/8 are loaded from chunk c mod
+// hd/8 of the same head and token instead (finite cache values, in bounds:
+// they meet q's zero dims in S, and O's columns past hd are not stored).
+__device__ __forceinline__ int dim_chunk(int c, int hd) {
+    const int ch = hd >> 3;
+    return c < ch ? c : c % ch;
+}
+
 }  // namespace
 
-template <int D, int MB, int DT, int OUT_DT, int TPB>
+// PAD: head_dim hd < D (dims past it masked); otherwise hd == D
+template <int D, int MB, int DT, int OUT_DT, int TPB, bool PAD>
 __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
+    const int hd = PAD ? p.hd : D;
     constexpr int KK = D / 32;                 // k-steps of S over head_dim
     constexpr int DB = D / 16;                 // 16-wide output column blocks
     constexpr int RB = D * 2;                  // bytes per tile row
@@ -98,10 +109,10 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
         const int slot = 64 * (w + kWaves * k) + lane;
         const int r = slot / CR, pc = slot % CR;
         dma_row[k] = r;
-        dma_col[k] = (uint32_t)((pc ^ pf_swz<D>(r)) * 16);
+        dma_col[k] = (uint32_t)(dim_chunk(pc ^ pf_swz<D>(r), hd) * 16);
     }
-    const uint16_t* kb = p.k + (int64_t)kvh * D;
-    const uint16_t* vb = p.v + (int64_t)kvh * D;
+    const uint16_t* kb = p.k + (int64_t)kvh * hd;
+    const uint16_t* vb = p.v + (int64_t)kvh * hd;
     auto issue = [&](int it) {
         const int kt = it * kKT;
         const uint32_t lds0 = ring_base + (it % NB) * (2 * MAT) + w * 1024;
@@ -125,9 +136,9 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
         const int hg = hs + 4 * mb;
         head_ok[mb] = hg < G;
         const int tok = min(t0 + n, p.N - 1);
-        const uint16_t* qp = p.q + ((int64_t)tok * p.H + kvh * G + (head_ok[mb] ? hg : 0)) * D + 8 * g;
+        const uint16_t* qp = p.q + ((int64_t)tok * p.H + kvh * G + (head_ok[mb] ? hg : 0)) * hd + 8 * g;
 #pragma unroll
-        for (int kk = 0; kk < KK; kk++) qf[mb][kk] = load16(qp + 32 * kk);
+        for (int kk = 0; kk < KK; kk++) qf[mb][kk] = 32 * kk + 8 * g < hd ? load16(qp + 32 * kk) : u32x4_t{0, 0, 0, 0};
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no compiler waits inside the loop
     MUGEN_TRACE(1);
@@ -310,9 +321,10 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
         const float c0 = a0 * inv, c1 = a1 * inv;
         if (tok < p.N) {
             const int h = kvh * G + hs + 4 * mb;
-            const int64_t base = ((int64_t)tok * p.H + h) * D + 4 * g;
+            const int64_t base = ((int64_t)tok * p.H + h) * hd + 4 * g;
 #pragma unroll
             for (int d = 0; d < DB; d++) {
+                if (16 * d + 4 * g >= hd) break;  // padded dims (head_dim < D)
                 const f32x4_t o1 = reinterpret_cast<const f32x4_t*>(xb)[d * 64 + lane];
                 const f32x4_t r = o[mb][d] * c0 + o1 * c1;
                 if constexpr (OUT_DT == DT_F32) {
@@ -349,9 +361,10 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
 //  * one barrier per tile: at barrier j tile j has landed, the S waves have
 //    written P(j-1), and the PV waves have finished tile j-2, whose slot
 //    then receives tile j+2.
-template <int D, int NS, int SMB, int NPV, int DT, int OUT_DT>
+template <int D, int NS, int SMB, int NPV, int DT, int OUT_DT, bool PAD>
 __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(GqaPrefillParams p, int nqb,
                                                                                int nslice, int Hk) {
+    const int hd = PAD ? p.hd : D;
     constexpr int TK = 32;                      // keys per tile
     constexpr int KK = D / 32;                  // k-steps of S over head_dim
     constexpr int DB = D / 16;                  // 16-wide output column blocks
@@ -402,9 +415,10 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             hok[mb] = hs < nh;
             const int tok = min(t0 + n, p.N - 1);
             const uint16_t* qp =
-                p.q + ((int64_t)tok * p.H + kvh * G + NS * slice + (hok[mb] ? hs : 0)) * D + 8 * g;
+                p.q + ((int64_t)tok * p.H + kvh * G + NS * slice + (hok[mb] ? hs : 0)) * hd + 8 * g;
 #pragma unroll
-            for (int kk = 0; kk < KK; kk++) qf[mb][kk] = load16(qp + 32 * kk);
+            for (int kk = 0; kk < KK; kk++)
+                qf[mb][kk] = 32 * kk + 8 * g < hd ? load16(qp + 32 * kk) : u32x4_t{0, 0, 0, 0};
         }
         const int row_lim = p.causal ? min(p.start_pos + t0 + n + 1, p.kv_len) : p.kv_len;
         const int mask_from = p.causal ? min(p.start_pos + t0 + 1, p.kv_len) : p.kv_len;
@@ -500,8 +514,8 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
         __syncthreads();  // E: 1/l published
     } else {
         // ================================================== PV waves
-        const uint16_t* kb = p.k + (int64_t)kvh * D;
-        const uint16_t* vb = p.v + (int64_t)kvh * D;
+        const uint16_t* kb = p.k + (int64_t)kvh * hd;
+        const uint16_t* vb = p.v + (int64_t)kvh * hd;
         const int rs_bytes = p.row_stride * 2;
         // DMA op k of this wave moves K / V chunks [64(wr + NPV k), +64) of the
         // tile: chunk slot s = row s / CR, physical chunk s % CR, holding
@@ -513,7 +527,7 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             const int slot = 64 * (wr + NPV * k) + lane;
             const int r = slot / CR, pc = slot % CR;
             dma_row[k] = r;
-            dma_col[k] = (uint32_t)((pc ^ pf_swz<D>(r)) * 16);
+            dma_col[k] = (uint32_t)(dim_chunk(pc ^ pf_swz<D>(r), hd) * 16);
         }
         auto issue = [&](int it) {
             const int kt = it * TK;
@@ -604,9 +618,10 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             for (int hh = 0; hh < HPW; hh++) {
                 if (hb + hh >= nh) continue;
                 const float inv = linv_x[hb + hh][n];
-                const int64_t base = ((int64_t)tok * p.H + kvh * G + NS * slice + hb + hh) * D + 4 * g;
+                const int64_t base = ((int64_t)tok * p.H + kvh * G + NS * slice + hb + hh) * hd + 4 * g;
 #pragma unroll
                 for (int d = 0; d < DB; d++) {
+                    if (16 * d + 4 * g >= hd) break;  // padded dims (head_dim < D)
                     const f32x4_t r = o[hh][d] * inv;
                     if constexpr (OUT_DT == DT_F32) {
                         *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.out) + base + 16 * d) = r;
@@ -622,42 +637,42 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
 
 // ------------------------------------------------------------------ launch
 
-template <int D, int MB, int DT, int OUT_DT>
+template <int D, bool PAD, int MB, int DT, int OUT_DT>
 static hipError_t launch_pf_t(const GqaPrefillParams& p, int Hk, hipStream_t st, KernelTimer* t) {
     dim3 grid((p.N + 15) / 16, Hk);
     // head_dim 64: two tiles per barrier (Llama-3.2-1B N = 512: 8.7 -> 8.0-8.2
     // us; four per barrier, in an 8-slot ring, measured the same); head_dim
     // 128 keeps one (the second tile's operands would not fit in registers)
     constexpr int TPB = D == 64 ? 2 : 1;
-    return launch_k(t, "gqa_prefill", gqa_prefill_kernel<D, MB, DT, OUT_DT, TPB>, grid, dim3(64 * kWaves), st, p);
+    return launch_k(t, "gqa_prefill", gqa_prefill_kernel<D, MB, DT, OUT_DT, TPB, PAD>, grid, dim3(64 * kWaves), st, p);
 }
 
-template <int D, int MB, int DT>
+template <int D, bool PAD, int MB, int DT>
 static hipError_t launch_pf_o(const GqaPrefillParams& p, int Hk, int out_dt, hipStream_t st, KernelTimer* t) {
-    if (out_dt == DT_F32) return launch_pf_t<D, MB, DT, DT_F32>(p, Hk, st, t);
-    if (out_dt == DT_F16) return launch_pf_t<D, MB, DT, DT_F16>(p, Hk, st, t);
-    return launch_pf_t<D, MB, DT, DT_BF16>(p, Hk, st, t);
+    if (out_dt == DT_F32) return launch_pf_t<D, PAD, MB, DT, DT_F32>(p, Hk, st, t);
+    if (out_dt == DT_F16) return launch_pf_t<D, PAD, MB, DT, DT_F16>(p, Hk, st, t);
+    return launch_pf_t<D, PAD, MB, DT, DT_BF16>(p, Hk, st, t);
 }
 
-template <int D, int MB>
+template <int D, bool PAD, int MB>
 static hipError_t launch_pf_d(const GqaPrefillParams& p, int Hk, int dt, int out_dt, hipStream_t st,
                               KernelTimer* t) {
-    if (dt == DT_F16) return launch_pf_o<D, MB, DT_F16>(p, Hk, out_dt, st, t);
-    return launch_pf_o<D, MB, DT_BF16>(p, Hk, out_dt, st, t);
+    if (dt == DT_F16) return launch_pf_o<D, PAD, MB, DT_F16>(p, Hk, out_dt, st, t);
+    return launch_pf_o<D, PAD, MB, DT_BF16>(p, Hk, out_dt, st, t);
 }
 
-template <int D>
+template <int D, bool PAD>
 static hipError_t launch_pf_g(const GqaPrefillParams& p, int Hk, int dt, int out_dt, hipStream_t st,
                               KernelTimer* t) {
-    if (p.G <= 4) return launch_pf_d<D, 1>(p, Hk, dt, out_dt, st, t);
-    return launch_pf_d<D, 2>(p, Hk, dt, out_dt, st, t);
+    if (p.G <= 4) return launch_pf_d<D, PAD, 1>(p, Hk, dt, out_dt, st, t);
+    return launch_pf_d<D, PAD, 2>(p, Hk, dt, out_dt, st, t);
 }
 
-template <int D, int DT, int OUT_DT>
+template <int D, bool PAD, int DT, int OUT_DT>
 static hipError_t launch_pf_ws_t(const GqaPrefillParams& p, int Hk, hipStream_t st, KernelTimer* t) {
     const int nqb = (p.N + 15) / 16;
     if (p.G <= 4)
-        return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 4, 1, 4, DT, OUT_DT>, dim3(nqb * Hk * ((p.G + 3) / 4)),
+        return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 4, 1, 4, DT, OUT_DT, PAD>, dim3(nqb * Hk * ((p.G + 3) / 4)),
                         dim3(64 * 8), st, p, nqb, (p.G + 3) / 4, Hk);
     const int nslice = (p.G + 7) / 8;
     // 8-head blocks keep 4 PV waves (2 heads each): 8 PV waves (one head
@@ -667,30 +682,35 @@ static hipError_t launch_pf_ws_t(const GqaPrefillParams& p, int Hk, hipStream_t 
     // and softmax phases); two heads per S wave, which halves the K reads
     // per row, measured slower (859 against 804 us at 7B N = 8192)
     constexpr int SMB = 1;
-    return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 8, SMB, NPV, DT, OUT_DT>, dim3(nqb * Hk * nslice),
+    return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 8, SMB, NPV, DT, OUT_DT, PAD>, dim3(nqb * Hk * nslice),
                     dim3(64 * (8 / SMB + NPV)), st, p, nqb, nslice, Hk);
 }
 
-template <int D, int DT>
+template <int D, bool PAD, int DT>
 static hipError_t launch_pf_ws_o(const GqaPrefillParams& p, int Hk, int out_dt, hipStream_t st, KernelTimer* t) {
-    if (out_dt == DT_F32) return launch_pf_ws_t<D, DT, DT_F32>(p, Hk, st, t);
-    if (out_dt == DT_F16) return launch_pf_ws_t<D, DT, DT_F16>(p, Hk, st, t);
-    return launch_pf_ws_t<D, DT, DT_BF16>(p, Hk, st, t);
+    if (out_dt == DT_F32) return launch_pf_ws_t<D, PAD, DT, DT_F32>(p, Hk, st, t);
+    if (out_dt == DT_F16) return launch_pf_ws_t<D, PAD, DT, DT_F16>(p, Hk, st, t);
+    return launch_pf_ws_t<D, PAD, DT, DT_BF16>(p, Hk, st, t);
 }
 
-template <int D>
+template <int D, bool PAD>
 static hipError_t launch_pf_ws(const GqaPrefillParams& p, int Hk, int dt, int out_dt, hipStream_t st,
                                KernelTimer* t) {
-    if (dt == DT_F16) return launch_pf_ws_o<D, DT_F16>(p, Hk, out_dt, st, t);
-    return launch_pf_ws_o<D, DT_BF16>(p, Hk, out_dt, st, t);
+    if (dt == DT_F16) return launch_pf_ws_o<D, PAD, DT_F16>(p, Hk, out_dt, st, t);
+    return launch_pf_ws_o<D, PAD, DT_BF16>(p, Hk, out_dt, st, t);
 }
 
 hipError_t launch_gqa_prefill(const GqaPrefillParams& p, int Hk, int D, int dt, int out_dt, int kernel,
                               hipStream_t st, KernelTimer* t) {
-    if (kernel == 2) return D == 128 ? launch_pf_ws<128>(p, Hk, dt, out_dt, st, t)
-                                      : launch_pf_ws<64>(p, Hk, dt, out_dt, st, t);
-    if (D == 128) return launch_pf_g<128>(p, Hk, dt, out_dt, st, t);
-    return launch_pf_g<64>(p, Hk, dt, out_dt, st, t);
+    const bool pad = p.hd != D;
+    if (kernel == 2) {
+        if (D == 128) return pad ? launch_pf_ws<128, true>(p, Hk, dt, out_dt, st, t)
+                                 : launch_pf_ws<128, false>(p, Hk, dt, out_dt, st, t);
+        return pad ? launch_pf_ws<64, true>(p, Hk, dt, out_dt, st, t) : launch_pf_ws<64, false>(p, Hk, dt, out_dt, st, t);
+    }
+    if (D == 128) return pad ? launch_pf_g<128, true>(p, Hk, dt, out_dt, st, t)
+                             : launch_pf_g<128, false>(p, Hk, dt, out_dt, st, t);
+    return pad ? launch_pf_g<64, true>(p, Hk, dt, out_dt, st, t) : launch_pf_g<64, false>(p, Hk, dt, out_dt, st, t);
 }
 
 }  // namespace mugen_attn

@@ -39,13 +39,13 @@ struct GqaDecodeParams {
     const uint16_t* v;
     const int32_t* seq_lens;
     void* out;
-    float* ws_o;   // [B][H][splits][D]   unnormalised partial outputs
+    float* ws_o;   // [B][H][splits][D]   unnormalised partial outputs (D = padded head_dim)
     float* ws_ml;  // [B][H][splits][2]   (max in log2 units, sum)
     int B;
     int Hk;
     int H;
     int G;           // query heads per kv head
-    int row_stride;  // elements between consecutive tokens (Hk * D)
+    int row_stride;  // elements between consecutive tokens (Hk * hd)
     int chunk;       // tokens per split
     int num_splits;
     int64_t seq_stride;
@@ -61,6 +61,7 @@ struct GqaDecodeParams {
     int ring;
     int per_xcd;            // 4-bit store: work items per XCD (0: blockIdx order)
     int max_T;              // device lengths are clamped to [0, max_T] (the caches' size)
+    int hd;                 // head_dim of the caches, q and out (<= D, a multiple of 8)
 };
 
 // nwg: workgroups of the compact work list (exact, or an upper bound)
@@ -97,11 +98,12 @@ struct GqaPrefillParams {
     int N;
     int H;
     int G;
-    int row_stride;  // Hk * D
+    int row_stride;  // Hk * hd
     int kv_len;
     int start_pos;
     int causal;
     float scale_log2;
+    int hd;          // head_dim of q, the caches and out (<= D, a multiple of 8)
 };
 
 // kernel 1 (MUGEN_ATTN_PREFILL_KERNEL_BLOCK): one (query block, kv head) per

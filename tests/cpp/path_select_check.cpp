@@ -53,6 +53,7 @@ int main() {
     show("moe", moe);
     show("qwen7b_off", qwen7b, GpuAttentionOverride::Off);
     show("small_kv_on", small_kv, GpuAttentionOverride::On);
+    show("tiny_on", tiny, GpuAttentionOverride::On);
     show("v2lite_on", v2lite, GpuAttentionOverride::On);
     show("v2lite_off", v2lite, GpuAttentionOverride::Off);
     return 0;

@@ -45,7 +45,8 @@ def _call_gqa(a, ws=None, nbytes=0):
 @pytest.mark.parametrize("kw,code", [
     (dict(q=0), _capi.E_INVALID),
     (dict(n_heads=30), _capi.E_INVALID),          # not a multiple of n_kv_heads
-    (dict(head_dim=96), _capi.E_UNSUPPORTED),
+    (dict(head_dim=100), _capi.E_UNSUPPORTED),    # not a multiple of 8
+    (dict(head_dim=136), _capi.E_UNSUPPORTED),    # above 128
     (dict(n_heads=68, n_kv_heads=4), _capi.E_UNSUPPORTED),  # G = 17 > 16
     (dict(kv_dtype=_capi.F32), _capi.E_UNSUPPORTED),
     (dict(batch=2, seq_stride=10), _capi.E_INVALID),
@@ -103,7 +104,9 @@ def test_prefill_rejects_bad_args():
     a.n_tokens, a.n_heads, a.n_kv_heads, a.head_dim, a.kv_len, a.start_pos, a.causal = 512, 32, 8, 64, 100, 0, 1
     a.dtype = a.out_dtype = _capi.BF16
     assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.E_INVALID  # kv_len < N
-    a.kv_len, a.head_dim = 512, 80
+    a.kv_len, a.head_dim = 512, 84   # not a multiple of 8
+    assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.E_UNSUPPORTED
+    a.head_dim = 256
     assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.E_UNSUPPORTED
     a.head_dim, a.n_tokens = 64, 0
     assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.OK  # nothing to do
@@ -247,6 +250,8 @@ def test_kv_q4_validation():
     assert L.mugen_attn_gqa_decode_q4(ctypes.byref(d), None, 0, None) == _capi.E_INVALID   # misaligned store
     d.store.q4_k, d.store.ring = 0x1000, 300
     assert L.mugen_attn_gqa_decode_q4(ctypes.byref(d), None, 0, None) == _capi.E_INVALID   # ring not a power of two
+    d.store.ring, d.head_dim = 512, 96
+    assert L.mugen_attn_gqa_decode_q4(ctypes.byref(d), None, 0, None) == _capi.E_UNSUPPORTED  # 4-bit store: 64/128
 
 
 def test_engine_header_compiles(tmp_path):

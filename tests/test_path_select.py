@@ -32,7 +32,8 @@ def choices(tmp_path_factory):
     ("qwen7b", "GqaAttention", True),        # 4 KV heads: GPU
     ("v2lite", "MlaAttention", True),        # MLA: cpu_mla_attention, replaced by the latent kernels
     ("v3", "MlaAttention", True),
-    ("tiny", "GqaAttentionQ4", False),       # 2 KV heads -> the reference's CPU path; d 16 is not served
+    ("tiny", "GqaAttentionQ4", False),       # 2 KV heads -> the reference's CPU path; the 4-bit store needs d 64/128
+    ("tiny_on", "GqaAttention", True),       # the same model forced onto f16 caches: d 16 runs padded to 64
     ("small_kv", "GqaAttentionQ4", True),    # 2 KV heads at d 64: the 4-bit store provider
     ("moe", "GqaAttention", True),           # MoE layers attend like dense ones
     ("qwen7b_off", "GqaAttentionQ4", True),  # set_use_gpu_attention(false)
