@@ -211,7 +211,10 @@ int mugen_attn_gqa_decode_q4(const mugen_attn_gqa_decode_q4_args* args, void* wo
  * n_heads / n_kv_heads in [1, 16] (more
  * than 8 runs on the warp-specialised kernel; forcing the per-block kernel
  * there is refused); dtype F16 or BF16 for q/k/v; out_dtype F16/BF16/F32.
- * No workspace.
+ * With BF16 inputs the kernels may compute P.V in fp16 (V converted on
+ * chip, exact inside the f16 range), so BF16 V values must lie
+ * within +-65504 -- the range of the reference's f16 cache; V magnitudes
+ * below 6.1e-5 keep an absolute precision of 2^-25.  No workspace.
  */
 typedef struct mugen_attn_gqa_prefill_args {
     const void* q;

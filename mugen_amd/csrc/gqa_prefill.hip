@@ -22,9 +22,13 @@
 //    operand straight from registers;
 //  * query blocks are launched longest-first; tiles above the causal
 //    diagonal are never loaded;
-//  * with bf16 inputs P is split into hi + lo bf16 terms (two MFMAs on the
-//    same V operand): a single bf16 P carries 2^-9 relative error per
-//    weight, which short causal rows do not average away.
+//  * with bf16 inputs a single bf16 P would carry 2^-9 relative error per
+//    weight, which short causal rows do not average away.  So P.V runs in
+//    fp16 (P with 11 significant bits): the V tiles are converted from bf16
+//    to fp16 in LDS by the waves that moved them (exact inside the f16
+//    range, the range of the reference's f16 cache).  The per-block kernel
+//    at head_dim 64 (two tiles per barrier) instead splits P into hi + lo
+//    bf16 terms, two MFMAs on the same V operand.
 #include "common.h"
 #include "kernels.h"
 
@@ -75,7 +79,14 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
     constexpr int CR = D / 8;                  // 16-byte chunks per row
     constexpr int MAT = kKT * RB;              // bytes of one K or V tile
     constexpr int DPW = 2 * MAT / 1024 / kWaves;  // 1-KiB DMA ops per wave per tile (K and V)
-    constexpr int NP = p_terms<DT>();
+    // bf16 inputs, one tile per barrier: each wave converts the V chunks it
+    // moved into the ring to fp16 in place (bf16 -> fp16 is exact inside
+    // the f16 range, which the reference's f16 cache has too), so P.V runs
+    // as ONE fp16 MFMA with an fp16 P (11 significant bits) instead of two
+    // bf16 MFMAs on a hi + lo split of P
+    constexpr bool VCVT = DT == DT_BF16 && TPB == 1;
+    constexpr int PDT = VCVT ? DT_F16 : DT;  // operand type of P.V
+    constexpr int NP = p_terms<PDT>();
     static_assert(DPW >= 2 && DPW % 2 == 0, "tile split");
     constexpr int NB = TPB == 1 ? kNBuf : 2 * TPB;  // ring slots
     __shared__ __attribute__((aligned(16))) char ring[NB][2 * MAT];
@@ -122,6 +133,26 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
             dma16s(lds0 + k * kWaves * 1024, kb, off);
             dma16s(lds0 + MAT + k * kWaves * 1024, vb, off);
         }
+    };
+    // fp16 conversion of this wave's V chunks of a tile: the chunks its own
+    // DMA wrote, so the wave waits for its own loads only.  The chunks are
+    // read before a tile's compute and written back after it, so the LDS
+    // latency hides behind the MFMAs
+    auto cv_addr = [&](int it, int k) {
+        return reinterpret_cast<u32x4_t*>(&ring[it % NB][MAT] + (64 * (w + kWaves * k) + lane) * 16);
+    };
+    auto cv_write = [&](int it, const u32x4_t (&x)[DPW / 2]) {
+#pragma unroll
+        for (int k = 0; k < DPW / 2; k++) {
+            u32x4_t y;
+#pragma unroll
+            for (int e = 0; e < 4; e++) y[e] = pack2<DT_F16>(lo_f32<DT_BF16>(x[k][e]), hi_f32<DT_BF16>(x[k][e]));
+            *cv_addr(it, k) = y;
+        }
+    };
+    auto cv_read = [&](int it, u32x4_t (&x)[DPW / 2]) {
+#pragma unroll
+        for (int k = 0; k < DPW / 2; k++) x[k] = *cv_addr(it, k);
     };
     // TPB = 1: three tiles in flight, one barrier per tile.  TPB > 1: TPB
     // tiles per barrier (the later tiles' operands are read during the
@@ -189,10 +220,9 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
     auto compute = [&](int it, const u32x4_t (&af)[2][KK], const u32x4_t (&vf)[DB]) {
         const int kt = it * kKT;
         const bool need_mask = kt + kKT > mask_from;
-#pragma unroll
-        for (int mb = 0; mb < MB; mb++) {
-            if (!head_ok[mb]) continue;
-            f32x4_t sacc[2];
+        // S of one head, raw scores (lane: query row t0+n, keys
+        // kt + 32kh + 8g + 4nb + i)
+        auto s_mfma = [&](int mb, f32x4_t (&sacc)[2]) {
 #pragma unroll
             for (int nb = 0; nb < 2; nb++) {
                 f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -200,7 +230,27 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
                 for (int kk = 0; kk < KK; kk++) acc = mfma16x16x32<DT>(af[nb][kk], qf[mb][kk], acc);
                 sacc[nb] = acc;
             }
-            // lane: query row t0+n, keys kt + 32kh + 8g + 4nb + i (raw scores)
+        };
+        // with the fp16 P.V (VCVT) the S MFMAs of every head go first, so a
+        // head's softmax overlaps the next head's S and the previous head's
+        // P.V in the MFMA pipe (measured 7% faster at 7B N = 8192; with the
+        // bf16 hi + lo P it measured slower, so that order stays per head)
+        f32x4_t s_all[MB][2];
+        if constexpr (VCVT) {
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++)
+                if (head_ok[mb]) s_mfma(mb, s_all[mb]);
+        }
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) {
+            if (!head_ok[mb]) continue;
+            f32x4_t sacc[2];
+            if constexpr (VCVT) {
+                sacc[0] = s_all[mb][0];
+                sacc[1] = s_all[mb][1];
+            } else {
+                s_mfma(mb, sacc);
+            }
             float s[8];
 #pragma unroll
             for (int nb = 0; nb < 2; nb++)
@@ -239,11 +289,11 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
             }
             l_part[mb] += ps;
             u32x4_t pfr[NP];
-            split_p<DT, NP>(x, pfr);
+            split_p<PDT, NP>(x, pfr);
 #pragma unroll
             for (int d = 0; d < DB; d++)
 #pragma unroll
-                for (int pp = 0; pp < NP; pp++) o[mb][d] = mfma16x16x32<DT>(vf[d], pfr[pp], o[mb][d]);
+                for (int pp = 0; pp < NP; pp++) o[mb][d] = mfma16x16x32<PDT>(vf[d], pfr[pp], o[mb][d]);
         }
     };
 
@@ -254,11 +304,33 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
             if (after >= 2) vm_wait<2 * DPW>();
             else if (after == 1) vm_wait<DPW>();
             else vm_wait<0>();
-            lds_barrier();  // tile `it` landed for all waves; tile it-1's buffer is free
+            if constexpr (VCVT) {
+                if (it == 0) {  // the first tile: converted before its barrier
+                    u32x4_t cv[DPW / 2];
+                    cv_read(0, cv);
+                    cv_write(0, cv);
+                }
+            }
+            lds_barrier();  // tile `it` landed (and is converted) for all waves; tile it-1's buffer is free
             if (it + kNBuf - 1 < ntiles) issue(it + kNBuf - 1);
             u32x4_t af[2][KK], vf[DB];
             load_ops(it, af, vf);
+            // tile it+1 is converted around this tile's compute, before
+            // B_{it+1}: this wave's DMA of it is done once at most the tiles
+            // issued after it are outstanding
+            u32x4_t cv[DPW / 2];
+            const int after1 = min(ntiles - 1, it + kNBuf - 1) - (it + 1);
+            if constexpr (VCVT) {
+                if (after1 >= 0) {
+                    if (after1 >= 2) vm_wait<2 * DPW>();
+                    else if (after1 == 1) vm_wait<DPW>();
+                    else vm_wait<0>();
+                    cv_read(it + 1, cv);
+                }
+            }
             compute(it, af, vf);
+            if constexpr (VCVT)
+                if (after1 >= 0) cv_write(it + 1, cv);
         }
     } else {
         for (int it = 0; it < ntiles; it += TPB) {
@@ -374,7 +446,11 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
     constexpr int SLOT = 2 * MAT;
     constexpr int NSLOT = 4;                    // NSLOT - 2 tiles in flight
     constexpr int DPW = 2 * MAT / 1024 / NPV;   // 1-KiB DMA ops per PV wave per tile (K and V)
-    constexpr int NP = p_terms<DT>();
+    // bf16 inputs: P.V in fp16 as in the per-block kernel (the PV waves
+    // convert the V chunks they moved; P goes to LDS as one fp16 term)
+    constexpr bool VCVT = DT == DT_BF16;
+    constexpr int PDT = VCVT ? DT_F16 : DT;
+    constexpr int NP = p_terms<PDT>();
     constexpr int PB = NS * NP * 64 * 16;       // one P buffer: NS heads x NP terms x 64 lanes x 16 B
     static_assert(DPW >= 2 && DPW % 2 == 0 && NS % NPV == 0, "tile split");
     __shared__ __attribute__((aligned(1024))) char ring[NSLOT * SLOT + 2 * PB];
@@ -496,7 +572,7 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
                 }
                 l_part[mb] += ps;
                 u32x4_t pfr[NP];
-                split_p<DT, NP>(x, pfr);
+                split_p<PDT, NP>(x, pfr);
                 char* pb = pbuf + (j & 1) * PB;
 #pragma unroll
                 for (int pp = 0; pp < NP; pp++)
@@ -540,6 +616,23 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             }
         };
         for (int it = 0; it < min(ntiles, NSLOT - 2); it++) issue(it);
+        // fp16 conversion (VCVT) of this wave's V chunks of a tile: read
+        // after the barrier that shows the tile landed, written back after
+        // this interval's P.V, visible to the other PV waves from the next
+        // barrier on (the interval in which they read that tile)
+        auto cv_addr = [&](int it, int k) {
+            return reinterpret_cast<u32x4_t*>(&ring[(it % NSLOT) * SLOT + MAT] + (64 * (wr + NPV * k) + lane) * 16);
+        };
+        u32x4_t cv[DPW / 2];
+        auto cv_write = [&](int it) {
+#pragma unroll
+            for (int k = 0; k < DPW / 2; k++) {
+                u32x4_t y;
+#pragma unroll
+                for (int e = 0; e < 4; e++) y[e] = pack2<DT_F16>(lo_f32<DT_BF16>(cv[k][e]), hi_f32<DT_BF16>(cv[k][e]));
+                *cv_addr(it, k) = y;
+            }
+        };
         // V operand (A, transpose reads): tile row 8g + n/4 (+4), logical
         // bytes 32d + 8(n%4) = chunk 2d + (n%4)/2, half n%2
         const int tr = 8 * g + (n >> 2);
@@ -570,6 +663,16 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             if (j == 8) MUGEN_TRACE(1);
             if (j == 16) MUGEN_TRACE(5);
             if (j + NSLOT - 2 < ntiles) issue(j + NSLOT - 2);  // into the slot of tile j-2
+            if constexpr (VCVT) {
+                if (j < ntiles) {
+#pragma unroll
+                    for (int k = 0; k < DPW / 2; k++) cv[k] = *cv_addr(j, k);
+                }
+                if (j == 0) {
+                    if (ntiles > 0) cv_write(0);
+                    continue;
+                }
+            }
             if (j == 0) continue;
             const int jp = j - 1;
             const char* tile = &ring[(jp % NSLOT) * SLOT];
@@ -607,7 +710,9 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
 #pragma unroll
                 for (int d = 0; d < DB; d++)
 #pragma unroll
-                    for (int hh = 0; hh < HPW; hh++) o[hh][d] = mfma16x16x32<DT>(vf[d], pf[hh][pp], o[hh][d]);
+                    for (int hh = 0; hh < HPW; hh++) o[hh][d] = mfma16x16x32<PDT>(vf[d], pf[hh][pp], o[hh][d]);
+            if constexpr (VCVT)
+                if (j < ntiles) cv_write(j);
             if (j == 8) MUGEN_TRACE(3);
         }
         __syncthreads();  // E: the S waves' 1/l

@@ -101,3 +101,16 @@ def test_more_than_8_heads_per_kv_head(device, N, H, Hk, D, start, dtype):
     with pytest.raises(_capi.MugenAttnError):
         run_gpu(c, device, C.F32, kernel=_capi.PREFILL_KERNEL_BLOCK)
 
+
+
+@pytest.mark.parametrize("v_scale", [1e-3, 300.0])
+def test_bf16_value_range(device, v_scale):
+    # bf16 prompts run P.V in fp16 (V converted in LDS): values far below
+    # and far above 1 (inside the f16 range) keep the tolerance
+    c = C.prefill_case(71, 300, 28, 4, 128, 20, C.BF16)
+    v = c["v"] * v_scale
+    v, vb = C.O.round_to(v, C.BF16)
+    c["v"], c["vb"] = v, vb
+    ref = C.prefill_ref(c)
+    got = run_gpu(c, device, C.F32, kernel=_capi.PREFILL_KERNEL_BLOCK)
+    C.assert_close(got, ref, f"bf16 prefill V x {v_scale}", atol=2e-3 * v_scale)
