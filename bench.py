@@ -221,6 +221,7 @@ class Prefill(Case):
     bound = "mfma"
     unit = "TFLOP/s"
     kernel = "gqa_prefill"
+    extra_kernels = ("gqa_prefill_v16",)  # the fp16 copy of V (long bf16 prompts)
 
     def __init__(self, dev, N, H, Hk, D, seed, name):
         self.name = name
@@ -232,9 +233,10 @@ class Prefill(Case):
         self.profile = ("gqa_prefill", "llama1b_n512" if N == 512 else f"qwen7b_n{N}")
         self.flops = 4.0 * H * D * N * (N + 1) / 2
         self.bytes = (N * H * D * 2) * 2 + N * Hk * D * 2 * 2
+        self.ws = mugen_amd.prefill_workspace(self.q, self.k, self.v, 0)
 
     def step(self):
-        mugen_amd.flash_prefill_attention(self.q, self.k, self.v, 0, out=self.out)
+        mugen_amd.flash_prefill_attention(self.q, self.k, self.v, 0, out=self.out, workspace=self.ws)
 
 
 class MlaFull(Case):

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define MUGEN_ATTN_ABI_VERSION 2
+#define MUGEN_ATTN_ABI_VERSION 3
 
 /* status codes */
 #define MUGEN_ATTN_OK 0
@@ -234,12 +234,25 @@ typedef struct mugen_attn_gqa_prefill_args {
     /* 0 = automatic; MUGEN_ATTN_PREFILL_KERNEL_BLOCK / _WS force one kernel
      * (same results within rounding; for kernel comparisons) */
     int32_t kernel;
+    /* optional workspace (NULL / 0: none).  For BF16 prompts of at least
+     * 1024 tokens, given at least kv_len * n_kv_heads * head_dim * 2 + 256
+     * bytes (mugen_attn_gqa_prefill_workspace_size), the call first copies
+     * V[0, kv_len) to fp16 there (one extra launch), so the attention
+     * kernels need no per-workgroup conversion; same results.  Otherwise
+     * unused. */
+    void* workspace;
+    size_t workspace_bytes;
 } mugen_attn_gqa_prefill_args;
 
 #define MUGEN_ATTN_PREFILL_KERNEL_BLOCK 1 /* one (16-token block, kv head) per workgroup */
 #define MUGEN_ATTN_PREFILL_KERNEL_WS 2    /* warp-specialised S / PV waves */
 
 int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* args, void* stream);
+/* Bytes of the optional prefill workspace worth passing: kv_len * n_kv_heads
+ * * head_dim * 2 + 256 for BF16 prompts of at least 1024 tokens (where the
+ * separate V conversion pays for its launch), else 0 (also for invalid args).
+ * No counterpart in the reference (its cache is f16). */
+size_t mugen_attn_gqa_prefill_workspace_size(const mugen_attn_gqa_prefill_args* args);
 
 /*
  * MLA absorbed attention over the compressed latent cache: decode (q_len 1)

@@ -193,6 +193,11 @@ public:
         d.q = d.out = a->k_[0].ptr;  // placeholders: only the shape matters for the size
         // (a shape the library rejects sizes to 0 here and fails at decode_layer)
         if (auto r = a->ws_.alloc(gqa_decode_workspace_size(d), "GqaAttention workspace"); !r) return r;
+        // BF16 caches: room for the prefill's fp16 copy of one sequence's V
+        // (the library uses it for long prompts)
+        if (s.kv_dtype == MUGEN_ATTN_BF16)
+            if (auto r = a->pf_ws_.alloc((size_t)s.max_seq_len * row * 2 + 256, "GqaAttention prefill workspace"); !r)
+                return r;
         // empty sequences: [0 | 1], so a step before any set_lengths is well defined
         if (auto r = a->set_lengths(std::vector<int32_t>(s.batch, 0), nullptr); !r) return r;
         *out = std::move(a);
@@ -272,6 +277,8 @@ public:
         pf.scale = s_.scale;
         pf.dtype = s_.kv_dtype;
         pf.out_dtype = s_.out_dtype;
+        pf.workspace = pf_ws_.ptr;
+        pf.workspace_bytes = pf_ws_.bytes;
         return gqa_prefill(pf, st);
     }
     // batch-1 form: sequence 0
@@ -346,7 +353,7 @@ private:
 
     GqaShape s_;
     std::vector<detail::DeviceBuffer> k_, v_;
-    detail::DeviceBuffer lens_, ws_;
+    detail::DeviceBuffer lens_, ws_, pf_ws_;
     std::vector<int32_t> host_lens_;
 };
 

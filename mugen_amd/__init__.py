@@ -6,10 +6,10 @@ up-projection and latent-cache writer, as hand-written HIP kernels behind the
 C ABI in include/mugen_attn.h (libmugen_attn.so).
 """
 from . import _capi
-from .attention import (attention_decode, flash_prefill_attention, kv_append, mla_absorb, mla_attention,
+from .attention import (attention_decode, flash_prefill_attention, kv_append, prefill_workspace, mla_absorb, mla_attention,
                         mla_attention_full, mla_latent_write, mla_prepare, mla_project, scatter_kv, seq_advance)
 from .kv_store import KVCacheQ4
 
-__all__ = ["KVCacheQ4", "attention_decode", "flash_prefill_attention", "kv_append", "mla_absorb", "mla_attention",
+__all__ = ["KVCacheQ4", "attention_decode", "flash_prefill_attention", "kv_append", "prefill_workspace", "mla_absorb", "mla_attention",
            "mla_attention_full", "mla_latent_write", "mla_prepare", "mla_project", "scatter_kv", "seq_advance", "_capi"]
 __version__ = "0.1.0"

@@ -28,6 +28,7 @@ EXPORTS = (
     "mugen_attn_gqa_decode_workspace_size",
     "mugen_attn_gqa_decode",
     "mugen_attn_gqa_prefill",
+    "mugen_attn_gqa_prefill_workspace_size",
     "mugen_attn_kv_q4_append",
     "mugen_attn_gqa_decode_q4_workspace_size",
     "mugen_attn_gqa_decode_q4",
@@ -98,6 +99,7 @@ class GqaPrefillArgs(ctypes.Structure):
         ("n_tokens", _i32), ("n_heads", _i32), ("n_kv_heads", _i32), ("head_dim", _i32),
         ("kv_len", _i32), ("start_pos", _i32), ("causal", _i32), ("scale", _f32),
         ("dtype", _i32), ("out_dtype", _i32), ("kernel", _i32),
+        ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -171,6 +173,8 @@ def lib() -> ctypes.CDLL:
         L.mugen_attn_gqa_decode_q4.argtypes = [ctypes.POINTER(GqaDecodeQ4Args), _vp, ctypes.c_size_t, _vp]
         L.mugen_attn_gqa_decode_q4.restype = ctypes.c_int
         L.mugen_attn_gqa_prefill.argtypes = [ctypes.POINTER(GqaPrefillArgs), _vp]
+        L.mugen_attn_gqa_prefill_workspace_size.argtypes = [ctypes.POINTER(GqaPrefillArgs)]
+        L.mugen_attn_gqa_prefill_workspace_size.restype = ctypes.c_size_t
         L.mugen_attn_gqa_prefill.restype = ctypes.c_int
         L.mugen_attn_mla_decode_workspace_size.argtypes = [ctypes.POINTER(MlaDecodeArgs)]
         L.mugen_attn_mla_decode_workspace_size.restype = ctypes.c_size_t

@@ -106,25 +106,49 @@ def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
 
 # ------------------------------------------------------------------ GQA prefill
 
-def flash_prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, start_pos: int = 0, *,
-                            causal: bool = True, out: torch.Tensor | None = None,
-                            out_dtype: torch.dtype | None = None, scale: float = 0.0,
-                            kernel: int = 0) -> torch.Tensor:
-    """Causal GQA prefill.  q [N,H,D]; k/v [kv_len,Hk,D] (cache incl. the new
-    tokens); token i sees keys [0, start_pos+i].  Returns out [N,H,D].
-    kernel: 0 automatic, PREFILL_KERNEL_BLOCK / PREFILL_KERNEL_WS force one."""
-    _need_cuda(q, k, v)
+def _prefill_args(q, k, v, start_pos, causal, out, scale=0.0, kernel=0):
     N, H, D = q.shape
     kv_len, Hk, Dk = k.shape
     if Dk != D or v.shape != k.shape:
         raise ValueError("k/v must be [kv_len, Hk, D] matching q's head_dim")
-    if out is None:
-        out = torch.empty(q.shape, dtype=out_dtype or q.dtype, device=q.device)
     a = _capi.GqaPrefillArgs()
     a.q, a.k, a.v, a.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
     a.n_tokens, a.n_heads, a.n_kv_heads, a.head_dim = N, H, Hk, D
     a.kv_len, a.start_pos, a.causal, a.scale = kv_len, int(start_pos), 1 if causal else 0, float(scale)
     a.dtype, a.out_dtype, a.kernel = _dt(q.dtype), _dt(out.dtype), int(kernel)
+    return a
+
+
+def prefill_workspace(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, start_pos: int = 0, *,
+                      causal: bool = True, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """The optional prefill workspace for this shape
+    (mugen_attn_gqa_prefill_workspace_size bytes; empty when none helps)."""
+    out = torch.empty((0,), dtype=out_dtype or q.dtype, device=q.device)
+    a = _prefill_args(q, k, v, start_pos, causal, out)
+    a.out = q.data_ptr()  # a placeholder: only the shape matters for the size
+    need = _capi.lib().mugen_attn_gqa_prefill_workspace_size(ctypes.byref(a))
+    return torch.empty(need, dtype=torch.uint8, device=q.device)
+
+def flash_prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, start_pos: int = 0, *,
+                            causal: bool = True, out: torch.Tensor | None = None,
+                            out_dtype: torch.dtype | None = None, scale: float = 0.0,
+                            kernel: int = 0, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal GQA prefill.  q [N,H,D]; k/v [kv_len,Hk,D] (cache incl. the new
+    tokens); token i sees keys [0, start_pos+i].  Returns out [N,H,D].
+    kernel: 0 automatic, PREFILL_KERNEL_BLOCK / PREFILL_KERNEL_WS force one.
+    workspace: the optional buffer for the fp16 copy of V (bf16 prompts of
+    1024+ tokens); None allocates one when the library asks for it, an empty
+    tensor passes none."""
+    _need_cuda(q, k, v)
+    if out is None:
+        out = torch.empty(q.shape, dtype=out_dtype or q.dtype, device=q.device)
+    a = _prefill_args(q, k, v, start_pos, causal, out, scale, kernel)
+    if workspace is None:
+        need = _capi.lib().mugen_attn_gqa_prefill_workspace_size(ctypes.byref(a))
+        if need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    if workspace is not None and workspace.numel():
+        a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     _capi.check(_capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), _stream(q.device)))
     return out
 

@@ -338,7 +338,7 @@ extern "C" {
 
 const char* mugen_attn_last_error(void) { return g_last_error.c_str(); }
 
-const char* mugen_attn_version(void) { return "mugen_attn 0.2.0 (gfx950, abi 2)"; }
+const char* mugen_attn_version(void) { return "mugen_attn 0.3.0 (gfx950, abi 3)"; }
 
 // ------------------------------------------------------------------ 4-bit store
 
@@ -533,7 +533,7 @@ int mugen_attn_gqa_decode(const mugen_attn_gqa_decode_args* a, void* ws, size_t 
     return hip_status(e, "gqa_decode launch");
 }
 
-int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
+static int gqa_prefill_validate(const mugen_attn_gqa_prefill_args* a) {
     if (!a) return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: null args");
     if (!a->q || !a->k || !a->v || !a->out) return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: null tensor pointer");
     if (a->n_tokens < 0 || a->n_heads <= 0 || a->n_kv_heads <= 0 || a->kv_len < 0 || a->start_pos < 0)
@@ -558,6 +558,25 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
                     a->start_pos + a->n_tokens, a->kv_len);
     if ((int64_t)a->kv_len * a->n_kv_heads * a->head_dim * 2 > INT32_MAX)
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: K/V cache larger than 2 GiB per tensor");
+    return MUGEN_ATTN_OK;
+}
+
+// the optional fp16 copy of V (BF16 prompts from kPrefillV16MinTokens on:
+// measured where the extra launch pays for itself)
+constexpr int kPrefillV16MinTokens = 1024;
+static size_t gqa_prefill_ws(const mugen_attn_gqa_prefill_args* a) {
+    return (size_t)a->kv_len * a->n_kv_heads * a->head_dim * 2 + 256;
+}
+
+size_t mugen_attn_gqa_prefill_workspace_size(const mugen_attn_gqa_prefill_args* a) {
+    if (gqa_prefill_validate(a) != MUGEN_ATTN_OK) return 0;
+    if (a->dtype != DT_BF16 || a->n_tokens < kPrefillV16MinTokens) return 0;
+    return gqa_prefill_ws(a);
+}
+
+int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
+    if (int rc = gqa_prefill_validate(a)) return rc;
+    if (a->n_tokens == 0) return MUGEN_ATTN_OK;
     GqaPrefillParams p{};
     p.q = static_cast<const uint16_t*>(a->q);
     p.k = static_cast<const uint16_t*>(a->k);
@@ -580,7 +599,19 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     int kernel = (a->n_tokens >= 1024 && a->n_tokens <= 4096) || p.G > 8 ? MUGEN_ATTN_PREFILL_KERNEL_WS
                                                                          : MUGEN_ATTN_PREFILL_KERNEL_BLOCK;
     if (a->kernel == MUGEN_ATTN_PREFILL_KERNEL_BLOCK || a->kernel == MUGEN_ATTN_PREFILL_KERNEL_WS) kernel = a->kernel;
-    hipError_t e = launch_gqa_prefill(p, a->n_kv_heads, padded_head_dim(a->head_dim), a->dtype, a->out_dtype, kernel,
+    int dt = a->dtype;
+    if (a->dtype == DT_BF16 && a->n_tokens >= kPrefillV16MinTokens && a->workspace &&
+        a->workspace_bytes >= gqa_prefill_ws(a)) {
+        // V -> fp16 once for the whole call (the kernels then skip their
+        // per-workgroup conversion)
+        uint16_t* v16 = reinterpret_cast<uint16_t*>(align256(a->workspace));
+        hipError_t e = launch_v_to_f16(p.v, v16, (int64_t)a->kv_len * p.row_stride, static_cast<hipStream_t>(stream),
+                                       active_timer());
+        if (e != hipSuccess) return hip_status(e, "gqa_prefill V conversion launch");
+        p.v = v16;
+        dt = kDtBf16V16;
+    }
+    hipError_t e = launch_gqa_prefill(p, a->n_kv_heads, padded_head_dim(a->head_dim), dt, a->out_dtype, kernel,
                                       static_cast<hipStream_t>(stream), active_timer());
     return hip_status(e, "gqa_prefill launch");
 }

@@ -69,9 +69,11 @@ __device__ __forceinline__ int dim_chunk(int c, int hd) {
 
 }  // namespace
 
-// PAD: head_dim hd < D (dims past it masked); otherwise hd == D
-template <int D, int MB, int DT, int OUT_DT, int TPB, bool PAD>
+// PAD: head_dim hd < D (dims past it masked); otherwise hd == D.
+// DTI: the input type, or kDtBf16V16 (bf16 q / K, V already fp16).
+template <int D, int MB, int DTI, int OUT_DT, int TPB, bool PAD>
 __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
+    constexpr int DT = DTI == kDtBf16V16 ? DT_BF16 : DTI;  // q and K
     const int hd = PAD ? p.hd : D;
     constexpr int KK = D / 32;                 // k-steps of S over head_dim
     constexpr int DB = D / 16;                 // 16-wide output column blocks
@@ -84,8 +86,9 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
     // the f16 range, which the reference's f16 cache has too), so P.V runs
     // as ONE fp16 MFMA with an fp16 P (11 significant bits) instead of two
     // bf16 MFMAs on a hi + lo split of P
-    constexpr bool VCVT = DT == DT_BF16 && TPB == 1;
-    constexpr int PDT = VCVT ? DT_F16 : DT;  // operand type of P.V
+    // bf16 V converted to fp16 before the call (kDtBf16V16) needs neither
+    constexpr bool VCVT = DTI == DT_BF16 && TPB == 1;
+    constexpr int PDT = (VCVT || DTI == kDtBf16V16) ? DT_F16 : DT;  // operand type of P.V
     constexpr int NP = p_terms<PDT>();
     static_assert(DPW >= 2 && DPW % 2 == 0, "tile split");
     constexpr int NB = TPB == 1 ? kNBuf : 2 * TPB;  // ring slots
@@ -231,12 +234,13 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
                 sacc[nb] = acc;
             }
         };
-        // with the fp16 P.V (VCVT) the S MFMAs of every head go first, so a
+        // with the fp16 P.V of bf16 inputs the S MFMAs of every head go first, so a
         // head's softmax overlaps the next head's S and the previous head's
         // P.V in the MFMA pipe (measured 7% faster at 7B N = 8192; with the
         // bf16 hi + lo P it measured slower, so that order stays per head)
+        constexpr bool SFIRST = PDT == DT_F16 && DT == DT_BF16;
         f32x4_t s_all[MB][2];
-        if constexpr (VCVT) {
+        if constexpr (SFIRST) {
 #pragma unroll
             for (int mb = 0; mb < MB; mb++)
                 if (head_ok[mb]) s_mfma(mb, s_all[mb]);
@@ -245,7 +249,7 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
         for (int mb = 0; mb < MB; mb++) {
             if (!head_ok[mb]) continue;
             f32x4_t sacc[2];
-            if constexpr (VCVT) {
+            if constexpr (SFIRST) {
                 sacc[0] = s_all[mb][0];
                 sacc[1] = s_all[mb][1];
             } else {
@@ -433,9 +437,10 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
 //  * one barrier per tile: at barrier j tile j has landed, the S waves have
 //    written P(j-1), and the PV waves have finished tile j-2, whose slot
 //    then receives tile j+2.
-template <int D, int NS, int SMB, int NPV, int DT, int OUT_DT, bool PAD>
+template <int D, int NS, int SMB, int NPV, int DTI, int OUT_DT, bool PAD>
 __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(GqaPrefillParams p, int nqb,
                                                                                int nslice, int Hk) {
+    constexpr int DT = DTI == kDtBf16V16 ? DT_BF16 : DTI;  // q and K
     const int hd = PAD ? p.hd : D;
     constexpr int TK = 32;                      // keys per tile
     constexpr int KK = D / 32;                  // k-steps of S over head_dim
@@ -448,8 +453,8 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
     constexpr int DPW = 2 * MAT / 1024 / NPV;   // 1-KiB DMA ops per PV wave per tile (K and V)
     // bf16 inputs: P.V in fp16 as in the per-block kernel (the PV waves
     // convert the V chunks they moved; P goes to LDS as one fp16 term)
-    constexpr bool VCVT = DT == DT_BF16;
-    constexpr int PDT = VCVT ? DT_F16 : DT;
+    constexpr bool VCVT = DTI == DT_BF16;
+    constexpr int PDT = (VCVT || DTI == kDtBf16V16) ? DT_F16 : DT;
     constexpr int NP = p_terms<PDT>();
     constexpr int PB = NS * NP * 64 * 16;       // one P buffer: NS heads x NP terms x 64 lanes x 16 B
     static_assert(DPW >= 2 && DPW % 2 == 0 && NS % NPV == 0, "tile split");
@@ -740,6 +745,26 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
     }
 }
 
+// bf16 -> fp16 copy of the V rows [0, kv_len) (RNE; exact inside the f16
+// range), 8 values per thread: the optional per-call pre-pass that lets the
+// prefill kernels read V as fp16 (kDtBf16V16)
+__global__ __launch_bounds__(256) void v_to_f16_kernel(const uint16_t* __restrict__ v, uint16_t* __restrict__ dst,
+                                                       int64_t n8) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n8) return;
+    const u32x4_t x = load16(v + 8 * i);
+    u32x4_t y;
+#pragma unroll
+    for (int e = 0; e < 4; e++) y[e] = pack2<DT_F16>(lo_f32<DT_BF16>(x[e]), hi_f32<DT_BF16>(x[e]));
+    *reinterpret_cast<u32x4_t*>(dst + 8 * i) = y;
+}
+
+hipError_t launch_v_to_f16(const uint16_t* v, uint16_t* dst, int64_t n, hipStream_t st, KernelTimer* t) {
+    const int64_t n8 = n / 8;
+    return launch_k(t, "gqa_prefill_v16", v_to_f16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), st, v, dst,
+                    n8);
+}
+
 // ------------------------------------------------------------------ launch
 
 template <int D, bool PAD, int MB, int DT, int OUT_DT>
@@ -763,6 +788,7 @@ template <int D, bool PAD, int MB>
 static hipError_t launch_pf_d(const GqaPrefillParams& p, int Hk, int dt, int out_dt, hipStream_t st,
                               KernelTimer* t) {
     if (dt == DT_F16) return launch_pf_o<D, PAD, MB, DT_F16>(p, Hk, out_dt, st, t);
+    if (dt == kDtBf16V16) return launch_pf_o<D, PAD, MB, kDtBf16V16>(p, Hk, out_dt, st, t);
     return launch_pf_o<D, PAD, MB, DT_BF16>(p, Hk, out_dt, st, t);
 }
 
@@ -802,6 +828,7 @@ template <int D, bool PAD>
 static hipError_t launch_pf_ws(const GqaPrefillParams& p, int Hk, int dt, int out_dt, hipStream_t st,
                                KernelTimer* t) {
     if (dt == DT_F16) return launch_pf_ws_o<D, PAD, DT_F16>(p, Hk, out_dt, st, t);
+    if (dt == kDtBf16V16) return launch_pf_ws_o<D, PAD, kDtBf16V16>(p, Hk, out_dt, st, t);
     return launch_pf_ws_o<D, PAD, DT_BF16>(p, Hk, out_dt, st, t);
 }
 

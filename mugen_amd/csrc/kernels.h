@@ -111,6 +111,10 @@ struct GqaPrefillParams {
 // S / PV waves
 hipError_t launch_gqa_prefill(const GqaPrefillParams& p, int Hk, int D, int dt, int out_dt, int kernel,
                               hipStream_t st, KernelTimer* t);
+// dt code for launch_gqa_prefill: bf16 q / K with V already converted to fp16
+constexpr int kDtBf16V16 = 100;
+// fp16 copy of n bf16 values (n a multiple of 8, 16-byte aligned buffers)
+hipError_t launch_v_to_f16(const uint16_t* v, uint16_t* dst, int64_t n, hipStream_t st, KernelTimer* t);
 
 struct MlaParams {
     const void* q;         // [B][q_len*H][576], f32 or the latent dtype

@@ -282,3 +282,18 @@ def test_kv_append_and_seq_advance_validation():
         assert L.mugen_attn_kv_append(ctypes.byref(b), None) in (_capi.E_INVALID, _capi.E_UNSUPPORTED), field
     assert L.mugen_attn_seq_advance(None, 1, 4, 64, None, None, None) == _capi.E_INVALID
     assert L.mugen_attn_seq_advance(None, 1, 0, 64, None, None, None) == _capi.OK
+
+
+def test_prefill_workspace_size():
+    a = _capi.GqaPrefillArgs()
+    a.q = a.k = a.v = a.out = 0x1000
+    a.n_tokens, a.n_heads, a.n_kv_heads, a.head_dim, a.kv_len, a.start_pos, a.causal = 2048, 28, 4, 128, 2048, 0, 1
+    a.dtype = a.out_dtype = _capi.BF16
+    size = _capi.lib().mugen_attn_gqa_prefill_workspace_size
+    assert size(ctypes.byref(a)) == 2048 * 4 * 128 * 2 + 256     # the fp16 copy of V
+    a.n_tokens, a.start_pos = 1000, 1048                         # a short prompt: no copy
+    assert size(ctypes.byref(a)) == 0
+    a.n_tokens, a.start_pos, a.dtype = 2048, 0, _capi.F16        # f16 inputs need none
+    assert size(ctypes.byref(a)) == 0
+    a.dtype, a.head_dim = _capi.BF16, 84                         # invalid args: 0
+    assert size(ctypes.byref(a)) == 0

@@ -114,3 +114,25 @@ def test_bf16_value_range(device, v_scale):
     ref = C.prefill_ref(c)
     got = run_gpu(c, device, C.F32, kernel=_capi.PREFILL_KERNEL_BLOCK)
     C.assert_close(got, ref, f"bf16 prefill V x {v_scale}", atol=2e-3 * v_scale)
+
+
+@pytest.mark.parametrize("kernel", [_capi.PREFILL_KERNEL_BLOCK, _capi.PREFILL_KERNEL_WS])
+def test_bf16_v_prepass(device, kernel):
+    # a bf16 prompt long enough for the optional fp16 copy of V: the result
+    # with the workspace equals the oracle, and the call without it
+    c = C.prefill_case(72, 2100, 28, 4, 128, 0, C.BF16)
+    q = C.to_dev(c["qb"], C.BF16, device)
+    k = C.to_dev(c["kb"], C.BF16, device)
+    v = C.to_dev(c["vb"], C.BF16, device)
+    ws = mugen_amd.prefill_workspace(q, k, v, 0)
+    assert ws.numel() == 2100 * 4 * 128 * 2 + 256
+    C.say(f"prefill bf16 V pre-pass N=2100 kernel={kernel}")
+    with_ws = mugen_amd.flash_prefill_attention(q, k, v, 0, out_dtype=torch.float32, kernel=kernel, workspace=ws)
+    without = mugen_amd.flash_prefill_attention(q, k, v, 0, out_dtype=torch.float32, kernel=kernel,
+                                                workspace=torch.empty(0, dtype=torch.uint8, device=device))
+    torch.cuda.synchronize()
+    n = 1024  # causal: the first rows depend on the first keys only
+    c1 = C.prefill_case(72, 2100, 28, 4, 128, 0, C.BF16)
+    ref = C.O.gqa_prefill(c1["q"][:n], c1["k"][:n], c1["v"][:n], n, 28, 4, 128, n, 0, nthreads=16)
+    C.assert_close(with_ws.cpu().numpy()[:n], ref, "bf16 prefill with the fp16 V copy")
+    assert torch.allclose(with_ws, without, atol=1e-5, rtol=1e-5)
