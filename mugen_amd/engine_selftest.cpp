@@ -46,6 +46,19 @@ std::vector<uint16_t> f16_rand(Rng& r, size_t n, float a) {
     return v;
 }
 
+// bf16 values (round to nearest even) of uniform draws in [-a, a]
+std::vector<uint16_t> bf16_rand(Rng& r, size_t n, float a) {
+    std::vector<uint16_t> v(n);
+    for (auto& x : v) {
+        const float f = r.uni(a);
+        uint32_t u;
+        std::memcpy(&u, &f, 4);
+        u += 0x7fffu + ((u >> 16) & 1u);
+        x = (uint16_t)(u >> 16);
+    }
+    return v;
+}
+
 int failures = 0;
 
 bool ok(const Status& st, const char* what) {
@@ -75,6 +88,15 @@ struct Dev {
         return h;
     }
 };
+
+bool finite_bf16(const std::vector<uint8_t>& b) {
+    for (size_t i = 0; i + 1 < b.size(); i += 2) {
+        uint16_t x;
+        std::memcpy(&x, &b[i], 2);
+        if ((x & 0x7f80u) == 0x7f80u) return false;
+    }
+    return true;
+}
 
 bool finite_f16(const std::vector<uint8_t>& b) {
     for (size_t i = 0; i + 1 < b.size(); i += 2) {
@@ -425,28 +447,36 @@ void gqa_q4_test(hipStream_t st) {
 // rows [start, start + N) must hold the chunk's K / V, and the output must be
 // the causal prefill over context + chunk computed directly from a buffer
 // assembled on the host; afterwards a decode step continues from start + N.
-void gqa_prefill_test(hipStream_t st) {
+// With BF16 caches and a chunk of 1024+ tokens the provider hands the
+// library its prefill workspace (the one-launch fp16 copy of V), while the
+// direct call passes none (the kernels convert V on chip): both must agree
+// bit for bit.
+void gqa_prefill_test(hipStream_t st, int dtype, int start, int n, int max_seq) {
     mugen_attn::GqaShape s;
     s.n_layers = 1;
     s.batch = 1;
     s.n_heads = 32;
     s.n_kv_heads = 8;
     s.head_dim = 128;
-    s.max_seq_len = 1024;
-    const int start = 200, n = 77;
-    std::printf("gqa prefill provider: H %d Hk %d d %d start %d chunk %d\n", s.n_heads, s.n_kv_heads, s.head_dim,
-                start, n);
+    s.max_seq_len = max_seq;
+    s.kv_dtype = dtype;
+    s.out_dtype = dtype;
+    auto rand16 = [&](Rng& rr, size_t cnt, float a) {
+        return dtype == MUGEN_ATTN_BF16 ? bf16_rand(rr, cnt, a) : f16_rand(rr, cnt, a);
+    };
+    std::printf("gqa prefill provider: %s H %d Hk %d d %d start %d chunk %d\n",
+                dtype == MUGEN_ATTN_BF16 ? "bf16" : "f16", s.n_heads, s.n_kv_heads, s.head_dim, start, n);
     std::fflush(stdout);
     std::unique_ptr<mugen_attn::GqaAttention> a;
     if (!ok(mugen_attn::GqaAttention::create(s, &a), "create")) return;
     const size_t row = (size_t)s.n_kv_heads * s.head_dim, cache = (size_t)s.max_seq_len * row * 2;
     Rng r(3);
-    auto k = f16_rand(r, cache / 2, 1.0f), v = f16_rand(r, cache / 2, 1.0f);
+    auto k = rand16(r, cache / 2, 1.0f), v = rand16(r, cache / 2, 1.0f);
     hip(hipMemcpyAsync(a->k_cache(0), k.data(), cache, hipMemcpyHostToDevice, st), "K init");
     hip(hipMemcpyAsync(a->v_cache(0), v.data(), cache, hipMemcpyHostToDevice, st), "V init");
     ok(a->set_lengths({start}, st), "lengths");
     const size_t qb = (size_t)n * s.n_heads * s.head_dim * 2, kb = (size_t)n * row * 2;
-    auto hq = f16_rand(r, qb / 2, 1.0f), hk = f16_rand(r, kb / 2, 1.0f), hv = f16_rand(r, kb / 2, 1.0f);
+    auto hq = rand16(r, qb / 2, 1.0f), hk = rand16(r, kb / 2, 1.0f), hv = rand16(r, kb / 2, 1.0f);
     Dev q(qb), kn(kb), vn(kb), out(qb), ref(qb), kc((size_t)(start + n) * row * 2), vc((size_t)(start + n) * row * 2);
     q.put(hq.data(), st);
     kn.put(hk.data(), st);
@@ -471,11 +501,11 @@ void gqa_prefill_test(hipStream_t st) {
     pf.kv_len = start + n;
     pf.start_pos = start;
     pf.causal = 1;
-    pf.dtype = MUGEN_ATTN_F16;
-    pf.out_dtype = MUGEN_ATTN_F16;
+    pf.dtype = dtype;
+    pf.out_dtype = dtype;
     ok(mugen_attn::gqa_prefill(pf, st), "direct prefill");
     const auto o = out.get(st), o_ref = ref.get(st);
-    if (o != o_ref || !finite_f16(o)) {
+    if (o != o_ref || !(dtype == MUGEN_ATTN_BF16 ? finite_bf16(o) : finite_f16(o))) {
         std::printf("FAIL gqa prefill: provider output differs from the direct prefill\n");
         failures++;
     }
@@ -716,7 +746,8 @@ int main() {
     gqa_test(st);
     mla_test(st, 1);
     mla_test(st, 3);
-    gqa_prefill_test(st);
+    gqa_prefill_test(st, MUGEN_ATTN_F16, 200, 77, 1024);
+    gqa_prefill_test(st, MUGEN_ATTN_BF16, 100, 1100, 1536);
     gqa_q4_test(st);
     prefill_batch_test(st);
     mla_prefill_test(st);
