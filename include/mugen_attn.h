@@ -239,7 +239,7 @@ typedef struct mugen_attn_gqa_prefill_args {
      * bytes (mugen_attn_gqa_prefill_workspace_size), the call first copies
      * V[0, kv_len) to fp16 there (one extra launch), so the attention
      * kernels need no per-workgroup conversion; same results.  Otherwise
-     * unused. */
+     * unused.  It must not overlap q, k, v or out. */
     void* workspace;
     size_t workspace_bytes;
 } mugen_attn_gqa_prefill_args;
