@@ -231,8 +231,8 @@ typedef struct mugen_attn_gqa_prefill_args {
     float scale;
     int32_t dtype;
     int32_t out_dtype;
-    /* 0 = automatic; MUGEN_ATTN_PREFILL_KERNEL_BLOCK / _WS force one kernel
-     * (same results within rounding; for kernel comparisons) */
+    /* 0 = automatic; MUGEN_ATTN_PREFILL_KERNEL_BLOCK / _WS / _SHORT force
+     * one kernel (same results within rounding; for kernel comparisons) */
     int32_t kernel;
     /* optional workspace (NULL / 0: none).  For BF16 prompts of at least
      * 1024 tokens, given at least kv_len * n_kv_heads * head_dim * 2 + 256
@@ -246,6 +246,9 @@ typedef struct mugen_attn_gqa_prefill_args {
 
 #define MUGEN_ATTN_PREFILL_KERNEL_BLOCK 1 /* one (16-token block, kv head) per workgroup */
 #define MUGEN_ATTN_PREFILL_KERNEL_WS 2    /* warp-specialised S / PV waves */
+#define MUGEN_ATTN_PREFILL_KERNEL_SHORT 3 /* every visible key held on chip: head_dim 64, n_heads / n_kv_heads
+                                           * <= 4, at most 512 keys (start_pos + n_tokens causal, kv_len
+                                           * otherwise); forcing it outside that range is refused */
 
 int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* args, void* stream);
 /* Bytes of the optional prefill workspace worth passing: kv_len * n_kv_heads

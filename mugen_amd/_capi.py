@@ -20,7 +20,7 @@ E_HIP = -4
 F32, F16, BF16 = 0, 1, 2
 W_F16, W_Q4_0, W_Q8_0 = 1, 2, 8  # weight encodings (GGML type ids)
 MLA_KERNEL_ROWS, MLA_KERNEL_WS = 1, 2  # mugen_attn_mla_decode_args.kernel
-PREFILL_KERNEL_BLOCK, PREFILL_KERNEL_WS = 1, 2  # mugen_attn_gqa_prefill_args.kernel
+PREFILL_KERNEL_BLOCK, PREFILL_KERNEL_WS, PREFILL_KERNEL_SHORT = 1, 2, 3  # mugen_attn_gqa_prefill_args.kernel
 MLA_SCRATCH_BYTES = 32 << 20  # MUGEN_ATTN_MLA_SCRATCH_BYTES: the fixed scratch of mugen_attn_mla_decode_noalloc
 
 # every symbol include/mugen_attn.h declares

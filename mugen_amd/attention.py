@@ -135,7 +135,8 @@ def flash_prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, s
                             kernel: int = 0, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Causal GQA prefill.  q [N,H,D]; k/v [kv_len,Hk,D] (cache incl. the new
     tokens); token i sees keys [0, start_pos+i].  Returns out [N,H,D].
-    kernel: 0 automatic, PREFILL_KERNEL_BLOCK / PREFILL_KERNEL_WS force one.
+    kernel: 0 automatic, PREFILL_KERNEL_BLOCK / _WS / _SHORT force one (_SHORT
+    only for head_dim 64, <= 4 heads per kv head and <= 512 visible keys).
     workspace: the optional buffer for the fp16 copy of V (bf16 prompts of
     1024+ tokens); None allocates one when the library asks for it, an empty
     tensor passes none."""

@@ -547,8 +547,9 @@ static int gqa_prefill_validate(const mugen_attn_gqa_prefill_args* a) {
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: head_dim %d (supported: multiples of 8 up to 128)",
                     a->head_dim);
     if (!is16(a->dtype) || !is_out(a->out_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: dtype");
-    if (a->kernel < 0 || a->kernel > MUGEN_ATTN_PREFILL_KERNEL_WS)
-        return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: kernel %d (0 auto, 1 per-block, 2 warp-specialised)", a->kernel);
+    if (a->kernel < 0 || a->kernel > MUGEN_ATTN_PREFILL_KERNEL_SHORT)
+        return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: kernel %d (0 auto, 1 per-block, 2 warp-specialised, 3 short)",
+                    a->kernel);
     if (((uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->v | (uintptr_t)a->out) & 15)
         return fail(MUGEN_ATTN_E_INVALID, "gqa_prefill: q/k/v/out must be 16-byte aligned");
     if (a->n_tokens == 0) return MUGEN_ATTN_OK;
@@ -598,10 +599,20 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     // args->kernel forces one
     int kernel = (a->n_tokens >= 1024 && a->n_tokens <= 4096) || p.G > 8 ? MUGEN_ATTN_PREFILL_KERNEL_WS
                                                                          : MUGEN_ATTN_PREFILL_KERNEL_BLOCK;
-    if (a->kernel == MUGEN_ATTN_PREFILL_KERNEL_BLOCK || a->kernel == MUGEN_ATTN_PREFILL_KERNEL_WS) kernel = a->kernel;
+    // prompts whose whole kv range fits on chip: the short-prompt kernel,
+    // from 256 visible keys on (below that the per-block kernel's shorter
+    // load phase wins: Llama-3.2-1B N = 128 4.6 against 4.9 us; N = 256 5.7
+    // against 5.6, N = 512 8.2 against 7.4)
+    const bool short_fits = gqa_prefill_short_fits(p, padded_head_dim(a->head_dim));
+    const int kv_range = a->causal ? a->start_pos + a->n_tokens : a->kv_len;
+    if (short_fits && kv_range >= 256) kernel = MUGEN_ATTN_PREFILL_KERNEL_SHORT;
+    if (a->kernel == MUGEN_ATTN_PREFILL_KERNEL_SHORT && !short_fits)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED,
+                    "gqa_prefill: the short kernel serves head_dim 64, n_heads/n_kv_heads <= 4 and <= 512 keys");
+    if (a->kernel) kernel = a->kernel;
     int dt = a->dtype;
-    if (a->dtype == DT_BF16 && a->n_tokens >= kPrefillV16MinTokens && a->workspace &&
-        a->workspace_bytes >= gqa_prefill_ws(a)) {
+    if (kernel != MUGEN_ATTN_PREFILL_KERNEL_SHORT && a->dtype == DT_BF16 && a->n_tokens >= kPrefillV16MinTokens &&
+        a->workspace && a->workspace_bytes >= gqa_prefill_ws(a)) {
         // V -> fp16 once for the whole call (the kernels then skip their
         // per-workgroup conversion)
         uint16_t* v16 = reinterpret_cast<uint16_t*>(align256(a->workspace));

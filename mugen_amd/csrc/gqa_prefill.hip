@@ -745,6 +745,265 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
     }
 }
 
+// ------------------------------------------------------------------ short-prompt kernel
+//
+// When every key a query block can see fits in LDS (kv range <= 512 keys at
+// head_dim 64: 64 KiB each of K and V per workgroup), the serial chain of
+// 64-key tiles goes away.  Workgroup = (16-token query block, kv head), 8
+// waves = 4 contiguous key ranges x 2 head pairs of the group (G <= 4):
+//  * all K rows, then all V rows, of the block's range move into LDS by DMA
+//    at once (the two waves of a key range move half each);
+//  * after the K rows land, each wave computes S^T = K . Q^T for its range
+//    and its 2 heads (the operand layouts of the kernels above) and an exact
+//    softmax over the range (all its scores are in registers: one max, no
+//    re-base) while the V rows are still in flight;
+//  * bf16 V rows are converted to fp16 in LDS by the wave whose DMA moved
+//    them (exact inside the f16 range), so O^T += V^T . P^T is one fp16
+//    MFMA with P (11 significant bits) straight from registers;
+//  * merge: each wave stages (max, sum) and its O^T in the K rows' space
+//    (free once every wave has passed the V barrier); after one barrier
+//    every wave sums and stores an eighth of the block's output.
+// The longest block's chain is one range of <= 128 keys instead of eight
+// dependent 64-key tiles.
+constexpr int kShortMaxKeys = 512;  // kv range the short kernel serves (head_dim 64)
+
+template <int DT, int OUT_DT>
+__global__ __launch_bounds__(512) void gqa_prefill_short_kernel(GqaPrefillParams p) {
+    constexpr int D = 64, KK = D / 32, DB = D / 16, RB = D * 2, CR = D / 8;
+    constexpr int MBW = 2;                      // heads (16-row blocks) per wave
+    constexpr int NU = kShortMaxKeys / 4 / 32;  // 32-key units per range, at most
+    constexpr int MAT = NU * 32 * RB;           // 16 KiB: K (or V) rows of one range
+    __shared__ __attribute__((aligned(1024))) char lds[2 * 4 * MAT];  // [K, V][range]
+    __shared__ float2 mlx[8][MBW][16];          // per wave, head, row: (max, sum) of its range
+    __shared__ __attribute__((aligned(16))) char qlds[4 * 16 * RB];  // q rows [head slot][token]
+
+    const int qb = gridDim.x - 1 - blockIdx.x;  // longest rows first
+    const int kvh = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kr = w & 3, rh = w >> 2;          // key range, head pair
+    const int n = lane & 15, g = lane >> 4;
+    const int t0 = qb * 16;
+    const int G = p.G;
+
+    int kend = p.kv_len;  // keys the block's last token sees
+    if (p.causal) kend = min(kend, p.start_pos + min(t0 + 16, p.N));
+    // range kr = keys [kr R, kr R + R), R a multiple of 32 (<= 128)
+    const int R = ((kend + 127) / 128) * 32;
+    const int kb0 = kr * R;
+    const int nu = max(0, min(R, kend - kb0) + 31) / 32;  // units holding keys (wave-uniform)
+    const int row_lim = p.causal ? min(p.start_pos + t0 + n + 1, p.kv_len) : p.kv_len;
+    const int mask_from = p.causal ? min(p.start_pos + t0 + 1, kend) : kend;  // first row's limit
+
+    // ---- q rows by DMA too (so that no compiler-tracked load is waited for
+    // behind the V rows): wave w moves LDS rows [8w, 8w+8) = head slot w/2,
+    // tokens t0 + 8(w%2) + r; tokens past N and head slots past G read a
+    // valid row (never stored)
+    {
+        const int r = lane >> 3, pc = lane & 7;
+        const int hs = w >> 1, tok = min(t0 + 8 * (w & 1) + r, p.N - 1);
+        const uint16_t* qbase = p.q + (int64_t)t0 * p.H * D;  // offsets stay within the block's 16 tokens
+        const uint32_t off = (uint32_t)(((tok - t0) * p.H + kvh * G + (hs < G ? hs : 0)) * D * 2 + pc * 16);
+        dma16s(lds_addr(qlds) + w * 1024, qbase, off);
+    }
+    // ---- K rows, then V rows, of range kr by DMA: op k moves rows [8k, 8k+8)
+    // (64 lanes x 16 B); the range's 4 nu ops per matrix are split between
+    // its two waves (op parity = rh), 2 nu each.  Chunk pc of row r holds
+    // source chunk pc ^ pf_swz(r); rows past kend read row kend - 1 (masked)
+    char* kreg = &lds[kr * MAT];
+    char* vreg = &lds[(4 + kr) * MAT];
+    {
+        const int rs_bytes = p.row_stride * 2;
+        const int r = lane / CR, pc = lane % CR;
+        uint32_t off[NU * 2];
+#pragma unroll
+        for (int k2 = 0; k2 < NU * 2; k2++) {
+            const int k = 2 * k2 + rh;
+            const int key = min(kb0 + 8 * k + r, kend - 1);
+            off[k2] = (uint32_t)key * rs_bytes + (uint32_t)((pc ^ pf_swz<D>(8 * k + r)) * 16);
+        }
+        const uint16_t* ksrc = p.k + (int64_t)kvh * D;
+        const uint16_t* vsrc = p.v + (int64_t)kvh * D;
+#pragma unroll
+        for (int k2 = 0; k2 < NU * 2; k2++)
+            if (k2 < 2 * nu) dma16s(lds_addr(kreg) + (2 * k2 + rh) * 1024, ksrc, off[k2]);
+#pragma unroll
+        for (int k2 = 0; k2 < NU * 2; k2++)
+            if (k2 < 2 * nu) dma16s(lds_addr(vreg) + (2 * k2 + rh) * 1024, vsrc, off[k2]);
+    }
+    // K operand (A): unit row 8(n/4) + n%4 (+4nb), logical chunk g + 4kk
+    const int ar = 8 * (n >> 2) + (n & 3);
+    uint32_t a_off[KK];
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++) a_off[kk] = ar * RB + (((g + 4 * kk) ^ pf_swz<D>(ar)) * 16);
+    // V operand (A of O^T, transpose reads): unit row 8g + n/4 (+4), logical
+    // bytes 32d + 8(n%4) = chunk 2d + (n%4)/2, half n%2
+    const int tr = 8 * g + (n >> 2);
+    uint32_t t_off[DB];
+#pragma unroll
+    for (int d = 0; d < DB; d++) t_off[d] = tr * RB + (((2 * d + ((n & 3) >> 1)) ^ pf_swz<D>(tr)) * 16) + 8 * (n & 1);
+
+    // this wave's q and K rows landed: at most its 2 nu V ops are in flight
+    switch (nu) {
+        case 4: vm_wait<8>(); break;
+        case 3: vm_wait<6>(); break;
+        case 2: vm_wait<4>(); break;
+        case 1: vm_wait<2>(); break;
+        default: vm_wait<0>(); break;
+    }
+    lds_barrier();  // B1: the range's K rows from both of its waves, every wave's q rows
+    // Q^T fragments (B operand) of the wave's heads: lane holds
+    // q[t0+n][head][32kk+8g .. +8]
+    u32x4_t qf[MBW][KK];
+#pragma unroll
+    for (int mb = 0; mb < MBW; mb++)
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++)
+            qf[mb][kk] = *reinterpret_cast<const u32x4_t*>(qlds + ((MBW * rh + mb) * 16 + n) * RB + (4 * kk + g) * 16);
+
+    // ---- S^T, then the exact softmax of the range.  Lane (n, g) holds row
+    // t0+n, keys kb0 + 32u + 8g + j (j < 8) in s[u][mb][j]
+    float s[NU][MBW][8];
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+        if (u >= nu) continue;
+        u32x4_t af[2][KK];
+#pragma unroll
+        for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++)
+                af[nb][kk] = *reinterpret_cast<const u32x4_t*>(kreg + u * 32 * RB + nb * 4 * RB + a_off[kk]);
+#pragma unroll
+        for (int mb = 0; mb < MBW; mb++) {
+#pragma unroll
+            for (int nb = 0; nb < 2; nb++) {
+                f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < KK; kk++) acc = mfma16x16x32<DT>(af[nb][kk], qf[mb][kk], acc);
+#pragma unroll
+                for (int i = 0; i < 4; i++) s[u][mb][4 * nb + i] = acc[i];  // raw score (scale > 0)
+            }
+            const int key0 = kb0 + 32 * u + 8 * g;
+            if (kb0 + 32 * u + 32 > mask_from) {  // wave-uniform: units below the diagonal carry no mask
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    if (key0 + j >= row_lim || key0 + j >= kend) s[u][mb][j] = kNegInf;
+            }
+        }
+    }
+    float m[MBW], l[MBW];
+    u32x4_t pf[NU][MBW];  // fp16 weights, the B operand of O^T = V^T . P^T
+#pragma unroll
+    for (int mb = 0; mb < MBW; mb++) {
+        float mx = kNegInf;
+#pragma unroll
+        for (int u = 0; u < NU; u++)
+            if (u < nu)
+#pragma unroll
+                for (int j = 0; j < 8; j++) mx = fmaxf(mx, s[u][mb][j]);
+        mx = max_x32(max_x16(mx));
+        m[mb] = mx * p.scale_log2;  // the range's max in log2 units
+        const float nm = mx == kNegInf ? 0.f : -m[mb];
+        float ls = 0.f;
+#pragma unroll
+        for (int u = 0; u < NU; u++) {
+            if (u >= nu) continue;
+            float x[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                x[j] = fast_exp2(fmaf(s[u][mb][j], p.scale_log2, nm));
+                ls += x[j];
+            }
+            split_p<DT_F16, 1>(x, &pf[u][mb]);
+        }
+        l[mb] = ls;
+    }
+
+    // ---- V rows: bf16 -> fp16 by the wave whose DMA moved them
+    vm_wait<0>();
+    if constexpr (DT == DT_BF16) {
+        // all reads first, so their LDS latencies overlap
+        u32x4_t x[NU * 2];
+#pragma unroll
+        for (int k2 = 0; k2 < NU * 2; k2++)
+            if (k2 < 2 * nu) x[k2] = *reinterpret_cast<const u32x4_t*>(vreg + (2 * k2 + rh) * 1024 + lane * 16);
+#pragma unroll
+        for (int k2 = 0; k2 < NU * 2; k2++) {
+            if (k2 < 2 * nu) {
+                u32x4_t y;
+#pragma unroll
+                for (int e = 0; e < 4; e++) y[e] = pack2<DT_F16>(lo_f32<DT_BF16>(x[k2][e]), hi_f32<DT_BF16>(x[k2][e]));
+                *reinterpret_cast<u32x4_t*>(vreg + (2 * k2 + rh) * 1024 + lane * 16) = y;
+            }
+        }
+    }
+    lds_barrier();  // B2: the range's V rows (fp16) from both waves; every wave is done with K
+
+    f32x4_t o[MBW][DB];
+#pragma unroll
+    for (int mb = 0; mb < MBW; mb++)
+#pragma unroll
+        for (int d = 0; d < DB; d++) o[mb][d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+        if (u >= nu) continue;
+        u32x4_t vf[DB];
+#pragma unroll
+        for (int d = 0; d < DB; d++) {
+            const char* tp = vreg + u * 32 * RB + t_off[d];
+            const u32x2_t lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(tp));
+            const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(tp + 4 * RB));
+            vf[d] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+        }
+#pragma unroll
+        for (int mb = 0; mb < MBW; mb++)
+#pragma unroll
+            for (int d = 0; d < DB; d++) o[mb][d] = mfma16x16x32<DT_F16>(vf[d], pf[u][mb], o[mb][d]);
+    }
+
+    // ---- merge the 4 key ranges of each head pair: (max, sum) and the
+    // unscaled O^T go to LDS (O^T into the K rows' space), one barrier
+    f32x4_t* stage = reinterpret_cast<f32x4_t*>(&lds[0]);  // [wave][mb][d][lane]: 64 KiB, the K rows
+#pragma unroll
+    for (int mb = 0; mb < MBW; mb++) {
+        l[mb] = sum_x32(sum_x16(l[mb]));
+        if (g == 0) mlx[w][mb][n] = make_float2(m[mb], l[mb]);
+#pragma unroll
+        for (int d = 0; d < DB; d++) stage[((w * MBW + mb) * DB + d) * 64 + lane] = o[mb][d];
+    }
+    __syncthreads();
+    // wave (kr, rh) sums and stores fragments 2kr, 2kr+1 of its head pair's
+    // MBW * DB = 8 (head, column block) fragments; both are of head mb = kr / 2
+    const int mb = kr >> 1;
+    const int tok = t0 + n;
+    if (MBW * rh + mb >= G || tok >= p.N) return;
+    float a[4], M = kNegInf, L = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) M = fmaxf(M, mlx[4 * rh + r][mb][n].x);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const float2 v = mlx[4 * rh + r][mb][n];
+        a[r] = v.x == kNegInf ? 0.f : fast_exp2(v.x - M);
+        L += a[r] * v.y;
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const int h = kvh * G + MBW * rh + mb;
+#pragma unroll
+    for (int f2 = 0; f2 < 2; f2++) {
+        const int f = 2 * kr + f2, d = f % DB;
+        f32x4_t r = stage[((4 * rh) * MBW * DB + f) * 64 + lane] * (a[0] * inv);
+#pragma unroll
+        for (int q = 1; q < 4; q++) r += stage[((4 * rh + q) * MBW * DB + f) * 64 + lane] * (a[q] * inv);
+        const int64_t base = ((int64_t)tok * p.H + h) * D + 16 * d + 4 * g;
+        if constexpr (OUT_DT == DT_F32) {
+            *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.out) + base) = r;
+        } else {
+            *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.out) + base) =
+                u32x2_t{pack2<OUT_DT>(r[0], r[1]), pack2<OUT_DT>(r[2], r[3])};
+        }
+    }
+}
+
 // bf16 -> fp16 copy of the V rows [0, kv_len) (RNE; exact inside the f16
 // range), 8 values per thread: the optional per-call pre-pass that lets the
 // prefill kernels read V as fp16 (kDtBf16V16)
@@ -832,9 +1091,26 @@ static hipError_t launch_pf_ws(const GqaPrefillParams& p, int Hk, int dt, int ou
     return launch_pf_ws_o<D, PAD, DT_BF16>(p, Hk, out_dt, st, t);
 }
 
+template <int DT>
+static hipError_t launch_pf_short(const GqaPrefillParams& p, int Hk, int out_dt, hipStream_t st, KernelTimer* t) {
+    dim3 grid((p.N + 15) / 16, Hk);
+    if (out_dt == DT_F32) return launch_k(t, "gqa_prefill", gqa_prefill_short_kernel<DT, DT_F32>, grid, dim3(512), st, p);
+    if (out_dt == DT_F16) return launch_k(t, "gqa_prefill", gqa_prefill_short_kernel<DT, DT_F16>, grid, dim3(512), st, p);
+    return launch_k(t, "gqa_prefill", gqa_prefill_short_kernel<DT, DT_BF16>, grid, dim3(512), st, p);
+}
+
+bool gqa_prefill_short_fits(const GqaPrefillParams& p, int D) {
+    const int kend = p.causal ? p.start_pos + p.N : p.kv_len;
+    return D == 64 && p.hd == 64 && p.G <= 4 && kend <= kShortMaxKeys;
+}
+
 hipError_t launch_gqa_prefill(const GqaPrefillParams& p, int Hk, int D, int dt, int out_dt, int kernel,
                               hipStream_t st, KernelTimer* t) {
     const bool pad = p.hd != D;
+    if (kernel == 3) {
+        if (!gqa_prefill_short_fits(p, D) || dt == kDtBf16V16) return hipErrorInvalidValue;
+        return dt == DT_F16 ? launch_pf_short<DT_F16>(p, Hk, out_dt, st, t) : launch_pf_short<DT_BF16>(p, Hk, out_dt, st, t);
+    }
     if (kernel == 2) {
         if (D == 128) return pad ? launch_pf_ws<128, true>(p, Hk, dt, out_dt, st, t)
                                  : launch_pf_ws<128, false>(p, Hk, dt, out_dt, st, t);

@@ -111,6 +111,10 @@ struct GqaPrefillParams {
 // S / PV waves
 hipError_t launch_gqa_prefill(const GqaPrefillParams& p, int Hk, int D, int dt, int out_dt, int kernel,
                               hipStream_t st, KernelTimer* t);
+// kernel 3 (MUGEN_ATTN_PREFILL_KERNEL_SHORT): every key a query block sees
+// held in LDS; serves head_dim 64 (unpadded), at most 4 heads per kv head
+// and a kv range (start_pos + N causal, kv_len otherwise) of at most 512
+bool gqa_prefill_short_fits(const GqaPrefillParams& p, int D);
 // dt code for launch_gqa_prefill: bf16 q / K with V already converted to fp16
 constexpr int kDtBf16V16 = 100;
 // fp16 copy of n bf16 values (n a multiple of 8, 16-byte aligned buffers)

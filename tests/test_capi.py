@@ -116,6 +116,27 @@ def test_prefill_rejects_bad_args():
     assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.E_UNSUPPORTED
     a.kernel = 0
     assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.OK
+    a.kernel = 4
+    assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.E_INVALID
+
+
+@pytest.mark.parametrize("n_tokens,start,kv_len,causal,H,Hk,hd", [
+    (512, 1, 513, 1, 32, 8, 64),   # 513 visible keys
+    (100, 0, 513, 0, 32, 8, 64),   # non-causal: all of kv_len is visible
+    (64, 0, 64, 1, 32, 4, 64),     # 8 heads per kv head
+    (64, 0, 64, 1, 32, 8, 128),    # head_dim 128
+    (64, 0, 64, 1, 32, 8, 56),     # padded head_dim
+])
+def test_prefill_short_kernel_refused_outside_its_range(n_tokens, start, kv_len, causal, H, Hk, hd):
+    # forcing the short kernel where it does not apply is refused before any
+    # launch (the pointers are placeholders)
+    a = _capi.GqaPrefillArgs()
+    a.q = a.k = a.v = a.out = 0x1000
+    a.n_tokens, a.n_heads, a.n_kv_heads, a.head_dim = n_tokens, H, Hk, hd
+    a.kv_len, a.start_pos, a.causal = kv_len, start, causal
+    a.dtype = a.out_dtype = _capi.BF16
+    a.kernel = _capi.PREFILL_KERNEL_SHORT
+    assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.E_UNSUPPORTED
 
 
 def test_scatter_kv_validation():

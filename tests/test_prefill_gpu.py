@@ -136,3 +136,33 @@ def test_bf16_v_prepass(device, kernel):
     ref = C.O.gqa_prefill(c1["q"][:n], c1["k"][:n], c1["v"][:n], n, 28, 4, 128, n, 0, nthreads=16)
     C.assert_close(with_ws.cpu().numpy()[:n], ref, "bf16 prefill with the fp16 V copy")
     assert torch.allclose(with_ws, without, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("N,H,Hk,start,dtype,causal", [
+    (512, 32, 8, 0, C.BF16, True),    # configs[2], the largest causal range
+    (300, 32, 8, 212, C.F16, True),   # a continued prompt ending at key 512
+    (1, 8, 2, 0, C.BF16, True), (17, 8, 2, 3, C.F16, True), (77, 12, 3, 0, C.BF16, True),
+    (130, 16, 8, 40, C.BF16, True), (33, 4, 4, 0, C.F16, True), (45, 8, 8, 450, C.BF16, True),
+    (200, 32, 8, 312, C.BF16, False),  # non-causal: every row sees all 512 keys
+])
+def test_short_kernel(device, N, H, Hk, start, dtype, causal):
+    # the short-prompt kernel (whole kv range on chip, 4 key ranges merged),
+    # G = 1..4, ranges that leave key ranges empty, all output types
+    c = C.prefill_case(90 + N + start, N, H, Hk, 64, start, dtype)
+    if not causal:
+        from oracle import oracle as O
+        kv = c["kv_len"]
+        ref = O.gqa_attention(c["q"], c["k"].reshape(1, kv, Hk, 64).repeat(N, 0),
+                              c["v"].reshape(1, kv, Hk, 64).repeat(N, 0), [kv] * N, H, Hk, 64, kv * Hk * 64)
+    else:
+        ref = C.prefill_ref(c, nthreads=8)
+    for odt in (C.F32, C.F16, C.BF16):
+        C.assert_close(run_gpu(c, device, odt, causal=causal, kernel=_capi.PREFILL_KERNEL_SHORT), ref,
+                       f"short kernel N={N} H={H} Hk={Hk} start={start} out={odt}")
+
+
+def test_short_kernel_is_the_default_where_it_fits(device):
+    # the automatic choice for a Llama-3.2-1B prompt of >= 256 visible keys
+    # equals the forced short kernel bit for bit
+    c = C.prefill_case(93, 250, 32, 8, 64, 10, C.BF16)
+    assert np.array_equal(run_gpu(c, device, C.F32), run_gpu(c, device, C.F32, kernel=_capi.PREFILL_KERNEL_SHORT))
