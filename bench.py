@@ -63,13 +63,19 @@ class MlaDecode(Case):
     bound = "hbm"
     kernel = "mla_decode"
 
-    def __init__(self, dev, B, H, q_len, lens, max_T, q_dtype, lat_dtype, seed, name, fallback_rows=0):
+    def __init__(self, dev, B, H, q_len, lens, max_T, q_dtype, lat_dtype, seed, name, fallback_rows=0, layers=1):
         self.name = name
         g = torch.Generator(device=dev).manual_seed(seed)
         self.B, self.H, self.q_len = B, H, q_len
         self.lens = np.asarray(lens, np.int32)
         self.q = randn((B, q_len, H, 576), 1.0, q_dtype, g, dev)
         self.lat = randn((B, max_T, 576), 0.5, lat_dtype, g, dev)
+        # layers > 1: consecutive steps read the latent caches of `layers`
+        # different layers in turn, as a model's decode step does, so that
+        # a cache is not still resident in the last-level cache (256 MB)
+        # when its layer comes round again
+        self.lats = [self.lat] + [randn((B, max_T, 576), 0.5, lat_dtype, g, dev) for _ in range(layers - 1)]
+        self.layer = 0
         if fallback_rows:
             # the exact-fallback cost: every 64-token block of each sequence
             # carries a spike token (latent dim 0 = 1000, its other dims 0)
@@ -99,7 +105,9 @@ class MlaDecode(Case):
             self.bound, self.unit = "mfma", "TFLOP/s"
 
     def step(self):
-        mugen_amd.mla_attention(self.q, self.lat, self.sl, self.max_T, scale=MLA_SCALE, out=self.out,
+        lat = self.lats[self.layer]
+        self.layer = (self.layer + 1) % len(self.lats)
+        mugen_amd.mla_attention(self.q, lat, self.sl, self.max_T, scale=MLA_SCALE, out=self.out,
                                 workspace=self.ws, seq_lens_host=self.lens)
 
     def cpu_sample(self, seconds_target=10.0):
@@ -483,6 +491,10 @@ def main():
                       "mla_decode_v3_fallback_1pct", fallback_rows=1),
             MlaDecode(dev, 8, 128, 1, seeded_lens(45, 8, 1024, 8192), 8192, torch.bfloat16, torch.bfloat16, 45,
                       "mla_decode_v3_fallback_10pct", fallback_rows=13),
+            # the headline step over 5 layers' caches in turn (277 MB read per
+            # 5 steps, more than the 256 MB last-level cache holds)
+            MlaDecode(dev, 8, 128, 1, seeded_lens(45, 8, 1024, 8192), 8192, torch.bfloat16, torch.bfloat16, 45,
+                      "mla_decode_v3_5layers", layers=5),
         ]
     if args.only:
         cases = [c for c in cases if c.name == args.only]
