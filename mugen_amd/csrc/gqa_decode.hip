@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     // per-wave V staging (32 rows), reused after the loop for the wave merge
     constexpr int STAGE = 4 * 32 * RB;
     constexpr int OROW = D + 4;  // merge rows padded: lanes n of one write land on distinct banks
-    constexpr int MERGE = 4 * 16 * OROW * 4 + 2 * 4 * 16 * 4;
+    constexpr int MERGE = 4 * 16 * OROW * 4 + 2 * 4 * 16 * 4 + 4 * 16 * 4 + 2 * 16 * 4;
     __shared__ __attribute__((aligned(16))) char lds[STAGE > MERGE ? STAGE : MERGE];
 
     // compact work list: item r of sequence b is split r / Hk of kv head r % Hk
@@ -384,29 +384,44 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         m_lds[w * 16 + n] = m_run;
         l_lds[w * 16 + n] = l_part;
     }
+    // per head: the 4 waves' factors 2^(m_w - M) (divided by the sum when
+    // this is the only split), once, then every output element is a 4-term sum
+    float* f_lds = l_lds + 4 * 16;    // [4][16]
+    float* ml_out = f_lds + 4 * 16;   // [16][2]: the head's (M, L)
     __syncthreads();
-    for (int idx = threadIdx.x; idx < G * D; idx += 256) {
-        const int h = idx / D, d = idx - h * D;
+    if (threadIdx.x < 16) {
+        const int h = threadIdx.x;
         float M = kNegInf;
 #pragma unroll
         for (int ww = 0; ww < 4; ww++) M = fmaxf(M, m_lds[ww * 16 + h]);
-        float L = 0.f, O = 0.f;
+        float f[4], L = 0.f;
 #pragma unroll
         for (int ww = 0; ww < 4; ww++) {
             const float mw = m_lds[ww * 16 + h];
-            const float f = (mw == kNegInf) ? 0.f : fast_exp2(mw - M);
-            L += f * l_lds[ww * 16 + h];
-            O += f * o_lds[(ww * 16 + h) * OROW + d];
+            f[ww] = (mw == kNegInf) ? 0.f : fast_exp2(mw - M);
+            L += f[ww] * l_lds[ww * 16 + h];
         }
+        const float c = p.num_splits == 1 ? (L > 0.f ? 1.f / L : 0.f) : 1.f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) f_lds[ww * 16 + h] = f[ww] * c;
+        ml_out[2 * h] = M;
+        ml_out[2 * h + 1] = L;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * D; idx += 256) {
+        const int h = idx / D, d = idx - h * D;
+        float O = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) O += f_lds[ww * 16 + h] * o_lds[(ww * 16 + h) * OROW + d];
         const int64_t bh = (int64_t)b * p.H + h0 + h;
         if (p.num_splits == 1) {
-            if (!PAD || d < hd) store_out<OUT_DT>(p.out, bh * hd + d, L > 0.f ? O / L : 0.f);
+            if (!PAD || d < hd) store_out<OUT_DT>(p.out, bh * hd + d, O);
         } else {
             const int64_t slot = bh * p.num_splits + s;
             p.ws_o[slot * D + d] = O;
             if (d == 0) {
-                p.ws_ml[slot * 2 + 0] = M;
-                p.ws_ml[slot * 2 + 1] = L;
+                p.ws_ml[slot * 2 + 0] = ml_out[2 * h];
+                p.ws_ml[slot * 2 + 1] = ml_out[2 * h + 1];
             }
         }
     }
