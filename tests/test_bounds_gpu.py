@@ -93,6 +93,22 @@ def test_gqa_prefill_guarded(device):
         C.assert_close(out.t.float().cpu().numpy(), ref, f"guarded prefill kernel {kernel}")
 
 
+@pytest.mark.parametrize("N,start", [(77, 30), (300, 212)])
+def test_gqa_prefill_short_guarded(device, N, start):
+    # the short-prompt kernel (head_dim 64, G = 4) with a last query block of
+    # fewer than 16 tokens and a kv range ending at 512 keys
+    c = C.prefill_case(505 + N, N, 32, 8, 64, start, C.BF16)
+    C.say(f"guarded gqa_prefill short N={N} start={start}")
+    q = C.to_dev(c["qb"], C.BF16, device)
+    k = C.to_dev(c["kb"], C.BF16, device)
+    v = C.to_dev(c["vb"], C.BF16, device)
+    ref = C.prefill_ref(c)
+    out = Guarded((N, 32, 64), torch.bfloat16, device)
+    mugen_amd.flash_prefill_attention(q, k, v, start, out=out.t, kernel=_capi.PREFILL_KERNEL_SHORT)
+    assert out.intact(), "guard band overwritten (short kernel)"
+    C.assert_close(out.t.float().cpu().numpy(), ref, f"guarded short prefill N={N}")
+
+
 def test_kv_append_guarded(device):
     # rows at positions >= max_seq_len are dropped, negative lengths too
     B, max_T, row = 3, 64, 512
