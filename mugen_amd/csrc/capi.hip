@@ -600,12 +600,12 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     int kernel = (a->n_tokens >= 1024 && a->n_tokens <= 4096) || p.G > 8 ? MUGEN_ATTN_PREFILL_KERNEL_WS
                                                                          : MUGEN_ATTN_PREFILL_KERNEL_BLOCK;
     // prompts whose whole kv range fits on chip: the short-prompt kernel,
-    // from 256 visible keys on (below that the per-block kernel's shorter
-    // load phase wins: Llama-3.2-1B N = 128 4.6 against 4.9 us; N = 256 5.7
-    // against 5.6, N = 512 8.2 against 7.4)
+    // from 384 visible keys on (below that the per-block kernel's shorter
+    // load phase wins: Llama-3.2-1B N = 128 4.4 against 4.9 us; N = 256 5.55
+    // against 5.6, N = 512 7.9 against 7.5)
     const bool short_fits = gqa_prefill_short_fits(p, padded_head_dim(a->head_dim));
     const int kv_range = a->causal ? a->start_pos + a->n_tokens : a->kv_len;
-    if (short_fits && kv_range >= 256) kernel = MUGEN_ATTN_PREFILL_KERNEL_SHORT;
+    if (short_fits && kv_range >= 384) kernel = MUGEN_ATTN_PREFILL_KERNEL_SHORT;
     if (a->kernel == MUGEN_ATTN_PREFILL_KERNEL_SHORT && !short_fits)
         return fail(MUGEN_ATTN_E_UNSUPPORTED,
                     "gqa_prefill: the short kernel serves head_dim 64, n_heads/n_kv_heads <= 4 and <= 512 keys");

@@ -202,7 +202,11 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
         for (int d = 0; d < DB; d++) o[mb][d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
     // lazy max: weights may grow to 2^kHeadroom before the row is re-based
+    // (the block's first tile); later tiles re-base when a lane's 8 weights
+    // sum past kClampW = 2^15 (each weight then stays within the 16-bit P
+    // range, fp16 max 65504)
     constexpr float kHeadroom = 8.f;
+    constexpr float kClampW = 32768.f;
 
     // operands of one tile: K fragments (A, shared by the MB heads) and the
     // V transpose fragments
@@ -245,6 +249,14 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
             for (int mb = 0; mb < MB; mb++)
                 if (head_ok[mb]) s_mfma(mb, s_all[mb]);
         }
+        // The block's first tile sets each row's reference max (re-base
+        // test on the tile's max).  Later tiles test the sums instead: the
+        // weights 2^(s - m_run) are formed first, and only when a lane's sum
+        // of its 8 weights passes 2^kClamp -- every weight is >= 0, so any
+        // weight past 2^kClamp (also an infinite one) shows -- is the row
+        // re-based and its weights formed again (rare).  That takes one
+        // compare per head and tile instead of a max over the 8 scores.
+        const bool first = it == 0;
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) {
             if (!head_ok[mb]) continue;
@@ -266,30 +278,53 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
                 for (int j = 0; j < 8; j++)
                     if (key0 + j >= row_lim) s[j] = kNegInf;
             }
-            float smax = s[0];
+            if (first) {
+                float smax = s[0];
 #pragma unroll
-            for (int j = 1; j < 8; j++) smax = fmaxf(smax, s[j]);
-            // re-base the row only when a weight would exceed 2^kHeadroom
-            if (__any(smax * p.scale_log2 > m_run[mb] + kHeadroom)) {
-                float mt = smax * p.scale_log2;
-                mt = max_x32(max_x16(mt));
-                const float m_new = fmaxf(m_run[mb], mt);
-                if (m_new > m_run[mb]) {
-                    const float alpha = fast_exp2(m_run[mb] - m_new);  // 0 when m_run = -inf
-                    l_part[mb] *= alpha;
+                for (int j = 1; j < 8; j++) smax = fmaxf(smax, s[j]);
+                // re-base the row only when a weight would exceed 2^kHeadroom
+                if (__any(smax * p.scale_log2 > m_run[mb] + kHeadroom)) {
+                    float mt = smax * p.scale_log2;
+                    mt = max_x32(max_x16(mt));
+                    const float m_new = fmaxf(m_run[mb], mt);
+                    if (m_new > m_run[mb]) {
+                        const float alpha = fast_exp2(m_run[mb] - m_new);  // 0 when m_run = -inf
+                        l_part[mb] *= alpha;
 #pragma unroll
-                    for (int d = 0; d < DB; d++) o[mb][d] *= alpha;
-                    m_run[mb] = m_new;
+                        for (int d = 0; d < DB; d++) o[mb][d] *= alpha;
+                        m_run[mb] = m_new;
+                    }
                 }
             }
-            // every row with a visible key has a finite m_run here
-            const float nm = m_run[mb] == kNegInf ? 0.f : -m_run[mb];
+            // every row with a visible key in the block's first tile has a
+            // finite m_run here; a row without one sees no later key either
+            // (its keys are [0, start_pos + token], or all of them)
+            float nm = m_run[mb] == kNegInf ? 0.f : -m_run[mb];
             float x[8];
             float ps = 0.f;
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 x[j] = fast_exp2(fmaf(s[j], p.scale_log2, nm));
                 ps += x[j];
+            }
+            if (!first && __any(!(ps <= kClampW))) {  // rare: re-base on the tile's row max
+                float mt = kNegInf;
+#pragma unroll
+                for (int j = 0; j < 8; j++) mt = fmaxf(mt, fmaf(s[j], p.scale_log2, nm));
+                mt = max_x32(max_x16(mt));
+                const float shift = fmaxf(mt, 0.f);  // rows under their reference keep it
+                const float alpha = fast_exp2(-shift);
+                l_part[mb] *= alpha;
+#pragma unroll
+                for (int d = 0; d < DB; d++) o[mb][d] *= alpha;
+                m_run[mb] = (m_run[mb] == kNegInf ? 0.f : m_run[mb]) + shift;
+                nm -= shift;
+                ps = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    x[j] = fast_exp2(fmaf(s[j], p.scale_log2, nm));
+                    ps += x[j];
+                }
             }
             l_part[mb] += ps;
             u32x4_t pfr[NP];
@@ -463,6 +498,7 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
     __shared__ int resc_x[2][NS];               // per P buffer: head's factors apply
     __shared__ float linv_x[NS][16];
     constexpr float kHeadroom = 8.f;
+    constexpr float kClampW = 32768.f;  // later tiles: re-base when a lane's 8 weights sum past 2^15
 
     // longest-first over (query block, kv head, slice)
     const int lin = blockIdx.x;
@@ -553,27 +589,54 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
                     for (int jj = 0; jj < 8; jj++)
                         if (key0 + jj >= row_lim) s[jj] = kNegInf;
                 }
-                float smax = s[0];
-#pragma unroll
-                for (int jj = 1; jj < 8; jj++) smax = fmaxf(smax, s[jj]);
+                // the block's first tile sets each row's reference max (test
+                // on the tile's max); later tiles form the weights first and
+                // re-base only when a lane's 8 weights sum past kClampW
+                // (every weight >= 0: any weight past it, also an infinite
+                // one, shows), one compare instead of a max over the scores
                 float alpha = 1.f;
-                const bool rebase = __any(smax * p.scale_log2 > m_run[mb] + kHeadroom);
-                if (rebase) {
-                    const float mt = max_x32(max_x16(smax * p.scale_log2));
-                    const float m_new = fmaxf(m_run[mb], mt);
-                    if (m_new > m_run[mb]) {
-                        alpha = fast_exp2(m_run[mb] - m_new);  // 0 when m_run = -inf
-                        l_part[mb] *= alpha;
-                        m_run[mb] = m_new;
+                bool rebase = false;
+                if (j == 0) {
+                    float smax = s[0];
+#pragma unroll
+                    for (int jj = 1; jj < 8; jj++) smax = fmaxf(smax, s[jj]);
+                    rebase = __any(smax * p.scale_log2 > m_run[mb] + kHeadroom);
+                    if (rebase) {
+                        const float mt = max_x32(max_x16(smax * p.scale_log2));
+                        const float m_new = fmaxf(m_run[mb], mt);
+                        if (m_new > m_run[mb]) {
+                            alpha = fast_exp2(m_run[mb] - m_new);  // 0 when m_run = -inf
+                            l_part[mb] *= alpha;
+                            m_run[mb] = m_new;
+                        }
                     }
                 }
-                const float nm = m_run[mb] == kNegInf ? 0.f : -m_run[mb];
+                // a row without a visible key in the first tile sees no later key
+                float nm = m_run[mb] == kNegInf ? 0.f : -m_run[mb];
                 float x[8];
                 float ps = 0.f;
 #pragma unroll
                 for (int jj = 0; jj < 8; jj++) {
                     x[jj] = fast_exp2(fmaf(s[jj], p.scale_log2, nm));
                     ps += x[jj];
+                }
+                if (j > 0 && __any(!(ps <= kClampW))) {  // rare: re-base on the tile's row max
+                    rebase = true;
+                    float mt = kNegInf;
+#pragma unroll
+                    for (int jj = 0; jj < 8; jj++) mt = fmaxf(mt, fmaf(s[jj], p.scale_log2, nm));
+                    mt = max_x32(max_x16(mt));
+                    const float shift = fmaxf(mt, 0.f);  // rows under their reference keep it
+                    alpha = fast_exp2(-shift);
+                    l_part[mb] *= alpha;
+                    m_run[mb] = (m_run[mb] == kNegInf ? 0.f : m_run[mb]) + shift;
+                    nm -= shift;
+                    ps = 0.f;
+#pragma unroll
+                    for (int jj = 0; jj < 8; jj++) {
+                        x[jj] = fast_exp2(fmaf(s[jj], p.scale_log2, nm));
+                        ps += x[jj];
+                    }
                 }
                 l_part[mb] += ps;
                 u32x4_t pfr[NP];

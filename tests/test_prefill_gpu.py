@@ -162,9 +162,9 @@ def test_short_kernel(device, N, H, Hk, start, dtype, causal):
 
 
 def test_short_kernel_is_the_default_where_it_fits(device):
-    # the automatic choice for a Llama-3.2-1B prompt of >= 256 visible keys
+    # the automatic choice for a Llama-3.2-1B prompt of >= 384 visible keys
     # equals the forced short kernel bit for bit
-    c = C.prefill_case(93, 250, 32, 8, 64, 10, C.BF16)
+    c = C.prefill_case(93, 400, 32, 8, 64, 10, C.BF16)
     assert np.array_equal(run_gpu(c, device, C.F32), run_gpu(c, device, C.F32, kernel=_capi.PREFILL_KERNEL_SHORT))
 
 
