@@ -711,7 +711,7 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
                 const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(tp + 4 * kRowBytes));
                 return u32x4_t{lo[0], lo[1], hi[0], hi[1]};
             };
-            constexpr int VPD = 4;
+            constexpr int VPD = 2;  // transpose reads ahead of their MFMAs (2 measured ahead of 1, 3, 4 and 8)
             u32x4_t vb[VPD];
 #pragma unroll
             for (int q = 0; q < VPD; q++) vb[q] = tr_load(q);
