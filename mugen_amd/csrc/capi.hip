@@ -594,11 +594,13 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     const float scale = a->scale > 0.f ? a->scale : 1.f / sqrtf((float)a->head_dim);
     p.scale_log2 = scale * kLog2e;
     // the warp-specialised kernel where it measured faster: 1024..4096-token
-    // prompts (at 512 tokens and at 8192 the per-block kernel is ahead), and
-    // for more than 8 heads per kv head (it takes them in slices of 8);
-    // args->kernel forces one
-    int kernel = (a->n_tokens >= 1024 && a->n_tokens <= 4096) || p.G > 8 ? MUGEN_ATTN_PREFILL_KERNEL_WS
-                                                                         : MUGEN_ATTN_PREFILL_KERNEL_BLOCK;
+    // prompts, up to 6144 at head_dim > 64 (Qwen2.5-7B N = 6144: 363 against
+    // 371 us; at 8192 the two tie, and at head_dim 64 the per-block kernel
+    // is ahead from 6144: 227 against 230 us), and for more than 8 heads per
+    // kv head (it takes them in slices of 8); args->kernel forces one
+    const int ws_max = a->head_dim > 64 ? 6144 : 4096;
+    int kernel = (a->n_tokens >= 1024 && a->n_tokens <= ws_max) || p.G > 8 ? MUGEN_ATTN_PREFILL_KERNEL_WS
+                                                                           : MUGEN_ATTN_PREFILL_KERNEL_BLOCK;
     // prompts whose whole kv range fits on chip: the short-prompt kernel,
     // from 384 visible keys on (below that the per-block kernel's shorter
     // load phase wins: Llama-3.2-1B N = 128 4.4 against 4.9 us; N = 256 5.55
