@@ -168,14 +168,14 @@ def test_short_kernel_is_the_default_where_it_fits(device):
     assert np.array_equal(run_gpu(c, device, C.F32), run_gpu(c, device, C.F32, kernel=_capi.PREFILL_KERNEL_SHORT))
 
 
-@pytest.mark.parametrize("kernel", [_capi.PREFILL_KERNEL_BLOCK, _capi.PREFILL_KERNEL_WS, _capi.PREFILL_KERNEL_SHORT])
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("kernel,D", [
+    (_capi.PREFILL_KERNEL_BLOCK, 64), (_capi.PREFILL_KERNEL_BLOCK, 128), (_capi.PREFILL_KERNEL_WS, 64),
+    (_capi.PREFILL_KERNEL_WS, 128), (_capi.PREFILL_KERNEL_SHORT, 64),  # (the short kernel: head_dim 64 only)
+])
 def test_climbing_scores_rebase(device, kernel, D):
     # scores that climb by > 15 log2 units per 64-key tile (key dim 0 grows
     # with the key index, q dim 0 is large), so every row's running max moves
     # on every tile and the kernels' re-base paths run throughout
-    if kernel == _capi.PREFILL_KERNEL_SHORT and D != 64:
-        pytest.skip("the short kernel serves head_dim 64")
     N, H, Hk = (300, 32, 8) if D == 64 else (300, 28, 4)
     c = C.prefill_case(97 + D, N, H, Hk, D, 20, C.BF16)
     q, k = c["q"].copy(), c["k"].copy()
