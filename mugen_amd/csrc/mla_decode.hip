@@ -480,16 +480,24 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
     // ---- PV waves: DMA of tile tt into slot sl (wave wr moves LDS chunks
     // [64K, 64K+64) for K = wr + 4k; chunk (r, pc) holds source chunk
     // (r, pc ^ swz(r)); the split's last tile is clamped to valid rows)
+    uint32_t dma_off[DPW];  // this lane's byte offset in a tile per DMA op (tile-invariant)
+#pragma unroll
+    for (int k = 0; k < DPW; k++) {
+        const int sl = 64 * (wr + 4 * k) + lane;
+        const int r = sl / (kRowBytes / 16), pc = sl - r * (kRowBytes / 16);
+        dma_off[k] = (uint32_t)(r * kRowBytes + ((pc ^ swz(r)) * 16));
+    }
     auto issue = [&](int tile_idx) {
         const int tt = t_begin + kTT * tile_idx;
         const uint16_t* src = lat + (int64_t)tt * kCD;
         const uint32_t lds0 = ring_base + (tile_idx % NSLOT) * kTileBytes + wr * 1024;
-        const uint32_t lim = tt + kTT <= t_end ? 0xFFFFFFFFu : (uint32_t)(t_end - tt) * kRowBytes - 16;
+        if (tt + kTT <= t_end) {  // wave-uniform: interior tiles need no clamp
 #pragma unroll
-        for (int k = 0; k < DPW; k++) {
-            const int sl = 64 * (wr + 4 * k) + lane;
-            const int r = sl / (kRowBytes / 16), pc = sl - r * (kRowBytes / 16);
-            dma16s(lds0 + k * 4096, src, min((uint32_t)(r * kRowBytes + ((pc ^ swz(r)) * 16)), lim));
+            for (int k = 0; k < DPW; k++) dma16s(lds0 + k * 4096, src, dma_off[k]);
+        } else {
+            const uint32_t lim = (uint32_t)(t_end - tt) * kRowBytes - 16;
+#pragma unroll
+            for (int k = 0; k < DPW; k++) dma16s(lds0 + k * 4096, src, min(dma_off[k], lim));
         }
     };
 
