@@ -822,7 +822,10 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
 //    re-base) while the V rows are still in flight;
 //  * bf16 V rows are converted to fp16 in LDS by the wave whose DMA moved
 //    them (exact inside the f16 range), so O^T += V^T . P^T is one fp16
-//    MFMA with P (11 significant bits) straight from registers;
+//    MFMA with P (11 significant bits) straight from registers; each row's
+//    weight sum comes from one more MFMA against an all-ones V block (the
+//    sum of exactly the fp16 weights P.V used, with no per-lane adds or
+//    cross-lane reduction);
 //  * merge: each wave stages (max, sum) and its O^T in the K rows' space
 //    (free once every wave has passed the V barrier); after one barrier
 //    every wave sums and stores an eighth of the block's output.
@@ -967,19 +970,14 @@ __global__ __launch_bounds__(512) void gqa_prefill_short_kernel(GqaPrefillParams
         mx = max_x32(max_x16(mx));
         m[mb] = mx * p.scale_log2;  // the range's max in log2 units
         const float nm = mx == kNegInf ? 0.f : -m[mb];
-        float ls = 0.f;
 #pragma unroll
         for (int u = 0; u < NU; u++) {
             if (u >= nu) continue;
             float x[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                x[j] = fast_exp2(fmaf(s[u][mb][j], p.scale_log2, nm));
-                ls += x[j];
-            }
+            for (int j = 0; j < 8; j++) x[j] = fast_exp2(fmaf(s[u][mb][j], p.scale_log2, nm));
             split_p<DT_F16, 1>(x, &pf[u][mb]);
         }
-        l[mb] = ls;
     }
 
     // ---- V rows: bf16 -> fp16 by the wave whose DMA moved them
@@ -1003,10 +1001,14 @@ __global__ __launch_bounds__(512) void gqa_prefill_short_kernel(GqaPrefillParams
     lds_barrier();  // B2: the range's V rows (fp16) from both waves; every wave is done with K
 
     f32x4_t o[MBW][DB];
+    f32x4_t osum[MBW];  // O^T rows of an all-ones V block: every row holds the row's weight sum
+    const u32x4_t ones = u32x4_t{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};  // fp16 1.0 pairs
 #pragma unroll
-    for (int mb = 0; mb < MBW; mb++)
+    for (int mb = 0; mb < MBW; mb++) {
+        osum[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int d = 0; d < DB; d++) o[mb][d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
     for (int u = 0; u < NU; u++) {
         if (u >= nu) continue;
@@ -1019,9 +1021,11 @@ __global__ __launch_bounds__(512) void gqa_prefill_short_kernel(GqaPrefillParams
             vf[d] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
         }
 #pragma unroll
-        for (int mb = 0; mb < MBW; mb++)
+        for (int mb = 0; mb < MBW; mb++) {
 #pragma unroll
             for (int d = 0; d < DB; d++) o[mb][d] = mfma16x16x32<DT_F16>(vf[d], pf[u][mb], o[mb][d]);
+            osum[mb] = mfma16x16x32<DT_F16>(ones, pf[u][mb], osum[mb]);
+        }
     }
 
     // ---- merge the 4 key ranges of each head pair: (max, sum) and the
@@ -1029,7 +1033,7 @@ __global__ __launch_bounds__(512) void gqa_prefill_short_kernel(GqaPrefillParams
     f32x4_t* stage = reinterpret_cast<f32x4_t*>(&lds[0]);  // [wave][mb][d][lane]: 64 KiB, the K rows
 #pragma unroll
     for (int mb = 0; mb < MBW; mb++) {
-        l[mb] = sum_x32(sum_x16(l[mb]));
+        l[mb] = osum[mb][0];  // the sum over the range's keys of the fp16 weights P.V used
         if (g == 0) mlx[w][mb][n] = make_float2(m[mb], l[mb]);
 #pragma unroll
         for (int d = 0; d < DB; d++) stage[((w * MBW + mb) * DB + d) * 64 + lane] = o[mb][d];
