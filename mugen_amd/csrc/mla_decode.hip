@@ -765,15 +765,17 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
 }
 
 // Log-sum-exp merge of the split partials.  Workgroup = (16-row block,
-// group of 8 column blocks, sequence).  The per-row split weights
-// w_s = 2^(m_s - M) l_s are formed once in LDS (16 splits x 16 rows in
-// parallel); then lane l of wave w reads, per split, the fp16 fragments
-// (4 rows x 1 column) of column blocks 2w, 2w+1 -- the order the main
-// kernel wrote, 512 B contiguous per wave -- and accumulates in fp32.
-template <int OUT_DT>
-__global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
+// group of 2 NW column blocks, sequence), NW waves.  The per-row split
+// weights w_s = 2^(m_s - M) l_s are formed once in LDS (4 NW splits x 16
+// rows in parallel); then lane l of wave w reads, per split, the fp16
+// fragments (4 rows x 1 column) of column blocks 2w, 2w+1 of the group --
+// the order the main kernel wrote, 512 B contiguous per wave -- and
+// accumulates in fp32.
+template <int OUT_DT, int NW>
+__global__ __launch_bounds__(64 * NW) void mla_decode_combine_kernel(MlaParams p) {
+    constexpr int SP = 64 * NW / 16;  // split phases of the weights
     __shared__ __attribute__((aligned(16))) float wts[kMaxMlaSplits][16];
-    __shared__ float red[16][16];
+    __shared__ float red[SP][16];
     __shared__ float linv[16];
     const int qb = blockIdx.x, dg = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, dsub = tid >> 6;
@@ -784,7 +786,7 @@ __global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
     const float* ml0 = p.ws_ml + (int64_t)b * p.num_splits * p.R * 2;
 
     MUGEN_TRACE(8);
-    const int d0 = dg * 8 + dsub * 2;
+    const int d0 = dg * 2 * NW + dsub * 2;
     const u32x4_t* src = reinterpret_cast<const u32x4_t*>(p.ws_o) + blob_pair(p, b, 0, qb, d0 >> 1, lane);
     const int64_t frag_st = (int64_t)p.nq * 16 * 64;  // 16-byte units between splits
     // the first PF splits' fp16 fragments are requested before the split
@@ -800,11 +802,11 @@ __global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
     // fragments; further splits are read from the workspace in the loops.
     const int r = tid & 15, sl = tid >> 4, row = qb * 16 + r;
     const bool rok = row < p.R;
-    constexpr int MLC = 2;
+    constexpr int MLC = 32 / SP;
     f32x2v_t mlc[MLC];
 #pragma unroll
     for (int k = 0; k < MLC; k++) {
-        const int s = sl + 16 * k;
+        const int s = sl + SP * k;
         mlc[k] = (rok && s < nact) ? *reinterpret_cast<const f32x2v_t*>(ml0 + s * ml_st + row * 2)
                                    : f32x2v_t{kNegInf, 0.f};
     }
@@ -812,24 +814,24 @@ __global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
     float mx = kNegInf;
 #pragma unroll
     for (int k = 0; k < MLC; k++) mx = fmaxf(mx, mlc[k][0]);
-    for (int s = sl + 16 * MLC; s < nact; s += 16) mx = fmaxf(mx, rok ? ml0[s * ml_st + row * 2] : kNegInf);
+    for (int s = sl + SP * MLC; s < nact; s += SP) mx = fmaxf(mx, rok ? ml0[s * ml_st + row * 2] : kNegInf);
     red[sl][r] = mx;
     __syncthreads();
     float M = kNegInf;
 #pragma unroll
-    for (int j = 0; j < 16; j++) M = fmaxf(M, red[j][r]);
+    for (int j = 0; j < SP; j++) M = fmaxf(M, red[j][r]);
     __syncthreads();
     float sum = 0.f;
 #pragma unroll
     for (int k = 0; k < MLC; k++) {
-        const int s = sl + 16 * k;
+        const int s = sl + SP * k;
         if (s < nact) {
             const float wgt = (mlc[k][0] == kNegInf) ? 0.f : fast_exp2(mlc[k][0] - M) * mlc[k][1];
             wts[s][r] = wgt;
             sum += wgt;
         }
     }
-    for (int s = sl + 16 * MLC; s < nact; s += 16) {
+    for (int s = sl + SP * MLC; s < nact; s += SP) {
         const float m = rok ? ml0[s * ml_st + row * 2] : kNegInf;
         const float wgt = (m == kNegInf) ? 0.f : fast_exp2(m - M) * ml0[s * ml_st + row * 2 + 1];
         wts[s][r] = wgt;
@@ -840,7 +842,7 @@ __global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaParams p) {
     if (tid < 16) {
         float L = 0.f;
 #pragma unroll
-        for (int j = 0; j < 16; j++) L += red[j][tid];
+        for (int j = 0; j < SP; j++) L += red[j][tid];
         linv[tid] = L > 0.f ? 1.f / L : 0.f;
     }
     __syncthreads();
@@ -906,8 +908,15 @@ static hipError_t launch_mla_t(const MlaParams& p, int kernel, hipStream_t st, K
                        ? launch_k(t, "mla_decode", mla_decode_kernel<QDT, DT>, dim3(grid), dim3(256), st, p)
                        : launch_k(t, "mla_decode", mla_decode_ws_kernel<QDT, DT>, dim3(grid), dim3(512), st, p);
     if (e != hipSuccess) return e;
-    return launch_k(t, "mla_decode_combine", mla_decode_combine_kernel<OUT_DT>, dim3(p.nq, 4, p.B),
-                    dim3(256), st, p);
+    // tiny merges (V2-Lite decode: one 16-row block of one sequence) spread
+    // over more, smaller workgroups: 2 waves of 2 column blocks each (10.8 ->
+    // 10.3-10.6 us per V2-Lite step); larger grids keep 4 waves (a 512-token
+    // prompt measured 9% slower with 2)
+    if (p.nq * p.B <= 4)
+        return launch_k(t, "mla_decode_combine", mla_decode_combine_kernel<OUT_DT, 2>, dim3(p.nq, 8, p.B), dim3(128),
+                        st, p);
+    return launch_k(t, "mla_decode_combine", mla_decode_combine_kernel<OUT_DT, 4>, dim3(p.nq, 4, p.B), dim3(256),
+                    st, p);
 }
 
 template <int QDT, int DT>
