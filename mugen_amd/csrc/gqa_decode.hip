@@ -437,11 +437,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 //  * more splits: the weights are formed block-wide in LDS (lse_weights),
 //    then the partials are summed 8 splits at a time.
 template <int D, int OUT_DT, bool PAD>
-__global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p) {
+__global__ __launch_bounds__(64) void gqa_decode_combine_kernel(GqaDecodeParams p) {
     constexpr int kPre = 32;
     __shared__ float f_lds[kMaxSplits];
     __shared__ float red_lds[4];
-    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    const int h = blockIdx.x, b = blockIdx.y, d = blockIdx.z * 64 + threadIdx.x;
     MUGEN_TRACE(8);
     const int T = clamp_len(p.seq_lens[b], p.max_T);
     const int nact = p.n_q4 ? min(p.num_splits, T > 0 ? splits_of<true>(p, b) : 0)
@@ -453,7 +453,7 @@ __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p
     float inv;
     if (nact <= 64) {
         const int lane = d & 63;
-        float* fw = &f_lds[(d >> 6) * 64];  // this wave's weights
+        float* fw = &f_lds[0];  // this wave's weights
         const float ms = lane < nact ? ml[2 * lane] : kNegInf;
         const float ls = lane < nact ? ml[2 * lane + 1] : 0.f;
         float v[kPre];  // clamped, unconditional loads: exact wait counts
@@ -481,7 +481,8 @@ __global__ __launch_bounds__(D) void gqa_decode_combine_kernel(GqaDecodeParams p
     } else {
         // this thread's split (m, l), then the first 8 splits' partials,
         // all in flight before the weights are formed
-        const float m0 = d < nact ? ml[2 * d] : kNegInf, l0 = d < nact ? ml[2 * d + 1] : 0.f;
+        const int ts = threadIdx.x;  // this thread's split for the weights (lse_weights' convention)
+        const float m0 = ts < nact ? ml[2 * ts] : kNegInf, l0 = ts < nact ? ml[2 * ts + 1] : 0.f;
         float v0[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) v0[j] = os[(int64_t)j * D];
@@ -515,9 +516,9 @@ static hipError_t launch_gqa_t(const GqaDecodeParams& p, int nwg, hipStream_t st
                        : launch_k(timer, "gqa_decode", gqa_decode_kernel<D, DT, OUT_DT, Q4>, dim3(grid), dim3(256), st, p);
     if (e != hipSuccess || p.num_splits == 1) return e;
     if (!Q4 && p.hd != D)
-        return launch_k(timer, "gqa_decode_combine", gqa_decode_combine_kernel<D, OUT_DT, true>, dim3(p.H, p.B),
-                        dim3(D), st, p);
-    return launch_k(timer, "gqa_decode_combine", gqa_decode_combine_kernel<D, OUT_DT, false>, dim3(p.H, p.B), dim3(D),
+        return launch_k(timer, "gqa_decode_combine", gqa_decode_combine_kernel<D, OUT_DT, true>, dim3(p.H, p.B, D / 64),
+                        dim3(64), st, p);
+    return launch_k(timer, "gqa_decode_combine", gqa_decode_combine_kernel<D, OUT_DT, false>, dim3(p.H, p.B, D / 64), dim3(64),
                     st, p);
 }
 

@@ -65,3 +65,13 @@ def test_golden_fixture(device):
     c = dict(B=int(fx["B"]), H=int(fx["H"]), Hk=int(fx["Hk"]), D=int(fx["D"]), max_T=int(fx["max_T"]),
              dtype=int(fx["dtype"]), qb=fx["qb"], kb=fx["kb"], vb=fx["vb"], seq_lens=fx["seq_lens"])
     C.assert_close(run_gpu(c, device, C.F32), fx["out_f64"], "golden gqa_decode_small")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_more_than_64_splits(device, D):
+    # 64-token splits over 8192 and 5000 tokens: 128 and 79 splits, past the
+    # combine's one-load-per-lane weights (<= 64), so the block-wide
+    # log-sum-exp weights run
+    c = C.gqa_decode_case(47 + D, 2, 28, 4, D, [8192, 5000], dtype=C.F16)
+    ref = C.gqa_decode_ref(c, nthreads=8)
+    C.assert_close(run_gpu(c, device, C.F32, 200), ref, f"gqa decode D={D} 128 / 79 splits")
