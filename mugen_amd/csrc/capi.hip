@@ -11,6 +11,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <mutex>
 #include <string>
@@ -593,12 +594,13 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     p.causal = a->causal ? 1 : 0;
     const float scale = a->scale > 0.f ? a->scale : 1.f / sqrtf((float)a->head_dim);
     p.scale_log2 = scale * kLog2e;
-    // the warp-specialised kernel where it measured faster: 1024..4096-token
-    // prompts, up to 6144 at head_dim > 64 (Qwen2.5-7B N = 6144: 363 against
-    // 371 us; at 8192 the two tie, and at head_dim 64 the per-block kernel
-    // is ahead from 6144: 227 against 230 us), and for more than 8 heads per
-    // kv head (it takes them in slices of 8); args->kernel forces one
-    const int ws_max = a->head_dim > 64 ? 6144 : 4096;
+    // the warp-specialised kernel where it measured faster: prompts from
+    // 1024 tokens, at head_dim 64 up to 4096 (bf16, eager calls: Qwen2.5-7B
+    // shape N = 8192 603 against 690 us, N = 32768 8.76 against 8.86 ms;
+    // Llama-3.2-1B shape N = 4096 114 against 116 us, N = 8192 423 against
+    // 381), and for more than 8 heads per kv head (it takes them in slices
+    // of 8); args->kernel forces one
+    const int ws_max = a->head_dim > 64 ? INT_MAX : 4096;
     int kernel = (a->n_tokens >= 1024 && a->n_tokens <= ws_max) || p.G > 8 ? MUGEN_ATTN_PREFILL_KERNEL_WS
                                                                            : MUGEN_ATTN_PREFILL_KERNEL_BLOCK;
     // prompts whose whole kv range fits on chip: the short-prompt kernel,

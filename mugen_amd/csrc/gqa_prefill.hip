@@ -472,27 +472,30 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
 //  * one barrier per tile: at barrier j tile j has landed, the S waves have
 //    written P(j-1), and the PV waves have finished tile j-2, whose slot
 //    then receives tile j+2.
-template <int D, int NS, int SMB, int NPV, int DTI, int OUT_DT, bool PAD>
+template <int D, int NS, int SMB, int NPV, int DTI, int OUT_DT, bool PAD, int TPS>
 __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(GqaPrefillParams p, int nqb,
                                                                                int nslice, int Hk) {
     constexpr int DT = DTI == kDtBf16V16 ? DT_BF16 : DTI;  // q and K
     const int hd = PAD ? p.hd : D;
-    constexpr int TK = 32;                      // keys per tile
+    constexpr int TK = 32;                      // keys per tile (one MFMA k-step of P.V)
+    constexpr int KS = TK * TPS;                // keys per step: TPS tiles between two barriers
     constexpr int KK = D / 32;                  // k-steps of S over head_dim
     constexpr int DB = D / 16;                  // 16-wide output column blocks
     constexpr int RB = D * 2;                   // bytes per tile row
     constexpr int CR = D / 8;                   // 16-byte chunks per row
     constexpr int MAT = TK * RB;                // bytes of one K or V tile
-    constexpr int SLOT = 2 * MAT;
-    constexpr int NSLOT = 4;                    // NSLOT - 2 tiles in flight
-    constexpr int DPW = 2 * MAT / 1024 / NPV;   // 1-KiB DMA ops per PV wave per tile (K and V)
+    constexpr int VOFF = TPS * MAT;             // a slot: the step's K rows, then its V rows
+    constexpr int SLOT = 2 * VOFF;
+    constexpr int NSLOT = TPS == 1 ? 4 : 3;     // NSLOT - 2 steps in flight
+    constexpr int DPW = SLOT / 1024 / NPV;      // 1-KiB DMA ops per PV wave per step (K and V)
     // bf16 inputs: P.V in fp16 as in the per-block kernel (the PV waves
     // convert the V chunks they moved; P goes to LDS as one fp16 term)
     constexpr bool VCVT = DTI == DT_BF16;
     constexpr int PDT = (VCVT || DTI == kDtBf16V16) ? DT_F16 : DT;
     constexpr int NP = p_terms<PDT>();
-    constexpr int PB = NS * NP * 64 * 16;       // one P buffer: NS heads x NP terms x 64 lanes x 16 B
+    constexpr int PB = TPS * NS * NP * 64 * 16; // one P buffer: TPS tiles x NS heads x NP terms x 64 lanes x 16 B
     static_assert(DPW >= 2 && DPW % 2 == 0 && NS % NPV == 0, "tile split");
+    static_assert(TPS == 1 || !VCVT, "in-LDS V conversion: one tile per step");
     __shared__ __attribute__((aligned(1024))) char ring[NSLOT * SLOT + 2 * PB];
     __shared__ float alpha_x[2][NS][16];        // per P buffer: re-base factor of (head, query)
     __shared__ int resc_x[2][NS];               // per P buffer: head's factors apply
@@ -517,7 +520,7 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
     const int nh = min(NS, G - NS * slice);     // heads of this slice
     int kend = p.kv_len;
     if (p.causal) kend = min(kend, p.start_pos + min(t0 + 16, p.N));
-    const int ntiles = (kend + TK - 1) / TK;
+    const int ntiles = (kend + KS - 1) / KS;    // steps
     const uint32_t ring_base = lds_addr(&ring[0]);
     char* pbuf = &ring[NSLOT * SLOT];
 
@@ -558,18 +561,22 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             if (j == ntiles) break;
             if (!hok[0]) continue;
             const char* tile = &ring[(j % NSLOT) * SLOT];
-            const int kt = j * TK;
-            u32x4_t af[2][KK];
+            const int kt = j * KS;
+            // block nb of tile u: keys kt + 32u + 8g + 4(nb % 2) + i
+            constexpr int NB = 2 * TPS;
+            u32x4_t af[NB][KK];
 #pragma unroll
-            for (int nb = 0; nb < 2; nb++)
+            for (int nb = 0; nb < NB; nb++)
 #pragma unroll
                 for (int kk = 0; kk < KK; kk++)
-                    af[nb][kk] = *reinterpret_cast<const u32x4_t*>(tile + a_off[kk] + nb * 4 * RB);
-            float sv[SMB][8];
+                    af[nb][kk] = *reinterpret_cast<const u32x4_t*>(tile + (nb >> 1) * MAT + a_off[kk] +
+                                                                   (nb & 1) * 4 * RB);
+            constexpr int NV = 4 * NB;          // scores per lane per head
+            float sv[SMB][NV];
 #pragma unroll
             for (int mb = 0; mb < SMB; mb++)
 #pragma unroll
-                for (int nb = 0; nb < 2; nb++) {
+                for (int nb = 0; nb < NB; nb++) {
                     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int kk = 0; kk < KK; kk++) acc = mfma16x16x32<DT>(af[nb][kk], qf[mb][kk], acc);
@@ -582,16 +589,15 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
                 if (!hok[mb]) continue;
                 const int hs = wr * SMB + mb;
                 float* s = sv[mb];
-                // lane: query t0+n, keys kt + 8g + 4nb + i
-                if (kt + TK > mask_from) {
-                    const int key0 = kt + 8 * g;
+                // lane: query t0+n, keys kt + 32u + 8g + 4nb + i
+                if (kt + KS > mask_from) {
 #pragma unroll
-                    for (int jj = 0; jj < 8; jj++)
-                        if (key0 + jj >= row_lim) s[jj] = kNegInf;
+                    for (int jj = 0; jj < NV; jj++)
+                        if (kt + 32 * (jj >> 3) + 8 * g + (jj & 7) >= row_lim) s[jj] = kNegInf;
                 }
                 // the block's first tile sets each row's reference max (test
                 // on the tile's max); later tiles form the weights first and
-                // re-base only when a lane's 8 weights sum past kClampW
+                // re-base only when a lane's weights of one tile sum past kClampW
                 // (every weight >= 0: any weight past it, also an infinite
                 // one, shows), one compare instead of a max over the scores
                 float alpha = 1.f;
@@ -599,7 +605,7 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
                 if (j == 0) {
                     float smax = s[0];
 #pragma unroll
-                    for (int jj = 1; jj < 8; jj++) smax = fmaxf(smax, s[jj]);
+                    for (int jj = 1; jj < NV; jj++) smax = fmaxf(smax, s[jj]);
                     rebase = __any(smax * p.scale_log2 > m_run[mb] + kHeadroom);
                     if (rebase) {
                         const float mt = max_x32(max_x16(smax * p.scale_log2));
@@ -613,38 +619,51 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
                 }
                 // a row without a visible key in the first tile sees no later key
                 float nm = m_run[mb] == kNegInf ? 0.f : -m_run[mb];
-                float x[8];
-                float ps = 0.f;
+                float x[NV];
+                float ps[TPS];
 #pragma unroll
-                for (int jj = 0; jj < 8; jj++) {
-                    x[jj] = fast_exp2(fmaf(s[jj], p.scale_log2, nm));
-                    ps += x[jj];
+                for (int u = 0; u < TPS; u++) {
+                    ps[u] = 0.f;
+#pragma unroll
+                    for (int jj = 8 * u; jj < 8 * u + 8; jj++) {
+                        x[jj] = fast_exp2(fmaf(s[jj], p.scale_log2, nm));
+                        ps[u] += x[jj];
+                    }
                 }
-                if (j > 0 && __any(!(ps <= kClampW))) {  // rare: re-base on the tile's row max
+                bool over = false;
+#pragma unroll
+                for (int u = 0; u < TPS; u++) over |= !(ps[u] <= kClampW);
+                if (j > 0 && __any(over)) {  // rare: re-base on the step's row max
                     rebase = true;
                     float mt = kNegInf;
 #pragma unroll
-                    for (int jj = 0; jj < 8; jj++) mt = fmaxf(mt, fmaf(s[jj], p.scale_log2, nm));
+                    for (int jj = 0; jj < NV; jj++) mt = fmaxf(mt, fmaf(s[jj], p.scale_log2, nm));
                     mt = max_x32(max_x16(mt));
                     const float shift = fmaxf(mt, 0.f);  // rows under their reference keep it
                     alpha = fast_exp2(-shift);
                     l_part[mb] *= alpha;
                     m_run[mb] = (m_run[mb] == kNegInf ? 0.f : m_run[mb]) + shift;
                     nm -= shift;
-                    ps = 0.f;
 #pragma unroll
-                    for (int jj = 0; jj < 8; jj++) {
-                        x[jj] = fast_exp2(fmaf(s[jj], p.scale_log2, nm));
-                        ps += x[jj];
+                    for (int u = 0; u < TPS; u++) {
+                        ps[u] = 0.f;
+#pragma unroll
+                        for (int jj = 8 * u; jj < 8 * u + 8; jj++) {
+                            x[jj] = fast_exp2(fmaf(s[jj], p.scale_log2, nm));
+                            ps[u] += x[jj];
+                        }
                     }
                 }
-                l_part[mb] += ps;
-                u32x4_t pfr[NP];
-                split_p<PDT, NP>(x, pfr);
                 char* pb = pbuf + (j & 1) * PB;
 #pragma unroll
-                for (int pp = 0; pp < NP; pp++)
-                    *reinterpret_cast<u32x4_t*>(pb + ((hs * NP + pp) * 64 + lane) * 16) = pfr[pp];
+                for (int u = 0; u < TPS; u++) {
+                    l_part[mb] += ps[u];
+                    u32x4_t pfr[NP];
+                    split_p<PDT, NP>(x + 8 * u, pfr);
+#pragma unroll
+                    for (int pp = 0; pp < NP; pp++)
+                        *reinterpret_cast<u32x4_t*>(pb + (((u * NS + hs) * NP + pp) * 64 + lane) * 16) = pfr[pp];
+                }
                 if (g == 0) alpha_x[j & 1][hs][n] = alpha;
                 if (lane == 0) resc_x[j & 1][hs] = rebase ? 1 : 0;
             }
@@ -662,25 +681,21 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
         const uint16_t* vb = p.v + (int64_t)kvh * hd;
         const int rs_bytes = p.row_stride * 2;
         // DMA op k of this wave moves K / V chunks [64(wr + NPV k), +64) of the
-        // tile: chunk slot s = row s / CR, physical chunk s % CR, holding
-        // logical chunk (s % CR) ^ pf_swz(row); rows past kend are clamped
-        int dma_row[DPW / 2];
-        uint32_t dma_col[DPW / 2];
-#pragma unroll
-        for (int k = 0; k < DPW / 2; k++) {
-            const int slot = 64 * (wr + NPV * k) + lane;
-            const int r = slot / CR, pc = slot % CR;
-            dma_row[k] = r;
-            dma_col[k] = (uint32_t)(dim_chunk(pc ^ pf_swz<D>(r), hd) * 16);
-        }
+        // step: chunk slot s = row s / CR, physical chunk s % CR, holding
+        // logical chunk (s % CR) ^ pf_swz(row); rows past kend are clamped.
+        // Op k's rows are op 0's + k RSTEP, a multiple of 16: same swizzle
+        constexpr int RSTEP = 64 * NPV / CR;
+        static_assert(RSTEP % 16 == 0, "swizzle period");
+        const int dma_row = (64 * wr + lane) / CR;
+        const uint32_t dma_col = (uint32_t)(dim_chunk((lane % CR) ^ pf_swz<D>(dma_row), hd) * 16);
         auto issue = [&](int it) {
-            const int kt = it * TK;
+            const int kt = it * KS + dma_row;
             const uint32_t lds0 = ring_base + (it % NSLOT) * SLOT + wr * 1024;
 #pragma unroll
             for (int k = 0; k < DPW / 2; k++) {
-                const uint32_t off = (uint32_t)min(kt + dma_row[k], kend - 1) * rs_bytes + dma_col[k];
+                const uint32_t off = (uint32_t)min(kt + k * RSTEP, kend - 1) * rs_bytes + dma_col;
                 dma16s(lds0 + k * NPV * 1024, kb, off);
-                dma16s(lds0 + MAT + k * NPV * 1024, vb, off);
+                dma16s(lds0 + VOFF + k * NPV * 1024, vb, off);
             }
         };
         for (int it = 0; it < min(ntiles, NSLOT - 2); it++) issue(it);
@@ -689,7 +704,7 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
         // this interval's P.V, visible to the other PV waves from the next
         // barrier on (the interval in which they read that tile)
         auto cv_addr = [&](int it, int k) {
-            return reinterpret_cast<u32x4_t*>(&ring[(it % NSLOT) * SLOT + MAT] + (64 * (wr + NPV * k) + lane) * 16);
+            return reinterpret_cast<u32x4_t*>(&ring[(it % NSLOT) * SLOT + VOFF] + (64 * (wr + NPV * k) + lane) * 16);
         };
         u32x4_t cv[DPW / 2];
         auto cv_write = [&](int it) {
@@ -707,7 +722,7 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
         uint32_t t_off[DB];
 #pragma unroll
         for (int d = 0; d < DB; d++)
-            t_off[d] = MAT + tr * RB + (((2 * d + ((n & 3) >> 1)) ^ pf_swz<D>(tr)) * 16) + 8 * (n & 1);
+            t_off[d] = VOFF + tr * RB + (((2 * d + ((n & 3) >> 1)) ^ pf_swz<D>(tr)) * 16) + 8 * (n & 1);
         // this wave's heads: HPW consecutive heads of the slice, every column
         constexpr int HPW = NS / NPV;
         const int hb = wr * HPW;
@@ -746,19 +761,26 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             const char* tile = &ring[(jp % NSLOT) * SLOT];
             const char* pb = pbuf + (jp & 1) * PB;
             // this wave's heads' P, then the V^T fragments, in flight together
-            u32x4_t pf[HPW][NP];
+            u32x4_t pf[TPS][HPW][NP];
 #pragma unroll
-            for (int hh = 0; hh < HPW; hh++)
+            for (int u = 0; u < TPS; u++)
 #pragma unroll
-                for (int pp = 0; pp < NP; pp++)
-                    pf[hh][pp] = *reinterpret_cast<const u32x4_t*>(pb + (((hb + hh) * NP + pp) * 64 + lane) * 16);
+                for (int hh = 0; hh < HPW; hh++)
+#pragma unroll
+                    for (int pp = 0; pp < NP; pp++)
+                        pf[u][hh][pp] = *reinterpret_cast<const u32x4_t*>(
+                            pb + (((u * NS + hb + hh) * NP + pp) * 64 + lane) * 16);
+            auto read_v = [&](int u, u32x4_t* vf) {
+#pragma unroll
+                for (int d = 0; d < DB; d++) {
+                    const char* vt = tile + u * MAT + t_off[d];
+                    const u32x2_t lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(vt));
+                    const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(vt + 4 * RB));
+                    vf[d] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+                }
+            };
             u32x4_t vf[DB];
-#pragma unroll
-            for (int d = 0; d < DB; d++) {
-                const u32x2_t lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(tile + t_off[d]));
-                const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(tile + t_off[d] + 4 * RB));
-                vf[d] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
-            }
+            read_v(0, vf);
             // re-base (rare after the first tiles): the factors are read only
             // when one of this wave's heads moved its max (factor 1 otherwise)
             int any_rs = 0;
@@ -774,11 +796,16 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             }
             // (heads past nh accumulate stale P; their sums are never stored)
 #pragma unroll
-            for (int pp = 0; pp < NP; pp++)
+            for (int u = 0; u < TPS; u++) {
+                if (u > 0) read_v(u, vf);
 #pragma unroll
-                for (int d = 0; d < DB; d++)
+                for (int pp = 0; pp < NP; pp++)
 #pragma unroll
-                    for (int hh = 0; hh < HPW; hh++) o[hh][d] = mfma16x16x32<PDT>(vf[d], pf[hh][pp], o[hh][d]);
+                    for (int d = 0; d < DB; d++)
+#pragma unroll
+                        for (int hh = 0; hh < HPW; hh++)
+                            o[hh][d] = mfma16x16x32<PDT>(vf[d], pf[u][hh][pp], o[hh][d]);
+            }
             if constexpr (VCVT)
                 if (j < ntiles) cv_write(j);
             if (j == 8) MUGEN_TRACE(3);
@@ -1125,11 +1152,15 @@ static hipError_t launch_pf_g(const GqaPrefillParams& p, int Hk, int dt, int out
     return launch_pf_d<D, PAD, 2>(p, Hk, dt, out_dt, st, t);
 }
 
+// tiles per barrier interval of the warp-specialised kernel
+template <int DT>
+constexpr int kWsTps = DT == DT_BF16 ? 1 : 2;
+
 template <int D, bool PAD, int DT, int OUT_DT>
 static hipError_t launch_pf_ws_t(const GqaPrefillParams& p, int Hk, hipStream_t st, KernelTimer* t) {
     const int nqb = (p.N + 15) / 16;
     if (p.G <= 4)
-        return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 4, 1, 4, DT, OUT_DT, PAD>, dim3(nqb * Hk * ((p.G + 3) / 4)),
+        return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 4, 1, 4, DT, OUT_DT, PAD, kWsTps<DT>>, dim3(nqb * Hk * ((p.G + 3) / 4)),
                         dim3(64 * 8), st, p, nqb, (p.G + 3) / 4, Hk);
     const int nslice = (p.G + 7) / 8;
     // 8-head blocks keep 4 PV waves (2 heads each): 8 PV waves (one head
@@ -1139,7 +1170,7 @@ static hipError_t launch_pf_ws_t(const GqaPrefillParams& p, int Hk, hipStream_t 
     // and softmax phases); two heads per S wave, which halves the K reads
     // per row, measured slower (859 against 804 us at 7B N = 8192)
     constexpr int SMB = 1;
-    return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 8, SMB, NPV, DT, OUT_DT, PAD>, dim3(nqb * Hk * nslice),
+    return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 8, SMB, NPV, DT, OUT_DT, PAD, kWsTps<DT>>, dim3(nqb * Hk * nslice),
                     dim3(64 * (8 / SMB + NPV)), st, p, nqb, nslice, Hk);
 }
 

@@ -135,7 +135,10 @@ def test_bf16_v_prepass(device, kernel):
     c1 = C.prefill_case(72, 2100, 28, 4, 128, 0, C.BF16)
     ref = C.O.gqa_prefill(c1["q"][:n], c1["k"][:n], c1["v"][:n], n, 28, 4, 128, n, 0, nthreads=16)
     C.assert_close(with_ws.cpu().numpy()[:n], ref, "bf16 prefill with the fp16 V copy")
-    assert torch.allclose(with_ws, without, atol=1e-5, rtol=1e-5)
+    C.assert_close(without.cpu().numpy()[:n], ref, "bf16 prefill converting V on chip")
+    if kernel == _capi.PREFILL_KERNEL_BLOCK:
+        # same tiles either way: only where V is converted differs
+        assert torch.allclose(with_ws, without, atol=1e-5, rtol=1e-5)
 
 
 @pytest.mark.parametrize("N,H,Hk,start,dtype,causal", [
