@@ -1152,7 +1152,12 @@ static hipError_t launch_pf_g(const GqaPrefillParams& p, int Hk, int dt, int out
     return launch_pf_d<D, PAD, 2>(p, Hk, dt, out_dt, st, t);
 }
 
-// tiles per barrier interval of the warp-specialised kernel
+// tiles per barrier interval of the warp-specialised kernel's 8-head
+// blocks: 2 where V arrives as fp16 (Qwen2.5-7B shape N = 2048 52.3 -> 48.5
+// us, N = 8192 619 -> 576). 4-head blocks keep 1: their smaller LDS ring
+// lets two (head_dim 128) or three (64) blocks share a CU, which two tiles
+// per step would halve (H32 Hk8 d128 N = 8192 673 against 805 us, d64
+// 400 against 429)
 template <int DT>
 constexpr int kWsTps = DT == DT_BF16 ? 1 : 2;
 
@@ -1160,7 +1165,7 @@ template <int D, bool PAD, int DT, int OUT_DT>
 static hipError_t launch_pf_ws_t(const GqaPrefillParams& p, int Hk, hipStream_t st, KernelTimer* t) {
     const int nqb = (p.N + 15) / 16;
     if (p.G <= 4)
-        return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 4, 1, 4, DT, OUT_DT, PAD, kWsTps<DT>>, dim3(nqb * Hk * ((p.G + 3) / 4)),
+        return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 4, 1, 4, DT, OUT_DT, PAD, 1>, dim3(nqb * Hk * ((p.G + 3) / 4)),
                         dim3(64 * 8), st, p, nqb, (p.G + 3) / 4, Hk);
     const int nslice = (p.G + 7) / 8;
     // 8-head blocks keep 4 PV waves (2 heads each): 8 PV waves (one head
