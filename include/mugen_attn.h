@@ -214,7 +214,8 @@ int mugen_attn_gqa_decode_q4(const mugen_attn_gqa_decode_q4_args* args, void* wo
  * With BF16 inputs the kernels may compute P.V in fp16 (V converted on
  * chip, exact inside the f16 range), so BF16 V values must lie
  * within +-65504 -- the range of the reference's f16 cache; V magnitudes
- * below 6.1e-5 keep an absolute precision of 2^-25.  No workspace.
+ * below 6.1e-5 keep an absolute precision of 2^-25.  The optional
+ * workspace (below) holds an fp16 copy of BF16 V for long prompts.
  */
 typedef struct mugen_attn_gqa_prefill_args {
     const void* q;

@@ -674,8 +674,11 @@ public:
         m.latent = a->lat_[0].ptr;
         m.seq_lens = a->lengths_after();
         size_t ws = mla_decode_workspace_size(m);
-        if (s.max_prefill > 0) {
-            mugen_attn_mla_decode_args pm = a->core_args(0, 1, s.max_prefill, a->lengths_after());
+        // prompt chunks: the split planner gives shorter chunks more splits,
+        // so a shorter chunk can need more workspace than max_prefill tokens
+        // do -- size for every chunk length (a host-side loop over the planner)
+        for (int n = 1; n <= s.max_prefill; n++) {
+            mugen_attn_mla_decode_args pm = a->core_args(0, 1, n, a->lengths_after());
             pm.q = pm.out = a->qabs_.ptr;
             pm.latent = a->lat_[0].ptr;
             ws = std::max(ws, mla_decode_workspace_size(pm));

@@ -20,7 +20,7 @@ E_HIP = -4
 F32, F16, BF16 = 0, 1, 2
 W_F16, W_Q4_0, W_Q8_0 = 1, 2, 8  # weight encodings (GGML type ids)
 MLA_KERNEL_ROWS, MLA_KERNEL_WS = 1, 2  # mugen_attn_mla_decode_args.kernel
-PREFILL_KERNEL_BLOCK, PREFILL_KERNEL_WS, PREFILL_KERNEL_SHORT = 1, 2, 3  # mugen_attn_gqa_prefill_args.kernel
+PREFILL_KERNEL_AUTO, PREFILL_KERNEL_BLOCK, PREFILL_KERNEL_WS, PREFILL_KERNEL_SHORT = 0, 1, 2, 3  # mugen_attn_gqa_prefill_args.kernel
 MLA_SCRATCH_BYTES = 32 << 20  # MUGEN_ATTN_MLA_SCRATCH_BYTES: the fixed scratch of mugen_attn_mla_decode_noalloc
 
 # every symbol include/mugen_attn.h declares
@@ -152,11 +152,20 @@ class MugenAttnError(RuntimeError):
 _lib = None
 
 
-def lib() -> ctypes.CDLL:
+def load(path: str) -> ctypes.CDLL:
+    """Load the library from an explicit path instead of the in-tree build
+    (side-by-side comparisons of two builds); must precede any other call."""
+    global _lib
+    if _lib is not None:
+        raise RuntimeError("libmugen_attn is already loaded")
+    return lib(path)
+
+
+def lib(path: str | None = None) -> ctypes.CDLL:
     """Load libmugen_attn.so; raise if it has not been built."""
     global _lib
     if _lib is None:
-        path = os.environ.get("MUGEN_ATTN_LIB", LIB_PATH)  # alternative build (kernel comparisons)
+        path = LIB_PATH if path is None else path
         if not os.path.exists(path):
             raise ImportError(
                 f"{path} not found: build it with `python -m mugen_amd.build` "

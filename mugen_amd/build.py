@@ -70,20 +70,25 @@ def build(verbose: bool = False) -> str:
 SELFTEST = os.path.join(HERE, "engine_selftest")
 
 
-def build_selftest(verbose: bool = False) -> str:
-    """The C++ provider check (engine_selftest.cpp, run by the GPU tests),
-    linked against the in-tree library."""
-    tmp = SELFTEST + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-O2", "-std=c++20", "-I", INCLUDE,
-           os.path.join(HERE, "engine_selftest.cpp"), "-o", tmp, "-L", HERE, "-lmugen_attn",
-           "-Wl,-rpath,$ORIGIN", "-Wno-unused-command-line-argument"]
+def build_program(src: str, exe: str, verbose: bool = False) -> str:
+    """A host program over the provider header (include/mugen_attn_engine.hpp),
+    linked against the in-tree library (rpath relative to the program)."""
+    tmp = exe + ".tmp"
+    rel = os.path.relpath(HERE, os.path.dirname(os.path.abspath(exe)))
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-O2", "-std=c++20", "-I", INCLUDE, src, "-o", tmp,
+           "-L", HERE, "-lmugen_attn", "-Wl,-rpath,$ORIGIN/" + rel, "-Wno-unused-command-line-argument"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"engine_selftest build failed:\n{r.stderr}")
-    os.replace(tmp, SELFTEST)
+        raise RuntimeError(f"{os.path.basename(src)} build failed:\n{r.stderr}")
+    os.replace(tmp, exe)
     if verbose:
-        print(f"built {SELFTEST}")
-    return SELFTEST
+        print(f"built {exe}")
+    return exe
+
+
+def build_selftest(verbose: bool = False) -> str:
+    """The C++ provider check (engine_selftest.cpp, run by the GPU tests)."""
+    return build_program(os.path.join(HERE, "engine_selftest.cpp"), SELFTEST, verbose)
 
 
 if __name__ == "__main__":

@@ -735,6 +735,24 @@ void bounds_test(hipStream_t st) {
         failures++;
     }
     ok(ma->set_lengths({59, 0}, st), "mla set_lengths max - q_len");
+    // prompt chunks shorter than max_prefill get more splits from the
+    // planner; the workspace sized at create() serves every chunk length
+    mugen_attn::MlaShape p;
+    p.n_layers = 1;
+    p.batch = 1;
+    p.n_heads = 16;
+    p.max_seq_len = 8192;
+    p.max_prefill = 300;
+    std::unique_ptr<mugen_attn::MlaAttention> pa;
+    if (!ok(mugen_attn::MlaAttention::create(p, &pa), "create mla prompt provider")) return;
+    Dev norm(512 * 2), wk((size_t)16 * 128 * 512 * 2), wv(wk.n), pq((size_t)300 * 16 * 192 * 2), pkv(300 * 576 * 2),
+        pout((size_t)300 * 16 * 128 * 2);
+    for (Dev* d : {&norm, &wk, &wv, &pq, &pkv}) hip(hipMemsetAsync(d->p, 0, d->n, st), "zero");
+    const mugen_attn::MlaLayerWeights w{norm.p, wk.p, wv.p, MUGEN_ATTN_W_F16};
+    for (int n : {1, 64, 256, 300})
+        if (!ok(pa->prefill_layer(0, 0, w, pq.p, pkv.p, pout.p, n, st), "mla prompt chunk shorter than max_prefill"))
+            std::printf("  (chunk of %d tokens)\n", n);
+    hip(hipStreamSynchronize(st), "sync");
     std::printf("length bounds done\n");
 }
 

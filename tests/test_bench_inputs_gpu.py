@@ -6,7 +6,8 @@ as bench.py builds it (seeded torch draws, its context lengths), run once,
 and compared with the CPU oracle on the same bytes.  So the numbers bench.py
 reports come from inputs whose results are parity-checked.  (The two longest
 prefill workloads are checked on their first 1024 query tokens, which the
-causal mask makes independent of the rest.)"""
+causal mask makes independent of the rest, and on their last 128 query
+tokens, which see every key.)"""
 import numpy as np
 import pytest
 import torch
@@ -105,6 +106,12 @@ def test_prefill_workloads(device, name, N, H, Hk, D, seed):
     n = min(N, 1024)  # causal: the first n rows depend on the first n keys only
     ref = O.gqa_prefill(_f32(c.q[:n]), _f32(c.k[:n]), _f32(c.v[:n]), n, H, Hk, D, n, 0, nthreads=16)
     C.assert_close(_f32(c.out[:n]), ref, name)
+    if N > n:
+        # the last 128 rows see every key: the start-offset form of the oracle
+        # (row i of the tail is query N-128+i over keys [0, N-128+i])
+        t = 128
+        ref = O.gqa_prefill(_f32(c.q[N - t:]), _f32(c.k[:N]), _f32(c.v[:N]), t, H, Hk, D, N, N - t, nthreads=16)
+        C.assert_close(_f32(c.out[N - t:]), ref, name + " last 128 rows")
 
 
 @pytest.mark.parametrize("name", ["mla_layer_v3_q8_0", "mla_layer_prefill_v2lite_n512"])

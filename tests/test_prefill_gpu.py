@@ -187,3 +187,18 @@ def test_climbing_scores_rebase(device, kernel, D):
     c["q"], c["qb"] = C.O.round_to(q, C.BF16)
     c["k"], c["kb"] = C.O.round_to(k, C.BF16)
     C.assert_close(run_gpu(c, device, C.F32, kernel=kernel), C.prefill_ref(c), f"climbing scores D={D} kernel={kernel}")
+
+
+@pytest.mark.parametrize("N", [2048, 8192])
+@pytest.mark.parametrize("kernel", [_capi.PREFILL_KERNEL_AUTO, _capi.PREFILL_KERNEL_BLOCK, _capi.PREFILL_KERNEL_WS])
+def test_long_range_tail(device, N, kernel):
+    # the 7B prompt lengths: the last 128 query rows see all N keys, so ring
+    # slots, offsets and re-base accumulation over N/64 key tiles are compared
+    # with the oracle's start-offset form (query N-128+i over keys [0, N-128+i])
+    H, Hk, D, t = 28, 4, 128, 128
+    c = C.prefill_case(80 + N // 1024, N, H, Hk, D, 0, C.BF16)
+    got = run_gpu(c, device, C.F32, kernel=kernel)
+    ref = C.O.gqa_prefill(c["q"][N - t:], c["k"], c["v"], t, H, Hk, D, N, N - t, nthreads=16)
+    C.assert_close(got[N - t:], ref, f"prefill tail N={N} kernel={kernel}")
+    head = C.O.gqa_prefill(c["q"][:64], c["k"][:64], c["v"][:64], 64, H, Hk, D, 64, 0, nthreads=16)
+    C.assert_close(got[:64], head, f"prefill head N={N} kernel={kernel}")
