@@ -889,8 +889,18 @@ __global__ __launch_bounds__(512) void gqa_prefill_short_kernel(GqaPrefillParams
     __shared__ float2 mlx[8][MBW][16];          // per wave, head, row: (max, sum) of its range
     __shared__ __attribute__((aligned(16))) char qlds[4 * 16 * RB];  // q rows [head slot][token]
 
-    const int qb = gridDim.x - 1 - blockIdx.x;  // longest rows first
-    const int kvh = blockIdx.y;
+    // XCD-aware mapping: workgroups are dealt to the 8 XCDs round-robin by
+    // blockIdx, and units (kv head-major: unit = kvh * nqb + i) go to the XCDs
+    // in contiguous ranges, so the blocks of one kv head share one XCD's L2
+    // for its K / V rows (Hk = 8: one kv head per XCD) instead of every XCD
+    // fetching every head; within a range the longest rows go first
+    const int nqb = (p.N + 15) / 16;
+    const int units = nqb * (p.H / p.G);  // x kv heads
+    const int upx = (units + 7) / 8;
+    const int slot = blockIdx.x / 8, unit = (blockIdx.x % 8) * upx + slot;
+    if (slot >= upx || unit >= units) return;
+    const int kvh = unit / nqb;
+    const int qb = nqb - 1 - (unit - kvh * nqb);  // longest rows first
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kr = w & 3, rh = w >> 2;          // key range, head pair
@@ -1215,7 +1225,9 @@ static hipError_t launch_pf_ws(const GqaPrefillParams& p, int Hk, int dt, int ou
 
 template <int DT>
 static hipError_t launch_pf_short(const GqaPrefillParams& p, int Hk, int out_dt, hipStream_t st, KernelTimer* t) {
-    dim3 grid((p.N + 15) / 16, Hk);
+    // a 1-D deal of (kv head, query block) units over the XCDs (see the kernel)
+    const int units = (p.N + 15) / 16 * Hk;
+    const dim3 grid(8 * ((units + 7) / 8));
     if (out_dt == DT_F32) return launch_k(t, "gqa_prefill", gqa_prefill_short_kernel<DT, DT_F32>, grid, dim3(512), st, p);
     if (out_dt == DT_F16) return launch_k(t, "gqa_prefill", gqa_prefill_short_kernel<DT, DT_F16>, grid, dim3(512), st, p);
     return launch_k(t, "gqa_prefill", gqa_prefill_short_kernel<DT, DT_BF16>, grid, dim3(512), st, p);
