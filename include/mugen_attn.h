@@ -81,9 +81,9 @@ typedef enum {
  *            writes past the workspace
  *   num_splits: 0 = automatic; otherwise the context-split count (>= 1)
  *
- * Supported: head_dim a multiple of 8 up to 128 (64 and 128 natively,
- * others on the next of those with the extra dims masked; the 4-bit store
- * entry point takes 64 and 128 only); n_heads / n_kv_heads in [1, 16];
+ * Supported: head_dim a multiple of 8 up to 256 (64, 128 and 256
+ * natively, others on the next of those with the extra dims masked; the
+ * 4-bit store entry point takes 64, 128 and 256 only); n_heads / n_kv_heads in [1, 16];
  * kv_dtype in {F16, BF16} (q has the same dtype); out_dtype F16/BF16/F32.
  */
 typedef struct mugen_attn_gqa_decode_args {
@@ -207,7 +207,9 @@ int mugen_attn_gqa_decode_q4(const mugen_attn_gqa_decode_q4_args* args, void* wo
  *   token i attends to keys [0, start_pos + i]   (kernel_sources.h:2796)
  *   causal = 0 lets every token see all kv_len keys.
  *
- * Supported: head_dim a multiple of 8 up to 128 (as gqa_decode);
+ * Supported: head_dim a multiple of 8 up to 256 (as gqa_decode; above 128
+ * every query token attends in its own workgroup, the reference's per-token
+ * CPU rule, and only kernel 0 is accepted);
  * n_heads / n_kv_heads in [1, 16] (more
  * than 8 runs on the warp-specialised kernel; forcing the per-block kernel
  * there is refused); dtype F16 or BF16 for q/k/v; out_dtype F16/BF16/F32.

@@ -68,8 +68,8 @@ struct PathChoice {
 // The provider that gives the reference's results for this model.  An MLA
 // model ignores the override, as the reference does (its MLA branch never
 // reads use_gpu_attention_).  `supported` is false for shapes the kernels do
-// not cover (head_dim not a multiple of 8 or above 128 -- only 64 / 128 for
-// the 4-bit store --, more than 16 query heads per KV head, MLA dims other
+// not cover (head_dim not a multiple of 8 or above 256 -- only 64 / 128 /
+// 256 for the 4-bit store --, more than 16 query heads per KV head, MLA dims other
 // than 512 / 64 / 128 / 128); the engine keeps the
 // reference's CPU attention for those.
 inline PathChoice select_attention_path(const ModelAttentionConfig& c,
@@ -96,12 +96,12 @@ inline PathChoice select_attention_path(const ModelAttentionConfig& c,
         r.reason = "n_heads must be a positive multiple of n_kv_heads";
         return r;
     }
-    // f16 caches: head_dim a multiple of 8 up to 128; the 4-bit store: 64, 128
-    const bool hd_ok = gpu ? (c.head_dim >= 8 && c.head_dim <= 128 && c.head_dim % 8 == 0)
-                           : (c.head_dim == 64 || c.head_dim == 128);
+    // f16 caches: head_dim a multiple of 8 up to 256; the 4-bit store: 64, 128, 256
+    const bool hd_ok = gpu ? (c.head_dim >= 8 && c.head_dim <= 256 && c.head_dim % 8 == 0)
+                           : (c.head_dim == 64 || c.head_dim == 128 || c.head_dim == 256);
     if (!hd_ok) {
         r.reason = "head_dim " + std::to_string(c.head_dim) +
-                   (gpu ? " (supported: multiples of 8 up to 128)" : " (4-bit store: 64, 128)");
+                   (gpu ? " (supported: multiples of 8 up to 256)" : " (4-bit store: 64, 128, 256)");
         return r;
     }
     if (c.n_heads / c.n_kv_heads > 16) {

@@ -183,7 +183,9 @@ static int gqa_chunk(const mugen_attn_gqa_decode_args* a, int extra = 0) {
     if (a->num_splits > 0) return explicit_chunk(maxT, a->num_splits, q, kMaxSplits - 1);
     const int cmax = ceil_div(maxT, q) * q;
     const int cmin = ceil_div(ceil_div(maxT, kMaxSplits - 1), q) * q;
-    const int64_t budget = 512;
+    // one dispatch round: two workgroups per CU, one at head_dim 256 (one
+    // wave per SIMD)
+    const int64_t budget = a->head_dim > 128 ? 256 : 512;
     if (gqa_items(a, cmax, extra) > budget) return cmax;  // one split per sequence already fills a round
     int lo = cmin < qmin ? qmin : cmin, hi = cmax;        // items(c) is non-increasing in c
     while (lo < hi) {
@@ -208,10 +210,10 @@ static int gqa_validate(const mugen_attn_gqa_decode_args* a, bool ring_store = f
     if (a->n_heads / a->n_kv_heads > 16)
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode: n_heads/n_kv_heads = %d > 16",
                     a->n_heads / a->n_kv_heads);
-    if (ring_store ? (a->head_dim != 64 && a->head_dim != 128)
-                   : (a->head_dim < 8 || a->head_dim > 128 || a->head_dim % 8))
+    if (ring_store ? (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
+                   : (a->head_dim < 8 || a->head_dim > 256 || a->head_dim % 8))
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "%s: head_dim %d (supported: %s)", ring_store ? "gqa_decode_q4" : "gqa_decode",
-                    a->head_dim, ring_store ? "64, 128" : "multiples of 8 up to 128");
+                    a->head_dim, ring_store ? "64, 128, 256" : "multiples of 8 up to 256");
     if (!is16(a->kv_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode: kv_dtype must be F16 or BF16");
     if (!is_out(a->out_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_decode: bad out_dtype");
     if (!ring_store && a->batch > 1 && a->seq_stride < (int64_t)a->max_seq_len * a->n_kv_heads * a->head_dim)
@@ -224,10 +226,10 @@ static int gqa_validate(const mugen_attn_gqa_decode_args* a, bool ring_store = f
     return MUGEN_ATTN_OK;
 }
 
-// The decode and prefill kernels are built for head_dim 64 and 128; a
-// smaller head_dim (a multiple of 8) runs on the next one up, its extra
-// dims masked (q zero, outputs not stored).
-static int padded_head_dim(int head_dim) { return head_dim <= 64 ? 64 : 128; }
+// The decode and prefill kernels are built for head_dim 64 and 128 (decode
+// also 256); a smaller head_dim (a multiple of 8) runs on the next one up,
+// its extra dims masked (q zero, outputs not stored).
+static int padded_head_dim(int head_dim) { return head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256; }
 
 // workspace: fp32 partials [B][H][splits][D] and (m, l) [B][H][splits][2]
 // (D = the padded head_dim)
@@ -544,8 +546,8 @@ static int gqa_prefill_validate(const mugen_attn_gqa_prefill_args* a) {
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: n_heads/n_kv_heads > 16");
     if (a->n_heads / a->n_kv_heads > 8 && a->kernel == MUGEN_ATTN_PREFILL_KERNEL_BLOCK)
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: the per-block kernel serves at most 8 heads per kv head");
-    if (a->head_dim < 8 || a->head_dim > 128 || a->head_dim % 8)
-        return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: head_dim %d (supported: multiples of 8 up to 128)",
+    if (a->head_dim < 8 || a->head_dim > 256 || a->head_dim % 8)
+        return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: head_dim %d (supported: multiples of 8 up to 256)",
                     a->head_dim);
     if (!is16(a->dtype) || !is_out(a->out_dtype)) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: dtype");
     if (a->kernel < 0 || a->kernel > MUGEN_ATTN_PREFILL_KERNEL_SHORT)
@@ -579,6 +581,36 @@ size_t mugen_attn_gqa_prefill_workspace_size(const mugen_attn_gqa_prefill_args* 
 int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     if (int rc = gqa_prefill_validate(a)) return rc;
     if (a->n_tokens == 0) return MUGEN_ATTN_OK;
+    if (a->head_dim > 128) {
+        // head_dim 129..256: the per-token rule of the reference's CPU path
+        // (query i of the prompt attends over start_pos + i + 1 keys,
+        // transformer.cpp:1334-1335) on the decode kernel's prompt mode, one
+        // (token, kv head) per workgroup over the shared cache
+        if (a->kernel) return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: head_dim > 128 has one kernel (kernel 0)");
+        GqaDecodeParams d{};
+        d.B = a->n_tokens;
+        d.Hk = a->n_kv_heads;
+        d.q = static_cast<const uint16_t*>(a->q);
+        d.k = static_cast<const uint16_t*>(a->k);
+        d.v = static_cast<const uint16_t*>(a->v);
+        d.out = a->out;
+        d.H = a->n_heads;
+        d.G = a->n_heads / a->n_kv_heads;
+        d.hd = a->head_dim;
+        d.row_stride = a->n_kv_heads * a->head_dim;
+        d.chunk = a->kv_len;
+        d.num_splits = 1;
+        d.seq_stride = 0;
+        d.scale_log2 = (a->scale > 0.f ? a->scale : 1.f / sqrtf((float)a->head_dim)) * kLog2e;
+        d.max_T = a->kv_len;
+        d.pf_start = a->start_pos;
+        d.pf_causal = a->causal ? 1 : 0;
+        if ((int64_t)a->n_tokens * a->n_kv_heads > INT32_MAX)
+            return fail(MUGEN_ATTN_E_UNSUPPORTED, "gqa_prefill: n_tokens * n_kv_heads too large");
+        return hip_status(launch_gqa_prefill_wide(d, a->dtype, a->out_dtype, static_cast<hipStream_t>(stream),
+                                                  active_timer()),
+                          "gqa_prefill launch");
+    }
     GqaPrefillParams p{};
     p.q = static_cast<const uint16_t*>(a->q);
     p.k = static_cast<const uint16_t*>(a->k);

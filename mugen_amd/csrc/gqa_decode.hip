@@ -85,8 +85,11 @@ __device__ __forceinline__ int splits_of(const GqaDecodeParams& p, int j) {
 
 // two waves per SIMD (the planner sizes the grid for two workgroups per CU)
 // PAD: head_dim p.hd < D (dims past it masked); otherwise p.hd == D
-template <int D, int DT, int OUT_DT, bool Q4 = false, bool PAD = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gqa_decode_kernel(GqaDecodeParams p) {
+// (head_dim 256: one wave per SIMD, so that its operands fit in registers).
+// PF: prompt mode (see GqaDecodeParams::pf_start).
+template <int D, int DT, int OUT_DT, bool Q4 = false, bool PAD = false, bool PF = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2))) void gqa_decode_kernel(
+    GqaDecodeParams p) {
     constexpr int KK = D / 32;           // MFMA k-steps of S
     constexpr int DB = D / 16;           // 16-dim blocks of O^T
     constexpr int RB = 2 * D;            // bytes per staged V row
@@ -107,6 +110,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     // items -- go to one XCD (workgroups are dealt to the 8 XCDs round-robin
     // by blockIdx): item = xcd * per_xcd + slot
     const int item = (Q4 && p.per_xcd > 0) ? (int)(blockIdx.x % 8) * p.per_xcd + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+    if constexpr (PF) {  // prompt mode: one split per (token, kv head)
+        if (item < p.B * p.Hk) {
+            b = item / p.Hk;
+            kvh = item - b * p.Hk;
+        }
+    } else
     for (int j = 0, r = item; j < p.B; j++) {  // uniform scalar loop over the batch
         const int nsj = splits_of<Q4>(p, j);
         if (r < nsj * p.Hk) {
@@ -120,7 +129,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     if (b < 0) return;  // grid padding (sized from an upper bound)
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
-    const int T = clamp_len(p.seq_lens[b], p.max_T);
+    const int T = PF ? (p.pf_causal ? min(p.pf_start + b + 1, p.max_T) : p.max_T) : clamp_len(p.seq_lens[b], p.max_T);
     // 4-bit store: the Q4 tokens [0, n_q4) and the f16 ring tokens
     // [n_q4, T) are split separately, so a split -- and every 32-token block
     // of it -- holds one kind only (Q4 splits first)
@@ -202,10 +211,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         constexpr bool QB = decltype(qb_tag)::value;
         if constexpr (QB) {
             // K: kq[nb][0] = the lane's 4*KK nibble bytes, kq[nb][1][0] = (scale|min)
+            // (head_dim 256: the lane's 64 dims are two groups, the second in
+            // kq[nb][2] / kq[nb][3][0])
             const int d0 = 8 * KK * g;
 #pragma unroll
             for (int nb = 0; nb < 2; nb++) {
                 const int tk = min(t0 + kr0 + 4 * nb, t_end - 1);
+                if constexpr (KK == 8) {
+#pragma unroll
+                    for (int h2 = 0; h2 < 2; h2++) {
+                        const int off = q4_off(tk, 2 * g + h2);
+                        kq[nb][2 * h2] = __builtin_amdgcn_raw_buffer_load_b128(rq4k, off + 4, 0, 0);
+                        kq[nb][2 * h2 + 1][0] = __builtin_amdgcn_raw_buffer_load_b32(rq4k, off, 0, 0);
+                    }
+                    continue;
+                }
                 const int off = q4_off(tk, d0 >> 5);
                 const int noff = off + 4 + ((d0 & 31) >> 1);
                 if constexpr (KK == 4) {
@@ -272,6 +292,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         if constexpr (decltype(qb_tag)::value) {
 #pragma unroll
             for (int nb = 0; nb < 2; nb++) {
+                if constexpr (KK == 8) {
+                    const u32x4_t nib0 = kq[nb][0], nib1 = kq[nb][2];
+                    const uint32_t sm0 = kq[nb][1][0], sm1 = kq[nb][3][0];
+#pragma unroll
+                    for (int kk = 0; kk < KK; kk++)
+                        kq[nb][kk] = dequant_q4x8(kk < 4 ? sm0 : sm1, kk < 4 ? nib0[kk] : nib1[kk - 4]);
+                    continue;
+                }
                 const u32x4_t nib = kq[nb][0];
                 const uint32_t sm = kq[nb][1][0];
 #pragma unroll
@@ -540,8 +568,32 @@ static hipError_t launch_gqa_g(const GqaDecodeParams& p, int nwg, int kv_dt, int
 
 hipError_t launch_gqa_decode(const GqaDecodeParams& p, int nwg, int D, int kv_dt, int out_dt, hipStream_t st,
                              KernelTimer* t) {
+    if (D == 256) return launch_gqa_g<256>(p, nwg, kv_dt, out_dt, st, t);
     if (D == 128) return launch_gqa_g<128>(p, nwg, kv_dt, out_dt, st, t);
     return launch_gqa_g<64>(p, nwg, kv_dt, out_dt, st, t);
+}
+
+// prompt mode at head_dim 129..256 (one split per item: no combine)
+template <int DT, int OUT_DT>
+static hipError_t launch_pf_wide_t(const GqaDecodeParams& p, hipStream_t st, KernelTimer* t) {
+    const dim3 grid(p.B * p.Hk);
+    if (p.hd != 256)
+        return launch_k(t, "gqa_prefill", gqa_decode_kernel<256, DT, OUT_DT, false, true, true>, grid, dim3(256), st, p);
+    return launch_k(t, "gqa_prefill", gqa_decode_kernel<256, DT, OUT_DT, false, false, true>, grid, dim3(256), st, p);
+}
+
+template <int DT>
+static hipError_t launch_pf_wide_o(const GqaDecodeParams& p, int out_dt, hipStream_t st, KernelTimer* t) {
+    switch (out_dt) {
+        case DT_F32: return launch_pf_wide_t<DT, DT_F32>(p, st, t);
+        case DT_F16: return launch_pf_wide_t<DT, DT_F16>(p, st, t);
+        default: return launch_pf_wide_t<DT, DT_BF16>(p, st, t);
+    }
+}
+
+hipError_t launch_gqa_prefill_wide(const GqaDecodeParams& p, int kv_dt, int out_dt, hipStream_t st, KernelTimer* t) {
+    if (kv_dt == DT_F16) return launch_pf_wide_o<DT_F16>(p, out_dt, st, t);
+    return launch_pf_wide_o<DT_BF16>(p, out_dt, st, t);
 }
 
 // 4-bit store: f16 values (the reference's format), fp16 MFMA
@@ -555,6 +607,7 @@ static hipError_t launch_gqa_q4_d(const GqaDecodeParams& p, int nwg, int out_dt,
 }
 
 hipError_t launch_gqa_decode_q4(const GqaDecodeParams& p, int nwg, int D, int out_dt, hipStream_t st, KernelTimer* t) {
+    if (D == 256) return launch_gqa_q4_d<256>(p, nwg, out_dt, st, t);
     if (D == 128) return launch_gqa_q4_d<128>(p, nwg, out_dt, st, t);
     return launch_gqa_q4_d<64>(p, nwg, out_dt, st, t);
 }

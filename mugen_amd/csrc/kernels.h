@@ -62,12 +62,20 @@ struct GqaDecodeParams {
     int per_xcd;            // 4-bit store: work items per XCD (0: blockIdx order)
     int max_T;              // device lengths are clamped to [0, max_T] (the caches' size)
     int hd;                 // head_dim of the caches, q and out (<= D, a multiple of 8)
+    // prompt mode (the PF instantiation, head_dim above 128): item b is
+    // query token b of one prompt over a single cache (seq_stride 0, one
+    // split); it sees pf_start + b + 1 keys if pf_causal, else max_T
+    int pf_start;
+    int pf_causal;
 };
 
 // nwg: workgroups of the compact work list (exact, or an upper bound)
 hipError_t launch_gqa_decode(const GqaDecodeParams& p, int nwg, int D, int kv_dt, int out_dt, hipStream_t st,
                              KernelTimer* t);
 hipError_t launch_gqa_decode_q4(const GqaDecodeParams& p, int nwg, int D, int out_dt, hipStream_t st, KernelTimer* t);
+// a prompt at head_dim 129..256 through the decode kernel's prompt mode
+// (p.B = query tokens, one split, p.pf_start / p.pf_causal set)
+hipError_t launch_gqa_prefill_wide(const GqaDecodeParams& p, int kv_dt, int out_dt, hipStream_t st, KernelTimer* t);
 
 // 4-bit group store append (kv_q4.hip)
 struct KvQ4AppendParams {

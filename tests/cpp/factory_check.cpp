@@ -10,7 +10,7 @@
 // ("name dtype dim0 dim1 ...") so that tests/test_factory_gpu.py can compare
 // them with the CPU oracle.
 //
-//   factory_check <out_dir> <config>...     configs: llama1b qwen7b v2lite hk2_d64
+//   factory_check <out_dir> <config>...     configs: llama1b qwen7b v2lite hk2_d64 wide_d256
 //
 // Exit status 0 when every provider was created and every call succeeded.
 #include <hip/hip_runtime.h>
@@ -287,6 +287,8 @@ int main(int argc, char** argv) {
             c.kv_lora_rank = 512, c.qk_rope_head_dim = 64, c.qk_nope_head_dim = 128, c.v_head_dim = 128;
             lim.rope = mugen_attn_rope_params{10000.f, 40.f, 4096};
             prompt = {150, 20};
+        } else if (name == "wide_d256") {  // head_dim 256 (Gemma-style), 8 KV heads -> GqaAttention
+            c.n_heads = 16, c.n_kv_heads = 8, c.head_dim = 256;
         } else if (name == "hk2_d64") {  // 2 KV heads, d 64 -> GqaAttentionQ4 (cpu_attention path)
             c.n_heads = 16, c.n_kv_heads = 2, c.head_dim = 64;
         } else {

@@ -42,6 +42,16 @@ int main() {
     small_kv.n_heads = 16;
     small_kv.n_kv_heads = 2;
     small_kv.head_dim = 64;
+    ModelAttentionConfig wide;  // head_dim 256 (Gemma-style), 8 KV heads
+    wide.n_heads = 16;
+    wide.n_kv_heads = 8;
+    wide.head_dim = 256;
+    ModelAttentionConfig wide_kv2 = wide;  // head_dim 256 with 2 KV heads: the 4-bit store
+    wide_kv2.n_kv_heads = 2;
+    ModelAttentionConfig odd = wide;  // head_dim 160: padded to 256 on f16 caches
+    odd.head_dim = 160;
+    ModelAttentionConfig huge = wide;  // head_dim 512: beyond the kernels
+    huge.head_dim = 512;
     ModelAttentionConfig moe = qwen7b;  // a GQA MoE model: same attention as dense
     moe.is_moe = true;
     show("llama1b", llama1b);
@@ -51,6 +61,11 @@ int main() {
     show("tiny", tiny);
     show("small_kv", small_kv);
     show("moe", moe);
+    show("wide", wide);
+    show("wide_kv2", wide_kv2);
+    show("odd", odd);
+    show("odd_kv_off", odd, GpuAttentionOverride::Off);
+    show("huge", huge);
     show("qwen7b_off", qwen7b, GpuAttentionOverride::Off);
     show("small_kv_on", small_kv, GpuAttentionOverride::On);
     show("tiny_on", tiny, GpuAttentionOverride::On);

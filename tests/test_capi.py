@@ -46,7 +46,7 @@ def _call_gqa(a, ws=None, nbytes=0):
     (dict(q=0), _capi.E_INVALID),
     (dict(n_heads=30), _capi.E_INVALID),          # not a multiple of n_kv_heads
     (dict(head_dim=100), _capi.E_UNSUPPORTED),    # not a multiple of 8
-    (dict(head_dim=136), _capi.E_UNSUPPORTED),    # above 128
+    (dict(head_dim=264), _capi.E_UNSUPPORTED),    # above 256
     (dict(n_heads=68, n_kv_heads=4), _capi.E_UNSUPPORTED),  # G = 17 > 16
     (dict(kv_dtype=_capi.F32), _capi.E_UNSUPPORTED),
     (dict(batch=2, seq_stride=10), _capi.E_INVALID),
@@ -106,7 +106,7 @@ def test_prefill_rejects_bad_args():
     assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.E_INVALID  # kv_len < N
     a.kv_len, a.head_dim = 512, 84   # not a multiple of 8
     assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.E_UNSUPPORTED
-    a.head_dim = 256
+    a.head_dim = 264  # above 256
     assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.E_UNSUPPORTED
     a.head_dim, a.n_tokens = 64, 0
     assert _capi.lib().mugen_attn_gqa_prefill(ctypes.byref(a), None) == _capi.OK  # nothing to do

@@ -13,6 +13,7 @@ output; this file rebuilds the caches from those inputs and runs the oracle:
   * 16/2 heads, d64 -> GqaAttentionQ4 (the reference's cpu_attention over
     its 4-bit KVCache): the same, decode reading tokens older than the
     newest 256 through the 4-bit groups (kv_cache.cpp:218-278);
+  * 16/8 heads at head_dim 256 -> GqaAttention (the 256-wide kernels);
   * DeepSeek-V2-Lite (MLA, 16 heads) -> MlaAttention: the latent rows written
     by the prompt chunks and steps (RMSNorm + YaRN RoPE), then
     cpu_mla_attention (absorb, core, project) for each decode step."""
@@ -29,7 +30,7 @@ pytestmark = pytest.mark.gpu
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 EXE = os.path.join(ROOT, "tests", "cpp", "factory_check")
 CONFIGS = {"llama1b": "GqaAttention", "qwen7b": "GqaAttention", "hk2_d64": "GqaAttentionQ4",
-           "v2lite": "MlaAttention"}
+           "v2lite": "MlaAttention", "wide_d256": "GqaAttention"}
 PRESERVE = 256  # ProviderLimits::fp16_preserve_last, the reference's KVCacheConfig value
 
 
@@ -62,7 +63,7 @@ def f16(bits):
     return O.bits_to_f32(bits, C.F16)
 
 
-@pytest.mark.parametrize("name", ["llama1b", "qwen7b", "hk2_d64"])
+@pytest.mark.parametrize("name", ["llama1b", "qwen7b", "hk2_d64", "wide_d256"])
 def test_gqa_providers(dumps, name):
     a, meta = load(os.path.join(dumps, name))
     assert meta["path"] == [CONFIGS[name]]

@@ -36,6 +36,11 @@ def choices(tmp_path_factory):
     ("tiny_on", "GqaAttention", True),       # the same model forced onto f16 caches: d 16 runs padded to 64
     ("small_kv", "GqaAttentionQ4", True),    # 2 KV heads at d 64: the 4-bit store provider
     ("moe", "GqaAttention", True),           # MoE layers attend like dense ones
+    ("wide", "GqaAttention", True),          # head_dim 256: the f16-cache kernels' 256 build
+    ("wide_kv2", "GqaAttentionQ4", True),    # head_dim 256, 2 KV heads: the 4-bit store at 256
+    ("odd", "GqaAttention", True),           # head_dim 160: runs padded to 256
+    ("odd_kv_off", "GqaAttentionQ4", False), # the 4-bit store keeps whole 32-value groups per head: 64/128/256
+    ("huge", "GqaAttention", False),         # head_dim 512: beyond every kernel -> the reference's CPU path
     ("qwen7b_off", "GqaAttentionQ4", True),  # set_use_gpu_attention(false)
     ("small_kv_on", "GqaAttention", True),   # set_use_gpu_attention(true)
     ("v2lite_on", "MlaAttention", True),     # MLA ignores the override
