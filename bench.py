@@ -545,13 +545,15 @@ def main():
         line["us_per_layer_step"] = h["us_per_step"]
         kb = head.bytes
         # achieved: algorithmic bytes / (main kernel + split-K combine), the
-        # kernels' own stamped durations; kernel_frac: main kernel alone
+        # kernels' own stamped durations capped by the step time;
+        # kernel_frac: main kernel alone
         ach = kb / (min(h["kernels_us"], h["us_per_step"]) * 1e-6) / 1e9
         line["roofline"] = {"bound": "hbm", "kernel": "mla_decode + mla_decode_combine", "achieved": round(ach, 1),
                             "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4),
                             "traffic": h["traffic"], "kernel_us": h["kernel_us"], "combine_us": h["combine_us"],
                             "kernel_frac": h["kernel_frac"],
-                            "definition": "algorithmic bytes per step / (main kernel + combine) duration"}
+                            "definition": "algorithmic bytes per step / (main kernel + combine) duration, "
+                                          "capped by the replayed step time"}
         if not args.no_cpu:
             full_s, sample = head.cpu_sample()
             line["cpu_baseline"] = {"value": round(head.bytes / full_s / 1e9, 4), "unit": "GB/s", "cores": 1,
