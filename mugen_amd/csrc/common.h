@@ -187,6 +187,20 @@ __device__ __forceinline__ float max_x16(float v) {
 // group, lane i receives element (i % 4) of the 8-byte chunks addressed by
 // lanes 4r + i/4, r = 0..3: with lane (4r + c) pointing at row r, columns
 // [4c, 4c+4) of a row-major 16-bit tile, lane i gets column i of rows 0..3.
+// LDS byte address -> LDS pointer: constant offsets added to the pointer
+// go into the instructions' offset field (one address register per base)
+typedef __attribute__((address_space(3))) char lds_char_t;
+__device__ __forceinline__ const lds_char_t* lds_ptr(uint32_t byte_addr) {
+    return reinterpret_cast<const lds_char_t*>(static_cast<uintptr_t>(byte_addr));
+}
+__device__ __forceinline__ u32x2_t lds_read_tr16(const lds_char_t* p) {
+    typedef short s16x4_t __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) const s16x4_t* lds_s16x4_cptr;
+    const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        const_cast<__attribute__((address_space(3))) s16x4_t*>(reinterpret_cast<lds_s16x4_cptr>(p)));
+    return __builtin_bit_cast(u32x2_t, v);
+}
+
 __device__ __forceinline__ u32x2_t lds_read_tr16(const uint16_t* p) {
     typedef short s16x4_t __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) s16x4_t* lds_s16x4_ptr;

@@ -770,7 +770,7 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             }
             if (j == 0) continue;
             const int jp = j - 1;
-            const char* tile = &ring[(jp % NSLOT) * SLOT];
+            const uint32_t slot_addr = ring_base + (uint32_t)((jp % NSLOT) * SLOT);
             const char* pb = pbuf + (jp & 1) * PB;
             // this wave's heads' P, then the V^T fragments, in flight together
             u32x4_t pf[TPS][HPW][NP];
@@ -782,12 +782,16 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
                     for (int pp = 0; pp < NP; pp++)
                         pf[u][hh][pp] = *reinterpret_cast<const u32x4_t*>(
                             pb + (((u * NS + hb + hh) * NP + pp) * 64 + lane) * 16);
+            // one address register per column block: tile u and the upper
+            // half rows are constant offsets of the instruction
+            const lds_char_t* va[DB];
+#pragma unroll
+            for (int d = 0; d < DB; d++) va[d] = lds_ptr(slot_addr + t_off[d]);
             auto read_v = [&](int u, u32x4_t* vf) {
 #pragma unroll
                 for (int d = 0; d < DB; d++) {
-                    const char* vt = tile + u * MAT + t_off[d];
-                    const u32x2_t lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(vt));
-                    const u32x2_t hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(vt + 4 * RB));
+                    const u32x2_t lo = lds_read_tr16(va[d] + u * MAT);
+                    const u32x2_t hi = lds_read_tr16(va[d] + u * MAT + 4 * RB);
                     vf[d] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
                 }
             };
