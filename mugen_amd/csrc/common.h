@@ -201,6 +201,10 @@ __device__ __forceinline__ u32x2_t lds_read_tr16(const lds_char_t* p) {
     return __builtin_bit_cast(u32x2_t, v);
 }
 
+__device__ __forceinline__ u32x4_t lds_read_b128(const lds_char_t* p) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(p);
+}
+
 __device__ __forceinline__ u32x2_t lds_read_tr16(const uint16_t* p) {
     typedef short s16x4_t __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) s16x4_t* lds_s16x4_ptr;

@@ -560,17 +560,19 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             if (j == 16) MUGEN_TRACE(5);
             if (j == ntiles) break;
             if (!hok[0]) continue;
-            const char* tile = &ring[(j % NSLOT) * SLOT];
+            const uint32_t slot_addr = ring_base + (uint32_t)((j % NSLOT) * SLOT);
             const int kt = j * KS;
-            // block nb of tile u: keys kt + 32u + 8g + 4(nb % 2) + i
+            // block nb of tile u: keys kt + 32u + 8g + 4(nb % 2) + i; one
+            // address register per k-step, the tile and half-block offsets
+            // in the instruction
             constexpr int NB = 2 * TPS;
             u32x4_t af[NB][KK];
 #pragma unroll
-            for (int nb = 0; nb < NB; nb++)
+            for (int kk = 0; kk < KK; kk++) {
+                const lds_char_t* ka = lds_ptr(slot_addr + a_off[kk]);
 #pragma unroll
-                for (int kk = 0; kk < KK; kk++)
-                    af[nb][kk] = *reinterpret_cast<const u32x4_t*>(tile + (nb >> 1) * MAT + a_off[kk] +
-                                                                   (nb & 1) * 4 * RB);
+                for (int nb = 0; nb < NB; nb++) af[nb][kk] = lds_read_b128(ka + (nb >> 1) * MAT + (nb & 1) * 4 * RB);
+            }
             constexpr int NV = 4 * NB;          // scores per lane per head
             float sv[SMB][NV];
 #pragma unroll
