@@ -774,6 +774,11 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             const int jp = j - 1;
             const uint32_t slot_addr = ring_base + (uint32_t)((jp % NSLOT) * SLOT);
             const char* pb = pbuf + (jp & 1) * PB;
+            // the step's re-base flags first: the branch on them then waits
+            // for these reads only, and the MFMAs for their own operands
+            int any_rs = 0;
+#pragma unroll
+            for (int hh = 0; hh < HPW; hh++) any_rs |= resc_x[jp & 1][hb + hh];
             // this wave's heads' P, then the V^T fragments, in flight together
             u32x4_t pf[TPS][HPW][NP];
 #pragma unroll
@@ -805,9 +810,6 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             __builtin_amdgcn_sched_barrier(0);
             // re-base (rare after the first tiles): the factors are read only
             // when one of this wave's heads moved its max (factor 1 otherwise)
-            int any_rs = 0;
-#pragma unroll
-            for (int hh = 0; hh < HPW; hh++) any_rs |= resc_x[jp & 1][hb + hh];
             if (__builtin_amdgcn_readfirstlane(any_rs)) {
 #pragma unroll
                 for (int hh = 0; hh < HPW; hh++) {
