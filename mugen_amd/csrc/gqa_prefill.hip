@@ -1210,7 +1210,8 @@ static hipError_t launch_pf_ws_t(const GqaPrefillParams& p, int Hk, hipStream_t 
     constexpr int NPV = 4;
     // one head per S wave (two S waves per SIMD overlap each other's MFMA
     // and softmax phases); two heads per S wave, which halves the K reads
-    // per row, measured slower (859 against 804 us at 7B N = 8192)
+    // per row, measured slower (859 against 804 us at 7B N = 8192; with two
+    // tiles per step 547 against 541 us)
     constexpr int SMB = 1;
     return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 8, SMB, NPV, DT, OUT_DT, PAD, kWsTps<DT>>, dim3(nqb * Hk * nslice),
                     dim3(64 * (8 / SMB + NPV)), st, p, nqb, nslice, Hk);
