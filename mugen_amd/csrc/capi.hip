@@ -252,16 +252,29 @@ static int mla_kernel(const mugen_attn_mla_decode_args* a) {
     return (R <= 64 && a->q_dtype != DT_F32) ? MUGEN_ATTN_MLA_KERNEL_ROWS : MUGEN_ATTN_MLA_KERNEL_WS;
 }
 
-// Active (sequence, split) groups for a chunk: exact from the host length
-// hint, else the batch * max_seq_len upper bound.
-static int64_t mla_groups(const mugen_attn_mla_decode_args* a, int chunk) {
-    if (!a->seq_lens_host) return (int64_t)a->batch * ceil_div(a->max_seq_len > 0 ? a->max_seq_len : 1, chunk);
-    int64_t g = 0;
+// Work units of the MLA kernels for a chunk (mla_map in mla_decode.hip):
+// the (sequence, split, 64-row block) triples that see at least one key --
+// every block of every split for decode steps, of a causal multi-token
+// step's split s the blocks whose last row sees past s * chunk.  Exact from
+// the host length hint, else an upper bound from max_seq_len (the count
+// grows with the length).
+static int64_t mla_units(const mugen_attn_mla_decode_args* a, int chunk, int64_t nrb) {
+    int64_t u = 0;
     for (int b = 0; b < a->batch; b++) {
-        const int T = std::min(a->seq_lens_host[b], a->max_seq_len);  // the kernels clamp to max_seq_len too
-        g += T > 0 ? ceil_div(T, chunk) : 0;
+        // the kernels clamp device lengths to [0, max_seq_len] too
+        const int T = a->seq_lens_host ? std::min(std::max(a->seq_lens_host[b], 0), a->max_seq_len)
+                                       : std::max(a->max_seq_len, 1);
+        const int ns = T > 0 ? ceil_div(T, chunk) : 0;
+        if (a->q_len == 1) {
+            u += ns * nrb;
+            continue;
+        }
+        for (int s = 0; s < ns; s++) {
+            const int64_t x = (int64_t)s * chunk - T + a->q_len;
+            u += nrb - (x <= 0 ? 0 : std::min<int64_t>(a->n_heads * x / 64, nrb - 1));
+        }
     }
-    return g;
+    return u;
 }
 
 // The MLA kernel runs one 256-thread workgroup per CU (~480 registers per
@@ -278,15 +291,15 @@ static int mla_chunk(const mugen_attn_mla_decode_args* a, int kernel) {
     const int cmax = ceil_div(maxT, q) * q;
     const int cmin = ceil_div(ceil_div(maxT, kMaxMlaSplits), q) * q;
     const int64_t wg_budget = 256;
-    if (nrb * mla_groups(a, cmax) > wg_budget) return cmax;  // one split per sequence already fills a round
-    int lo = cmin < q ? q : cmin, hi = cmax;                 // groups(c) is non-increasing in c
+    if (mla_units(a, cmax, nrb) > wg_budget) return cmax;  // one split per sequence already fills a round
+    int lo = cmin < q ? q : cmin, hi = cmax;               // units(c) is non-increasing in c
     while (lo < hi) {
         const int mid = ((lo + hi) / 2) / q * q;
         if (mid <= lo) break;
-        if (nrb * mla_groups(a, mid) <= wg_budget) hi = mid;
+        if (mla_units(a, mid, nrb) <= wg_budget) hi = mid;
         else lo = mid + q;
     }
-    if (nrb * mla_groups(a, lo) > wg_budget) lo = hi;
+    if (mla_units(a, lo, nrb) > wg_budget) lo = hi;
     return lo;
 }
 
@@ -692,11 +705,11 @@ static int mla_decode_impl(const mugen_attn_mla_decode_args* a, void* ws, size_t
     p.R = a->q_len * a->n_heads;
     p.nrb = ceil_div(p.R, mla_rows_per_block(kernel));
     p.nq = ceil_div(p.R, 16);
-    const int64_t groups = mla_groups(a, chunk);
-    // the kernels number (group, row block) units and the grid in 32 bits
-    if (groups * p.nrb > (int64_t)1 << 30)
+    const int64_t units = mla_units(a, chunk, p.nrb);
+    // the kernels number the work units and the grid in 32 bits
+    if (units > (int64_t)1 << 30)
         return fail(MUGEN_ATTN_E_UNSUPPORTED, "mla_decode: batch * splits * row blocks too large");
-    p.groups = (int)groups;
+    p.units = (int)units;
     p.chunk = chunk;
     p.num_splits = splits;
     p.max_T = a->max_seq_len;

@@ -141,7 +141,7 @@ struct MlaParams {
     int R;                 // q_len * H rows per sequence
     int nrb;               // row blocks per sequence (ceil(R / rows per block))
     int nq;                // 16-row blocks per sequence (ceil(R / 16))
-    int groups;            // active (sequence, split) groups the grid covers (upper bound)
+    int units;             // (sequence, split, row block) work units the grid covers (upper bound)
     int chunk;
     int num_splits;
     int max_T;             // device lengths are clamped to [0, max_T] (the cache's size)

@@ -81,36 +81,91 @@ __device__ __forceinline__ int64_t blob_pair(const MlaParams& p, int b, int s, i
     return ((((int64_t)b * p.num_splits + s) * p.nq + q) * 16 + dp) * 64 + lane;
 }
 
+// First 64-row block of a sequence of T tokens that sees a key of split s.
+// Query row r of a q_len-token step sees T - q_len + r / H + 1 keys, so
+// block rb (rows 64 rb .. 64 rb + 63) sees split s iff (64 rb + 63) / H >=
+// s chunk - T + q_len; the last block, whose last row sees all T keys, sees
+// every split.  Decode steps (q_len 1): every block sees every split.
+__device__ __forceinline__ int mla_rb_first(const MlaParams& p, int T, int s) {
+    const int x = s * p.chunk - T + p.q_len;
+    return x <= 0 ? 0 : min((p.H * x) >> 6, p.nrb - 1);
+}
+
 // XCD-aware work mapping, shared by both kernels.  Workgroups are dealt to
 // the 8 XCDs round-robin by blockIdx.  The work units are the (sequence,
-// split, 64-row block) triples of the ACTIVE splits (sequence j contributes
-// ceil(seq_lens[j] / chunk) splits, in order), numbered group-major: unit =
-// (sequence, split) group * nrb + row block.  Each XCD takes a contiguous
-// range of ceil(units / 8), so the row blocks of a group share one XCD's L2
-// for the latent tiles (a group straddles two XCDs at most at a range
-// boundary), consecutive splits of a sequence share it for the query rows,
-// and every XCD gets an even share, also with fewer groups than XCDs (a long
-// prompt: many row blocks, few splits).  The grid is sized from the host's
-// group count (exact with the length hint, an upper bound without); surplus
-// workgroups exit at once.
+// split, 64-row block) triples that see at least one key: sequence j
+// contributes ceil(seq_lens[j] / chunk) splits, and of split s the blocks
+// from mla_rb_first on (all of them for decode steps; a causal prompt's
+// early blocks see only its first splits).  Units are numbered group-major
+// over the (sequence, split) groups, a group's blocks consecutive.  Each
+// XCD takes a contiguous range of ceil(units / 8), so the row blocks of a
+// group share one XCD's L2 for the latent tiles (a group straddles two XCDs
+// at most at a range boundary), consecutive splits of a sequence share it
+// for the query rows, and every XCD gets an even share, also with fewer
+// groups than XCDs (a long prompt: many row blocks, few splits).  The grid
+// is sized from the host's unit count (exact with the length hint, an upper
+// bound without); surplus workgroups exit at once.
 __device__ __forceinline__ bool mla_map(const MlaParams& p, int& b, int& s, int& rb) {
     const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
-    int nact = 0;
-    for (int j = 0; j < p.B; j++) nact += (clamp_len(p.seq_lens[j], p.max_T) + p.chunk - 1) / p.chunk;  // uniform scalar loop
-    const int units = nact * p.nrb;
+    if (p.q_len == 1) {  // decode: every block of every split
+        int nact = 0;
+        for (int j = 0; j < p.B; j++) nact += (clamp_len(p.seq_lens[j], p.max_T) + p.chunk - 1) / p.chunk;  // uniform scalar loop
+        const int units = nact * p.nrb;
+        const int upx = (units + 7) / 8;
+        const int unit = xcd * upx + slot;
+        if (slot >= upx || unit >= units) return false;
+        const int grp = unit / p.nrb;
+        rb = unit - grp * p.nrb;
+        for (int j = 0, acc = 0; j < p.B; j++) {
+            const int nsj = (clamp_len(p.seq_lens[j], p.max_T) + p.chunk - 1) / p.chunk;
+            if (grp < acc + nsj) {
+                b = j;
+                s = grp - acc;
+                return true;
+            }
+            acc += nsj;
+        }
+        return false;
+    }
+    // causal multi-token step: the splits every block sees (s chunk <=
+    // T - q_len) whole, then the last few from mla_rb_first on
+    auto split_range = [&](int Tj, int& nsj, int& s0) {
+        nsj = (Tj + p.chunk - 1) / p.chunk;
+        s0 = min(nsj, Tj >= p.q_len ? (Tj - p.q_len) / p.chunk + 1 : 0);
+    };
+    int units = 0;  // uniform scalar loops
+    for (int j = 0; j < p.B; j++) {
+        const int Tj = clamp_len(p.seq_lens[j], p.max_T);
+        int nsj, s0;
+        split_range(Tj, nsj, s0);
+        units += s0 * p.nrb;
+        for (int sj = s0; sj < nsj; sj++) units += p.nrb - mla_rb_first(p, Tj, sj);
+    }
     const int upx = (units + 7) / 8;
     const int unit = xcd * upx + slot;
     if (slot >= upx || unit >= units) return false;
-    const int grp = unit / p.nrb;
-    rb = unit - grp * p.nrb;
     for (int j = 0, acc = 0; j < p.B; j++) {
-        const int nsj = (clamp_len(p.seq_lens[j], p.max_T) + p.chunk - 1) / p.chunk;
-        if (grp < acc + nsj) {
+        const int Tj = clamp_len(p.seq_lens[j], p.max_T);
+        int nsj, s0;
+        split_range(Tj, nsj, s0);
+        if (unit < acc + s0 * p.nrb) {
+            const int u = unit - acc;
             b = j;
-            s = grp - acc;
+            s = u / p.nrb;
+            rb = u - s * p.nrb;
             return true;
         }
-        acc += nsj;
+        acc += s0 * p.nrb;
+        for (int sj = s0; sj < nsj; sj++) {
+            const int first = mla_rb_first(p, Tj, sj);
+            if (unit < acc + p.nrb - first) {
+                b = j;
+                s = sj;
+                rb = first + (unit - acc);
+                return true;
+            }
+            acc += p.nrb - first;
+        }
     }
     return false;
 }
@@ -781,7 +836,13 @@ __global__ __launch_bounds__(64 * NW) void mla_decode_combine_kernel(MlaParams p
     const int tid = threadIdx.x, lane = tid & 63, dsub = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
     const int T = clamp_len(p.seq_lens[b], p.max_T);
-    const int nact = min(p.num_splits, (T + p.chunk - 1) / p.chunk);
+    int nact = min(p.num_splits, (T + p.chunk - 1) / p.chunk);
+    if (p.q_len > 1) {
+        // the rows' 64-row block has units for the splits its last row sees
+        // only (mla_map): the first ceil(visible / chunk)
+        const int vis = T - p.q_len + min(qb / 4 * 64 + 63, p.R - 1) / p.H + 1;
+        nact = min(nact, (max(vis, 0) + p.chunk - 1) / p.chunk);
+    }
     const int64_t ml_st = (int64_t)p.R * 2;  // floats between splits of one row
     const float* ml0 = p.ws_ml + (int64_t)b * p.num_splits * p.R * 2;
 
@@ -903,7 +964,7 @@ int mla_tile_tokens(int) { return kTT; }
 
 template <int QDT, int DT, int OUT_DT>
 static hipError_t launch_mla_t(const MlaParams& p, int kernel, hipStream_t st, KernelTimer* t) {
-    const int grid = 8 * ((p.nrb * p.groups + 7) / 8);  // see mla_map
+    const int grid = 8 * ((p.units + 7) / 8);  // see mla_map
     hipError_t e = kernel == 1
                        ? launch_k(t, "mla_decode", mla_decode_kernel<QDT, DT>, dim3(grid), dim3(256), st, p)
                        : launch_k(t, "mla_decode", mla_decode_ws_kernel<QDT, DT>, dim3(grid), dim3(512), st, p);
