@@ -39,12 +39,15 @@ def mla_shape(seed):
 def test_mla_random(device, seed):
     B, q_len, H, max_T, lens, q_dt, lat_dt, kernel, splits = mla_shape(seed)
     C.say(f"mla random seed={seed}: B={B} q_len={q_len} H={H} max_T={max_T} lens={list(lens)} q={q_dt} "
-          f"lat={lat_dt} kernel={kernel} splits={splits}")
+          f"lat={lat_dt} kernel={kernel} splits={splits} hint={seed % 2}")
     c = C.mla_case(2000 + seed, B, q_len, H, lens, max_T=max_T, q_dtype=q_dt, lat_dtype=lat_dt)
     q = C.to_dev(c["q"] if q_dt == C.F32 else c["qb"], q_dt, device)
     lat = C.to_dev(c["latb"], lat_dt, device)
     sl = torch.from_numpy(lens).to(device)
-    out = mugen_amd.mla_attention(q, lat, sl, max_T, scale=C.MLA_SCALE, num_splits=splits, kernel=kernel)
+    # odd seeds pass the host length hint (the planner's exact unit count)
+    hint = lens if seed % 2 else None
+    out = mugen_amd.mla_attention(q, lat, sl, max_T, scale=C.MLA_SCALE, num_splits=splits, kernel=kernel,
+                                  seq_lens_host=hint)
     torch.cuda.synchronize()
     C.assert_close(out.cpu().numpy(), C.mla_ref(c, nthreads=16), f"mla random seed={seed}")
 
