@@ -600,6 +600,8 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
             if (j == 4) MUGEN_TRACE(6);
             lds_barrier();  // B_j: tile j landed (the PV waves waited for it)
             if (j == 4) MUGEN_TRACE(7);
+            if (j == 1) MUGEN_TRACE(14);
+            if (j == 2) MUGEN_TRACE(15);
             if (j == ntiles) break;
             const char* tile = &ring[(j % NSLOT) * kTileBytes];
             const int tt = t_begin + kTT * j;
