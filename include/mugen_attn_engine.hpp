@@ -57,6 +57,36 @@ inline Status hip_ok(hipError_t e, const char* what) {
     return fail(std::string(what) + ": " + hipGetErrorString(e));
 }
 
+// The prefill workspace that serves every prompt chunk of up to max_tokens
+// tokens in a cache of max_seq_len rows: the largest
+// mugen_attn_gqa_prefill_workspace_size over the chunk lengths (the fp16 V
+// copy of BF16 prompts, and the key splits' partials of chunks that continue
+// a long context; neither falls as the key range grows, so each length is
+// sized at the end of the cache).  `placeholder`: any 16-byte aligned device pointer
+// (only the shape matters for the size).
+inline size_t prefill_workspace_bytes(int n_heads, int n_kv_heads, int head_dim, int dtype, int max_seq_len,
+                                      int max_tokens, const void* placeholder) {
+    mugen_attn_gqa_prefill_args a{};
+    a.q = a.k = a.v = placeholder;
+    a.out = const_cast<void*>(placeholder);
+    a.n_heads = n_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.head_dim = head_dim;
+    a.causal = 1;
+    a.dtype = dtype;
+    a.out_dtype = dtype;
+    a.kv_len = max_seq_len;
+    size_t best = 0;
+    // within one count of 16-token query blocks the size grows with the length
+    for (int n = 16;; n += 16) {
+        a.n_tokens = std::min(n, max_tokens);
+        a.start_pos = max_seq_len - a.n_tokens;
+        best = std::max(best, mugen_attn_gqa_prefill_workspace_size(&a));
+        if (n >= max_tokens) break;
+    }
+    return best;
+}
+
 // every length in [0, max_seq_len - n_new]: room for the step's n_new tokens
 inline Status check_lengths(const std::vector<int32_t>& lens, int batch, int max_seq_len, int n_new,
                             const char* who) {
@@ -193,11 +223,13 @@ public:
         d.q = d.out = a->k_[0].ptr;  // placeholders: only the shape matters for the size
         // (a shape the library rejects sizes to 0 here and fails at decode_layer)
         if (auto r = a->ws_.alloc(gqa_decode_workspace_size(d), "GqaAttention workspace"); !r) return r;
-        // BF16 caches: room for the prefill's fp16 copy of one sequence's V
-        // (the library uses it for long prompts)
-        if (s.kv_dtype == MUGEN_ATTN_BF16)
-            if (auto r = a->pf_ws_.alloc((size_t)s.max_seq_len * row * 2 + 256, "GqaAttention prefill workspace"); !r)
-                return r;
+        // the prefill workspace: the fp16 copy of one sequence's V for long
+        // BF16 prompts, and the key splits' partials of prompt chunks that
+        // continue a long context
+        const size_t pf = detail::prefill_workspace_bytes(s.n_heads, s.n_kv_heads, s.head_dim, s.kv_dtype,
+                                                          s.max_seq_len, s.max_seq_len, a->k_[0].ptr);
+        if (pf)
+            if (auto r = a->pf_ws_.alloc(pf, "GqaAttention prefill workspace"); !r) return r;
         // empty sequences: [0 | 1], so a step before any set_lengths is well defined
         if (auto r = a->set_lengths(std::vector<int32_t>(s.batch, 0), nullptr); !r) return r;
         *out = std::move(a);
@@ -422,6 +454,12 @@ public:
         mugen_attn_gqa_decode_q4_args d = a->decode_args(0, nullptr, nullptr);
         d.q = d.out = a->rk_[0].ptr;  // placeholders: only the shape matters for the size
         if (auto r = a->ws_.alloc(gqa_decode_q4_workspace_size(d), "GqaAttentionQ4 workspace"); !r) return r;
+        if (s.f16_cache) {  // prompt chunks of up to max_new tokens over the f16 cache
+            const size_t pf = detail::prefill_workspace_bytes(s.n_heads, s.n_kv_heads, s.head_dim, MUGEN_ATTN_F16,
+                                                              s.max_seq_len, s.max_new, a->k16_[0].ptr);
+            if (pf)
+                if (auto r = a->pf_ws_.alloc(pf, "GqaAttentionQ4 prefill workspace"); !r) return r;
+        }
         if (auto r = a->set_lengths(std::vector<int32_t>(s.batch, 0), nullptr); !r) return r;
         *out = std::move(a);
         return Status{};
@@ -515,6 +553,8 @@ public:
         pf.scale = s_.scale;
         pf.dtype = MUGEN_ATTN_F16;
         pf.out_dtype = s_.out_dtype;
+        pf.workspace = pf_ws_.ptr;
+        pf.workspace_bytes = pf_ws_.bytes;
         return gqa_prefill(pf, st);
     }
 
@@ -622,7 +662,7 @@ private:
     GqaQ4Shape s_;
     int ring_ = 0, row_bytes_ = 0;
     std::vector<detail::DeviceBuffer> q4k_, q4v_, rk_, rv_, k16_, v16_;
-    detail::DeviceBuffer lens_, q4n_, ws_;
+    detail::DeviceBuffer lens_, q4n_, ws_, pf_ws_;
     std::vector<int32_t> host_lens_;
 };
 

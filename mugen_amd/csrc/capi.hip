@@ -585,10 +585,56 @@ static size_t gqa_prefill_ws(const mugen_attn_gqa_prefill_args* a) {
     return (size_t)a->kv_len * a->n_kv_heads * a->head_dim * 2 + 256;
 }
 
+static bool gqa_prefill_uses_v16(const mugen_attn_gqa_prefill_args* a) {
+    return a->head_dim <= 128 && a->dtype == DT_BF16 && a->n_tokens >= kPrefillV16MinTokens;
+}
+
+// Key splits for the warp-specialised kernel.  A prompt chunk that
+// continues a long context has few 16-token query blocks over a long key
+// range: unsplit, workgroups for fewer than half the CUs walk the
+// whole range each.  Each block's keys are then split into ranges of whole
+// steps (at least kMinSteps, so that the partials' merge stays a small part
+// of the call) until the work list fills about one round; the partials go
+// to the workspace after the fp16 V copy, and gqa_prefill_combine merges
+// them.  The plan depends on the arguments only, so the workspace size
+// function and the call agree.
+struct PrefillSplit {
+    int ksplit = 1, kchunk = 0;
+    size_t bytes = 0;  // partial O and (max, sum) of every row and split
+};
+static PrefillSplit gqa_prefill_split(const mugen_attn_gqa_prefill_args* a) {
+    PrefillSplit r;
+    if (a->head_dim > 128 || a->n_tokens <= 0 || a->kv_len <= 0) return r;
+    if (a->kernel && a->kernel != MUGEN_ATTN_PREFILL_KERNEL_WS) return r;
+    const int G = a->n_heads / a->n_kv_heads;
+    const int D = padded_head_dim(a->head_dim);
+    const int dt = gqa_prefill_uses_v16(a) ? kDtBf16V16 : a->dtype;
+    const int64_t units = (int64_t)ceil_div(a->n_tokens, 16) * a->n_kv_heads * gqa_prefill_ws_slices(G);
+    const int64_t target = 256 * (int64_t)gqa_prefill_ws_blocks_per_cu(G, D);
+    // half the CUs or more busy unsplit: the partials' round trip costs
+    // more than the idle CUs would add (4-head blocks at 256 units, one per
+    // CU: 39.6 us split against 34.1 unsplit)
+    if (units * 2 > 256) return r;
+    const int step = gqa_prefill_ws_step_keys(G, dt);
+    const int kend = a->causal ? std::min(a->kv_len, a->start_pos + a->n_tokens) : a->kv_len;
+    const int steps = ceil_div(kend, step);
+    constexpr int kMinSteps = 8, kMaxSplits = 16;
+    const int64_t want = std::min<int64_t>({ceil_div(target, units), (int64_t)steps / kMinSteps, kMaxSplits});
+    if (want < 2) return r;
+    const int kchunk = ceil_div(steps, (int)want) * step;
+    const int ks = ceil_div(kend, kchunk);
+    if (ks < 2) return r;
+    r.ksplit = ks;
+    r.kchunk = kchunk;
+    // sized for `want` ranges (ks <= want): want never falls as the key
+    // range grows, so the size at the longest range covers every shorter one
+    r.bytes = (size_t)a->n_tokens * a->n_heads * want * (a->head_dim + 2) * sizeof(float) + 512;
+    return r;
+}
+
 size_t mugen_attn_gqa_prefill_workspace_size(const mugen_attn_gqa_prefill_args* a) {
     if (gqa_prefill_validate(a) != MUGEN_ATTN_OK) return 0;
-    if (a->dtype != DT_BF16 || a->n_tokens < kPrefillV16MinTokens) return 0;
-    return gqa_prefill_ws(a);
+    return (gqa_prefill_uses_v16(a) ? gqa_prefill_ws(a) : 0) + gqa_prefill_split(a).bytes;
 }
 
 int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
@@ -660,8 +706,18 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
                     "gqa_prefill: the short kernel serves head_dim 64, n_heads/n_kv_heads <= 4 and <= 512 keys");
     if (a->kernel) kernel = a->kernel;
     int dt = a->dtype;
-    if (kernel != MUGEN_ATTN_PREFILL_KERNEL_SHORT && a->dtype == DT_BF16 && a->n_tokens >= kPrefillV16MinTokens &&
-        a->workspace && a->workspace_bytes >= gqa_prefill_ws(a)) {
+    const size_t v16_bytes = gqa_prefill_uses_v16(a) ? gqa_prefill_ws(a) : 0;
+    const PrefillSplit split = kernel == MUGEN_ATTN_PREFILL_KERNEL_SHORT ? PrefillSplit{} : gqa_prefill_split(a);
+    p.ksplit = 1;
+    if (split.ksplit > 1 && a->workspace && a->workspace_bytes >= v16_bytes + split.bytes) {
+        // key splits (the warp-specialised kernel): partials after the V copy
+        kernel = MUGEN_ATTN_PREFILL_KERNEL_WS;
+        p.ksplit = split.ksplit;
+        p.kchunk = split.kchunk;
+        p.ws_o = align256(static_cast<char*>(a->workspace) + v16_bytes);
+        p.ws_ml = p.ws_o + (size_t)a->n_tokens * a->n_heads * split.ksplit * a->head_dim;
+    }
+    if (kernel != MUGEN_ATTN_PREFILL_KERNEL_SHORT && v16_bytes && a->workspace && a->workspace_bytes >= v16_bytes) {
         // V -> fp16 once for the whole call (the kernels then skip their
         // per-workgroup conversion)
         uint16_t* v16 = reinterpret_cast<uint16_t*>(align256(a->workspace));

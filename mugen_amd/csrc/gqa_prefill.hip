@@ -472,7 +472,7 @@ __global__ __launch_bounds__(512) void gqa_prefill_kernel(GqaPrefillParams p) {
 //  * one barrier per tile: at barrier j tile j has landed, the S waves have
 //    written P(j-1), and the PV waves have finished tile j-2, whose slot
 //    then receives tile j+2.
-template <int D, int NS, int SMB, int NPV, int DTI, int OUT_DT, bool PAD, int TPS>
+template <int D, int NS, int SMB, int NPV, int DTI, int OUT_DT, bool PAD, int TPS, bool SPLIT>
 __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(GqaPrefillParams p, int nqb,
                                                                                int nslice, int Hk) {
     constexpr int DT = DTI == kDtBf16V16 ? DT_BF16 : DTI;  // q and K
@@ -505,10 +505,13 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
 
     // longest-first over (query block, kv head, slice)
     const int lin = blockIdx.x;
+    // (query block, kv head, slice, key split), longest-first by query block
+    const int ks_id = SPLIT ? lin % p.ksplit : 0;
+    const int lq = SPLIT ? lin / p.ksplit : lin;
     const int per_qb = Hk * nslice;
-    const int qb = nqb - 1 - lin / per_qb;
-    const int kvh = (lin / nslice) % Hk;
-    const int slice = lin % nslice;
+    const int qb = nqb - 1 - lq / per_qb;
+    const int kvh = (lq / nslice) % Hk;
+    const int slice = lq % nslice;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     constexpr int NSW = NS / SMB;               // S waves, SMB heads each
@@ -520,7 +523,10 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
     const int nh = min(NS, G - NS * slice);     // heads of this slice
     int kend = p.kv_len;
     if (p.causal) kend = min(kend, p.start_pos + min(t0 + 16, p.N));
-    const int ntiles = (kend + KS - 1) / KS;    // steps
+    // this workgroup's keys [k_beg, kend) (the block's whole range unless split)
+    const int k_beg = SPLIT ? ks_id * p.kchunk : 0;
+    if (SPLIT) kend = min(kend, k_beg + p.kchunk);
+    const int ntiles = SPLIT ? (kend > k_beg ? (kend - k_beg + KS - 1) / KS : 0) : (kend + KS - 1) / KS;  // steps
     const uint32_t ring_base = lds_addr(&ring[0]);
     char* pbuf = &ring[NSLOT * SLOT];
 
@@ -561,7 +567,7 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             if (j == ntiles) break;
             if (!hok[0]) continue;
             const uint32_t slot_addr = ring_base + (uint32_t)((j % NSLOT) * SLOT);
-            const int kt = j * KS;
+            const int kt = k_beg + j * KS;
             // block nb of tile u: keys kt + 32u + 8g + 4(nb % 2) + i; one
             // address register per k-step, the tile and half-block offsets
             // in the instruction
@@ -675,6 +681,11 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
         for (int mb = 0; mb < SMB; mb++) {
             const float l = sum_x32(sum_x16(l_part[mb]));
             if (g == 0) linv_x[wr * SMB + mb][n] = l > 0.f ? 1.f / l : 0.f;
+            if (SPLIT && g == 0 && hok[mb] && t0 + n < p.N) {
+                // split partial: the row's reference max (log2 units) and sum
+                const int64_t row = (int64_t)(t0 + n) * p.H + kvh * G + NS * slice + wr * SMB + mb;
+                *reinterpret_cast<f32x2v_t*>(p.ws_ml + (row * p.ksplit + ks_id) * 2) = f32x2v_t{m_run[mb], l};
+            }
         }
         __syncthreads();  // E: 1/l published
     } else {
@@ -691,9 +702,9 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
         const int dma_row = (64 * wr + lane) / CR;
         const uint32_t dma_col = (uint32_t)(dim_chunk((lane % CR) ^ pf_swz<D>(dma_row), hd) * 16);
         auto issue = [&](int it) {
-            const int kt = it * KS + dma_row;
+            const int kt = k_beg + it * KS + dma_row;
             const uint32_t lds0 = ring_base + (it % NSLOT) * SLOT + wr * 1024;
-            if ((it + 1) * KS <= kend) {
+            if (k_beg + (it + 1) * KS <= kend) {
                 // every row in range: one offset, op k's rows through the
                 // scalar base (no per-op vector arithmetic)
                 const uint32_t off = (uint32_t)kt * rs_bytes + dma_col;
@@ -844,6 +855,16 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
 #pragma unroll
             for (int hh = 0; hh < HPW; hh++) {
                 if (hb + hh >= nh) continue;
+                if (SPLIT) {  // split partial: the unnormalised O
+                    const int64_t row = (int64_t)tok * p.H + kvh * G + NS * slice + hb + hh;
+                    float* dst = p.ws_o + (row * p.ksplit + ks_id) * hd + 4 * g;
+#pragma unroll
+                    for (int d = 0; d < DB; d++) {
+                        if (16 * d + 4 * g >= hd) break;  // padded dims (head_dim < D)
+                        *reinterpret_cast<f32x4_t*>(dst + 16 * d) = o[hh][d];
+                    }
+                    continue;
+                }
                 const float inv = linv_x[hb + hh][n];
                 const int64_t base = ((int64_t)tok * p.H + kvh * G + NS * slice + hb + hh) * hd + 4 * g;
 #pragma unroll
@@ -1198,12 +1219,64 @@ static hipError_t launch_pf_g(const GqaPrefillParams& p, int Hk, int dt, int out
 template <int DT>
 constexpr int kWsTps = DT == DT_BF16 ? 1 : 2;
 
-template <int D, bool PAD, int DT, int OUT_DT>
-static hipError_t launch_pf_ws_t(const GqaPrefillParams& p, int Hk, hipStream_t st, KernelTimer* t) {
+// Merge of the key splits' partials: thread = (row, 4 output dims), rows
+// (token, head); out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s with M
+// the largest reference max (a split that saw no key of the row: m = -inf,
+// weight 0)
+template <int OUT_DT>
+__global__ __launch_bounds__(256) void gqa_prefill_combine_kernel(GqaPrefillParams p) {
+    const int dq = p.hd >> 2;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t row = i / dq;
+    if (row >= (int64_t)p.N * p.H) return;
+    const int c = (int)(i - row * dq);
+    const float* ml = p.ws_ml + row * p.ksplit * 2;
+    const float* o = p.ws_o + row * p.ksplit * p.hd + 4 * c;
+    float M = kNegInf;
+    for (int s = 0; s < p.ksplit; s++) M = fmaxf(M, ml[2 * s]);
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    float L = 0.f;
+    if (M != kNegInf) {
+        for (int s = 0; s < p.ksplit; s++) {
+            const float m = ml[2 * s];
+            if (m == kNegInf) continue;
+            const float w = fast_exp2(m - M);
+            L += w * ml[2 * s + 1];
+            acc += w * *reinterpret_cast<const f32x4_t*>(o + (int64_t)s * p.hd);
+        }
+    }
+    const f32x4_t r = acc * (L > 0.f ? 1.f / L : 0.f);
+    const int64_t base = row * p.hd + 4 * c;
+    if constexpr (OUT_DT == DT_F32) {
+        *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.out) + base) = r;
+    } else {
+        *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.out) + base) =
+            u32x2_t{pack2<OUT_DT>(r[0], r[1]), pack2<OUT_DT>(r[2], r[3])};
+    }
+}
+
+template <int OUT_DT>
+static hipError_t launch_pf_combine(const GqaPrefillParams& p, hipStream_t st, KernelTimer* t) {
+    const int64_t threads = (int64_t)p.N * p.H * (p.hd / 4);
+    return launch_k(t, "gqa_prefill_combine", gqa_prefill_combine_kernel<OUT_DT>,
+                    dim3((unsigned)((threads + 255) / 256)), dim3(256), st, p);
+}
+
+int gqa_prefill_ws_slices(int G) { return G <= 4 ? 1 : (G + 7) / 8; }
+int gqa_prefill_ws_step_keys(int G, int dt) { return (G <= 4 || dt == DT_BF16) ? 32 : 64; }
+// one 8-head block per CU (128 KiB of LDS at head_dim 128); 4-head blocks:
+// two at head_dim 128, three at 64
+int gqa_prefill_ws_blocks_per_cu(int G, int D) { return G > 4 ? 1 : (D > 64 ? 2 : 3); }
+
+// SPLIT: the kernel stores fp32 partials whatever the output type (one
+// instantiation, OUT_DT = f32), and the combine writes the output
+template <int D, bool PAD, int DT, int OUT_DT, bool SPLIT>
+static hipError_t launch_pf_ws_k(const GqaPrefillParams& p, int Hk, hipStream_t st, KernelTimer* t) {
     const int nqb = (p.N + 15) / 16;
+    const int ks = SPLIT ? p.ksplit : 1;
     if (p.G <= 4)
-        return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 4, 1, 4, DT, OUT_DT, PAD, 1>, dim3(nqb * Hk * ((p.G + 3) / 4)),
-                        dim3(64 * 8), st, p, nqb, (p.G + 3) / 4, Hk);
+        return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 4, 1, 4, DT, OUT_DT, PAD, 1, SPLIT>,
+                        dim3(nqb * Hk * ((p.G + 3) / 4) * ks), dim3(64 * 8), st, p, nqb, (p.G + 3) / 4, Hk);
     const int nslice = (p.G + 7) / 8;
     // 8-head blocks keep 4 PV waves (2 heads each): 8 PV waves (one head
     // each, 16-wave blocks) measured no faster
@@ -1213,8 +1286,15 @@ static hipError_t launch_pf_ws_t(const GqaPrefillParams& p, int Hk, hipStream_t 
     // per row, measured slower (859 against 804 us at 7B N = 8192; with two
     // tiles per step 547 against 541 us)
     constexpr int SMB = 1;
-    return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 8, SMB, NPV, DT, OUT_DT, PAD, kWsTps<DT>>, dim3(nqb * Hk * nslice),
-                    dim3(64 * (8 / SMB + NPV)), st, p, nqb, nslice, Hk);
+    return launch_k(t, "gqa_prefill", gqa_prefill_ws_kernel<D, 8, SMB, NPV, DT, OUT_DT, PAD, kWsTps<DT>, SPLIT>,
+                    dim3(nqb * Hk * nslice * ks), dim3(64 * (8 / SMB + NPV)), st, p, nqb, nslice, Hk);
+}
+
+template <int D, bool PAD, int DT, int OUT_DT>
+static hipError_t launch_pf_ws_t(const GqaPrefillParams& p, int Hk, hipStream_t st, KernelTimer* t) {
+    if (p.ksplit <= 1) return launch_pf_ws_k<D, PAD, DT, OUT_DT, false>(p, Hk, st, t);
+    const hipError_t e = launch_pf_ws_k<D, PAD, DT, DT_F32, true>(p, Hk, st, t);
+    return e != hipSuccess ? e : launch_pf_combine<OUT_DT>(p, st, t);
 }
 
 template <int D, bool PAD, int DT>

@@ -112,6 +112,15 @@ struct GqaPrefillParams {
     int causal;
     float scale_log2;
     int hd;          // head_dim of q, the caches and out (<= D, a multiple of 8)
+    // key splits (warp-specialised kernel; 1 = none): workgroup split s takes
+    // keys [s kchunk, (s+1) kchunk) of its query block and writes the rows'
+    // unnormalised fp32 partial O to ws_o [N][H][ksplit][hd] and (reference
+    // max in log2 units, weight sum) to ws_ml [N][H][ksplit][2]; the
+    // gqa_prefill_combine kernel then merges them into out
+    int ksplit;
+    int kchunk;
+    float* ws_o;
+    float* ws_ml;
 };
 
 // kernel 1 (MUGEN_ATTN_PREFILL_KERNEL_BLOCK): one (query block, kv head) per
@@ -123,6 +132,11 @@ hipError_t launch_gqa_prefill(const GqaPrefillParams& p, int Hk, int D, int dt, 
 // held in LDS; serves head_dim 64 (unpadded), at most 4 heads per kv head
 // and a kv range (start_pos + N causal, kv_len otherwise) of at most 512
 bool gqa_prefill_short_fits(const GqaPrefillParams& p, int D);
+// key steps of the warp-specialised kernel (32 or 64 keys) and its
+// workgroups per CU, for the split planner (dt as for launch_gqa_prefill)
+int gqa_prefill_ws_step_keys(int G, int dt);
+int gqa_prefill_ws_blocks_per_cu(int G, int D);
+int gqa_prefill_ws_slices(int G);
 // dt code for launch_gqa_prefill: bf16 q / K with V already converted to fp16
 constexpr int kDtBf16V16 = 100;
 // fp16 copy of n bf16 values (n a multiple of 8, 16-byte aligned buffers)

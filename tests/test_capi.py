@@ -318,3 +318,25 @@ def test_prefill_workspace_size():
     assert size(ctypes.byref(a)) == 0
     a.dtype, a.head_dim = _capi.BF16, 84                         # invalid args: 0
     assert size(ctypes.byref(a)) == 0
+    # a 256-token chunk after 7900 cached tokens: 64 workgroups unsplit, so
+    # each block's 8156 keys go to 4 ranges of 2048 (32 steps of 64 keys);
+    # the partials are fp32 O plus (max, sum) per row and range
+    a.n_tokens, a.start_pos, a.kv_len, a.head_dim, a.dtype = 256, 7900, 8156, 128, _capi.F16
+    assert size(ctypes.byref(a)) == 256 * 28 * 4 * (128 + 2) * 4 + 512
+    a.causal = 0                                                 # non-causal: the same key range here
+    assert size(ctypes.byref(a)) == 256 * 28 * 4 * (128 + 2) * 4 + 512
+    a.causal, a.kernel = 1, _capi.PREFILL_KERNEL_BLOCK            # a forced non-split kernel: none
+    assert size(ctypes.byref(a)) == 0
+    a.kernel, a.start_pos, a.kv_len = 0, 0, 256                  # a short range: no split
+    assert size(ctypes.byref(a)) == 0
+    # the size never falls as the range grows (an engine sizes one workspace
+    # at the end of its cache for every shorter context)
+    for n, H, Hk in [(64, 28, 4), (256, 8, 1), (48, 32, 2), (100, 32, 8)]:
+        a.n_tokens, a.n_heads, a.n_kv_heads = n, H, Hk
+        last = 0
+        for start in range(0, 20000, 37):
+            a.start_pos, a.kv_len = start, start + n
+            got = size(ctypes.byref(a))
+            assert got >= last, (n, H, Hk, start)
+            last = got
+        assert last > 0
