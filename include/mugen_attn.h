@@ -217,7 +217,8 @@ int mugen_attn_gqa_decode_q4(const mugen_attn_gqa_decode_q4_args* args, void* wo
  * chip, exact inside the f16 range), so BF16 V values must lie
  * within +-65504 -- the range of the reference's f16 cache; V magnitudes
  * below 6.1e-5 keep an absolute precision of 2^-25.  The optional
- * workspace (below) holds an fp16 copy of BF16 V for long prompts.
+ * workspace (below) holds an fp16 copy of BF16 V for long prompts, and the
+ * partials of split key ranges for short chunks over a long context.
  */
 typedef struct mugen_attn_gqa_prefill_args {
     const void* q;
@@ -241,8 +242,13 @@ typedef struct mugen_attn_gqa_prefill_args {
      * 1024 tokens, given at least kv_len * n_kv_heads * head_dim * 2 + 256
      * bytes (mugen_attn_gqa_prefill_workspace_size), the call first copies
      * V[0, kv_len) to fp16 there (one extra launch), so the attention
-     * kernels need no per-workgroup conversion; same results.  Otherwise
-     * unused.  It must not overlap q, k, v or out. */
+     * kernels need no per-workgroup conversion; same results.  When the
+     * query blocks would occupy fewer than half the CUs (a short chunk
+     * after a long context), a workspace of the full
+     * mugen_attn_gqa_prefill_workspace_size also holds fp32 partials of
+     * split key ranges, merged by a second launch (same results to
+     * rounding).  Smaller workspaces use what fits; a call never fails for
+     * want of one.  It must not overlap q, k, v or out. */
     void* workspace;
     size_t workspace_bytes;
 } mugen_attn_gqa_prefill_args;
@@ -254,10 +260,13 @@ typedef struct mugen_attn_gqa_prefill_args {
                                            * otherwise); forcing it outside that range is refused */
 
 int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* args, void* stream);
-/* Bytes of the optional prefill workspace worth passing: kv_len * n_kv_heads
- * * head_dim * 2 + 256 for BF16 prompts of at least 1024 tokens (where the
- * separate V conversion pays for its launch), else 0 (also for invalid args).
- * No counterpart in the reference (its cache is f16). */
+/* Bytes of the optional prefill workspace worth passing: the fp16 V copy
+ * (kv_len * n_kv_heads * head_dim * 2 + 256 for BF16 prompts of at least
+ * 1024 tokens, where the separate conversion pays for its launch) plus the
+ * split partials (n_tokens * n_heads * splits * (head_dim + 2) * 4 + 512
+ * when the key range is split), else 0 (also for invalid args).  The size
+ * never falls as kv_len grows at a fixed n_tokens.  No counterpart in the
+ * reference (it runs each chunk on one pass over its keys). */
 size_t mugen_attn_gqa_prefill_workspace_size(const mugen_attn_gqa_prefill_args* args);
 
 /*
