@@ -229,22 +229,29 @@ class Prefill(Case):
     bound = "mfma"
     unit = "TFLOP/s"
     kernel = "gqa_prefill"
-    extra_kernels = ("gqa_prefill_v16",)  # the fp16 copy of V (long bf16 prompts)
+    # the fp16 copy of V (long bf16 prompts); the merge of split key ranges
+    # (short chunks over a long context)
+    extra_kernels = ("gqa_prefill_v16", "gqa_prefill_combine")
 
-    def __init__(self, dev, N, H, Hk, D, seed, name):
+    def __init__(self, dev, N, H, Hk, D, seed, name, start=0):
+        """N prompt tokens at start_pos `start` (a chunk after `start` cached
+        tokens: the cache holds start + N rows, token i sees start + i + 1)."""
         self.name = name
+        self.start = start
+        kv = start + N
         g = torch.Generator(device=dev).manual_seed(seed)
         self.q = randn((N, H, D), 1.0, torch.bfloat16, g, dev)
-        self.k = randn((N, Hk, D), 1.0, torch.bfloat16, g, dev)
-        self.v = randn((N, Hk, D), 1.0, torch.bfloat16, g, dev)
+        self.k = randn((kv, Hk, D), 1.0, torch.bfloat16, g, dev)
+        self.v = randn((kv, Hk, D), 1.0, torch.bfloat16, g, dev)
         self.out = torch.empty((N, H, D), dtype=torch.bfloat16, device=dev)
-        self.profile = ("gqa_prefill", "llama1b_n512" if N == 512 else f"qwen7b_n{N}")
-        self.flops = 4.0 * H * D * N * (N + 1) / 2
-        self.bytes = (N * H * D * 2) * 2 + N * Hk * D * 2 * 2
-        self.ws = mugen_amd.prefill_workspace(self.q, self.k, self.v, 0)
+        self.profile = ("gqa_prefill", "llama1b_n512" if N == 512 else
+                        f"qwen7b_n{N}" + (f"_at{start}" if start else ""))
+        self.flops = 4.0 * H * D * N * (start + (N + 1) / 2)
+        self.bytes = (N * H * D * 2) * 2 + kv * Hk * D * 2 * 2
+        self.ws = mugen_amd.prefill_workspace(self.q, self.k, self.v, start)
 
     def step(self):
-        mugen_amd.flash_prefill_attention(self.q, self.k, self.v, 0, out=self.out, workspace=self.ws)
+        mugen_amd.flash_prefill_attention(self.q, self.k, self.v, self.start, out=self.out, workspace=self.ws)
 
 
 class MlaFull(Case):
@@ -486,6 +493,9 @@ def main():
             Prefill(dev, 512, 32, 8, 64, 46, "gqa_prefill_llama1b"),
             Prefill(dev, 2048, 28, 4, 128, 50, "gqa_prefill_qwen7b_n2048"),
             Prefill(dev, 8192, 28, 4, 128, 49, "gqa_prefill_qwen7b_n8192"),
+            # a 256-token prompt chunk after 7936 cached tokens (the key
+            # ranges split across workgroups, then merged)
+            Prefill(dev, 256, 28, 4, 128, 53, "gqa_prefill_qwen7b_chunk256_at7936", start=7936),
             MlaDecode(dev, 4, 128, 5, [32768] * 4, 32768, torch.bfloat16, torch.bfloat16, 47, "mla_verify_v3"),
             # a 512-token prompt of V2-Lite in one verify-shaped call (the
             # reference runs cpu_mla_attention once per prompt token)

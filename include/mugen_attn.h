@@ -245,7 +245,7 @@ typedef struct mugen_attn_gqa_prefill_args {
      * kernels need no per-workgroup conversion; same results.  When the
      * query blocks would occupy fewer than half the CUs (a short chunk
      * after a long context), a workspace of the full
-     * mugen_attn_gqa_prefill_workspace_size also holds fp32 partials of
+     * mugen_attn_gqa_prefill_workspace_size also holds the partials of
      * split key ranges, merged by a second launch (same results to
      * rounding).  Smaller workspaces use what fits; a call never fails for
      * want of one.  It must not overlap q, k, v or out. */
@@ -263,7 +263,7 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* args, void* stream
 /* Bytes of the optional prefill workspace worth passing: the fp16 V copy
  * (kv_len * n_kv_heads * head_dim * 2 + 256 for BF16 prompts of at least
  * 1024 tokens, where the separate conversion pays for its launch) plus the
- * split partials (n_tokens * n_heads * splits * (head_dim + 2) * 4 + 512
+ * split partials (n_tokens * n_heads * splits * (2 * head_dim + 8) + 512
  * when the key range is split), else 0 (also for invalid args).  The size
  * never falls as kv_len grows at a fixed n_tokens.  No counterpart in the
  * reference (it runs each chunk on one pass over its keys). */

@@ -594,8 +594,8 @@ static bool gqa_prefill_uses_v16(const mugen_attn_gqa_prefill_args* a) {
 // range: unsplit, workgroups for fewer than half the CUs walk the
 // whole range each.  Each block's keys are then split into ranges of whole
 // steps (at least kMinSteps, so that the partials' merge stays a small part
-// of the call) until the work list fills about one round; the partials go
-// to the workspace after the fp16 V copy, and gqa_prefill_combine merges
+// of the call) until the work list fills about one round; the partials
+// (fp16 O / l, fp32 max and sum) go to the workspace after the fp16 V copy, and gqa_prefill_combine merges
 // them.  The plan depends on the arguments only, so the workspace size
 // function and the call agree.
 struct PrefillSplit {
@@ -628,7 +628,7 @@ static PrefillSplit gqa_prefill_split(const mugen_attn_gqa_prefill_args* a) {
     r.kchunk = kchunk;
     // sized for `want` ranges (ks <= want): want never falls as the key
     // range grows, so the size at the longest range covers every shorter one
-    r.bytes = (size_t)a->n_tokens * a->n_heads * want * (a->head_dim + 2) * sizeof(float) + 512;
+    r.bytes = (size_t)a->n_tokens * a->n_heads * want * (a->head_dim * 2 + 2 * sizeof(float)) + 512;
     return r;
 }
 
@@ -714,8 +714,8 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
         kernel = MUGEN_ATTN_PREFILL_KERNEL_WS;
         p.ksplit = split.ksplit;
         p.kchunk = split.kchunk;
-        p.ws_o = align256(static_cast<char*>(a->workspace) + v16_bytes);
-        p.ws_ml = p.ws_o + (size_t)a->n_tokens * a->n_heads * split.ksplit * a->head_dim;
+        p.ws_ml = align256(static_cast<char*>(a->workspace) + v16_bytes);
+        p.ws_o = reinterpret_cast<uint16_t*>(p.ws_ml + (size_t)a->n_tokens * a->n_heads * split.ksplit * 2);
     }
     if (kernel != MUGEN_ATTN_PREFILL_KERNEL_SHORT && v16_bytes && a->workspace && a->workspace_bytes >= v16_bytes) {
         // V -> fp16 once for the whole call (the kernels then skip their

@@ -855,17 +855,21 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
 #pragma unroll
             for (int hh = 0; hh < HPW; hh++) {
                 if (hb + hh >= nh) continue;
-                if (SPLIT) {  // split partial: the unnormalised O
+                const float inv = linv_x[hb + hh][n];
+                if (SPLIT) {
+                    // split partial: O / l in fp16 (a convex combination of
+                    // V rows, inside V's +-65504); l and the max from the S waves
                     const int64_t row = (int64_t)tok * p.H + kvh * G + NS * slice + hb + hh;
-                    float* dst = p.ws_o + (row * p.ksplit + ks_id) * hd + 4 * g;
+                    uint16_t* dst = p.ws_o + (row * p.ksplit + ks_id) * hd + 4 * g;
 #pragma unroll
                     for (int d = 0; d < DB; d++) {
                         if (16 * d + 4 * g >= hd) break;  // padded dims (head_dim < D)
-                        *reinterpret_cast<f32x4_t*>(dst + 16 * d) = o[hh][d];
+                        const f32x4_t r = o[hh][d] * inv;
+                        *reinterpret_cast<u32x2_t*>(dst + 16 * d) =
+                            u32x2_t{pack2<DT_F16>(r[0], r[1]), pack2<DT_F16>(r[2], r[3])};
                     }
                     continue;
                 }
-                const float inv = linv_x[hb + hh][n];
                 const int64_t base = ((int64_t)tok * p.H + kvh * G + NS * slice + hb + hh) * hd + 4 * g;
 #pragma unroll
                 for (int d = 0; d < DB; d++) {
@@ -1220,9 +1224,9 @@ template <int DT>
 constexpr int kWsTps = DT == DT_BF16 ? 1 : 2;
 
 // Merge of the key splits' partials: thread = (row, 4 output dims), rows
-// (token, head); out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s with M
-// the largest reference max (a split that saw no key of the row: m = -inf,
-// weight 0)
+// (token, head); with o_s = O_s / l_s stored, out = sum_s w_s o_s / sum_s w_s,
+// w_s = 2^(m_s - M) l_s, M the largest reference max (a split that saw no
+// key of the row: m = -inf, l = 0, weight 0)
 template <int OUT_DT>
 __global__ __launch_bounds__(256) void gqa_prefill_combine_kernel(GqaPrefillParams p) {
     const int dq = p.hd >> 2;
@@ -1231,7 +1235,7 @@ __global__ __launch_bounds__(256) void gqa_prefill_combine_kernel(GqaPrefillPara
     if (row >= (int64_t)p.N * p.H) return;
     const int c = (int)(i - row * dq);
     const float* ml = p.ws_ml + row * p.ksplit * 2;
-    const float* o = p.ws_o + row * p.ksplit * p.hd + 4 * c;
+    const uint16_t* o = p.ws_o + row * p.ksplit * p.hd + 4 * c;
     float M = kNegInf;
     for (int s = 0; s < p.ksplit; s++) M = fmaxf(M, ml[2 * s]);
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -1240,9 +1244,10 @@ __global__ __launch_bounds__(256) void gqa_prefill_combine_kernel(GqaPrefillPara
         for (int s = 0; s < p.ksplit; s++) {
             const float m = ml[2 * s];
             if (m == kNegInf) continue;
-            const float w = fast_exp2(m - M);
-            L += w * ml[2 * s + 1];
-            acc += w * *reinterpret_cast<const f32x4_t*>(o + (int64_t)s * p.hd);
+            const float w = fast_exp2(m - M) * ml[2 * s + 1];
+            const u32x2_t h = *reinterpret_cast<const u32x2_t*>(o + (int64_t)s * p.hd);
+            L += w;
+            acc += w * f32x4_t{lo_f32<DT_F16>(h[0]), hi_f32<DT_F16>(h[0]), lo_f32<DT_F16>(h[1]), hi_f32<DT_F16>(h[1])};
         }
     }
     const f32x4_t r = acc * (L > 0.f ? 1.f / L : 0.f);
@@ -1268,7 +1273,7 @@ int gqa_prefill_ws_step_keys(int G, int dt) { return (G <= 4 || dt == DT_BF16) ?
 // two at head_dim 128, three at 64
 int gqa_prefill_ws_blocks_per_cu(int G, int D) { return G > 4 ? 1 : (D > 64 ? 2 : 3); }
 
-// SPLIT: the kernel stores fp32 partials whatever the output type (one
+// SPLIT: the kernel stores fp16 partials whatever the output type (one
 // instantiation, OUT_DT = f32), and the combine writes the output
 template <int D, bool PAD, int DT, int OUT_DT, bool SPLIT>
 static hipError_t launch_pf_ws_k(const GqaPrefillParams& p, int Hk, hipStream_t st, KernelTimer* t) {

@@ -114,12 +114,13 @@ struct GqaPrefillParams {
     int hd;          // head_dim of q, the caches and out (<= D, a multiple of 8)
     // key splits (warp-specialised kernel; 1 = none): workgroup split s takes
     // keys [s kchunk, (s+1) kchunk) of its query block and writes the rows'
-    // unnormalised fp32 partial O to ws_o [N][H][ksplit][hd] and (reference
-    // max in log2 units, weight sum) to ws_ml [N][H][ksplit][2]; the
-    // gqa_prefill_combine kernel then merges them into out
+    // normalised partial O (O_s / l_s, fp16) to ws_o [N][H][ksplit][hd] and
+    // (reference max in log2 units, weight sum l_s) to ws_ml
+    // [N][H][ksplit][2]; the gqa_prefill_combine kernel then merges them
+    // into out
     int ksplit;
     int kchunk;
-    float* ws_o;
+    uint16_t* ws_o;
     float* ws_ml;
 };
 

@@ -320,11 +320,11 @@ def test_prefill_workspace_size():
     assert size(ctypes.byref(a)) == 0
     # a 256-token chunk after 7900 cached tokens: 64 workgroups unsplit, so
     # each block's 8156 keys go to 4 ranges of 2048 (32 steps of 64 keys);
-    # the partials are fp32 O plus (max, sum) per row and range
+    # the partials are fp16 O / l plus fp32 (max, sum) per row and range
     a.n_tokens, a.start_pos, a.kv_len, a.head_dim, a.dtype = 256, 7900, 8156, 128, _capi.F16
-    assert size(ctypes.byref(a)) == 256 * 28 * 4 * (128 + 2) * 4 + 512
+    assert size(ctypes.byref(a)) == 256 * 28 * 4 * (128 * 2 + 8) + 512
     a.causal = 0                                                 # non-causal: the same key range here
-    assert size(ctypes.byref(a)) == 256 * 28 * 4 * (128 + 2) * 4 + 512
+    assert size(ctypes.byref(a)) == 256 * 28 * 4 * (128 * 2 + 8) + 512
     a.causal, a.kernel = 1, _capi.PREFILL_KERNEL_BLOCK            # a forced non-split kernel: none
     assert size(ctypes.byref(a)) == 0
     a.kernel, a.start_pos, a.kv_len = 0, 0, 256                  # a short range: no split
