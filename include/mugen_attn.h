@@ -239,8 +239,9 @@ typedef struct mugen_attn_gqa_prefill_args {
      * one kernel (same results within rounding; for kernel comparisons) */
     int32_t kernel;
     /* optional workspace (NULL / 0: none).  For BF16 prompts of at least
-     * 1024 tokens, given at least kv_len * n_kv_heads * head_dim * 2 + 256
-     * bytes (mugen_attn_gqa_prefill_workspace_size), the call first copies
+     * 1024 tokens (and split calls, below), given at least kv_len *
+     * n_kv_heads * head_dim * 2 + 256 bytes
+     * (mugen_attn_gqa_prefill_workspace_size), the call first copies
      * V[0, kv_len) to fp16 there (one extra launch), so the attention
      * kernels need no per-workgroup conversion; same results.  When the
      * query blocks would occupy fewer than half the CUs (a short chunk
@@ -262,7 +263,8 @@ typedef struct mugen_attn_gqa_prefill_args {
 int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* args, void* stream);
 /* Bytes of the optional prefill workspace worth passing: the fp16 V copy
  * (kv_len * n_kv_heads * head_dim * 2 + 256 for BF16 prompts of at least
- * 1024 tokens, where the separate conversion pays for its launch) plus the
+ * 1024 tokens and for split calls, where the separate conversion pays for
+ * its launch) plus the
  * split partials (n_tokens * n_heads * splits * (2 * head_dim + 8) + 512
  * when the key range is split), else 0 (also for invalid args).  The size
  * never falls as kv_len grows at a fixed n_tokens.  No counterpart in the

@@ -585,8 +585,8 @@ static size_t gqa_prefill_ws(const mugen_attn_gqa_prefill_args* a) {
     return (size_t)a->kv_len * a->n_kv_heads * a->head_dim * 2 + 256;
 }
 
-static bool gqa_prefill_uses_v16(const mugen_attn_gqa_prefill_args* a) {
-    return a->head_dim <= 128 && a->dtype == DT_BF16 && a->n_tokens >= kPrefillV16MinTokens;
+static bool gqa_prefill_v16_capable(const mugen_attn_gqa_prefill_args* a) {
+    return a->head_dim <= 128 && a->dtype == DT_BF16;
 }
 
 // Key splits for the warp-specialised kernel.  A prompt chunk that
@@ -608,7 +608,8 @@ static PrefillSplit gqa_prefill_split(const mugen_attn_gqa_prefill_args* a) {
     if (a->kernel && a->kernel != MUGEN_ATTN_PREFILL_KERNEL_WS) return r;
     const int G = a->n_heads / a->n_kv_heads;
     const int D = padded_head_dim(a->head_dim);
-    const int dt = gqa_prefill_uses_v16(a) ? kDtBf16V16 : a->dtype;
+    // a split call with BF16 inputs also takes the fp16 V copy
+    const int dt = gqa_prefill_v16_capable(a) ? kDtBf16V16 : a->dtype;
     const int64_t units = (int64_t)ceil_div(a->n_tokens, 16) * a->n_kv_heads * gqa_prefill_ws_slices(G);
     const int64_t target = 256 * (int64_t)gqa_prefill_ws_blocks_per_cu(G, D);
     // half the CUs or more busy unsplit: the partials' round trip costs
@@ -630,6 +631,21 @@ static PrefillSplit gqa_prefill_split(const mugen_attn_gqa_prefill_args* a) {
     // range grows, so the size at the longest range covers every shorter one
     r.bytes = (size_t)a->n_tokens * a->n_heads * want * (a->head_dim * 2 + 2 * sizeof(float)) + 512;
     return r;
+}
+
+// The fp16 copy of V (one extra launch over kv_len rows): for long BF16
+// prompts, and for split chunks of 8-head blocks with ranges of 1024+ keys.
+// Those otherwise convert V in LDS at 32 keys a step (256 tokens after
+// 7936: 0.85 us per 32-key step against ~0.6 with the copy; 64.6 -> 55.7 us
+// for the call).  4-head blocks keep 32-key steps either way, and 512-key
+// ranges (64 tokens after 8000) gain less than the launch costs.  kchunk
+// grows with the key range once the split count is capped, so the choice
+// never turns off as kv_len grows.
+static bool gqa_prefill_uses_v16(const mugen_attn_gqa_prefill_args* a) {
+    if (!gqa_prefill_v16_capable(a)) return false;
+    if (a->n_tokens >= kPrefillV16MinTokens) return true;
+    const PrefillSplit s = gqa_prefill_split(a);
+    return s.ksplit > 1 && a->n_heads / a->n_kv_heads > 4 && s.kchunk >= 1024;
 }
 
 size_t mugen_attn_gqa_prefill_workspace_size(const mugen_attn_gqa_prefill_args* a) {

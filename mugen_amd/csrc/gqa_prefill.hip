@@ -518,6 +518,7 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
     const bool s_wave = w < NSW;
     const int wr = s_wave ? w : w - NSW;        // S wave index; PV wave index
     const int n = lane & 15, g = lane >> 4;
+    MUGEN_TRACE(6);
     const int t0 = qb * 16;
     const int G = p.G;
     const int nh = min(NS, G - NS * slice);     // heads of this slice
@@ -564,6 +565,9 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             lds_barrier();  // B_j: tile j landed
             if (j == 8) MUGEN_TRACE(1);
             if (j == 16) MUGEN_TRACE(5);
+            if (j == 0) MUGEN_TRACE(7);
+            if (j == 24) MUGEN_TRACE(11);
+            if (j == 28) MUGEN_TRACE(12);
             if (j == ntiles) break;
             if (!hok[0]) continue;
             const uint32_t slot_addr = ring_base + (uint32_t)((j % NSLOT) * SLOT);
@@ -687,6 +691,7 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
                 *reinterpret_cast<f32x2v_t*>(p.ws_ml + (row * p.ksplit + ks_id) * 2) = f32x2v_t{m_run[mb], l};
             }
         }
+        MUGEN_TRACE(9);
         __syncthreads();  // E: 1/l published
     } else {
         // ================================================== PV waves
@@ -770,6 +775,7 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             lds_barrier();  // B_j
             if (j == 8) MUGEN_TRACE(1);
             if (j == 16) MUGEN_TRACE(5);
+            if (j == 0) MUGEN_TRACE(7);
             if (j + NSLOT - 2 < ntiles) issue(j + NSLOT - 2);  // into the slot of tile j-2
             if constexpr (VCVT) {
                 if (j < ntiles) {
@@ -848,6 +854,7 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
                 if (j < ntiles) cv_write(j);
             if (j == 8) MUGEN_TRACE(3);
         }
+        MUGEN_TRACE(9);
         __syncthreads();  // E: the S waves' 1/l
         // lane (g, n): O[query t0+n][16d + 4g + i]
         const int tok = t0 + n;
@@ -885,6 +892,7 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             }
         }
     }
+    MUGEN_TRACE(10);
 }
 
 // ------------------------------------------------------------------ short-prompt kernel

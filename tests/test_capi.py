@@ -325,14 +325,19 @@ def test_prefill_workspace_size():
     assert size(ctypes.byref(a)) == 256 * 28 * 4 * (128 * 2 + 8) + 512
     a.causal = 0                                                 # non-causal: the same key range here
     assert size(ctypes.byref(a)) == 256 * 28 * 4 * (128 * 2 + 8) + 512
+    a.dtype = _capi.BF16                                         # BF16: the fp16 V copy first
+    assert size(ctypes.byref(a)) == 8156 * 4 * 128 * 2 + 256 + 256 * 28 * 4 * (128 * 2 + 8) + 512
+    a.dtype = _capi.F16
     a.causal, a.kernel = 1, _capi.PREFILL_KERNEL_BLOCK            # a forced non-split kernel: none
     assert size(ctypes.byref(a)) == 0
     a.kernel, a.start_pos, a.kv_len = 0, 0, 256                  # a short range: no split
     assert size(ctypes.byref(a)) == 0
     # the size never falls as the range grows (an engine sizes one workspace
     # at the end of its cache for every shorter context)
-    for n, H, Hk in [(64, 28, 4), (256, 8, 1), (48, 32, 2), (100, 32, 8)]:
-        a.n_tokens, a.n_heads, a.n_kv_heads = n, H, Hk
+    for n, H, Hk, dt in [(64, 28, 4, _capi.F16), (256, 8, 1, _capi.F16), (48, 32, 2, _capi.F16),
+                         (100, 32, 8, _capi.F16), (64, 28, 4, _capi.BF16), (256, 28, 4, _capi.BF16),
+                         (16, 8, 1, _capi.BF16), (100, 32, 8, _capi.BF16)]:
+        a.n_tokens, a.n_heads, a.n_kv_heads, a.dtype = n, H, Hk, dt
         last = 0
         for start in range(0, 20000, 37):
             a.start_pos, a.kv_len = start, start + n

@@ -19,15 +19,18 @@ pytestmark = pytest.mark.gpu
 
 
 def split_bytes(c, out_dtype, causal=True):
-    """The workspace beyond the fp16 V copy: > 0 when the call splits keys."""
+    """> 0 when the call splits keys."""
     a = _capi.GqaPrefillArgs()
     a.q = a.k = a.v = a.out = 0x1000
     a.n_tokens, a.n_heads, a.n_kv_heads, a.head_dim = c["N"], c["H"], c["Hk"], c["D"]
     a.kv_len, a.start_pos, a.causal = c["kv_len"], c["start"], int(causal)
     a.dtype, a.out_dtype = c["dtype"], out_dtype
     need = _capi.lib().mugen_attn_gqa_prefill_workspace_size(ctypes.byref(a))
-    v16 = c["kv_len"] * c["Hk"] * c["D"] * 2 + 256 if (c["dtype"] == C.BF16 and c["N"] >= 1024) else 0
-    return need - v16
+    # the fp16 V copy of BF16 prompts of 1024+ tokens is there with or
+    # without a split; below 1024 tokens anything at all means a split
+    # (partials, and for 8-head blocks over long ranges the copy as well)
+    long_v16 = c["kv_len"] * c["Hk"] * c["D"] * 2 + 256 if (c["dtype"] == C.BF16 and c["N"] >= 1024) else 0
+    return need - long_v16
 
 
 def run(c, device, out_dtype, causal=True, workspace=None, kernel=0):
@@ -50,6 +53,7 @@ def run(c, device, out_dtype, causal=True, workspace=None, kernel=0):
     (40, 16, 2, 96, 1500, C.F16),     # head_dim 96 in 128-wide tiles
     (300, 8, 1, 64, 1000, C.BF16),    # a split boundary inside some blocks' causal tail
     (1100, 8, 1, 64, 3000, C.BF16),   # with the fp16 V copy in front of the partials
+    (256, 32, 4, 64, 6000, C.BF16),   # a short chunk whose 1600-key ranges take the fp16 V copy
 ])
 @pytest.mark.parametrize("out_dtype", ["same", C.F32])
 def test_split_chunk_vs_oracle(device, N, H, Hk, D, start, dtype, out_dtype):
@@ -75,7 +79,7 @@ def test_split_equals_unsplit(device):
 
 def test_split_workspace_too_small(device):
     # a workspace that holds the V copy but not the partials: the call runs
-    # unsplit and is still correct
+    # unsplit over the copy and is still correct
     c = C.prefill_case(312, 1100, 8, 1, 64, 3000, C.BF16)
     v16 = c["kv_len"] * 1 * 64 * 2 + 256
     ws = torch.empty(v16, dtype=torch.uint8, device=device)
