@@ -450,8 +450,11 @@ void gqa_q4_test(hipStream_t st) {
 // With BF16 caches and a chunk of 1024+ tokens the provider hands the
 // library its prefill workspace (the one-launch fp16 copy of V), while the
 // direct call passes none (the kernels convert V on chip): both must agree
-// bit for bit.
-void gqa_prefill_test(hipStream_t st, int dtype, int start, int n, int max_seq) {
+// bit for bit.  A short chunk after a long context (`direct_ws`): the
+// provider's workspace holds the split key ranges' partials, and the direct
+// call passes a workspace of the size the library asks for, so both split
+// the same way and agree bit for bit.
+void gqa_prefill_test(hipStream_t st, int dtype, int start, int n, int max_seq, bool direct_ws = false) {
     mugen_attn::GqaShape s;
     s.n_layers = 1;
     s.batch = 1;
@@ -503,6 +506,18 @@ void gqa_prefill_test(hipStream_t st, int dtype, int start, int n, int max_seq) 
     pf.causal = 1;
     pf.dtype = dtype;
     pf.out_dtype = dtype;
+    std::unique_ptr<Dev> ws;
+    if (direct_ws) {
+        const size_t need = mugen_attn_gqa_prefill_workspace_size(&pf);
+        if (need == 0) {
+            std::printf("FAIL gqa prefill: no split planned for a %d-token chunk after %d\n", n, start);
+            failures++;
+        } else {
+            ws = std::make_unique<Dev>(need);
+            pf.workspace = ws->p;
+            pf.workspace_bytes = need;
+        }
+    }
     ok(mugen_attn::gqa_prefill(pf, st), "direct prefill");
     const auto o = out.get(st), o_ref = ref.get(st);
     if (o != o_ref || !(dtype == MUGEN_ATTN_BF16 ? finite_bf16(o) : finite_f16(o))) {
@@ -766,6 +781,8 @@ int main() {
     mla_test(st, 3);
     gqa_prefill_test(st, MUGEN_ATTN_F16, 200, 77, 1024);
     gqa_prefill_test(st, MUGEN_ATTN_BF16, 100, 1100, 1536);
+    gqa_prefill_test(st, MUGEN_ATTN_F16, 7000, 200, 8192, true);  // 4-head blocks, split
+    gqa_prefill_test(st, MUGEN_ATTN_BF16, 3000, 64, 4096, true);
     gqa_q4_test(st);
     prefill_batch_test(st);
     mla_prefill_test(st);
