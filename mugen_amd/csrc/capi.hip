@@ -619,8 +619,9 @@ static PrefillSplit gqa_prefill_split(const mugen_attn_gqa_prefill_args* a) {
     const int step = gqa_prefill_ws_step_keys(G, dt);
     const int kend = a->causal ? std::min(a->kv_len, a->start_pos + a->n_tokens) : a->kv_len;
     const int steps = ceil_div(kend, step);
-    constexpr int kMinSteps = 8, kMaxSplits = 16;
-    const int64_t want = std::min<int64_t>({ceil_div(target, units), (int64_t)steps / kMinSteps, kMaxSplits});
+    constexpr int kMinSteps = 8;
+    const int64_t want =
+        std::min<int64_t>({ceil_div(target, units), (int64_t)steps / kMinSteps, (int64_t)kPrefillMaxSplits});
     if (want < 2) return r;
     const int kchunk = ceil_div(steps, (int)want) * step;
     const int ks = ceil_div(kend, kchunk);

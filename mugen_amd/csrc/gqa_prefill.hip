@@ -1235,28 +1235,39 @@ constexpr int kWsTps = DT == DT_BF16 ? 1 : 2;
 // (token, head); with o_s = O_s / l_s stored, out = sum_s w_s o_s / sum_s w_s,
 // w_s = 2^(m_s - M) l_s, M the largest reference max (a split that saw no
 // key of the row: m = -inf, l = 0, weight 0)
-template <int OUT_DT>
+template <int OUT_DT, int MAXS>
 __global__ __launch_bounds__(256) void gqa_prefill_combine_kernel(GqaPrefillParams p) {
     const int dq = p.hd >> 2;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t row = i / dq;
     if (row >= (int64_t)p.N * p.H) return;
     const int c = (int)(i - row * dq);
-    const float* ml = p.ws_ml + row * p.ksplit * 2;
-    const uint16_t* o = p.ws_o + row * p.ksplit * p.hd + 4 * c;
+    const int ks = p.ksplit;  // <= MAXS
+    const f32x2v_t* ml = reinterpret_cast<const f32x2v_t*>(p.ws_ml) + row * ks;
+    const uint16_t* o = p.ws_o + row * ks * p.hd + 4 * c;
+    // every split's (max, sum) and partial requested at once, unconditionally
+    // (indices past ks re-read the last split and get weight 0): one memory
+    // round trip instead of one per split
+    f32x2v_t mls[MAXS];
+    u32x2_t h[MAXS];
+#pragma unroll
+    for (int s = 0; s < MAXS; s++) {
+        const int sc = min(s, ks - 1);
+        mls[s] = ml[sc];
+        h[s] = *reinterpret_cast<const u32x2_t*>(o + sc * p.hd);
+    }
     float M = kNegInf;
-    for (int s = 0; s < p.ksplit; s++) M = fmaxf(M, ml[2 * s]);
+#pragma unroll
+    for (int s = 0; s < MAXS; s++) M = fmaxf(M, mls[s][0]);
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
     float L = 0.f;
-    if (M != kNegInf) {
-        for (int s = 0; s < p.ksplit; s++) {
-            const float m = ml[2 * s];
-            if (m == kNegInf) continue;
-            const float w = fast_exp2(m - M) * ml[2 * s + 1];
-            const u32x2_t h = *reinterpret_cast<const u32x2_t*>(o + (int64_t)s * p.hd);
-            L += w;
-            acc += w * f32x4_t{lo_f32<DT_F16>(h[0]), hi_f32<DT_F16>(h[0]), lo_f32<DT_F16>(h[1]), hi_f32<DT_F16>(h[1])};
-        }
+#pragma unroll
+    for (int s = 0; s < MAXS; s++) {
+        const bool live = s < ks && mls[s][0] != kNegInf;
+        const float w = live ? fast_exp2(mls[s][0] - M) * mls[s][1] : 0.f;
+        L += w;
+        acc += w * f32x4_t{lo_f32<DT_F16>(h[s][0]), hi_f32<DT_F16>(h[s][0]), lo_f32<DT_F16>(h[s][1]),
+                           hi_f32<DT_F16>(h[s][1])};
     }
     const f32x4_t r = acc * (L > 0.f ? 1.f / L : 0.f);
     const int64_t base = row * p.hd + 4 * c;
@@ -1271,8 +1282,13 @@ __global__ __launch_bounds__(256) void gqa_prefill_combine_kernel(GqaPrefillPara
 template <int OUT_DT>
 static hipError_t launch_pf_combine(const GqaPrefillParams& p, hipStream_t st, KernelTimer* t) {
     const int64_t threads = (int64_t)p.N * p.H * (p.hd / 4);
-    return launch_k(t, "gqa_prefill_combine", gqa_prefill_combine_kernel<OUT_DT>,
-                    dim3((unsigned)((threads + 255) / 256)), dim3(256), st, p);
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    static_assert(kPrefillMaxSplits == 16, "merge instantiations");
+    if (p.ksplit <= 4)
+        return launch_k(t, "gqa_prefill_combine", gqa_prefill_combine_kernel<OUT_DT, 4>, grid, dim3(256), st, p);
+    if (p.ksplit <= 8)
+        return launch_k(t, "gqa_prefill_combine", gqa_prefill_combine_kernel<OUT_DT, 8>, grid, dim3(256), st, p);
+    return launch_k(t, "gqa_prefill_combine", gqa_prefill_combine_kernel<OUT_DT, 16>, grid, dim3(256), st, p);
 }
 
 int gqa_prefill_ws_slices(int G) { return G <= 4 ? 1 : (G + 7) / 8; }
@@ -1306,6 +1322,7 @@ static hipError_t launch_pf_ws_k(const GqaPrefillParams& p, int Hk, hipStream_t 
 template <int D, bool PAD, int DT, int OUT_DT>
 static hipError_t launch_pf_ws_t(const GqaPrefillParams& p, int Hk, hipStream_t st, KernelTimer* t) {
     if (p.ksplit <= 1) return launch_pf_ws_k<D, PAD, DT, OUT_DT, false>(p, Hk, st, t);
+    if (p.ksplit > kPrefillMaxSplits) return hipErrorInvalidValue;  // the merge's unrolled bound
     const hipError_t e = launch_pf_ws_k<D, PAD, DT, DT_F32, true>(p, Hk, st, t);
     return e != hipSuccess ? e : launch_pf_combine<OUT_DT>(p, st, t);
 }
