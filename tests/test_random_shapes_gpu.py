@@ -1,7 +1,8 @@
 """Seeded random shape sweeps against the CPU oracle: MLA decode / verify /
 prompt (both kernels, fp32 and 16-bit q, forced split counts), GQA decode
-(head groups 1..16, both head dims, ragged and empty sequences) and causal
-prefill (both kernels, offsets).  Every case draws its shape from its own
+(head groups 1..16, both head dims, ragged and empty sequences), causal
+prefill (both kernels, offsets) and short prompt chunks after long contexts
+(the key-split path).  Every case draws its shape from its own
 seed, so a failure names a reproducible case; sizes are bounded so the
 oracle stays fast."""
 import numpy as np
@@ -94,3 +95,34 @@ def test_prefill_random(device, seed):
     out = mugen_amd.flash_prefill_attention(q, k, v, start, out_dtype=torch.float32, kernel=kernel)
     torch.cuda.synchronize()
     C.assert_close(out.cpu().numpy(), C.prefill_ref(c, nthreads=16), f"prefill random seed={seed}")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_prefill_chunk_random(device, seed):
+    # short chunks after long contexts (the key-split path when the
+    # workspace is given: None allocates the size the library asks for),
+    # head dims padded or not, causal or not
+    r = np.random.default_rng(7000 + seed)
+    H, Hk = GQA_HEADS[int(r.integers(len(GQA_HEADS)))]
+    D = int(r.choice([64, 96, 128]))
+    N = int(r.integers(1, 300))
+    start = int(r.integers(500, 6000))
+    dt = C.F16 if r.random() < 0.5 else C.BF16
+    causal = r.random() < 0.8
+    out_dt = [torch.float32, None][int(r.integers(2))]
+    C.say(f"prefill chunk random seed={seed}: N={N} H={H} Hk={Hk} D={D} start={start} dt={dt} causal={causal} "
+          f"out={out_dt}")
+    c = C.prefill_case(8000 + seed, N, H, Hk, D, start, dt)
+    q = C.to_dev(c["qb"], dt, device)
+    k = C.to_dev(c["kb"], dt, device)
+    v = C.to_dev(c["vb"], dt, device)
+    out = mugen_amd.flash_prefill_attention(q, k, v, start, causal=causal, out_dtype=out_dt)
+    torch.cuda.synchronize()
+    if causal:
+        ref = C.prefill_ref(c, nthreads=16)
+    else:
+        kv = c["kv_len"]
+        ref = C.O.gqa_attention(c["q"], c["k"].reshape(1, kv, Hk, D).repeat(N, 0),
+                                c["v"].reshape(1, kv, Hk, D).repeat(N, 0), [kv] * N, H, Hk, D, kv * Hk * D,
+                                nthreads=16)
+    C.assert_close(out.float().cpu().numpy(), ref, f"prefill chunk random seed={seed}")
