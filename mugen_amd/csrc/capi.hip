@@ -618,6 +618,11 @@ static PrefillSplit gqa_prefill_split(const mugen_attn_gqa_prefill_args* a) {
     if (units * 2 > 256) return r;
     const int step = gqa_prefill_ws_step_keys(G, dt);
     const int kend = a->causal ? std::min(a->kv_len, a->start_pos + a->n_tokens) : a->kv_len;
+    // 4-head blocks on more than a quarter of the CUs (each running alone on
+    // its CU, faster per step than the 2-3 a split puts there) gain only
+    // over long ranges: H32 Hk8 d64, 256 tokens after 1024 measured 15.0
+    // split against 13.9 us, after 2048 19.3 against 23.4
+    if (G <= 4 && units * 4 > 256 && kend < 2048) return r;
     const int steps = ceil_div(kend, step);
     constexpr int kMinSteps = 8;
     const int64_t want =

@@ -336,7 +336,7 @@ def test_prefill_workspace_size():
     # at the end of its cache for every shorter context)
     for n, H, Hk, dt in [(64, 28, 4, _capi.F16), (256, 8, 1, _capi.F16), (48, 32, 2, _capi.F16),
                          (100, 32, 8, _capi.F16), (64, 28, 4, _capi.BF16), (256, 28, 4, _capi.BF16),
-                         (16, 8, 1, _capi.BF16), (100, 32, 8, _capi.BF16)]:
+                         (16, 8, 1, _capi.BF16), (100, 32, 8, _capi.BF16), (256, 32, 8, _capi.F16)]:
         a.n_tokens, a.n_heads, a.n_kv_heads, a.dtype = n, H, Hk, dt
         last = 0
         for start in range(0, 20000, 37):
