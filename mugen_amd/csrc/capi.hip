@@ -589,6 +589,22 @@ static bool gqa_prefill_v16_capable(const mugen_attn_gqa_prefill_args* a) {
     return a->head_dim <= 128 && a->dtype == DT_BF16;
 }
 
+// The automatic choice of the short-prompt kernel: the whole kv range fits
+// on chip, from 384 visible keys on (below that the per-block kernel's
+// shorter load phase wins: Llama-3.2-1B N = 128 4.4 against 4.9 us; N = 256
+// 5.55 against 5.6, N = 512 7.9 against 7.5)
+static bool gqa_prefill_short_default(const mugen_attn_gqa_prefill_args* a) {
+    GqaPrefillParams p{};
+    p.N = a->n_tokens;
+    p.G = a->n_heads / a->n_kv_heads;
+    p.hd = a->head_dim;
+    p.kv_len = a->kv_len;
+    p.start_pos = a->start_pos;
+    p.causal = a->causal ? 1 : 0;
+    const int kv_range = a->causal ? a->start_pos + a->n_tokens : a->kv_len;
+    return gqa_prefill_short_fits(p, padded_head_dim(a->head_dim)) && kv_range >= 384;
+}
+
 // Key splits for the warp-specialised kernel.  A prompt chunk that
 // continues a long context has few 16-token query blocks over a long key
 // range: unsplit, workgroups for fewer than half the CUs walk the
@@ -606,6 +622,7 @@ static PrefillSplit gqa_prefill_split(const mugen_attn_gqa_prefill_args* a) {
     PrefillSplit r;
     if (a->head_dim > 128 || a->n_tokens <= 0 || a->kv_len <= 0) return r;
     if (a->kernel && a->kernel != MUGEN_ATTN_PREFILL_KERNEL_WS) return r;
+    if (!a->kernel && gqa_prefill_short_default(a)) return r;  // every key on chip already
     const int G = a->n_heads / a->n_kv_heads;
     const int D = padded_head_dim(a->head_dim);
     // a split call with BF16 inputs also takes the fp16 V copy
@@ -716,20 +733,16 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     const int ws_max = a->head_dim > 64 ? INT_MAX : 4096;
     int kernel = (a->n_tokens >= 1024 && a->n_tokens <= ws_max) || p.G > 8 ? MUGEN_ATTN_PREFILL_KERNEL_WS
                                                                            : MUGEN_ATTN_PREFILL_KERNEL_BLOCK;
-    // prompts whose whole kv range fits on chip: the short-prompt kernel,
-    // from 384 visible keys on (below that the per-block kernel's shorter
-    // load phase wins: Llama-3.2-1B N = 128 4.4 against 4.9 us; N = 256 5.55
-    // against 5.6, N = 512 7.9 against 7.5)
+    // prompts whose whole kv range fits on chip: the short-prompt kernel
     const bool short_fits = gqa_prefill_short_fits(p, padded_head_dim(a->head_dim));
-    const int kv_range = a->causal ? a->start_pos + a->n_tokens : a->kv_len;
-    if (short_fits && kv_range >= 384) kernel = MUGEN_ATTN_PREFILL_KERNEL_SHORT;
+    if (gqa_prefill_short_default(a)) kernel = MUGEN_ATTN_PREFILL_KERNEL_SHORT;
     if (a->kernel == MUGEN_ATTN_PREFILL_KERNEL_SHORT && !short_fits)
         return fail(MUGEN_ATTN_E_UNSUPPORTED,
                     "gqa_prefill: the short kernel serves head_dim 64, n_heads/n_kv_heads <= 4 and <= 512 keys");
     if (a->kernel) kernel = a->kernel;
     int dt = a->dtype;
     const size_t v16_bytes = gqa_prefill_uses_v16(a) ? gqa_prefill_ws(a) : 0;
-    const PrefillSplit split = kernel == MUGEN_ATTN_PREFILL_KERNEL_SHORT ? PrefillSplit{} : gqa_prefill_split(a);
+    const PrefillSplit split = gqa_prefill_split(a);  // none for the short kernel (default or forced)
     p.ksplit = 1;
     if (split.ksplit > 1 && a->workspace && a->workspace_bytes >= v16_bytes + split.bytes) {
         // key splits (the warp-specialised kernel): partials after the V copy
