@@ -138,8 +138,10 @@ def flash_prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, s
     kernel: 0 automatic, PREFILL_KERNEL_BLOCK / _WS / _SHORT force one (_SHORT
     only for head_dim 64, <= 4 heads per kv head and <= 512 visible keys).
     workspace: the optional buffer for the fp16 copy of V (bf16 prompts of
-    1024+ tokens); None allocates one when the library asks for it, an empty
-    tensor passes none."""
+    1024+ tokens) and for the partials of split key ranges (short chunks
+    over long contexts, merged by a second launch); None allocates one when
+    the library asks for it, an empty tensor passes none (the call then runs
+    unsplit, same result to rounding)."""
     _need_cuda(q, k, v)
     if out is None:
         out = torch.empty(q.shape, dtype=out_dtype or q.dtype, device=q.device)
