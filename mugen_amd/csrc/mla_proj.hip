@@ -95,17 +95,47 @@ __device__ __forceinline__ void dequant(const WRaw<WT, N>& r, int d0, float* w) 
     }
 }
 
+// the value of lane (this lane ^ M), M = 1, 2, 4 or 8, by DPP (no LDS
+// round trip as with ds_bpermute): quad permutations for 1 and 2, a
+// half-row mirror (i -> 7 - i) then a quad reversal (i -> 3 - i) for 4, a
+// row rotation by 8 for 8
+template <int M>
+__device__ __forceinline__ float dpp_xor(float v) {
+    const int b = __float_as_int(v);
+    if constexpr (M == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false));
+    if constexpr (M == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false));
+    if constexpr (M == 4)
+        return __int_as_float(
+            __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(b, 0x141, 0xF, 0xF, false), 0x1B, 0xF, 0xF, false));
+    if constexpr (M == 8) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false));
+}
+
 // one butterfly step over lane bit M: the lane keeps half of its M/2 live
-// values (the upper half if its bit M is set) plus its partner's copy of it
+// values (the upper half if its bit M is set) plus its partner's copy of it.
+// M = 32 / 16: one v_permlane32_swap / v_permlane16_swap per pair moves both
+// halves at once (swapping x[t + N] of the lower lanes with x[t] of the
+// upper ones leaves each lane its kept value and its partner's given one,
+// whose sum is the step's result); smaller M: DPP.
 template <int M>
 __device__ __forceinline__ void halve(float* x, int lane) {
     constexpr int N = M / 2;
-    const bool up = (lane & M) != 0;
+    if constexpr (M >= 16) {
 #pragma unroll
-    for (int t = 0; t < N; t++) {
-        const float keep = up ? x[t + N] : x[t];
-        const float give = up ? x[t] : x[t + N];
-        x[t] = keep + __shfl_xor(give, M, 64);
+        for (int t = 0; t < N; t++) {
+            const auto r = M == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(x[t]), __float_as_uint(x[t + N]),
+                                                                     false, false)
+                                   : __builtin_amdgcn_permlane16_swap(__float_as_uint(x[t]), __float_as_uint(x[t + N]),
+                                                                     false, false);
+            x[t] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+    } else {
+        const bool up = (lane & M) != 0;
+#pragma unroll
+        for (int t = 0; t < N; t++) {
+            const float keep = up ? x[t + N] : x[t];
+            const float give = up ? x[t] : x[t + N];
+            x[t] = keep + dpp_xor<M>(give);
+        }
     }
 }
 
@@ -118,19 +148,43 @@ __device__ __forceinline__ void absorb_block(const MlaProjParams& p, int h, int 
     __shared__ __attribute__((aligned(16))) float qs[RC][NOPE];
     __shared__ __attribute__((aligned(16))) f32x4_t red[8][RC][64];  // [wave][row][lane] partials
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    MUGEN_TRACE(6);
     const int d0 = half * 256 + 4 * lane;
     constexpr int RB = wrow_bytes<WT>(KR);
     const uint8_t* wrow = static_cast<const uint8_t*>(p.w) + ((size_t)h * NOPE + w * IPW) * RB;
+    // a chunk's q (nope and rope parts), loaded ahead of use: the first
+    // chunk's loads go out before the weights', so that staging them (and
+    // the barrier after it) waits for q only -- loads return in order
+    const uint16_t* q = static_cast<const uint16_t*>(p.in);
+    constexpr int QPT = RC * NOPE / 512;  // nope values per thread per chunk
+    uint16_t qn[QPT], qr0 = 0, qr1 = 0;
+    auto q_load = [&](int r0, int nr) {
+#pragma unroll
+        for (int u = 0; u < QPT; u++) {
+            const int k = tid + 512 * u, r = k / NOPE, i = k % NOPE;
+            qn[u] = r < nr ? q[((int64_t)(r0 + r) * p.H + h) * (NOPE + ROPE) + i] : uint16_t(0x3c00);  // 1.0
+        }
+        if (half == 0 && tid < RC * ROPE / 2) {
+            const int r = tid / (ROPE / 2), c = tid % (ROPE / 2);
+            if (r < nr) {
+                const uint16_t* qr = q + ((int64_t)(r0 + r) * p.H + h) * (NOPE + ROPE) + NOPE;
+                qr0 = qr[c];
+                qr1 = qr[c + ROPE / 2];
+            }
+        }
+    };
+    q_load(0, min(RC, p.rows));
     WRaw<WT, 4> raw[IPW];
 #pragma unroll
     for (int k = 0; k < IPW; k++) raw[k] = wload<WT, 4>(wrow + (size_t)k * RB, d0);
-    const uint16_t* q = static_cast<const uint16_t*>(p.in);
     for (int r0 = 0; r0 < p.rows; r0 += RC) {
         const int nr = min(RC, p.rows - r0);
+        if (r0 > 0) q_load(r0, nr);
         bool zero = false;  // a zero q term in a real row of the chunk
-        for (int k = tid; k < RC * NOPE; k += 512) {
-            const int r = k / NOPE, i = k % NOPE;
-            const float v = r < nr ? to_f32<DT_F16>(q[((int64_t)(r0 + r) * p.H + h) * (NOPE + ROPE) + i]) : 1.f;
+#pragma unroll
+        for (int u = 0; u < QPT; u++) {
+            const int k = tid + 512 * u, r = k / NOPE, i = k % NOPE;
+            const float v = to_f32<DT_F16>(qn[u]);
             zero |= v == 0.f;
             qs[r][i] = r < nr ? v : 0.f;
         }
@@ -139,8 +193,7 @@ __device__ __forceinline__ void absorb_block(const MlaProjParams& p, int h, int 
             // (NeoX pairs c, c + 32, f16 results; transformer.cpp:3882-3921)
             const int r = tid / (ROPE / 2), c = tid % (ROPE / 2);
             if (r < nr) {
-                const uint16_t* qr = q + ((int64_t)(r0 + r) * p.H + h) * (NOPE + ROPE) + NOPE;
-                uint16_t y0 = qr[c], y1 = qr[c + ROPE / 2];
+                uint16_t y0 = qr0, y1 = qr1;
                 if (p.positions || p.seq_base)
                     rope_pair_f16(to_f32<DT_F16>(y0), to_f32<DT_F16>(y1),
                                   row_position(p.positions, p.seq_base, p.rows_per_seq, r0 + r), p.freqs.f[c], y0, y1);
@@ -177,8 +230,10 @@ __device__ __forceinline__ void absorb_block(const MlaProjParams& p, int h, int 
                 }
             }
         };
+        MUGEN_TRACE(7);
         if (skip_zero) accumulate(std::true_type{});
         else accumulate(std::false_type{});
+        MUGEN_TRACE(8);
 #pragma unroll
         for (int r = 0; r < RC; r++) red[w][r][lane] = acc[r];
         __syncthreads();
@@ -199,6 +254,7 @@ __device__ __forceinline__ void absorb_block(const MlaProjParams& p, int h, int 
         }
         __syncthreads();  // qs / red are rewritten by the next chunk
     }
+    MUGEN_TRACE(9);
 }
 
 template <int WT, int OUT_DT>
@@ -226,6 +282,7 @@ __global__ __launch_bounds__(256) void mla_project_kernel(MlaProjParams p) {
     constexpr int KR = 512, VH = 128, RC = 16, JW = 8;  // o rows staged per pass, output rows per wave
     __shared__ __attribute__((aligned(16))) float os[RC][KR];
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    MUGEN_TRACE(10);
     const int j0 = blockIdx.y * 32 + JW * w;
     const int d0 = 8 * lane;
     constexpr int RB = wrow_bytes<WT>(KR);
@@ -233,22 +290,37 @@ __global__ __launch_bounds__(256) void mla_project_kernel(MlaProjParams p) {
     WRaw<WT, 8> raw[JW];
 #pragma unroll
     for (int j = 0; j < JW; j++) raw[j] = wload<WT, 8>(wrow + (size_t)j * RB, d0);
+    // the first pass's o rows requested with the weights (two round trips
+    // in flight together instead of one after the other)
+    const float* o = static_cast<const float*>(p.in);
+    constexpr int OPT = RC * KR / 4 / 256;  // 16-byte o loads per thread per pass
+    auto o_load = [&](int r0, int nr, f32x4_t* dst) {
+#pragma unroll
+        for (int i = 0; i < OPT; i++) {
+            const int k = tid + 256 * i, r = k / (KR / 4), c4 = k % (KR / 4);
+            dst[i] = r < nr ? *reinterpret_cast<const f32x4_t*>(o + ((int64_t)(r0 + r) * p.H + h) * KR + 4 * c4)
+                            : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    f32x4_t ov[OPT];
+    o_load(0, min(RC, p.rows), ov);
     float wv[JW][8];
 #pragma unroll
     for (int j = 0; j < JW; j++) dequant<WT, 8>(raw[j], d0, wv[j]);
-    const float* o = static_cast<const float*>(p.in);
+    MUGEN_TRACE(11);
     // after the butterfly, lane pair (2v, 2v+1) holds sum v = 8 * row + j
     const int v = lane >> 1;
     for (int r0 = 0; r0 < p.rows; r0 += RC) {
         const int nr = min(RC, p.rows - r0);
+        if (r0 > 0) o_load(r0, nr, ov);
         __syncthreads();
-        for (int k = tid; k < RC * KR / 4; k += 256) {
-            const int r = k / (KR / 4), c4 = k % (KR / 4);
-            *reinterpret_cast<f32x4_t*>(&os[r][4 * c4]) =
-                r < nr ? *reinterpret_cast<const f32x4_t*>(o + ((int64_t)(r0 + r) * p.H + h) * KR + 4 * c4)
-                       : f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < OPT; i++) {
+            const int k = tid + 256 * i, r = k / (KR / 4), c4 = k % (KR / 4);
+            *reinterpret_cast<f32x4_t*>(&os[r][4 * c4]) = ov[i];
         }
         __syncthreads();
+        MUGEN_TRACE(12);
         for (int rs = 0; rs < nr; rs += 4) {
             float x[32];  // x[8 * r + j]: rows rs..rs+3 x this wave's 8 output rows, over this lane's 8 dims
 #pragma unroll
@@ -275,12 +347,13 @@ __global__ __launch_bounds__(256) void mla_project_kernel(MlaProjParams p) {
             halve<8>(x, lane);
             halve<4>(x, lane);
             halve<2>(x, lane);
-            const float tot = x[0] + __shfl_xor(x[0], 1, 64);
+            const float tot = x[0] + dpp_xor<1>(x[0]);
             const int r = v >> 3, j = v & 7;
             if ((lane & 1) == 0 && rs + r < nr)
                 store_out<OUT_DT>(p.out, ((int64_t)(r0 + rs + r) * p.H + h) * VH + j0 + j, tot);
         }
     }
+    MUGEN_TRACE(13);
 }
 
 // ---------------------------------------------------------------- MFMA forms
