@@ -212,16 +212,37 @@ __device__ __forceinline__ u32x2_t lds_read_tr16(const uint16_t* p) {
     return __builtin_bit_cast(u32x2_t, v);
 }
 
-// block-wide (wave64 x nwaves) max / sum through a small LDS scratch
+// the value of lane (this lane ^ M), M = 1, 2, 4 or 8, by DPP (no LDS
+// round trip as with ds_bpermute): quad permutations for 1 and 2, a
+// half-row mirror (i -> 7 - i) then a quad reversal (i -> 3 - i) for 4, a
+// row rotation by 8 for 8
+template <int M>
+__device__ __forceinline__ float dpp_xor(float v) {
+    const int b = __float_as_int(v);
+    if constexpr (M == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false));
+    if constexpr (M == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false));
+    if constexpr (M == 4)
+        return __int_as_float(
+            __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(b, 0x141, 0xF, 0xF, false), 0x1B, 0xF, 0xF, false));
+    if constexpr (M == 8) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false));
+}
+
+// max / sum over the wave's 64 lanes, in every lane: lane swaps for 32 and
+// 16 apart, DPP below (the pairs of the xor butterfly 32, 16, .., 1, so the
+// sum's order is that butterfly's)
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-    return v;
+    v = max_x16(max_x32(v));
+    v = fmaxf(v, dpp_xor<8>(v));
+    v = fmaxf(v, dpp_xor<4>(v));
+    v = fmaxf(v, dpp_xor<2>(v));
+    return fmaxf(v, dpp_xor<1>(v));
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-    return v;
+    v = sum_x16(sum_x32(v));
+    v += dpp_xor<8>(v);
+    v += dpp_xor<4>(v);
+    v += dpp_xor<2>(v);
+    return v + dpp_xor<1>(v);
 }
 
 // Split-K log-sum-exp weights for one output row: given the (m, l) pairs of

@@ -95,21 +95,6 @@ __device__ __forceinline__ void dequant(const WRaw<WT, N>& r, int d0, float* w) 
     }
 }
 
-// the value of lane (this lane ^ M), M = 1, 2, 4 or 8, by DPP (no LDS
-// round trip as with ds_bpermute): quad permutations for 1 and 2, a
-// half-row mirror (i -> 7 - i) then a quad reversal (i -> 3 - i) for 4, a
-// row rotation by 8 for 8
-template <int M>
-__device__ __forceinline__ float dpp_xor(float v) {
-    const int b = __float_as_int(v);
-    if constexpr (M == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false));
-    if constexpr (M == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false));
-    if constexpr (M == 4)
-        return __int_as_float(
-            __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(b, 0x141, 0xF, 0xF, false), 0x1B, 0xF, 0xF, false));
-    if constexpr (M == 8) return __int_as_float(__builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false));
-}
-
 // one butterfly step over lane bit M: the lane keeps half of its M/2 live
 // values (the upper half if its bit M is set) plus its partner's copy of it.
 // M = 32 / 16: one v_permlane32_swap / v_permlane16_swap per pair moves both
