@@ -237,6 +237,16 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp_xor<2>(v));
     return fmaxf(v, dpp_xor<1>(v));
 }
+__device__ __forceinline__ int wave_min_i32(int v) {
+    const auto r32 = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    v = min((int)r32[0], (int)r32[1]);
+    const auto r16 = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+    v = min((int)r16[0], (int)r16[1]);
+    v = min(v, __float_as_int(dpp_xor<8>(__int_as_float(v))));
+    v = min(v, __float_as_int(dpp_xor<4>(__int_as_float(v))));
+    v = min(v, __float_as_int(dpp_xor<2>(__int_as_float(v))));
+    return min(v, __float_as_int(dpp_xor<1>(__int_as_float(v))));
+}
 __device__ __forceinline__ float wave_sum(float v) {
     v = sum_x16(sum_x32(v));
     v += dpp_xor<8>(v);

@@ -265,9 +265,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
         }
     }
     // smallest visible length over the wave's rows: tiles below it need no mask
-    int teff_min = teff;
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) teff_min = min(teff_min, __shfl_xor(teff_min, m, 64));
+    const int teff_min = wave_min_i32(teff);
 
     // Q loads complete here, through a wait the compiler's wait-count pass
     // understands: it then inserts no vmcnt(0) inside the tile loop (where
@@ -584,10 +582,7 @@ __global__ __launch_bounds__(512) void mla_decode_ws_kernel(MlaParams p) {
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) qf[0][ks] = ok ? load16(qp + 32 * ks) : u32x4_t{0, 0, 0, 0};
         }
-        int teff_min = teff;
-#pragma unroll
-        for (int m = 1; m < 64; m <<= 1) teff_min = min(teff_min, __shfl_xor(teff_min, m, 64));
-        teff_min = __builtin_amdgcn_readfirstlane(teff_min);  // wave-uniform: the mask test branches on it
+        const int teff_min = __builtin_amdgcn_readfirstlane(wave_min_i32(teff));  // wave-uniform: the mask test branches on it
         // q is waited for chunk by chunk in the first tile's k-loop
         MUGEN_TRACE(1);
         const int ar0 = 8 * (n >> 2) + (n & 3);
