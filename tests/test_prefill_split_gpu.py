@@ -115,3 +115,32 @@ def test_split_large_scores(device):
     c["k"], c["kb"] = k, kbits
     assert split_bytes(c, C.F32) > 0
     C.assert_close(run(c, device, C.F32), C.prefill_ref(c, nthreads=16), "split with a dominant key band")
+
+
+def test_split_graph_replays(device):
+    # the split call (fp16 V copy, partials, merge) captured in a graph and
+    # replayed with eager work between the replays: every replay equals the
+    # eager result bit for bit
+    c = C.prefill_case(316, 256, 28, 4, 128, 7936, C.BF16)
+    assert split_bytes(c, C.BF16) > 0
+    q = C.to_dev(c["qb"], C.BF16, device)
+    k = C.to_dev(c["kb"], C.BF16, device)
+    v = C.to_dev(c["vb"], C.BF16, device)
+    ws = mugen_amd.prefill_workspace(q, k, v, c["start"])
+    eager = mugen_amd.flash_prefill_attention(q, k, v, c["start"], workspace=ws)
+    torch.cuda.synchronize()
+    out = torch.empty_like(eager)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            mugen_amd.flash_prefill_attention(q, k, v, c["start"], out=out, workspace=ws)
+    torch.cuda.synchronize()
+    for i in range(3):
+        out.fill_(float("nan"))
+        ws.fill_(0x7f)
+        g.replay()
+        torch.cuda.synchronize()
+        C.say(f"split graph replay {i}")
+        assert torch.equal(out, eager), f"replay {i} differs from the eager call"
