@@ -607,13 +607,13 @@ static bool gqa_prefill_short_default(const mugen_attn_gqa_prefill_args* a) {
 
 // Key splits for the warp-specialised kernel.  A prompt chunk that
 // continues a long context has few 16-token query blocks over a long key
-// range: unsplit, workgroups for fewer than half the CUs walk the
-// whole range each.  Each block's keys are then split into ranges of whole
-// steps (at least kMinSteps, so that the partials' merge stays a small part
-// of the call) until the work list fills about one round; the partials
-// (fp16 O / l, fp32 max and sum) go to the workspace after the fp16 V copy, and gqa_prefill_combine merges
-// them.  The plan depends on the arguments only, so the workspace size
-// function and the call agree.
+// range: unsplit, workgroups for fewer than half the CUs walk the whole
+// range each.  Each block's keys are then split into ranges of whole steps
+// (at least kMinSteps, so that the partials' merge stays a small part of
+// the call) until the work list fills about one round; the partials (fp16
+// O / l, fp32 max and sum) go to the workspace after the fp16 V copy, and
+// gqa_prefill_combine merges them.  The plan depends on the arguments only,
+// so the workspace size function and the call agree.
 struct PrefillSplit {
     int ksplit = 1, kchunk = 0;
     size_t bytes = 0;  // partial O and (max, sum) of every row and split
