@@ -454,12 +454,13 @@ void gqa_q4_test(hipStream_t st) {
 // provider's workspace holds the split key ranges' partials, and the direct
 // call passes a workspace of the size the library asks for, so both split
 // the same way and agree bit for bit.
-void gqa_prefill_test(hipStream_t st, int dtype, int start, int n, int max_seq, bool direct_ws = false) {
+void gqa_prefill_test(hipStream_t st, int dtype, int start, int n, int max_seq, bool direct_ws = false,
+                      int n_heads = 32, int n_kv_heads = 8) {
     mugen_attn::GqaShape s;
     s.n_layers = 1;
     s.batch = 1;
-    s.n_heads = 32;
-    s.n_kv_heads = 8;
+    s.n_heads = n_heads;
+    s.n_kv_heads = n_kv_heads;
     s.head_dim = 128;
     s.max_seq_len = max_seq;
     s.kv_dtype = dtype;
@@ -783,6 +784,7 @@ int main() {
     gqa_prefill_test(st, MUGEN_ATTN_BF16, 100, 1100, 1536);
     gqa_prefill_test(st, MUGEN_ATTN_F16, 7000, 200, 8192, true);  // 4-head blocks, split
     gqa_prefill_test(st, MUGEN_ATTN_BF16, 3000, 64, 4096, true);
+    gqa_prefill_test(st, MUGEN_ATTN_BF16, 7000, 256, 8192, true, 28, 4);  // 8-head blocks: split + fp16 V copy
     gqa_q4_test(st);
     prefill_batch_test(st);
     mla_prefill_test(st);
