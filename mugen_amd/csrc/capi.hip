@@ -609,8 +609,8 @@ static bool gqa_prefill_short_default(const mugen_attn_gqa_prefill_args* a) {
 // continues a long context has few 16-token query blocks over a long key
 // range: unsplit, workgroups for fewer than half the CUs walk the whole
 // range each.  Each block's keys are then split into ranges of whole steps
-// (at least kMinSteps, so that the partials' merge stays a small part of
-// the call) until the work list fills about one round; the partials (fp16
+// (at least kMinKeys, so that the partials' merge stays a small part of the
+// call) until the work list fills about one round; the partials (fp16
 // O / l, fp32 max and sum) go to the workspace after the fp16 V copy, and
 // gqa_prefill_combine merges them.  The plan depends on the arguments only,
 // so the workspace size function and the call agree.
@@ -641,9 +641,12 @@ static PrefillSplit gqa_prefill_split(const mugen_attn_gqa_prefill_args* a) {
     // split against 13.9 us, after 2048 19.3 against 23.4
     if (G <= 4 && units * 4 > 256 && kend < 2048) return r;
     const int steps = ceil_div(kend, step);
-    constexpr int kMinSteps = 8;
+    // ranges of at least 256 keys (4 steps of 64, 8 of 32): verify-sized
+    // chunks (5 tokens after 4000, 7B shape) 18.1 -> 13.8 us against 512
+    // keys; 4-head blocks at 128 keys measured slower (9.2 -> 10.3 us)
+    constexpr int kMinKeys = 256;
     const int64_t want =
-        std::min<int64_t>({ceil_div(target, units), (int64_t)steps / kMinSteps, (int64_t)kPrefillMaxSplits});
+        std::min<int64_t>({ceil_div(target, units), (int64_t)steps / (kMinKeys / step), (int64_t)kPrefillMaxSplits});
     if (want < 2) return r;
     const int kchunk = ceil_div(steps, (int)want) * step;
     const int ks = ceil_div(kend, kchunk);

@@ -1283,12 +1283,14 @@ template <int OUT_DT>
 static hipError_t launch_pf_combine(const GqaPrefillParams& p, hipStream_t st, KernelTimer* t) {
     const int64_t threads = (int64_t)p.N * p.H * (p.hd / 4);
     const dim3 grid((unsigned)((threads + 255) / 256));
-    static_assert(kPrefillMaxSplits == 16, "merge instantiations");
+    static_assert(kPrefillMaxSplits == 32, "merge instantiations");
     if (p.ksplit <= 4)
         return launch_k(t, "gqa_prefill_combine", gqa_prefill_combine_kernel<OUT_DT, 4>, grid, dim3(256), st, p);
     if (p.ksplit <= 8)
         return launch_k(t, "gqa_prefill_combine", gqa_prefill_combine_kernel<OUT_DT, 8>, grid, dim3(256), st, p);
-    return launch_k(t, "gqa_prefill_combine", gqa_prefill_combine_kernel<OUT_DT, 16>, grid, dim3(256), st, p);
+    if (p.ksplit <= 16)
+        return launch_k(t, "gqa_prefill_combine", gqa_prefill_combine_kernel<OUT_DT, 16>, grid, dim3(256), st, p);
+    return launch_k(t, "gqa_prefill_combine", gqa_prefill_combine_kernel<OUT_DT, 32>, grid, dim3(256), st, p);
 }
 
 int gqa_prefill_ws_slices(int G) { return G <= 4 ? 1 : (G + 7) / 8; }

@@ -139,7 +139,7 @@ int gqa_prefill_ws_step_keys(int G, int dt);
 int gqa_prefill_ws_blocks_per_cu(int G, int D);
 int gqa_prefill_ws_slices(int G);
 // most key splits the planner gives a prefill call (the merge unrolls to it)
-constexpr int kPrefillMaxSplits = 16;
+constexpr int kPrefillMaxSplits = 32;
 // dt code for launch_gqa_prefill: bf16 q / K with V already converted to fp16
 constexpr int kDtBf16V16 = 100;
 // fp16 copy of n bf16 values (n a multiple of 8, 16-byte aligned buffers)
