@@ -109,6 +109,26 @@ def test_gqa_prefill_short_guarded(device, N, start):
     C.assert_close(out.t.float().cpu().numpy(), ref, f"guarded short prefill N={N}")
 
 
+@pytest.mark.parametrize("N,H,Hk,D,start,dt", [(77, 28, 4, 128, 6000, C.BF16), (5, 32, 8, 96, 3000, C.F16),
+                                               (200, 32, 2, 64, 2500, C.BF16)])
+def test_gqa_prefill_split_guarded(device, N, H, Hk, D, start, dt):
+    # the key-split path: the fp16 V copy, the partials and the merge write
+    # only inside the workspace and the output (a ragged last query block,
+    # padded head_dim, two 8-head slices)
+    c = C.prefill_case(520 + N, N, H, Hk, D, start, dt)
+    C.say(f"guarded gqa_prefill split N={N} H={H} Hk={Hk} D={D} start={start} dt={dt}")
+    q = C.to_dev(c["qb"], dt, device)
+    k = C.to_dev(c["kb"], dt, device)
+    v = C.to_dev(c["vb"], dt, device)
+    out = Guarded((N, H, D), torch.float32, device)
+    need = mugen_amd.prefill_workspace(q, k, v, start, out_dtype=torch.float32).numel()
+    assert need > 0
+    ws = guarded_ws(need, device)
+    mugen_amd.flash_prefill_attention(q, k, v, start, out=out.t, workspace=ws.t)
+    assert out.intact() and ws.intact(), "guard band overwritten (split prefill)"
+    C.assert_close(out.t.cpu().numpy(), C.prefill_ref(c, nthreads=16), f"guarded split prefill N={N}")
+
+
 def test_kv_append_guarded(device):
     # rows at positions >= max_seq_len are dropped, negative lengths too
     B, max_T, row = 3, 64, 512
