@@ -170,19 +170,29 @@ static int64_t gqa_items(const mugen_attn_gqa_decode_args* a, int chunk, int ext
 }
 
 // GQA decode: a workgroup's 4 waves take 32-token blocks round-robin, so
-// chunks are multiples of 32 tokens, at least 128 (one block per wave).  The
-// kernel holds two 256-thread workgroups per CU; the plan is the smallest
-// chunk whose work list fits ONE dispatch round of 512 workgroups (every CU
-// streaming, no second round), with at most kMaxSplits splits per sequence.
-// The 32-token step keeps the round fuller than 128-token steps would (the
-// CUs holding two workgroups set the time): Qwen2.5-7B B16 ragged decode
-// 19.0 -> 18.2 us.
+// chunks are multiples of 32 tokens, at least 64.  The kernel holds two
+// 256-thread workgroups per CU; the plan is the smallest chunk whose work
+// list fits ONE dispatch round of 512 workgroups (every CU streaming, no
+// second round) and splits the longest sequence at most 32 ways.  The
+// 32-token step keeps the round fuller than 128-token steps would (the CUs
+// holding two workgroups set the time): Qwen2.5-7B B16 ragged decode 19.0
+// -> 18.2 us.  The 32-way cap (with the floor lowered from 128 to 64
+// tokens): B1 T2048 7.38 -> 6.87 us, T8192 10.83 -> 9.17, B2 T8192 12.98
+// -> 10.0; B16 and B1 T4096 unchanged (their plans were ~32 splits).
 static int gqa_chunk(const mugen_attn_gqa_decode_args* a, int extra = 0) {
-    constexpr int q = 32, qmin = 128;
+    constexpr int q = 32, qmin = 64, kSplitCap = 32;
     const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
     if (a->num_splits > 0) return explicit_chunk(maxT, a->num_splits, q, kMaxSplits - 1);
     const int cmax = ceil_div(maxT, q) * q;
-    const int cmin = ceil_div(ceil_div(maxT, kMaxSplits - 1), q) * q;
+    // the longest sequence (host lengths when given) in at most kSplitCap
+    // splits: more, shorter splits cost the merge more than they shorten
+    // the tile chains
+    int tlong = maxT;
+    if (a->seq_lens_host) {
+        tlong = 1;
+        for (int b = 0; b < a->batch; b++) tlong = std::max(tlong, std::min(a->seq_lens_host[b], maxT));
+    }
+    const int cmin = std::max(ceil_div(ceil_div(maxT, kMaxSplits - 1), q), ceil_div(ceil_div(tlong, kSplitCap), q)) * q;
     // one dispatch round: two workgroups per CU, one at head_dim 256 (one
     // wave per SIMD)
     const int64_t budget = a->head_dim > 128 ? 256 : 512;
