@@ -291,7 +291,8 @@ static int64_t mla_units(const mugen_attn_mla_decode_args* a, int chunk, int64_t
 // lane, 108 KiB LDS), and each workgroup pays a fixed cost (Q fragments,
 // ring fill, partial store) on top of ~1.8 us per 32-token tile.  The plan:
 // the smallest chunk (multiple of 32) whose nrb * active groups fit ONE
-// dispatch round of 256 CUs -- maximum parallelism, no second round.
+// dispatch round of 256 CUs -- maximum parallelism, no second round -- with
+// the longest sequence split at most 32 ways.
 static int mla_chunk(const mugen_attn_mla_decode_args* a, int kernel) {
     const int q = mla_tile_tokens(kernel);  // chunks are whole tiles
     if (a->num_splits > 0) return explicit_chunk(a->max_seq_len, a->num_splits, q, kMaxMlaSplits);
@@ -299,7 +300,18 @@ static int mla_chunk(const mugen_attn_mla_decode_args* a, int kernel) {
     const int64_t nrb = ceil_div(R, mla_rows_per_block(kernel));
     const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
     const int cmax = ceil_div(maxT, q) * q;
-    const int cmin = ceil_div(ceil_div(maxT, kMaxMlaSplits), q) * q;
+    // the longest sequence (host lengths when given) in at most kSplitCap
+    // splits: small batches otherwise fill the round with one-tile splits
+    // whose merge costs more than the tiles (DeepSeek-V2-Lite heads, B1
+    // T8192: 256 splits 36.5 us, 32 splits 16.9; one V3 sequence at T8192
+    // 26.0 -> 17.3 us)
+    constexpr int kSplitCap = 32;
+    int tlong = maxT;
+    if (a->seq_lens_host) {
+        tlong = 1;
+        for (int b = 0; b < a->batch; b++) tlong = std::max(tlong, std::min(a->seq_lens_host[b], maxT));
+    }
+    const int cmin = std::max(ceil_div(ceil_div(maxT, kMaxMlaSplits), q), ceil_div(ceil_div(tlong, kSplitCap), q)) * q;
     const int64_t wg_budget = 256;
     if (mla_units(a, cmax, nrb) > wg_budget) return cmax;  // one split per sequence already fills a round
     int lo = cmin < q ? q : cmin, hi = cmax;               // units(c) is non-increasing in c
