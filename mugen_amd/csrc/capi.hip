@@ -749,15 +749,18 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     p.causal = a->causal ? 1 : 0;
     const float scale = a->scale > 0.f ? a->scale : 1.f / sqrtf((float)a->head_dim);
     p.scale_log2 = scale * kLog2e;
-    // the warp-specialised kernel where it measured faster: prompts from
-    // 1024 tokens, at head_dim 64 up to 4096 (bf16, eager calls: Qwen2.5-7B
-    // shape N = 8192 603 against 690 us, N = 32768 8.76 against 8.86 ms;
-    // Llama-3.2-1B shape N = 4096 114 against 116 us, N = 8192 423 against
-    // 381), and for more than 8 heads per kv head (it takes them in slices
-    // of 8); args->kernel forces one
-    const int ws_max = a->head_dim > 64 ? INT_MAX : 4096;
-    int kernel = (a->n_tokens >= 1024 && a->n_tokens <= ws_max) || p.G > 8 ? MUGEN_ATTN_PREFILL_KERNEL_WS
-                                                                           : MUGEN_ATTN_PREFILL_KERNEL_BLOCK;
+    // the warp-specialised kernel where it measured faster: every prompt
+    // above head_dim 64 (graph replays: Qwen2.5-7B shape N = 16 / 256 / 768
+    // 5.9 / 10.7 / 21.6 against 7.5 / 11.9 / 22.4 us, H32 Hk8 d128 N = 768
+    // 18.0 against 26.5; eager: N = 8192 603 against 690 us, 32768 8.76
+    // against 8.86 ms), at head_dim 64 from 1024 to 4096 tokens (Llama-3.2-1B
+    // shape N = 4096 114 against 116 us, N = 8192 423 against 381; below 1024
+    // the per-block and short-prompt kernels lead: N = 512 7.7 against 9.2),
+    // and for more than 8 heads per kv head (it takes them in slices of 8);
+    // args->kernel forces one
+    const bool ws_default =
+        a->head_dim > 64 || (a->n_tokens >= 1024 && a->n_tokens <= 4096) || p.G > 8;
+    int kernel = ws_default ? MUGEN_ATTN_PREFILL_KERNEL_WS : MUGEN_ATTN_PREFILL_KERNEL_BLOCK;
     // prompts whose whole kv range fits on chip: the short-prompt kernel
     const bool short_fits = gqa_prefill_short_fits(p, padded_head_dim(a->head_dim));
     if (gqa_prefill_short_default(a)) kernel = MUGEN_ATTN_PREFILL_KERNEL_SHORT;
