@@ -755,11 +755,13 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
     // 18.0 against 26.5; eager: N = 8192 603 against 690 us, 32768 8.76
     // against 8.86 ms), at head_dim 64 from 1024 to 4096 tokens (Llama-3.2-1B
     // shape N = 4096 114 against 116 us, N = 8192 423 against 381; below 1024
-    // the per-block and short-prompt kernels lead: N = 512 7.7 against 9.2),
-    // and for more than 8 heads per kv head (it takes them in slices of 8);
-    // args->kernel forces one
+    // the per-block and short-prompt kernels lead: N = 512 7.7 against 9.2);
+    // args->kernel forces one.  At head_dim 64 the limits above are the
+    // 4-head blocks' (G <= 4); its 8-head blocks (G > 4) lead at every length
+    // (H28 Hk4 d64 N = 6144 203 against 245 us, H16 Hk2 N = 256 7.4 against
+    // 8.0; within 1 us either way at N = 512)
     const bool ws_default =
-        a->head_dim > 64 || (a->n_tokens >= 1024 && a->n_tokens <= 4096) || p.G > 8;
+        a->head_dim > 64 || p.G > 4 || (a->n_tokens >= 1024 && a->n_tokens <= 4096);
     int kernel = ws_default ? MUGEN_ATTN_PREFILL_KERNEL_WS : MUGEN_ATTN_PREFILL_KERNEL_BLOCK;
     // prompts whose whole kv range fits on chip: the short-prompt kernel
     const bool short_fits = gqa_prefill_short_fits(p, padded_head_dim(a->head_dim));
