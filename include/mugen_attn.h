@@ -239,7 +239,8 @@ typedef struct mugen_attn_gqa_prefill_args {
      * one kernel (same results within rounding; for kernel comparisons) */
     int32_t kernel;
     /* optional workspace (NULL / 0: none).  For BF16 prompts of at least
-     * 1024 tokens (and split calls, below), given at least kv_len *
+     * 1024 tokens (and split calls, below, of more than 4 heads per kv head
+     * over ranges of 1024+ keys), given at least kv_len *
      * n_kv_heads * head_dim * 2 + 256 bytes
      * (mugen_attn_gqa_prefill_workspace_size), the call first copies
      * V[0, kv_len) to fp16 there (one extra launch), so the attention
@@ -263,7 +264,7 @@ typedef struct mugen_attn_gqa_prefill_args {
 int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* args, void* stream);
 /* Bytes of the optional prefill workspace worth passing: the fp16 V copy
  * (kv_len * n_kv_heads * head_dim * 2 + 256 for BF16 prompts of at least
- * 1024 tokens and for split calls, where the separate conversion pays for
+ * 1024 tokens and for some split calls, where the separate conversion pays for
  * its launch) plus the
  * split partials (n_tokens * n_heads * splits * (2 * head_dim + 8) + 512
  * when the key range is split), else 0 (also for invalid args).  The size
