@@ -264,12 +264,12 @@ typedef struct mugen_attn_gqa_prefill_args {
 int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* args, void* stream);
 /* Bytes of the optional prefill workspace worth passing: the fp16 V copy
  * (kv_len * n_kv_heads * head_dim * 2 + 256 for BF16 prompts of at least
- * 1024 tokens and for some split calls, where the separate conversion pays for
- * its launch) plus the
- * split partials (n_tokens * n_heads * splits * (2 * head_dim + 8) + 512
- * when the key range is split), else 0 (also for invalid args).  The size
- * never falls as kv_len grows at a fixed n_tokens.  No counterpart in the
- * reference (it runs each chunk on one pass over its keys). */
+ * 1024 tokens and for some split calls, where the separate conversion pays
+ * for its launch) plus the split partials (n_tokens * n_heads * splits *
+ * (2 * head_dim + 8) + 512 when the key range is split), else 0 (also for
+ * invalid args).  The size never falls as kv_len grows at a fixed n_tokens.
+ * No counterpart in the reference (it runs each chunk on one pass over its
+ * keys). */
 size_t mugen_attn_gqa_prefill_workspace_size(const mugen_attn_gqa_prefill_args* args);
 
 /*
