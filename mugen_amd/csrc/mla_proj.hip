@@ -366,12 +366,14 @@ __global__ __launch_bounds__(256) void mla_project_kernel(MlaProjParams p) {
 // the B operand straight from global memory (8 consecutive nope dims per
 // lane).  Lane (g, n) ends with 4 consecutive columns of row n: one 16-byte
 // store.
+// one absorb workgroup (256 threads): head h, column quarter cq, row groups
+// z, z + nz, ..
 template <int WT, int OUT_DT>
-__global__ __launch_bounds__(256) void mla_absorb_mfma_kernel(MlaProjParams p) {
+__device__ __forceinline__ void absorb_mfma_block(const MlaProjParams& p, int h, int cq, int z, int nz) {
     constexpr int NOPE = 128, ROPE = 64, KR = 512, CQ = 128, RB = CQ * 2;  // LDS row bytes per plane
     constexpr int WRB = wrow_bytes<WT>(KR);
     __shared__ __attribute__((aligned(16))) char wl[2][NOPE * RB];  // [hi|lo][nope row][128 columns]
-    const int h = blockIdx.x, cq = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
     auto swz = [](int r) { return ((r & 1) * 2) ^ (((r >> 1) & 1) * 4) ^ (((r >> 3) & 1) * 8) ^ ((r >> 4) & 1); };
     MUGEN_TRACE(0);
@@ -387,7 +389,7 @@ __global__ __launch_bounds__(256) void mla_absorb_mfma_kernel(MlaProjParams p) {
                 qraw[rb][kk] = load16(q + ((int64_t)r * p.H + h) * (NOPE + ROPE) + 32 * kk + 8 * g);
         }
     };
-    load_q(blockIdx.z * 64);  // in flight during the dequantisation
+    load_q(z * 64);  // in flight during the dequantisation
     {   // dequantise the quarter: 128 rows x 16 chunks of 8 columns, all
         // of a thread's loads issued before any conversion
         const uint8_t* wh = static_cast<const uint8_t*>(p.w) + (size_t)h * NOPE * WRB;
@@ -420,8 +422,8 @@ __global__ __launch_bounds__(256) void mla_absorb_mfma_kernel(MlaProjParams p) {
     MUGEN_TRACE(1);
     __syncthreads();
     MUGEN_TRACE(2);
-    for (int r0 = blockIdx.z * 64; r0 < p.rows; r0 += gridDim.z * 64) {
-        if (r0 != blockIdx.z * 64) load_q(r0);
+    for (int r0 = z * 64; r0 < p.rows; r0 += nz * 64) {
+        if (r0 != z * 64) load_q(r0);
         {   // q_rope appended: as is, or rotated by the reference's q RoPE
             // stage (NeoX pairs c, c + 32, f16 results); the 4 quarter
             // workgroups of a row group take 16 of its rows each
@@ -498,6 +500,28 @@ __global__ __launch_bounds__(256) void mla_absorb_mfma_kernel(MlaProjParams p) {
         }
     }
     MUGEN_TRACE(5);
+}
+
+template <int WT, int OUT_DT>
+__global__ __launch_bounds__(256) void mla_absorb_mfma_kernel(MlaProjParams p) {
+    absorb_mfma_block<WT, OUT_DT>(p, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.z);
+}
+
+// One launch for the latent write and the absorption at prompt sizes: the
+// first H * 4 * nz workgroups absorb (the order of mla_absorb_mfma_kernel's
+// grid: head fastest, then column quarter, then row group), the rest write
+// the new tokens' latent rows, one wave per token, beside them on the CUs
+// (no LDS of their own)
+template <int WT, int OUT_DT, int LDT>
+__global__ __launch_bounds__(256) void mla_prepare_mfma_kernel(MlaProjParams pa, LatentWriteParams pl, int nz) {
+    const int nab = pa.H * 4 * nz;
+    const int bx = (int)blockIdx.x;
+    if (bx < nab) {
+        absorb_mfma_block<WT, OUT_DT>(pa, bx % pa.H, (bx / pa.H) % 4, bx / (pa.H * 4), nz);
+        return;
+    }
+    const int r = (bx - nab) * 4 + (int)(threadIdx.x >> 6);
+    if (r < pl.rows) latent_write_row<LDT>(pl, r, threadIdx.x & 63);
 }
 
 // project: workgroup = (head, half of the 128 output rows j, row group);
@@ -599,14 +623,18 @@ __global__ __launch_bounds__(256) void mla_project_mfma_kernel(MlaProjParams p) 
     }
 }
 
+// absorb MFMA form: row groups of 64, enough workgroups for ~two per CU,
+// each group of a workgroup reusing its dequantised quarter
+static int absorb_mfma_groups(const MlaProjParams& p) {
+    const int groups = (p.rows + 63) / 64;
+    const int per = std::max(1, 512 / (p.H * 4));
+    return std::min(groups, per);
+}
+
 template <int WT>
 static hipError_t launch_absorb_w(const MlaProjParams& p, int out_dt, hipStream_t st, KernelTimer* t) {
     if (p.rows >= kProjMfmaRows) {
-        // row groups of 64: enough workgroups for ~two per CU, each group
-        // of a workgroup reusing its dequantised quarter
-        const int groups = (p.rows + 63) / 64;
-        const int per = std::max(1, 512 / (p.H * 4));
-        const dim3 grid(p.H, 4, std::min(groups, per));
+        const dim3 grid(p.H, 4, absorb_mfma_groups(p));
         if (out_dt == DT_BF16)
             return launch_k(t, "mla_absorb", mla_absorb_mfma_kernel<WT, DT_BF16>, grid, dim3(256), st, p);
         return launch_k(t, "mla_absorb", mla_absorb_mfma_kernel<WT, DT_F32>, grid, dim3(256), st, p);
@@ -638,14 +666,35 @@ static hipError_t launch_prepare_w(const MlaProjParams& pa, const LatentWritePar
     return launch_prepare_o<WT, DT_F32>(pa, pl, lat_dt, st, t);
 }
 
+template <int WT, int OUT_DT>
+static hipError_t launch_prepare_mfma_o(const MlaProjParams& pa, const LatentWriteParams& pl, int lat_dt,
+                                        hipStream_t st, KernelTimer* t) {
+    const int nz = absorb_mfma_groups(pa);
+    const dim3 grid(pa.H * 4 * nz + (pl.rows + 3) / 4);
+    if (lat_dt == DT_BF16)
+        return launch_k(t, "mla_prepare", mla_prepare_mfma_kernel<WT, OUT_DT, DT_BF16>, grid, dim3(256), st, pa, pl, nz);
+    return launch_k(t, "mla_prepare", mla_prepare_mfma_kernel<WT, OUT_DT, DT_F16>, grid, dim3(256), st, pa, pl, nz);
+}
+
+template <int WT>
+static hipError_t launch_prepare_mfma_w(const MlaProjParams& pa, const LatentWriteParams& pl, int out_dt, int lat_dt,
+                                        hipStream_t st, KernelTimer* t) {
+    if (out_dt == DT_BF16) return launch_prepare_mfma_o<WT, DT_BF16>(pa, pl, lat_dt, st, t);
+    return launch_prepare_mfma_o<WT, DT_F32>(pa, pl, lat_dt, st, t);
+}
+
 hipError_t launch_mla_prepare(const MlaProjParams& pa, const LatentWriteParams& pl, int w_type, int out_dt,
                               int lat_dt, hipStream_t st, KernelTimer* t) {
-    if (pa.rows >= kProjMfmaRows || pa.rows == 0 || pl.rows == 0) {
-        // prompt sizes (the absorb MFMA form) or one stage empty: two launches
+    if (pa.rows == 0 || pl.rows == 0) {
+        // one stage empty: the other alone
         if (pl.rows > 0)
             if (hipError_t e = launch_mla_latent_write(pl, lat_dt, st, t); e != hipSuccess) return e;
         return pa.rows > 0 ? launch_mla_absorb(pa, w_type, out_dt, st, t) : hipSuccess;
     }
+    if (pa.rows >= kProjMfmaRows)  // prompt sizes: the absorb MFMA form with the latent rows
+        return w_type == W_F16 ? launch_prepare_mfma_w<W_F16>(pa, pl, out_dt, lat_dt, st, t)
+             : w_type == W_Q8_0 ? launch_prepare_mfma_w<W_Q8_0>(pa, pl, out_dt, lat_dt, st, t)
+                                : launch_prepare_mfma_w<W_Q4_0>(pa, pl, out_dt, lat_dt, st, t);
     return w_type == W_F16 ? launch_prepare_w<W_F16>(pa, pl, out_dt, lat_dt, st, t)
          : w_type == W_Q8_0 ? launch_prepare_w<W_Q8_0>(pa, pl, out_dt, lat_dt, st, t)
                             : launch_prepare_w<W_Q4_0>(pa, pl, out_dt, lat_dt, st, t);
