@@ -168,10 +168,12 @@ def test_seq_base_positions_match_explicit_positions(device):
 
 
 @pytest.mark.parametrize("ldt", [C.F16, C.BF16])
-@pytest.mark.parametrize("B,q_len,H", [(8, 1, 128), (2, 3, 16), (1, 100, 16)])
+@pytest.mark.parametrize("B,q_len,H", [(8, 1, 128), (2, 3, 16), (1, 100, 16), (3, 67, 16)])
 def test_prepare_equals_separate_calls(device, ldt, B, q_len, H):
-    """mla_prepare (one launch at decode sizes, two at prompt sizes) writes
-    the same latent rows and q_abs as mla_latent_write + mla_absorb."""
+    """mla_prepare (one launch: the VALU absorb at decode sizes, the MFMA
+    absorb at prompt sizes, with the latent rows beside it) writes the same
+    latent rows and q_abs as mla_latent_write + mla_absorb (201 rows: four
+    row groups and a last latent workgroup with one row)."""
     rows = B * q_len
     g = torch.Generator(device=device).manual_seed(70 + rows)
     kv_a = torch.randn((rows, 576), generator=g, device=device).half()
