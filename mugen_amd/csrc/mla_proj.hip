@@ -551,9 +551,9 @@ __global__ __launch_bounds__(256) void mla_project_mfma_kernel(MlaProjParams p) 
 #pragma unroll
     for (int i = 0; i < kPf; i++) load_o(blockIdx.z * 64, i, ob[i]);
     {   // dequantise the half: 64 rows x 64 chunks of 8 dims, 16 per
-        // thread in two batches of 8 (a batch's loads issued together)
+        // thread, every load issued before any conversion
         const uint8_t* wh = static_cast<const uint8_t*>(p.w) + ((size_t)h * VH + jh * JH) * WRB;
-        constexpr int JOBS = 8;
+        constexpr int JOBS = 16;
 #pragma unroll 1
         for (int j0 = 0; j0 < JH * 64; j0 += 256 * JOBS) {
             WRaw<WT, 8> raw[JOBS];
