@@ -67,6 +67,23 @@ def test_gqa_workspace_size_and_missing_workspace():
     assert _capi.lib().mugen_attn_gqa_decode_workspace_size(ctypes.byref(a1)) == 0
 
 
+def _gqa_splits(a):
+    # the workspace holds B * H * splits fp32 partials of padded head_dim plus (m, l)
+    ws = _capi.lib().mugen_attn_gqa_decode_workspace_size(ctypes.byref(a))
+    return 1 if ws == 0 else (ws - 256) // (a.batch * a.n_heads * (4 * 128 + 8))
+
+
+@pytest.mark.parametrize("B,T,splits", [(1, 512, 8), (1, 2048, 32), (1, 4096, 32), (1, 8192, 32), (2, 8192, 32),
+                                         (4, 8192, 32), (8, 8192, 16)])
+def test_gqa_decode_plan(B, T, splits):
+    # the longest sequence in at most 32 splits of 64+ tokens, one round of
+    # 512 workgroups (B * Hk * splits): the measured optimum at 1-2
+    # sequences, where the smallest chunk that fits the round gave 64 splits
+    # at T = 8192 and 16 at T = 2048
+    a = _gqa_args(batch=B, max_seq_len=T, seq_stride=T * 4 * 128)
+    assert _gqa_splits(a) == splits
+
+
 def _mla_args(**kw):
     a = _capi.MlaDecodeArgs()
     a.q = a.latent = a.seq_lens = a.out = 0x1000
@@ -89,6 +106,23 @@ def _mla_args(**kw):
 def test_mla_rejects_bad_args(kw, code):
     a = _mla_args(**kw)
     assert _capi.lib().mugen_attn_mla_decode(ctypes.byref(a), None, 0, None) == code
+
+
+def _mla_splits(a):
+    # fp16 O blocks of 16 rows plus fp32 (m, l) per row, per (sequence, split)
+    ws = _capi.lib().mugen_attn_mla_decode_workspace_size(ctypes.byref(a))
+    R = a.q_len * a.n_heads
+    return (ws - 256) // (a.batch * ((R + 15) // 16 * 16 * 512 * 2 + R * 8))
+
+
+@pytest.mark.parametrize("B,H,q_len,T,splits", [(1, 16, 1, 1024, 32), (1, 16, 1, 8192, 32), (1, 128, 1, 8192, 32),
+                                                 (8, 128, 1, 8192, 16), (4, 128, 5, 32768, 6)])
+def test_mla_decode_plan(B, H, q_len, T, splits):
+    # the longest sequence in at most 32 splits, one round of 256 workgroups
+    # (row blocks x splits): V2-Lite heads at T = 8192 once took 256
+    # one-tile splits (36.5 us against 16.9 with 32)
+    a = _mla_args(batch=B, n_heads=H, q_len=q_len, max_seq_len=T, seq_stride=T * 576)
+    assert _mla_splits(a) == splits
 
 
 def test_mla_workspace():
