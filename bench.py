@@ -496,6 +496,11 @@ def main():
             # a 256-token prompt chunk after 7936 cached tokens (the key
             # ranges split across workgroups, then merged)
             Prefill(dev, 256, 28, 4, 128, 53, "gqa_prefill_qwen7b_chunk256_at7936", start=7936),
+            # a speculative-verify step of the 7B model: a 4-token draft plus
+            # one through the prompt path after 8000 held tokens
+            # (forward_prefill_all_logits, transformer.cpp:3499-3514, runs the
+            # verify tokens through forward_prefill_layers at start_position)
+            Prefill(dev, 5, 28, 4, 128, 54, "gqa_prefill_qwen7b_verify5_at8000", start=8000),
             MlaDecode(dev, 4, 128, 5, [32768] * 4, 32768, torch.bfloat16, torch.bfloat16, 47, "mla_verify_v3"),
             # a 512-token prompt of V2-Lite in one verify-shaped call (the
             # reference runs cpu_mla_attention once per prompt token)

@@ -114,15 +114,17 @@ def test_prefill_workloads(device, name, N, H, Hk, D, seed):
         C.assert_close(_f32(c.out[N - t:]), ref, name + " last 128 rows")
 
 
-def test_prefill_chunk_workload(device):
-    # the bench's chunk over a long context: every row against the oracle's
+@pytest.mark.parametrize("name,N,start,seed", [("gqa_prefill_qwen7b_chunk256_at7936", 256, 7936, 53),
+                                               ("gqa_prefill_qwen7b_verify5_at8000", 5, 8000, 54)])
+def test_prefill_chunk_workload(device, name, N, start, seed):
+    # the bench's chunks over a long context: every row against the oracle's
     # start-offset form (the key ranges are split, then merged)
-    N, H, Hk, D, start = 256, 28, 4, 128, 7936
-    c = bench.Prefill(device, N, H, Hk, D, 53, "gqa_prefill_qwen7b_chunk256_at7936", start=start)
+    H, Hk, D = 28, 4, 128
+    c = bench.Prefill(device, N, H, Hk, D, seed, name, start=start)
     assert c.ws.numel() > 0
     _run(c)
     ref = O.gqa_prefill(_f32(c.q), _f32(c.k), _f32(c.v), N, H, Hk, D, start + N, start, nthreads=16)
-    C.assert_close(_f32(c.out), ref, "gqa_prefill_qwen7b_chunk256_at7936")
+    C.assert_close(_f32(c.out), ref, name)
 
 
 @pytest.mark.parametrize("name", ["mla_layer_v3_q8_0", "mla_layer_prefill_v2lite_n512"])
