@@ -103,7 +103,10 @@ typedef struct mugen_attn_gqa_decode_args {
     int32_t kv_dtype;   /* mugen_attn_dtype */
     int32_t out_dtype;  /* mugen_attn_dtype */
     /* optional HOST copy of seq_lens (NULL allowed): lets the planner size
-     * the context splits for ragged batches; results do not depend on it */
+     * the context splits for ragged batches.  It must equal the device
+     * lengths; a copy that is too short gives wrong results but never writes
+     * outside the workspace.  The workspace size depends on it; a size asked
+     * for without it (and num_splits 0) covers every host copy. */
     const int32_t* seq_lens_host;
 } mugen_attn_gqa_decode_args;
 
@@ -188,7 +191,7 @@ typedef struct mugen_attn_gqa_decode_q4_args {
     int32_t num_splits;
     float scale;
     int32_t out_dtype;
-    const int32_t* seq_lens_host;
+    const int32_t* seq_lens_host; /* as in mugen_attn_gqa_decode_args */
 } mugen_attn_gqa_decode_q4_args;
 size_t mugen_attn_gqa_decode_q4_workspace_size(const mugen_attn_gqa_decode_q4_args* args);
 int mugen_attn_gqa_decode_q4(const mugen_attn_gqa_decode_q4_args* args, void* workspace, size_t workspace_bytes,
@@ -317,7 +320,10 @@ typedef struct mugen_attn_mla_decode_args {
     /* optional HOST copy of seq_lens (NULL allowed).  When given it sizes the
      * grid to exactly the active context splits, so every entry must be >=
      * the device value (normally equal; a larger value only costs idle
-     * workgroups).  NULL sizes the grid for batch * max_seq_len. */
+     * workgroups; a smaller one gives wrong results but never writes outside
+     * the workspace).  NULL sizes the grid for batch * max_seq_len.  The
+     * workspace size depends on it; a size asked for without it (and
+     * num_splits 0) covers every host copy. */
     const int32_t* seq_lens_host;
     /* 0 = automatic; MUGEN_ATTN_MLA_KERNEL_ROWS / _WS force
      * one kernel (same results within rounding; for kernel comparisons) */

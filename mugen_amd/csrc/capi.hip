@@ -169,6 +169,10 @@ static int64_t gqa_items(const mugen_attn_gqa_decode_args* a, int chunk, int ext
     return n * a->n_kv_heads;
 }
 
+// automatic split plans: the longest sequence in at most kPlanSplitCap
+// splits; GQA decode chunks of at least kGqaChunkMin tokens
+constexpr int kPlanSplitCap = 32, kGqaChunkMin = 64;
+
 // GQA decode: a workgroup's 4 waves take 32-token blocks round-robin, so
 // chunks are multiples of 32 tokens, at least 64.  The kernel holds two
 // 256-thread workgroups per CU; the plan is the smallest chunk whose work
@@ -180,7 +184,7 @@ static int64_t gqa_items(const mugen_attn_gqa_decode_args* a, int chunk, int ext
 // tokens): B1 T2048 7.38 -> 6.87 us, T8192 10.83 -> 9.17, B2 T8192 12.98
 // -> 10.0; B16 and B1 T4096 unchanged (their plans were ~32 splits).
 static int gqa_chunk(const mugen_attn_gqa_decode_args* a, int extra = 0) {
-    constexpr int q = 32, qmin = 64, kSplitCap = 32;
+    constexpr int q = 32, qmin = kGqaChunkMin, kSplitCap = kPlanSplitCap;
     const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
     if (a->num_splits > 0) return explicit_chunk(maxT, a->num_splits, q, kMaxSplits - 1);
     const int cmax = ceil_div(maxT, q) * q;
@@ -243,9 +247,35 @@ static int padded_head_dim(int head_dim) { return head_dim <= 64 ? 64 : head_dim
 
 // workspace: fp32 partials [B][H][splits][D] and (m, l) [B][H][splits][2]
 // (D = the padded head_dim)
-static size_t gqa_ws(const mugen_attn_gqa_decode_args* a, int chunk, int* splits_out) {
-    const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
-    const int splits = ceil_div(maxT, chunk);
+// The split-K partials' stride (splits per (sequence, head) slot): the
+// plan's largest split count.  With host lengths that is the longest
+// sequence's (the automatic plans split it at most 32 ways, plus the 4-bit
+// store's separate ring split: `extra`), so a short batch in a long cache
+// needs no more than its plan; the kernels skip any split index past the
+// stride, so a device length above its host copy never writes past it.
+// Without host lengths every length up to max_seq_len may come.
+static int plan_stride(int max_seq_len, int chunk, const int32_t* host, int batch, int extra) {
+    const int maxT = max_seq_len > 0 ? max_seq_len : 1;
+    if (!host) return ceil_div(maxT, chunk) + extra;
+    int s = 1;
+    for (int b = 0; b < batch; b++) {
+        const int T = std::min(std::max(host[b], 0), maxT);
+        if (T > 0) s = std::max(s, ceil_div(T, chunk) + extra);
+    }
+    return s;
+}
+
+// A workspace sized without host lengths (a caller sizing once, then
+// passing host lengths per call) must cover every plan those lengths can
+// give: the automatic plans keep the longest sequence within kPlanSplitCap
+// splits of at least `qmin` tokens
+static int stride_bound(int max_seq_len, int qmin, int extra) {
+    const int maxT = max_seq_len > 0 ? max_seq_len : 1;
+    return std::min(kPlanSplitCap, ceil_div(maxT, qmin)) + extra;
+}
+
+static size_t gqa_ws(const mugen_attn_gqa_decode_args* a, int chunk, int* splits_out, int min_splits = 0) {
+    const int splits = std::max(plan_stride(a->max_seq_len, chunk, a->seq_lens_host, a->batch, 0), min_splits);
     if (splits_out) *splits_out = splits;
     if (splits <= 1) return 0;
     const size_t slots = (size_t)a->batch * a->n_heads * splits;
@@ -305,7 +335,7 @@ static int mla_chunk(const mugen_attn_mla_decode_args* a, int kernel) {
     // whose merge costs more than the tiles (DeepSeek-V2-Lite heads, B1
     // T8192: 256 splits 36.5 us, 32 splits 16.9; one V3 sequence at T8192
     // 26.0 -> 17.3 us)
-    constexpr int kSplitCap = 32;
+    constexpr int kSplitCap = kPlanSplitCap;
     int tlong = maxT;
     if (a->seq_lens_host) {
         tlong = 1;
@@ -353,9 +383,8 @@ static int mla_validate(const mugen_attn_mla_decode_args* a) {
     return MUGEN_ATTN_OK;
 }
 
-static size_t mla_ws(const mugen_attn_mla_decode_args* a, int chunk, int* splits_out) {
-    const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
-    const int splits = ceil_div(maxT, chunk);
+static size_t mla_ws(const mugen_attn_mla_decode_args* a, int chunk, int* splits_out, int min_splits = 0) {
+    const int splits = std::max(plan_stride(a->max_seq_len, chunk, a->seq_lens_host, a->batch, 0), min_splits);
     if (splits_out) *splits_out = splits;
     // every split (a single one included) writes an fp32 (m, l, o) partial
     const size_t R = (size_t)a->q_len * a->n_heads;
@@ -465,9 +494,8 @@ static int gqa_q4_validate(const mugen_attn_gqa_decode_q4_args* a) {
 // 4-bit store decode: the Q4 and f16-ring tokens of a sequence are split
 // separately (at most one split more than the f16 plan), and the partials
 // always go through the workspace and the combine
-static size_t gqa_q4_ws(const mugen_attn_gqa_decode_q4_args* a, int chunk, int* splits_out) {
-    const int maxT = a->max_seq_len > 0 ? a->max_seq_len : 1;
-    const int splits = ceil_div(maxT, chunk) + 1;
+static size_t gqa_q4_ws(const mugen_attn_gqa_decode_q4_args* a, int chunk, int* splits_out, int min_splits = 0) {
+    const int splits = std::max(plan_stride(a->max_seq_len, chunk, a->seq_lens_host, a->batch, 1), min_splits);
     if (splits_out) *splits_out = splits;
     const size_t slots = (size_t)a->batch * a->n_heads * splits;
     return slots * (size_t)padded_head_dim(a->head_dim) * 4 + slots * 2 * 4 + 256;
@@ -476,7 +504,8 @@ static size_t gqa_q4_ws(const mugen_attn_gqa_decode_q4_args* a, int chunk, int* 
 size_t mugen_attn_gqa_decode_q4_workspace_size(const mugen_attn_gqa_decode_q4_args* a) {
     if (gqa_q4_validate(a) != MUGEN_ATTN_OK) return 0;
     const mugen_attn_gqa_decode_args g = q4_as_gqa(a);
-    return gqa_q4_ws(a, gqa_chunk(&g, 1), nullptr);
+    const int bound = (!a->seq_lens_host && a->num_splits <= 0) ? stride_bound(a->max_seq_len, kGqaChunkMin, 1) : 0;
+    return gqa_q4_ws(a, gqa_chunk(&g, 1), nullptr, bound);
 }
 
 int mugen_attn_gqa_decode_q4(const mugen_attn_gqa_decode_q4_args* a, void* ws, size_t ws_bytes, void* stream) {
@@ -528,7 +557,8 @@ int mugen_attn_gqa_decode_q4(const mugen_attn_gqa_decode_q4_args* a, void* ws, s
 
 size_t mugen_attn_gqa_decode_workspace_size(const mugen_attn_gqa_decode_args* a) {
     if (gqa_validate(a) != MUGEN_ATTN_OK) return 0;
-    return gqa_ws(a, gqa_chunk(a), nullptr);
+    const int bound = (!a->seq_lens_host && a->num_splits <= 0) ? stride_bound(a->max_seq_len, kGqaChunkMin, 0) : 0;
+    return gqa_ws(a, gqa_chunk(a), nullptr, bound);
 }
 
 int mugen_attn_gqa_decode(const mugen_attn_gqa_decode_args* a, void* ws, size_t ws_bytes, void* stream) {
@@ -799,7 +829,10 @@ int mugen_attn_gqa_prefill(const mugen_attn_gqa_prefill_args* a, void* stream) {
 
 size_t mugen_attn_mla_decode_workspace_size(const mugen_attn_mla_decode_args* a) {
     if (mla_validate(a) != MUGEN_ATTN_OK) return 0;
-    return mla_ws(a, mla_chunk(a, mla_kernel(a)), nullptr);
+    const int bound = (!a->seq_lens_host && a->num_splits <= 0)
+                          ? stride_bound(a->max_seq_len, mla_tile_tokens(mla_kernel(a)), 0)
+                          : 0;
+    return mla_ws(a, mla_chunk(a, mla_kernel(a)), nullptr, bound);
 }
 
 }  // extern "C"

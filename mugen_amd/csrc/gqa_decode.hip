@@ -127,6 +127,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D > 128 ? 1
         r -= nsj * p.Hk;
     }
     if (b < 0) return;  // grid padding (sized from an upper bound)
+    // a split past the workspace's stride (a device length above the host
+    // copy the plan was made from): nothing to write it to
+    if (p.num_splits > 1 && s >= p.num_splits) return;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int T = PF ? (p.pf_causal ? min(p.pf_start + b + 1, p.max_T) : p.max_T) : clamp_len(p.seq_lens[b], p.max_T);

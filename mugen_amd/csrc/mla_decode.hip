@@ -121,7 +121,7 @@ __device__ __forceinline__ bool mla_map(const MlaParams& p, int& b, int& s, int&
             if (grp < acc + nsj) {
                 b = j;
                 s = grp - acc;
-                return true;
+                return s < p.num_splits;  // (a split past the partials' stride: nothing to write it to)
             }
             acc += nsj;
         }
@@ -153,7 +153,7 @@ __device__ __forceinline__ bool mla_map(const MlaParams& p, int& b, int& s, int&
             b = j;
             s = u / p.nrb;
             rb = u - s * p.nrb;
-            return true;
+            return s < p.num_splits;
         }
         acc += s0 * p.nrb;
         for (int sj = s0; sj < nsj; sj++) {
@@ -162,7 +162,7 @@ __device__ __forceinline__ bool mla_map(const MlaParams& p, int& b, int& s, int&
                 b = j;
                 s = sj;
                 rb = first + (unit - acc);
-                return true;
+                return s < p.num_splits;
             }
             acc += p.nrb - first;
         }

@@ -79,6 +79,37 @@ def test_mla_decode_guarded(device, q_len, lens):
         C.assert_close(out.t.cpu().numpy(), C.mla_ref(c), f"clamped lens {lens} kernel {kernel}")
 
 
+def test_decode_short_host_copy_guarded(device):
+    # host lengths below the device ones: the plan (grid, workspace, the
+    # partials' stride) follows the host copy, and the splits it has no
+    # room for are skipped -- the result is not defined, but nothing is
+    # written outside the output or the workspace sized for that plan
+    T = 4096
+    dev_lens, host_lens = [4000, 3000], np.array([200, 100], np.int32)
+    c = C.gqa_decode_case(530, 2, 28, 4, 128, dev_lens, max_T=T, dtype=C.F16)
+    C.say(f"guarded gqa_decode, host lengths {list(host_lens)} below device {dev_lens}")
+    q = C.to_dev(c["qb"], C.F16, device)
+    k = C.to_dev(c["kb"], C.F16, device)
+    v = C.to_dev(c["vb"], C.F16, device)
+    sl = torch.tensor(dev_lens, dtype=torch.int32, device=device)
+    out = Guarded((2, 28, 128), torch.float32, device)
+    a = A.gqa_decode_args(q, k, v, sl, out.t, T, 0.0, 0)
+    a.seq_lens_host = host_lens.ctypes.data
+    ws = guarded_ws(_capi.lib().mugen_attn_gqa_decode_workspace_size(ctypes.byref(a)), device)
+    mugen_amd.attention_decode(q, k, v, sl, T, out=out.t, workspace=ws.t, seq_lens_host=host_lens)
+    assert out.intact() and ws.intact(), "guard band overwritten (gqa decode, short host copy)"
+    m = C.mla_case(531, 2, 1, 16, dev_lens, max_T=T, q_dtype=C.F32, lat_dtype=C.F16)
+    C.say(f"guarded mla_decode, host lengths {list(host_lens)} below device {dev_lens}")
+    mq = C.to_dev(m["q"], C.F32, device)
+    lat = C.to_dev(m["latb"], C.F16, device)
+    mout = Guarded((2, 1, 16, 512), torch.float32, device)
+    ma = A.mla_args(mq, lat, sl, mout.t, T, C.MLA_SCALE, 0, 0)
+    ma.seq_lens_host = host_lens.ctypes.data
+    mws = guarded_ws(_capi.lib().mugen_attn_mla_decode_workspace_size(ctypes.byref(ma)), device)
+    mugen_amd.mla_attention(mq, lat, sl, T, scale=C.MLA_SCALE, out=mout.t, workspace=mws.t, seq_lens_host=host_lens)
+    assert mout.intact() and mws.intact(), "guard band overwritten (mla decode, short host copy)"
+
+
 def test_gqa_prefill_guarded(device):
     c = C.prefill_case(503, 77, 28, 4, 128, 30, C.BF16)
     C.say("guarded gqa_prefill N=77 start=30")

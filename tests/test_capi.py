@@ -73,6 +73,11 @@ def _gqa_splits(a):
     return 1 if ws == 0 else (ws - 256) // (a.batch * a.n_heads * (4 * 128 + 8))
 
 
+def _host_lens(lens):
+    arr = (ctypes.c_int32 * len(lens))(*lens)
+    return arr, ctypes.addressof(arr)
+
+
 @pytest.mark.parametrize("B,T,splits", [(1, 512, 8), (1, 2048, 32), (1, 4096, 32), (1, 8192, 32), (2, 8192, 32),
                                          (4, 8192, 32), (8, 8192, 16)])
 def test_gqa_decode_plan(B, T, splits):
@@ -81,7 +86,30 @@ def test_gqa_decode_plan(B, T, splits):
     # sequences, where the smallest chunk that fits the round gave 64 splits
     # at T = 8192 and 16 at T = 2048
     a = _gqa_args(batch=B, max_seq_len=T, seq_stride=T * 4 * 128)
+    keep, a.seq_lens_host = _host_lens([T] * B)  # exact plan sizes
     assert _gqa_splits(a) == splits
+
+
+def test_decode_workspace_without_host_lengths_covers_every_plan():
+    # a workspace sized once without host lengths serves every call that
+    # passes them (short batches in a long cache plan finer chunks)
+    import random
+    rnd = random.Random(5)
+    for _ in range(200):
+        B = rnd.randint(1, 16)
+        T = rnd.choice([256, 1024, 4096, 8192, 32768])
+        lens = [rnd.randint(0, T) for _ in range(B)]
+        a = _gqa_args(batch=B, max_seq_len=T, seq_stride=T * 4 * 128)
+        size = _capi.lib().mugen_attn_gqa_decode_workspace_size
+        bound = size(ctypes.byref(a))
+        keep, a.seq_lens_host = _host_lens(lens)
+        assert size(ctypes.byref(a)) <= bound, (B, T, lens)
+        m = _mla_args(batch=B, n_heads=rnd.choice([16, 128]), q_len=rnd.choice([1, 5]), max_seq_len=T,
+                      seq_stride=T * 576)
+        msize = _capi.lib().mugen_attn_mla_decode_workspace_size
+        mbound = msize(ctypes.byref(m))
+        keep2, m.seq_lens_host = _host_lens([max(v, m.q_len) for v in lens])
+        assert msize(ctypes.byref(m)) <= mbound, (B, T, lens)
 
 
 def _mla_args(**kw):
@@ -122,6 +150,7 @@ def test_mla_decode_plan(B, H, q_len, T, splits):
     # (row blocks x splits): V2-Lite heads at T = 8192 once took 256
     # one-tile splits (36.5 us against 16.9 with 32)
     a = _mla_args(batch=B, n_heads=H, q_len=q_len, max_seq_len=T, seq_stride=T * 576)
+    keep, a.seq_lens_host = _host_lens([T] * B)  # exact plan sizes
     assert _mla_splits(a) == splits
 
 
