@@ -819,11 +819,16 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
                     vf[d] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
                 }
             };
-            u32x4_t vf[DB];
-            read_v(0, vf);
-            // a tile's V^T reads all in flight before its MFMAs (left to
-            // itself the scheduler keeps two: -1.4% at 7B N = 8192; the same
-            // for the S waves' K reads measured 3.9% slower)
+            // every tile's V^T reads in flight before the first MFMA (left
+            // to itself the scheduler keeps two: -1.4% at 7B N = 8192; the
+            // same for the S waves' K reads measured 3.9% slower).  Both
+            // tiles' fragments up front, in their own registers (165 VGPRs,
+            // within the 168 of three waves per SIMD), instead of the second
+            // tile's reads after the first tile's MFMAs: 7B N = 8192 539.5 ->
+            // 522.5 us, N = 2048 46.4 -> 44.9
+            u32x4_t vf[TPS][DB];
+#pragma unroll
+            for (int u = 0; u < TPS; u++) read_v(u, vf[u]);
             __builtin_amdgcn_sched_barrier(0);
             // re-base (rare after the first tiles): the factors are read only
             // when one of this wave's heads moved its max (factor 1 otherwise)
@@ -838,17 +843,13 @@ __global__ __launch_bounds__(64 * (NS / SMB + NPV)) void gqa_prefill_ws_kernel(G
             // (heads past nh accumulate stale P; their sums are never stored)
 #pragma unroll
             for (int u = 0; u < TPS; u++) {
-                if (u > 0) {
-                    read_v(u, vf);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
 #pragma unroll
                 for (int pp = 0; pp < NP; pp++)
 #pragma unroll
                     for (int d = 0; d < DB; d++)
 #pragma unroll
                         for (int hh = 0; hh < HPW; hh++)
-                            o[hh][d] = mfma16x16x32<PDT>(vf[d], pf[u][hh][pp], o[hh][d]);
+                            o[hh][d] = mfma16x16x32<PDT>(vf[u][d], pf[u][hh][pp], o[hh][d]);
             }
             if constexpr (VCVT)
                 if (j < ntiles) cv_write(j);
